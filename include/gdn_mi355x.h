@@ -1,0 +1,252 @@
+/*
+ * gdn_mi355x.h -- C ABI of libgdn_mi355x.so, the gfx950 (MI355X) kernels of
+ * the Gated DeltaNet linear-attention hot path.
+ *
+ * Every entry point:
+ *   - takes plain device pointers, element strides (in elements, not bytes,
+ *     unless a name says _bytes), sizes and a hipStream_t passed as void*;
+ *   - launches asynchronously on that stream, performs no host<->device
+ *     synchronisation and never allocates, so it is HIP-graph capturable;
+ *   - returns GDN_OK or an error code and records a message readable through
+ *     gdn_last_error() (thread-local).  Nothing throws across the ABI.
+ *
+ * Index arrays (slots, cu_seqlens, ...) may be int32 or int64 (GDN_I32 /
+ * GDN_I64).  Negative slots are sentinels: a negative read slot means "zero
+ * state" where the reference does so, a negative write slot means "skip".
+ * Element types are GDN_F32, GDN_BF16 or GDN_F16.
+ *
+ * Citations are to the reference repository (dakingffo/LogSSMs), paths below
+ * python/logssms/ unless rooted at csrc/.
+ */
+#ifndef GDN_MI355X_H
+#define GDN_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { GDN_F32 = 0, GDN_BF16 = 1, GDN_F16 = 2 };
+enum { GDN_I32 = 0, GDN_I64 = 1 };
+enum { GDN_OK = 0, GDN_ERR_INVALID = 1, GDN_ERR_UNSUPPORTED = 2, GDN_ERR_HIP = 3 };
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* gdn_last_error(void);
+/* ABI version of this library (bumped on any signature change). */
+int gdn_abi_version(void);
+
+/*
+ * Packed varlen causal depthwise conv1d + SiLU with conv-window snapshots.
+ * Replaces kernel/linear_attention/packed_conv.py:143-192 (packed_causal_conv1d,
+ * Triton kernel _packed_conv_kernel :53-140).
+ *   x        [T, C] element (x_row_stride, x_col_stride), dtype
+ *   weight   [C, W] contiguous (the reference's [C, 1, W]), dtype
+ *   bias     [C] or NULL, dtype
+ *   history  [N, C, W-1] contiguous, dtype: inputs before each sequence
+ *   cu_seqlens [N+1]
+ *   out      [T, C] contiguous, dtype: SiLU(round_dtype(sum_tap w x + b))
+ *   conv_state [slots, L, C, W-1] (slot/layer strides, inner contiguous) or NULL;
+ *     token_slots[T] (>=0: write the window ending at t), final_slots[N] or NULL
+ *     (>=0: write the window of the last token of sequence n).
+ *   boundary0/1 + scale0/1/2: per-channel-range input scale (packed_conv.py:24-30);
+ *     pass C, C, 1, 1, 1 for none.
+ */
+int gdn_packed_causal_conv1d(const void* x, int64_t x_row_stride, int64_t x_col_stride, int dtype,
+                             const void* weight, const void* bias, const void* history,
+                             const void* cu_seqlens, int cu_dtype, int64_t num_seqs,
+                             int64_t total_tokens, int64_t channels, int kernel_width, void* out,
+                             void* conv_state, int64_t state_slot_stride, int64_t state_layer_stride,
+                             int64_t layer, const void* token_slots, int token_slots_dtype,
+                             const void* final_slots, int final_slots_dtype, int64_t boundary0,
+                             int64_t boundary1, float scale0, float scale1, float scale2, void* stream);
+
+/*
+ * prepare_gdn: q,k <- x * rsqrt(sum x^2 + 1e-6); v copied; g = -exp(A_log) *
+ * softplus(gate + dt_bias) (threshold 20); beta <- sigmoid(beta).
+ * Replaces kernel/fused.py:120-158 (Triton _prepare_gdn_kernel :53-117).
+ *   query/key [B, T, H, dk] with 4 element strides each (qs[4], ks[4]), value
+ *   [B, T, HV, dv] with vs[4]; io dtype.  gate/beta [B, T, HV] with 3 strides,
+ *   own dtypes.  A_log/dt_bias [HV] with 1 stride, own dtypes.
+ *   Outputs contiguous: q_out/k_out [B,T,H,dk], v_out [B,T,HV,dv] (io dtype),
+ *   g_out/beta_out [B,T,HV] fp32.
+ */
+int gdn_prepare(const void* query, const int64_t* qs, const void* key, const int64_t* ks,
+                const void* value, const int64_t* vs, int io_dtype, const void* gate,
+                const int64_t* gs, int gate_dtype, const void* beta, const int64_t* bs, int beta_dtype,
+                const void* A_log, int64_t a_stride, int a_dtype, const void* dt_bias, int64_t dt_stride,
+                int dt_dtype, int64_t batch, int64_t tokens, int64_t H, int64_t HV, int64_t dk, int64_t dv,
+                void* q_out, void* k_out, void* v_out, float* g_out, float* beta_out, void* stream);
+
+/*
+ * Fused prefill front end (one pass over mixed_qkv): conv-history gather from
+ * the conv pool (layers/linear_attention_backend/gdn.py:107-113), packed conv +
+ * SiLU + window snapshots (packed_conv.py), q/k/v split (gdn.py:51-72) and
+ * prepare_gdn (fused.py).  Bitwise the same rounding chain as running the two
+ * reference ops back to back.
+ *   mixed [T, C] strided, C = 2*H*dk + HV*dv; gate/beta [T, HV] strided (2 strides).
+ *   conv_state [slots, L, C, W-1]; baseline_slots[N] (<0: zero history);
+ *   token_slots[T] or NULL (snapshot destinations).
+ *   Outputs: q_out/k_out [T, H, dk], v_out [T, HV, dv] (dtype), g_out/beta_out [T, HV] fp32.
+ */
+int gdn_prefill_frontend(const void* mixed, int64_t row_stride, int64_t col_stride, int dtype,
+                         const void* weight, const void* bias, int kernel_width, const void* cu_seqlens,
+                         int cu_dtype, int64_t num_seqs, int64_t total_tokens, int64_t H, int64_t HV,
+                         int64_t dk, int64_t dv, void* conv_state, int64_t state_slot_stride,
+                         int64_t state_layer_stride, int64_t layer, const void* baseline_slots,
+                         int baseline_dtype, const void* token_slots, int token_slots_dtype,
+                         const void* gate, int64_t gate_row_stride, int64_t gate_head_stride,
+                         int gate_dtype, const void* beta, int64_t beta_row_stride,
+                         int64_t beta_head_stride, int beta_dtype, const void* A_log, int a_dtype,
+                         const void* dt_bias, int dt_dtype, void* q_out, void* k_out, void* v_out,
+                         float* g_out, float* beta_out, void* stream);
+
+/*
+ * Chunked gated delta rule over packed varlen sequences with state-pool I/O
+ * (chunk size 64).  Replaces vendor/fla/gated_delta.py:15-82
+ * (chunk_gated_delta_rule_to_cache -> cumsum, kkt/solve, wy, fwd_h, fwd_o
+ * kernels) and kernel/linear_attention/state_io.py:15-28 (ChunkStateIO).
+ *   q, k [T, H, dk], v [T, HV, dv] contiguous, io dtype (bf16 or f16);
+ *   g, beta [T, HV] fp32 contiguous (prepared: natural-log decay, beta in [0,1]).
+ *   state pool [slots, L, HV, dk, dv] (slot/layer/head strides, inner
+ *   contiguous), state_dtype; read_slots[N] (<0: zero initial state);
+ *   chunk_write_slots[NT] indexed by global 64-token chunk (<0: skip);
+ *   final_write_slots[N] or NULL.
+ *   out [T, HV, dv] io dtype; v_new [T, HV, dv] or NULL (u - w h of the reference).
+ */
+int gdn_chunk_gated_delta_rule(const void* q, const void* k, const void* v, int io_dtype, const float* g,
+                               const float* beta, const void* cu_seqlens, int cu_dtype, int64_t num_seqs,
+                               int64_t total_tokens, int64_t H, int64_t HV, int64_t dk, int64_t dv,
+                               void* state, int state_dtype, int64_t slot_stride, int64_t layer_stride,
+                               int64_t head_stride, int64_t layer, const void* read_slots, int read_dtype,
+                               const void* chunk_write_slots, int chunk_write_dtype,
+                               const void* final_write_slots, int final_write_dtype, void* out,
+                               void* v_new, float scale, void* stream);
+
+/*
+ * Single-token conv update from slot windows.  Replaces
+ * kernel/linear_attention/conv_decode.py:293-352 (Triton _conv_decode_kernel
+ * :25-289), standard-state mode.
+ *   x [B, C] strided; conv_state [slots, L, C, W-1]; read/write slots [B] with strides.
+ *   Writes conv_state[write] = [window[1:], x] and the SiLU output either split
+ *   (q_out [B, key_dim], k_out [B, key_dim], v_out [B, C - 2 key_dim]) or
+ *   whole (q_out [B, C]; split_qkv = 0).
+ */
+int gdn_conv_decode(const void* x, int64_t x_row_stride, int64_t x_col_stride, int dtype,
+                    const void* weight, const void* bias, int kernel_width, int64_t batch,
+                    int64_t channels, void* conv_state, int64_t state_slot_stride,
+                    int64_t state_layer_stride, int64_t layer, const void* read_slots,
+                    int64_t read_stride, int read_dtype, const void* write_slots, int64_t write_stride,
+                    int write_dtype, void* q_out, void* k_out, void* v_out, int64_t key_dim,
+                    int split_qkv, int round_conv, int64_t boundary0, int64_t boundary1, float scale0,
+                    float scale1, float scale2, void* stream);
+
+/*
+ * Recurrent gated delta rule over T steps per sequence, raw inputs (q/k are
+ * L2-normalised, g = -exp(A_log) softplus(gate + dt_bias) and beta = sigmoid(beta)
+ * inside).  Replaces vendor/fla/fused_recurrent.py:396-458
+ * (fused_recurrent_gated_delta_rule_to_slots) and :461-550
+ * (fused_recurrent_gated_delta_rule).
+ *   q, k [B, T, H, dk], v [B, T, HV, dv] contiguous, io dtype; gate/beta
+ *   [B, T, HV] with strides (b, t, h), own dtypes; A_log/dt_bias [HV] contiguous.
+ *   Slot mode (init_state == NULL): state pool [slots, L, HV, dk, dv];
+ *     initial state from pool[read_slots[b]]; write_t_stride == 0 writes the
+ *     final state to pool[write_slots[b]] (decode), otherwise every step t to
+ *     pool[write_slots[b*write_b_stride + t*write_t_stride]] (skip <0).
+ *   Plain mode (init_state != NULL): init_state [B, HV, dk, dv] contiguous,
+ *     every step to states_out [B, T, HV, dk, dv] (state_dtype).
+ *   out [B, T, HV, dv] io dtype.
+ */
+int gdn_fused_recurrent(const void* q, const void* k, const void* v, int io_dtype, const void* gate,
+                        int64_t gate_b_stride, int64_t gate_t_stride, int64_t gate_h_stride,
+                        int gate_dtype, const void* beta, int64_t beta_b_stride, int64_t beta_t_stride,
+                        int64_t beta_h_stride, int beta_dtype, const void* A_log, int a_dtype,
+                        const void* dt_bias, int dt_dtype, int64_t batch, int64_t steps, int64_t H,
+                        int64_t HV, int64_t dk, int64_t dv, void* state, int state_dtype,
+                        int64_t slot_stride, int64_t layer_stride, int64_t head_stride, int64_t layer,
+                        const void* read_slots, int64_t read_stride, int read_dtype,
+                        const void* write_slots, int64_t write_b_stride, int64_t write_t_stride,
+                        int write_dtype, const void* init_state, void* states_out, void* out,
+                        float scale, void* stream);
+
+/*
+ * Fused decode / spec-decode verify step of the backend: conv over the
+ * token(s) from the conv pool window + recurrent update from the state pool,
+ * one pass.  Replaces layers/linear_attention_backend/gdn.py:222-265
+ * (_forward_decode: conv_decode + fused_recurrent_..._to_slots) when steps == 1
+ * and write_t_stride == 0, and gdn.py:151-220 (_forward_verify: torch conv,
+ * conv snapshots via index_copy_, fused_recurrent_gated_delta_rule, store_state)
+ * for one length group when write_t_stride != 0.
+ *   mixed [rows, C] strided; row of (b, t) = row_index[b*steps + t] if
+ *   row_index != NULL else b*steps + t (the verify group's row_indices).
+ *   gate/beta [rows, HV] strided (row, head).
+ *   Decode rounds nothing before SiLU (conv_decode GDN mode); verify rounds the
+ *   conv output to dtype before SiLU like the reference's torch conv1d.
+ *   out [B*steps, HV, dv] dtype, written in (b, t) order at out_row = row index.
+ *   steps <= 16.
+ */
+int gdn_fused_conv_recurrent(const void* mixed, int64_t row_stride, int64_t col_stride, int dtype,
+                             const void* row_index, int row_index_dtype, const void* weight,
+                             const void* bias, int kernel_width, const void* gate,
+                             int64_t gate_row_stride, int64_t gate_head_stride, int gate_dtype,
+                             const void* beta, int64_t beta_row_stride, int64_t beta_head_stride,
+                             int beta_dtype, const void* A_log, int a_dtype, const void* dt_bias,
+                             int dt_dtype, int64_t batch, int64_t steps, int64_t H, int64_t HV, int64_t dk,
+                             int64_t dv, void* conv_state, int64_t conv_slot_stride,
+                             int64_t conv_layer_stride, void* state, int state_dtype, int64_t slot_stride,
+                             int64_t layer_stride, int64_t head_stride, int64_t layer,
+                             const void* read_slots, int64_t read_stride, int read_dtype,
+                             const void* write_slots, int64_t write_b_stride, int64_t write_t_stride,
+                             int write_dtype, void* out, float scale, void* stream);
+
+/*
+ * pool[indices[i]] = states[i] for indices[i] >= 0 (row copy).  Replaces
+ * kernel/store.py:69-83 -> csrc/jit/store.cu:143-252 (StateStoreKernel).
+ *   pool_row_stride_bytes / state_row_stride_bytes: distance between rows;
+ *   row_bytes: bytes per row (multiple of 16, rows 16-byte aligned).
+ */
+int gdn_store_state(void* pool, int64_t pool_row_stride_bytes, const void* indices, int index_dtype,
+                    const void* states, int64_t state_row_stride_bytes, int64_t rows, int64_t row_bytes,
+                    void* stream);
+
+/*
+ * Batched strided row copy dst_base[dst_idx[i]] <- src_base[src_idx[i]]
+ * (pairs with a negative index are skipped).  A row is `segments` runs of
+ * `segment_bytes` each, `segment_stride_bytes` apart (Marconi's lane stride).
+ * Replaces cache/marconi/block_pool.py:90-94 (HybridBlockPool.copy_state: a
+ * Python loop of .copy_() per block) and serves cache/marconi/manager.py:272-278
+ * (after_forward checkpoint_copies).  src and dst may alias the same pool.
+ */
+int gdn_copy_rows(void* dst_base, int64_t dst_row_stride_bytes, const void* dst_idx, int dst_idx_dtype,
+                  const void* src_base, int64_t src_row_stride_bytes, const void* src_idx,
+                  int src_idx_dtype, int64_t pairs, int64_t segments, int64_t segment_bytes,
+                  int64_t segment_stride_bytes, void* stream);
+
+/*
+ * Zero `rows` rows of the same segmented shape.  Replaces
+ * cache/marconi/block_pool.py:96-99 (HybridBlockPool.zero_state).
+ */
+int gdn_zero_rows(void* base, int64_t row_stride_bytes, const void* idx, int idx_dtype, int64_t rows,
+                  int64_t segments, int64_t segment_bytes, int64_t segment_stride_bytes, void* stream);
+
+/*
+ * Spec-decode commit by copy: for each sequence b with accepted[b] in [1, T],
+ * pool[live_slots[b]] <- pool[write_slots[b, accepted[b]-1]] for one layer of
+ * both the recurrent-state pool and the conv pool.  The device-side
+ * alternative to the host slot remap of cache/radix/manager.py:248-268
+ * (commit_speculative), for callers that keep a fixed live slot per sequence.
+ *   rows are `state_row_bytes` at (slot_stride_bytes, layer offset) for the
+ *   state pool and `conv_row_bytes` for the conv pool.
+ */
+int gdn_commit_accepted(void* state, int64_t state_slot_stride_bytes, int64_t state_layer_offset_bytes,
+                        int64_t state_row_bytes, void* conv_state, int64_t conv_slot_stride_bytes,
+                        int64_t conv_layer_offset_bytes, int64_t conv_row_bytes, const void* live_slots,
+                        int live_dtype, const void* write_slots, int64_t write_b_stride,
+                        int64_t write_t_stride, int write_dtype, const void* accepted, int accepted_dtype,
+                        int64_t batch, int64_t steps, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN_MI355X_H */

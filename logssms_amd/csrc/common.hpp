@@ -1,0 +1,95 @@
+// Shared device/host helpers for the gfx950 GDN kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/gdn_mi355x.h"
+
+namespace gdn {
+
+// ---------------------------------------------------------------- element types
+// bf16 is carried as raw bits; conversions are written out so that rounding is
+// explicit (round-to-nearest-even, NaN kept quiet), matching torch's
+// ``.to(torch.bfloat16)``.
+struct bf16 {
+  uint16_t bits;
+};
+using f16 = _Float16;
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(f16 x) { return static_cast<float>(x); }
+__device__ __forceinline__ float to_f32(bf16 x) {
+  return __uint_as_float(static_cast<uint32_t>(x.bits) << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+template <class T> __device__ __forceinline__ T from_f32(float x);
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <> __device__ __forceinline__ f16 from_f32<f16>(float x) { return static_cast<f16>(x); }
+template <> __device__ __forceinline__ bf16 from_f32<bf16>(float x) {
+  bf16 r;
+  r.bits = f32_to_bf16_bits(x);
+  return r;
+}
+
+// Round a float through element type T and back (models a store + load).
+template <class T> __device__ __forceinline__ float round_to(float x) { return to_f32(from_f32<T>(x)); }
+
+// Scalar load of a runtime-typed value.
+__device__ __forceinline__ float load_any(const void* p, int64_t i, int dtype) {
+  switch (dtype) {
+    case GDN_BF16: return to_f32(static_cast<const bf16*>(p)[i]);
+    case GDN_F16: return to_f32(static_cast<const f16*>(p)[i]);
+    default: return static_cast<const float*>(p)[i];
+  }
+}
+
+__device__ __forceinline__ int64_t load_index(const void* p, int64_t i, int is64) {
+  return is64 ? static_cast<const int64_t*>(p)[i] : static_cast<int64_t>(static_cast<const int32_t*>(p)[i]);
+}
+
+// ---------------------------------------------------------------- math
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float exp_f(float x) { return __expf(x); }
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+// Decode/verify softplus (vendor/fla/fused_recurrent.py:20-22).
+__device__ __forceinline__ float softplus_decode(float x) { return x < 20.0f ? logf(1.0f + expf(x)) : x; }
+// Prefill softplus (kernel/fused.py:115).
+__device__ __forceinline__ float softplus_prefill(float x) {
+  return x > 20.0f ? x : log1pf(expf(fminf(x, 20.0f)));
+}
+
+template <int W> __device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = W / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// ---------------------------------------------------------------- host errors
+void set_error(const char* fmt, ...);
+int hip_status(hipError_t err, const char* what);
+
+}  // namespace gdn
+
+#define GDN_REQUIRE(cond, ...)            \
+  do {                                    \
+    if (!(cond)) {                        \
+      ::gdn::set_error(__VA_ARGS__);      \
+      return GDN_ERR_INVALID;             \
+    }                                     \
+  } while (0)
+
+#define GDN_LAUNCH_CHECK(what) ::gdn::hip_status(hipGetLastError(), what)

@@ -1,0 +1,410 @@
+// Prefill front end: packed varlen causal conv1d (+ SiLU, window snapshots),
+// prepare_gdn, and the fused conv -> split -> prepare pass used by the backend.
+//
+// Roofline: HBM.  Each thread owns one channel and walks a tile of
+// consecutive packed tokens with the W-1 previous inputs in registers, so
+// every input element is read once (the reference's Triton kernel reloads
+// each element W times through 4 shifted masked loads, packed_conv.py:99-110)
+// and consecutive threads touch consecutive channels (coalesced rows).
+// Per token and channel: 2 bytes in, 2 bytes out (bf16).
+#include "common.hpp"
+
+namespace gdn {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kTile = 32;  // tokens per thread
+
+__device__ __forceinline__ int64_t find_sequence(const void* cu, int cu_is64, int64_t n, int64_t t) {
+  // largest r with cu[r] <= t (cu is non-decreasing, cu[0] = 0)
+  int64_t lo = 0, hi = n - 1;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) >> 1;
+    if (load_index(cu, mid, cu_is64) <= t) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+struct ConvParams {
+  const void* x;
+  int64_t xr, xc;
+  const void* w;
+  const void* bias;
+  const void* history;  // [N, C, W-1] or nullptr (use pool + baseline slots)
+  const void* cu;
+  int cu_is64;
+  int64_t N, T, C;
+  int W;
+  void* out;
+  void* state;
+  int64_t slot_stride, layer_stride, layer;
+  const void* token_slots;
+  int token_is64;
+  const void* final_slots;
+  int final_is64;
+  const void* baseline;  // frontend: history from state[baseline[r]]
+  int baseline_is64;
+  int64_t end0, end1;
+  float s0, s1, s2;
+};
+
+// Walks tokens [t0, t1) of one channel.  Emits, per token, the rounded SiLU
+// output through `emit(t, y)` and writes window snapshots.
+template <class T, class Emit>
+__device__ __forceinline__ void conv_channel(const ConvParams& p, int64_t ch, int64_t t0, int64_t t1, Emit&& emit) {
+  const int W = p.W;
+  const int S = W - 1;
+  float w[8];
+  for (int i = 0; i < W; ++i) w[i] = to_f32(static_cast<const T*>(p.w)[ch * W + i]);
+  const float bias = p.bias ? to_f32(static_cast<const T*>(p.bias)[ch]) : 0.f;
+  const bool scaled = p.s0 != 1.f || p.s1 != 1.f || p.s2 != 1.f;
+  const float sc = ch < p.end0 ? p.s0 : (ch < p.end1 ? p.s1 : p.s2);
+  int64_t r = find_sequence(p.cu, p.cu_is64, p.N, t0);
+  int64_t begin = load_index(p.cu, r, p.cu_is64);
+  int64_t end = load_index(p.cu, r + 1, p.cu_is64);
+  float win[8];
+  auto history_at = [&](int64_t req, int i) -> float {  // i in [0, S): oldest first
+    if (p.history) return to_f32(static_cast<const T*>(p.history)[(req * p.C + ch) * S + i]);
+    const int64_t slot = load_index(p.baseline, req, p.baseline_is64);
+    if (slot < 0) return 0.f;
+    return to_f32(static_cast<const T*>(p.state)[slot * p.slot_stride + p.layer * p.layer_stride + ch * S + i]);
+  };
+  auto x_at = [&](int64_t t) -> float {
+    float v = to_f32(static_cast<const T*>(p.x)[t * p.xr + ch * p.xc]);
+    return scaled ? round_to<T>(v * sc) : v;
+  };
+  auto load_window = [&](int64_t t) {
+    // window = inputs at positions t-S .. t-1 of the sequence containing t
+    for (int i = 0; i < S; ++i) {
+      const int64_t pos = t - S + i;
+      win[i] = pos >= begin ? x_at(pos) : history_at(r, static_cast<int>(pos - begin + S));
+    }
+  };
+  load_window(t0);
+  for (int64_t t = t0; t < t1; ++t) {
+    while (t >= end) {  // next sequence (skips empty ones)
+      ++r;
+      begin = end;
+      end = load_index(p.cu, r + 1, p.cu_is64);
+      if (t < end) load_window(t);
+    }
+    const float xv = x_at(t);
+    float acc = 0.f;
+    for (int i = 0; i < S; ++i) acc = fmaf(win[i], w[i], acc);
+    acc = fmaf(xv, w[S], acc);
+    acc += bias;
+    const float y = round_to<T>(silu(round_to<T>(acc)));
+    emit(t, y);
+    for (int i = 0; i + 1 < S; ++i) win[i] = win[i + 1];
+    win[S - 1] = xv;
+    if (p.state) {
+      int64_t slot = p.token_slots ? load_index(p.token_slots, t, p.token_is64) : -1;
+      const bool last = t == end - 1;
+      int64_t fslot = (last && p.final_slots) ? load_index(p.final_slots, r, p.final_is64) : -1;
+      for (int k = 0; k < 2; ++k) {
+        const int64_t s = k == 0 ? slot : fslot;
+        if (s < 0) continue;
+        T* dst = static_cast<T*>(p.state) + s * p.slot_stride + p.layer * p.layer_stride + ch * S;
+        for (int i = 0; i < S; ++i) dst[i] = from_f32<T>(win[i]);
+      }
+    }
+  }
+}
+
+template <class T>
+__global__ __launch_bounds__(kThreads) void packed_conv_kernel(ConvParams p) {
+  const int64_t ch = static_cast<int64_t>(blockIdx.y) * kThreads + threadIdx.x;
+  if (ch >= p.C) return;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kTile;
+  const int64_t t1 = t0 + kTile < p.T ? t0 + kTile : p.T;
+  T* out = static_cast<T*>(p.out);
+  conv_channel<T>(p, ch, t0, t1, [&](int64_t t, float y) { out[t * p.C + ch] = from_f32<T>(y); });
+}
+
+// ------------------------------------------------------------ fused frontend
+struct FrontParams {
+  ConvParams conv;
+  int64_t H, HV, DK, DV;
+  const void* gate;
+  int64_t gate_r, gate_h;
+  int gate_dtype;
+  const void* beta;
+  int64_t beta_r, beta_h;
+  int beta_dtype;
+  const void* A_log;
+  int a_dtype;
+  const void* dt_bias;
+  int dt_dtype;
+  void* q_out;
+  void* k_out;
+  void* v_out;
+  float* g_out;
+  float* b_out;
+};
+
+// grid: (token tiles, C / 256).  A 256-channel slab holds whole q/k heads
+// (DK divides 256 and the q/k sections start at multiples of DK).
+template <class T, int DK>
+__global__ __launch_bounds__(kThreads) void frontend_kernel(FrontParams fp) {
+  __shared__ float part[kTile][kThreads / 64];
+  const ConvParams& p = fp.conv;
+  const int64_t ch = static_cast<int64_t>(blockIdx.y) * kThreads + threadIdx.x;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kTile;
+  const int64_t t1 = t0 + kTile < p.T ? t0 + kTile : p.T;
+  const int n = static_cast<int>(t1 - t0);
+  const int64_t key_dim = fp.H * DK;
+  const bool active = ch < p.C;
+  const bool is_qk = active && ch < 2 * key_dim;
+  // Each thread parks its own column here (no cross-thread traffic), so the
+  // per-token loop below can index registers statically.
+  __shared__ float tile[kTile][kThreads];
+  if (active) conv_channel<T>(p, ch, t0, t1, [&](int64_t t, float v) { tile[t - t0][threadIdx.x] = v; });
+  float y[kTile];
+#pragma unroll
+  for (int i = 0; i < kTile; ++i) y[i] = (active && i < n) ? tile[i][threadIdx.x] : 0.f;
+  // per-token sum of squares over each q/k head (DK consecutive channels)
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  constexpr int kWidth = DK < 64 ? DK : 64;
+#pragma unroll
+  for (int i = 0; i < kTile; ++i) {
+    float s = is_qk ? y[i] * y[i] : 0.f;
+    s = wave_sum<kWidth>(s);
+    if (DK >= 64 && lane == 0) part[i][wave] = s;
+    if (DK < 64) y[i] = is_qk ? y[i] * rsqrtf(s + 1e-6f) : y[i];
+  }
+  if (DK >= 64) {
+    __syncthreads();
+    constexpr int waves_per_head = DK / 64;
+    const int first = (wave / waves_per_head) * waves_per_head;
+#pragma unroll
+    for (int i = 0; i < kTile; ++i) {
+      float s = 0.f;
+      for (int w = 0; w < waves_per_head; ++w) s += part[i][first + w];
+      if (is_qk) y[i] *= rsqrtf(s + 1e-6f);
+    }
+  }
+  if (active) {
+    const int64_t value_dim = fp.HV * fp.DV;
+    for (int i = 0; i < n; ++i) {
+      const int64_t t = t0 + i;
+      const T v = from_f32<T>(y[i]);
+      if (ch < key_dim)
+        static_cast<T*>(fp.q_out)[t * key_dim + ch] = v;
+      else if (ch < 2 * key_dim)
+        static_cast<T*>(fp.k_out)[t * key_dim + ch - key_dim] = v;
+      else
+        static_cast<T*>(fp.v_out)[t * value_dim + ch - 2 * key_dim] = v;
+    }
+  }
+  if (blockIdx.y == 0) {
+    for (int idx = threadIdx.x; idx < n * fp.HV; idx += kThreads) {
+      const int64_t t = t0 + idx / fp.HV;
+      const int64_t h = idx % fp.HV;
+      const float a = load_any(fp.A_log, h, fp.a_dtype);
+      const float bias = load_any(fp.dt_bias, h, fp.dt_dtype);
+      const float gv = load_any(fp.gate, t * fp.gate_r + h * fp.gate_h, fp.gate_dtype) + bias;
+      const float bv = load_any(fp.beta, t * fp.beta_r + h * fp.beta_h, fp.beta_dtype);
+      fp.g_out[t * fp.HV + h] = -expf(a) * softplus_prefill(gv);
+      fp.b_out[t * fp.HV + h] = sigmoid(bv);
+    }
+  }
+}
+
+// ------------------------------------------------------------- prepare_gdn
+struct PrepParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  int64_t qs[4], ks[4], vs[4];
+  const void* gate;
+  int64_t gs[3];
+  int gate_dtype;
+  const void* beta;
+  int64_t bs[3];
+  int beta_dtype;
+  const void* A_log;
+  int64_t a_stride;
+  int a_dtype;
+  const void* dt_bias;
+  int64_t dt_stride;
+  int dt_dtype;
+  int64_t B, T, H, HV, DK, DV;
+  void* q_out;
+  void* k_out;
+  void* v_out;
+  float* g_out;
+  float* b_out;
+};
+
+// One wave per (b, t, v-head) row, 4 rows per block (kernel/fused.py:53-117).
+template <class T>
+__global__ __launch_bounds__(kThreads) void prepare_kernel(PrepParams p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
+  const int64_t rows = p.B * p.T * p.HV;
+  if (row >= rows) return;
+  const int64_t h = row % p.HV;
+  const int64_t t = (row / p.HV) % p.T;
+  const int64_t b = row / (p.HV * p.T);
+  const int64_t group = p.HV / p.H;
+  const int64_t kh = h / group;
+  if (h % group == 0) {
+    for (int which = 0; which < 2; ++which) {
+      const T* src = static_cast<const T*>(which == 0 ? p.q : p.k);
+      const int64_t* st = which == 0 ? p.qs : p.ks;
+      const int64_t base = b * st[0] + t * st[1] + kh * st[2];
+      float ss = 0.f;
+      for (int64_t d = lane; d < p.DK; d += 64) {
+        const float v = to_f32(src[base + d * st[3]]);
+        ss += v * v;
+      }
+      ss = wave_sum<64>(ss);
+      const float r = rsqrtf(ss + 1e-6f);
+      T* dst = static_cast<T*>(which == 0 ? p.q_out : p.k_out) + ((b * p.T + t) * p.H + kh) * p.DK;
+      for (int64_t d = lane; d < p.DK; d += 64) dst[d] = from_f32<T>(to_f32(src[base + d * st[3]]) * r);
+    }
+  }
+  const T* vsrc = static_cast<const T*>(p.v);
+  const int64_t vbase = b * p.vs[0] + t * p.vs[1] + h * p.vs[2];
+  T* vdst = static_cast<T*>(p.v_out) + row * p.DV;
+  for (int64_t d = lane; d < p.DV; d += 64) vdst[d] = vsrc[vbase + d * p.vs[3]];
+  if (lane == 0) {
+    const float a = load_any(p.A_log, h * p.a_stride, p.a_dtype);
+    const float bias = load_any(p.dt_bias, h * p.dt_stride, p.dt_dtype);
+    const float g = load_any(p.gate, b * p.gs[0] + t * p.gs[1] + h * p.gs[2], p.gate_dtype) + bias;
+    const float bt = load_any(p.beta, b * p.bs[0] + t * p.bs[1] + h * p.bs[2], p.beta_dtype);
+    p.g_out[row] = -expf(a) * softplus_prefill(g);
+    p.b_out[row] = sigmoid(bt);
+  }
+}
+
+template <class F>
+int dispatch_dtype(int dtype, F&& f) {
+  if (dtype == GDN_BF16) return f(bf16{});
+  if (dtype == GDN_F16) return f(f16{});
+  if (dtype == GDN_F32) return f(float{});
+  set_error("unsupported dtype %d", dtype);
+  return GDN_ERR_UNSUPPORTED;
+}
+
+}  // namespace
+}  // namespace gdn
+
+using namespace gdn;
+
+extern "C" int gdn_packed_causal_conv1d(const void* x, int64_t x_row_stride, int64_t x_col_stride, int dtype,
+                                        const void* weight, const void* bias, const void* history,
+                                        const void* cu_seqlens, int cu_dtype, int64_t num_seqs,
+                                        int64_t total_tokens, int64_t channels, int kernel_width, void* out,
+                                        void* conv_state, int64_t state_slot_stride, int64_t state_layer_stride,
+                                        int64_t layer, const void* token_slots, int token_slots_dtype,
+                                        const void* final_slots, int final_slots_dtype, int64_t boundary0,
+                                        int64_t boundary1, float scale0, float scale1, float scale2,
+                                        void* stream) {
+  GDN_REQUIRE(num_seqs >= 1 && total_tokens >= 0 && channels > 0, "gdn_packed_causal_conv1d: bad sizes");
+  if (total_tokens == 0) return GDN_OK;
+  GDN_REQUIRE(kernel_width >= 2 && kernel_width <= 8, "gdn_packed_causal_conv1d: kernel width %d not in [2, 8]",
+              kernel_width);
+  GDN_REQUIRE(x && weight && history && cu_seqlens && out, "gdn_packed_causal_conv1d: null input");
+  GDN_REQUIRE(channels <= 65535LL * kThreads, "gdn_packed_causal_conv1d: too many channels");
+  ConvParams p{};
+  p.x = x; p.xr = x_row_stride; p.xc = x_col_stride; p.w = weight; p.bias = bias; p.history = history;
+  p.cu = cu_seqlens; p.cu_is64 = cu_dtype == GDN_I64; p.N = num_seqs; p.T = total_tokens; p.C = channels;
+  p.W = kernel_width; p.out = out; p.state = conv_state; p.slot_stride = state_slot_stride;
+  p.layer_stride = state_layer_stride; p.layer = layer; p.token_slots = token_slots;
+  p.token_is64 = token_slots_dtype == GDN_I64; p.final_slots = final_slots;
+  p.final_is64 = final_slots_dtype == GDN_I64; p.end0 = boundary0; p.end1 = boundary1;
+  p.s0 = scale0; p.s1 = scale1; p.s2 = scale2;
+  dim3 grid(static_cast<unsigned>((total_tokens + kTile - 1) / kTile),
+            static_cast<unsigned>((channels + kThreads - 1) / kThreads));
+  return dispatch_dtype(dtype, [&](auto tag) {
+    using T = decltype(tag);
+    hipLaunchKernelGGL((packed_conv_kernel<T>), grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream), p);
+    return GDN_LAUNCH_CHECK("gdn_packed_causal_conv1d launch");
+  });
+}
+
+extern "C" int gdn_prefill_frontend(const void* mixed, int64_t row_stride, int64_t col_stride, int dtype,
+                                    const void* weight, const void* bias, int kernel_width, const void* cu_seqlens,
+                                    int cu_dtype, int64_t num_seqs, int64_t total_tokens, int64_t H, int64_t HV,
+                                    int64_t dk, int64_t dv, void* conv_state, int64_t state_slot_stride,
+                                    int64_t state_layer_stride, int64_t layer, const void* baseline_slots,
+                                    int baseline_dtype, const void* token_slots, int token_slots_dtype,
+                                    const void* gate, int64_t gate_row_stride, int64_t gate_head_stride,
+                                    int gate_dtype, const void* beta, int64_t beta_row_stride,
+                                    int64_t beta_head_stride, int beta_dtype, const void* A_log, int a_dtype,
+                                    const void* dt_bias, int dt_dtype, void* q_out, void* k_out, void* v_out,
+                                    float* g_out, float* beta_out, void* stream) {
+  GDN_REQUIRE(num_seqs >= 1 && total_tokens >= 0 && H > 0 && HV > 0 && HV % H == 0,
+              "gdn_prefill_frontend: bad sizes");
+  if (total_tokens == 0) return GDN_OK;
+  GDN_REQUIRE(kernel_width >= 2 && kernel_width <= 8, "gdn_prefill_frontend: kernel width %d not in [2, 8]",
+              kernel_width);
+  GDN_REQUIRE(mixed && weight && cu_seqlens && conv_state && baseline_slots && gate && beta && A_log && dt_bias &&
+                  q_out && k_out && v_out && g_out && beta_out,
+              "gdn_prefill_frontend: null input");
+  const int64_t channels = 2 * H * dk + HV * dv;
+  ConvParams p{};
+  p.x = mixed; p.xr = row_stride; p.xc = col_stride; p.w = weight; p.bias = bias; p.history = nullptr;
+  p.cu = cu_seqlens; p.cu_is64 = cu_dtype == GDN_I64; p.N = num_seqs; p.T = total_tokens; p.C = channels;
+  p.W = kernel_width; p.out = nullptr; p.state = conv_state; p.slot_stride = state_slot_stride;
+  p.layer_stride = state_layer_stride; p.layer = layer; p.token_slots = token_slots;
+  p.token_is64 = token_slots_dtype == GDN_I64; p.final_slots = nullptr; p.final_is64 = 0;
+  p.baseline = baseline_slots; p.baseline_is64 = baseline_dtype == GDN_I64;
+  p.end0 = channels; p.end1 = channels; p.s0 = p.s1 = p.s2 = 1.f;
+  FrontParams fp{};
+  fp.conv = p; fp.H = H; fp.HV = HV; fp.DK = dk; fp.DV = dv;
+  fp.gate = gate; fp.gate_r = gate_row_stride; fp.gate_h = gate_head_stride; fp.gate_dtype = gate_dtype;
+  fp.beta = beta; fp.beta_r = beta_row_stride; fp.beta_h = beta_head_stride; fp.beta_dtype = beta_dtype;
+  fp.A_log = A_log; fp.a_dtype = a_dtype; fp.dt_bias = dt_bias; fp.dt_dtype = dt_dtype;
+  fp.q_out = q_out; fp.k_out = k_out; fp.v_out = v_out; fp.g_out = g_out; fp.b_out = beta_out;
+  dim3 grid(static_cast<unsigned>((total_tokens + kTile - 1) / kTile),
+            static_cast<unsigned>((channels + kThreads - 1) / kThreads));
+  return dispatch_dtype(dtype, [&](auto tag) -> int {
+    using T = decltype(tag);
+    auto s = static_cast<hipStream_t>(stream);
+    switch (dk) {
+      case 32: hipLaunchKernelGGL((frontend_kernel<T, 32>), grid, dim3(kThreads), 0, s, fp); break;
+      case 64: hipLaunchKernelGGL((frontend_kernel<T, 64>), grid, dim3(kThreads), 0, s, fp); break;
+      case 128: hipLaunchKernelGGL((frontend_kernel<T, 128>), grid, dim3(kThreads), 0, s, fp); break;
+      case 256: hipLaunchKernelGGL((frontend_kernel<T, 256>), grid, dim3(kThreads), 0, s, fp); break;
+      default:
+        set_error("gdn_prefill_frontend: head_k_dim %lld not in {32, 64, 128, 256}", (long long)dk);
+        return GDN_ERR_UNSUPPORTED;
+    }
+    return GDN_LAUNCH_CHECK("gdn_prefill_frontend launch");
+  });
+}
+
+extern "C" int gdn_prepare(const void* query, const int64_t* qs, const void* key, const int64_t* ks,
+                           const void* value, const int64_t* vs, int io_dtype, const void* gate, const int64_t* gs,
+                           int gate_dtype, const void* beta, const int64_t* bs, int beta_dtype, const void* A_log,
+                           int64_t a_stride, int a_dtype, const void* dt_bias, int64_t dt_stride, int dt_dtype,
+                           int64_t batch, int64_t tokens, int64_t H, int64_t HV, int64_t dk, int64_t dv,
+                           void* q_out, void* k_out, void* v_out, float* g_out, float* beta_out, void* stream) {
+  GDN_REQUIRE(batch >= 0 && tokens >= 0 && H > 0 && HV > 0 && HV % H == 0 && dk > 0 && dv > 0,
+              "gdn_prepare: bad sizes");
+  const int64_t rows = batch * tokens * HV;
+  if (rows == 0) return GDN_OK;
+  GDN_REQUIRE(query && key && value && gate && beta && A_log && dt_bias && q_out && k_out && v_out && g_out &&
+                  beta_out && qs && ks && vs && gs && bs,
+              "gdn_prepare: null input");
+  PrepParams p{};
+  p.q = query; p.k = key; p.v = value;
+  for (int i = 0; i < 4; ++i) { p.qs[i] = qs[i]; p.ks[i] = ks[i]; p.vs[i] = vs[i]; }
+  for (int i = 0; i < 3; ++i) { p.gs[i] = gs[i]; p.bs[i] = bs[i]; }
+  p.gate = gate; p.gate_dtype = gate_dtype; p.beta = beta; p.beta_dtype = beta_dtype;
+  p.A_log = A_log; p.a_stride = a_stride; p.a_dtype = a_dtype;
+  p.dt_bias = dt_bias; p.dt_stride = dt_stride; p.dt_dtype = dt_dtype;
+  p.B = batch; p.T = tokens; p.H = H; p.HV = HV; p.DK = dk; p.DV = dv;
+  p.q_out = q_out; p.k_out = k_out; p.v_out = v_out; p.g_out = g_out; p.b_out = beta_out;
+  const int64_t blocks = (rows + (kThreads / 64) - 1) / (kThreads / 64);
+  GDN_REQUIRE(blocks <= 0x7fffffff, "gdn_prepare: too many rows");
+  return dispatch_dtype(io_dtype, [&](auto tag) {
+    using T = decltype(tag);
+    hipLaunchKernelGGL((prepare_kernel<T>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
+                       static_cast<hipStream_t>(stream), p);
+    return GDN_LAUNCH_CHECK("gdn_prepare launch");
+  });
+}

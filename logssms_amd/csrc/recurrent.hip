@@ -1,0 +1,641 @@
+// Recurrent gated delta rule: decode, spec-decode verify and the plain
+// T-step recurrence, plus the single-token conv update.
+//
+// Roofline: HBM.  Per (sequence, v-head) the whole d_k x d_v state is read
+// once and written once per launch (decode) or once per step (verify); the
+// arithmetic (two column reductions and a rank-1 update) is ~6 flop/element,
+// far below the CDNA4 balance point, so no MFMA is used.  The state lives in
+// VGPRs for all steps of a launch: thread (rg, cg) owns 4 consecutive columns
+// (one 16-byte global access) of rows rg, rg + RG, rg + 2 RG, ..., so each
+// load instruction of the block covers RG full rows contiguously.
+//
+// Both column reductions (S^T k and S^T q) are taken from the decayed state
+// in one pass, using o = e^g S^T q + delta (k.q) with S' = e^g S + k delta^T
+// (vendor/fla/fused_recurrent.py:219-222), so the state is touched exactly
+// once per step.
+#include "common.hpp"
+
+namespace gdn {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxFusedSteps = 16;
+constexpr int kStepChunk = 16;
+
+// -------------------------------------------------------------- vector I/O
+template <class T> struct Vec4;
+template <> struct Vec4<float> {
+  static __device__ __forceinline__ void load(const float* p, float (&v)[4]) {
+    float4 x = *reinterpret_cast<const float4*>(p);
+    v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+  }
+  static __device__ __forceinline__ void store(float* p, const float (&v)[4]) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+};
+template <> struct Vec4<bf16> {
+  static __device__ __forceinline__ void load(const bf16* p, float (&v)[4]) {
+    uint2 x = *reinterpret_cast<const uint2*>(p);
+    v[0] = __uint_as_float(x.x << 16);
+    v[1] = __uint_as_float(x.x & 0xffff0000u);
+    v[2] = __uint_as_float(x.y << 16);
+    v[3] = __uint_as_float(x.y & 0xffff0000u);
+  }
+  static __device__ __forceinline__ void store(bf16* p, const float (&v)[4]) {
+    uint2 x;
+    x.x = static_cast<uint32_t>(f32_to_bf16_bits(v[0])) | (static_cast<uint32_t>(f32_to_bf16_bits(v[1])) << 16);
+    x.y = static_cast<uint32_t>(f32_to_bf16_bits(v[2])) | (static_cast<uint32_t>(f32_to_bf16_bits(v[3])) << 16);
+    *reinterpret_cast<uint2*>(p) = x;
+  }
+};
+template <> struct Vec4<f16> {
+  static __device__ __forceinline__ void load(const f16* p, float (&v)[4]) {
+    const f16* q = p;
+    v[0] = (float)q[0]; v[1] = (float)q[1]; v[2] = (float)q[2]; v[3] = (float)q[3];
+  }
+  static __device__ __forceinline__ void store(f16* p, const float (&v)[4]) {
+    p[0] = (f16)v[0]; p[1] = (f16)v[1]; p[2] = (f16)v[2]; p[3] = (f16)v[3];
+  }
+};
+
+struct RecParams {
+  // raw token inputs (unfused): q, k [B, T, H, DK], v [B, T, HV, DV]
+  const void* q;
+  const void* k;
+  const void* v;
+  // fused conv source: mixed [rows, C]
+  const void* mixed;
+  int64_t mixed_row_stride, mixed_col_stride;
+  const void* row_index;
+  int row_index_is64;
+  const void* conv_w;
+  const void* conv_b;
+  int kernel_width;
+  void* conv_state;
+  int64_t conv_slot_stride, conv_layer_stride;
+  int round_conv;
+  // gates
+  const void* gate;
+  int64_t gate_b, gate_t, gate_h;
+  int gate_dtype;
+  const void* beta;
+  int64_t beta_b, beta_t, beta_h;
+  int beta_dtype;
+  const void* A_log;
+  int a_dtype;
+  const void* dt_bias;
+  int dt_dtype;
+  // state
+  void* state;
+  int64_t slot_stride, layer_stride, head_stride, layer;
+  const void* read_slots;
+  int64_t read_stride;
+  int read_is64;
+  const void* write_slots;
+  int64_t write_b, write_t;
+  int write_is64;
+  const void* init_state;
+  void* states_out;
+  // output
+  void* out;
+  int64_t B, T, H, HV;
+  float scale;
+};
+
+// LDS carve-up for `steps` staged steps and `group` v-heads.
+struct Smem {
+  float* qn;     // [steps][DK]   normalised q * scale
+  float* kn;     // [steps][DK]   normalised k
+  float* vv;     // [steps][group][DV]
+  float* kq;     // [steps]       k.q
+  float* decay;  // [steps][group]
+  float* beta;   // [steps][group]
+  float2* red;   // [RG][DV]
+  float* delta;  // [DV]
+};
+
+template <int DK, int DV>
+__host__ __device__ constexpr int64_t smem_bytes(int steps, int group) {
+  constexpr int CG = DV / 4;
+  constexpr int RG = kThreads / CG;
+  return (int64_t)4 * (steps * (2 * DK + group * DV + 1 + 2 * group) + DV) + (int64_t)8 * RG * DV;
+}
+
+template <int DK, int DV>
+__device__ __forceinline__ Smem carve(char* base, int steps, int group) {
+  constexpr int CG = DV / 4;
+  constexpr int RG = kThreads / CG;
+  Smem s;
+  s.red = reinterpret_cast<float2*>(base);
+  float* f = reinterpret_cast<float*>(base + 8 * RG * DV);
+  s.qn = f; f += steps * DK;
+  s.kn = f; f += steps * DK;
+  s.vv = f; f += steps * group * DV;
+  s.kq = f; f += steps;
+  s.decay = f; f += steps * group;
+  s.beta = f; f += steps * group;
+  s.delta = f;
+  return s;
+}
+
+// Normalise the staged raw q/k of `steps` steps in place and compute gates.
+template <int DK>
+__device__ __forceinline__ void normalise_and_gate(const RecParams& p, Smem& s, int64_t b, int t0, int steps,
+                                                   int head0, int group) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  for (int t = wave; t < steps; t += kThreads / 64) {
+    float sq = 0.f, sk = 0.f;
+    for (int i = lane; i < DK; i += 64) {
+      const float qv = s.qn[t * DK + i], kv = s.kn[t * DK + i];
+      sq += qv * qv;
+      sk += kv * kv;
+    }
+    sq = wave_sum<64>(sq);
+    sk = wave_sum<64>(sk);
+    const float rq = rsqrtf(sq + 1e-6f) * p.scale;
+    const float rk = rsqrtf(sk + 1e-6f);
+    float kq = 0.f;
+    for (int i = lane; i < DK; i += 64) {
+      const float qv = s.qn[t * DK + i] * rq, kv = s.kn[t * DK + i] * rk;
+      s.qn[t * DK + i] = qv;
+      s.kn[t * DK + i] = kv;
+      kq += qv * kv;
+    }
+    kq = wave_sum<64>(kq);
+    if (lane == 0) s.kq[t] = kq;
+  }
+  for (int i = threadIdx.x; i < steps * group; i += kThreads) {
+    const int t = i / group, j = i % group;
+    const int64_t h = head0 + j;
+    const int64_t tt = t0 + t;
+    const float a = load_any(p.A_log, h, p.a_dtype);
+    const float bias = load_any(p.dt_bias, h, p.dt_dtype);
+    const float gv = load_any(p.gate, b * p.gate_b + tt * p.gate_t + h * p.gate_h, p.gate_dtype);
+    const float bv = load_any(p.beta, b * p.beta_b + tt * p.beta_t + h * p.beta_h, p.beta_dtype);
+    const float g = -expf(a) * softplus_decode(gv + bias);
+    s.decay[i] = expf(g);
+    s.beta[i] = sigmoid(bv);
+  }
+}
+
+// Advance the register-resident state of v-head `j` over staged steps.
+template <int DK, int DV, class IOT, class ST>
+__device__ __forceinline__ void run_steps(const RecParams& p, Smem& s, float (&st)[DK / (kThreads / (DV / 4))][4],
+                                          int64_t b, int64_t h, int j, int group, int t0, int steps, bool fused) {
+  constexpr int CG = DV / 4;
+  constexpr int RG = kThreads / CG;
+  constexpr int RPT = DK / RG;
+  const int cg = threadIdx.x % CG;
+  const int rg = threadIdx.x / CG;
+  for (int t = 0; t < steps; ++t) {
+    const float* kn = s.kn + t * DK;
+    const float* qn = s.qn + t * DK;
+    float pk[4] = {0.f, 0.f, 0.f, 0.f}, pq[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const float kr = kn[rg + RG * i], qr = qn[rg + RG * i];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        pk[c] = fmaf(st[i][c], kr, pk[c]);
+        pq[c] = fmaf(st[i][c], qr, pq[c]);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) s.red[rg * DV + cg * 4 + c] = make_float2(pk[c], pq[c]);
+    __syncthreads();
+    const float d = s.decay[t * group + j];
+    if (threadIdx.x < DV) {
+      const int col = threadIdx.x;
+      float sk = 0.f, sq = 0.f;
+#pragma unroll
+      for (int r = 0; r < RG; ++r) {
+        const float2 v = s.red[r * DV + col];
+        sk += v.x;
+        sq += v.y;
+      }
+      const float delta = (s.vv[(t * group + j) * DV + col] - d * sk) * s.beta[t * group + j];
+      const float o = d * sq + delta * s.kq[t];
+      s.delta[col] = delta;
+      int64_t orow;
+      if (fused) {
+        const int64_t flat = b * p.T + t0 + t;
+        orow = p.row_index ? load_index(p.row_index, flat, p.row_index_is64) : flat;
+      } else {
+        orow = b * p.T + t0 + t;
+      }
+      static_cast<IOT*>(p.out)[(orow * p.HV + h) * DV + col] = from_f32<IOT>(o);
+    }
+    __syncthreads();
+    float dl[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) dl[c] = s.delta[cg * 4 + c];
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const float kr = kn[rg + RG * i];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) st[i][c] = fmaf(d, st[i][c], kr * dl[c]);
+    }
+    // per-step state writes (verify / plain mode)
+    ST* dst = nullptr;
+    if (p.init_state) {
+      dst = static_cast<ST*>(p.states_out) + (((b * p.T + t0 + t) * p.HV + h) * DK) * DV;
+    } else if (p.write_t != 0) {
+      const int64_t slot = load_index(p.write_slots, b * p.write_b + (t0 + t) * p.write_t, p.write_is64);
+      if (slot >= 0) dst = static_cast<ST*>(p.state) + slot * p.slot_stride + p.layer * p.layer_stride + h * p.head_stride;
+    }
+    if (dst) {
+#pragma unroll
+      for (int i = 0; i < RPT; ++i) Vec4<ST>::store(dst + (rg + RG * i) * DV + cg * 4, st[i]);
+    }
+  }
+}
+
+template <int DK, int DV, class ST>
+__device__ __forceinline__ void load_state(const RecParams& p, float (&st)[DK / (kThreads / (DV / 4))][4], int64_t b,
+                                           int64_t h) {
+  constexpr int CG = DV / 4;
+  constexpr int RG = kThreads / CG;
+  constexpr int RPT = DK / RG;
+  const int cg = threadIdx.x % CG;
+  const int rg = threadIdx.x / CG;
+  const ST* src;
+  if (p.init_state) {
+    src = static_cast<const ST*>(p.init_state) + (b * p.HV + h) * DK * DV;
+  } else {
+    const int64_t slot = load_index(p.read_slots, b * p.read_stride, p.read_is64);
+    src = static_cast<const ST*>(p.state) + slot * p.slot_stride + p.layer * p.layer_stride + h * p.head_stride;
+  }
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) Vec4<ST>::load(src + (rg + RG * i) * DV + cg * 4, st[i]);
+}
+
+template <int DK, int DV, class ST>
+__device__ __forceinline__ void store_final(const RecParams& p, const float (&st)[DK / (kThreads / (DV / 4))][4],
+                                            int64_t b, int64_t h) {
+  constexpr int CG = DV / 4;
+  constexpr int RG = kThreads / CG;
+  constexpr int RPT = DK / RG;
+  if (p.init_state || p.write_t != 0) return;  // per-step writes already done
+  const int64_t slot = load_index(p.write_slots, b * p.write_b, p.write_is64);
+  if (slot < 0) return;
+  const int cg = threadIdx.x % CG;
+  const int rg = threadIdx.x / CG;
+  ST* dst = static_cast<ST*>(p.state) + slot * p.slot_stride + p.layer * p.layer_stride + h * p.head_stride;
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) Vec4<ST>::store(dst + (rg + RG * i) * DV + cg * 4, st[i]);
+}
+
+// Unfused: one block per (sequence, v-head); q/k/v read from global memory.
+template <int DK, int DV, class IOT, class ST>
+__global__ __launch_bounds__(kThreads) void recurrent_kernel(RecParams p) {
+  extern __shared__ __align__(16) char smem_raw[];
+  constexpr int CG = DV / 4;
+  constexpr int RG = kThreads / CG;
+  constexpr int RPT = DK / RG;
+  const int64_t b = blockIdx.x / p.HV;
+  const int64_t h = blockIdx.x % p.HV;
+  const int64_t kh = h / (p.HV / p.H);
+  const int chunk = p.T < kStepChunk ? static_cast<int>(p.T) : kStepChunk;
+  Smem s = carve<DK, DV>(smem_raw, chunk, 1);
+  float st[RPT][4];
+  load_state<DK, DV, ST>(p, st, b, h);
+  for (int64_t t0 = 0; t0 < p.T; t0 += chunk) {
+    const int steps = static_cast<int>(p.T - t0 < chunk ? p.T - t0 : chunk);
+    for (int i = threadIdx.x; i < steps * DK; i += kThreads) {
+      const int t = i / DK, c = i % DK;
+      const int64_t base = ((b * p.T + t0 + t) * p.H + kh) * DK + c;
+      s.qn[i] = to_f32(static_cast<const IOT*>(p.q)[base]);
+      s.kn[i] = to_f32(static_cast<const IOT*>(p.k)[base]);
+    }
+    for (int i = threadIdx.x; i < steps * DV; i += kThreads) {
+      const int t = i / DV, c = i % DV;
+      s.vv[i] = to_f32(static_cast<const IOT*>(p.v)[((b * p.T + t0 + t) * p.HV + h) * DV + c]);
+    }
+    __syncthreads();
+    normalise_and_gate<DK>(p, s, b, static_cast<int>(t0), steps, static_cast<int>(h), 1);
+    __syncthreads();
+    run_steps<DK, DV, IOT, ST>(p, s, st, b, h, 0, 1, static_cast<int>(t0), steps, false);
+    __syncthreads();
+  }
+  store_final<DK, DV, ST>(p, st, b, h);
+}
+
+// Fused conv + recurrence: one block per (sequence, key head) owning the q/k
+// channels of that key head and the v channels of its HV/H v-heads, so the
+// conv window of every channel is read and rewritten by exactly one block
+// (in-place decode, read slot == write slot, is race free).
+template <int DK, int DV, class IOT, class ST>
+__global__ __launch_bounds__(kThreads) void fused_kernel(RecParams p) {
+  extern __shared__ __align__(16) char smem_raw[];
+  constexpr int CG = DV / 4;
+  constexpr int RG = kThreads / CG;
+  constexpr int RPT = DK / RG;
+  const int64_t b = blockIdx.x / p.H;
+  const int64_t kh = blockIdx.x % p.H;
+  const int group = static_cast<int>(p.HV / p.H);
+  const int steps = static_cast<int>(p.T);
+  Smem s = carve<DK, DV>(smem_raw, steps, group);
+  const int64_t key_dim = p.H * DK;
+  const int nch = 2 * DK + group * DV;
+  const int W = p.kernel_width;
+  const int64_t read_slot = load_index(p.read_slots, b * p.read_stride, p.read_is64);
+  for (int c = threadIdx.x; c < nch; c += kThreads) {
+    int64_t ch;
+    float* dst;
+    int dst_stride;
+    if (c < DK) {
+      ch = kh * DK + c;
+      dst = s.qn + c;
+      dst_stride = DK;
+    } else if (c < 2 * DK) {
+      ch = key_dim + kh * DK + (c - DK);
+      dst = s.kn + (c - DK);
+      dst_stride = DK;
+    } else {
+      const int vc = c - 2 * DK;  // = j * DV + col
+      ch = 2 * key_dim + kh * group * DV + vc;
+      dst = s.vv + vc;
+      dst_stride = group * DV;
+    }
+    float win[8];
+    float w[9];
+    const IOT* cs = static_cast<const IOT*>(p.conv_state) + read_slot * p.conv_slot_stride +
+                    p.layer * p.conv_layer_stride + ch * (W - 1);
+    for (int i = 0; i < W - 1; ++i) win[i] = to_f32(cs[i]);
+    for (int i = 0; i < W; ++i) w[i] = to_f32(static_cast<const IOT*>(p.conv_w)[ch * W + i]);
+    const float bias = p.conv_b ? to_f32(static_cast<const IOT*>(p.conv_b)[ch]) : 0.f;
+    for (int t = 0; t < steps; ++t) {
+      const int64_t flat = b * p.T + t;
+      const int64_t row = p.row_index ? load_index(p.row_index, flat, p.row_index_is64) : flat;
+      const float x = to_f32(static_cast<const IOT*>(p.mixed)[row * p.mixed_row_stride + ch * p.mixed_col_stride]);
+      float acc = 0.f;
+      for (int i = 0; i < W - 1; ++i) acc = fmaf(w[i], win[i], acc);
+      acc = fmaf(w[W - 1], x, acc);
+      acc += bias;
+      if (p.round_conv) acc = round_to<IOT>(acc);
+      dst[t * dst_stride] = round_to<IOT>(silu(acc));
+      for (int i = 0; i + 1 < W - 1; ++i) win[i] = win[i + 1];
+      win[W - 2] = x;
+      const int64_t ws = load_index(p.write_slots, b * p.write_b + t * p.write_t, p.write_is64);
+      if (ws >= 0) {
+        IOT* out = static_cast<IOT*>(p.conv_state) + ws * p.conv_slot_stride + p.layer * p.conv_layer_stride +
+                   ch * (W - 1);
+        for (int i = 0; i < W - 1; ++i) out[i] = from_f32<IOT>(win[i]);
+      }
+    }
+  }
+  __syncthreads();
+  // gate/beta rows follow the token rows: (row, head) strides
+  {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    for (int t = wave; t < steps; t += kThreads / 64) {
+      float sq = 0.f, sk = 0.f;
+      for (int i = lane; i < DK; i += 64) {
+        const float qv = s.qn[t * DK + i], kv = s.kn[t * DK + i];
+        sq += qv * qv;
+        sk += kv * kv;
+      }
+      sq = wave_sum<64>(sq);
+      sk = wave_sum<64>(sk);
+      const float rq = rsqrtf(sq + 1e-6f) * p.scale;
+      const float rk = rsqrtf(sk + 1e-6f);
+      float kq = 0.f;
+      for (int i = lane; i < DK; i += 64) {
+        const float qv = s.qn[t * DK + i] * rq, kv = s.kn[t * DK + i] * rk;
+        s.qn[t * DK + i] = qv;
+        s.kn[t * DK + i] = kv;
+        kq += qv * kv;
+      }
+      kq = wave_sum<64>(kq);
+      if (lane == 0) s.kq[t] = kq;
+    }
+    for (int i = threadIdx.x; i < steps * group; i += kThreads) {
+      const int t = i / group, j = i % group;
+      const int64_t h = kh * group + j;
+      const int64_t flat = b * p.T + t;
+      const int64_t row = p.row_index ? load_index(p.row_index, flat, p.row_index_is64) : flat;
+      const float a = load_any(p.A_log, h, p.a_dtype);
+      const float bias = load_any(p.dt_bias, h, p.dt_dtype);
+      const float gv = load_any(p.gate, row * p.gate_t + h * p.gate_h, p.gate_dtype);
+      const float bv = load_any(p.beta, row * p.beta_t + h * p.beta_h, p.beta_dtype);
+      const float g = -expf(a) * softplus_decode(gv + bias);
+      s.decay[i] = expf(g);
+      s.beta[i] = sigmoid(bv);
+    }
+  }
+  __syncthreads();
+  for (int j = 0; j < group; ++j) {
+    const int64_t h = kh * group + j;
+    float st[RPT][4];
+    load_state<DK, DV, ST>(p, st, b, h);
+    run_steps<DK, DV, IOT, ST>(p, s, st, b, h, j, group, 0, steps, true);
+    store_final<DK, DV, ST>(p, st, b, h);
+    __syncthreads();
+  }
+}
+
+// Single-token conv update (conv_decode.py:25-289, standard state).
+template <class IOT>
+__global__ __launch_bounds__(kThreads) void conv_decode_kernel(
+    const IOT* x, int64_t xr, int64_t xc, const IOT* weight, const IOT* bias, int W, int64_t C, IOT* state,
+    int64_t slot_stride, int64_t layer_stride, int64_t layer, const void* reads, int64_t read_stride,
+    int read_is64, const void* writes, int64_t write_stride, int write_is64, IOT* q, IOT* k, IOT* v,
+    int64_t key_dim, int split, int round_conv, int64_t end0, int64_t end1, float s0, float s1, float s2) {
+  const int64_t b = blockIdx.y;
+  const int64_t ch = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (ch >= C) return;
+  const int64_t rs = load_index(reads, b * read_stride, read_is64);
+  const int64_t ws = load_index(writes, b * write_stride, write_is64);
+  const IOT* src = state + rs * slot_stride + layer * layer_stride + ch * (W - 1);
+  float win[8];
+  for (int i = 0; i < W - 1; ++i) win[i] = to_f32(src[i]);
+  float xv = to_f32(x[b * xr + ch * xc]);
+  if (s0 != 1.f || s1 != 1.f || s2 != 1.f) {
+    const float sc = ch < end0 ? s0 : (ch < end1 ? s1 : s2);
+    xv = round_to<IOT>(xv * sc);
+  }
+  float acc = 0.f;
+  for (int i = 0; i < W - 1; ++i) acc = fmaf(to_f32(weight[ch * W + i]), win[i], acc);
+  acc = fmaf(to_f32(weight[ch * W + W - 1]), xv, acc);
+  if (bias) acc += to_f32(bias[ch]);
+  if (round_conv) acc = round_to<IOT>(acc);
+  const IOT y = from_f32<IOT>(silu(acc));
+  IOT* dst = state + ws * slot_stride + layer * layer_stride + ch * (W - 1);
+  for (int i = 0; i + 1 < W - 1; ++i) dst[i] = from_f32<IOT>(win[i + 1]);
+  dst[W - 2] = from_f32<IOT>(xv);
+  if (!split) {
+    q[b * C + ch] = y;
+  } else if (ch < key_dim) {
+    q[b * key_dim + ch] = y;
+  } else if (ch < 2 * key_dim) {
+    k[b * key_dim + ch - key_dim] = y;
+  } else {
+    v[b * (C - 2 * key_dim) + ch - 2 * key_dim] = y;
+  }
+}
+
+// ------------------------------------------------------------------ dispatch
+template <class F>
+int dispatch_dims(int64_t dk, int64_t dv, F&& f) {
+  if (dk == 128 && dv == 128) return f(std::integral_constant<int, 128>{}, std::integral_constant<int, 128>{});
+  if (dk == 64 && dv == 64) return f(std::integral_constant<int, 64>{}, std::integral_constant<int, 64>{});
+  if (dk == 32 && dv == 32) return f(std::integral_constant<int, 32>{}, std::integral_constant<int, 32>{});
+  if (dk == 128 && dv == 64) return f(std::integral_constant<int, 128>{}, std::integral_constant<int, 64>{});
+  if (dk == 64 && dv == 128) return f(std::integral_constant<int, 64>{}, std::integral_constant<int, 128>{});
+  set_error("unsupported head dims dk=%lld dv=%lld (supported: 32/32, 64/64, 128/128, 64/128, 128/64)",
+            (long long)dk, (long long)dv);
+  return GDN_ERR_UNSUPPORTED;
+}
+
+template <class F>
+int dispatch_io_state(int io, int st, F&& f) {
+  if (io == GDN_BF16 && st == GDN_F32) return f(bf16{}, float{});
+  if (io == GDN_BF16 && st == GDN_BF16) return f(bf16{}, bf16{});
+  if (io == GDN_F16 && st == GDN_F32) return f(f16{}, float{});
+  if (io == GDN_F16 && st == GDN_F16) return f(f16{}, f16{});
+  if (io == GDN_F32 && st == GDN_F32) return f(float{}, float{});
+  set_error("unsupported (io dtype %d, state dtype %d)", io, st);
+  return GDN_ERR_UNSUPPORTED;
+}
+
+}  // namespace
+}  // namespace gdn
+
+using namespace gdn;
+
+extern "C" int gdn_fused_recurrent(const void* q, const void* k, const void* v, int io_dtype, const void* gate,
+                                   int64_t gate_b_stride, int64_t gate_t_stride, int64_t gate_h_stride,
+                                   int gate_dtype, const void* beta, int64_t beta_b_stride, int64_t beta_t_stride,
+                                   int64_t beta_h_stride, int beta_dtype, const void* A_log, int a_dtype,
+                                   const void* dt_bias, int dt_dtype, int64_t batch, int64_t steps, int64_t H,
+                                   int64_t HV, int64_t dk, int64_t dv, void* state, int state_dtype,
+                                   int64_t slot_stride, int64_t layer_stride, int64_t head_stride, int64_t layer,
+                                   const void* read_slots, int64_t read_stride, int read_dtype,
+                                   const void* write_slots, int64_t write_b_stride, int64_t write_t_stride,
+                                   int write_dtype, const void* init_state, void* states_out, void* out,
+                                   float scale, void* stream) {
+  GDN_REQUIRE(batch >= 0 && steps >= 0 && H > 0 && HV > 0 && HV % H == 0, "gdn_fused_recurrent: bad sizes");
+  if (batch == 0 || steps == 0) return GDN_OK;
+  GDN_REQUIRE(q && k && v && gate && beta && A_log && dt_bias && out, "gdn_fused_recurrent: null input");
+  if (init_state) {
+    GDN_REQUIRE(states_out != nullptr, "gdn_fused_recurrent: plain mode needs states_out");
+  } else {
+    GDN_REQUIRE(state && read_slots && write_slots, "gdn_fused_recurrent: slot mode needs pool and slots");
+  }
+  GDN_REQUIRE(batch * HV <= 0x7fffffff, "gdn_fused_recurrent: grid too large");
+  RecParams p{};
+  p.q = q; p.k = k; p.v = v;
+  p.gate = gate; p.gate_b = gate_b_stride; p.gate_t = gate_t_stride; p.gate_h = gate_h_stride; p.gate_dtype = gate_dtype;
+  p.beta = beta; p.beta_b = beta_b_stride; p.beta_t = beta_t_stride; p.beta_h = beta_h_stride; p.beta_dtype = beta_dtype;
+  p.A_log = A_log; p.a_dtype = a_dtype; p.dt_bias = dt_bias; p.dt_dtype = dt_dtype;
+  p.state = state; p.slot_stride = slot_stride; p.layer_stride = layer_stride; p.head_stride = head_stride;
+  p.layer = layer;
+  p.read_slots = read_slots; p.read_stride = read_stride; p.read_is64 = read_dtype == GDN_I64;
+  p.write_slots = write_slots; p.write_b = write_b_stride; p.write_t = write_t_stride;
+  p.write_is64 = write_dtype == GDN_I64;
+  p.init_state = init_state; p.states_out = states_out;
+  p.out = out; p.B = batch; p.T = steps; p.H = H; p.HV = HV; p.scale = scale;
+  return dispatch_dims(dk, dv, [&](auto DKc, auto DVc) {
+    constexpr int DK = decltype(DKc)::value, DV = decltype(DVc)::value;
+    return dispatch_io_state(io_dtype, state_dtype, [&](auto iot, auto stt) {
+      using IOT = decltype(iot);
+      using ST = decltype(stt);
+      const int chunk = steps < kStepChunk ? static_cast<int>(steps) : kStepChunk;
+      const size_t shm = smem_bytes<DK, DV>(chunk, 1);
+      hipLaunchKernelGGL((recurrent_kernel<DK, DV, IOT, ST>), dim3(static_cast<unsigned>(batch * HV)),
+                         dim3(kThreads), shm, static_cast<hipStream_t>(stream), p);
+      return GDN_LAUNCH_CHECK("gdn_fused_recurrent launch");
+    });
+  });
+}
+
+extern "C" int gdn_fused_conv_recurrent(const void* mixed, int64_t row_stride, int64_t col_stride, int dtype,
+                                        const void* row_index, int row_index_dtype, const void* weight,
+                                        const void* bias, int kernel_width, const void* gate,
+                                        int64_t gate_row_stride, int64_t gate_head_stride, int gate_dtype,
+                                        const void* beta, int64_t beta_row_stride, int64_t beta_head_stride,
+                                        int beta_dtype, const void* A_log, int a_dtype, const void* dt_bias,
+                                        int dt_dtype, int64_t batch, int64_t steps, int64_t H, int64_t HV,
+                                        int64_t dk, int64_t dv, void* conv_state, int64_t conv_slot_stride,
+                                        int64_t conv_layer_stride, void* state, int state_dtype,
+                                        int64_t slot_stride, int64_t layer_stride, int64_t head_stride,
+                                        int64_t layer, const void* read_slots, int64_t read_stride,
+                                        int read_dtype, const void* write_slots, int64_t write_b_stride,
+                                        int64_t write_t_stride, int write_dtype, void* out, float scale,
+                                        void* stream) {
+  GDN_REQUIRE(batch >= 0 && steps >= 0 && H > 0 && HV > 0 && HV % H == 0, "gdn_fused_conv_recurrent: bad sizes");
+  if (batch == 0 || steps == 0) return GDN_OK;
+  GDN_REQUIRE(steps <= kMaxFusedSteps, "gdn_fused_conv_recurrent: steps %lld > %d", (long long)steps,
+              kMaxFusedSteps);
+  GDN_REQUIRE(kernel_width >= 2 && kernel_width <= 8, "gdn_fused_conv_recurrent: kernel width %d not in [2, 8]",
+              kernel_width);
+  GDN_REQUIRE(mixed && weight && gate && beta && A_log && dt_bias && conv_state && state && read_slots &&
+                  write_slots && out,
+              "gdn_fused_conv_recurrent: null input");
+  GDN_REQUIRE(HV / H <= 4, "gdn_fused_conv_recurrent: at most 4 v-heads per key head");
+  GDN_REQUIRE(steps == 1 || write_t_stride != 0, "gdn_fused_conv_recurrent: multi-step needs per-step slots");
+  GDN_REQUIRE(batch * H <= 0x7fffffff, "gdn_fused_conv_recurrent: grid too large");
+  RecParams p{};
+  p.mixed = mixed; p.mixed_row_stride = row_stride; p.mixed_col_stride = col_stride;
+  p.row_index = row_index; p.row_index_is64 = row_index_dtype == GDN_I64;
+  p.conv_w = weight; p.conv_b = bias; p.kernel_width = kernel_width;
+  p.conv_state = conv_state; p.conv_slot_stride = conv_slot_stride; p.conv_layer_stride = conv_layer_stride;
+  p.round_conv = write_t_stride != 0 ? 1 : 0;
+  p.gate = gate; p.gate_b = 0; p.gate_t = gate_row_stride; p.gate_h = gate_head_stride; p.gate_dtype = gate_dtype;
+  p.beta = beta; p.beta_b = 0; p.beta_t = beta_row_stride; p.beta_h = beta_head_stride; p.beta_dtype = beta_dtype;
+  p.A_log = A_log; p.a_dtype = a_dtype; p.dt_bias = dt_bias; p.dt_dtype = dt_dtype;
+  p.state = state; p.slot_stride = slot_stride; p.layer_stride = layer_stride; p.head_stride = head_stride;
+  p.layer = layer;
+  p.read_slots = read_slots; p.read_stride = read_stride; p.read_is64 = read_dtype == GDN_I64;
+  p.write_slots = write_slots; p.write_b = write_b_stride; p.write_t = write_t_stride;
+  p.write_is64 = write_dtype == GDN_I64;
+  p.out = out; p.B = batch; p.T = steps; p.H = H; p.HV = HV; p.scale = scale;
+  return dispatch_dims(dk, dv, [&](auto DKc, auto DVc) {
+    constexpr int DK = decltype(DKc)::value, DV = decltype(DVc)::value;
+    return dispatch_io_state(dtype, state_dtype, [&](auto iot, auto stt) {
+      using IOT = decltype(iot);
+      using ST = decltype(stt);
+      const size_t shm = smem_bytes<DK, DV>(static_cast<int>(steps), static_cast<int>(HV / H));
+      hipLaunchKernelGGL((fused_kernel<DK, DV, IOT, ST>), dim3(static_cast<unsigned>(batch * H)), dim3(kThreads),
+                         shm, static_cast<hipStream_t>(stream), p);
+      return GDN_LAUNCH_CHECK("gdn_fused_conv_recurrent launch");
+    });
+  });
+}
+
+extern "C" int gdn_conv_decode(const void* x, int64_t x_row_stride, int64_t x_col_stride, int dtype,
+                               const void* weight, const void* bias, int kernel_width, int64_t batch,
+                               int64_t channels, void* conv_state, int64_t state_slot_stride,
+                               int64_t state_layer_stride, int64_t layer, const void* read_slots,
+                               int64_t read_stride, int read_dtype, const void* write_slots, int64_t write_stride,
+                               int write_dtype, void* q_out, void* k_out, void* v_out, int64_t key_dim,
+                               int split_qkv, int round_conv, int64_t boundary0, int64_t boundary1, float scale0,
+                               float scale1, float scale2, void* stream) {
+  GDN_REQUIRE(batch >= 0 && channels > 0, "gdn_conv_decode: bad sizes");
+  if (batch == 0) return GDN_OK;
+  GDN_REQUIRE(kernel_width >= 2 && kernel_width <= 8, "gdn_conv_decode: kernel width %d not in [2, 8]",
+              kernel_width);
+  GDN_REQUIRE(x && weight && conv_state && read_slots && write_slots && q_out, "gdn_conv_decode: null input");
+  GDN_REQUIRE(!split_qkv || (k_out && v_out && 2 * key_dim < channels), "gdn_conv_decode: bad split");
+  GDN_REQUIRE(batch <= 65535, "gdn_conv_decode: batch too large");
+  dim3 grid(static_cast<unsigned>((channels + kThreads - 1) / kThreads), static_cast<unsigned>(batch));
+  auto s = static_cast<hipStream_t>(stream);
+  auto launch = [&](auto tag) {
+    using T = decltype(tag);
+    hipLaunchKernelGGL((conv_decode_kernel<T>), grid, dim3(kThreads), 0, s, static_cast<const T*>(x), x_row_stride,
+                       x_col_stride, static_cast<const T*>(weight), static_cast<const T*>(bias), kernel_width,
+                       channels, static_cast<T*>(conv_state), state_slot_stride, state_layer_stride, layer,
+                       read_slots, read_stride, read_dtype == GDN_I64, write_slots, write_stride,
+                       write_dtype == GDN_I64, static_cast<T*>(q_out), static_cast<T*>(k_out),
+                       static_cast<T*>(v_out), key_dim, split_qkv, round_conv, boundary0, boundary1, scale0, scale1,
+                       scale2);
+    return GDN_LAUNCH_CHECK("gdn_conv_decode launch");
+  };
+  if (dtype == GDN_BF16) return launch(bf16{});
+  if (dtype == GDN_F16) return launch(f16{});
+  if (dtype == GDN_F32) return launch(float{});
+  set_error("gdn_conv_decode: unsupported dtype %d", dtype);
+  return GDN_ERR_UNSUPPORTED;
+}

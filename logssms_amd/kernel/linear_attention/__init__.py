@@ -1,0 +1,22 @@
+"""Linear-attention operators mirroring ``logssms.kernel.linear_attention``
+(packed conv, conv decode) and its vendored FLA entry points."""
+
+from .conv_decode import conv_decode
+from .gdn import (
+    chunk_gated_delta_rule_to_cache,
+    fused_recurrent_gated_delta_rule,
+    fused_recurrent_gated_delta_rule_to_slots,
+)
+from .packed_conv import PackedConvStateIO, packed_causal_conv1d
+from .state_io import ChunkLogIO, ChunkStateIO
+
+__all__ = [
+    "ChunkLogIO",
+    "ChunkStateIO",
+    "PackedConvStateIO",
+    "chunk_gated_delta_rule_to_cache",
+    "conv_decode",
+    "fused_recurrent_gated_delta_rule",
+    "fused_recurrent_gated_delta_rule_to_slots",
+    "packed_causal_conv1d",
+]

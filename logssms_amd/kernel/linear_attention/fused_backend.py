@@ -1,0 +1,131 @@
+"""Backend-level fused operators: the three phases of
+``GatedDeltaBackend.forward`` (reference
+``python/logssms/layers/linear_attention_backend/gdn.py:74-265``) each as the
+smallest number of gfx950 kernels.
+
+* ``prefill_frontend`` -- conv-history gather + packed conv + snapshots + split
+  + ``prepare_gdn`` in one pass over ``mixed_qkv`` (``gdn.py:100-132``).
+* ``decode_step`` -- ``conv_decode`` + slotted recurrent update in one kernel
+  (``gdn.py:222-265``).
+* ``verify_group`` -- one verify length group: conv over the drafts, conv
+  snapshots and per-step states straight into the write slots, outputs at the
+  group's rows (``gdn.py:165-218``; replaces the torch conv, ``index_copy_``
+  snapshots, the temporary ``states`` tensor and ``store_state``).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from ... import _lib
+
+
+def _check_pools(conv_state: torch.Tensor, recurrent_state: torch.Tensor | None, config) -> None:
+    assert conv_state.ndim == 4 and tuple(conv_state.shape[2:]) == (config.conv_dim, config.state_len)
+    assert conv_state.stride(3) == 1 and conv_state.stride(2) == config.state_len
+    if recurrent_state is not None:
+        assert recurrent_state.ndim == 5
+        assert tuple(recurrent_state.shape[2:]) == (config.num_v_heads, config.head_k_dim, config.head_v_dim)
+        assert recurrent_state.stride(4) == 1 and recurrent_state.stride(3) == config.head_v_dim
+
+
+def prefill_frontend(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, conv_state, cu_seqlens,
+                     baseline_slots, conv_token_slots=None):
+    """Returns ``(q [1,T,H,dk], k, v [1,T,HV,dv], g [1,T,HV] fp32, beta fp32)``
+    exactly as ``prepare_gdn(split(packed_causal_conv1d(...)))`` would, with
+    the conv history read from ``conv_state[baseline_slots, layer]`` (zeros for
+    negative slots) and windows written to ``conv_state[conv_token_slots[t]]``."""
+    T, C = mixed_qkv.shape
+    assert C == config.conv_dim == 2 * config.key_dim + config.value_dim
+    assert gate.shape == beta.shape == (T, config.num_v_heads)
+    _check_pools(conv_state, None, config)
+    dev, dt = mixed_qkv.device, mixed_qkv.dtype
+    q = torch.empty(1, T, config.num_k_heads, config.head_k_dim, device=dev, dtype=dt)
+    k = torch.empty_like(q)
+    v = torch.empty(1, T, config.num_v_heads, config.head_v_dim, device=dev, dtype=dt)
+    g = torch.empty(1, T, config.num_v_heads, device=dev, dtype=torch.float32)
+    b = torch.empty_like(g)
+    if T == 0:
+        return q, k, v, g, b
+    weight = conv_weight.contiguous()
+    A_log = A_log.contiguous()
+    dt_bias = dt_bias.contiguous()
+    _lib.call(
+        "gdn_prefill_frontend",
+        mixed_qkv.data_ptr(), mixed_qkv.stride(0), mixed_qkv.stride(1), _lib.dtype_code(dt),
+        weight.data_ptr(), None, config.state_len + 1, cu_seqlens.data_ptr(), _lib.index_code(cu_seqlens),
+        len(cu_seqlens) - 1, T, config.num_k_heads, config.num_v_heads, config.head_k_dim, config.head_v_dim,
+        conv_state.data_ptr(), conv_state.stride(0), conv_state.stride(1), config.layer_idx,
+        baseline_slots.data_ptr(), _lib.index_code(baseline_slots),
+        _lib.ptr(conv_token_slots), _lib.index_code(conv_token_slots) if conv_token_slots is not None else 0,
+        gate.data_ptr(), gate.stride(0), gate.stride(1), _lib.dtype_code(gate.dtype),
+        beta.data_ptr(), beta.stride(0), beta.stride(1), _lib.dtype_code(beta.dtype),
+        A_log.data_ptr(), _lib.dtype_code(A_log.dtype), dt_bias.data_ptr(), _lib.dtype_code(dt_bias.dtype),
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), b.data_ptr(), _lib.stream_of(mixed_qkv),
+    )
+    return q, k, v, g, b
+
+
+def _fused(mixed, row_index, gate, beta, conv_weight, A_log, dt_bias, config, conv_state, recurrent_state,
+           read_slots, write_slots, batch, steps, write_b, write_t, out):
+    weight = conv_weight.contiguous()
+    A_log = A_log.contiguous()
+    dt_bias = dt_bias.contiguous()
+    _lib.call(
+        "gdn_fused_conv_recurrent",
+        mixed.data_ptr(), mixed.stride(0), mixed.stride(1), _lib.dtype_code(mixed.dtype),
+        _lib.ptr(row_index), _lib.index_code(row_index) if row_index is not None else 0,
+        weight.data_ptr(), None, config.state_len + 1,
+        gate.data_ptr(), gate.stride(0), gate.stride(1), _lib.dtype_code(gate.dtype),
+        beta.data_ptr(), beta.stride(0), beta.stride(1), _lib.dtype_code(beta.dtype),
+        A_log.data_ptr(), _lib.dtype_code(A_log.dtype), dt_bias.data_ptr(), _lib.dtype_code(dt_bias.dtype),
+        batch, steps, config.num_k_heads, config.num_v_heads, config.head_k_dim, config.head_v_dim,
+        conv_state.data_ptr(), conv_state.stride(0), conv_state.stride(1),
+        recurrent_state.data_ptr(), _lib.dtype_code(recurrent_state.dtype), recurrent_state.stride(0),
+        recurrent_state.stride(1), recurrent_state.stride(2), config.layer_idx,
+        read_slots.data_ptr(), read_slots.stride(0), _lib.index_code(read_slots),
+        write_slots.data_ptr(), write_b, write_t, _lib.index_code(write_slots),
+        out.data_ptr(), float(config.head_k_dim) ** -0.5, _lib.stream_of(mixed),
+    )
+
+
+def decode_step(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, conv_state, recurrent_state,
+                read_slots, write_slots, out=None):
+    """``gdn.py:222-265`` in one kernel: conv window of ``read_slots`` -> SiLU
+    (unrounded pre-activation, like ``conv_decode`` in GDN mode) -> recurrent
+    step; windows and states go to ``write_slots`` (in place when equal).
+    Returns o [B, HV, dv]."""
+    B, C = mixed_qkv.shape
+    assert C == config.conv_dim
+    assert read_slots.shape == write_slots.shape == (B,)
+    _check_pools(conv_state, recurrent_state, config)
+    if out is None:
+        out = torch.empty(B, config.num_v_heads, config.head_v_dim, device=mixed_qkv.device, dtype=mixed_qkv.dtype)
+    assert out.shape == (B, config.num_v_heads, config.head_v_dim) and out.is_contiguous()
+    if B:
+        _fused(mixed_qkv, None, gate, beta, conv_weight, A_log, dt_bias, config, conv_state, recurrent_state,
+               read_slots, write_slots, B, 1, write_slots.stride(0), 0, out)
+    return out
+
+
+def verify_group(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, conv_state, recurrent_state,
+                 row_indices, baseline_slots, write_slots, output):
+    """One verify length group (``gdn.py:165-218``): B sequences of T drafts at
+    rows ``row_indices`` (``[B*T]``, or None for rows ``0..B*T-1``) of
+    ``mixed_qkv``/``gate``/``beta``.  Step t's conv window and state go to
+    ``write_slots[b, t]``; outputs land in ``output[row]`` ([rows, HV, dv])."""
+    B, T = write_slots.shape
+    assert baseline_slots.shape == (B,)
+    assert 1 <= T <= 16
+    _check_pools(conv_state, recurrent_state, config)
+    assert output.is_contiguous() and output.shape[1:] == (config.num_v_heads, config.head_v_dim)
+    if row_indices is not None:
+        assert row_indices.shape == (B * T,)
+    if B:
+        _fused(mixed_qkv, row_indices, gate, beta, conv_weight, A_log, dt_bias, config, conv_state,
+               recurrent_state, baseline_slots, write_slots, B, T, write_slots.stride(0), write_slots.stride(1),
+               output)
+    return output
+
+
+__all__ = ["decode_step", "prefill_frontend", "verify_group"]

@@ -1,0 +1,204 @@
+"""Gated delta rule operators (drop-in for the reference's vendored FLA entry
+points, ``python/logssms/kernel/linear_attention/vendor/fla/__init__.py``):
+
+* ``chunk_gated_delta_rule_to_cache``  -- ``vendor/fla/gated_delta.py:15-82``
+* ``fused_recurrent_gated_delta_rule_to_slots`` -- ``vendor/fla/fused_recurrent.py:396-458``
+* ``fused_recurrent_gated_delta_rule`` -- ``vendor/fla/fused_recurrent.py:461-550``
+
+All run one hand-written gfx950 kernel each (``libgdn_mi355x.so``).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from ... import _lib
+from .state_io import ChunkLogIO, ChunkStateIO
+
+
+def _check_state_storage(storage: torch.Tensor, hv: int, dk: int, dv: int) -> None:
+    assert storage.ndim == 5 and tuple(storage.shape[2:]) == (hv, dk, dv), storage.shape
+    assert storage.stride(4) == 1 and storage.stride(3) == dv, "state rows must be contiguous"
+
+
+@torch.compiler.disable
+def chunk_gated_delta_rule_to_cache(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    gate: torch.Tensor,
+    beta: torch.Tensor,
+    state_io: ChunkStateIO,
+    cu_seqlens: torch.Tensor,
+    chunk_size: int = 64,
+    chunk_indices: torch.Tensor | None = None,
+    chunk_offsets: torch.Tensor | None = None,
+    *,
+    log_io: ChunkLogIO | None = None,
+    out: torch.Tensor | None = None,
+    return_v_new: bool = True,
+) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """Chunked gated delta rule over packed sequences with pool I/O
+    (``gated_delta.py:15-82``): initial state of sequence n from
+    ``storage[read_slots[n], layer]`` (zero if negative), chunk-end states to
+    ``storage[chunk_write_slots[c], layer]`` for every 64-token chunk ``c``
+    with a non-negative slot, optional final states to ``final_write_slots``.
+    ``gate`` is the natural-log decay and ``beta`` the prepared write strength
+    (``prepare_gdn`` outputs).  Returns ``(o, v_new)``; ``v_new`` is
+    ``u - w h`` (None when ``return_v_new=False``).
+
+    ``chunk_indices``/``chunk_offsets`` are accepted for signature
+    compatibility (the kernel derives chunk boundaries from ``cu_seqlens``).
+    """
+    del chunk_offsets
+    assert query.shape[0] == key.shape[0] == value.shape[0] == 1
+    assert chunk_size in (16, 32, 64)
+    assert cu_seqlens.ndim == 1
+    assert len(cu_seqlens) == len(state_io.read_slots) + 1
+    if chunk_size != 64:
+        raise NotImplementedError("the MI355X chunk kernel is specialised for chunk_size=64")
+    if log_io is not None or state_io.payload_frames is not None:
+        raise NotImplementedError("LogState state I/O is not supported by the MI355X backend")
+    _, T, H, dk = query.shape
+    HV, dv = value.shape[2:]
+    assert key.shape == query.shape and value.shape[:2] == query.shape[:2]
+    assert HV % H == 0
+    assert gate.shape == beta.shape == (1, T, HV)
+    storage = state_io.storage
+    _check_state_storage(storage, HV, dk, dv)
+    assert storage.device == query.device
+    if chunk_indices is not None:
+        assert state_io.chunk_write_slots.shape == (len(chunk_indices),)
+    if state_io.final_write_slots is not None:
+        assert state_io.final_write_slots.shape == state_io.read_slots.shape
+    query, key, value = query.contiguous(), key.contiguous(), value.contiguous()
+    gate = gate.float().contiguous()
+    beta = beta.float().contiguous()
+    o = torch.empty_like(value) if out is None else out
+    assert o.shape == value.shape and o.dtype == value.dtype and o.is_contiguous()
+    v_new = torch.empty_like(value) if return_v_new else None
+    if T:
+        fw = state_io.final_write_slots
+        _lib.call(
+            "gdn_chunk_gated_delta_rule",
+            query.data_ptr(), key.data_ptr(), value.data_ptr(), _lib.dtype_code(value.dtype),
+            gate.data_ptr(), beta.data_ptr(), cu_seqlens.data_ptr(), _lib.index_code(cu_seqlens),
+            len(cu_seqlens) - 1, T, H, HV, dk, dv,
+            storage.data_ptr(), _lib.dtype_code(storage.dtype), storage.stride(0), storage.stride(1),
+            storage.stride(2), state_io.layer,
+            state_io.read_slots.data_ptr(), _lib.index_code(state_io.read_slots),
+            state_io.chunk_write_slots.data_ptr(), _lib.index_code(state_io.chunk_write_slots),
+            _lib.ptr(fw), _lib.index_code(fw) if fw is not None else 0,
+            o.data_ptr(), _lib.ptr(v_new), float(dk) ** -0.5, _lib.stream_of(query),
+        )
+    return o, v_new
+
+
+def _gates(gate: torch.Tensor, beta: torch.Tensor, A_log: torch.Tensor, dt_bias: torch.Tensor):
+    A_log = A_log.contiguous()
+    dt_bias = dt_bias.contiguous()
+    return gate, beta, A_log, dt_bias
+
+
+@torch.compiler.disable
+def fused_recurrent_gated_delta_rule_to_slots(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    gate: torch.Tensor,
+    beta: torch.Tensor,
+    A_log: torch.Tensor,
+    dt_bias: torch.Tensor,
+    state_pool: torch.Tensor,
+    read_slots: torch.Tensor,
+    write_slots: torch.Tensor,
+    layer: int,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """fused_recurrent.py:396-458: one decode step per sequence with the state
+    read from ``state_pool[read_slots[b], layer]`` and written to
+    ``state_pool[write_slots[b], layer]`` (in place when equal).  Raw inputs:
+    q/k are L2-normalised, ``g = -exp(A_log) softplus(gate + dt_bias)`` and
+    ``beta = sigmoid(beta)`` inside the kernel."""
+    batch_size, seq_len, num_k_heads, head_k_dim = query.shape
+    num_v_heads, head_v_dim = value.shape[2:]
+    assert seq_len == 1 and state_pool.ndim == 5
+    assert read_slots.shape == write_slots.shape == (batch_size,)
+    assert tuple(state_pool.shape[2:]) == (num_v_heads, head_k_dim, head_v_dim)
+    assert num_v_heads % num_k_heads == 0
+    _check_state_storage(state_pool, num_v_heads, head_k_dim, head_v_dim)
+    output = torch.empty_like(value) if out is None else out
+    assert output.shape == value.shape and output.dtype == value.dtype and output.is_contiguous()
+    if batch_size == 0:
+        return output
+    query, key, value = query.contiguous(), key.contiguous(), value.contiguous()
+    gate, beta, A_log, dt_bias = _gates(gate, beta, A_log, dt_bias)
+    _lib.call(
+        "gdn_fused_recurrent",
+        query.data_ptr(), key.data_ptr(), value.data_ptr(), _lib.dtype_code(value.dtype),
+        gate.data_ptr(), gate.stride(0), gate.stride(1), gate.stride(2), _lib.dtype_code(gate.dtype),
+        beta.data_ptr(), beta.stride(0), beta.stride(1), beta.stride(2), _lib.dtype_code(beta.dtype),
+        A_log.data_ptr(), _lib.dtype_code(A_log.dtype), dt_bias.data_ptr(), _lib.dtype_code(dt_bias.dtype),
+        batch_size, 1, num_k_heads, num_v_heads, head_k_dim, head_v_dim,
+        state_pool.data_ptr(), _lib.dtype_code(state_pool.dtype), state_pool.stride(0), state_pool.stride(1),
+        state_pool.stride(2), int(layer),
+        read_slots.data_ptr(), read_slots.stride(0), _lib.index_code(read_slots),
+        write_slots.data_ptr(), write_slots.stride(0), 0, _lib.index_code(write_slots),
+        None, None, output.data_ptr(), float(head_k_dim) ** -0.5, _lib.stream_of(query),
+    )
+    return output
+
+
+@torch.compiler.disable
+def fused_recurrent_gated_delta_rule(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    gate: torch.Tensor,
+    beta: torch.Tensor,
+    A_log: torch.Tensor,
+    dt_bias: torch.Tensor,
+    initial_state: torch.Tensor,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """fused_recurrent.py:461-550: T recurrent steps from ``initial_state``
+    [B, HV, dk, dv]; returns ``(o [B, T, HV, dv], states [B, T, HV, dk, dv])``
+    with every per-step state kept (the reference verify path)."""
+    assert query.is_cuda and key.is_cuda and value.is_cuda
+    assert query.ndim == key.ndim == value.ndim == 4
+    batch_size, seq_len, num_k_heads, head_k_dim = query.shape
+    num_v_heads, head_v_dim = value.shape[2:]
+    assert key.shape == query.shape
+    assert value.shape[:2] == (batch_size, seq_len)
+    assert num_v_heads % num_k_heads == 0
+    assert gate.shape == beta.shape == (batch_size, seq_len, num_v_heads)
+    assert initial_state.shape == (batch_size, num_v_heads, head_k_dim, head_v_dim)
+    query, key, value = query.contiguous(), key.contiguous(), value.contiguous()
+    initial_state = initial_state.contiguous()
+    output = torch.empty_like(value)
+    states = torch.empty(batch_size, seq_len, num_v_heads, head_k_dim, head_v_dim,
+                         dtype=initial_state.dtype, device=initial_state.device)
+    if batch_size == 0 or seq_len == 0:
+        return output, states
+    gate, beta, A_log, dt_bias = _gates(gate, beta, A_log, dt_bias)
+    _lib.call(
+        "gdn_fused_recurrent",
+        query.data_ptr(), key.data_ptr(), value.data_ptr(), _lib.dtype_code(value.dtype),
+        gate.data_ptr(), gate.stride(0), gate.stride(1), gate.stride(2), _lib.dtype_code(gate.dtype),
+        beta.data_ptr(), beta.stride(0), beta.stride(1), beta.stride(2), _lib.dtype_code(beta.dtype),
+        A_log.data_ptr(), _lib.dtype_code(A_log.dtype), dt_bias.data_ptr(), _lib.dtype_code(dt_bias.dtype),
+        batch_size, seq_len, num_k_heads, num_v_heads, head_k_dim, head_v_dim,
+        None, _lib.dtype_code(initial_state.dtype), 0, 0, 0, 0,
+        None, 0, 0, None, 0, 0, 0,
+        initial_state.data_ptr(), states.data_ptr(), output.data_ptr(), float(head_k_dim) ** -0.5,
+        _lib.stream_of(query),
+    )
+    return output, states
+
+
+__all__ = [
+    "ChunkLogIO",
+    "ChunkStateIO",
+    "chunk_gated_delta_rule_to_cache",
+    "fused_recurrent_gated_delta_rule",
+    "fused_recurrent_gated_delta_rule_to_slots",
+]

@@ -1,0 +1,44 @@
+"""State-pool descriptors of the chunked prefill (reference
+``python/logssms/kernel/linear_attention/state_io.py:15-39``)."""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+
+@dataclass(frozen=True)
+class ChunkStateIO:
+    """state_io.py:15-28.  ``storage`` is ``[slots, layers, HV, dk, dv]``
+    (any slot/layer/head strides, inner dims contiguous).  ``payload_frames``
+    and the frame/log fields describe the LogState layout and are rejected
+    with ``NotImplementedError`` when set."""
+
+    storage: torch.Tensor
+    read_slots: torch.Tensor
+    chunk_write_slots: torch.Tensor
+    final_write_slots: torch.Tensor | None = None
+    payload_frames: torch.Tensor | None = None
+    frame_bytes: int = 0
+    head_payload_bytes: int = 0
+    layer: int = 0
+    num_layers: int = 1
+    granularity: int = 64
+    page_size: int = 64
+
+
+@dataclass(frozen=True)
+class ChunkLogIO:
+    """state_io.py:31-39 (LogState only; accepted for signature compatibility)."""
+
+    slots: torch.Tensor
+    token_offsets: torch.Tensor
+    decay_frames: torch.Tensor
+    gate: torch.Tensor
+    page_size: int
+    decay_record_bytes: int
+    num_key_heads: int
+
+
+__all__ = ["ChunkStateIO", "ChunkLogIO"]
