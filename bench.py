@@ -1,0 +1,302 @@
+"""Benchmark of the MI355X Gated DeltaNet hot path.
+
+Headline (``value``): Qwen3-Next linear-attention layer prefill (BASELINE
+config 2) -- 4 x 4096 packed tokens, 16 qk / 32 v heads, d = 128, bf16
+q/k/v, fp32 state pool, conv width 4.  One step = the backend prefill:
+``prefill_frontend`` (conv-history gather, packed conv + SiLU + window
+snapshots, split, prepare_gdn) followed by the chunked gated-delta-rule kernel
+writing the output and the final per-sequence states into pool slots.
+``value`` is prefill tokens/s; ``roofline`` reports the chunk kernel against
+the dense 16-bit MFMA peak from the algorithmic flop count
+(10 C d + 6 d^2 + 2/3 C^2 per token per v-head).
+
+``extra`` reports the HBM-bound paths: decode (config 3) and spec-decode
+verify (config 5) in GB/s against 8 TB/s, from the canonical byte formulas.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_MFMA_16BIT = 2.5e15  # MI355X dense bf16/fp16 FLOP/s
+PEAK_HBM = 8.0e12  # MI355X HBM3E bytes/s
+
+H, HV, D, W = 16, 32, 128, 4
+CONV_DIM = 2 * H * D + HV * D  # 8192
+C = 64
+FLOP_PER_TOKEN_HEAD = 10 * C * D + 6 * D * D + (2 / 3) * C * C  # 182,954.67
+S_BYTES = HV * D * D * 4  # fp32 state per sequence
+SC_BYTES = CONV_DIM * (W - 1) * 2  # bf16 conv window per sequence
+
+
+def _config(layer=0):
+    from logssms_amd.layers import GatedDeltaConfig
+    return GatedDeltaConfig(H, HV, D, D, CONV_DIM, W - 1, layer)
+
+
+def _time(fn, steps, warmup, events=None):
+    """Times `steps` calls of fn between synchronize barriers; returns ms/step.
+    `events` (list) collects per-kernel (start, end) pairs recorded inside fn."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    if events is not None:
+        events.clear()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def _kernel_ms(events):
+    if not events:
+        return None
+    return sum(a.elapsed_time(b) for a, b in events) / len(events)
+
+
+# ---------------------------------------------------------------- prefill (config 2)
+
+def make_prefill(seed=2, lengths=(4096, 4096, 4096, 4096)):
+    g = torch.Generator().manual_seed(seed)
+    T = sum(lengths)
+    N = len(lengths)
+    cu = [0]
+    for n in lengths:
+        cu.append(cu[-1] + n)
+    mixed = torch.randn(T, CONV_DIM, generator=g).to(torch.bfloat16)
+    weight = (torch.randn(CONV_DIM, 1, W, generator=g) * 0.02).to(torch.bfloat16)
+    gate = torch.randn(T, HV, generator=g).to(torch.bfloat16)
+    beta = torch.randn(T, HV, generator=g).to(torch.bfloat16)
+    A_log = -torch.rand(HV, generator=g)  # g = -softplus(a) * exp(U(-1, 0))
+    dt_bias = torch.zeros(HV)
+    nchunks = [(n + C - 1) // C for n in lengths]
+    chunk_write = torch.full((sum(nchunks),), -1, dtype=torch.int64)
+    off = 0
+    for i, nc in enumerate(nchunks):
+        off += nc
+        chunk_write[off - 1] = i  # final state of sequence i -> pool slot i
+    return dict(mixed=mixed, weight=weight, gate=gate, beta=beta, A_log=A_log, dt_bias=dt_bias,
+                cu=torch.tensor(cu), baseline=torch.full((N,), -1, dtype=torch.int64), chunk_write=chunk_write,
+                conv_tokens=torch.full((T,), -1, dtype=torch.int64), N=N, T=T)
+
+
+def prefill_gpu(inp, dev, events=None):
+    from logssms_amd.kernel.linear_attention import ChunkStateIO, chunk_gated_delta_rule_to_cache
+    from logssms_amd.kernel.linear_attention.fused_backend import prefill_frontend
+    cfg = _config()
+    d = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    conv_pool = torch.zeros(max(8, d["N"]), 1, CONV_DIM, W - 1, device=dev, dtype=torch.bfloat16)
+    state_pool = torch.zeros(max(8, d["N"]), 1, HV, D, D, device=dev, dtype=torch.float32)
+    out = torch.empty(1, d["T"], HV, D, device=dev, dtype=torch.bfloat16)
+    io = ChunkStateIO(state_pool, d["baseline"], d["chunk_write"], layer=0)
+
+    def step():
+        q, k, v, g, b = prefill_frontend(d["mixed"], d["gate"], d["beta"], d["weight"], d["A_log"], d["dt_bias"],
+                                         cfg, conv_pool, d["cu"], d["baseline"], d["conv_tokens"])
+        if events is not None:
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+        chunk_gated_delta_rule_to_cache(q, k, v, g, b, io, d["cu"], out=out, return_v_new=False)
+        if events is not None:
+            e.record()
+            events.append((s, e))
+        return out
+
+    return step, state_pool, out
+
+
+def prefill_cpu_sample(inp, tokens, threads):
+    """Times the oracle's chunked restatement (conv + prepare + chunk rule) on
+    the first `tokens` tokens of sequence 0 at full head count."""
+    from oracle import gdn as ref
+    torch.set_num_threads(threads)
+    mixed = inp["mixed"][:tokens]
+    gate = inp["gate"][:tokens]
+    beta = inp["beta"][:tokens]
+    conv = torch.zeros(1, 1, CONV_DIM, W - 1, dtype=torch.bfloat16)
+    state = torch.zeros(1, 1, HV, D, D)
+    nc = (tokens + C - 1) // C
+    t0 = time.perf_counter()
+    ref.forward_prefill(mixed, gate, beta, inp["weight"], inp["A_log"], inp["dt_bias"], conv, state, 0,
+                        [0, tokens], [-1], [-1] * nc, [-1] * tokens, H, D, HV, D)
+    return time.perf_counter() - t0
+
+
+# ---------------------------------------------------------------- decode (config 3) / verify (config 5)
+
+def decode_bytes(B):
+    return B * (2 * S_BYTES + 2 * SC_BYTES + 2 * CONV_DIM + 2 * HV * D + 4 * HV) + CONV_DIM * W * 2 + 8 * HV
+
+
+def verify_bytes(B, T):
+    return (B * ((1 + T) * S_BYTES + (1 + T) * SC_BYTES + T * (2 * CONV_DIM + 2 * HV * D + 4 * HV))
+            + CONV_DIM * W * 2 + 8 * HV)
+
+
+def make_pools(g, slots, dev):
+    state = torch.empty(slots, 1, HV, D, D, device=dev)
+    state.normal_(0.0, 0.1, generator=torch.Generator(device=dev).manual_seed(int(torch.randint(1 << 30, (1,),
+                                                                                                generator=g))))
+    conv = torch.randn(slots, 1, CONV_DIM, W - 1, device=dev).to(torch.bfloat16)
+    return state, conv
+
+
+def decode_gpu(dev, B=256, slots=1024, seed=3, events=None):
+    from logssms_amd.kernel.linear_attention.fused_backend import decode_step
+    g = torch.Generator().manual_seed(seed)
+    cfg = _config()
+    state, conv = make_pools(g, slots, dev)
+    slot_idx = torch.randperm(slots, generator=g)[:B].to(dev)
+    mixed = torch.randn(B, CONV_DIM, generator=g).to(torch.bfloat16).to(dev)
+    gate = torch.randn(B, HV, generator=g).to(torch.bfloat16).to(dev)
+    beta = torch.randn(B, HV, generator=g).to(torch.bfloat16).to(dev)
+    weight = (torch.randn(CONV_DIM, 1, W, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    A_log = (-torch.rand(HV, generator=g)).to(dev)
+    dt_bias = torch.zeros(HV, device=dev)
+    out = torch.empty(B, HV, D, device=dev, dtype=torch.bfloat16)
+
+    def step():
+        decode_step(mixed, gate, beta, weight, A_log, dt_bias, cfg, conv, state, slot_idx, slot_idx, out=out)
+
+    return step
+
+
+def verify_gpu(dev, B=64, T=8, slots=1024, seed=5):
+    from logssms_amd.kernel.linear_attention.fused_backend import verify_group
+    from logssms_amd import _lib
+    g = torch.Generator().manual_seed(seed)
+    cfg = _config()
+    state, conv = make_pools(g, slots, dev)
+    perm = torch.randperm(slots, generator=g)
+    live = perm[:B].to(dev)
+    writes = perm[B:B + B * T].view(B, T).to(dev)
+    accepted = torch.randint(1, T + 1, (B,), generator=g).to(dev)
+    rows = B * T
+    mixed = torch.randn(rows, CONV_DIM, generator=g).to(torch.bfloat16).to(dev)
+    gate = torch.randn(rows, HV, generator=g).to(torch.bfloat16).to(dev)
+    beta = torch.randn(rows, HV, generator=g).to(torch.bfloat16).to(dev)
+    weight = (torch.randn(CONV_DIM, 1, W, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    A_log = (-torch.rand(HV, generator=g)).to(dev)
+    dt_bias = torch.zeros(HV, device=dev)
+    out = torch.empty(rows, HV, D, device=dev, dtype=torch.bfloat16)
+
+    def step():
+        verify_group(mixed, gate, beta, weight, A_log, dt_bias, cfg, conv, state, None, live, writes, out)
+
+    def commit():
+        _lib.call("gdn_commit_accepted", state.data_ptr(), state.stride(0) * 4, 0, S_BYTES, conv.data_ptr(),
+                  conv.stride(0) * 2, 0, SC_BYTES, live.data_ptr(), 1, writes.data_ptr(), T, 1, 1,
+                  accepted.data_ptr(), 1, B, T, _lib.stream_of(state))
+
+    return step, commit
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--only", choices=["all", "prefill", "decode", "verify"], default="all")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the GDN path shards by heads/sequences with no collective; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    result = {}
+    extra = {}
+
+    if args.only in ("all", "prefill"):
+        inp = make_prefill()
+        events = []
+        step, state_pool, out = prefill_gpu(inp, dev, events)
+        ms = _time(step, args.steps, args.warmup, events)
+        chunk_ms = _kernel_ms(events)
+        T = inp["T"]
+        flops = FLOP_PER_TOKEN_HEAD * T * HV
+        achieved = flops / (chunk_ms * 1e-3)
+        # HBM traffic of the chunk kernel (algorithmic): q,k,v in, o out, g/beta in, final states out
+        chunk_bytes = T * (2 * H * D * 2 + HV * D * 2) + T * HV * D * 2 + 2 * T * HV * 4 + inp["N"] * S_BYTES
+        result.update(
+            metric="GDN prefill tokens/s (Qwen3-Next layer, 4x4096 packed)",
+            value=T / (ms * 1e-3),
+            unit="tokens/s",
+            n_gpus=1, steps=args.steps, warmup=args.warmup, ms_per_step=ms,
+            higher_is_better=True, scaling="weak", vs_baseline=None,
+            dtype="bf16 in / fp16 MFMA operands / fp32 state",
+            data="synthetic (seeded N(0,1) mixed_qkv, conv w N(0,0.02), zero initial state)",
+            config={"workload": "BASELINE config 2: Qwen3-Next GDN layer prefill", "global_batch": inp["N"],
+                    "seq_len": 4096, "heads_qk": H, "heads_v": HV, "head_dim": D, "chunk": C,
+                    "parallelism": "single GPU"},
+            roofline={"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_MFMA_16BIT / 1e12,
+                      "unit": "TFLOP/s", "frac": achieved / PEAK_MFMA_16BIT, "traffic": None,
+                      "kernel": "chunk_kernel", "kernel_ms": chunk_ms,
+                      "algorithmic_flop_per_launch": flops, "algorithmic_bytes_per_launch": chunk_bytes},
+        )
+        extra["prefill_frontend_ms"] = ms - chunk_ms
+        if not args.no_cpu_baseline:
+            threads = len(os.sched_getaffinity(0))
+            sample = 4096
+            times = []
+            t_start = time.perf_counter()
+            while not times or (time.perf_counter() - t_start < args.cpu_seconds and len(times) < 50):
+                times.append(prefill_cpu_sample(inp, sample, threads))
+            times.sort()
+            med = times[len(times) // 2]
+            result["cpu_baseline"] = {
+                "value": sample / med, "unit": "tokens/s", "cores": threads, "kind": "port",
+                "sample": f"oracle forward_prefill (conv+prepare+chunked rule, fp32 torch) on the first {sample} "
+                          f"tokens of sequence 0 at full head count; median of {len(times)} runs",
+            }
+            torch.set_num_threads(threads)
+
+    if args.only in ("all", "decode"):
+        step = decode_gpu(dev)
+        ms = _time(step, max(args.steps, 20), args.warmup)
+        nb = decode_bytes(256)
+        extra["decode"] = {"config": "BASELINE config 3 (256 seqs, in-place RMW of randperm pool slots)",
+                           "ms": ms, "bytes": nb, "GB/s": nb / (ms * 1e-3) / 1e9,
+                           "frac_hbm": nb / (ms * 1e-3) / PEAK_HBM}
+    if args.only in ("all", "verify"):
+        step, commit = verify_gpu(dev)
+        ms = _time(step, max(args.steps, 20), args.warmup)
+        nb = verify_bytes(64, 8)
+        cms = _time(commit, max(args.steps, 20), args.warmup)
+        cb = 64 * 2 * (S_BYTES + SC_BYTES)
+        extra["verify"] = {"config": "BASELINE config 5 (64 seqs x 8 drafts, per-step states to slots)",
+                           "ms": ms, "bytes": nb, "GB/s": nb / (ms * 1e-3) / 1e9,
+                           "frac_hbm": nb / (ms * 1e-3) / PEAK_HBM,
+                           "commit_ms": cms, "commit_GB/s": cb / (cms * 1e-3) / 1e9}
+    if not result:
+        key = "decode" if "decode" in extra else "verify"
+        e = extra[key]
+        result.update(metric=f"GDN {key} state-update GB/s", value=e["GB/s"], unit="GB/s", n_gpus=1,
+                      steps=args.steps, warmup=args.warmup, ms_per_step=e["ms"], higher_is_better=True,
+                      scaling="weak", vs_baseline=None, dtype="bf16 io / fp32 state", data="synthetic",
+                      config={"workload": e["config"]},
+                      roofline={"bound": "hbm", "achieved": e["GB/s"], "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                                "frac": e["frac_hbm"], "traffic": None})
+    result["extra"] = extra
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()
