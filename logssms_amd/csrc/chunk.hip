@@ -14,18 +14,25 @@
 // W and U: the state pass needs only k h (the same product the reference
 // spends on w h) plus one 64x64 triangular product.
 //
-// Mapping: one workgroup (4 waves) per (sequence, v-head, 64-column slice of
-// d_v), walking the sequence's chunks in order.  The fp32 state slice
-// (d_k x 64) lives in MFMA accumulator registers for the whole sequence; a
-// half-precision copy is staged in LDS as the B operand of the next chunk's
-// products.  All dense products run on v_mfma_f32_16x16x32_f16 with fp32
-// accumulation: operands are held in fp16 whatever the input dtype (bf16
-// inputs convert exactly), because fp16's 10-bit mantissa keeps the carried
-// fp32 state within 1e-3 of an fp32 recurrence where bf16 operands drift to
-// ~4e-3, at the same MFMA rate.  Operand magnitudes must stay below 65504
-// (values are saturated there).  The 16x16 diagonal blocks of the triangular
-// inverse use fp32 forward substitution and the off-diagonal blocks fp32
-// products (the reference solves in fp32 as well).
+// Mapping: one workgroup per (sequence, v-head, 64-column slice of d_v),
+// walking the sequence's chunks in order, 8 waves software-pipelined:
+//   * state waves 0-3 run only the recurrence chain of chunk c in three
+//     barrier-separated stages: (I) k h -> R, (II) A R -> v', (III)
+//     h <- 2^G_last h + (2^(G_last-G) k)^T v'.  The fp32 state slice
+//     (d_k x 64) lives in MFMA accumulators for the whole sequence; an f16
+//     copy is staged in LDS as the B operand of the next chunk's products.
+//   * side waves 4-7 do everything off that chain in the same stages: the
+//     global prefetch of later chunks into registers, M = q k^T tiles and
+//     o = 2^G q h + M v' of chunk c, and the triangular inverse
+//     A = (I + L)^-1 of chunk c+1 (k k^T tiles; 16x16 diagonal blocks by fp32
+//     forward substitution; off-diagonal blocks by block products on
+//     split-f16 MFMA -- x = hi + lo -- which keeps them at ~fp32 accuracy).
+// All dense products run on v_mfma_f32_16x16x32_f16 with fp32 accumulation:
+// operands are held in fp16 whatever the input dtype (bf16 inputs convert
+// exactly), because fp16's 10-bit mantissa keeps the carried fp32 state
+// within 1e-3 of an fp32 recurrence where bf16 operands drift to ~4e-3, at
+// the same MFMA rate.  Operand magnitudes must stay below 65504 (values are
+// saturated there).
 // Workgroups sharing a key head (HV/H v-heads x slices) get block ids that
 // are equal modulo 8, so they land on the same XCD and share its L2 for q/k.
 //
@@ -37,7 +44,7 @@ namespace gdn {
 namespace {
 
 constexpr int kC = 64;
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
 constexpr float kRcpLn2 = 1.4426950216f;  // gated_delta.py:12
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -90,29 +97,35 @@ template <> __device__ __forceinline__ uint4 to_operands<bf16>(uint4 raw) {
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+// fp32 16x16 blocks of the triangular solve live in LDS with a row stride of
+// 20 floats: 16-byte row reads of 16 different rows hit distinct banks.
+constexpr int LDB = 20;
+constexpr int BLK = 16 * LDB;
+__device__ __forceinline__ int blk(int ti, int tj) { return ti * (ti + 1) / 2 + tj; }
+
 // LDS carve-up (bytes).  Row paddings of 8 halfs keep 16-byte fragment reads
 // of consecutive rows on different banks.
 template <int DK, int DVS>
 struct Smem {
-  static constexpr int LDK = DK + 8;   // Kr, Qr: [64][LDK] token-major
-  static constexpr int LDT = kC + 8;   // Ktd [DK][LDT], Ab/Mb [64][LDT], Rt/Vt [DVS][LDT]
-  static constexpr int LDF = kC + 4;   // Lf/Af fp32 [64][LDF]
-  static constexpr int LDV = DVS + 8;  // Vr [64][LDV]
-  static constexpr int LDH = DK + 8;   // ht [DVS][LDH]
-  static constexpr size_t kr = 0;
-  static constexpr size_t qr = kr + 2ull * kC * LDK;
-  static constexpr size_t ktd = qr + 2ull * kC * LDK;
-  static constexpr size_t vr = ktd + 2ull * DK * LDT;
-  static constexpr size_t ab = vr + 2ull * kC * LDV;
-  static constexpr size_t mb = ab + 2ull * kC * LDT;
+  static constexpr int LDK = DK + 8;   // Kb[2], Qb: [64][LDK] token-major f16
+  static constexpr int LDT = kC + 8;   // A16[2], Mb: [64][LDT]; Rt/Vt: [DVS][LDT]
+  static constexpr int LDV = DVS + 8;  // Vb: [64][LDV]
+  static constexpr int LDH = DK + 8;   // Ht: [DVS][LDH] (h transposed)
+  static constexpr int GT = 4 * kC + 4;  // G, 2^G, 2^(G_last-G), beta, 2^G_last
+  static constexpr size_t kb = 0;
+  static constexpr size_t qb = kb + 2 * 2ull * kC * LDK;
+  static constexpr size_t vb = qb + 2ull * kC * LDK;
+  static constexpr size_t gt = vb + 2ull * kC * LDV;
+  static constexpr size_t lf = gt + 2 * 4ull * GT;
+  static constexpr size_t af = lf + 10 * 4ull * BLK;
+  static constexpr size_t a16 = af + 10 * 4ull * BLK;
+  static constexpr size_t mb = a16 + 2 * 2ull * kC * LDT;
   static constexpr size_t rt = mb + 2ull * kC * LDT;
   static constexpr size_t vt = rt + 2ull * DVS * LDT;
   static constexpr size_t ht = vt + 2ull * DVS * LDT;
-  static constexpr size_t lf = ht + 2ull * DVS * LDH;
-  static constexpr size_t af = lf + 4ull * kC * LDF;
-  static constexpr size_t tmp = af + 4ull * kC * LDF;  // 4 scratch 16x16 fp32 tiles
-  static constexpr size_t gates = tmp + 4ull * 4 * 256;
-  static constexpr size_t total = gates + 4ull * (4 * kC + 4);
+  static constexpr size_t tmp = ht + 2ull * DVS * LDH;
+  static constexpr size_t total = tmp + 2 * 2 * 4ull * BLK;
+  static_assert(total <= 160 * 1024, "LDS budget");
 };
 
 struct ChunkParams {
@@ -139,24 +152,80 @@ struct ChunkParams {
   int members;  // workgroups per (sequence, key head)
 };
 
-// 16-byte fragment: row (row0 + lane % 16), halfs k0 + 8 (lane / 16) .. + 7.
-template <class IOT>
-__device__ __forceinline__ typename Mma<IOT>::frag frag_at(const uint16_t* base, int ld, int row0, int k0, int lane) {
-  return *reinterpret_cast<const typename Mma<IOT>::frag*>(base + (row0 + (lane & 15)) * ld + k0 + 8 * (lane >> 4));
-}
+typedef f16x8_t frag_t;
 
-// (X Y)[row][col0 .. col0+3] for 16x16 fp32 tiles, row = lane / 4, col0 = 4 (lane % 4).
-__device__ __forceinline__ void mm16(const float* X, int ldx, const float* Y, int ldy, int lane, float (&acc)[4]) {
-  const int row = lane >> 2, col0 = 4 * (lane & 3);
+// 16-byte f16 fragment: row (row0 + lane % 16), halfs k0 + 8 (lane / 16) .. + 7.
+__device__ __forceinline__ frag_t frag_at(const uint16_t* base, int ld, int row0, int k0, int lane) {
+  return *reinterpret_cast<const frag_t*>(base + (row0 + (lane & 15)) * ld + k0 + 8 * (lane >> 4));
+}
+__device__ __forceinline__ f32x4 mma(frag_t a, frag_t b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// Synchronisation.  Every cross-wave hand-off in this kernel goes through
+// LDS, and nothing the kernel writes to global memory is read back by it, so
+// barriers wait only for LDS traffic (lgkmcnt) -- not for the global
+// prefetch loads still in flight, which a full __syncthreads() fence would
+// drain every stage.  The asm "memory" clobber keeps the compiler from moving
+// memory accesses across either point.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// In-wave LDS hand-off (DS operations of one wave execute in order).
+__device__ __forceinline__ void wave_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// ---- split-f16 products on fp32 LDS blocks: x = hi + lo, both f16, so a
+// product of hi/lo pairs (dropping lo*lo) carries ~fp32 accuracy.
+struct Split {
+  frag_t hi, lo;
+};
+__device__ __forceinline__ Split split8(const float (&x)[8]) {
+  Split s;
 #pragma unroll
-  for (int kk = 0; kk < 16; ++kk) {
-    const float x = X[row * ldx + kk];
-    const float4 y = *reinterpret_cast<const float4*>(Y + kk * ldy + col0);
-    acc[0] = fmaf(x, y.x, acc[0]);
-    acc[1] = fmaf(x, y.y, acc[1]);
-    acc[2] = fmaf(x, y.z, acc[2]);
-    acc[3] = fmaf(x, y.w, acc[3]);
+  for (int e = 0; e < 8; ++e) {
+    const f16 h = static_cast<f16>(x[e]);
+    s.hi[e] = h;
+    s.lo[e] = static_cast<f16>(x[e] - static_cast<float>(h));
   }
+  return s;
+}
+// A operand of a 16 x 32 matrix [X0 | X1] (fp32 blocks; nullptr = zero block).
+__device__ __forceinline__ Split a_operand(const float* X0, const float* X1, int lane) {
+  const int row = lane & 15, kq = lane >> 4;
+  const float* X = kq < 2 ? X0 : X1;
+  float x[8];
+  if (X) {
+    const float4 a = *reinterpret_cast<const float4*>(X + row * LDB + 8 * (kq & 1));
+    const float4 b = *reinterpret_cast<const float4*>(X + row * LDB + 8 * (kq & 1) + 4);
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = 0.f;
+  }
+  return split8(x);
+}
+// B operand of a 32 x 16 matrix [Y0; Y1].
+__device__ __forceinline__ Split b_operand(const float* Y0, const float* Y1, int lane) {
+  const int col = lane & 15, kq = lane >> 4;
+  const float* Y = kq < 2 ? Y0 : Y1;
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = Y ? Y[(8 * (kq & 1) + e) * LDB + col] : 0.f;
+  return split8(x);
+}
+__device__ __forceinline__ f32x4 mma_split(const Split& a, const Split& b, f32x4 c) {
+  c = mma(a.hi, b.hi, c);
+  c = mma(a.hi, b.lo, c);
+  return mma(a.lo, b.hi, c);
+}
+// C-layout tile (rows 4 (lane/16) + e, col lane % 16) -> fp32 block.
+__device__ __forceinline__ void store_block(float* B, f32x4 v, int lane, float sign) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) B[(4 * (lane >> 4) + e) * LDB + (lane & 15)] = sign * v[e];
+}
+__device__ __forceinline__ void store_a16(uint16_t* A16, int ld, int ti, int tj, f32x4 v, int lane, float sign) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    A16[(ti * 16 + 4 * (lane >> 4) + e) * ld + tj * 16 + (lane & 15)] = op_bits(sign * v[e]);
 }
 
 template <class ST> __device__ __forceinline__ float load_st(const ST* p) { return to_f32(*p); }
@@ -165,38 +234,50 @@ template <class ST> __device__ __forceinline__ void store_st(ST* p, float v) { *
 template <int DK, int DVS, class IOT, class ST>
 __global__ __launch_bounds__(kThreads, 1) void chunk_kernel(ChunkParams p) {
   using SM = Smem<DK, DVS>;
-  using M = Mma<f16>;
-  constexpr int HT = DK / 16;         // h row tiles
-  constexpr int CT = DVS / 16;        // column tiles of the slice
-  constexpr int HTILES = HT * CT;     // h tiles, distributed t = wave + 4 i
-  constexpr int HPW = (HTILES + 3) / 4;
-  constexpr int PTILES = 8 * CT;      // [k; q] h tiles (128 rows)
-  constexpr int PPW = PTILES / 4;
-  constexpr int VTILES = 4 * CT;      // v' / o tiles (64 rows)
-  constexpr int VPW = VTILES / 4;
-  static_assert(PTILES % 4 == 0 && VTILES % 4 == 0, "tile split");
+  constexpr int HT = DK / 16;            // h row tiles
+  constexpr int CT = DVS / 16;           // column tiles of the slice
+  constexpr int HRT = (HT + 3) / 4;      // h row tiles per state wave (ti = wave + 4 i)
+  constexpr int KPT = (kC * DK / 8) / 256;   // 16-byte K (or Q) pieces per side thread
+  constexpr int VPT = (kC * DVS / 8) / 256;  // 16-byte V pieces per side thread
+  static_assert(KPT >= 1 && VPT >= 1, "tile split");
 
-  __shared__ __align__(16) char smem[SM::total];
-  uint16_t* Kr = reinterpret_cast<uint16_t*>(smem + SM::kr);
-  uint16_t* Qr = reinterpret_cast<uint16_t*>(smem + SM::qr);
-  uint16_t* Ktd = reinterpret_cast<uint16_t*>(smem + SM::ktd);
-  uint16_t* Vr = reinterpret_cast<uint16_t*>(smem + SM::vr);
-  uint16_t* Ab = reinterpret_cast<uint16_t*>(smem + SM::ab);
-  uint16_t* Mb = reinterpret_cast<uint16_t*>(smem + SM::mb);
-  uint16_t* Rt = reinterpret_cast<uint16_t*>(smem + SM::rt);
-  uint16_t* Vt = reinterpret_cast<uint16_t*>(smem + SM::vt);
-  uint16_t* Ht = reinterpret_cast<uint16_t*>(smem + SM::ht);
-  float* Lf = reinterpret_cast<float*>(smem + SM::lf);
-  float* Af = reinterpret_cast<float*>(smem + SM::af);
-  float* Tmp = reinterpret_cast<float*>(smem + SM::tmp);
-  float* gG = reinterpret_cast<float*>(smem + SM::gates);
-  float* eG = gG + kC;
-  float* eGl = eG + kC;
-  float* bt = eGl + kC;
-  float* misc = bt + kC;  // [0] = 2^G_last
+  // Separate LDS objects (not one carved buffer) so the compiler can tell the
+  // buffers apart and overlap loads of one with stores to another.
+  __shared__ __align__(16) uint16_t sK[2 * kC * SM::LDK];
+  __shared__ __align__(16) uint16_t sQ[kC * SM::LDK];
+  __shared__ __align__(16) uint16_t sV[kC * SM::LDV];
+  __shared__ __align__(16) float sG[2 * SM::GT];
+  __shared__ __align__(16) float sL[10 * BLK];
+  __shared__ __align__(16) float sA[10 * BLK];
+  __shared__ __align__(16) uint16_t sA16[2 * kC * SM::LDT];
+  __shared__ __align__(16) uint16_t sM[kC * SM::LDT];
+  __shared__ __align__(16) uint16_t sR[DVS * SM::LDT];
+  __shared__ __align__(16) uint16_t sVt[DVS * SM::LDT];
+  __shared__ __align__(16) uint16_t sH[DVS * SM::LDH];
+  __shared__ __align__(16) float sT[4 * BLK];
+  uint16_t* Kb0 = sK;
+  uint16_t* Qb = sQ;
+  uint16_t* Vb = sV;
+  float* Gt0 = sG;
+  float* Lf = sL;
+  float* Af = sA;
+  uint16_t* A160 = sA16;
+  uint16_t* Mb = sM;
+  uint16_t* Rt = sR;
+  uint16_t* Vt = sVt;
+  uint16_t* Ht = sH;
+  float* Tmp = sT;
+  auto Kb = [&](int64_t c) { return Kb0 + (c & 1) * kC * SM::LDK; };
+  auto Gt = [&](int64_t c) { return Gt0 + (c & 1) * SM::GT; };
+  auto A16 = [&](int64_t c) { return A160 + (c & 1) * kC * SM::LDT; };
+  auto Lb = [&](int ti, int tj) { return Lf + blk(ti, tj) * BLK; };
+  auto Ab = [&](int ti, int tj) { return Af + blk(ti, tj) * BLK; };
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int lr = lane & 15, lq = lane >> 4;
+  const bool side = wave >= 4;
+  const int sw = wave - 4;      // side wave index
+  const int st_ = tid - 256;    // side thread index
 
   // ---- block -> (sequence, key head, member) with XCD-aware grouping
   const int64_t L = blockIdx.x;
@@ -219,6 +300,10 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_kernel(ChunkParams p) {
     const int64_t lm = load_index(p.cu, m + 1, p.cu_is64) - load_index(p.cu, m, p.cu_is64);
     chunk_base += (lm + kC - 1) / kC;
   }
+  auto valid_rows = [&](int64_t c) -> int {
+    const int64_t rem = len - c * kC;
+    return rem <= 0 ? 0 : (rem < kC ? static_cast<int>(rem) : kC);
+  };
 
   const uint16_t* qg = static_cast<const uint16_t*>(p.q);
   const uint16_t* kg = static_cast<const uint16_t*>(p.k);
@@ -227,288 +312,442 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_kernel(ChunkParams p) {
   uint16_t* vng = static_cast<uint16_t*>(p.v_new);
   ST* pool = static_cast<ST*>(p.state);
 
-  // upper off-diagonal tiles of A and M stay zero for the whole launch
-  for (int e = tid; e < kC * kC; e += kThreads) {
-    const int i = e / kC, j = e % kC;
-    if (j > i) {
-      Ab[i * SM::LDT + j] = 0;
-      Mb[i * SM::LDT + j] = 0;
+  // ---------------------------------------------------------------- side-wave prefetch
+  uint4 pk[KPT], pq[KPT], pv[VPT];
+  float pg = 0.f, pb = 0.f;
+  // Each side thread owns KPT (VPT) consecutive 16-byte pieces of one row, so
+  // a single base address (plus immediate offsets) covers all of them.
+  const int krow = (st_ * KPT) / (DK / 8), kch = (st_ * KPT) % (DK / 8);
+  const int vrow = (st_ * VPT) / (DVS / 8), vch = (st_ * VPT) % (DVS / 8);
+  const uint16_t* kbase = kg + ((bos + krow) * p.H + kh) * DK + kch * 8;
+  const uint16_t* qbase = qg + ((bos + krow) * p.H + kh) * DK + kch * 8;
+  const uint16_t* vbase = vg + ((bos + vrow) * p.HV + h) * p.DV + col_base + vch * 8;
+  const int64_t kstride = kC * p.H * DK;     // one chunk of K/Q rows
+  const int64_t vstride = kC * p.HV * p.DV;  // one chunk of V rows
+  auto prefetch = [&](int64_t ck, int64_t cq) {  // K, g, beta of chunk ck; Q, V of chunk cq
+    const int nk = valid_rows(ck), nq = valid_rows(cq);
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) pk[i] = pq[i] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) pv[i] = make_uint4(0, 0, 0, 0);
+    if (krow < nk) {
+      const uint4* src = reinterpret_cast<const uint4*>(kbase + ck * kstride);
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) pk[i] = src[i];
     }
-  }
-
-  // ---- initial state slice -> accumulators (tile t = wave + 4 i)
-  f32x4 hacc[HPW];
-  {
-    const int64_t rs = load_index(p.read_slots, n, p.read_is64);
-    const ST* src = rs >= 0 ? pool + rs * p.slot_stride + p.layer * p.layer_stride + h * p.head_stride : nullptr;
+    if (krow < nq) {
+      const uint4* src = reinterpret_cast<const uint4*>(qbase + cq * kstride);
 #pragma unroll
-    for (int i = 0; i < HPW; ++i) {
-      const int t = wave + 4 * i;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) hacc[i][e] = 0.f;
-      if (t < HTILES && src) {
-        const int row0 = (t / CT) * 16 + 4 * lq, col = (t % CT) * 16 + lr;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) hacc[i][e] = load_st(src + (row0 + e) * p.DV + col_base + col);
-      }
+      for (int i = 0; i < KPT; ++i) pq[i] = src[i];
     }
-  }
-  auto stage_state = [&]() {  // bf16/f16 copy of h, column-major (B operand)
+    if (vrow < nq) {
+      const uint4* src = reinterpret_cast<const uint4*>(vbase + cq * vstride);
 #pragma unroll
-    for (int i = 0; i < HPW; ++i) {
-      const int t = wave + 4 * i;
-      if (t < HTILES) {
-        const int row0 = (t / CT) * 16 + 4 * lq, col = (t % CT) * 16 + lr;
-        uint2 w;
-        w.x = op_bits(hacc[i][0]) | (static_cast<uint32_t>(op_bits(hacc[i][1])) << 16);
-        w.y = op_bits(hacc[i][2]) | (static_cast<uint32_t>(op_bits(hacc[i][3])) << 16);
-        *reinterpret_cast<uint2*>(Ht + col * SM::LDH + row0) = w;
-      }
+      for (int i = 0; i < VPT; ++i) pv[i] = src[i];
     }
-  };
-  auto store_state_to = [&](int64_t slot_idx) {
-    ST* dst = pool + slot_idx * p.slot_stride + p.layer * p.layer_stride + h * p.head_stride;
-#pragma unroll
-    for (int i = 0; i < HPW; ++i) {
-      const int t = wave + 4 * i;
-      if (t < HTILES) {
-        const int row0 = (t / CT) * 16 + 4 * lq, col = (t % CT) * 16 + lr;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) store_st(dst + (row0 + e) * p.DV + col_base + col, hacc[i][e]);
-      }
+    if (st_ < 64) {
+      const bool ok = st_ < nk;
+      const int64_t off = (bos + ck * kC + (ok ? st_ : 0)) * p.HV + h;
+      pg = ok ? p.g[off] : 0.f;
+      pb = ok ? p.beta[off] : 0.f;
     }
   };
-  stage_state();
-
-  for (int64_t c = 0; c < nchunks; ++c) {
-    const int64_t t0 = bos + c * kC;
-    const int nv = static_cast<int>(len - c * kC < kC ? len - c * kC : kC);
-
-    // ---- phase 0: chunk tiles -> LDS; gates (wave 0)
-    {
-      constexpr int KCH = DK / 8;  // 16-byte chunks per key row
-      for (int e = tid; e < kC * KCH; e += kThreads) {
-        const int row = e / KCH, ch = e % KCH;
-        uint4 kv = make_uint4(0, 0, 0, 0), qv = kv;
-        if (row < nv) {
-          const int64_t off = ((t0 + row) * p.H + kh) * DK + ch * 8;
-          kv = to_operands<IOT>(*reinterpret_cast<const uint4*>(kg + off));
-          qv = to_operands<IOT>(*reinterpret_cast<const uint4*>(qg + off));
-        }
-        *reinterpret_cast<uint4*>(Kr + row * SM::LDK + ch * 8) = kv;
-        *reinterpret_cast<uint4*>(Qr + row * SM::LDK + ch * 8) = qv;
-      }
-      constexpr int VCH = DVS / 8;
-      for (int e = tid; e < kC * VCH; e += kThreads) {
-        const int row = e / VCH, ch = e % VCH;
-        uint4 vv = make_uint4(0, 0, 0, 0);
-        if (row < nv)
-          vv = to_operands<IOT>(
-              *reinterpret_cast<const uint4*>(vg + ((t0 + row) * p.HV + h) * p.DV + col_base + ch * 8));
-        *reinterpret_cast<uint4*>(Vr + row * SM::LDV + ch * 8) = vv;
-      }
-      if (wave == 0) {
-        const bool ok = lane < nv;
-        float x = ok ? p.g[(t0 + lane) * p.HV + h] : 0.f;
-        const float b = ok ? p.beta[(t0 + lane) * p.HV + h] : 0.f;
+  // Prefetched registers -> LDS (K and gates of chunk ck, Q and V of chunk cq).
+  auto stage = [&](int64_t ck, bool with_k, int64_t cq, bool with_qv) {
+    if (with_k) {
+      uint4* dst = reinterpret_cast<uint4*>(Kb(ck) + krow * SM::LDK + kch * 8);
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) dst[i] = to_operands<IOT>(pk[i]);
+      if (st_ < 64) {  // chunk-local cumulative gate, log2 units (cumsum.py:19-75)
+        const int nk = valid_rows(ck);
+        float x = pg;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
           const float y = __shfl_up(x, off, 64);
-          if (lane >= off) x += y;
+          if (st_ >= off) x += y;
         }
         const float G = x * kRcpLn2;
-        const float Glast = __shfl(G, nv - 1, 64);
-        gG[lane] = G;
-        eG[lane] = fast_exp2(G);
-        eGl[lane] = ok ? fast_exp2(Glast - G) : 0.f;
-        bt[lane] = b;
-        if (lane == 0) misc[0] = fast_exp2(Glast);
+        const float Glast = __shfl(G, nk > 0 ? nk - 1 : 0, 64);
+        float* gt = Gt(ck);
+        gt[st_] = G;
+        gt[kC + st_] = fast_exp2(G);
+        gt[2 * kC + st_] = st_ < nk ? fast_exp2(Glast - G) : 0.f;
+        gt[3 * kC + st_] = pb;
+        if (st_ == 0) gt[4 * kC] = fast_exp2(Glast);
       }
     }
-    __syncthreads();
-
-    // ---- phase 1: K Kt, Q Kt (lower tiles), [K; Q] h, decayed K^T
-    for (int e = tid; e < DK * (kC / 2); e += kThreads) {
-      const int d = e / (kC / 2), i = 2 * (e % (kC / 2));
-      const float a = op_val(Kr[i * SM::LDK + d]) * eGl[i];
-      const float b = op_val(Kr[(i + 1) * SM::LDK + d]) * eGl[i + 1];
-      *reinterpret_cast<uint32_t*>(Ktd + d * SM::LDT + i) =
-          op_bits(a) | (static_cast<uint32_t>(op_bits(b)) << 16);
+    if (with_qv) {
+      uint4* qdst = reinterpret_cast<uint4*>(Qb + krow * SM::LDK + kch * 8);
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) qdst[i] = to_operands<IOT>(pq[i]);
+      uint4* vdst = reinterpret_cast<uint4*>(Vb + vrow * SM::LDV + vch * 8);
+#pragma unroll
+      for (int i = 0; i < VPT; ++i) vdst[i] = to_operands<IOT>(pv[i]);
     }
-    for (int s = wave; s < 20; s += 4) {
-      const bool is_q = s >= 10;
-      int idx = is_q ? s - 10 : s;
-      int ti = 0;
-      while (idx > ti) { idx -= ti + 1; ++ti; }
-      const int tj = idx;  // tj <= ti
-      const uint16_t* X = is_q ? Qr : Kr;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  };
+
+  // ---------------------------------------------------------------- side-wave solve pieces
+  // S = K K^T tile (ti, tj) of chunk c -> L values (fp32), C layout.
+  auto skk_tile = [&](int64_t c, int ti, int tj) {
+    const uint16_t* K = Kb(c);
+    f32x4 acc = zero4();
 #pragma unroll
-      for (int k0 = 0; k0 < DK; k0 += 32)
-        acc = M::run(frag_at<f16>(X, SM::LDK, ti * 16, k0, lane), frag_at<f16>(Kr, SM::LDK, tj * 16, k0, lane), acc);
-      const int j = tj * 16 + lr;
+    for (int k0 = 0; k0 < DK; k0 += 32)
+      acc = mma(frag_at(K, SM::LDK, ti * 16, k0, lane), frag_at(K, SM::LDK, tj * 16, k0, lane), acc);
+    const float* gt = Gt(c);
+    const int j = tj * 16 + lr;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int i = ti * 16 + 4 * lq + e;
-        const float decay = fast_exp2(fminf(gG[i] - gG[j], 0.f));
-        if (is_q) {
-          Mb[i * SM::LDT + j] = op_bits(i >= j ? acc[e] * decay : 0.f);
-        } else {
-          Lf[i * SM::LDF + j] = i > j ? bt[i] * acc[e] * decay : 0.f;
+    for (int e = 0; e < 4; ++e) {
+      const int i = ti * 16 + 4 * lq + e;
+      acc[e] = i > j ? gt[3 * kC + i] * acc[e] * fast_exp2(fminf(gt[i] - gt[j], 0.f)) : 0.f;
+    }
+    return acc;
+  };
+  // M = tril_incl(Q K^T 2^(G_i - G_j)) tile of the current chunk -> Mb.
+  auto sqk_tile = [&](int64_t c, int ti, int tj) {
+    const uint16_t* K = Kb(c);
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int k0 = 0; k0 < DK; k0 += 32)
+      acc = mma(frag_at(Qb, SM::LDK, ti * 16, k0, lane), frag_at(K, SM::LDK, tj * 16, k0, lane), acc);
+    const float* gt = Gt(c);
+    const int j = tj * 16 + lr;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = ti * 16 + 4 * lq + e;
+      Mb[i * SM::LDT + j] = op_bits(i >= j ? acc[e] * fast_exp2(fminf(gt[i] - gt[j], 0.f)) : 0.f);
+    }
+  };
+  // (I + L_bb)^-1 for the 4 diagonal blocks by forward substitution (one wave:
+  // lane = (block, column)), fp32.  Writes Af diagonal blocks and A16.
+  auto diag_inverse = [&](int64_t c) {
+    asm volatile("" ::: "memory");  // keep surrounding loads from being hoisted into this region
+    const int b = lane >> 4, col = lane & 15;
+    const float* Lbb = Lb(b, b);
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float v0 = (i == col) ? 1.f : 0.f, v1 = 0.f;
+#pragma unroll
+      for (int j = 0; j < i; j += 2) {
+        v0 = fmaf(-Lbb[i * LDB + j], x[j], v0);
+        if (j + 1 < i) v1 = fmaf(-Lbb[i * LDB + j + 1], x[j + 1], v1);
+      }
+      x[i] = v0 + v1;
+      // keep the compiler from hoisting every row's loads (register pressure)
+      asm volatile("" ::: "memory");
+    }
+    float* Abb = Ab(b, b);
+    uint16_t* A = A16(c);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      Abb[i * LDB + col] = x[i];
+      A[(16 * b + i) * SM::LDT + 16 * b + col] = op_bits(x[i]);
+    }
+    asm volatile("" ::: "memory");
+  };
+  // A_{j+1,j} = -A_{j+1,j+1} L_{j+1,j} A_jj for j = 0 (A10) or j = 2 (A32).
+  auto first_offdiag = [&](int64_t c, int j, float* T) {
+    f32x4 t = mma_split(a_operand(Lb(j + 1, j), nullptr, lane), b_operand(Ab(j, j), nullptr, lane), zero4());
+    store_block(T, t, lane, 1.f);
+    wave_sync();
+    f32x4 a = mma_split(a_operand(Ab(j + 1, j + 1), nullptr, lane), b_operand(T, nullptr, lane), zero4());
+    store_block(Ab(j + 1, j), a, lane, -1.f);
+    store_a16(A16(c), SM::LDT, j + 1, j, a, lane, -1.f);
+  };
+  // Lower-left 32x32 block, column q: [A2q; A3q] = -A_(1,1) L_(1,0) [A0q; A1q].
+  auto corner_column = [&](int64_t c, int q, float* T0, float* T1) {
+    const float* A0q = q == 0 ? Ab(0, 0) : nullptr;
+    const float* A1q = Ab(1, q);
+    const Split b0 = b_operand(A0q, A1q, lane);
+    f32x4 t0 = mma_split(a_operand(Lb(2, 0), Lb(2, 1), lane), b0, zero4());
+    f32x4 t1 = mma_split(a_operand(Lb(3, 0), Lb(3, 1), lane), b0, zero4());
+    store_block(T0, t0, lane, 1.f);
+    store_block(T1, t1, lane, 1.f);
+    wave_sync();
+    f32x4 a2 = mma_split(a_operand(Ab(2, 2), nullptr, lane), b_operand(T0, nullptr, lane), zero4());
+    f32x4 a3 = mma_split(a_operand(Ab(3, 2), Ab(3, 3), lane), b_operand(T0, T1, lane), zero4());
+    store_a16(A16(c), SM::LDT, 2, q, a2, lane, -1.f);
+    store_a16(A16(c), SM::LDT, 3, q, a3, lane, -1.f);
+  };
+
+  // ---------------------------------------------------------------- state-wave pieces
+  f32x4 hacc[HRT][CT];
+  auto load_initial = [&]() {
+    const int64_t rs = load_index(p.read_slots, n, p.read_is64);
+    const ST* src = rs >= 0 ? pool + rs * p.slot_stride + p.layer * p.layer_stride + h * p.head_stride : nullptr;
+#pragma unroll
+    for (int i = 0; i < HRT; ++i) {
+      const int ti = wave + 4 * i;
+#pragma unroll
+      for (int tj = 0; tj < CT; ++tj) {
+        hacc[i][tj] = zero4();
+        if (ti < HT && src) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            hacc[i][tj][e] = load_st(src + (ti * 16 + 4 * lq + e) * p.DV + col_base + tj * 16 + lr);
         }
       }
     }
-    f32x4 pacc[PPW];
+  };
+  auto stage_h = [&]() {  // f16 copy of h, column-major (B operand)
 #pragma unroll
-    for (int i = 0; i < PPW; ++i) {
-      const int t = wave + 4 * i;
-      const int ti = t / CT, tj = t % CT;
-      const uint16_t* X = ti < 4 ? Kr : Qr;
-      const int row0 = (ti & 3) * 16;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < HRT; ++i) {
+      const int ti = wave + 4 * i;
+      if (ti < HT) {
 #pragma unroll
-      for (int k0 = 0; k0 < DK; k0 += 32)
-        acc = M::run(frag_at<f16>(X, SM::LDK, row0, k0, lane), frag_at<f16>(Ht, SM::LDH, tj * 16, k0, lane), acc);
-      pacc[i] = acc;
-      if (ti < 4) {  // R = beta (v - 2^G (k h)) -> Rt (column-major)
+        for (int tj = 0; tj < CT; ++tj) {
+          uint2 w;
+          w.x = op_pack(hacc[i][tj][0], hacc[i][tj][1]);
+          w.y = op_pack(hacc[i][tj][2], hacc[i][tj][3]);
+          *reinterpret_cast<uint2*>(Ht + (tj * 16 + lr) * SM::LDH + ti * 16 + 4 * lq) = w;
+        }
+      }
+    }
+  };
+  auto store_h = [&](int64_t slot_idx) {
+    ST* dst = pool + slot_idx * p.slot_stride + p.layer * p.layer_stride + h * p.head_stride;
+#pragma unroll
+    for (int i = 0; i < HRT; ++i) {
+      const int ti = wave + 4 * i;
+      if (ti < HT) {
+#pragma unroll
+        for (int tj = 0; tj < CT; ++tj)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            store_st(dst + (ti * 16 + 4 * lq + e) * p.DV + col_base + tj * 16 + lr, hacc[i][tj][e]);
+      }
+    }
+  };
+
+  // ---------------------------------------------------------------- prologue
+  for (int e = tid; e < kC * kC; e += kThreads) {  // upper triangles of A and M stay zero
+    const int i = e / kC, j = e % kC;
+    if (j > i) {
+      A160[i * SM::LDT + j] = 0;
+      A160[kC * SM::LDT + i * SM::LDT + j] = 0;
+      Mb[i * SM::LDT + j] = 0;
+    }
+  }
+  // The two roles run separate code paths (wave-uniform branch) that execute
+  // the same sequence of workgroup barriers: 1 + 3 (if any chunk) in the
+  // prologue, then 3 per chunk.
+  if (!side) {
+    // ============================================================ state waves
+    load_initial();
+    stage_h();
+    lds_barrier();
+    if (nchunks > 0) {
+      lds_barrier();
+      lds_barrier();
+      lds_barrier();
+    }
+    for (int64_t c = 0; c < nchunks; ++c) {
+      const int nv = valid_rows(c);
+      // ----- stage I: k h for token tile `wave` -> R = beta (v - 2^G k h) -> Rt
+      {
+        const uint16_t* K = Kb(c);
+        const float* gt = Gt(c);
+        f32x4 acc[CT];
+#pragma unroll
+        for (int tj = 0; tj < CT; ++tj) acc[tj] = zero4();
+#pragma unroll
+        for (int k0 = 0; k0 < DK; k0 += 32) {
+          const frag_t a = frag_at(K, SM::LDK, wave * 16, k0, lane);
+#pragma unroll
+          for (int tj = 0; tj < CT; ++tj) acc[tj] = mma(a, frag_at(Ht, SM::LDH, tj * 16, k0, lane), acc[tj]);
+        }
+        const int row0 = wave * 16 + 4 * lq;
+#pragma unroll
+        for (int tj = 0; tj < CT; ++tj) {
+          const int col = tj * 16 + lr;
+          float rv[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int row = row0 + e;
+            rv[e] = gt[3 * kC + row] * (op_val(Vb[row * SM::LDV + col]) - gt[kC + row] * acc[tj][e]);
+          }
+          uint2 w;
+          w.x = op_pack(rv[0], rv[1]);
+          w.y = op_pack(rv[2], rv[3]);
+          *reinterpret_cast<uint2*>(Rt + col * SM::LDT + row0) = w;
+        }
+      }
+      lds_barrier();
+      // ----- stage II: v' = A R for token tile `wave` -> Vt; gather decayed k^T
+      frag_t kd[HRT][2];
+      float gl;
+      {
+        const uint16_t* A = A16(c);
+        f32x4 acc[CT];
+#pragma unroll
+        for (int tj = 0; tj < CT; ++tj) acc[tj] = zero4();
+#pragma unroll
+        for (int k0 = 0; k0 < kC; k0 += 32) {
+          if (k0 <= wave * 16 + 15) {
+            const frag_t a = frag_at(A, SM::LDT, wave * 16, k0, lane);
+#pragma unroll
+            for (int tj = 0; tj < CT; ++tj) acc[tj] = mma(a, frag_at(Rt, SM::LDT, tj * 16, k0, lane), acc[tj]);
+          }
+        }
+        const int row0 = wave * 16 + 4 * lq;
+#pragma unroll
+        for (int tj = 0; tj < CT; ++tj) {
+          const int col = tj * 16 + lr;
+          uint2 w;
+          w.x = op_pack(acc[tj][0], acc[tj][1]);
+          w.y = op_pack(acc[tj][2], acc[tj][3]);
+          *reinterpret_cast<uint2*>(Vt + col * SM::LDT + row0) = w;
+          if (vng) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (row0 + e < nv)
+                vng[((bos + c * kC + row0 + e) * p.HV + h) * p.DV + col_base + col] = bits_of<IOT>(acc[tj][e]);
+          }
+        }
+        // K and the gates of this chunk are overwritten during stage III
+        const uint16_t* K = Kb(c);
+        const float* gt = Gt(c);
+        gl = gt[4 * kC];
+#pragma unroll
+        for (int i = 0; i < HRT; ++i) {
+          const int ti = wave + 4 * i;
+          const int d = ti < HT ? ti * 16 + lr : 0;
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            frag_t f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const int tok = ks * 32 + 8 * lq + e;
+              f[e] = static_cast<f16>(op_val(K[tok * SM::LDK + d]) * gt[2 * kC + tok]);
+            }
+            kd[i][ks] = f;
+          }
+        }
+      }
+      lds_barrier();
+      // ----- stage III: h <- 2^G_last h + (2^(G_last - G) k)^T v'
+#pragma unroll
+      for (int i = 0; i < HRT; ++i) {
+        const int ti = wave + 4 * i;
+        if (ti < HT) {
+#pragma unroll
+          for (int tj = 0; tj < CT; ++tj) {
+            f32x4 acc = hacc[i][tj] * gl;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) acc = mma(kd[i][ks], frag_at(Vt, SM::LDT, tj * 16, ks * 32, lane), acc);
+            hacc[i][tj] = acc;
+          }
+        }
+      }
+      const int64_t cw = load_index(p.cw_slots, chunk_base + c, p.cw_is64);
+      if (cw >= 0) store_h(cw);
+      stage_h();
+      lds_barrier();
+    }
+    if (p.fw_slots) {
+      const int64_t fw = load_index(p.fw_slots, n, p.fw_is64);
+      if (fw >= 0) store_h(fw);
+    }
+  } else {
+    // ============================================================ side waves
+    prefetch(0, 0);
+    stage(0, true, 0, true);
+    prefetch(1, 1);
+    stage(1, nchunks > 1, 1, false);
+    prefetch(2, 1);  // K, g, beta of chunk 2; Q, V of chunk 1 (staged in iteration 0)
+    lds_barrier();
+    if (nchunks > 0) {  // full solve of chunk 0
+      for (int s = sw; s < 10; s += 4) {
+        int ti = 0, idx = s;
+        while (idx > ti) { idx -= ti + 1; ++ti; }
+        store_block(Lb(ti, idx), skk_tile(0, ti, idx), lane, 1.f);
+      }
+      lds_barrier();
+      if (sw == 0) diag_inverse(0);
+      lds_barrier();
+      if (sw == 0) first_offdiag(0, 0, Tmp);
+      if (sw == 1) first_offdiag(0, 2, Tmp + 2 * BLK);
+      lds_barrier();
+    }
+    for (int64_t c = 0; c < nchunks; ++c) {
+      const bool next = c + 1 < nchunks;
+      const int nv = valid_rows(c);
+      // ----- stage I: corner of A(c) (waves 4, 5); M tiles of chunk c; k k^T tiles of chunk c+1
+      f32x4 late0 = zero4(), late1 = zero4();
+      if (sw < 2) corner_column(c, sw, Tmp + (2 * sw) * BLK, Tmp + (2 * sw + 1) * BLK);
+      if (sw == 0) { sqk_tile(c, 0, 0); sqk_tile(c, 1, 0); sqk_tile(c, 1, 1); }
+      if (sw == 1) { sqk_tile(c, 2, 0); sqk_tile(c, 2, 1); sqk_tile(c, 2, 2); }
+      if (sw == 2) {
+        sqk_tile(c, 3, 0);
+        sqk_tile(c, 3, 1);
+        if (next) {
+          store_block(Lb(0, 0), skk_tile(c + 1, 0, 0), lane, 1.f);
+          store_block(Lb(1, 1), skk_tile(c + 1, 1, 1), lane, 1.f);
+          store_block(Lb(2, 2), skk_tile(c + 1, 2, 2), lane, 1.f);
+          store_block(Lb(3, 3), skk_tile(c + 1, 3, 3), lane, 1.f);
+        }
+      }
+      if (sw == 3) {
+        sqk_tile(c, 3, 2);
+        sqk_tile(c, 3, 3);
+        if (next) {
+          store_block(Lb(1, 0), skk_tile(c + 1, 1, 0), lane, 1.f);
+          store_block(Lb(3, 2), skk_tile(c + 1, 3, 2), lane, 1.f);
+        }
+      }
+      if (next && sw < 2) {  // blocks (2,0),(2,1) / (3,0),(3,1): the corner above still reads them
+        late0 = skk_tile(c + 1, 2 + sw, 0);
+        late1 = skk_tile(c + 1, 2 + sw, 1);
+      }
+      lds_barrier();
+      // ----- stage II: late L blocks; diagonal inverses of chunk c+1; q h of chunk c
+      if (next && sw < 2) {
+        store_block(Lb(2 + sw, 0), late0, lane, 1.f);
+        store_block(Lb(2 + sw, 1), late1, lane, 1.f);
+      }
+      if (next && sw == 0) diag_inverse(c + 1);
+      f32x4 oq[CT];
+      {
+        const float* gt = Gt(c);
+#pragma unroll
+        for (int tj = 0; tj < CT; ++tj) oq[tj] = zero4();
+#pragma unroll
+        for (int k0 = 0; k0 < DK; k0 += 32) {
+          const frag_t a = frag_at(Qb, SM::LDK, sw * 16, k0, lane);
+#pragma unroll
+          for (int tj = 0; tj < CT; ++tj) oq[tj] = mma(a, frag_at(Ht, SM::LDH, tj * 16, k0, lane), oq[tj]);
+        }
+#pragma unroll
+        for (int tj = 0; tj < CT; ++tj)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) oq[tj][e] *= gt[kC + sw * 16 + 4 * lq + e];
+      }
+      lds_barrier();
+      // ----- stage III: A10/A32 of chunk c+1; o of chunk c; stage / prefetch later chunks
+      if (next && sw < 2) first_offdiag(c + 1, 2 * sw, Tmp + (2 * sw) * BLK);
+#pragma unroll
+      for (int k0 = 0; k0 < kC; k0 += 32) {
+        if (k0 <= sw * 16 + 15) {
+          const frag_t a = frag_at(Mb, SM::LDT, sw * 16, k0, lane);
+#pragma unroll
+          for (int tj = 0; tj < CT; ++tj) oq[tj] = mma(a, frag_at(Vt, SM::LDT, tj * 16, k0, lane), oq[tj]);
+        }
+      }
+#pragma unroll
+      for (int tj = 0; tj < CT; ++tj) {
         const int col = tj * 16 + lr;
-        float rv[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int row = row0 + 4 * lq + e;
-          rv[e] = bt[row] * (op_val(Vr[row * SM::LDV + col]) - eG[row] * acc[e]);
-        }
-        uint2 w;
-        w.x = op_bits(rv[0]) | (static_cast<uint32_t>(op_bits(rv[1])) << 16);
-        w.y = op_bits(rv[2]) | (static_cast<uint32_t>(op_bits(rv[3])) << 16);
-        *reinterpret_cast<uint2*>(Rt + col * SM::LDT + row0 + 4 * lq) = w;
-      }
-    }
-    __syncthreads();
-
-    // ---- phase 2: A = (I + L)^-1 -- diagonal 16x16 blocks by forward substitution
-    {
-      const int blk = wave;
-      if (lane < 16) {
-        float x[16];
-        const float* Lb = Lf + (blk * 16) * SM::LDF + blk * 16;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          float v = (i == lane) ? 1.f : 0.f;
-#pragma unroll
-          for (int j = 0; j < i; ++j) v = fmaf(-Lb[i * SM::LDF + j], x[j], v);
-          x[i] = v;
-        }
-        float* Ad = Af + (blk * 16) * SM::LDF + blk * 16;
-        uint16_t* Bd = Ab + (blk * 16) * SM::LDT + blk * 16;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          Ad[i * SM::LDF + lane] = x[i];
-          Bd[i * SM::LDT + lane] = op_bits(x[i]);
+          const int row = sw * 16 + 4 * lq + e;
+          if (row < nv)
+            og[((bos + c * kC + row) * p.HV + h) * p.DV + col_base + col] = bits_of<IOT>(p.scale * oq[tj][e]);
         }
       }
+      stage(c + 2, c + 2 < nchunks, c + 1, next);
+      prefetch(c + 3, c + 2);
+      lds_barrier();
     }
-    __syncthreads();
-    // off-diagonal blocks: A_ij = -A_ii (sum_{k=j}^{i-1} L_ik A_kj), by block distance
-    auto lblk = [&](int i, int j) { return Lf + (i * 16) * SM::LDF + j * 16; };
-    auto ablk = [&](int i, int j) { return Af + (i * 16) * SM::LDF + j * 16; };
-    auto finish = [&](int i, int j, const float* T) {
-      float acc[4] = {0.f, 0.f, 0.f, 0.f};
-      mm16(ablk(i, i), SM::LDF, T, 16, lane, acc);
-      const int row = lane >> 2, col0 = 4 * (lane & 3);
-      float* Ad = ablk(i, j);
-      uint16_t* Bd = Ab + (i * 16) * SM::LDT + j * 16;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        Ad[row * SM::LDF + col0 + e] = -acc[e];
-        Bd[row * SM::LDT + col0 + e] = op_bits(-acc[e]);
-      }
-    };
-    for (int dist = 1; dist < 4; ++dist) {
-      const int count = 4 - dist;
-      if (wave < count) {
-        const int j = wave, i = wave + dist;
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int k = j; k < i; ++k) mm16(lblk(i, k), SM::LDF, ablk(k, j), SM::LDF, lane, acc);
-        float* T = Tmp + wave * 256;
-        const int row = lane >> 2, col0 = 4 * (lane & 3);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) T[row * 16 + col0 + e] = acc[e];
-      }
-      __syncthreads();
-      if (wave < count) finish(wave + dist, wave, Tmp + wave * 256);
-      __syncthreads();
-    }
-
-    // ---- phase 3: v' = A R  (tile t = wave + 4 i over 4 x CT)
-#pragma unroll
-    for (int i = 0; i < VPW; ++i) {
-      const int t = wave + 4 * i;
-      const int ti = t / CT, tj = t % CT;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int k0 = 0; k0 < kC; k0 += 32)
-        if (k0 <= ti * 16 + 15)
-          acc = M::run(frag_at<f16>(Ab, SM::LDT, ti * 16, k0, lane), frag_at<f16>(Rt, SM::LDT, tj * 16, k0, lane), acc);
-      const int col = tj * 16 + lr, row0 = ti * 16 + 4 * lq;
-      uint2 w;
-      w.x = op_bits(acc[0]) | (static_cast<uint32_t>(op_bits(acc[1])) << 16);
-      w.y = op_bits(acc[2]) | (static_cast<uint32_t>(op_bits(acc[3])) << 16);
-      *reinterpret_cast<uint2*>(Vt + col * SM::LDT + row0) = w;
-      if (vng) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (row0 + e < nv) vng[((t0 + row0 + e) * p.HV + h) * p.DV + col_base + col] = bits_of<IOT>(acc[e]);
-      }
-    }
-    __syncthreads();
-
-    // ---- phase 4: o = scale (2^G q h + M v'); h <- 2^G_last h + Kd^T v'
-#pragma unroll
-    for (int i = 0; i < PPW; ++i) {
-      const int t = wave + 4 * i;
-      const int ti = t / CT, tj = t % CT;
-      if (ti < 4) continue;
-      const int qt = ti - 4;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int k0 = 0; k0 < kC; k0 += 32)
-        if (k0 <= qt * 16 + 15)
-          acc = M::run(frag_at<f16>(Mb, SM::LDT, qt * 16, k0, lane), frag_at<f16>(Vt, SM::LDT, tj * 16, k0, lane), acc);
-      const int col = tj * 16 + lr;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = qt * 16 + 4 * lq + e;
-        if (row < nv) {
-          const float o = p.scale * (eG[row] * pacc[i][e] + acc[e]);
-          og[((t0 + row) * p.HV + h) * p.DV + col_base + col] = bits_of<IOT>(o);
-        }
-      }
-    }
-    {
-      const float gl = misc[0];
-#pragma unroll
-      for (int i = 0; i < HPW; ++i) {
-        const int t = wave + 4 * i;
-        if (t < HTILES) {
-          const int ti = t / CT, tj = t % CT;
-          f32x4 acc = hacc[i] * gl;
-#pragma unroll
-          for (int k0 = 0; k0 < kC; k0 += 32)
-            acc = M::run(frag_at<f16>(Ktd, SM::LDT, ti * 16, k0, lane), frag_at<f16>(Vt, SM::LDT, tj * 16, k0, lane),
-                         acc);
-          hacc[i] = acc;
-        }
-      }
-    }
-    const int64_t cw = load_index(p.cw_slots, chunk_base + c, p.cw_is64);
-    if (cw >= 0) store_state_to(cw);
-    __syncthreads();  // all reads of Ht / chunk tiles done
-    stage_state();
-  }
-  if (p.fw_slots) {
-    const int64_t fw = load_index(p.fw_slots, n, p.fw_is64);
-    if (fw >= 0) store_state_to(fw);
   }
 }
 
