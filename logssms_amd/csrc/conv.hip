@@ -7,6 +7,8 @@
 // each element W times through 4 shifted masked loads, packed_conv.py:99-110)
 // and consecutive threads touch consecutive channels (coalesced rows).
 // Per token and channel: 2 bytes in, 2 bytes out (bf16).
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace gdn {
@@ -211,6 +213,230 @@ __global__ __launch_bounds__(kThreads) void frontend_kernel(FrontParams fp) {
   }
 }
 
+// ---------------------------------------------- vectorised path (8 channels / thread)
+// Used when the input rows are unit-stride, 16-byte aligned and C % 8 == 0.
+// Each thread owns 8 consecutive channels for a tile of kVTok tokens: one
+// 16-byte load and one 16-byte store per token, the W-1 previous inputs in
+// registers, and the per-head q/k sum of squares reduced across the DK/8
+// lanes of the head with cross-lane shuffles (no LDS).
+constexpr int kVTok = 16;
+
+template <class T> __device__ __forceinline__ void unpack8(uint4 v, float (&x)[8]);
+template <> __device__ __forceinline__ void unpack8<bf16>(uint4 v, float (&x)[8]) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = __uint_as_float(w[i] << 16);
+    x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+template <> __device__ __forceinline__ void unpack8<f16>(uint4 v, float (&x)[8]) {
+  const f16* h = reinterpret_cast<const f16*>(&v);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = static_cast<float>(h[i]);
+}
+template <class T> __device__ __forceinline__ uint16_t half_bits(float x);
+template <> __device__ __forceinline__ uint16_t half_bits<bf16>(float x) { return f32_to_bf16_bits(x); }
+template <> __device__ __forceinline__ uint16_t half_bits<f16>(float x) {
+  const f16 h = static_cast<f16>(x);
+  return *reinterpret_cast<const uint16_t*>(&h);
+}
+template <class T> __device__ __forceinline__ uint4 pack8(const float (&x)[8]) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = half_bits<T>(x[2 * i]) | (static_cast<uint32_t>(half_bits<T>(x[2 * i + 1])) << 16);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+__device__ __forceinline__ float fast_silu(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + fast_exp2(-1.4426950408889634f * x));
+}
+
+// FRONT: fused front end (q/k normalised into q_out/k_out, v into v_out, history
+// from the pool); otherwise the plain packed conv into conv.out.
+template <class T, int W, int DK, bool FRONT>
+__global__ __launch_bounds__(256) void conv_vec_kernel(FrontParams fp) {
+  const ConvParams& p = fp.conv;
+  constexpr int S = W - 1;
+  const int64_t ch0 = (static_cast<int64_t>(blockIdx.y) * 256 + threadIdx.x) * 8;
+  const bool active = ch0 < p.C;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kVTok;
+  const int64_t t1 = t0 + kVTok < p.T ? t0 + kVTok : p.T;
+  const int64_t key_dim = FRONT ? fp.H * DK : 0;
+  float w[W][8], bias[8];
+  float win[S > 0 ? S : 1][8];
+  const bool scaled = !FRONT && (p.s0 != 1.f || p.s1 != 1.f || p.s2 != 1.f);
+  float sc[8];
+  if (active) {
+    // weights [C][W] contiguous: 8 channels x W taps = W 16-byte pieces
+    const uint4* wp = reinterpret_cast<const uint4*>(static_cast<const T*>(p.w) + ch0 * W);
+    float wv[8 * W];
+#pragma unroll
+    for (int i = 0; i < W; ++i) {
+      float x[8];
+      unpack8<T>(wp[i], x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) wv[8 * i + e] = x[e];
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+      for (int tap = 0; tap < W; ++tap) w[tap][c] = wv[c * W + tap];
+    if (p.bias) {
+      unpack8<T>(*reinterpret_cast<const uint4*>(static_cast<const T*>(p.bias) + ch0), bias);
+    } else {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) bias[c] = 0.f;
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int64_t ch = ch0 + c;
+      sc[c] = ch < p.end0 ? p.s0 : (ch < p.end1 ? p.s1 : p.s2);
+    }
+  }
+  const T* x = static_cast<const T*>(p.x);
+  auto x_at = [&](int64_t t, float (&v)[8]) {
+    unpack8<T>(*reinterpret_cast<const uint4*>(x + t * p.xr + ch0), v);
+    if (scaled) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) v[c] = round_to<T>(v[c] * sc[c]);
+    }
+  };
+  int64_t r = find_sequence(p.cu, p.cu_is64, p.N, t0);
+  int64_t begin = load_index(p.cu, r, p.cu_is64);
+  int64_t end = load_index(p.cu, r + 1, p.cu_is64);
+  auto load_window = [&](int64_t t) {
+    for (int i = 0; i < S; ++i) {
+      const int64_t pos = t - S + i;
+      if (pos >= begin) {
+        float v[8];
+        x_at(pos, v);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) win[i][c] = v[c];
+      } else {
+        const int j = static_cast<int>(pos - begin + S);
+        const T* src;
+        if (p.history) {
+          src = static_cast<const T*>(p.history) + (r * p.C + ch0) * S + j;
+        } else {
+          const int64_t slot = load_index(p.baseline, r, p.baseline_is64);
+          src = slot >= 0 ? static_cast<const T*>(p.state) + slot * p.slot_stride + p.layer * p.layer_stride +
+                                ch0 * S + j
+                          : nullptr;
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c) win[i][c] = src ? to_f32(src[c * S]) : 0.f;
+      }
+    }
+  };
+  if (active) load_window(t0);
+  for (int64_t t = t0; t < t1; ++t) {
+    while (t >= end) {  // next sequence (skips empty ones)
+      ++r;
+      begin = end;
+      end = load_index(p.cu, r + 1, p.cu_is64);
+      if (t < end && active) load_window(t);
+    }
+    float xv[8], y[8];
+    if (active) x_at(t, xv);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      float acc = bias[c];
+#pragma unroll
+      for (int i = 0; i < S; ++i) acc = fmaf(win[i][c], w[i][c], acc);
+      acc = fmaf(xv[c], w[S][c], acc);
+      y[c] = round_to<T>(fast_silu(round_to<T>(acc)));
+    }
+    if (active && p.state) {  // window snapshots (raw inputs, oldest first)
+      const int64_t slot = p.token_slots ? load_index(p.token_slots, t, p.token_is64) : -1;
+      const int64_t fslot = (!FRONT && p.final_slots && t == end - 1) ? load_index(p.final_slots, r, p.final_is64) : -1;
+      for (int k = 0; k < 2; ++k) {
+        const int64_t s_ = k == 0 ? slot : fslot;
+        if (s_ < 0) continue;
+        T* dst = static_cast<T*>(p.state) + s_ * p.slot_stride + p.layer * p.layer_stride + ch0 * S;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+#pragma unroll
+          for (int i = 0; i + 1 < S; ++i) dst[c * S + i] = from_f32<T>(win[i + 1][c]);
+          dst[c * S + S - 1] = from_f32<T>(xv[c]);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i + 1 < S; ++i)
+#pragma unroll
+      for (int c = 0; c < 8; ++c) win[i][c] = win[i + 1][c];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) win[S - 1][c] = xv[c];
+    if (FRONT) {
+      // per-head sum of squares over DK / 8 lanes (heads start at multiples of DK)
+      float ss = 0.f;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) ss = fmaf(y[c], y[c], ss);
+#pragma unroll
+      for (int off = 1; off < DK / 8; off <<= 1) ss += __shfl_xor(ss, off, 64);
+      if (active) {
+        if (ch0 < 2 * key_dim) {
+          const float rn = rsqrtf(ss + 1e-6f);
+#pragma unroll
+          for (int c = 0; c < 8; ++c) y[c] *= rn;
+          T* dst = ch0 < key_dim ? static_cast<T*>(fp.q_out) + t * key_dim + ch0
+                                 : static_cast<T*>(fp.k_out) + t * key_dim + ch0 - key_dim;
+          *reinterpret_cast<uint4*>(dst) = pack8<T>(y);
+        } else {
+          *reinterpret_cast<uint4*>(static_cast<T*>(fp.v_out) + t * (fp.HV * fp.DV) + ch0 - 2 * key_dim) =
+              pack8<T>(y);
+        }
+      }
+    } else if (active) {
+      *reinterpret_cast<uint4*>(static_cast<T*>(p.out) + t * p.C + ch0) = pack8<T>(y);
+    }
+  }
+  if (FRONT && blockIdx.y == 0) {
+    const int n = static_cast<int>(t1 - t0);
+    for (int idx = threadIdx.x; idx < n * fp.HV; idx += 256) {
+      const int64_t t = t0 + idx / fp.HV;
+      const int64_t h = idx % fp.HV;
+      const float a = load_any(fp.A_log, h, fp.a_dtype);
+      const float b = load_any(fp.dt_bias, h, fp.dt_dtype);
+      const float gv = load_any(fp.gate, t * fp.gate_r + h * fp.gate_h, fp.gate_dtype) + b;
+      const float bv = load_any(fp.beta, t * fp.beta_r + h * fp.beta_h, fp.beta_dtype);
+      fp.g_out[t * fp.HV + h] = -expf(a) * softplus_prefill(gv);
+      fp.b_out[t * fp.HV + h] = sigmoid(bv);
+    }
+  }
+}
+
+// Launch the vectorised kernel when the layout allows it; returns -1 if not.
+template <class T, bool FRONT>
+int launch_vec(const FrontParams& fp, int dk, hipStream_t s) {
+  const ConvParams& p = fp.conv;
+  const bool aligned = p.xc == 1 && p.xr % 8 == 0 && p.C % 8 == 0 &&
+                       (reinterpret_cast<uintptr_t>(p.x) & 15) == 0 && (reinterpret_cast<uintptr_t>(p.w) & 15) == 0 &&
+                       (!p.bias || (reinterpret_cast<uintptr_t>(p.bias) & 15) == 0) &&
+                       (FRONT || (reinterpret_cast<uintptr_t>(p.out) & 15) == 0) && p.W >= 2 && p.W <= 4;
+  if (!aligned) return -1;
+  dim3 grid(static_cast<unsigned>((p.T + kVTok - 1) / kVTok), static_cast<unsigned>((p.C / 8 + 255) / 256));
+  auto go = [&](auto Wc, auto DKc) {
+    constexpr int Wv = decltype(Wc)::value, DKv = decltype(DKc)::value;
+    hipLaunchKernelGGL((conv_vec_kernel<T, Wv, DKv, FRONT>), grid, dim3(256), 0, s, fp);
+  };
+  auto by_dk = [&](auto Wc) {
+    switch (dk) {
+      case 32: go(Wc, std::integral_constant<int, 32>{}); return 0;
+      case 64: go(Wc, std::integral_constant<int, 64>{}); return 0;
+      case 128: go(Wc, std::integral_constant<int, 128>{}); return 0;
+      case 256: go(Wc, std::integral_constant<int, 256>{}); return 0;
+      default: return -1;
+    }
+  };
+  switch (p.W) {
+    case 2: return by_dk(std::integral_constant<int, 2>{});
+    case 3: return by_dk(std::integral_constant<int, 3>{});
+    default: return by_dk(std::integral_constant<int, 4>{});
+  }
+}
+
 // ------------------------------------------------------------- prepare_gdn
 struct PrepParams {
   const void* q;
@@ -320,7 +546,13 @@ extern "C" int gdn_packed_causal_conv1d(const void* x, int64_t x_row_stride, int
             static_cast<unsigned>((channels + kThreads - 1) / kThreads));
   return dispatch_dtype(dtype, [&](auto tag) {
     using T = decltype(tag);
-    hipLaunchKernelGGL((packed_conv_kernel<T>), grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream), p);
+    auto s = static_cast<hipStream_t>(stream);
+    if constexpr (sizeof(T) == 2) {
+      FrontParams fp{};
+      fp.conv = p;
+      if (launch_vec<T, false>(fp, 128, s) == 0) return GDN_LAUNCH_CHECK("gdn_packed_causal_conv1d launch");
+    }
+    hipLaunchKernelGGL((packed_conv_kernel<T>), grid, dim3(kThreads), 0, s, p);
     return GDN_LAUNCH_CHECK("gdn_packed_causal_conv1d launch");
   });
 }
@@ -364,6 +596,9 @@ extern "C" int gdn_prefill_frontend(const void* mixed, int64_t row_stride, int64
   return dispatch_dtype(dtype, [&](auto tag) -> int {
     using T = decltype(tag);
     auto s = static_cast<hipStream_t>(stream);
+    if constexpr (sizeof(T) == 2) {
+      if (launch_vec<T, true>(fp, static_cast<int>(dk), s) == 0) return GDN_LAUNCH_CHECK("gdn_prefill_frontend launch");
+    }
     switch (dk) {
       case 32: hipLaunchKernelGGL((frontend_kernel<T, 32>), grid, dim3(kThreads), 0, s, fp); break;
       case 64: hipLaunchKernelGGL((frontend_kernel<T, 64>), grid, dim3(kThreads), 0, s, fp); break;
