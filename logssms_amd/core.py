@@ -1,0 +1,103 @@
+"""Minimal engine-side records the GDN backend reads (mirrors of the fields the
+reference's ``python/logssms/core.py`` ``Context`` / ``Batch`` / ``Request``
+expose to ``layers/linear_attention_backend``).  The engine, scheduler and
+cache managers that fill them in are outside this library."""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Any, Literal
+
+import torch
+
+
+@dataclass
+class Request:
+    table_idx: int
+    cached_len: int
+    device_len: int
+
+    @property
+    def extend_len(self) -> int:
+        return self.device_len - self.cached_len
+
+
+@dataclass
+class MarconiCacheMetadata:
+    """cache/marconi/metadata.py:6-9."""
+
+    checkpoint_writes: list[list[tuple[int, int]]] | None = None
+    checkpoint_copies: list[tuple[int, int]] = field(default_factory=list)
+
+
+@dataclass
+class Batch:
+    reqs: list[Request]
+    phase: Literal["prefill", "decode", "verify"]
+    padded_reqs: list[Request] | None = None
+    cache_metadata: Any = None
+    linear_attn_metadata: Any = None
+
+    def __post_init__(self):
+        if self.padded_reqs is None:
+            self.padded_reqs = self.reqs
+
+    @property
+    def is_prefill(self) -> bool:
+        return self.phase == "prefill"
+
+    @property
+    def is_decode(self) -> bool:
+        return self.phase == "decode"
+
+    @property
+    def is_verify(self) -> bool:
+        return self.phase == "verify"
+
+    @property
+    def size(self) -> int:
+        return len(self.reqs)
+
+    @property
+    def padded_size(self) -> int:
+        return len(self.padded_reqs)
+
+
+@dataclass
+class Context:
+    page_size: int
+    linear_state: Any = None
+    state_table: torch.Tensor | None = None
+    work_state_table: torch.Tensor | None = None
+    _backend: Any = field(default=None, repr=False)
+
+    @property
+    def linear_attn_backend(self):
+        """The GDN backend bound to this context (created on first use)."""
+        if self._backend is None:
+            from .layers.linear_attention_backend import GatedDeltaBackend
+
+            self._backend = GatedDeltaBackend(self)
+        return self._backend
+
+
+_GLOBAL_CTX: Context | None = None
+
+
+def set_global_ctx(ctx: Context) -> None:
+    global _GLOBAL_CTX
+    _GLOBAL_CTX = ctx
+
+
+def clear_global_ctx() -> None:
+    global _GLOBAL_CTX
+    _GLOBAL_CTX = None
+
+
+def get_global_ctx() -> Context:
+    assert _GLOBAL_CTX is not None, "no global context set"
+    return _GLOBAL_CTX
+
+
+__all__ = ["Batch", "Context", "MarconiCacheMetadata", "Request", "clear_global_ctx", "get_global_ctx",
+           "set_global_ctx"]
