@@ -41,6 +41,22 @@ S_BYTES = HV * D * D * 4  # fp32 state per sequence
 SC_BYTES = CONV_DIM * (W - 1) * 2  # bf16 conv window per sequence
 
 
+def _traffic(name):
+    """HBM bytes per launch measured with the FETCH_SIZE / WRITE_SIZE counter
+    passes (calibrated on a plain copy), from the committed profile summary;
+    None when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "gdn_kernels_hbm_traffic_pmc.md")
+    try:
+        with open(path) as fh:
+            for line in fh:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "traffic" and parts[1] == name:
+                    return int(parts[2])
+    except OSError:
+        pass
+    return None
+
+
 def _config(layer=0):
     from logssms_amd.layers import GatedDeltaConfig
     return GatedDeltaConfig(H, HV, D, D, CONV_DIM, W - 1, layer)
@@ -213,7 +229,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--only", choices=["all", "prefill", "decode", "verify"], default="all")
+    ap.add_argument("--only", choices=["all", "prefill", "decode", "verify", "copy"], default="all",
+                    help="'copy' times a plain 512 MiB device copy (the calibration kernel for the "
+                         "FETCH_SIZE / WRITE_SIZE counter passes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -223,6 +241,14 @@ def main():
     torch.cuda.set_device(0)
     result = {}
     extra = {}
+    if args.only == "copy":
+        nbytes = 512 << 20
+        src = torch.ones(nbytes // 4, device=dev)
+        dst = torch.empty_like(src)
+        ms = _time(lambda: dst.copy_(src), args.steps, args.warmup)
+        print(json.dumps({"metric": "plain device copy GB/s", "value": 2 * nbytes / (ms * 1e-3) / 1e9,
+                          "unit": "GB/s", "read_bytes": nbytes, "write_bytes": nbytes, "ms_per_step": ms}))
+        return
 
     if args.only in ("all", "prefill"):
         inp = make_prefill()
@@ -247,7 +273,7 @@ def main():
                     "seq_len": 4096, "heads_qk": H, "heads_v": HV, "head_dim": D, "chunk": C,
                     "parallelism": "single GPU"},
             roofline={"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_MFMA_16BIT / 1e12,
-                      "unit": "TFLOP/s", "frac": achieved / PEAK_MFMA_16BIT, "traffic": None,
+                      "unit": "TFLOP/s", "frac": achieved / PEAK_MFMA_16BIT, "traffic": _traffic("chunk_kernel_cfg2"),
                       "kernel": "chunk_kernel", "kernel_ms": chunk_ms,
                       "algorithmic_flop_per_launch": flops, "algorithmic_bytes_per_launch": chunk_bytes},
         )
@@ -274,7 +300,7 @@ def main():
         nb = decode_bytes(256)
         extra["decode"] = {"config": "BASELINE config 3 (256 seqs, in-place RMW of randperm pool slots)",
                            "ms": ms, "bytes": nb, "GB/s": nb / (ms * 1e-3) / 1e9,
-                           "frac_hbm": nb / (ms * 1e-3) / PEAK_HBM}
+                           "frac_hbm": nb / (ms * 1e-3) / PEAK_HBM, "traffic": _traffic("fused_kernel_decode_cfg3")}
     if args.only in ("all", "verify"):
         step, commit = verify_gpu(dev)
         ms = _time(step, max(args.steps, 20), args.warmup)
@@ -283,8 +309,9 @@ def main():
         cb = 64 * 2 * (S_BYTES + SC_BYTES)
         extra["verify"] = {"config": "BASELINE config 5 (64 seqs x 8 drafts, per-step states to slots)",
                            "ms": ms, "bytes": nb, "GB/s": nb / (ms * 1e-3) / 1e9,
-                           "frac_hbm": nb / (ms * 1e-3) / PEAK_HBM,
-                           "commit_ms": cms, "commit_GB/s": cb / (cms * 1e-3) / 1e9}
+                           "frac_hbm": nb / (ms * 1e-3) / PEAK_HBM, "traffic": _traffic("fused_kernel_verify_cfg5"),
+                           "commit_ms": cms, "commit_GB/s": cb / (cms * 1e-3) / 1e9,
+                           "commit_traffic": _traffic("commit_kernel_cfg5")}
     if not result:
         key = "decode" if "decode" in extra else "verify"
         e = extra[key]
@@ -293,7 +320,7 @@ def main():
                       scaling="weak", vs_baseline=None, dtype="bf16 io / fp32 state", data="synthetic",
                       config={"workload": e["config"]},
                       roofline={"bound": "hbm", "achieved": e["GB/s"], "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                                "frac": e["frac_hbm"], "traffic": None})
+                                "frac": e["frac_hbm"], "traffic": e["traffic"]})
     result["extra"] = extra
     print(json.dumps(result))
 

@@ -164,3 +164,17 @@ def test_bf16_pool_and_chunk_aligned_resume():
     _run(q.to(DEV), k.to(DEV), v.to(DEV), gg.to(DEV), beta.to(DEV), bpool, torch.tensor([-1], device=DEV),
          torch.tensor([-1, -1, -1, 1], device=DEV), torch.tensor([0, T], device=DEV))
     assert_bf16_close(bpool[1], full[1], rel=2e-2, atol=2e-3)
+
+
+def test_config1_against_committed_fixture():
+    """The kernel against ``tests/golden/cfg1_bf16.npz`` (float64 recurrence of
+    the same bf16 inputs), without running the oracle."""
+    from tests.golden.make_golden import D, EVERY, H, T, cfg1_inputs
+    from tests.test_golden import load_fixture
+    o_rows, state = load_fixture()
+    q, k, v, gg, beta = cfg1_inputs()
+    storage = torch.zeros(2, 1, H, D, D, device=DEV)
+    o, _ = _run(q.to(DEV), k.to(DEV), v.to(DEV), gg.to(DEV), beta.to(DEV), storage, torch.tensor([-1], device=DEV),
+                torch.tensor([-1] * 7 + [1], device=DEV), torch.tensor([0, T], device=DEV))
+    assert_bf16_close(o[0, ::EVERY], o_rows)
+    assert_state_close(storage[1, 0], state)
