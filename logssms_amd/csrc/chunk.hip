@@ -38,7 +38,7 @@
 //
 // Roofline: MFMA (16-bit).  Algorithmic flops per token per v-head:
 // 10 C d + 6 d^2 + 2/3 C^2 (C = 64, d = 128).
-#include "common.hpp"
+#include "chunk_common.hpp"
 
 namespace gdn {
 namespace {
@@ -126,30 +126,6 @@ struct Smem {
   static constexpr size_t tmp = ht + 2ull * DVS * LDH;
   static constexpr size_t total = tmp + 2 * 2 * 4ull * BLK;
   static_assert(total <= 160 * 1024, "LDS budget");
-};
-
-struct ChunkParams {
-  const void* q;
-  const void* k;
-  const void* v;
-  const float* g;
-  const float* beta;
-  const void* cu;
-  int cu_is64;
-  int64_t N, T, H, HV, DV;
-  void* state;
-  int64_t slot_stride, layer_stride, head_stride, layer;
-  const void* read_slots;
-  int read_is64;
-  const void* cw_slots;
-  int cw_is64;
-  const void* fw_slots;
-  int fw_is64;
-  void* out;
-  void* v_new;
-  float scale;
-  int nvs;      // v slices per head
-  int members;  // workgroups per (sequence, key head)
 };
 
 typedef f16x8_t frag_t;
@@ -807,6 +783,8 @@ extern "C" int gdn_chunk_gated_delta_rule(const void* q, const void* k, const vo
   if (dv % 64 == 0) {
     p.nvs = static_cast<int>(dv / 64);
     p.members = static_cast<int>(r * p.nvs);
+    const int rc = launch_chunk_chain(p, dk, io_dtype, state_dtype, groups, s);
+    if (rc != GDN_ERR_UNSUPPORTED) return rc;
     if (dk == 128) return dispatch_types<128, 64>(p, io_dtype, state_dtype, groups, s);
     if (dk == 64) return dispatch_types<64, 64>(p, io_dtype, state_dtype, groups, s);
     if (dk == 32) return dispatch_types<32, 64>(p, io_dtype, state_dtype, groups, s);
