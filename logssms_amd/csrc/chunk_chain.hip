@@ -8,24 +8,27 @@
 //   v' = (I + L)^-1 R                                             (= U - W h)
 //   o  = scale (2^G (q h) + tril_incl(q k^T 2^(G_i - G_j)) v')    (chunk_o.py:85-130)
 //   h <- 2^G_last h + (2^(G_last - G) k)^T v'                     (chunk_delta_h.py:194-224)
-// The solve uses the 2x2 split of the 64-token chunk into 32-token halves:
+// The solve splits the 64-token chunk into 32-token halves:
 //   v'_top = A11 R_top,  v'_bot = A22 (R_bot - L21 v'_top),  A_ii = (I + L_ii)^-1,
-// so only the two 32x32 diagonal inverses are formed off the chain.
+// and each 32x32 inverse is the product form
+//   (I + L)^-1 = (I - L + L^2 - L^3)(I + L^4)(I + L^8)(I + L^16)
+// (L is nilpotent), evaluated with MFMA products in registers.
 //
 // Mapping: one workgroup per (sequence, v-head, 64-column slice of d_v); 8 waves.
-//   * Chain waves 0-3: wave j owns state columns 16j..16j+15 for the whole
-//     sequence, as fp32 MFMA accumulator tiles.  Every product of the chain
+//   * Chain waves 0-1: wave j owns state columns 32j..32j+31 for the whole
+//     sequence as fp32 MFMA accumulator tiles.  Every product of the chain
 //     takes its right operand straight from accumulator registers: the k index
-//     of each 32-deep product is ordered so that lane group g holds rows
-//     4g..4g+3 and 16+4g..16+4g+3 of the block -- exactly the rows a C-layout
-//     tile pair holds -- and the left operand (K, Q, A, M or K^T rows in LDS)
-//     is read in that same order.  Per chunk: P = K h and Q h, R, v', o (M v'
-//     added), h update; nothing but the output goes through LDS.
-//   * Side waves 4-7 prepare chunk c+1 while the chain runs chunk c: k k^T and
-//     q k^T tiles with the decay masks (L, the masked M), the 16x16 diagonal
-//     inverses (fp32 forward substitution), the two off-diagonal blocks of
-//     A11/A22 (split-f16 products, ~fp32 accurate), the d-major copy of K the
-//     state update reads, and the staging / global prefetch of later chunks.
+//     of each 32-deep product is ordered so that lane group g (= lane / 16)
+//     holds rows 4g..4g+3 and 16+4g..16+4g+3 of the block -- exactly the rows
+//     a C-layout tile pair holds -- and the left operand (K, Q, A or M rows in
+//     LDS) is read in that same order; K^T rows come from the token-major K
+//     tile through the LDS transpose read.  Per chunk: P = K h and o^T = h^T
+//     q^T, R, v', o^T += v'^T M^T (stored directly: a lane holds 4 consecutive
+//     output columns of one token), h update.
+//   * Side waves 2-7 prepare chunk c+1 while the chain runs chunk c: waves 2
+//     and 3 form A11 and A22 (k k^T tiles, masks, product-form inverse, all
+//     in registers), waves 4-7 the masked q k^T tiles (M) and -L21, and stage
+//     / prefetch later chunks (K, Q, V tiles and the gate table).
 // Two workgroup barriers per chunk (LDS-only waits, so global prefetches stay
 // in flight).  MFMA operands are f16 (bf16 inputs convert exactly; values
 // saturate at +-65504) with fp32 accumulation.
@@ -44,18 +47,19 @@ constexpr float kRcpLn2 = 1.4426950216f;  // gated_delta.py:12
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef short s4_t __attribute__((ext_vector_type(4)));
 
-constexpr int LDA = kC + 8;  // row stride (halfs) of the A and M tiles
-constexpr int LDT = kC + 4;  // row stride (halfs) of the d-major K and column-major V tiles
-constexpr int LDB = 20;      // row stride (floats) of fp32 16x16 blocks
-constexpr int BLK = 16 * LDB + 16;  // block stride: consecutive blocks start 16 banks apart
+// LDS row strides (halfs).  K rows: 76 dwords, so both the 8-byte row reads
+// of the left operands and the 4-row transpose reads avoid bank conflicts.
+constexpr int LDK = 152;
+constexpr int LDV = 80;      // V rows (64 columns)
+constexpr int LDA = kC + 8;  // A and M rows
 // Gate table per chunk (floats): G, 2^G, 2^(G_last - G) (0 past the end),
 // beta, then 2^G_last.
 constexpr int GTS = 264;
 constexpr int G_EXP = 64, G_DEC = 128, G_BETA = 192, G_LAST = 256;
 
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-__device__ __forceinline__ void wave_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 __device__ __forceinline__ f4_t mma(h8_t a, h8_t b, f4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -65,12 +69,23 @@ __device__ __forceinline__ f4_t zero4() { return f4_t{0.f, 0.f, 0.f, 0.f}; }
 __device__ __forceinline__ _Float16 to_op(float x) {
   return static_cast<_Float16>(__builtin_amdgcn_fmed3f(x, -65504.f, 65504.f));
 }
+__device__ __forceinline__ h8_t cat(h4_t lo, h4_t hi) { return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7); }
 // Left operand, row `row` of a row-major f16 matrix, k block at column k0.
 __device__ __forceinline__ h8_t afrag(const _Float16* base, int ld, int row, int k0, int g) {
   const _Float16* p = base + row * ld + k0 + 4 * g;
-  const h4_t lo = *reinterpret_cast<const h4_t*>(p);
-  const h4_t hi = *reinterpret_cast<const h4_t*>(p + 16);
-  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return cat(*reinterpret_cast<const h4_t*>(p), *reinterpret_cast<const h4_t*>(p + 16));
+}
+// LDS transpose read: the 16 lanes of a group read a 4-row x 16-column block
+// (lane r: row r / 4, columns 4 (r % 4)..+3) and lane r receives column r.
+__device__ __forceinline__ h4_t tr_read(const _Float16* p) {
+  typedef __attribute__((address_space(3))) s4_t lds_s4;
+  return __builtin_bit_cast(h4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p)));
+}
+// Left operand of X^T for a row-major X: rows of X^T = columns c0 + lane % 16
+// of X, k block = rows t0..t0+31 of X in the k order above.
+__device__ __forceinline__ h8_t tfrag(const _Float16* X, int ld, int t0, int c0, int lr, int lg) {
+  const _Float16* p = X + (t0 + 4 * lg + (lr >> 2)) * ld + c0 + 4 * (lr & 3);
+  return cat(tr_read(p), tr_read(p + 16 * ld));
 }
 // Right operand from two C-layout accumulator tiles (rows 0-15, rows 16-31).
 __device__ __forceinline__ h8_t bfrag(f4_t a, f4_t b) {
@@ -100,84 +115,63 @@ template <> __device__ __forceinline__ uint16_t out_bits<f16>(float x) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
 }
 
-// ---- split-f16 products of fp32 16x16 blocks (x = hi + lo; the product
-// drops lo*lo).  Standard operand layout, second half of k zero.
-struct Split {
-  h8_t hi, lo;
-};
-__device__ __forceinline__ Split split8(const float (&x)[8]) {
-  Split s;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const _Float16 h = static_cast<_Float16>(x[e]);
-    s.hi[e] = h;
-    s.lo[e] = static_cast<_Float16>(x[e] - static_cast<float>(h));
-  }
-  return s;
-}
-__device__ __forceinline__ Split a_block(const float* X, int lane) {
-  float x[8];
-  const int row = lane & 15, kq = lane >> 4;
-  if (kq < 2) {
-    const float4 a = *reinterpret_cast<const float4*>(X + row * LDB + 8 * kq);
-    const float4 b = *reinterpret_cast<const float4*>(X + row * LDB + 8 * kq + 4);
-    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = 0.f;
-  }
-  return split8(x);
-}
-__device__ __forceinline__ Split b_block(const float* Y, int lane) {
-  float x[8];
-  const int col = lane & 15, kq = lane >> 4;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) x[e] = kq < 2 ? Y[(8 * kq + e) * LDB + col] : 0.f;
-  return split8(x);
-}
-__device__ __forceinline__ f4_t mma_split(const Split& a, const Split& b) {
-  f4_t c = mma(a.hi, b.hi, zero4());
-  c = mma(a.hi, b.lo, c);
-  return mma(a.lo, b.hi, c);
-}
-
 template <class ST> __device__ __forceinline__ float load_st(const ST* p) { return to_f32(*p); }
 template <class ST> __device__ __forceinline__ void store_st(ST* p, float v) { *p = from_f32<ST>(v); }
 
-// Side-thread staging blocks: a thread moves 4 tokens x 8 columns.  Within a
-// wave, lane l takes token block (l & 3) + 4 ((l >> 4) & 1) and column block
-// ((l >> 2) & 3) + 4 (l >> 5) of an 8 x 8 patch, which keeps both the 16-byte
-// row accesses (4 passes of 16 lanes) and the 8-byte transposed accesses
-// (2 passes of 32 lanes) free of LDS bank conflicts for the row strides used
-// here (136 B token rows, 136 B transposed rows).
-struct Blk {
-  int tb, db;
+// ---- 32x32 lower-triangular matrices held as C-layout tiles of X and X^T.
+// x[0] = X(0,0), x[1] = X(1,0), x[2] = X(1,1); t[0] = X^T(0,0), t[1] =
+// X^T(0,1), t[2] = X^T(1,1) (tile (a, b): rows 16a.., columns 16b..).
+struct Tri {
+  f4_t x[3], t[3];
 };
-__device__ __forceinline__ Blk staging_block(int idx, int ndb) {
-  const int w = idx >> 6, l = idx & 63;
-  if (ndb >= 8) return {8 * (w & 1) + (l & 3) + 4 * ((l >> 4) & 1), 8 * (w >> 1) + ((l >> 2) & 3) + 4 * (l >> 5)};
-  return {(l & 3) + 4 * (l >> 4), (l >> 2) & 3};
+// Left operand for row tile a of X (= C-layout tiles of X^T in column a),
+// right operand for column tile b of X.
+__device__ __forceinline__ h8_t tri_row(const Tri& X, int a) {
+  return a == 0 ? bfrag(X.t[0], zero4()) : bfrag(X.t[1], X.t[2]);
+}
+__device__ __forceinline__ h8_t tri_col(const Tri& X, int b) {
+  return b == 0 ? bfrag(X.x[0], X.x[1]) : bfrag(zero4(), X.x[2]);
+}
+// Z = X Y for lower-triangular X, Y (both orientations).
+__device__ __forceinline__ Tri tri_mul(const Tri& X, const Tri& Y) {
+  const h8_t r0 = tri_row(X, 0), r1 = tri_row(X, 1), c0 = tri_col(Y, 0), c1 = tri_col(Y, 1);
+  Tri Z;
+  Z.x[0] = mma(r0, c0, zero4());
+  Z.x[1] = mma(r1, c0, zero4());
+  Z.x[2] = mma(r1, c1, zero4());
+  Z.t[0] = mma(c0, r0, zero4());
+  Z.t[1] = mma(c0, r1, zero4());
+  Z.t[2] = mma(c1, r1, zero4());
+  return Z;
+}
+// P + P Y (both orientations).
+__device__ __forceinline__ Tri tri_mul_add(const Tri& P, const Tri& Y) {
+  const h8_t r0 = tri_row(P, 0), r1 = tri_row(P, 1), c0 = tri_col(Y, 0), c1 = tri_col(Y, 1);
+  Tri Z;
+  Z.x[0] = mma(r0, c0, P.x[0]);
+  Z.x[1] = mma(r1, c0, P.x[1]);
+  Z.x[2] = mma(r1, c1, P.x[2]);
+  Z.t[0] = mma(c0, r0, P.t[0]);
+  Z.t[1] = mma(c0, r1, P.t[1]);
+  Z.t[2] = mma(c1, r1, P.t[2]);
+  return Z;
 }
 
 template <int DK, class IOT, class ST>
 __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p) {
-  constexpr int HT = DK / 16;   // 16-row state tiles
-  constexpr int KS = DK / 32;   // 32-deep k steps over d_k
-  constexpr int LDK = DK + 8;   // K / Q row stride (halfs)
-  constexpr int DB = DK / 8;    // 8-column blocks of a K row
-  constexpr int KBLK = 16 * DB; // K (Q) staging blocks per chunk
-  static_assert(KS >= 1, "d_k >= 32");
+  constexpr int HT = DK / 16;    // 16-row state tiles
+  constexpr int KS = DK / 32;    // 32-deep k steps over d_k
+  constexpr int LDQ = DK + 8;    // Q row stride (halfs)
+  constexpr int DB = DK / 8;     // 8-column blocks of a K row
+  constexpr int KBLK = 16 * DB;  // K (Q) staging blocks (4 tokens x 8 columns) per chunk
+  static_assert(KS >= 1 && KBLK <= 256, "d_k in {32, 64, 128}");
 
-  __shared__ __align__(16) _Float16 sKx[2 * kC * LDK];
-  __shared__ __align__(16) _Float16 sQx[2 * kC * LDK];
-  __shared__ __align__(16) _Float16 sKt[DK * LDT];     // K of the running chunk, d-major
-  __shared__ __align__(16) _Float16 sVt[64 * LDT];     // V of the running chunk, column-major
+  __shared__ __align__(16) _Float16 sK[3 * kC * LDK];
+  __shared__ __align__(16) _Float16 sQ[2 * kC * LDQ];
+  __shared__ __align__(16) _Float16 sV[kC * LDV];
   __shared__ __align__(16) _Float16 sA[2 * kC * LDA];  // [A11 | 0 ; -L21 | A22]
   __shared__ __align__(16) _Float16 sM[2 * kC * LDA];  // tril_incl(q k^T 2^(G_i - G_j))
   __shared__ __align__(16) float sG[3 * GTS];
-  __shared__ __align__(16) float sL[6 * BLK];   // L diagonal blocks 0-3, L_10, L_32
-  __shared__ __align__(16) float sAf[4 * BLK];  // fp32 inverses of the diagonal blocks
-  __shared__ __align__(16) float sT[2 * BLK];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int lr = lane & 15, lg = lane >> 4;
@@ -203,26 +197,44 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
 
   ST* pool = static_cast<ST*>(p.state);
   const int64_t head_off = p.layer * p.layer_stride + h * p.head_stride + col_base;
-  const int j = wave;  // chain wave: state columns 16j..16j+15
-  f4_t hT[HT];
+  const int j = wave;  // chain wave: state columns 32j..32j+31 (tiles 2j, 2j+1)
+  f4_t hT[2][HT];
+  // State slice rows 16 ti + 4 lg + e, columns 32 j + 16 u + lr: a wave-uniform
+  // base plus a 32-bit lane offset (kept opaque so the per-element offsets are
+  // not hoisted and held in registers across the chunk loop).
+  auto state_lane_off = [&]() {
+    uint32_t o = static_cast<uint32_t>((4 * lg * p.DV + 32 * j + lr) * sizeof(ST));
+    asm volatile("" : "+v"(o));
+    return o;
+  };
   auto load_state = [&]() {
     const int64_t rs = load_index(p.read_slots, n, p.read_is64);
-    const ST* src = rs >= 0 ? pool + rs * p.slot_stride + head_off + 16 * j + lr : nullptr;
+    const char* src = rs >= 0 ? reinterpret_cast<const char*>(pool + rs * p.slot_stride + head_off) : nullptr;
+    const uint32_t o = state_lane_off();
 #pragma unroll
-    for (int ti = 0; ti < HT; ++ti)
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) hT[ti][e] = src ? load_st(src + (16 * ti + 4 * lg + e) * p.DV) : 0.f;
+      for (int ti = 0; ti < HT; ++ti)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          hT[u][ti][e] = src ? load_st(reinterpret_cast<const ST*>(
+                                   src + ((16 * ti + e) * p.DV + 16 * u) * sizeof(ST) + o))
+                             : 0.f;
   };
   auto store_state = [&](int64_t slot_idx) {
-    ST* dst = pool + slot_idx * p.slot_stride + head_off + 16 * j + lr;
+    char* dst = reinterpret_cast<char*>(pool + slot_idx * p.slot_stride + head_off);
+    const uint32_t o = state_lane_off();
 #pragma unroll
-    for (int ti = 0; ti < HT; ++ti)
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) store_st(dst + (16 * ti + 4 * lg + e) * p.DV, hT[ti][e]);
+      for (int ti = 0; ti < HT; ++ti)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          store_st(reinterpret_cast<ST*>(dst + ((16 * ti + e) * p.DV + 16 * u) * sizeof(ST) + o), hT[u][ti][e]);
   };
 
   if (nchunks == 0) {  // empty sequence: the final state is the initial state
-    if (wave < 4 && p.fw_slots) {
+    if (wave < 2 && p.fw_slots) {
       const int64_t fw = load_index(p.fw_slots, n, p.fw_is64);
       if (fw >= 0) {
         load_state();
@@ -243,99 +255,170 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     reinterpret_cast<uint4*>(sM)[e] = make_uint4(0, 0, 0, 0);
   }
 
-  if (wave < 4) {
+  if (wave < 2) {
     // ==================================================================== chain waves
-    uint16_t* og = static_cast<uint16_t*>(p.out) + (bos * p.HV + h) * p.DV + col_base + 16 * j;
-    uint16_t* vng = p.v_new ? static_cast<uint16_t*>(p.v_new) + (bos * p.HV + h) * p.DV + col_base + 16 * j : nullptr;
+    uint16_t* og = static_cast<uint16_t*>(p.out) + (bos * p.HV + h) * p.DV + col_base + 32 * j;
+    uint16_t* vng = p.v_new ? static_cast<uint16_t*>(p.v_new) + (bos * p.HV + h) * p.DV + col_base + 32 * j : nullptr;
     const int64_t tok_stride = p.HV * p.DV;
     load_state();
     lds_barrier();  // P0
-    lds_barrier();  // P1
     lds_barrier();  // B(0)
     for (int64_t c = 0; c < nchunks; ++c) {
       const int nv = valid_rows(c);
-      const _Float16* K = sKx + (c & 1) * kC * LDK;
-      const _Float16* Q = sQx + (c & 1) * kC * LDK;
+      const _Float16* K = sK + (c % 3) * kC * LDK;
+      const _Float16* Q = sQ + (c & 1) * kC * LDQ;
       const float* gt = sG + (c % 3) * GTS;
-      // ---- S1: P = K h;  O^T = h^T Q^T (token columns);  R = beta (v - 2^G P)
-      f4_t P[4], Ot[4], R[4];
+      // ---- S1: P = K h -> R = beta (v - 2^G P);  O^T = h^T Q^T (token columns)
+      f4_t R[2][4];
+      {
+        f4_t P[2][4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) P[i] = Ot[i] = zero4();
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int m = 0; m < KS; ++m) {
-        const h8_t hb = bfrag(hT[2 * m], hT[2 * m + 1]);  // also the left operand of h^T
+          for (int i = 0; i < 4; ++i) P[u][i] = zero4();
+#pragma unroll
+        for (int m = 0; m < KS; ++m) {
+          const h8_t hb0 = bfrag(hT[0][2 * m], hT[0][2 * m + 1]);
+          const h8_t hb1 = bfrag(hT[1][2 * m], hT[1][2 * m + 1]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const h8_t kf = afrag(K, LDK, 16 * i + lr, 32 * m, lg);
+            P[0][i] = mma(kf, hb0, P[0][i]);
+            P[1][i] = mma(kf, hb1, P[1][i]);
+          }
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          P[i] = mma(afrag(K, LDK, 16 * i + lr, 32 * m, lg), hb, P[i]);
-          Ot[i] = mma(hb, afrag(Q, LDK, 16 * i + lr, 32 * m, lg), Ot[i]);
+          const int t0 = 16 * i + 4 * lg;
+          const f4_t e4 = *reinterpret_cast<const f4_t*>(gt + G_EXP + t0);
+          const f4_t b4 = *reinterpret_cast<const f4_t*>(gt + G_BETA + t0);
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            // V rows t0..t0+3 at column 32j + 16u + lr
+            const h4_t v4 = tr_read(sV + (16 * i + 4 * lg + (lr >> 2)) * LDV + 32 * j + 16 * u + 4 * (lr & 3));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) R[u][i][e] = b4[e] * (static_cast<float>(v4[e]) - e4[e] * P[u][i][e]);
+          }
+        }
+      }
+      f4_t Ot[2][4];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Ot[u][i] = zero4();
+#pragma unroll
+      for (int m = 0; m < KS; ++m) {
+        // the right operand of h doubles as the left operand of h^T
+        const h8_t hb0 = bfrag(hT[0][2 * m], hT[0][2 * m + 1]);
+        const h8_t hb1 = bfrag(hT[1][2 * m], hT[1][2 * m + 1]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const h8_t qf = afrag(Q, LDQ, 16 * i + lr, 32 * m, lg);
+          Ot[0][i] = mma(hb0, qf, Ot[0][i]);
+          Ot[1][i] = mma(hb1, qf, Ot[1][i]);
         }
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int t0 = 16 * i + 4 * lg;
-        const f4_t e4 = *reinterpret_cast<const f4_t*>(gt + G_EXP + t0);
-        const f4_t b4 = *reinterpret_cast<const f4_t*>(gt + G_BETA + t0);
-        const h4_t v4 = *reinterpret_cast<const h4_t*>(sVt + (16 * j + lr) * LDT + t0);
+        const float eo = gt[G_EXP + 16 * i + lr];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) R[i][e] = b4[e] * (static_cast<float>(v4[e]) - e4[e] * P[i][e]);
-        Ot[i] *= gt[G_EXP + 16 * i + lr];
+        for (int u = 0; u < 2; ++u) Ot[u][i] *= eo;
       }
       lds_barrier();  // M(c)
       // ---- S2: v'_top = A11 R_top; R_bot -= L21 v'_top; v'_bot = A22 R_bot
       const _Float16* A = sA + (c & 1) * kC * LDA;
-      f4_t V[4];
+      f4_t V[2][4];
+      h8_t vb0[2], vb1[2];
       {
-        const h8_t rb0 = bfrag(R[0], R[1]);
-        V[0] = mma(afrag(A, LDA, lr, 0, lg), rb0, zero4());
-        V[1] = mma(afrag(A, LDA, 16 + lr, 0, lg), rb0, zero4());
+        const h8_t a0 = afrag(A, LDA, lr, 0, lg), a1 = afrag(A, LDA, 16 + lr, 0, lg);
+        const h8_t l2 = afrag(A, LDA, 32 + lr, 0, lg), l3 = afrag(A, LDA, 48 + lr, 0, lg);  // -L21
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const h8_t rb0 = bfrag(R[u][0], R[u][1]);
+          V[u][0] = mma(a0, rb0, zero4());
+          V[u][1] = mma(a1, rb0, zero4());
+          vb0[u] = bfrag(V[u][0], V[u][1]);  // also the left operand of v'^T
+          R[u][2] = mma(l2, vb0[u], R[u][2]);
+          R[u][3] = mma(l3, vb0[u], R[u][3]);
+        }
+        const h8_t a2 = afrag(A, LDA, 32 + lr, 32, lg), a3 = afrag(A, LDA, 48 + lr, 32, lg);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const h8_t rb1 = bfrag(R[u][2], R[u][3]);
+          V[u][2] = mma(a2, rb1, zero4());
+          V[u][3] = mma(a3, rb1, zero4());
+          vb1[u] = bfrag(V[u][2], V[u][3]);
+        }
       }
-      const h8_t vb0 = bfrag(V[0], V[1]);  // also the left operand of v'^T
-      R[2] = mma(afrag(A, LDA, 32 + lr, 0, lg), vb0, R[2]);  // rows 32-63, cols 0-31 hold -L21
-      R[3] = mma(afrag(A, LDA, 48 + lr, 0, lg), vb0, R[3]);
+      // ---- S3a: o^T += v'^T M^T; a lane holds 4 consecutive output columns of one token
       {
-        const h8_t rb1 = bfrag(R[2], R[3]);
-        V[2] = mma(afrag(A, LDA, 32 + lr, 32, lg), rb1, zero4());
-        V[3] = mma(afrag(A, LDA, 48 + lr, 32, lg), rb1, zero4());
+        const _Float16* M = sM + (c & 1) * kC * LDA;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const h8_t mf = afrag(M, LDA, 16 * i + lr, 0, lg);
+#pragma unroll
+          for (int u = 0; u < 2; ++u) Ot[u][i] = mma(vb0[u], mf, Ot[u][i]);
+        }
+#pragma unroll
+        for (int i = 2; i < 4; ++i) {
+          const h8_t mf = afrag(M, LDA, 16 * i + lr, 32, lg);
+#pragma unroll
+          for (int u = 0; u < 2; ++u) Ot[u][i] = mma(vb1[u], mf, Ot[u][i]);
+        }
       }
-      const h8_t vb1 = bfrag(V[2], V[3]);
-      // ---- S3a: o^T += v'^T M^T; lane holds 4 consecutive output columns of one token
-      const _Float16* M = sM + (c & 1) * kC * LDA;
+      {
+        char* ob = reinterpret_cast<char*>(og + c * kC * tok_stride);
+        uint32_t o = static_cast<uint32_t>((lr * tok_stride + 4 * lg) * 2);
+        asm volatile("" : "+v"(o));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) Ot[i] = mma(vb0, afrag(M, LDA, 16 * i + lr, 0, lg), Ot[i]);
-      Ot[2] = mma(vb1, afrag(M, LDA, 32 + lr, 32, lg), Ot[2]);
-      Ot[3] = mma(vb1, afrag(M, LDA, 48 + lr, 32, lg), Ot[3]);
+        for (int i = 0; i < 4; ++i) {
+          if (16 * i + lr < nv) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = 16 * i + lr;
-        if (t < nv) {
-          uint2 w;
-          w.x = out_bits<IOT>(p.scale * Ot[i][0]) | (static_cast<uint32_t>(out_bits<IOT>(p.scale * Ot[i][1])) << 16);
-          w.y = out_bits<IOT>(p.scale * Ot[i][2]) | (static_cast<uint32_t>(out_bits<IOT>(p.scale * Ot[i][3])) << 16);
-          *reinterpret_cast<uint2*>(og + (c * kC + t) * tok_stride + 4 * lg) = w;
+            for (int u = 0; u < 2; ++u) {
+              uint2 w;
+              w.x = out_bits<IOT>(p.scale * Ot[u][i][0]) |
+                    (static_cast<uint32_t>(out_bits<IOT>(p.scale * Ot[u][i][1])) << 16);
+              w.y = out_bits<IOT>(p.scale * Ot[u][i][2]) |
+                    (static_cast<uint32_t>(out_bits<IOT>(p.scale * Ot[u][i][3])) << 16);
+              *reinterpret_cast<uint2*>(ob + (16 * i * tok_stride + 16 * u) * 2 + o) = w;
+            }
+          }
         }
       }
       if (vng) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int t = 16 * i + 4 * lg + e;
-            if (t < nv) vng[(c * kC + t) * tok_stride + lr] = out_bits<IOT>(V[i][e]);
-          }
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int t = 16 * i + 4 * lg + e;
+              if (t < nv) vng[(c * kC + t) * tok_stride + 16 * u + lr] = out_bits<IOT>(V[u][i][e]);
+            }
       }
       // ---- S3b: h <- 2^G_last h + K^T (2^(G_last - G) v')
       {
-        f4_t Vd[4];
+        h8_t db0[2], db1[2];
+        const f4_t d0 = *reinterpret_cast<const f4_t*>(gt + G_DEC + 4 * lg);
+        const f4_t d1 = *reinterpret_cast<const f4_t*>(gt + G_DEC + 16 + 4 * lg);
+        const f4_t d2 = *reinterpret_cast<const f4_t*>(gt + G_DEC + 32 + 4 * lg);
+        const f4_t d3 = *reinterpret_cast<const f4_t*>(gt + G_DEC + 48 + 4 * lg);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) Vd[i] = V[i] * *reinterpret_cast<const f4_t*>(gt + G_DEC + 16 * i + 4 * lg);
-        const h8_t db0 = bfrag(Vd[0], Vd[1]);
-        const h8_t db1 = bfrag(Vd[2], Vd[3]);
+        for (int u = 0; u < 2; ++u) {
+          db0[u] = bfrag(V[u][0] * d0, V[u][1] * d1);
+          db1[u] = bfrag(V[u][2] * d2, V[u][3] * d3);
+        }
         const float gl = gt[G_LAST];
 #pragma unroll
         for (int ti = 0; ti < HT; ++ti) {
-          f4_t acc = hT[ti] * gl;
-          acc = mma(afrag(sKt, LDT, 16 * ti + lr, 0, lg), db0, acc);
-          hT[ti] = mma(afrag(sKt, LDT, 16 * ti + lr, 32, lg), db1, acc);
+          const h8_t k0 = tfrag(K, LDK, 0, 16 * ti, lr, lg);
+          const h8_t k1 = tfrag(K, LDK, 32, 16 * ti, lr, lg);
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            f4_t acc = hT[u][ti] * gl;
+            acc = mma(k0, db0[u], acc);
+            hT[u][ti] = mma(k1, db1[u], acc);
+          }
         }
       }
       const int64_t cw = load_index(p.cw_slots, chunk_base + c, p.cw_is64);
@@ -348,18 +431,20 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     }
   } else {
     // ==================================================================== side waves
-    const int sw = wave - 4, st = tid - 256;
-    const bool kq_thread = st < KBLK;
-    const Blk kb = staging_block(st, DB);
+    const int sw = wave - 2;        // 0..5
+    const int st = tid - 256;       // staging thread index (waves 4-7)
+    const bool kq_thread = st >= 0 && st < KBLK;
     const bool v_thread = st >= 128;  // waves 6, 7: 4 tokens x 8 columns of the 64-column V slice
-    const Blk vb = staging_block(st - 128, 8);
-    const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + ((bos + 4 * kb.tb) * p.H + kh) * DK + 8 * kb.db;
-    const uint16_t* qbase = static_cast<const uint16_t*>(p.q) + ((bos + 4 * kb.tb) * p.H + kh) * DK + 8 * kb.db;
+    // K/Q block: 16-byte column block fastest (conflict-free 16-byte LDS writes)
+    const int ktb = st / DB, kdb = st % DB;
+    const int vtb = (st - 128) >> 3, vdb = (st - 128) & 7;
+    const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + ((bos + 4 * ktb) * p.H + kh) * DK + 8 * kdb;
+    const uint16_t* qbase = static_cast<const uint16_t*>(p.q) + ((bos + 4 * ktb) * p.H + kh) * DK + 8 * kdb;
     const uint16_t* vbase =
-        static_cast<const uint16_t*>(p.v) + ((bos + 4 * vb.tb) * p.HV + h) * p.DV + col_base + 8 * vb.db;
+        static_cast<const uint16_t*>(p.v) + ((bos + 4 * vtb) * p.HV + h) * p.DV + col_base + 8 * vdb;
     const int64_t krow = p.H * DK, kstride = kC * krow;
     const int64_t vrow = p.HV * p.DV, vstride = kC * vrow;
-    const int gtid = st - 192;  // wave 7 carries the gates
+    const int gtid = lane;  // wave 7 carries the gates
     uint4 pk[4], pq[4], pv[4];
     float pgate = 0.f, pbeta = 0.f;
 
@@ -368,12 +453,12 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         pk[u] = pq[u] = make_uint4(0, 0, 0, 0);
-        if (kq_thread && 4 * kb.tb + u < nk) {
+        if (kq_thread && 4 * ktb + u < nk) {
           pk[u] = *reinterpret_cast<const uint4*>(kbase + ck * kstride + u * krow);
           pq[u] = *reinterpret_cast<const uint4*>(qbase + ck * kstride + u * krow);
         }
       }
-      if (sw == 3) {
+      if (wave == 7) {
         const bool ok = gtid < nk;
         const int64_t off = (bos + ck * kC + (ok ? gtid : 0)) * p.HV + h;
         pgate = ok ? p.g[off] : 0.f;
@@ -385,20 +470,20 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         pv[u] = make_uint4(0, 0, 0, 0);
-        if (v_thread && 4 * vb.tb + u < nk) pv[u] = *reinterpret_cast<const uint4*>(vbase + cv * vstride + u * vrow);
+        if (v_thread && 4 * vtb + u < nk) pv[u] = *reinterpret_cast<const uint4*>(vbase + cv * vstride + u * vrow);
       }
     };
     auto stage_kq = [&](int64_t ck) {
       if (kq_thread) {
-        _Float16* kd = sKx + (ck & 1) * kC * LDK + (4 * kb.tb) * LDK + 8 * kb.db;
-        _Float16* qd = sQx + (ck & 1) * kC * LDK + (4 * kb.tb) * LDK + 8 * kb.db;
+        _Float16* kd = sK + (ck % 3) * kC * LDK + (4 * ktb) * LDK + 8 * kdb;
+        _Float16* qd = sQ + (ck & 1) * kC * LDQ + (4 * ktb) * LDQ + 8 * kdb;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           *reinterpret_cast<uint4*>(kd + u * LDK) = to_f16x8<IOT>(pk[u]);
-          *reinterpret_cast<uint4*>(qd + u * LDK) = to_f16x8<IOT>(pq[u]);
+          *reinterpret_cast<uint4*>(qd + u * LDQ) = to_f16x8<IOT>(pq[u]);
         }
       }
-      if (sw == 3) {  // chunk-local cumulative gate in log2 units (cumsum.py:19-75)
+      if (wave == 7) {  // chunk-local cumulative gate in log2 units (cumsum.py:19-75)
         const int nk = valid_rows(ck);
         float x = pgate;
 #pragma unroll
@@ -416,213 +501,176 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         if (gtid == 0) gt[G_LAST] = fast_exp2(Gl);
       }
     };
-    // 4 token rows x 8 columns (registers, raw) -> 8 column rows x 4 tokens (f16)
-    auto write_transposed = [&](_Float16* dst, const uint4 (&rows)[4], int tb, int db) {
-      h8_t r[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) r[u] = __builtin_bit_cast(h8_t, to_f16x8<IOT>(rows[u]));
-#pragma unroll
-      for (int d = 0; d < 8; ++d) {
-        const h4_t w = {r[0][d], r[1][d], r[2][d], r[3][d]};
-        *reinterpret_cast<h4_t*>(dst + (8 * db + d) * LDT + 4 * tb) = w;
-      }
-    };
     auto stage_v = [&]() {
-      if (v_thread) write_transposed(sVt, pv, vb.tb, vb.db);
-    };
-    // d-major copy of K(ck) for the state update, read back from the f16 K rows.
-    auto stage_kt = [&](int64_t ck) {
-      if (kq_thread) {
-        const _Float16* src = sKx + (ck & 1) * kC * LDK + (4 * kb.tb) * LDK + 8 * kb.db;
-        h8_t r[4];
+      if (v_thread) {
+        _Float16* vd = sV + (4 * vtb) * LDV + 8 * vdb;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) r[u] = *reinterpret_cast<const h8_t*>(src + u * LDK);
-#pragma unroll
-        for (int d = 0; d < 8; ++d) {
-          const h4_t w = {r[0][d], r[1][d], r[2][d], r[3][d]};
-          *reinterpret_cast<h4_t*>(sKt + (8 * kb.db + d) * LDT + 4 * kb.tb) = w;
-        }
+        for (int u = 0; u < 4; ++u) *reinterpret_cast<uint4*>(vd + u * LDV) = to_f16x8<IOT>(pv[u]);
       }
     };
 
-    // First half of the solve for chunk nc: tiles (transposed: lane = one row
-    // t, 4 consecutive columns s), masks, diagonal inverses.
-    auto solve_front = [&](int64_t nc) {
-      const _Float16* K = sKx + (nc & 1) * kC * LDK;
-      const _Float16* Q = sQx + (nc & 1) * kC * LDK;
+    // Solve for chunk nc.  S tiles (ti, tj) of X K^T in the "row" orientation:
+    // lane (g, c) holds entry (t = 16 ti + c, s = 16 tj + 4 g + e).
+    auto solve = [&](int64_t nc) {
+      const _Float16* K = sK + (nc % 3) * kC * LDK;
+      const _Float16* Q = sQ + (nc & 1) * kC * LDQ;
       const float* gt = sG + (nc % 3) * GTS;
       _Float16* A = sA + (nc & 1) * kC * LDA;
       _Float16* M = sM + (nc & 1) * kC * LDA;
-      // tile (ti, tj) entry for row t = 16 ti + lr, columns s = 16 tj + 4 lg + e
-      auto decays = [&](int ti, int tj) {
-        const f4_t gs = *reinterpret_cast<const f4_t*>(gt + 16 * tj + 4 * lg);
-        const float gti = gt[16 * ti + lr];
-        f4_t d;
+      // entries (t, s..s+3) of a row-orientation tile -> masked values
+      auto masked = [&](f4_t s, int t, int s0, bool strict, bool with_beta) {
+        const f4_t gs = *reinterpret_cast<const f4_t*>(gt + s0);
+        const float gti = gt[t];
+        const float bt = with_beta ? gt[G_BETA + t] : 1.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) d[e] = fast_exp2(fminf(gti - gs[e], 0.f));
-        return d;
-      };
-      auto lmask = [&](f4_t s, int ti, int tj) {
-        const f4_t d = decays(ti, tj);
-        const float bt = gt[G_BETA + 16 * ti + lr];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) s[e] = (16 * ti + lr > 16 * tj + 4 * lg + e) ? bt * s[e] * d[e] : 0.f;
+        for (int e = 0; e < 4; ++e) {
+          const bool keep = strict ? t > s0 + e : t >= s0 + e;
+          s[e] = keep ? bt * s[e] * fast_exp2(fminf(gti - gs[e], 0.f)) : 0.f;
+        }
         return s;
       };
-      auto store_blockf = [&](float* B, f4_t v) { *reinterpret_cast<f4_t*>(B + lr * LDB + 4 * lg) = v; };
-      auto store_h4 = [&](_Float16* X, int ti, int tj, f4_t v) {
+      auto store_row4 = [&](_Float16* X, int t, int s0, f4_t v) {
         const h4_t w = {to_op(v[0]), to_op(v[1]), to_op(v[2]), to_op(v[3])};
-        *reinterpret_cast<h4_t*>(X + (16 * ti + lr) * LDA + 16 * tj + 4 * lg) = w;
+        *reinterpret_cast<h4_t*>(X + t * LDA + s0) = w;
       };
-      auto mstore = [&](f4_t s, int ti, int tj) {
-        const f4_t d = decays(ti, tj);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) s[e] = (16 * ti + lr >= 16 * tj + 4 * lg + e) ? s[e] * d[e] : 0.f;
-        store_h4(M, ti, tj, s);
-      };
-      // transposed tile (ti, tj) of X K^T: left operand K rows of tj, right X rows of ti
-      if (sw == 0) {
-        f4_t dg[4];
-#pragma unroll
-        for (int b = 0; b < 4; ++b) dg[b] = zero4();
-#pragma unroll
-        for (int m = 0; m < KS; ++m)
-#pragma unroll
-          for (int b = 0; b < 4; ++b) {
-            const h8_t kf = afrag(K, LDK, 16 * b + lr, 32 * m, lg);
-            dg[b] = mma(kf, kf, dg[b]);
-          }
-#pragma unroll
-        for (int b = 0; b < 4; ++b) store_blockf(sL + b * BLK, lmask(dg[b], b, b));
-        wave_sync();
-        // (I + L_bb)^-1 by forward substitution; lane = (block, column)
-        const int b = lane >> 4, col = lane & 15;
-        const float* Lbb = sL + b * BLK;
-        float x[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          float a0 = (i == col) ? 1.f : 0.f, a1 = 0.f;
-#pragma unroll
-          for (int jj = 0; jj < i; jj += 2) {
-            a0 = fmaf(-Lbb[i * LDB + jj], x[jj], a0);
-            if (jj + 1 < i) a1 = fmaf(-Lbb[i * LDB + jj + 1], x[jj + 1], a1);
-          }
-          x[i] = a0 + a1;
-        }
-        float* Ab = sAf + b * BLK;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          Ab[i * LDB + col] = x[i];
-          A[(16 * b + i) * LDA + 16 * b + col] = to_op(x[i]);
-        }
-      } else if (sw == 1) {
-        f4_t s10 = zero4(), s32 = zero4(), s20 = zero4(), s21 = zero4(), s30 = zero4(), s31 = zero4();
-#pragma unroll
-        for (int m = 0; m < KS; ++m) {
-          const h8_t k0 = afrag(K, LDK, lr, 32 * m, lg);
-          const h8_t k1 = afrag(K, LDK, 16 + lr, 32 * m, lg);
-          const h8_t k2 = afrag(K, LDK, 32 + lr, 32 * m, lg);
-          const h8_t k3 = afrag(K, LDK, 48 + lr, 32 * m, lg);
-          s10 = mma(k0, k1, s10);
-          s32 = mma(k2, k3, s32);
-          s20 = mma(k0, k2, s20);
-          s21 = mma(k1, k2, s21);
-          s30 = mma(k0, k3, s30);
-          s31 = mma(k1, k3, s31);
-        }
-        store_blockf(sL + 4 * BLK, lmask(s10, 1, 0));
-        store_blockf(sL + 5 * BLK, lmask(s32, 3, 2));
-        store_h4(A, 2, 0, -lmask(s20, 2, 0));
-        store_h4(A, 2, 1, -lmask(s21, 2, 1));
-        store_h4(A, 3, 0, -lmask(s30, 3, 0));
-        store_h4(A, 3, 1, -lmask(s31, 3, 1));
-      } else if (sw == 2) {
-        f4_t m00 = zero4(), m10 = zero4(), m11 = zero4(), m20 = zero4(), m21 = zero4();
-#pragma unroll
-        for (int m = 0; m < KS; ++m) {
-          const h8_t q0 = afrag(Q, LDK, lr, 32 * m, lg);
-          const h8_t q1 = afrag(Q, LDK, 16 + lr, 32 * m, lg);
-          const h8_t q2 = afrag(Q, LDK, 32 + lr, 32 * m, lg);
-          const h8_t k0 = afrag(K, LDK, lr, 32 * m, lg);
-          const h8_t k1 = afrag(K, LDK, 16 + lr, 32 * m, lg);
-          m00 = mma(k0, q0, m00);
-          m10 = mma(k0, q1, m10);
-          m11 = mma(k1, q1, m11);
-          m20 = mma(k0, q2, m20);
-          m21 = mma(k1, q2, m21);
-        }
-        mstore(m00, 0, 0);
-        mstore(m10, 1, 0);
-        mstore(m11, 1, 1);
-        mstore(m20, 2, 0);
-        mstore(m21, 2, 1);
-      } else {
-        f4_t m22 = zero4(), m30 = zero4(), m31 = zero4(), m32 = zero4(), m33 = zero4();
-#pragma unroll
-        for (int m = 0; m < KS; ++m) {
-          const h8_t q2 = afrag(Q, LDK, 32 + lr, 32 * m, lg);
-          const h8_t q3 = afrag(Q, LDK, 48 + lr, 32 * m, lg);
-          const h8_t k0 = afrag(K, LDK, lr, 32 * m, lg);
-          const h8_t k1 = afrag(K, LDK, 16 + lr, 32 * m, lg);
-          const h8_t k2 = afrag(K, LDK, 32 + lr, 32 * m, lg);
-          const h8_t k3 = afrag(K, LDK, 48 + lr, 32 * m, lg);
-          m22 = mma(k2, q2, m22);
-          m30 = mma(k0, q3, m30);
-          m31 = mma(k1, q3, m31);
-          m32 = mma(k2, q3, m32);
-          m33 = mma(k3, q3, m33);
-        }
-        mstore(m22, 2, 2);
-        mstore(m30, 3, 0);
-        mstore(m31, 3, 1);
-        mstore(m32, 3, 2);
-        mstore(m33, 3, 3);
-      }
-    };
-    // Second half: A_{j+1,j} = -A_{j+1,j+1} L_{j+1,j} A_jj for j = 0 (wave 4) and j = 2 (wave 5).
-    auto solve_back = [&](int64_t nc) {
       if (sw < 2) {
-        const int jb = 2 * sw;
-        float* T = sT + sw * BLK;
-        const f4_t t = mma_split(a_block(sL + (4 + sw) * BLK, lane), b_block(sAf + jb * BLK, lane));
+        // A_bb = (I + L_bb)^-1 for the 32-token half b = sw
+        const int r0 = 32 * sw;
+        f4_t s00 = zero4(), s11 = zero4(), s10 = zero4(), s01 = zero4();
 #pragma unroll
-        for (int e = 0; e < 4; ++e) T[(4 * lg + e) * LDB + lr] = t[e];
-        wave_sync();
-        const f4_t a = mma_split(a_block(sAf + (jb + 1) * BLK, lane), b_block(T, lane));
-        _Float16* A = sA + (nc & 1) * kC * LDA;
+        for (int m = 0; m < KS; ++m) {
+          const h8_t k0 = afrag(K, LDK, r0 + lr, 32 * m, lg);
+          const h8_t k1 = afrag(K, LDK, r0 + 16 + lr, 32 * m, lg);
+          s00 = mma(k0, k0, s00);
+          s11 = mma(k1, k1, s11);
+          s10 = mma(k1, k0, s10);  // C layout: entry (16 + 4g + e, c)
+          s01 = mma(k0, k1, s01);  // C layout: entry (4g + e, 16 + c) of S^T
+        }
+        // C-layout tiles of L (row 4g + e, col c) and of L^T (row 4g + e, col c
+        // of L^T = entry (c, 4g + e) of L); S is symmetric on the diagonal tiles.
+        auto lmask_c = [&](f4_t s, int t0, int sc) {  // entries (t0 + 4g + e, sc + c)
+          const f4_t gt4 = *reinterpret_cast<const f4_t*>(gt + t0 + 4 * lg);
+          const f4_t bt4 = *reinterpret_cast<const f4_t*>(gt + G_BETA + t0 + 4 * lg);
+          const float gsc = gt[sc + lr];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) A[(16 * (jb + 1) + 4 * lg + e) * LDA + 16 * jb + lr] = to_op(-a[e]);
+          for (int e = 0; e < 4; ++e)
+            s[e] = (t0 + 4 * lg + e > sc + lr) ? bt4[e] * s[e] * fast_exp2(fminf(gt4[e] - gsc, 0.f)) : 0.f;
+          return s;
+        };
+        auto lmask_t = [&](f4_t s, int tc, int s0) {  // entries (tc + c, s0 + 4g + e)
+          return masked(s, tc + lr, s0 + 4 * lg, true, true);
+        };
+        Tri L;
+        L.x[0] = lmask_c(s00, r0, r0);
+        L.x[1] = lmask_c(s10, r0 + 16, r0);
+        L.x[2] = lmask_c(s11, r0 + 16, r0 + 16);
+        L.t[0] = lmask_t(s00, r0, r0);
+        L.t[1] = lmask_t(s01, r0 + 16, r0);
+        L.t[2] = lmask_t(s11, r0 + 16, r0 + 16);
+        // P1 = I - L + L^2 - L^3, then P <- P + P L^(2^k)
+        const Tri L2 = tri_mul(L, L);
+        const Tri L3 = tri_mul(L, L2);
+        Tri P;
+#pragma unroll
+        for (int q = 0; q < 3; ++q) {
+          P.x[q] = L2.x[q] - L.x[q] - L3.x[q];
+          P.t[q] = L2.t[q] - L.t[q] - L3.t[q];
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float one = (4 * lg + e == lr) ? 1.f : 0.f;
+          P.x[0][e] += one;
+          P.x[2][e] += one;
+          P.t[0][e] += one;
+          P.t[2][e] += one;
+        }
+        const Tri L4 = tri_mul(L2, L2);
+        P = tri_mul_add(P, L4);
+        const Tri L8 = tri_mul(L4, L4);
+        P = tri_mul_add(P, L8);
+        const Tri L16 = tri_mul(L8, L8);
+        P = tri_mul_add(P, L16);
+        // row-major A_bb: C-layout tile (a, b) of A^T holds row 16b + c, columns 16a + 4g..+3
+        store_row4(A, r0 + lr, r0 + 4 * lg, P.t[0]);
+        store_row4(A, r0 + 16 + lr, r0 + 4 * lg, P.t[1]);
+        store_row4(A, r0 + 16 + lr, r0 + 16 + 4 * lg, P.t[2]);
+      } else {
+        // Row-orientation tiles: (ti, tj) of Q K^T -> M, and of K K^T for -L21.
+        // Waves 4-7 split them: {-L21 (2,0),(2,1)} {-L21 (3,0),(3,1)} and M rows.
+        const int w = sw - 2;  // 0..3
+        auto tile = [&](const _Float16* X, int ldx, int ti, int tj) {
+          f4_t acc = zero4();
+#pragma unroll
+          for (int m = 0; m < KS; ++m)
+            acc = mma(afrag(K, LDK, 16 * tj + lr, 32 * m, lg), afrag(X, ldx, 16 * ti + lr, 32 * m, lg), acc);
+          return acc;
+        };
+        auto mtile = [&](int ti, int tj) {
+          const int t = 16 * ti + lr, s0 = 16 * tj + 4 * lg;
+          store_row4(M, t, s0, masked(tile(Q, LDQ, ti, tj), t, s0, false, false));
+        };
+        auto ltile = [&](int ti, int tj) {
+          const int t = 16 * ti + lr, s0 = 16 * tj + 4 * lg;
+          store_row4(A, t, s0, -masked(tile(K, LDK, ti, tj), t, s0, true, true));
+        };
+        if (w == 0) {
+          ltile(2, 0);
+          ltile(2, 1);
+          mtile(0, 0);
+          mtile(1, 0);
+        } else if (w == 1) {
+          ltile(3, 0);
+          ltile(3, 1);
+          mtile(1, 1);
+          mtile(2, 0);
+        } else if (w == 2) {
+          mtile(2, 1);
+          mtile(2, 2);
+          mtile(3, 0);
+        } else {
+          mtile(3, 1);
+          mtile(3, 2);
+          mtile(3, 3);
+        }
       }
     };
 
-    // ---- prologue: chunks 0 and 1 staged, chunk 0 solved
-    prefetch_kq(0);
-    prefetch_v(0);
-    stage_kq(0);
-    stage_v();
-    if (nchunks > 1) {
-      prefetch_kq(1);
-      prefetch_v(1);
-      stage_kq(1);
-    }
-    if (nchunks > 2) prefetch_kq(2);
-    lds_barrier();  // P0
-    solve_front(0);
-    lds_barrier();  // P1
-    solve_back(0);
-    lds_barrier();  // B(0)
-    for (int64_t c = 0; c < nchunks; ++c) {
-      if (c + 1 < nchunks) solve_front(c + 1);
-      stage_kt(c);
-      lds_barrier();  // M(c)
-      if (c + 1 < nchunks) {
-        solve_back(c + 1);
-        stage_v();
+    // Waves 2-3 (the inverses) and 4-7 (tiles, staging) run separate loops
+    // with the same barrier sequence, so that the prefetch registers of the
+    // staging waves are not live in the inverse code.
+    if (sw < 2) {
+      lds_barrier();  // P0
+      solve(0);
+      lds_barrier();  // B(0)
+      for (int64_t c = 0; c < nchunks; ++c) {
+        if (c + 1 < nchunks) solve(c + 1);
+        lds_barrier();  // M(c)
+        lds_barrier();  // B(c+1)
       }
-      if (c + 2 < nchunks) stage_kq(c + 2);
-      if (c + 3 < nchunks) prefetch_kq(c + 3);
-      if (c + 2 < nchunks) prefetch_v(c + 2);
-      lds_barrier();  // B(c+1)
+    } else {
+      // ---- prologue: chunks 0 and 1 staged, chunk 0 solved
+      prefetch_kq(0);
+      prefetch_v(0);
+      stage_kq(0);
+      stage_v();
+      if (nchunks > 1) {
+        prefetch_kq(1);
+        prefetch_v(1);
+        stage_kq(1);
+      }
+      if (nchunks > 2) prefetch_kq(2);
+      lds_barrier();  // P0
+      solve(0);
+      lds_barrier();  // B(0)
+      for (int64_t c = 0; c < nchunks; ++c) {
+        if (c + 1 < nchunks) solve(c + 1);
+        lds_barrier();  // M(c)
+        if (c + 1 < nchunks) stage_v();
+        if (c + 2 < nchunks) stage_kq(c + 2);
+        if (c + 3 < nchunks) prefetch_kq(c + 3);
+        if (c + 2 < nchunks) prefetch_v(c + 2);
+        lds_barrier();  // B(c+1)
+      }
     }
   }
 }
