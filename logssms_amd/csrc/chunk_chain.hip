@@ -109,10 +109,30 @@ template <> __device__ __forceinline__ uint4 to_f16x8<bf16>(uint4 raw) {
   };
   return make_uint4(cvt(raw.x), cvt(raw.y), cvt(raw.z), cvt(raw.w));
 }
+// Two outputs rounded to the io type (round-to-nearest-even, one packed convert).
+typedef float f2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+template <class IOT> __device__ __forceinline__ uint32_t out_pack2(float a, float b);
+template <> __device__ __forceinline__ uint32_t out_pack2<bf16>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2_t{a, b}, bf2_t));
+}
+template <> __device__ __forceinline__ uint32_t out_pack2<f16>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2_t{a, b}, h2_t));
+}
 template <class IOT> __device__ __forceinline__ uint16_t out_bits(float x);
 template <> __device__ __forceinline__ uint16_t out_bits<bf16>(float x) { return f32_to_bf16_bits(x); }
 template <> __device__ __forceinline__ uint16_t out_bits<f16>(float x) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+}
+
+// Block-uniform index read through the scalar data cache (a scalar load: it
+// is waited on with the LDS counter, never behind outstanding vector stores).
+__device__ __forceinline__ int64_t uniform_index(const void* p, int64_t i, int is64) {
+  typedef __attribute__((address_space(4))) const int64_t ci64;
+  typedef __attribute__((address_space(4))) const int32_t ci32;
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  return is64 ? reinterpret_cast<ci64*>(a)[i] : static_cast<int64_t>(reinterpret_cast<ci32*>(a)[i]);
 }
 
 template <class ST> __device__ __forceinline__ float load_st(const ST* p) { return to_f32(*p); }
@@ -187,8 +207,8 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
   const int64_t h = kh * (p.HV / p.H) + member / p.nvs;
   const int64_t col_base = static_cast<int64_t>(member % p.nvs) * 64;
 
-  const int64_t bos = load_index(p.cu, n, p.cu_is64);
-  const int64_t len = load_index(p.cu, n + 1, p.cu_is64) - bos;
+  const int64_t bos = uniform_index(p.cu, n, p.cu_is64);
+  const int64_t len = uniform_index(p.cu, n + 1, p.cu_is64) - bos;
   const int64_t nchunks = (len + kC - 1) / kC;
   auto valid_rows = [&](int64_t c) -> int {
     const int64_t rem = len - c * kC;
@@ -208,7 +228,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     return o;
   };
   auto load_state = [&]() {
-    const int64_t rs = load_index(p.read_slots, n, p.read_is64);
+    const int64_t rs = uniform_index(p.read_slots, n, p.read_is64);
     const char* src = rs >= 0 ? reinterpret_cast<const char*>(pool + rs * p.slot_stride + head_off) : nullptr;
     const uint32_t o = state_lane_off();
 #pragma unroll
@@ -235,7 +255,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
 
   if (nchunks == 0) {  // empty sequence: the final state is the initial state
     if (wave < 2 && p.fw_slots) {
-      const int64_t fw = load_index(p.fw_slots, n, p.fw_is64);
+      const int64_t fw = uniform_index(p.fw_slots, n, p.fw_is64);
       if (fw >= 0) {
         load_state();
         store_state(fw);
@@ -245,7 +265,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
   }
   int64_t chunk_base = 0;
   for (int64_t m = 0; m < n; ++m) {
-    const int64_t lm = load_index(p.cu, m + 1, p.cu_is64) - load_index(p.cu, m, p.cu_is64);
+    const int64_t lm = uniform_index(p.cu, m + 1, p.cu_is64) - uniform_index(p.cu, m, p.cu_is64);
     chunk_base += (lm + kC - 1) / kC;
   }
 
@@ -261,10 +281,18 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     uint16_t* vng = p.v_new ? static_cast<uint16_t*>(p.v_new) + (bos * p.HV + h) * p.DV + col_base + 32 * j : nullptr;
     const int64_t tok_stride = p.HV * p.DV;
     load_state();
+    // No vector-memory load may be outstanding at the loop head (a wait there
+    // would also wait for the previous chunk's output stores): consume the
+    // loaded state before entering the loop.
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int ti = 0; ti < HT; ++ti) asm volatile("" ::"v"(hT[u][ti]));
     lds_barrier();  // P0
     lds_barrier();  // B(0)
     for (int64_t c = 0; c < nchunks; ++c) {
       const int nv = valid_rows(c);
+      const int64_t cw = uniform_index(p.cw_slots, chunk_base + c, p.cw_is64);  // checkpoint slot
       const _Float16* K = sK + (c % 3) * kC * LDK;
       const _Float16* Q = sQ + (c & 1) * kC * LDQ;
       const float* gt = sG + (c % 3) * GTS;
@@ -376,10 +404,8 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
               uint2 w;
-              w.x = out_bits<IOT>(p.scale * Ot[u][i][0]) |
-                    (static_cast<uint32_t>(out_bits<IOT>(p.scale * Ot[u][i][1])) << 16);
-              w.y = out_bits<IOT>(p.scale * Ot[u][i][2]) |
-                    (static_cast<uint32_t>(out_bits<IOT>(p.scale * Ot[u][i][3])) << 16);
+              w.x = out_pack2<IOT>(p.scale * Ot[u][i][0], p.scale * Ot[u][i][1]);
+              w.y = out_pack2<IOT>(p.scale * Ot[u][i][2], p.scale * Ot[u][i][3]);
               *reinterpret_cast<uint2*>(ob + (16 * i * tok_stride + 16 * u) * 2 + o) = w;
             }
           }
@@ -421,12 +447,11 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
           }
         }
       }
-      const int64_t cw = load_index(p.cw_slots, chunk_base + c, p.cw_is64);
       if (cw >= 0) store_state(cw);
       lds_barrier();  // B(c+1)
     }
     if (p.fw_slots) {
-      const int64_t fw = load_index(p.fw_slots, n, p.fw_is64);
+      const int64_t fw = uniform_index(p.fw_slots, n, p.fw_is64);
       if (fw >= 0) store_state(fw);
     }
   } else {
