@@ -2,13 +2,16 @@
 
 Headline (``value``): Qwen3-Next linear-attention layer prefill (BASELINE
 config 2) -- 4 x 4096 packed tokens, 16 qk / 32 v heads, d = 128, bf16
-q/k/v, fp32 state pool, conv width 4.  One step = the backend prefill:
-``prefill_frontend`` (conv-history gather, packed conv + SiLU + window
-snapshots, split, prepare_gdn) followed by the chunked gated-delta-rule kernel
-writing the output and the final per-sequence states into pool slots.
-``value`` is prefill tokens/s; ``roofline`` reports the chunk kernel against
-the dense 16-bit MFMA peak from the algorithmic flop count
-(10 C d + 6 d^2 + 2/3 C^2 per token per v-head).
+projections, fp32 state pool, conv width 4.  One step = the backend prefill
+``prefill_fused``: the q/k pass (conv + SiLU + L2 norm of the q/k channels),
+the chunk-kernel launch whose staging waves compute the v conv + SiLU and the
+gates of each chunk from mixed_qkv, writing the output and the final
+per-sequence states into pool slots, then the conv-window snapshot launch.
+``value`` is prefill tokens/s; ``roofline`` reports the chunk kernel (timed
+alone with events around its launch) against the dense 16-bit MFMA peak from
+the algorithmic flop count (10 C d + 6 d^2 + 2/3 C^2 per token per v-head).
+``extra.prefill_two_step_ms`` times the unfused path (``prefill_frontend``
+then the chunk kernel) on the same inputs.
 
 ``extra`` reports the HBM-bound paths: decode (config 3) and spec-decode
 verify (config 5) in GB/s against 8 TB/s, from the canonical byte formulas.
@@ -102,18 +105,26 @@ def make_prefill(seed=2, lengths=(4096, 4096, 4096, 4096)):
     dt_bias = torch.zeros(HV)
     nchunks = [(n + C - 1) // C for n in lengths]
     chunk_write = torch.full((sum(nchunks),), -1, dtype=torch.int64)
+    conv_tokens = torch.full((T,), -1, dtype=torch.int64)
     off = 0
     for i, nc in enumerate(nchunks):
         off += nc
         chunk_write[off - 1] = i  # final state of sequence i -> pool slot i
+        conv_tokens[cu[i + 1] - 1] = i  # final conv window of sequence i -> pool slot i
+    snap_rows = torch.tensor(cu[1:], dtype=torch.int64) - 1
     return dict(mixed=mixed, weight=weight, gate=gate, beta=beta, A_log=A_log, dt_bias=dt_bias,
                 cu=torch.tensor(cu), baseline=torch.full((N,), -1, dtype=torch.int64), chunk_write=chunk_write,
-                conv_tokens=torch.full((T,), -1, dtype=torch.int64), N=N, T=T)
+                conv_tokens=conv_tokens, snap_rows=snap_rows, snap_slots=torch.arange(N, dtype=torch.int64), N=N, T=T)
 
 
-def prefill_gpu(inp, dev, events=None):
+def prefill_gpu(inp, dev, events=None, fused=True):
+    """One backend prefill step.  fused: ``prefill_fused`` (q/k pass, then the
+    chunk kernel computing the v conv + SiLU and the gates itself, then the
+    conv-snapshot launch); otherwise the two-step path (``prefill_frontend``
+    writing q, k, v, g, beta, then the chunk kernel).  `events` collects a
+    (start, end) event pair around each chunk-kernel launch."""
     from logssms_amd.kernel.linear_attention import ChunkStateIO, chunk_gated_delta_rule_to_cache
-    from logssms_amd.kernel.linear_attention.fused_backend import prefill_frontend
+    from logssms_amd.kernel.linear_attention.fused_backend import prefill_frontend, prefill_fused
     cfg = _config()
     d = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
     conv_pool = torch.zeros(max(8, d["N"]), 1, CONV_DIM, W - 1, device=dev, dtype=torch.bfloat16)
@@ -121,16 +132,31 @@ def prefill_gpu(inp, dev, events=None):
     out = torch.empty(1, d["T"], HV, D, device=dev, dtype=torch.bfloat16)
     io = ChunkStateIO(state_pool, d["baseline"], d["chunk_write"], layer=0)
 
+    def mark():
+        if events is None:
+            return None
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        return ev
+
     def step():
-        q, k, v, g, b = prefill_frontend(d["mixed"], d["gate"], d["beta"], d["weight"], d["A_log"], d["dt_bias"],
-                                         cfg, conv_pool, d["cu"], d["baseline"], d["conv_tokens"])
-        if events is not None:
-            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s.record()
-        chunk_gated_delta_rule_to_cache(q, k, v, g, b, io, d["cu"], out=out, return_v_new=False)
-        if events is not None:
-            e.record()
-            events.append((s, e))
+        if fused:
+            ev = None
+            if events is not None:
+                ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                events.append(ev)
+            o = prefill_fused(d["mixed"], d["gate"], d["beta"], d["weight"], d["A_log"], d["dt_bias"], cfg,
+                              conv_pool, state_pool, d["cu"], d["baseline"], d["chunk_write"], d["snap_rows"],
+                              d["snap_slots"], out=out[0], chunk_events=ev)
+            assert o is not None
+            return out
+        else:
+            q, k, v, g, b = prefill_frontend(d["mixed"], d["gate"], d["beta"], d["weight"], d["A_log"],
+                                             d["dt_bias"], cfg, conv_pool, d["cu"], d["baseline"], d["conv_tokens"])
+            s = mark()
+            chunk_gated_delta_rule_to_cache(q, k, v, g, b, io, d["cu"], out=out, return_v_new=False)
+            if events is not None:
+                events.append((s, mark()))
         return out
 
     return step, state_pool, out
@@ -256,11 +282,15 @@ def main():
         step, state_pool, out = prefill_gpu(inp, dev, events)
         ms = _time(step, args.steps, args.warmup, events)
         chunk_ms = _kernel_ms(events)
+        step2, _, _ = prefill_gpu(inp, dev, None, fused=False)
+        extra["prefill_two_step_ms"] = _time(step2, args.steps, args.warmup)
+        del step2
         T = inp["T"]
         flops = FLOP_PER_TOKEN_HEAD * T * HV
         achieved = flops / (chunk_ms * 1e-3)
-        # HBM traffic of the chunk kernel (algorithmic): q,k,v in, o out, g/beta in, final states out
-        chunk_bytes = T * (2 * H * D * 2 + HV * D * 2) + T * HV * D * 2 + 2 * T * HV * 4 + inp["N"] * S_BYTES
+        # HBM traffic of the fused chunk kernel (algorithmic): normalised q, k and the v columns of
+        # mixed_qkv in, the bf16 gate/beta projections in, o out, final states out
+        chunk_bytes = T * (2 * H * D + HV * D) * 2 + 2 * T * HV * 2 + T * HV * D * 2 + inp["N"] * S_BYTES
         result.update(
             metric="GDN prefill tokens/s (Qwen3-Next layer, 4x4096 packed)",
             value=T / (ms * 1e-3),
@@ -273,11 +303,12 @@ def main():
                     "seq_len": 4096, "heads_qk": H, "heads_v": HV, "head_dim": D, "chunk": C,
                     "parallelism": "single GPU"},
             roofline={"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_MFMA_16BIT / 1e12,
-                      "unit": "TFLOP/s", "frac": achieved / PEAK_MFMA_16BIT, "traffic": _traffic("chunk_kernel_cfg2"),
-                      "kernel": "chunk_kernel", "kernel_ms": chunk_ms,
+                      "unit": "TFLOP/s", "frac": achieved / PEAK_MFMA_16BIT,
+                      "traffic": _traffic("chunk_chain_kernel_fused_cfg2"),
+                      "kernel": "chunk_chain_kernel<128, bf16, float, fused>", "kernel_ms": chunk_ms,
                       "algorithmic_flop_per_launch": flops, "algorithmic_bytes_per_launch": chunk_bytes},
         )
-        extra["prefill_frontend_ms"] = ms - chunk_ms
+        extra["prefill_qk_and_snapshot_ms"] = ms - chunk_ms
         if not args.no_cpu_baseline:
             threads = len(os.sched_getaffinity(0))
             sample = 4096

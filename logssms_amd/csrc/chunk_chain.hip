@@ -29,12 +29,21 @@
 //     and 3 form A11 and A22 (k k^T tiles, masks, product-form inverse, all
 //     in registers), waves 4-7 the masked q k^T tiles (M) and -L21, and stage
 //     / prefetch later chunks (K, Q, V tiles and the gate table).
+//   * Waves i and i + 4 share a SIMD (chain waves with waves 4-5, inverse
+//     waves with waves 6-7).
+//   * Fused variant (FUSED): the V tiles are the conv + SiLU of the raw
+//     projections, computed by waves 4-5 before the M barrier, and the gate
+//     table is prepared from the raw gate / beta projections; q and k come
+//     normalised from a separate pass (their conv is shared by every
+//     workgroup of a key head).
 // Two workgroup barriers per chunk (LDS-only waits, so global prefetches stay
 // in flight).  MFMA operands are f16 (bf16 inputs convert exactly; values
 // saturate at +-65504) with fp32 accumulation.
 //
 // Roofline: MFMA (16-bit).  Algorithmic flops per token per v-head:
 // 10 C d + 6 d^2 + 2/3 C^2 (C = 64, d = 128).
+#include <type_traits>
+
 #include "chunk_common.hpp"
 
 namespace gdn {
@@ -48,6 +57,8 @@ typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef short s4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 to_uint4(u4_t v) { return make_uint4(v[0], v[1], v[2], v[3]); }
 
 // LDS row strides (halfs).  K rows: 76 dwords, so both the 8-byte row reads
 // of the left operands and the 4-row transpose reads avoid bank conflicts.
@@ -109,17 +120,6 @@ template <> __device__ __forceinline__ uint4 to_f16x8<bf16>(uint4 raw) {
   };
   return make_uint4(cvt(raw.x), cvt(raw.y), cvt(raw.z), cvt(raw.w));
 }
-// Two outputs rounded to the io type (round-to-nearest-even, one packed convert).
-typedef float f2_t __attribute__((ext_vector_type(2)));
-typedef __bf16 bf2_t __attribute__((ext_vector_type(2)));
-typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
-template <class IOT> __device__ __forceinline__ uint32_t out_pack2(float a, float b);
-template <> __device__ __forceinline__ uint32_t out_pack2<bf16>(float a, float b) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2_t{a, b}, bf2_t));
-}
-template <> __device__ __forceinline__ uint32_t out_pack2<f16>(float a, float b) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2_t{a, b}, h2_t));
-}
 template <class IOT> __device__ __forceinline__ uint16_t out_bits(float x);
 template <> __device__ __forceinline__ uint16_t out_bits<bf16>(float x) { return f32_to_bf16_bits(x); }
 template <> __device__ __forceinline__ uint16_t out_bits<f16>(float x) {
@@ -177,7 +177,7 @@ __device__ __forceinline__ Tri tri_mul_add(const Tri& P, const Tri& Y) {
   return Z;
 }
 
-template <int DK, class IOT, class ST>
+template <int DK, class IOT, class ST, bool FUSED>
 __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p) {
   constexpr int HT = DK / 16;    // 16-row state tiles
   constexpr int KS = DK / 32;    // 32-deep k steps over d_k
@@ -457,86 +457,9 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
   } else {
     // ==================================================================== side waves
     const int sw = wave - 2;        // 0..5
-    const int st = tid - 256;       // staging thread index (waves 4-7)
-    const bool kq_thread = st >= 0 && st < KBLK;
-    const bool v_thread = st >= 128;  // waves 6, 7: 4 tokens x 8 columns of the 64-column V slice
-    // K/Q block: 16-byte column block fastest (conflict-free 16-byte LDS writes)
-    const int ktb = st / DB, kdb = st % DB;
-    const int vtb = (st - 128) >> 3, vdb = (st - 128) & 7;
-    const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + ((bos + 4 * ktb) * p.H + kh) * DK + 8 * kdb;
-    const uint16_t* qbase = static_cast<const uint16_t*>(p.q) + ((bos + 4 * ktb) * p.H + kh) * DK + 8 * kdb;
-    const uint16_t* vbase =
-        static_cast<const uint16_t*>(p.v) + ((bos + 4 * vtb) * p.HV + h) * p.DV + col_base + 8 * vdb;
-    const int64_t krow = p.H * DK, kstride = kC * krow;
-    const int64_t vrow = p.HV * p.DV, vstride = kC * vrow;
-    const int gtid = lane;  // wave 7 carries the gates
-    uint4 pk[4], pq[4], pv[4];
-    float pgate = 0.f, pbeta = 0.f;
-
-    auto prefetch_kq = [&](int64_t ck) {
-      const int nk = valid_rows(ck);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        pk[u] = pq[u] = make_uint4(0, 0, 0, 0);
-        if (kq_thread && 4 * ktb + u < nk) {
-          pk[u] = *reinterpret_cast<const uint4*>(kbase + ck * kstride + u * krow);
-          pq[u] = *reinterpret_cast<const uint4*>(qbase + ck * kstride + u * krow);
-        }
-      }
-      if (wave == 7) {
-        const bool ok = gtid < nk;
-        const int64_t off = (bos + ck * kC + (ok ? gtid : 0)) * p.HV + h;
-        pgate = ok ? p.g[off] : 0.f;
-        pbeta = ok ? p.beta[off] : 0.f;
-      }
-    };
-    auto prefetch_v = [&](int64_t cv) {
-      const int nk = valid_rows(cv);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        pv[u] = make_uint4(0, 0, 0, 0);
-        if (v_thread && 4 * vtb + u < nk) pv[u] = *reinterpret_cast<const uint4*>(vbase + cv * vstride + u * vrow);
-      }
-    };
-    auto stage_kq = [&](int64_t ck) {
-      if (kq_thread) {
-        _Float16* kd = sK + (ck % 3) * kC * LDK + (4 * ktb) * LDK + 8 * kdb;
-        _Float16* qd = sQ + (ck & 1) * kC * LDQ + (4 * ktb) * LDQ + 8 * kdb;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          *reinterpret_cast<uint4*>(kd + u * LDK) = to_f16x8<IOT>(pk[u]);
-          *reinterpret_cast<uint4*>(qd + u * LDQ) = to_f16x8<IOT>(pq[u]);
-        }
-      }
-      if (wave == 7) {  // chunk-local cumulative gate in log2 units (cumsum.py:19-75)
-        const int nk = valid_rows(ck);
-        float x = pgate;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-          const float y = __shfl_up(x, off, 64);
-          if (gtid >= off) x += y;
-        }
-        const float G = x * kRcpLn2;
-        const float Gl = __shfl(G, nk > 0 ? nk - 1 : 0, 64);
-        float* gt = sG + (ck % 3) * GTS;
-        gt[gtid] = G;
-        gt[G_EXP + gtid] = fast_exp2(G);
-        gt[G_DEC + gtid] = gtid < nk ? fast_exp2(Gl - G) : 0.f;
-        gt[G_BETA + gtid] = pbeta;
-        if (gtid == 0) gt[G_LAST] = fast_exp2(Gl);
-      }
-    };
-    auto stage_v = [&]() {
-      if (v_thread) {
-        _Float16* vd = sV + (4 * vtb) * LDV + 8 * vdb;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) *reinterpret_cast<uint4*>(vd + u * LDV) = to_f16x8<IOT>(pv[u]);
-      }
-    };
-
     // Solve for chunk nc.  S tiles (ti, tj) of X K^T in the "row" orientation:
     // lane (g, c) holds entry (t = 16 ti + c, s = 16 tj + 4 g + e).
-    auto solve = [&](int64_t nc) {
+    auto solve = [&](int64_t nc) __attribute__((always_inline)) {
       const _Float16* K = sK + (nc % 3) * kC * LDK;
       const _Float16* Q = sQ + (nc & 1) * kC * LDQ;
       const float* gt = sG + (nc % 3) * GTS;
@@ -660,6 +583,25 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       }
     };
 
+    // Gate table of chunk ck from per-lane (token) g and beta: chunk-local
+    // cumulative gate in log2 units (cumsum.py:19-75) and its exponentials.
+    auto gate_table = [&](int64_t ck, float x, float bt) __attribute__((always_inline)) {
+      const int nk = valid_rows(ck);
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+      }
+      const float G = x * kRcpLn2;
+      const float Gl = __shfl(G, nk > 0 ? nk - 1 : 0, 64);
+      float* gt = sG + (ck % 3) * GTS;
+      gt[lane] = G;
+      gt[G_EXP + lane] = fast_exp2(G);
+      gt[G_DEC + lane] = lane < nk ? fast_exp2(Gl - G) : 0.f;
+      gt[G_BETA + lane] = bt;
+      if (lane == 0) gt[G_LAST] = fast_exp2(Gl);
+    };
+
     // Waves 2-3 (the inverses) and 4-7 (tiles, staging) run separate loops
     // with the same barrier sequence, so that the prefetch registers of the
     // staging waves are not live in the inverse code.
@@ -673,10 +615,242 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         lds_barrier();  // B(c+1)
       }
     } else {
+      const int st = tid - 256;       // staging thread index (waves 4-7)
+      const bool kq_thread = st >= 0 && st < KBLK;
+      const bool v_thread = st >= 128;  // two-step path, waves 6, 7: 4 tokens x 8 columns of the V slice
+      // K/Q block: 16-byte column block fastest (conflict-free 16-byte LDS writes)
+      const int ktb = st / DB, kdb = st % DB;
+      const int vtb = (st - 128) >> 3, vdb = (st - 128) & 7;
+      const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + ((bos + 4 * ktb) * p.H + kh) * DK + 8 * kdb;
+      const uint16_t* qbase = static_cast<const uint16_t*>(p.q) + ((bos + 4 * ktb) * p.H + kh) * DK + 8 * kdb;
+      const int64_t krow = p.H * DK, kstride = kC * krow;
+      const int gtid = lane;  // wave 7 carries the gates
+      uint4 pk[4], pq[4];
+      float pgate = 0.f, pbeta = 0.f;
+      // two-step path: V rows and prepared gates from HBM
+      uint4 pv[4];
+      const uint16_t* vbase = FUSED ? nullptr
+                                    : static_cast<const uint16_t*>(p.v) + ((bos + 4 * vtb) * p.HV + h) * p.DV +
+                                          col_base + 8 * vdb;
+      const int64_t vrow = p.HV * p.DV, vstride = kC * vrow;
+      // fused path: V rows are the conv + SiLU of the projections (packed_conv.py:49-133):
+      // a lane convolves its VT tokens with the 3 inputs before them (the tokens
+      // before, or the conv history at the sequence start); gates are prepared
+      // from the raw projections (kernel/fused.py:53-117)
+      const FrontIn& f = p.front;
+      const uint16_t* mixed = static_cast<const uint16_t*>(f.mixed);
+      const int64_t rs = f.row_stride;
+      // V conv threads: waves 4-5 (they share SIMDs with the chain waves, which
+      // leave more issue slots free than the inverse waves do), VT tokens x 8
+      // channels each
+      constexpr int VT = 4, VNR = VT + 3, VST0 = 0, VTHREADS = 8 * kC / VT;
+      const int fst = st - VST0;
+      const bool fv_thread = fst >= 0 && fst < VTHREADS;
+      const int fvtb = fst >> 3, fvdb = fst & 7;
+      const int64_t vch = 2 * f.key_dim + h * p.DV + col_base;  // first channel of the slice
+      const int64_t ch0 = vch + 8 * fvdb;
+      u4_t vraw[VNR];
+      float vw[4][8];
+      uint32_t vlo = 0;
+      const uint16_t* hist = nullptr;
+      float nA = 0.f, dtb = 0.f;
+      if constexpr (FUSED) {
+        if (fv_thread) {
+          const uint4* wp = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(f.weight) + ch0 * 4);
+          float wv[32];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float x[8];
+            unpack8<IOT>(wp[i], x);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) wv[8 * i + e] = x[e];
+          }
+#pragma unroll
+          for (int c = 0; c < 8; ++c)
+#pragma unroll
+            for (int tap = 0; tap < 4; ++tap) vw[tap][c] = wv[c * 4 + tap];
+        }
+        vlo = static_cast<uint32_t>((VT * fvtb * rs + 8 * fvdb) * 2);
+        asm volatile("" : "+v"(vlo));
+        const int64_t bslot = uniform_index(p.read_slots, n, p.read_is64);
+        if (bslot >= 0)
+          hist = static_cast<const uint16_t*>(f.conv_state) + bslot * f.conv_slot_stride +
+                 p.layer * f.conv_layer_stride;
+        if (wave == 7) {
+          nA = -expf(load_any(f.A_log, h, f.a_dtype));
+          dtb = load_any(f.dt_bias, h, f.dt_dtype);
+        }
+      }
+
+      auto prefetch_kq = [&](int64_t ck) __attribute__((always_inline)) {
+        const int nk = valid_rows(ck);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          pk[u] = pq[u] = make_uint4(0, 0, 0, 0);
+          if (kq_thread && 4 * ktb + u < nk) {
+            pk[u] = *reinterpret_cast<const uint4*>(kbase + ck * kstride + u * krow);
+            pq[u] = *reinterpret_cast<const uint4*>(qbase + ck * kstride + u * krow);
+          }
+        }
+        if (wave == 7) {
+          const bool ok = gtid < nk;
+          const int64_t t = bos + ck * kC + (ok ? gtid : 0);
+          if constexpr (FUSED) {
+            const float gv = load_any(f.gate, t * f.gate_r + h * f.gate_h, f.gate_dtype);
+            const float bv = load_any(f.beta, t * f.beta_r + h * f.beta_h, f.beta_dtype);
+            pgate = ok ? gv : 0.f;
+            pbeta = ok ? bv : 0.f;
+          } else {
+            pgate = ok ? p.g[t * p.HV + h] : 0.f;
+            pbeta = ok ? p.beta[t * p.HV + h] : 0.f;
+          }
+        }
+      };
+      auto prefetch_v = [&](int64_t cv) __attribute__((always_inline)) {
+        if constexpr (!FUSED) {
+          const int nk = valid_rows(cv);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            pv[u] = make_uint4(0, 0, 0, 0);
+            if (v_thread && 4 * vtb + u < nk)
+              pv[u] = *reinterpret_cast<const uint4*>(vbase + cv * vstride + u * vrow);
+          }
+        } else if (fv_thread) {
+          if (cv > 0 && (cv + 1) * kC <= len) {
+            // a uniform row pointer stepped per row (kept opaque so that the
+            // row addresses are not precomputed and held across the loop)
+            int64_t step = rs * 2;
+            asm volatile("" : "+s"(step));
+            const char* rp = reinterpret_cast<const char*>(mixed + (bos + cv * kC) * rs + vch) - 3 * step;
+#pragma unroll
+            for (int i = 0; i < VNR; ++i) {
+              vraw[i] = *reinterpret_cast<const u4_t*>(rp + vlo);
+              rp += step;
+            }
+          } else {
+            // first or last chunk: rows outside the sequence read a clamped
+            // (valid) row and are zeroed; the rows before it are the history
+            const int64_t t0 = cv * kC + VT * fvtb - 3;
+            const u4_t zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int i = 0; i < VNR; ++i) {
+              const int64_t t = t0 + i;
+              const int64_t tc = t < 0 ? 0 : (t >= len ? len - 1 : t);
+              const u4_t v = *reinterpret_cast<const u4_t*>(mixed + (bos + tc) * rs + ch0);
+              vraw[i] = (t >= 0 && t < len) ? v : zero;
+            }
+            if (cv == 0) {  // conv history: [channel][3] layout, 48 contiguous bytes
+              const bool hl = fvtb == 0 && hist != nullptr;
+              const uint16_t* hp = hl ? hist + ch0 * 3 : mixed + bos * rs + ch0;
+#pragma unroll
+              for (int i = 0; i < 3; ++i) {
+                const u4_t v = *reinterpret_cast<const u4_t*>(hp + (hl ? 8 * i : 0));
+                vraw[i] = hl ? v : vraw[i];
+              }
+            }
+          }
+        }
+      };
+      auto stage_kq = [&](int64_t ck) __attribute__((always_inline)) {
+        if (kq_thread) {
+          _Float16* kd = sK + (ck % 3) * kC * LDK + (4 * ktb) * LDK + 8 * kdb;
+          _Float16* qd = sQ + (ck & 1) * kC * LDQ + (4 * ktb) * LDQ + 8 * kdb;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            *reinterpret_cast<uint4*>(kd + u * LDK) = to_f16x8<IOT>(pk[u]);
+            *reinterpret_cast<uint4*>(qd + u * LDQ) = to_f16x8<IOT>(pq[u]);
+          }
+        }
+        if (wave == 7) {
+          if constexpr (FUSED) {
+            const bool ok = gtid < valid_rows(ck);
+            const float g = ok ? nA * softplus_prefill(pgate + dtb) : 0.f;
+            const float bt = ok ? sigmoid(pbeta) : 0.f;
+            gate_table(ck, g, bt);
+          } else {
+            gate_table(ck, pgate, pbeta);
+          }
+        }
+      };
+      // V conv of chunk cv into registers (fused path): the VT tokens x 8
+      // channels of a lane, computed stage by stage over all values so the
+      // exp / reciprocal latencies overlap.  Same operation order and rounding
+      // as the standalone front end: y = round(silu(round(sum_tap w x))), the
+      // outer rounding being the io-type pack.
+      uint4 vo[VT];
+      auto conv_v = [&](int64_t cv) __attribute__((always_inline)) {
+        if (!fv_thread) return;
+        const int nv = valid_rows(cv);
+        float win[3][8];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) unpack8<IOT>(to_uint4(vraw[j]), win[j]);
+        if (cv == 0 && fvtb == 0) {  // history rows hold [channel][tap]
+          float e[3][8];
+#pragma unroll
+          for (int j = 0; j < 3; ++j) unpack8<IOT>(to_uint4(vraw[j]), e[j]);
+#pragma unroll
+          for (int c = 0; c < 8; ++c)
+#pragma unroll
+            for (int j = 0; j < 3; ++j) win[j][c] = e[(3 * c + j) / 8][(3 * c + j) % 8];
+        }
+        float y[VT][8];
+#pragma unroll
+        for (int i = 0; i < VT; ++i) {
+          float x[8];
+          unpack8<IOT>(to_uint4(vraw[3 + i]), x);
+#pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            float acc = 0.f;
+            acc = fmaf(win[0][c], vw[0][c], acc);
+            acc = fmaf(win[1][c], vw[1][c], acc);
+            acc = fmaf(win[2][c], vw[2][c], acc);
+            acc = fmaf(x[c], vw[3][c], acc);
+            y[i][c] = acc;
+            win[0][c] = win[1][c];
+            win[1][c] = win[2][c];
+            win[2][c] = x[c];
+          }
+          round8<IOT>(y[i]);
+        }
+        float d[VT][8];
+#pragma unroll
+        for (int i = 0; i < VT; ++i)
+#pragma unroll
+          for (int c = 0; c < 8; ++c) d[i][c] = fast_exp2(-1.4426950408889634f * y[i][c]);
+#pragma unroll
+        for (int i = 0; i < VT; ++i)
+#pragma unroll
+          for (int c = 0; c < 8; ++c) d[i][c] = __builtin_amdgcn_rcpf(1.0f + d[i][c]);
+#pragma unroll
+        for (int i = 0; i < VT; ++i) {
+#pragma unroll
+          for (int c = 0; c < 8; ++c) y[i][c] *= d[i][c];  // fast_silu
+          const uint4 o = to_f16x8<IOT>(pack8_io<IOT>(y[i]));
+          const bool ok = VT * fvtb + i < nv;
+          vo[i] = make_uint4(ok ? o.x : 0u, ok ? o.y : 0u, ok ? o.z : 0u, ok ? o.w : 0u);
+        }
+      };
+      // V rows of the next chunk into the single V buffer (after M: the chain
+      // has read the previous one)
+      auto stage_v = [&]() __attribute__((always_inline)) {
+        if constexpr (FUSED) {
+          if (!fv_thread) return;
+          _Float16* vd = sV + (VT * fvtb) * LDV + 8 * fvdb;
+#pragma unroll
+          for (int u = 0; u < VT; ++u) *reinterpret_cast<uint4*>(vd + u * LDV) = vo[u];
+        } else {
+          if (!v_thread) return;
+          _Float16* vd = sV + (4 * vtb) * LDV + 8 * vdb;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) *reinterpret_cast<uint4*>(vd + u * LDV) = to_f16x8<IOT>(pv[u]);
+        }
+      };
+
       // ---- prologue: chunks 0 and 1 staged, chunk 0 solved
       prefetch_kq(0);
       prefetch_v(0);
       stage_kq(0);
+      if constexpr (FUSED) conv_v(0);
       stage_v();
       if (nchunks > 1) {
         prefetch_kq(1);
@@ -688,7 +862,10 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       solve(0);
       lds_barrier();  // B(0)
       for (int64_t c = 0; c < nchunks; ++c) {
-        if (c + 1 < nchunks) solve(c + 1);
+        if (c + 1 < nchunks) {
+          solve(c + 1);
+          if constexpr (FUSED) conv_v(c + 1);  // before M: overlaps the chain's first phase
+        }
         lds_barrier();  // M(c)
         if (c + 1 < nchunks) stage_v();
         if (c + 2 < nchunks) stage_kq(c + 2);
@@ -700,24 +877,33 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
   }
 }
 
-template <int DK, class IOT, class ST>
+template <int DK, class IOT, class ST, bool FUSED>
 int launch_typed(const ChunkParams& p, int64_t groups, hipStream_t stream) {
   const int64_t blocks = ((groups + 7) / 8) * 8 * p.members;
   if (blocks > 0x7fffffff) {
     set_error("gdn_chunk_gated_delta_rule: grid too large");
     return GDN_ERR_INVALID;
   }
-  hipLaunchKernelGGL((chunk_chain_kernel<DK, IOT, ST>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
-                     stream, p);
+  hipLaunchKernelGGL((chunk_chain_kernel<DK, IOT, ST, FUSED>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads),
+                     0, stream, p);
   return GDN_LAUNCH_CHECK("gdn_chunk_gated_delta_rule launch");
 }
 
-template <int DK>
+template <int DK, bool FUSED>
 int launch_dk(const ChunkParams& p, int io, int st, int64_t groups, hipStream_t s) {
-  if (io == GDN_BF16 && st == GDN_F32) return launch_typed<DK, bf16, float>(p, groups, s);
-  if (io == GDN_BF16 && st == GDN_BF16) return launch_typed<DK, bf16, bf16>(p, groups, s);
-  if (io == GDN_F16 && st == GDN_F32) return launch_typed<DK, f16, float>(p, groups, s);
-  if (io == GDN_F16 && st == GDN_F16) return launch_typed<DK, f16, f16>(p, groups, s);
+  if (io == GDN_BF16 && st == GDN_F32) return launch_typed<DK, bf16, float, FUSED>(p, groups, s);
+  if (io == GDN_BF16 && st == GDN_BF16) return launch_typed<DK, bf16, bf16, FUSED>(p, groups, s);
+  if (io == GDN_F16 && st == GDN_F32) return launch_typed<DK, f16, float, FUSED>(p, groups, s);
+  if (io == GDN_F16 && st == GDN_F16) return launch_typed<DK, f16, f16, FUSED>(p, groups, s);
+  return GDN_ERR_UNSUPPORTED;
+}
+
+template <bool FUSED>
+int launch_any(const ChunkParams& p, int64_t dk, int io_dtype, int state_dtype, int64_t groups, hipStream_t stream) {
+  if (p.DV % 64 != 0) return GDN_ERR_UNSUPPORTED;
+  if (dk == 128) return launch_dk<128, FUSED>(p, io_dtype, state_dtype, groups, stream);
+  if (dk == 64) return launch_dk<64, FUSED>(p, io_dtype, state_dtype, groups, stream);
+  if (dk == 32) return launch_dk<32, FUSED>(p, io_dtype, state_dtype, groups, stream);
   return GDN_ERR_UNSUPPORTED;
 }
 
@@ -725,11 +911,60 @@ int launch_dk(const ChunkParams& p, int io, int st, int64_t groups, hipStream_t 
 
 int launch_chunk_chain(const ChunkParams& p, int64_t dk, int io_dtype, int state_dtype, int64_t groups,
                        hipStream_t stream) {
-  if (p.DV % 64 != 0) return GDN_ERR_UNSUPPORTED;
-  if (dk == 128) return launch_dk<128>(p, io_dtype, state_dtype, groups, stream);
-  if (dk == 64) return launch_dk<64>(p, io_dtype, state_dtype, groups, stream);
-  if (dk == 32) return launch_dk<32>(p, io_dtype, state_dtype, groups, stream);
-  return GDN_ERR_UNSUPPORTED;
+  return launch_any<false>(p, dk, io_dtype, state_dtype, groups, stream);
+}
+
+int launch_chunk_chain_fused(const ChunkParams& p, int64_t dk, int io_dtype, int state_dtype, int64_t groups,
+                             hipStream_t stream) {
+  return launch_any<true>(p, dk, io_dtype, state_dtype, groups, stream);
 }
 
 }  // namespace gdn
+
+extern "C" int gdn_prefill_fused(const void* q, const void* k, const void* mixed, int64_t row_stride, int io_dtype,
+                                 const void* weight, int kernel_width, const void* cu_seqlens, int cu_dtype,
+                                 int64_t num_seqs, int64_t total_tokens, int64_t H, int64_t HV, int64_t dk,
+                                 int64_t dv, const void* conv_state, int64_t conv_slot_stride,
+                                 int64_t conv_layer_stride, const void* gate, int64_t gate_row_stride,
+                                 int64_t gate_head_stride, int gate_dtype, const void* beta, int64_t beta_row_stride,
+                                 int64_t beta_head_stride, int beta_dtype, const void* A_log, int a_dtype,
+                                 const void* dt_bias, int dt_dtype, void* state, int state_dtype,
+                                 int64_t slot_stride, int64_t layer_stride, int64_t head_stride, int64_t layer,
+                                 const void* baseline_slots, int baseline_dtype, const void* chunk_write_slots,
+                                 int chunk_write_dtype, const void* final_write_slots, int final_write_dtype,
+                                 void* out, float scale, void* stream) {
+  using namespace gdn;
+  GDN_REQUIRE(num_seqs >= 1 && total_tokens >= 0 && H > 0 && HV > 0 && HV % H == 0, "gdn_prefill_fused: bad sizes");
+  GDN_REQUIRE(q && k && mixed && weight && cu_seqlens && conv_state && baseline_slots && gate && beta && A_log &&
+                  dt_bias && state && chunk_write_slots && out,
+              "gdn_prefill_fused: null input");
+  const bool covered = kernel_width == 4 && (io_dtype == GDN_BF16 || io_dtype == GDN_F16) && dv % 64 == 0 &&
+                       (dk == 32 || dk == 64 || dk == 128) && row_stride % 8 == 0 && aligned16(mixed) &&
+                       aligned16(weight) && aligned16(conv_state) && conv_slot_stride % 8 == 0 &&
+                       conv_layer_stride % 8 == 0 && (state_dtype == GDN_F32 || state_dtype == io_dtype);
+  if (!covered) {
+    set_error("gdn_prefill_fused: not covered (needs conv width 4, 16-bit io, dk in {32, 64, 128}, dv %% 64 == 0, "
+              "16-byte aligned rows and conv pool, fp32 or io-typed state)");
+    return GDN_ERR_UNSUPPORTED;
+  }
+  ChunkParams p{};
+  p.q = q; p.k = k;
+  p.cu = cu_seqlens; p.cu_is64 = cu_dtype == GDN_I64;
+  p.N = num_seqs; p.T = total_tokens; p.H = H; p.HV = HV; p.DV = dv;
+  p.state = state; p.slot_stride = slot_stride; p.layer_stride = layer_stride; p.head_stride = head_stride;
+  p.layer = layer;
+  p.read_slots = baseline_slots; p.read_is64 = baseline_dtype == GDN_I64;
+  p.cw_slots = chunk_write_slots; p.cw_is64 = chunk_write_dtype == GDN_I64;
+  p.fw_slots = final_write_slots; p.fw_is64 = final_write_dtype == GDN_I64;
+  p.out = out; p.v_new = nullptr; p.scale = scale;
+  p.nvs = static_cast<int>(dv / 64);
+  p.members = static_cast<int>((HV / H) * p.nvs);
+  FrontIn& f = p.front;
+  f.mixed = mixed; f.row_stride = row_stride; f.weight = weight;
+  f.conv_state = conv_state; f.conv_slot_stride = conv_slot_stride; f.conv_layer_stride = conv_layer_stride;
+  f.key_dim = H * dk;
+  f.gate = gate; f.gate_r = gate_row_stride; f.gate_h = gate_head_stride; f.gate_dtype = gate_dtype;
+  f.beta = beta; f.beta_r = beta_row_stride; f.beta_h = beta_head_stride; f.beta_dtype = beta_dtype;
+  f.A_log = A_log; f.a_dtype = a_dtype; f.dt_bias = dt_bias; f.dt_dtype = dt_dtype;
+  return launch_chunk_chain_fused(p, dk, io_dtype, state_dtype, num_seqs * H, static_cast<hipStream_t>(stream));
+}

@@ -72,6 +72,56 @@ __device__ __forceinline__ float softplus_prefill(float x) {
   return x > 20.0f ? x : log1pf(expf(fminf(x, 20.0f)));
 }
 
+// SiLU with the hardware exp2 and reciprocal (the prefill conv's activation).
+__device__ __forceinline__ float fast_silu(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + fast_exp2(-1.4426950408889634f * x));
+}
+
+// 8 packed 16-bit values -> 8 floats (exact).
+template <class T> __device__ __forceinline__ void unpack8(uint4 v, float (&x)[8]);
+template <> __device__ __forceinline__ void unpack8<bf16>(uint4 v, float (&x)[8]) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = __uint_as_float(w[i] << 16);
+    x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+template <> __device__ __forceinline__ void unpack8<f16>(uint4 v, float (&x)[8]) {
+  const f16* h = reinterpret_cast<const f16*>(&v);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = static_cast<float>(h[i]);
+}
+
+// Two outputs rounded to the io type (round-to-nearest-even, one packed convert).
+typedef float f2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+template <class IOT> __device__ __forceinline__ uint32_t out_pack2(float a, float b);
+template <> __device__ __forceinline__ uint32_t out_pack2<bf16>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2_t{a, b}, bf2_t));
+}
+template <> __device__ __forceinline__ uint32_t out_pack2<f16>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2_t{a, b}, h2_t));
+}
+// Round 8 floats through the io type (round-to-nearest-even, packed converts).
+template <class IOT> __device__ __forceinline__ void round8(float (&y)[8]);
+template <> __device__ __forceinline__ void round8<bf16>(float (&y)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t u = out_pack2<bf16>(y[2 * i], y[2 * i + 1]);
+    y[2 * i] = __uint_as_float(u << 16);
+    y[2 * i + 1] = __uint_as_float(u & 0xffff0000u);
+  }
+}
+template <> __device__ __forceinline__ void round8<f16>(float (&y)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) y[i] = static_cast<float>(static_cast<_Float16>(y[i]));
+}
+template <class IOT> __device__ __forceinline__ uint4 pack8_io(const float (&y)[8]) {
+  return make_uint4(out_pack2<IOT>(y[0], y[1]), out_pack2<IOT>(y[2], y[3]), out_pack2<IOT>(y[4], y[5]),
+                    out_pack2<IOT>(y[6], y[7]));
+}
 template <int W> __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = W / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);

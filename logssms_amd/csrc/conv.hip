@@ -221,37 +221,6 @@ __global__ __launch_bounds__(kThreads) void frontend_kernel(FrontParams fp) {
 // lanes of the head with cross-lane shuffles (no LDS).
 constexpr int kVTok = 16;
 
-template <class T> __device__ __forceinline__ void unpack8(uint4 v, float (&x)[8]);
-template <> __device__ __forceinline__ void unpack8<bf16>(uint4 v, float (&x)[8]) {
-  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    x[2 * i] = __uint_as_float(w[i] << 16);
-    x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-  }
-}
-template <> __device__ __forceinline__ void unpack8<f16>(uint4 v, float (&x)[8]) {
-  const f16* h = reinterpret_cast<const f16*>(&v);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) x[i] = static_cast<float>(h[i]);
-}
-template <class T> __device__ __forceinline__ uint16_t half_bits(float x);
-template <> __device__ __forceinline__ uint16_t half_bits<bf16>(float x) { return f32_to_bf16_bits(x); }
-template <> __device__ __forceinline__ uint16_t half_bits<f16>(float x) {
-  const f16 h = static_cast<f16>(x);
-  return *reinterpret_cast<const uint16_t*>(&h);
-}
-template <class T> __device__ __forceinline__ uint4 pack8(const float (&x)[8]) {
-  uint32_t w[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    w[i] = half_bits<T>(x[2 * i]) | (static_cast<uint32_t>(half_bits<T>(x[2 * i + 1])) << 16);
-  return make_uint4(w[0], w[1], w[2], w[3]);
-}
-__device__ __forceinline__ float fast_silu(float x) {
-  return x * __builtin_amdgcn_rcpf(1.0f + fast_exp2(-1.4426950408889634f * x));
-}
-
 // FRONT: fused front end (q/k normalised into q_out/k_out, v into v_out, history
 // from the pool); otherwise the plain packed conv into conv.out.
 template <class T, int W, int DK, bool FRONT>
@@ -329,24 +298,27 @@ __global__ __launch_bounds__(256) void conv_vec_kernel(FrontParams fp) {
       }
     }
   };
-  if (active) load_window(t0);
-  for (int64_t t = t0; t < t1; ++t) {
-    while (t >= end) {  // next sequence (skips empty ones)
-      ++r;
-      begin = end;
-      end = load_index(p.cu, r + 1, p.cu_is64);
-      if (t < end && active) load_window(t);
-    }
-    float xv[8], y[8];
-    if (active) x_at(t, xv);
+  // One token: conv of the window + current input, SiLU, snapshots, window
+  // shift, outputs.
+  auto token = [&](int64_t t, const float (&xv)[8]) __attribute__((always_inline)) {
+    // y = round(silu(round(sum_tap w x + b))), each stage over all 8 channels
+    // (independent exp / reciprocal latencies overlap)
+    float y[8], d[8];
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       float acc = bias[c];
 #pragma unroll
       for (int i = 0; i < S; ++i) acc = fmaf(win[i][c], w[i][c], acc);
-      acc = fmaf(xv[c], w[S][c], acc);
-      y[c] = round_to<T>(fast_silu(round_to<T>(acc)));
+      y[c] = fmaf(xv[c], w[S][c], acc);
     }
+    round8<T>(y);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) d[c] = fast_exp2(-1.4426950408889634f * y[c]);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) d[c] = __builtin_amdgcn_rcpf(1.0f + d[c]);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) y[c] *= d[c];  // fast_silu
+    round8<T>(y);
     if (active && p.state) {  // window snapshots (raw inputs, oldest first)
       const int64_t slot = p.token_slots ? load_index(p.token_slots, t, p.token_is64) : -1;
       const int64_t fslot = (!FRONT && p.final_slots && t == end - 1) ? load_index(p.final_slots, r, p.final_is64) : -1;
@@ -382,17 +354,29 @@ __global__ __launch_bounds__(256) void conv_vec_kernel(FrontParams fp) {
           for (int c = 0; c < 8; ++c) y[c] *= rn;
           T* dst = ch0 < key_dim ? static_cast<T*>(fp.q_out) + t * key_dim + ch0
                                  : static_cast<T*>(fp.k_out) + t * key_dim + ch0 - key_dim;
-          *reinterpret_cast<uint4*>(dst) = pack8<T>(y);
+          *reinterpret_cast<uint4*>(dst) = pack8_io<T>(y);
         } else {
           *reinterpret_cast<uint4*>(static_cast<T*>(fp.v_out) + t * (fp.HV * fp.DV) + ch0 - 2 * key_dim) =
-              pack8<T>(y);
+              pack8_io<T>(y);
         }
       }
     } else if (active) {
-      *reinterpret_cast<uint4*>(static_cast<T*>(p.out) + t * p.C + ch0) = pack8<T>(y);
+      *reinterpret_cast<uint4*>(static_cast<T*>(p.out) + t * p.C + ch0) = pack8_io<T>(y);
     }
+  };
+  if (active) load_window(t0);
+  for (int64_t t = t0; t < t1; ++t) {
+    while (t >= end) {  // next sequence (skips empty ones)
+      ++r;
+      begin = end;
+      end = load_index(p.cu, r + 1, p.cu_is64);
+      if (t < end && active) load_window(t);
+    }
+    float xv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (active) x_at(t, xv);
+    token(t, xv);
   }
-  if (FRONT && blockIdx.y == 0) {
+  if (FRONT && blockIdx.y == 0 && fp.g_out) {
     const int n = static_cast<int>(t1 - t0);
     for (int idx = threadIdx.x; idx < n * fp.HV; idx += 256) {
       const int64_t t = t0 + idx / fp.HV;
@@ -514,7 +498,52 @@ int dispatch_dtype(int dtype, F&& f) {
   return GDN_ERR_UNSUPPORTED;
 }
 
+struct SnapshotParams {
+  const void* mixed;
+  int64_t row_stride;
+  const void* cu;
+  int cu_is64;
+  int64_t N, T, C;
+  int S;  // kernel width - 1
+  void* conv_state;
+  int64_t slot_stride, layer_stride, layer;
+  const void* baseline;
+  int baseline_is64;
+  const void* rows;
+  int rows_is64;
+  const void* slots;
+  int slots_is64;
+};
+
+// Grid (snapshot, 256-channel block), one channel per thread (16-bit values
+// copied as bits, so the window is the raw input exactly).
+__global__ __launch_bounds__(kThreads) void conv_snapshot_kernel(SnapshotParams sp) {
+  const int64_t i = blockIdx.x;
+  const int64_t ch = static_cast<int64_t>(blockIdx.y) * kThreads + threadIdx.x;
+  if (ch >= sp.C) return;
+  const int64_t slot = load_index(sp.slots, i, sp.slots_is64);
+  if (slot < 0) return;
+  const int64_t row = load_index(sp.rows, i, sp.rows_is64);
+  if (row < 0 || row >= sp.T) return;
+  const int64_t r = find_sequence(sp.cu, sp.cu_is64, sp.N, row);
+  const int64_t begin = load_index(sp.cu, r, sp.cu_is64);
+  const int64_t base = load_index(sp.baseline, r, sp.baseline_is64);
+  const uint16_t* x = static_cast<const uint16_t*>(sp.mixed);
+  uint16_t* pool = static_cast<uint16_t*>(sp.conv_state);
+  const uint16_t* hist = base >= 0 ? pool + base * sp.slot_stride + sp.layer * sp.layer_stride : nullptr;
+  uint16_t* dst = pool + slot * sp.slot_stride + sp.layer * sp.layer_stride;
+  const int S = sp.S;
+  for (int j = 0; j < S; ++j) {
+    const int64_t pos = row - (S - 1) + j;
+    uint16_t v;
+    if (pos >= begin) v = x[pos * sp.row_stride + ch];
+    else v = hist ? hist[ch * S + (pos - begin + S)] : 0;
+    dst[ch * S + j] = v;
+  }
+}
+
 }  // namespace
+
 }  // namespace gdn
 
 using namespace gdn;
@@ -642,4 +671,68 @@ extern "C" int gdn_prepare(const void* query, const int64_t* qs, const void* key
                        static_cast<hipStream_t>(stream), p);
     return GDN_LAUNCH_CHECK("gdn_prepare launch");
   });
+}
+
+extern "C" int gdn_prefill_qk(const void* mixed, int64_t row_stride, int io_dtype, const void* weight, int kernel_width,
+                              const void* cu_seqlens, int cu_dtype, int64_t num_seqs, int64_t total_tokens, int64_t H,
+                              int64_t dk, const void* conv_state, int64_t conv_slot_stride, int64_t conv_layer_stride,
+                              int64_t layer, const void* baseline_slots, int baseline_dtype, void* q_out, void* k_out,
+                              void* stream) {
+  using namespace gdn;
+  GDN_REQUIRE(num_seqs >= 1 && total_tokens >= 0 && H > 0, "gdn_prefill_qk: bad sizes");
+  GDN_REQUIRE(mixed && weight && cu_seqlens && conv_state && baseline_slots && q_out && k_out,
+              "gdn_prefill_qk: null input");
+  auto al = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+  const bool covered = kernel_width == 4 && (io_dtype == GDN_BF16 || io_dtype == GDN_F16) &&
+                       (dk == 32 || dk == 64 || dk == 128) && row_stride % 8 == 0 && al(mixed) && al(weight) &&
+                       al(q_out) && al(k_out);
+  if (!covered) {
+    set_error("gdn_prefill_qk: not covered (needs conv width 4, 16-bit io, dk in {32, 64, 128}, 16-byte aligned "
+              "rows)");
+    return GDN_ERR_UNSUPPORTED;
+  }
+  if (total_tokens == 0) return GDN_OK;
+  ConvParams p{};
+  p.x = mixed; p.xr = row_stride; p.xc = 1; p.w = weight; p.bias = nullptr; p.history = nullptr;
+  p.cu = cu_seqlens; p.cu_is64 = cu_dtype == GDN_I64; p.N = num_seqs; p.T = total_tokens; p.C = 2 * H * dk; p.W = 4;
+  p.out = nullptr; p.state = const_cast<void*>(conv_state); p.slot_stride = conv_slot_stride;
+  p.layer_stride = conv_layer_stride; p.layer = layer; p.token_slots = nullptr; p.final_slots = nullptr;
+  p.baseline = baseline_slots; p.baseline_is64 = baseline_dtype == GDN_I64;
+  p.end0 = p.C; p.end1 = p.C; p.s0 = p.s1 = p.s2 = 1.f;
+  FrontParams fp{};
+  fp.conv = p; fp.H = H; fp.HV = H; fp.DK = dk; fp.DV = dk;
+  fp.q_out = q_out; fp.k_out = k_out;  // no v_out, no gates: channels [0, 2 H dk) only
+  auto s = static_cast<hipStream_t>(stream);
+  const int rc = io_dtype == GDN_BF16 ? launch_vec<bf16, true>(fp, static_cast<int>(dk), s)
+                                      : launch_vec<f16, true>(fp, static_cast<int>(dk), s);
+  if (rc != 0) {
+    set_error("gdn_prefill_qk: layout not covered");
+    return GDN_ERR_UNSUPPORTED;
+  }
+  return GDN_LAUNCH_CHECK("gdn_prefill_qk launch");
+}
+
+extern "C" int gdn_conv_snapshots(const void* mixed, int64_t row_stride, int dtype, const void* cu_seqlens,
+                                  int cu_dtype, int64_t num_seqs, int64_t total_tokens, int64_t channels,
+                                  int kernel_width, void* conv_state, int64_t state_slot_stride,
+                                  int64_t state_layer_stride, int64_t layer, const void* baseline_slots,
+                                  int baseline_dtype, const void* rows, int rows_dtype, const void* slots,
+                                  int slots_dtype, int64_t count, void* stream) {
+  using namespace gdn;
+  GDN_REQUIRE(num_seqs >= 1 && total_tokens >= 0 && channels > 0 && count >= 0 && count <= 0x7fffffff &&
+                  kernel_width >= 2 && kernel_width <= 8,
+              "gdn_conv_snapshots: bad sizes");
+  GDN_REQUIRE(dtype == GDN_BF16 || dtype == GDN_F16, "gdn_conv_snapshots: 16-bit dtype expected");
+  if (count == 0) return GDN_OK;
+  GDN_REQUIRE(mixed && cu_seqlens && conv_state && baseline_slots && rows && slots, "gdn_conv_snapshots: null input");
+  SnapshotParams sp{};
+  sp.mixed = mixed; sp.row_stride = row_stride; sp.cu = cu_seqlens; sp.cu_is64 = cu_dtype == GDN_I64;
+  sp.N = num_seqs; sp.T = total_tokens; sp.C = channels; sp.S = kernel_width - 1;
+  sp.conv_state = conv_state; sp.slot_stride = state_slot_stride; sp.layer_stride = state_layer_stride;
+  sp.layer = layer; sp.baseline = baseline_slots; sp.baseline_is64 = baseline_dtype == GDN_I64;
+  sp.rows = rows; sp.rows_is64 = rows_dtype == GDN_I64; sp.slots = slots; sp.slots_is64 = slots_dtype == GDN_I64;
+  hipLaunchKernelGGL(conv_snapshot_kernel,
+                     dim3(static_cast<unsigned>(count), static_cast<unsigned>((channels + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, static_cast<hipStream_t>(stream), sp);
+  return GDN_LAUNCH_CHECK("gdn_conv_snapshots launch");
 }

@@ -3,8 +3,12 @@
 ``python/logssms/layers/linear_attention_backend/gdn.py:74-265``) each as the
 smallest number of gfx950 kernels.
 
+* ``prefill_fused`` -- the whole prefill (``gdn.py:100-150``): a q/k pass,
+  the chunk kernel computing the v conv + SiLU and the gates in its staging
+  waves, and a small conv-snapshot launch.
 * ``prefill_frontend`` -- conv-history gather + packed conv + snapshots + split
-  + ``prepare_gdn`` in one pass over ``mixed_qkv`` (``gdn.py:100-132``).
+  + ``prepare_gdn`` in one pass over ``mixed_qkv`` (``gdn.py:100-132``), for
+  shapes outside the fused kernel.
 * ``decode_step`` -- ``conv_decode`` + slotted recurrent update in one kernel
   (``gdn.py:222-265``).
 * ``verify_group`` -- one verify length group: conv over the drafts, conv
@@ -64,6 +68,87 @@ def prefill_frontend(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config,
         q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), b.data_ptr(), _lib.stream_of(mixed_qkv),
     )
     return q, k, v, g, b
+
+
+def prefill_fused(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, conv_state, recurrent_state,
+                  cu_seqlens, baseline_slots, chunk_write_slots, snapshot_rows, snapshot_slots, out=None,
+                  chunk_events=None):
+    """``gdn.py:100-150`` in three launches: the q/k pass writes normalised
+    q and k (their conv is shared by all the v heads and d_v slices of a key
+    head), the chunk kernel's staging waves compute the v conv + SiLU and
+    the gates of each 64-token chunk from ``mixed_qkv`` (no v/g/beta round
+    trip through HBM), and the conv windows of ``snapshot_rows`` go to
+    ``conv_state[snapshot_slots]`` last.  Conv history and initial state come
+    from ``baseline_slots``; chunk-end states go to ``chunk_write_slots``.
+    Results equal ``prefill_frontend`` + ``chunk_gated_delta_rule_to_cache``
+    bit for bit.  Returns o [T, HV, dv], or None (nothing launched) when the
+    shapes are outside the fused kernel -- conv width 4, d_k in {32, 64, 128},
+    d_v % 64 == 0, 16-byte aligned rows, fp32 or io-typed state -- and the
+    two-step path has to be used.  ``chunk_events``: optional (start, end)
+    ``torch.cuda.Event`` pair recorded around the chunk-kernel launch."""
+    T, C = mixed_qkv.shape
+    assert C == config.conv_dim == 2 * config.key_dim + config.value_dim
+    assert gate.shape == beta.shape == (T, config.num_v_heads)
+    _check_pools(conv_state, recurrent_state, config)
+    assert snapshot_rows.shape == snapshot_slots.shape and snapshot_rows.ndim == 1
+    if (mixed_qkv.stride(1) != 1 or config.state_len != 3 or config.head_v_dim % 64
+            or config.head_k_dim not in (32, 64, 128) or mixed_qkv.dtype not in (torch.bfloat16, torch.float16)
+            or recurrent_state.dtype not in (torch.float32, mixed_qkv.dtype)):
+        return None
+    if out is None:
+        out = torch.empty(T, config.num_v_heads, config.head_v_dim, device=mixed_qkv.device, dtype=mixed_qkv.dtype)
+    assert out.shape == (T, config.num_v_heads, config.head_v_dim) and out.is_contiguous()
+    weight = conv_weight.contiguous()
+    A_log = A_log.contiguous()
+    dt_bias = dt_bias.contiguous()
+    q = torch.empty(T, config.num_k_heads, config.head_k_dim, device=mixed_qkv.device, dtype=mixed_qkv.dtype)
+    k = torch.empty_like(q)
+    stream = _lib.stream_of(mixed_qkv)
+    N = len(cu_seqlens) - 1
+    try:
+        _lib.call("gdn_prefill_qk", mixed_qkv.data_ptr(), mixed_qkv.stride(0), _lib.dtype_code(mixed_qkv.dtype),
+                  weight.data_ptr(), 4, cu_seqlens.data_ptr(), _lib.index_code(cu_seqlens), N, T,
+                  config.num_k_heads, config.head_k_dim, conv_state.data_ptr(), conv_state.stride(0),
+                  conv_state.stride(1), config.layer_idx, baseline_slots.data_ptr(), _lib.index_code(baseline_slots),
+                  q.data_ptr(), k.data_ptr(), stream)
+    except NotImplementedError:
+        return None
+    if chunk_events is not None:
+        chunk_events[0].record()
+    prefill_chunk_fused(q, k, mixed_qkv, gate, beta, weight, A_log, dt_bias, config, conv_state, recurrent_state,
+                        cu_seqlens, baseline_slots, chunk_write_slots, out)
+    if chunk_events is not None:
+        chunk_events[1].record()
+    if snapshot_rows.numel():
+        _lib.call("gdn_conv_snapshots", mixed_qkv.data_ptr(), mixed_qkv.stride(0), _lib.dtype_code(mixed_qkv.dtype),
+                  cu_seqlens.data_ptr(), _lib.index_code(cu_seqlens), N, T, C, 4, conv_state.data_ptr(),
+                  conv_state.stride(0), conv_state.stride(1), config.layer_idx, baseline_slots.data_ptr(),
+                  _lib.index_code(baseline_slots), snapshot_rows.data_ptr(), _lib.index_code(snapshot_rows),
+                  snapshot_slots.data_ptr(), _lib.index_code(snapshot_slots), snapshot_rows.numel(), stream)
+    return out
+
+
+def prefill_chunk_fused(q, k, mixed_qkv, gate, beta, weight, A_log, dt_bias, config, conv_state, recurrent_state,
+                        cu_seqlens, baseline_slots, chunk_write_slots, out):
+    """The chunk-kernel launch of ``prefill_fused`` (q, k from the q/k pass;
+    v and the gates computed from ``mixed_qkv`` inside)."""
+    T = mixed_qkv.shape[0]
+    _lib.call(
+        "gdn_prefill_fused",
+        q.data_ptr(), k.data_ptr(), mixed_qkv.data_ptr(), mixed_qkv.stride(0), _lib.dtype_code(mixed_qkv.dtype),
+        weight.data_ptr(), 4, cu_seqlens.data_ptr(), _lib.index_code(cu_seqlens), len(cu_seqlens) - 1, T,
+        config.num_k_heads, config.num_v_heads, config.head_k_dim, config.head_v_dim,
+        conv_state.data_ptr(), conv_state.stride(0), conv_state.stride(1),
+        gate.data_ptr(), gate.stride(0), gate.stride(1), _lib.dtype_code(gate.dtype),
+        beta.data_ptr(), beta.stride(0), beta.stride(1), _lib.dtype_code(beta.dtype),
+        A_log.data_ptr(), _lib.dtype_code(A_log.dtype), dt_bias.data_ptr(), _lib.dtype_code(dt_bias.dtype),
+        recurrent_state.data_ptr(), _lib.dtype_code(recurrent_state.dtype), recurrent_state.stride(0),
+        recurrent_state.stride(1), recurrent_state.stride(2), config.layer_idx,
+        baseline_slots.data_ptr(), _lib.index_code(baseline_slots),
+        chunk_write_slots.data_ptr(), _lib.index_code(chunk_write_slots), None, 0,
+        out.data_ptr(), float(config.head_k_dim) ** -0.5, _lib.stream_of(mixed_qkv),
+    )
+    return out
 
 
 def _fused(mixed, row_index, gate, beta, conv_weight, A_log, dt_bias, config, conv_state, recurrent_state,
@@ -128,4 +213,4 @@ def verify_group(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, con
     return output
 
 
-__all__ = ["decode_step", "prefill_frontend", "verify_group"]
+__all__ = ["decode_step", "prefill_chunk_fused", "prefill_frontend", "prefill_fused", "verify_group"]

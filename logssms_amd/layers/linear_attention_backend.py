@@ -27,7 +27,7 @@ import numpy as np
 import torch
 
 from ..core import MarconiCacheMetadata, get_global_ctx
-from ..kernel.linear_attention.fused_backend import decode_step, prefill_frontend, verify_group
+from ..kernel.linear_attention.fused_backend import decode_step, prefill_frontend, prefill_fused, verify_group
 from ..kernel.linear_attention.gdn import chunk_gated_delta_rule_to_cache
 from ..kernel.linear_attention.state_io import ChunkStateIO
 
@@ -256,6 +256,11 @@ class GatedDeltaBackend:
     def _forward_prefill(self, mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, metadata, out=None):
         pool = self.ctx.linear_state
         idx = metadata.prefill_indices
+        o = prefill_fused(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, pool.conv_state,
+                          pool.recurrent_state, idx.cu_seqlens, metadata.baseline_slots, metadata.chunk_write_slots,
+                          metadata.snapshot_rows, metadata.checkpoint_slots, out=out)
+        if o is not None:
+            return o
         q, k, v, g, b = prefill_frontend(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, pool.conv_state,
                                          idx.cu_seqlens, metadata.baseline_slots, metadata.conv_token_slots)
         io = ChunkStateIO(storage=pool.recurrent_state, read_slots=metadata.baseline_slots,

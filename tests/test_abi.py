@@ -42,7 +42,7 @@ def test_header_declares_expected_entry_points():
     assert {"gdn_last_error", "gdn_abi_version", "gdn_chunk_gated_delta_rule", "gdn_fused_recurrent",
             "gdn_fused_conv_recurrent", "gdn_packed_causal_conv1d", "gdn_prepare", "gdn_prefill_frontend",
             "gdn_conv_decode", "gdn_store_state", "gdn_copy_rows", "gdn_zero_rows",
-            "gdn_commit_accepted"} <= names
+            "gdn_commit_accepted", "gdn_prefill_qk", "gdn_prefill_fused", "gdn_conv_snapshots"} <= names
 
 
 def test_ctypes_table_matches_header():
@@ -64,7 +64,7 @@ def test_library_loads_and_exports_every_symbol():
     lib = _lib.lib()
     for name in _declarations():
         assert hasattr(lib, name), name
-    assert lib.gdn_abi_version() == 1
+    assert lib.gdn_abi_version() == 2
     assert lib.gdn_last_error() in (b"",) or isinstance(lib.gdn_last_error(), bytes)
 
 
@@ -84,3 +84,29 @@ def test_invalid_arguments_report_errors_without_a_gpu():
     assert b"steps" in lib.gdn_last_error()
     # empty work is a no-op success
     assert lib.gdn_copy_rows(None, 0, None, 1, None, 0, None, 1, 0, 1, 16, 0, None) == 0
+
+
+def test_fused_prefill_reports_uncovered_shapes_without_launching():
+    """gdn_prefill_qk / gdn_prefill_fused check their coverage on the host and
+    return GDN_ERR_UNSUPPORTED (the caller then takes the two-step path)
+    before any HIP call; the dummy device pointers are never dereferenced."""
+    from logssms_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("library not built")
+    lib = _lib.lib()
+    d = 0x10000  # 16-byte aligned dummy address
+
+    def qk(width, dk, row_stride=8192):
+        return lib.gdn_prefill_qk(d, row_stride, 1, d, width, d, 1, 1, 64, 16, dk, d, 0, 0, 0, d, 1, d, d, None)
+
+    def fused(width, dk, dv, row_stride=8192):
+        return lib.gdn_prefill_fused(d, d, d, row_stride, 1, d, width, d, 1, 1, 64, 16, 32, dk, dv, d, 0, 0, d, 32, 1,
+                                     1, d, 32, 1, 1, d, 0, d, 0, d, 0, 0, 0, 0, 0, d, 1, d, 1, None, 1, d, 0.1, None)
+    assert qk(3, 128) == 2
+    assert b"not covered" in lib.gdn_last_error()
+    assert qk(4, 256) == 2
+    assert qk(4, 128, row_stride=8190) == 2
+    assert fused(3, 128, 128) == 2
+    assert b"not covered" in lib.gdn_last_error()
+    assert fused(4, 128, 96) == 2
+    assert lib.gdn_conv_snapshots(d, 8192, 0, d, 1, 1, 64, 8192, 4, d, 0, 0, 0, d, 1, d, 1, d, 1, 4, None) == 1
