@@ -602,85 +602,236 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       if (lane == 0) gt[G_LAST] = fast_exp2(Gl);
     };
 
-    // Waves 2-3 (the inverses) and 4-7 (tiles, staging) run separate loops
-    // with the same barrier sequence, so that the prefetch registers of the
-    // staging waves are not live in the inverse code.
+    // ---- gates (wave 2, after the M barrier), one token per lane.  The raw
+    // values stay bits until staged, so the prefetch never waits for its loads.
+    const FrontIn& f = p.front;
+    uint32_t graw = 0, braw = 0;
+    float nA = 0.f, dtb = 0.f;
+    if constexpr (FUSED) {
+      if (wave == 2) {
+        nA = -expf(load_any(f.A_log, h, f.a_dtype));
+        dtb = load_any(f.dt_bias, h, f.dt_dtype);
+      }
+    }
+    auto raw_bits = [](const void* ptr, int64_t i, int dtype) __attribute__((always_inline)) -> uint32_t {
+      if (dtype == GDN_BF16 || dtype == GDN_F16) return static_cast<const uint16_t*>(ptr)[i];
+      return static_cast<const uint32_t*>(ptr)[i];
+    };
+    auto bits_f32 = [](uint32_t b, int dtype) __attribute__((always_inline)) -> float {
+      if (dtype == GDN_BF16) return __uint_as_float(b << 16);
+      if (dtype == GDN_F16) return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b)));
+      return __uint_as_float(b);
+    };
+    auto prefetch_g = [&](int64_t ck) __attribute__((always_inline)) {
+      const bool ok = lane < valid_rows(ck);
+      const int64_t t = bos + (ok ? ck * kC + lane : 0);  // a valid row for every chunk index
+      if constexpr (FUSED) {
+        graw = raw_bits(f.gate, t * f.gate_r + h * f.gate_h, f.gate_dtype);
+        braw = raw_bits(f.beta, t * f.beta_r + h * f.beta_h, f.beta_dtype);
+      } else {
+        graw = __float_as_uint(p.g[t * p.HV + h]);
+        braw = __float_as_uint(p.beta[t * p.HV + h]);
+      }
+    };
+    auto stage_g = [&](int64_t ck) __attribute__((always_inline)) {
+      const bool ok = lane < valid_rows(ck);
+      float g, bt;
+      if constexpr (FUSED) {  // kernel/fused.py:105-117
+        g = nA * softplus_prefill(bits_f32(graw, f.gate_dtype) + dtb);
+        bt = sigmoid(bits_f32(braw, f.beta_dtype));
+      } else {
+        g = __uint_as_float(graw);
+        bt = __uint_as_float(braw);
+      }
+      gate_table(ck, ok ? g : 0.f, ok ? bt : 0.f);
+    };
+
+    // ---- fused path: V rows are the conv + SiLU of the projections
+    // (packed_conv.py:49-133), computed by waves 2-3 after the M barrier (their
+    // SIMDs are idle then).  A lane convolves VT tokens x 8 channels with the 3
+    // inputs before them (the tokens before, or the conv history at the
+    // sequence start).
+    constexpr int VT = 4, VNR = VT + 3;
+    const int fst = tid - 128;
+    const bool fv_thread = FUSED && fst >= 0 && fst < 128;
+    const int fvtb = fst >> 3, fvdb = fst & 7;
+    const uint16_t* mixed = static_cast<const uint16_t*>(f.mixed);
+    const int64_t rs = f.row_stride;
+    const int64_t vch = 2 * f.key_dim + h * p.DV + col_base;  // first channel of the slice
+    const int64_t ch0 = vch + 8 * fvdb;
+    u4_t vraw[VNR];
+    float vw[4][8];
+    uint32_t vlo = 0;
+    const uint16_t* hist = nullptr;
+    if constexpr (FUSED) {
+      if (fv_thread) {
+        const uint4* wp = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(f.weight) + ch0 * 4);
+        float wv[32];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float x[8];
+          unpack8<IOT>(wp[i], x);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) wv[8 * i + e] = x[e];
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+#pragma unroll
+          for (int tap = 0; tap < 4; ++tap) vw[tap][c] = wv[c * 4 + tap];
+      }
+      vlo = static_cast<uint32_t>((VT * fvtb * rs + 8 * fvdb) * 2);
+      asm volatile("" : "+v"(vlo));
+      const int64_t bslot = uniform_index(p.read_slots, n, p.read_is64);
+      if (bslot >= 0)
+        hist = static_cast<const uint16_t*>(f.conv_state) + bslot * f.conv_slot_stride + p.layer * f.conv_layer_stride;
+    }
+    auto prefetch_fv = [&](int64_t cv) __attribute__((always_inline)) {
+      if (!fv_thread) return;
+      if (cv > 0 && (cv + 1) * kC <= len) {
+        // a uniform row pointer stepped per row (kept opaque so that the row
+        // addresses are not precomputed and held across the loop)
+        int64_t step = rs * 2;
+        asm volatile("" : "+s"(step));
+        const char* rp = reinterpret_cast<const char*>(mixed + (bos + cv * kC) * rs + vch) - 3 * step;
+#pragma unroll
+        for (int i = 0; i < VNR; ++i) {
+          vraw[i] = *reinterpret_cast<const u4_t*>(rp + vlo);
+          rp += step;
+        }
+      } else {
+        // first, last or past-the-end chunk: rows outside the sequence read a
+        // clamped (valid) row and are zeroed; the rows before it are the history
+        const int64_t t0 = cv * kC + VT * fvtb - 3;
+        const u4_t zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int i = 0; i < VNR; ++i) {
+          const int64_t t = t0 + i;
+          const int64_t tc = t < 0 ? 0 : (t >= len ? len - 1 : t);
+          const u4_t v = *reinterpret_cast<const u4_t*>(mixed + (bos + tc) * rs + ch0);
+          vraw[i] = (t >= 0 && t < len) ? v : zero;
+        }
+        if (cv == 0) {  // conv history: [channel][3] layout, 48 contiguous bytes
+          const bool hl = fvtb == 0 && hist != nullptr;
+          const uint16_t* hp = hl ? hist + ch0 * 3 : mixed + bos * rs + ch0;
+#pragma unroll
+          for (int i = 0; i < 3; ++i) {
+            const u4_t v = *reinterpret_cast<const u4_t*>(hp + (hl ? 8 * i : 0));
+            vraw[i] = hl ? v : vraw[i];
+          }
+        }
+      }
+    };
+    // conv of chunk cv, stage by stage over all VT x 8 values so the exp /
+    // reciprocal latencies overlap, then the rows into the single V buffer
+    // (after M: the chain has read the previous chunk's).  Same operation
+    // order and rounding as the standalone front end:
+    // y = round(silu(round(sum_tap w x))), the outer rounding being the io pack.
+    auto conv_stage_v = [&](int64_t cv) __attribute__((always_inline)) {
+      if (!fv_thread) return;
+      const int nv = valid_rows(cv);
+      float win[3][8];
+#pragma unroll
+      for (int j = 0; j < 3; ++j) unpack8<IOT>(to_uint4(vraw[j]), win[j]);
+      if (cv == 0 && fvtb == 0) {  // history rows hold [channel][tap]
+        float e[3][8];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) unpack8<IOT>(to_uint4(vraw[j]), e[j]);
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+#pragma unroll
+          for (int j = 0; j < 3; ++j) win[j][c] = e[(3 * c + j) / 8][(3 * c + j) % 8];
+      }
+      float y[VT][8];
+#pragma unroll
+      for (int i = 0; i < VT; ++i) {
+        float x[8];
+        unpack8<IOT>(to_uint4(vraw[3 + i]), x);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          float acc = 0.f;
+          acc = fmaf(win[0][c], vw[0][c], acc);
+          acc = fmaf(win[1][c], vw[1][c], acc);
+          acc = fmaf(win[2][c], vw[2][c], acc);
+          acc = fmaf(x[c], vw[3][c], acc);
+          y[i][c] = acc;
+          win[0][c] = win[1][c];
+          win[1][c] = win[2][c];
+          win[2][c] = x[c];
+        }
+        round8<IOT>(y[i]);
+      }
+      float d[VT][8];
+#pragma unroll
+      for (int i = 0; i < VT; ++i)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) d[i][c] = fast_exp2(-1.4426950408889634f * y[i][c]);
+#pragma unroll
+      for (int i = 0; i < VT; ++i)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) d[i][c] = __builtin_amdgcn_rcpf(1.0f + d[i][c]);
+      _Float16* vd = sV + (VT * fvtb) * LDV + 8 * fvdb;
+#pragma unroll
+      for (int i = 0; i < VT; ++i) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) y[i][c] *= d[i][c];  // fast_silu
+        const uint4 o = to_f16x8<IOT>(pack8_io<IOT>(y[i]));
+        const bool ok = VT * fvtb + i < nv;
+        *reinterpret_cast<uint4*>(vd + i * LDV) =
+            make_uint4(ok ? o.x : 0u, ok ? o.y : 0u, ok ? o.z : 0u, ok ? o.w : 0u);
+      }
+    };
+
+    // Waves 2-3 (inverses; fused v conv and gates after M) and 4-7 (tiles,
+    // K/Q staging) run separate loops with the same barrier sequence.  Staging
+    // and prefetches run unconditionally, also for chunks past the end (their
+    // loads are masked off or clamped and their LDS targets are free): a
+    // skipped consumer would leave the prefetch registers "maybe pending" at
+    // the loop head, and the next prefetch would then wait for every load in
+    // flight.
     if (sw < 2) {
+      if (wave == 2) {
+        prefetch_g(0);
+        stage_g(0);
+        prefetch_g(1);
+        stage_g(1);
+        prefetch_g(2);
+      }
+      if constexpr (FUSED) {
+        prefetch_fv(0);
+        conv_stage_v(0);
+        prefetch_fv(1);
+      }
       lds_barrier();  // P0
       solve(0);
       lds_barrier();  // B(0)
       for (int64_t c = 0; c < nchunks; ++c) {
         if (c + 1 < nchunks) solve(c + 1);
         lds_barrier();  // M(c)
+        if constexpr (FUSED) {
+          conv_stage_v(c + 1);
+          prefetch_fv(c + 2);
+        }
+        if (wave == 2) {
+          stage_g(c + 2);
+          prefetch_g(c + 3);
+        }
         lds_barrier();  // B(c+1)
       }
     } else {
       const int st = tid - 256;       // staging thread index (waves 4-7)
       const bool kq_thread = st >= 0 && st < KBLK;
-      const bool v_thread = st >= 128;  // two-step path, waves 6, 7: 4 tokens x 8 columns of the V slice
+      const bool v_thread = !FUSED && st >= 128;  // two-step path, waves 6, 7: 4 tokens x 8 columns of V
       // K/Q block: 16-byte column block fastest (conflict-free 16-byte LDS writes)
       const int ktb = st / DB, kdb = st % DB;
       const int vtb = (st - 128) >> 3, vdb = (st - 128) & 7;
       const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + ((bos + 4 * ktb) * p.H + kh) * DK + 8 * kdb;
       const uint16_t* qbase = static_cast<const uint16_t*>(p.q) + ((bos + 4 * ktb) * p.H + kh) * DK + 8 * kdb;
       const int64_t krow = p.H * DK, kstride = kC * krow;
-      const int gtid = lane;  // wave 7 carries the gates
-      uint4 pk[4], pq[4];
-      float pgate = 0.f, pbeta = 0.f;
-      // two-step path: V rows and prepared gates from HBM
-      uint4 pv[4];
+      uint4 pk[4], pq[4], pv[4];
       const uint16_t* vbase = FUSED ? nullptr
                                     : static_cast<const uint16_t*>(p.v) + ((bos + 4 * vtb) * p.HV + h) * p.DV +
                                           col_base + 8 * vdb;
       const int64_t vrow = p.HV * p.DV, vstride = kC * vrow;
-      // fused path: V rows are the conv + SiLU of the projections (packed_conv.py:49-133):
-      // a lane convolves its VT tokens with the 3 inputs before them (the tokens
-      // before, or the conv history at the sequence start); gates are prepared
-      // from the raw projections (kernel/fused.py:53-117)
-      const FrontIn& f = p.front;
-      const uint16_t* mixed = static_cast<const uint16_t*>(f.mixed);
-      const int64_t rs = f.row_stride;
-      // V conv threads: waves 4-5 (they share SIMDs with the chain waves, which
-      // leave more issue slots free than the inverse waves do), VT tokens x 8
-      // channels each
-      constexpr int VT = 4, VNR = VT + 3, VST0 = 0, VTHREADS = 8 * kC / VT;
-      const int fst = st - VST0;
-      const bool fv_thread = fst >= 0 && fst < VTHREADS;
-      const int fvtb = fst >> 3, fvdb = fst & 7;
-      const int64_t vch = 2 * f.key_dim + h * p.DV + col_base;  // first channel of the slice
-      const int64_t ch0 = vch + 8 * fvdb;
-      u4_t vraw[VNR];
-      float vw[4][8];
-      uint32_t vlo = 0;
-      const uint16_t* hist = nullptr;
-      float nA = 0.f, dtb = 0.f;
-      if constexpr (FUSED) {
-        if (fv_thread) {
-          const uint4* wp = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(f.weight) + ch0 * 4);
-          float wv[32];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float x[8];
-            unpack8<IOT>(wp[i], x);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) wv[8 * i + e] = x[e];
-          }
-#pragma unroll
-          for (int c = 0; c < 8; ++c)
-#pragma unroll
-            for (int tap = 0; tap < 4; ++tap) vw[tap][c] = wv[c * 4 + tap];
-        }
-        vlo = static_cast<uint32_t>((VT * fvtb * rs + 8 * fvdb) * 2);
-        asm volatile("" : "+v"(vlo));
-        const int64_t bslot = uniform_index(p.read_slots, n, p.read_is64);
-        if (bslot >= 0)
-          hist = static_cast<const uint16_t*>(f.conv_state) + bslot * f.conv_slot_stride +
-                 p.layer * f.conv_layer_stride;
-        if (wave == 7) {
-          nA = -expf(load_any(f.A_log, h, f.a_dtype));
-          dtb = load_any(f.dt_bias, h, f.dt_dtype);
-        }
-      }
 
       auto prefetch_kq = [&](int64_t ck) __attribute__((always_inline)) {
         const int nk = valid_rows(ck);
@@ -692,63 +843,13 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
             pq[u] = *reinterpret_cast<const uint4*>(qbase + ck * kstride + u * krow);
           }
         }
-        if (wave == 7) {
-          const bool ok = gtid < nk;
-          const int64_t t = bos + ck * kC + (ok ? gtid : 0);
-          if constexpr (FUSED) {
-            const float gv = load_any(f.gate, t * f.gate_r + h * f.gate_h, f.gate_dtype);
-            const float bv = load_any(f.beta, t * f.beta_r + h * f.beta_h, f.beta_dtype);
-            pgate = ok ? gv : 0.f;
-            pbeta = ok ? bv : 0.f;
-          } else {
-            pgate = ok ? p.g[t * p.HV + h] : 0.f;
-            pbeta = ok ? p.beta[t * p.HV + h] : 0.f;
-          }
-        }
       };
       auto prefetch_v = [&](int64_t cv) __attribute__((always_inline)) {
-        if constexpr (!FUSED) {
-          const int nk = valid_rows(cv);
+        const int nk = valid_rows(cv);
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            pv[u] = make_uint4(0, 0, 0, 0);
-            if (v_thread && 4 * vtb + u < nk)
-              pv[u] = *reinterpret_cast<const uint4*>(vbase + cv * vstride + u * vrow);
-          }
-        } else if (fv_thread) {
-          if (cv > 0 && (cv + 1) * kC <= len) {
-            // a uniform row pointer stepped per row (kept opaque so that the
-            // row addresses are not precomputed and held across the loop)
-            int64_t step = rs * 2;
-            asm volatile("" : "+s"(step));
-            const char* rp = reinterpret_cast<const char*>(mixed + (bos + cv * kC) * rs + vch) - 3 * step;
-#pragma unroll
-            for (int i = 0; i < VNR; ++i) {
-              vraw[i] = *reinterpret_cast<const u4_t*>(rp + vlo);
-              rp += step;
-            }
-          } else {
-            // first or last chunk: rows outside the sequence read a clamped
-            // (valid) row and are zeroed; the rows before it are the history
-            const int64_t t0 = cv * kC + VT * fvtb - 3;
-            const u4_t zero = {0u, 0u, 0u, 0u};
-#pragma unroll
-            for (int i = 0; i < VNR; ++i) {
-              const int64_t t = t0 + i;
-              const int64_t tc = t < 0 ? 0 : (t >= len ? len - 1 : t);
-              const u4_t v = *reinterpret_cast<const u4_t*>(mixed + (bos + tc) * rs + ch0);
-              vraw[i] = (t >= 0 && t < len) ? v : zero;
-            }
-            if (cv == 0) {  // conv history: [channel][3] layout, 48 contiguous bytes
-              const bool hl = fvtb == 0 && hist != nullptr;
-              const uint16_t* hp = hl ? hist + ch0 * 3 : mixed + bos * rs + ch0;
-#pragma unroll
-              for (int i = 0; i < 3; ++i) {
-                const u4_t v = *reinterpret_cast<const u4_t*>(hp + (hl ? 8 * i : 0));
-                vraw[i] = hl ? v : vraw[i];
-              }
-            }
-          }
+        for (int u = 0; u < 4; ++u) {
+          pv[u] = make_uint4(0, 0, 0, 0);
+          if (v_thread && 4 * vtb + u < nk) pv[u] = *reinterpret_cast<const uint4*>(vbase + cv * vstride + u * vrow);
         }
       };
       auto stage_kq = [&](int64_t ck) __attribute__((always_inline)) {
@@ -761,116 +862,33 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
             *reinterpret_cast<uint4*>(qd + u * LDQ) = to_f16x8<IOT>(pq[u]);
           }
         }
-        if (wave == 7) {
-          if constexpr (FUSED) {
-            const bool ok = gtid < valid_rows(ck);
-            const float g = ok ? nA * softplus_prefill(pgate + dtb) : 0.f;
-            const float bt = ok ? sigmoid(pbeta) : 0.f;
-            gate_table(ck, g, bt);
-          } else {
-            gate_table(ck, pgate, pbeta);
-          }
-        }
       };
-      // V conv of chunk cv into registers (fused path): the VT tokens x 8
-      // channels of a lane, computed stage by stage over all values so the
-      // exp / reciprocal latencies overlap.  Same operation order and rounding
-      // as the standalone front end: y = round(silu(round(sum_tap w x))), the
-      // outer rounding being the io-type pack.
-      uint4 vo[VT];
-      auto conv_v = [&](int64_t cv) __attribute__((always_inline)) {
-        if (!fv_thread) return;
-        const int nv = valid_rows(cv);
-        float win[3][8];
-#pragma unroll
-        for (int j = 0; j < 3; ++j) unpack8<IOT>(to_uint4(vraw[j]), win[j]);
-        if (cv == 0 && fvtb == 0) {  // history rows hold [channel][tap]
-          float e[3][8];
-#pragma unroll
-          for (int j = 0; j < 3; ++j) unpack8<IOT>(to_uint4(vraw[j]), e[j]);
-#pragma unroll
-          for (int c = 0; c < 8; ++c)
-#pragma unroll
-            for (int j = 0; j < 3; ++j) win[j][c] = e[(3 * c + j) / 8][(3 * c + j) % 8];
-        }
-        float y[VT][8];
-#pragma unroll
-        for (int i = 0; i < VT; ++i) {
-          float x[8];
-          unpack8<IOT>(to_uint4(vraw[3 + i]), x);
-#pragma unroll
-          for (int c = 0; c < 8; ++c) {
-            float acc = 0.f;
-            acc = fmaf(win[0][c], vw[0][c], acc);
-            acc = fmaf(win[1][c], vw[1][c], acc);
-            acc = fmaf(win[2][c], vw[2][c], acc);
-            acc = fmaf(x[c], vw[3][c], acc);
-            y[i][c] = acc;
-            win[0][c] = win[1][c];
-            win[1][c] = win[2][c];
-            win[2][c] = x[c];
-          }
-          round8<IOT>(y[i]);
-        }
-        float d[VT][8];
-#pragma unroll
-        for (int i = 0; i < VT; ++i)
-#pragma unroll
-          for (int c = 0; c < 8; ++c) d[i][c] = fast_exp2(-1.4426950408889634f * y[i][c]);
-#pragma unroll
-        for (int i = 0; i < VT; ++i)
-#pragma unroll
-          for (int c = 0; c < 8; ++c) d[i][c] = __builtin_amdgcn_rcpf(1.0f + d[i][c]);
-#pragma unroll
-        for (int i = 0; i < VT; ++i) {
-#pragma unroll
-          for (int c = 0; c < 8; ++c) y[i][c] *= d[i][c];  // fast_silu
-          const uint4 o = to_f16x8<IOT>(pack8_io<IOT>(y[i]));
-          const bool ok = VT * fvtb + i < nv;
-          vo[i] = make_uint4(ok ? o.x : 0u, ok ? o.y : 0u, ok ? o.z : 0u, ok ? o.w : 0u);
-        }
-      };
-      // V rows of the next chunk into the single V buffer (after M: the chain
-      // has read the previous one)
       auto stage_v = [&]() __attribute__((always_inline)) {
-        if constexpr (FUSED) {
-          if (!fv_thread) return;
-          _Float16* vd = sV + (VT * fvtb) * LDV + 8 * fvdb;
+        if (!v_thread) return;
+        _Float16* vd = sV + (4 * vtb) * LDV + 8 * vdb;
 #pragma unroll
-          for (int u = 0; u < VT; ++u) *reinterpret_cast<uint4*>(vd + u * LDV) = vo[u];
-        } else {
-          if (!v_thread) return;
-          _Float16* vd = sV + (4 * vtb) * LDV + 8 * vdb;
-#pragma unroll
-          for (int u = 0; u < 4; ++u) *reinterpret_cast<uint4*>(vd + u * LDV) = to_f16x8<IOT>(pv[u]);
-        }
+        for (int u = 0; u < 4; ++u) *reinterpret_cast<uint4*>(vd + u * LDV) = to_f16x8<IOT>(pv[u]);
       };
 
       // ---- prologue: chunks 0 and 1 staged, chunk 0 solved
       prefetch_kq(0);
       prefetch_v(0);
       stage_kq(0);
-      if constexpr (FUSED) conv_v(0);
       stage_v();
-      if (nchunks > 1) {
-        prefetch_kq(1);
-        prefetch_v(1);
-        stage_kq(1);
-      }
-      if (nchunks > 2) prefetch_kq(2);
+      prefetch_kq(1);
+      prefetch_v(1);
+      stage_kq(1);
+      prefetch_kq(2);
       lds_barrier();  // P0
       solve(0);
       lds_barrier();  // B(0)
       for (int64_t c = 0; c < nchunks; ++c) {
-        if (c + 1 < nchunks) {
-          solve(c + 1);
-          if constexpr (FUSED) conv_v(c + 1);  // before M: overlaps the chain's first phase
-        }
+        if (c + 1 < nchunks) solve(c + 1);
         lds_barrier();  // M(c)
-        if (c + 1 < nchunks) stage_v();
-        if (c + 2 < nchunks) stage_kq(c + 2);
-        if (c + 3 < nchunks) prefetch_kq(c + 3);
-        if (c + 2 < nchunks) prefetch_v(c + 2);
+        stage_v();
+        stage_kq(c + 2);
+        prefetch_kq(c + 3);
+        prefetch_v(c + 2);
         lds_barrier();  // B(c+1)
       }
     }
