@@ -128,10 +128,10 @@ int gdn_chunk_gated_delta_rule(const void* q, const void* k, const void* v, int 
  * history gather, packed_causal_conv1d, split, prepare_gdn,
  * chunk_gated_delta_rule_to_cache) as three launches whose results equal
  * gdn_prefill_frontend followed by gdn_chunk_gated_delta_rule bit for bit:
- *   1. gdn_prefill_qk: the q/k channels only -> normalised q, k.
- *   2. gdn_prefill_fused: the chunk kernel, with the v conv + SiLU and the
- *      gate preparation done by its staging waves from the projections (v, g
- *      and beta never reach HBM).
+ *   1. gdn_prefill_qk: the q/k channels only -> normalised q, k, plus the
+ *      prepared gates g, beta.
+ *   2. gdn_prefill_fused: the chunk kernel, with the v conv + SiLU done by its
+ *      staging waves from the projections (v never reaches HBM).
  *   3. gdn_conv_snapshots: conv windows into the pool, after 2 has read the
  *      histories (a snapshot may overwrite a baseline slot).
  * Each returns GDN_ERR_UNSUPPORTED, launching nothing, for shapes outside it:
@@ -140,31 +140,35 @@ int gdn_chunk_gated_delta_rule(const void* q, const void* k, const void* v, int 
  *
  * gdn_prefill_qk: mixed [T, 2 H dk + ...] (row_stride, unit column stride);
  *   weight [conv_dim, 4]; conv_state [slots, L, conv_dim, 3] (slot/layer
- *   strides); baseline_slots[N] (<0: zero history); q_out, k_out [T, H, dk].
+ *   strides); baseline_slots[N] (<0: zero history); q_out, k_out [T, H, dk]
+ *   in out_dtype: the io dtype, or GDN_F16 for the f16 MFMA operands that
+ *   gdn_prefill_fused reads (the io-rounded values, converted toward zero);
+ *   gate, beta [T, HV] (row/head strides, any float dtype), A_log, dt_bias
+ *   [HV] -> g_out, beta_out [T, HV] fp32 (prepare_gdn, kernel/fused.py:105-117).
  */
 int gdn_prefill_qk(const void* mixed, int64_t row_stride, int io_dtype, const void* weight, int kernel_width,
                    const void* cu_seqlens, int cu_dtype, int64_t num_seqs, int64_t total_tokens, int64_t H,
                    int64_t dk, const void* conv_state, int64_t conv_slot_stride, int64_t conv_layer_stride,
                    int64_t layer, const void* baseline_slots, int baseline_dtype, void* q_out, void* k_out,
-                   void* stream);
+                   int out_dtype, int64_t HV, const void* gate, int64_t gate_row_stride, int64_t gate_head_stride,
+                   int gate_dtype, const void* beta, int64_t beta_row_stride, int64_t beta_head_stride,
+                   int beta_dtype, const void* A_log, int a_dtype, const void* dt_bias, int dt_dtype, float* g_out,
+                   float* beta_out, void* stream);
 
 /*
- * gdn_prefill_fused: q, k from gdn_prefill_qk; mixed, weight, conv_state and
- * baseline_slots as there (the v channels' history, and the initial
- * recurrent state, come from baseline_slots); gate, beta [T, HV] (row/head
- * strides, any float dtype), A_log, dt_bias [HV]; state pool, chunk/final
- * write slots and out as in gdn_chunk_gated_delta_rule.
+ * gdn_prefill_fused: q, k (f16), g, beta from gdn_prefill_qk; mixed, weight,
+ * conv_state and baseline_slots as there (the v channels' history, and the
+ * initial recurrent state, come from baseline_slots); state pool,
+ * chunk/final write slots and out as in gdn_chunk_gated_delta_rule.
  */
 int gdn_prefill_fused(const void* q, const void* k, const void* mixed, int64_t row_stride, int io_dtype,
                       const void* weight, int kernel_width, const void* cu_seqlens, int cu_dtype, int64_t num_seqs,
                       int64_t total_tokens, int64_t H, int64_t HV, int64_t dk, int64_t dv, const void* conv_state,
-                      int64_t conv_slot_stride, int64_t conv_layer_stride, const void* gate, int64_t gate_row_stride,
-                      int64_t gate_head_stride, int gate_dtype, const void* beta, int64_t beta_row_stride,
-                      int64_t beta_head_stride, int beta_dtype, const void* A_log, int a_dtype, const void* dt_bias,
-                      int dt_dtype, void* state, int state_dtype, int64_t slot_stride, int64_t layer_stride,
-                      int64_t head_stride, int64_t layer, const void* baseline_slots, int baseline_dtype,
-                      const void* chunk_write_slots, int chunk_write_dtype, const void* final_write_slots,
-                      int final_write_dtype, void* out, float scale, void* stream);
+                      int64_t conv_slot_stride, int64_t conv_layer_stride, const float* g, const float* beta,
+                      void* state, int state_dtype, int64_t slot_stride, int64_t layer_stride, int64_t head_stride,
+                      int64_t layer, const void* baseline_slots, int baseline_dtype, const void* chunk_write_slots,
+                      int chunk_write_dtype, const void* final_write_slots, int final_write_dtype, void* out,
+                      float scale, void* stream);
 
 /*
  * gdn_conv_snapshots: for each i < count with slots[i] >= 0, conv_state[slots[i],

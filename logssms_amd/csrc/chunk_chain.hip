@@ -50,7 +50,11 @@ namespace gdn {
 namespace {
 
 constexpr int kC = 64;
-constexpr int kThreads = 512;
+// Workgroup roles (waves i, i + 4 and i + 8 share a SIMD):
+//   0-3 chain, 4-5 inverses, 6-9 tiles and K/Q (V) staging, 10-11 fused v conv and gates.
+constexpr int kThreads = 768;
+constexpr int kChainWaves = 4;
+constexpr int kGateWave = 10;
 constexpr float kRcpLn2 = 1.4426950216f;  // gated_delta.py:12
 
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
@@ -109,21 +113,27 @@ __device__ __forceinline__ h8_t bfrag(f4_t a, f4_t b) {
   return o;
 }
 
-// 8 input halfs -> 8 f16 operand halfs (bf16 -> f16 is exact in range;
-// round-toward-zero saturates out-of-range values at +-65504).
-template <class IOT> __device__ __forceinline__ uint4 to_f16x8(uint4 raw);
-template <> __device__ __forceinline__ uint4 to_f16x8<f16>(uint4 raw) { return raw; }
-template <> __device__ __forceinline__ uint4 to_f16x8<bf16>(uint4 raw) {
-  auto cvt = [](uint32_t w) {
-    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(w << 16),
-                                                                   __uint_as_float(w & 0xffff0000u)));
-  };
-  return make_uint4(cvt(raw.x), cvt(raw.y), cvt(raw.z), cvt(raw.w));
-}
 template <class IOT> __device__ __forceinline__ uint16_t out_bits(float x);
 template <> __device__ __forceinline__ uint16_t out_bits<bf16>(float x) { return f32_to_bf16_bits(x); }
 template <> __device__ __forceinline__ uint16_t out_bits<f16>(float x) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave with DPP moves (no LDS):
+// a scan within each 16-lane row (row_shr 1, 2, 4, 8), then the row totals
+// carried upwards (row_bcast 15 into rows 1 and 3, row_bcast 31 into rows 2
+// and 3).  Masked-off rows and lanes shifted in from outside a row add 0.
+template <int CTRL, int ROW_MASK> __device__ __forceinline__ float dpp_src(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xf, true));
+}
+__device__ __forceinline__ float wave_prefix_sum(float x) {
+  x += dpp_src<0x111, 0xf>(x);
+  x += dpp_src<0x112, 0xf>(x);
+  x += dpp_src<0x114, 0xf>(x);
+  x += dpp_src<0x118, 0xf>(x);
+  x += dpp_src<0x142, 0xa>(x);
+  x += dpp_src<0x143, 0xc>(x);
+  return x;
 }
 
 // Block-uniform index read through the scalar data cache (a scalar load: it
@@ -217,13 +227,13 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
 
   ST* pool = static_cast<ST*>(p.state);
   const int64_t head_off = p.layer * p.layer_stride + h * p.head_stride + col_base;
-  const int j = wave;  // chain wave: state columns 32j..32j+31 (tiles 2j, 2j+1)
-  f4_t hT[2][HT];
-  // State slice rows 16 ti + 4 lg + e, columns 32 j + 16 u + lr: a wave-uniform
-  // base plus a 32-bit lane offset (kept opaque so the per-element offsets are
-  // not hoisted and held in registers across the chunk loop).
+  const int j = wave;  // chain wave: state columns 16j..16j+15
+  f4_t hT[HT];
+  // State slice rows 16 ti + 4 lg + e, column 16 j + lr: a wave-uniform base
+  // plus a 32-bit lane offset (kept opaque so the per-element offsets are not
+  // hoisted and held in registers across the chunk loop).
   auto state_lane_off = [&]() {
-    uint32_t o = static_cast<uint32_t>((4 * lg * p.DV + 32 * j + lr) * sizeof(ST));
+    uint32_t o = static_cast<uint32_t>((4 * lg * p.DV + 16 * j + lr) * sizeof(ST));
     asm volatile("" : "+v"(o));
     return o;
   };
@@ -232,29 +242,23 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     const char* src = rs >= 0 ? reinterpret_cast<const char*>(pool + rs * p.slot_stride + head_off) : nullptr;
     const uint32_t o = state_lane_off();
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int ti = 0; ti < HT; ++ti)
 #pragma unroll
-      for (int ti = 0; ti < HT; ++ti)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          hT[u][ti][e] = src ? load_st(reinterpret_cast<const ST*>(
-                                   src + ((16 * ti + e) * p.DV + 16 * u) * sizeof(ST) + o))
-                             : 0.f;
+      for (int e = 0; e < 4; ++e)
+        hT[ti][e] = src ? load_st(reinterpret_cast<const ST*>(src + (16 * ti + e) * p.DV * sizeof(ST) + o)) : 0.f;
   };
   auto store_state = [&](int64_t slot_idx) {
     char* dst = reinterpret_cast<char*>(pool + slot_idx * p.slot_stride + head_off);
     const uint32_t o = state_lane_off();
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int ti = 0; ti < HT; ++ti)
 #pragma unroll
-      for (int ti = 0; ti < HT; ++ti)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          store_st(reinterpret_cast<ST*>(dst + ((16 * ti + e) * p.DV + 16 * u) * sizeof(ST) + o), hT[u][ti][e]);
+      for (int e = 0; e < 4; ++e)
+        store_st(reinterpret_cast<ST*>(dst + (16 * ti + e) * p.DV * sizeof(ST) + o), hT[ti][e]);
   };
 
   if (nchunks == 0) {  // empty sequence: the final state is the initial state
-    if (wave < 2 && p.fw_slots) {
+    if (wave < kChainWaves && p.fw_slots) {
       const int64_t fw = uniform_index(p.fw_slots, n, p.fw_is64);
       if (fw >= 0) {
         load_state();
@@ -275,19 +279,17 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     reinterpret_cast<uint4*>(sM)[e] = make_uint4(0, 0, 0, 0);
   }
 
-  if (wave < 2) {
+  if (wave < kChainWaves) {
     // ==================================================================== chain waves
-    uint16_t* og = static_cast<uint16_t*>(p.out) + (bos * p.HV + h) * p.DV + col_base + 32 * j;
-    uint16_t* vng = p.v_new ? static_cast<uint16_t*>(p.v_new) + (bos * p.HV + h) * p.DV + col_base + 32 * j : nullptr;
+    uint16_t* og = static_cast<uint16_t*>(p.out) + (bos * p.HV + h) * p.DV + col_base + 16 * j;
+    uint16_t* vng = p.v_new ? static_cast<uint16_t*>(p.v_new) + (bos * p.HV + h) * p.DV + col_base + 16 * j : nullptr;
     const int64_t tok_stride = p.HV * p.DV;
     load_state();
     // No vector-memory load may be outstanding at the loop head (a wait there
     // would also wait for the previous chunk's output stores): consume the
     // loaded state before entering the loop.
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-      for (int ti = 0; ti < HT; ++ti) asm volatile("" ::"v"(hT[u][ti]));
+    for (int ti = 0; ti < HT; ++ti) asm volatile("" ::"v"(hT[ti]));
     lds_barrier();  // P0
     lds_barrier();  // B(0)
     for (int64_t c = 0; c < nchunks; ++c) {
@@ -296,103 +298,79 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       const _Float16* K = sK + (c % 3) * kC * LDK;
       const _Float16* Q = sQ + (c & 1) * kC * LDQ;
       const float* gt = sG + (c % 3) * GTS;
-      // ---- S1: P = K h -> R = beta (v - 2^G P);  O^T = h^T Q^T (token columns)
-      f4_t R[2][4];
+      // ---- S1: P = K h -> R = beta (v - 2^G P);  O^T = h^T Q^T (token columns).
+      // The 4 fragments of a 32-deep k step are read together; the converted
+      // state is the right operand of K h and the left operand of h^T Q^T.
+      f4_t R[4], Ot[4];
       {
-        f4_t P[2][4];
+        f4_t P[4];
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) P[u][i] = zero4();
+        for (int i = 0; i < 4; ++i) P[i] = zero4();
 #pragma unroll
         for (int m = 0; m < KS; ++m) {
-          const h8_t hb0 = bfrag(hT[0][2 * m], hT[0][2 * m + 1]);
-          const h8_t hb1 = bfrag(hT[1][2 * m], hT[1][2 * m + 1]);
+          h8_t kf[4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const h8_t kf = afrag(K, LDK, 16 * i + lr, 32 * m, lg);
-            P[0][i] = mma(kf, hb0, P[0][i]);
-            P[1][i] = mma(kf, hb1, P[1][i]);
-          }
+          for (int i = 0; i < 4; ++i) kf[i] = afrag(K, LDK, 16 * i + lr, 32 * m, lg);
+          const h8_t hb = bfrag(hT[2 * m], hT[2 * m + 1]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) P[i] = mma(kf[i], hb, P[i]);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int t0 = 16 * i + 4 * lg;
           const f4_t e4 = *reinterpret_cast<const f4_t*>(gt + G_EXP + t0);
           const f4_t b4 = *reinterpret_cast<const f4_t*>(gt + G_BETA + t0);
+          // V rows t0..t0+3 at column 16j + lr
+          const h4_t v4 = tr_read(sV + (16 * i + 4 * lg + (lr >> 2)) * LDV + 16 * j + 4 * (lr & 3));
 #pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            // V rows t0..t0+3 at column 32j + 16u + lr
-            const h4_t v4 = tr_read(sV + (16 * i + 4 * lg + (lr >> 2)) * LDV + 32 * j + 16 * u + 4 * (lr & 3));
-#pragma unroll
-            for (int e = 0; e < 4; ++e) R[u][i][e] = b4[e] * (static_cast<float>(v4[e]) - e4[e] * P[u][i][e]);
-          }
+          for (int e = 0; e < 4; ++e) R[i][e] = b4[e] * (static_cast<float>(v4[e]) - e4[e] * P[i][e]);
         }
       }
-      f4_t Ot[2][4];
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) Ot[u][i] = zero4();
+      for (int i = 0; i < 4; ++i) Ot[i] = zero4();
 #pragma unroll
       for (int m = 0; m < KS; ++m) {
-        // the right operand of h doubles as the left operand of h^T
-        const h8_t hb0 = bfrag(hT[0][2 * m], hT[0][2 * m + 1]);
-        const h8_t hb1 = bfrag(hT[1][2 * m], hT[1][2 * m + 1]);
+        h8_t qf[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const h8_t qf = afrag(Q, LDQ, 16 * i + lr, 32 * m, lg);
-          Ot[0][i] = mma(hb0, qf, Ot[0][i]);
-          Ot[1][i] = mma(hb1, qf, Ot[1][i]);
-        }
+        for (int i = 0; i < 4; ++i) qf[i] = afrag(Q, LDQ, 16 * i + lr, 32 * m, lg);
+        const h8_t hb = bfrag(hT[2 * m], hT[2 * m + 1]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Ot[i] = mma(hb, qf[i], Ot[i]);
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float eo = gt[G_EXP + 16 * i + lr];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) Ot[u][i] *= eo;
-      }
+      for (int i = 0; i < 4; ++i) Ot[i] *= gt[G_EXP + 16 * i + lr];
       lds_barrier();  // M(c)
       // ---- S2: v'_top = A11 R_top; R_bot -= L21 v'_top; v'_bot = A22 R_bot
       const _Float16* A = sA + (c & 1) * kC * LDA;
-      f4_t V[2][4];
-      h8_t vb0[2], vb1[2];
+      f4_t V[4];
+      h8_t vb0, vb1;
       {
         const h8_t a0 = afrag(A, LDA, lr, 0, lg), a1 = afrag(A, LDA, 16 + lr, 0, lg);
         const h8_t l2 = afrag(A, LDA, 32 + lr, 0, lg), l3 = afrag(A, LDA, 48 + lr, 0, lg);  // -L21
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const h8_t rb0 = bfrag(R[u][0], R[u][1]);
-          V[u][0] = mma(a0, rb0, zero4());
-          V[u][1] = mma(a1, rb0, zero4());
-          vb0[u] = bfrag(V[u][0], V[u][1]);  // also the left operand of v'^T
-          R[u][2] = mma(l2, vb0[u], R[u][2]);
-          R[u][3] = mma(l3, vb0[u], R[u][3]);
-        }
         const h8_t a2 = afrag(A, LDA, 32 + lr, 32, lg), a3 = afrag(A, LDA, 48 + lr, 32, lg);
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const h8_t rb1 = bfrag(R[u][2], R[u][3]);
-          V[u][2] = mma(a2, rb1, zero4());
-          V[u][3] = mma(a3, rb1, zero4());
-          vb1[u] = bfrag(V[u][2], V[u][3]);
-        }
+        const h8_t rb0 = bfrag(R[0], R[1]);
+        V[0] = mma(a0, rb0, zero4());
+        V[1] = mma(a1, rb0, zero4());
+        vb0 = bfrag(V[0], V[1]);  // also the left operand of v'^T
+        R[2] = mma(l2, vb0, R[2]);
+        R[3] = mma(l3, vb0, R[3]);
+        const h8_t rb1 = bfrag(R[2], R[3]);
+        V[2] = mma(a2, rb1, zero4());
+        V[3] = mma(a3, rb1, zero4());
+        vb1 = bfrag(V[2], V[3]);
       }
       // ---- S3a: o^T += v'^T M^T; a lane holds 4 consecutive output columns of one token
       {
         const _Float16* M = sM + (c & 1) * kC * LDA;
+        h8_t mf[6];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const h8_t mf = afrag(M, LDA, 16 * i + lr, 0, lg);
+        for (int i = 0; i < 4; ++i) mf[i] = afrag(M, LDA, 16 * i + lr, 0, lg);
+        mf[4] = afrag(M, LDA, 32 + lr, 32, lg);
+        mf[5] = afrag(M, LDA, 48 + lr, 32, lg);
 #pragma unroll
-          for (int u = 0; u < 2; ++u) Ot[u][i] = mma(vb0[u], mf, Ot[u][i]);
-        }
-#pragma unroll
-        for (int i = 2; i < 4; ++i) {
-          const h8_t mf = afrag(M, LDA, 16 * i + lr, 32, lg);
-#pragma unroll
-          for (int u = 0; u < 2; ++u) Ot[u][i] = mma(vb1[u], mf, Ot[u][i]);
-        }
+        for (int i = 0; i < 4; ++i) Ot[i] = mma(vb0, mf[i], Ot[i]);
+        Ot[2] = mma(vb1, mf[4], Ot[2]);
+        Ot[3] = mma(vb1, mf[5], Ot[3]);
       }
       {
         char* ob = reinterpret_cast<char*>(og + c * kC * tok_stride);
@@ -401,50 +379,38 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           if (16 * i + lr < nv) {
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-              uint2 w;
-              w.x = out_pack2<IOT>(p.scale * Ot[u][i][0], p.scale * Ot[u][i][1]);
-              w.y = out_pack2<IOT>(p.scale * Ot[u][i][2], p.scale * Ot[u][i][3]);
-              *reinterpret_cast<uint2*>(ob + (16 * i * tok_stride + 16 * u) * 2 + o) = w;
-            }
+            uint2 w;
+            w.x = out_pack2<IOT>(p.scale * Ot[i][0], p.scale * Ot[i][1]);
+            w.y = out_pack2<IOT>(p.scale * Ot[i][2], p.scale * Ot[i][3]);
+            *reinterpret_cast<uint2*>(ob + 16 * i * tok_stride * 2 + o) = w;
           }
         }
       }
-      if (vng) {
+      if (vng) {  // v' (u - w h of the reference): uniform row base plus an opaque 32-bit lane offset
+        char* vb = reinterpret_cast<char*>(vng + c * kC * tok_stride);
+        uint32_t ov = static_cast<uint32_t>((4 * lg * tok_stride + lr) * 2);
+        asm volatile("" : "+v"(ov));
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int t = 16 * i + 4 * lg + e;
-              if (t < nv) vng[(c * kC + t) * tok_stride + 16 * u + lr] = out_bits<IOT>(V[u][i][e]);
-            }
+          for (int e = 0; e < 4; ++e)
+            if (16 * i + 4 * lg + e < nv)
+              *reinterpret_cast<uint16_t*>(vb + (16 * i + e) * tok_stride * 2 + ov) = out_bits<IOT>(V[i][e]);
       }
       // ---- S3b: h <- 2^G_last h + K^T (2^(G_last - G) v')
       {
-        h8_t db0[2], db1[2];
         const f4_t d0 = *reinterpret_cast<const f4_t*>(gt + G_DEC + 4 * lg);
         const f4_t d1 = *reinterpret_cast<const f4_t*>(gt + G_DEC + 16 + 4 * lg);
         const f4_t d2 = *reinterpret_cast<const f4_t*>(gt + G_DEC + 32 + 4 * lg);
         const f4_t d3 = *reinterpret_cast<const f4_t*>(gt + G_DEC + 48 + 4 * lg);
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          db0[u] = bfrag(V[u][0] * d0, V[u][1] * d1);
-          db1[u] = bfrag(V[u][2] * d2, V[u][3] * d3);
-        }
+        const h8_t db0 = bfrag(V[0] * d0, V[1] * d1);
+        const h8_t db1 = bfrag(V[2] * d2, V[3] * d3);
         const float gl = gt[G_LAST];
 #pragma unroll
         for (int ti = 0; ti < HT; ++ti) {
           const h8_t k0 = tfrag(K, LDK, 0, 16 * ti, lr, lg);
           const h8_t k1 = tfrag(K, LDK, 32, 16 * ti, lr, lg);
-#pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            f4_t acc = hT[u][ti] * gl;
-            acc = mma(k0, db0[u], acc);
-            hT[u][ti] = mma(k1, db1[u], acc);
-          }
+          hT[ti] = mma(k1, db1, mma(k0, db0, hT[ti] * gl));
         }
       }
       if (cw >= 0) store_state(cw);
@@ -456,111 +422,136 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     }
   } else {
     // ==================================================================== side waves
-    const int sw = wave - 2;        // 0..5
-    // Solve for chunk nc.  S tiles (ti, tj) of X K^T in the "row" orientation:
-    // lane (g, c) holds entry (t = 16 ti + c, s = 16 tj + 4 g + e).
-    auto solve = [&](int64_t nc) __attribute__((always_inline)) {
+    const int sw = wave - kChainWaves;  // 0-1 inverses, 2-5 tiles and staging, 6-7 conv and gates
+    // Entries (t, s..s+3) of a row-orientation tile -> masked values.
+    auto masked = [&](const float* gt, f4_t s, int t, int s0, bool strict, bool with_beta)
+        __attribute__((always_inline)) {
+      const f4_t gs = *reinterpret_cast<const f4_t*>(gt + s0);
+      const float gti = gt[t];
+      const float bt = with_beta ? gt[G_BETA + t] : 1.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool keep = strict ? t > s0 + e : t >= s0 + e;
+        s[e] = keep ? bt * s[e] * fast_exp2(fminf(gti - gs[e], 0.f)) : 0.f;
+      }
+      return s;
+    };
+    auto store_row4 = [&](_Float16* X, int t, int s0, f4_t v) __attribute__((always_inline)) {
+      const h4_t w = {to_op(v[0]), to_op(v[1]), to_op(v[2]), to_op(v[3])};
+      *reinterpret_cast<h4_t*>(X + t * LDA + s0) = w;
+    };
+
+    // ---- inverses (waves 4-5): A_bb = (I + L_bb)^-1 for the 32-token half b,
+    // in two parts so that it spans both phases of a chunk:
+    //   first:  L, P = I - L + L^2 - L^3, L^4
+    //   second: P <- P (I + L^4)(I + L^8)(I + L^16), stored into A.
+    Tri invP, invL4;
+    auto inv_first = [&](int64_t nc) __attribute__((always_inline)) {
+      const _Float16* K = sK + (nc % 3) * kC * LDK;
+      const float* gt = sG + (nc % 3) * GTS;
+      const int r0 = 32 * sw;
+      f4_t s00 = zero4(), s11 = zero4(), s10 = zero4(), s01 = zero4();
+      h8_t k0[KS], k1[KS];
+#pragma unroll
+      for (int m = 0; m < KS; ++m) {
+        k0[m] = afrag(K, LDK, r0 + lr, 32 * m, lg);
+        k1[m] = afrag(K, LDK, r0 + 16 + lr, 32 * m, lg);
+      }
+#pragma unroll
+      for (int m = 0; m < KS; ++m) {
+        s00 = mma(k0[m], k0[m], s00);
+        s11 = mma(k1[m], k1[m], s11);
+        s10 = mma(k1[m], k0[m], s10);  // C layout: entry (16 + 4g + e, c)
+        s01 = mma(k0[m], k1[m], s01);  // C layout: entry (4g + e, 16 + c) of S^T
+      }
+      // C-layout tiles of L (row 4g + e, col c) and of L^T (row 4g + e, col c
+      // of L^T = entry (c, 4g + e) of L); S is symmetric on the diagonal tiles.
+      auto lmask_c = [&](f4_t s, int t0, int sc) {  // entries (t0 + 4g + e, sc + c)
+        const f4_t gt4 = *reinterpret_cast<const f4_t*>(gt + t0 + 4 * lg);
+        const f4_t bt4 = *reinterpret_cast<const f4_t*>(gt + G_BETA + t0 + 4 * lg);
+        const float gsc = gt[sc + lr];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          s[e] = (t0 + 4 * lg + e > sc + lr) ? bt4[e] * s[e] * fast_exp2(fminf(gt4[e] - gsc, 0.f)) : 0.f;
+        return s;
+      };
+      auto lmask_t = [&](f4_t s, int tc, int s0) {  // entries (tc + c, s0 + 4g + e)
+        return masked(gt, s, tc + lr, s0 + 4 * lg, true, true);
+      };
+      Tri L;
+      L.x[0] = lmask_c(s00, r0, r0);
+      L.x[1] = lmask_c(s10, r0 + 16, r0);
+      L.x[2] = lmask_c(s11, r0 + 16, r0 + 16);
+      L.t[0] = lmask_t(s00, r0, r0);
+      L.t[1] = lmask_t(s01, r0 + 16, r0);
+      L.t[2] = lmask_t(s11, r0 + 16, r0 + 16);
+      // P1 = I - L + L^2 - L^3, then P <- P + P L^4
+      const Tri L2 = tri_mul(L, L);
+      const Tri L3 = tri_mul(L, L2);
+      Tri P;
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        P.x[q] = L2.x[q] - L.x[q] - L3.x[q];
+        P.t[q] = L2.t[q] - L.t[q] - L3.t[q];
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float one = (4 * lg + e == lr) ? 1.f : 0.f;
+        P.x[0][e] += one;
+        P.x[2][e] += one;
+        P.t[0][e] += one;
+        P.t[2][e] += one;
+      }
+      invL4 = tri_mul(L2, L2);
+      invP = P;
+    };
+    auto inv_second = [&](int64_t nc) __attribute__((always_inline)) {
+      _Float16* A = sA + (nc & 1) * kC * LDA;
+      const int r0 = 32 * sw;
+      Tri P = tri_mul_add(invP, invL4);
+      const Tri L8 = tri_mul(invL4, invL4);
+      P = tri_mul_add(P, L8);
+      const Tri L16 = tri_mul(L8, L8);
+      P = tri_mul_add(P, L16);
+      // row-major A_bb: C-layout tile (a, b) of A^T holds row 16b + c, columns 16a + 4g..+3
+      store_row4(A, r0 + lr, r0 + 4 * lg, P.t[0]);
+      store_row4(A, r0 + 16 + lr, r0 + 4 * lg, P.t[1]);
+      store_row4(A, r0 + 16 + lr, r0 + 16 + 4 * lg, P.t[2]);
+    };
+
+    // ---- row-orientation tiles (waves 6-9): (ti, tj) of Q K^T -> M, and of
+    // K K^T for -L21 (lane (g, c) holds entry (t = 16 ti + c, s = 16 tj + 4 g + e)).
+    // Each wave forms some before the M barrier and the rest after it (the
+    // chain reads them one chunk later).
+    auto tiles = [&](int64_t nc, bool second) __attribute__((always_inline)) {
       const _Float16* K = sK + (nc % 3) * kC * LDK;
       const _Float16* Q = sQ + (nc & 1) * kC * LDQ;
       const float* gt = sG + (nc % 3) * GTS;
       _Float16* A = sA + (nc & 1) * kC * LDA;
       _Float16* M = sM + (nc & 1) * kC * LDA;
-      // entries (t, s..s+3) of a row-orientation tile -> masked values
-      auto masked = [&](f4_t s, int t, int s0, bool strict, bool with_beta) {
-        const f4_t gs = *reinterpret_cast<const f4_t*>(gt + s0);
-        const float gti = gt[t];
-        const float bt = with_beta ? gt[G_BETA + t] : 1.f;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const bool keep = strict ? t > s0 + e : t >= s0 + e;
-          s[e] = keep ? bt * s[e] * fast_exp2(fminf(gti - gs[e], 0.f)) : 0.f;
-        }
-        return s;
-      };
-      auto store_row4 = [&](_Float16* X, int t, int s0, f4_t v) {
-        const h4_t w = {to_op(v[0]), to_op(v[1]), to_op(v[2]), to_op(v[3])};
-        *reinterpret_cast<h4_t*>(X + t * LDA + s0) = w;
-      };
-      if (sw < 2) {
-        // A_bb = (I + L_bb)^-1 for the 32-token half b = sw
-        const int r0 = 32 * sw;
-        f4_t s00 = zero4(), s11 = zero4(), s10 = zero4(), s01 = zero4();
+      auto tile = [&](const _Float16* X, int ldx, int ti, int tj) {
+        h8_t a[KS], b[KS];
 #pragma unroll
         for (int m = 0; m < KS; ++m) {
-          const h8_t k0 = afrag(K, LDK, r0 + lr, 32 * m, lg);
-          const h8_t k1 = afrag(K, LDK, r0 + 16 + lr, 32 * m, lg);
-          s00 = mma(k0, k0, s00);
-          s11 = mma(k1, k1, s11);
-          s10 = mma(k1, k0, s10);  // C layout: entry (16 + 4g + e, c)
-          s01 = mma(k0, k1, s01);  // C layout: entry (4g + e, 16 + c) of S^T
+          a[m] = afrag(K, LDK, 16 * tj + lr, 32 * m, lg);
+          b[m] = afrag(X, ldx, 16 * ti + lr, 32 * m, lg);
         }
-        // C-layout tiles of L (row 4g + e, col c) and of L^T (row 4g + e, col c
-        // of L^T = entry (c, 4g + e) of L); S is symmetric on the diagonal tiles.
-        auto lmask_c = [&](f4_t s, int t0, int sc) {  // entries (t0 + 4g + e, sc + c)
-          const f4_t gt4 = *reinterpret_cast<const f4_t*>(gt + t0 + 4 * lg);
-          const f4_t bt4 = *reinterpret_cast<const f4_t*>(gt + G_BETA + t0 + 4 * lg);
-          const float gsc = gt[sc + lr];
+        f4_t acc = zero4();
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            s[e] = (t0 + 4 * lg + e > sc + lr) ? bt4[e] * s[e] * fast_exp2(fminf(gt4[e] - gsc, 0.f)) : 0.f;
-          return s;
-        };
-        auto lmask_t = [&](f4_t s, int tc, int s0) {  // entries (tc + c, s0 + 4g + e)
-          return masked(s, tc + lr, s0 + 4 * lg, true, true);
-        };
-        Tri L;
-        L.x[0] = lmask_c(s00, r0, r0);
-        L.x[1] = lmask_c(s10, r0 + 16, r0);
-        L.x[2] = lmask_c(s11, r0 + 16, r0 + 16);
-        L.t[0] = lmask_t(s00, r0, r0);
-        L.t[1] = lmask_t(s01, r0 + 16, r0);
-        L.t[2] = lmask_t(s11, r0 + 16, r0 + 16);
-        // P1 = I - L + L^2 - L^3, then P <- P + P L^(2^k)
-        const Tri L2 = tri_mul(L, L);
-        const Tri L3 = tri_mul(L, L2);
-        Tri P;
-#pragma unroll
-        for (int q = 0; q < 3; ++q) {
-          P.x[q] = L2.x[q] - L.x[q] - L3.x[q];
-          P.t[q] = L2.t[q] - L.t[q] - L3.t[q];
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float one = (4 * lg + e == lr) ? 1.f : 0.f;
-          P.x[0][e] += one;
-          P.x[2][e] += one;
-          P.t[0][e] += one;
-          P.t[2][e] += one;
-        }
-        const Tri L4 = tri_mul(L2, L2);
-        P = tri_mul_add(P, L4);
-        const Tri L8 = tri_mul(L4, L4);
-        P = tri_mul_add(P, L8);
-        const Tri L16 = tri_mul(L8, L8);
-        P = tri_mul_add(P, L16);
-        // row-major A_bb: C-layout tile (a, b) of A^T holds row 16b + c, columns 16a + 4g..+3
-        store_row4(A, r0 + lr, r0 + 4 * lg, P.t[0]);
-        store_row4(A, r0 + 16 + lr, r0 + 4 * lg, P.t[1]);
-        store_row4(A, r0 + 16 + lr, r0 + 16 + 4 * lg, P.t[2]);
-      } else {
-        // Row-orientation tiles: (ti, tj) of Q K^T -> M, and of K K^T for -L21.
-        // Waves 4-7 split them: {-L21 (2,0),(2,1)} {-L21 (3,0),(3,1)} and M rows.
-        const int w = sw - 2;  // 0..3
-        auto tile = [&](const _Float16* X, int ldx, int ti, int tj) {
-          f4_t acc = zero4();
-#pragma unroll
-          for (int m = 0; m < KS; ++m)
-            acc = mma(afrag(K, LDK, 16 * tj + lr, 32 * m, lg), afrag(X, ldx, 16 * ti + lr, 32 * m, lg), acc);
-          return acc;
-        };
-        auto mtile = [&](int ti, int tj) {
-          const int t = 16 * ti + lr, s0 = 16 * tj + 4 * lg;
-          store_row4(M, t, s0, masked(tile(Q, LDQ, ti, tj), t, s0, false, false));
-        };
-        auto ltile = [&](int ti, int tj) {
-          const int t = 16 * ti + lr, s0 = 16 * tj + 4 * lg;
-          store_row4(A, t, s0, -masked(tile(K, LDK, ti, tj), t, s0, true, true));
-        };
+        for (int m = 0; m < KS; ++m) acc = mma(a[m], b[m], acc);
+        return acc;
+      };
+      auto mtile = [&](int ti, int tj) {
+        const int t = 16 * ti + lr, s0 = 16 * tj + 4 * lg;
+        store_row4(M, t, s0, masked(gt, tile(Q, LDQ, ti, tj), t, s0, false, false));
+      };
+      auto ltile = [&](int ti, int tj) {
+        const int t = 16 * ti + lr, s0 = 16 * tj + 4 * lg;
+        store_row4(A, t, s0, -masked(gt, tile(K, LDK, ti, tj), t, s0, true, true));
+      };
+      const int w = sw - 2;  // 0..3
+      // waves 6-7 share SIMDs with the v conv waves, 8-9 with the inverse waves
+      if (!second) {
         if (w == 0) {
           ltile(2, 0);
           ltile(2, 1);
@@ -574,10 +565,14 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         } else if (w == 2) {
           mtile(2, 1);
           mtile(2, 2);
-          mtile(3, 0);
         } else {
+          mtile(3, 0);
           mtile(3, 1);
+        }
+      } else {
+        if (w == 2) {
           mtile(3, 2);
+        } else if (w == 3) {
           mtile(3, 3);
         }
       }
@@ -587,13 +582,8 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     // cumulative gate in log2 units (cumsum.py:19-75) and its exponentials.
     auto gate_table = [&](int64_t ck, float x, float bt) __attribute__((always_inline)) {
       const int nk = valid_rows(ck);
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const float y = __shfl_up(x, off, 64);
-        if (lane >= off) x += y;
-      }
-      const float G = x * kRcpLn2;
-      const float Gl = __shfl(G, nk > 0 ? nk - 1 : 0, 64);
+      const float G = wave_prefix_sum(x) * kRcpLn2;
+      const float Gl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(G), nk > 0 ? nk - 1 : 0));
       float* gt = sG + (ck % 3) * GTS;
       gt[lane] = G;
       gt[G_EXP + lane] = fast_exp2(G);
@@ -602,57 +592,27 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       if (lane == 0) gt[G_LAST] = fast_exp2(Gl);
     };
 
-    // ---- gates (wave 2, after the M barrier), one token per lane.  The raw
-    // values stay bits until staged, so the prefetch never waits for its loads.
+    // ---- gates (one wave, after the M barrier), one token per lane; the
+    // prepared g and beta (kernel/fused.py:105-117) feed the gate table.
     const FrontIn& f = p.front;
-    uint32_t graw = 0, braw = 0;
-    float nA = 0.f, dtb = 0.f;
-    if constexpr (FUSED) {
-      if (wave == 2) {
-        nA = -expf(load_any(f.A_log, h, f.a_dtype));
-        dtb = load_any(f.dt_bias, h, f.dt_dtype);
-      }
-    }
-    auto raw_bits = [](const void* ptr, int64_t i, int dtype) __attribute__((always_inline)) -> uint32_t {
-      if (dtype == GDN_BF16 || dtype == GDN_F16) return static_cast<const uint16_t*>(ptr)[i];
-      return static_cast<const uint32_t*>(ptr)[i];
-    };
-    auto bits_f32 = [](uint32_t b, int dtype) __attribute__((always_inline)) -> float {
-      if (dtype == GDN_BF16) return __uint_as_float(b << 16);
-      if (dtype == GDN_F16) return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b)));
-      return __uint_as_float(b);
-    };
+    float pgate = 0.f, pbeta = 0.f;
     auto prefetch_g = [&](int64_t ck) __attribute__((always_inline)) {
       const bool ok = lane < valid_rows(ck);
       const int64_t t = bos + (ok ? ck * kC + lane : 0);  // a valid row for every chunk index
-      if constexpr (FUSED) {
-        graw = raw_bits(f.gate, t * f.gate_r + h * f.gate_h, f.gate_dtype);
-        braw = raw_bits(f.beta, t * f.beta_r + h * f.beta_h, f.beta_dtype);
-      } else {
-        graw = __float_as_uint(p.g[t * p.HV + h]);
-        braw = __float_as_uint(p.beta[t * p.HV + h]);
-      }
+      pgate = p.g[t * p.HV + h];
+      pbeta = p.beta[t * p.HV + h];
     };
     auto stage_g = [&](int64_t ck) __attribute__((always_inline)) {
       const bool ok = lane < valid_rows(ck);
-      float g, bt;
-      if constexpr (FUSED) {  // kernel/fused.py:105-117
-        g = nA * softplus_prefill(bits_f32(graw, f.gate_dtype) + dtb);
-        bt = sigmoid(bits_f32(braw, f.beta_dtype));
-      } else {
-        g = __uint_as_float(graw);
-        bt = __uint_as_float(braw);
-      }
-      gate_table(ck, ok ? g : 0.f, ok ? bt : 0.f);
+      gate_table(ck, ok ? pgate : 0.f, ok ? pbeta : 0.f);
     };
 
     // ---- fused path: V rows are the conv + SiLU of the projections
-    // (packed_conv.py:49-133), computed by waves 2-3 after the M barrier (their
-    // SIMDs are idle then).  A lane convolves VT tokens x 8 channels with the 3
-    // inputs before them (the tokens before, or the conv history at the
-    // sequence start).
+    // (packed_conv.py:49-133), computed by waves 10-11 after the M barrier.  A
+    // lane convolves VT tokens x 8 channels with the 3 inputs before them (the
+    // tokens before, or the conv history at the sequence start).
     constexpr int VT = 4, VNR = VT + 3;
-    const int fst = tid - 128;
+    const int fst = tid - 640;
     const bool fv_thread = FUSED && fst >= 0 && fst < 128;
     const int fvtb = fst >> 3, fvdb = fst & 7;
     const uint16_t* mixed = static_cast<const uint16_t*>(f.mixed);
@@ -721,12 +681,13 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         }
       }
     };
-    // conv of chunk cv, stage by stage over all VT x 8 values so the exp /
-    // reciprocal latencies overlap, then the rows into the single V buffer
-    // (after M: the chain has read the previous chunk's).  Same operation
-    // order and rounding as the standalone front end:
+    // conv of chunk cv into registers, stage by stage over all VT x 8 values
+    // so the exp / reciprocal latencies overlap (before M); the rows go into
+    // the single V buffer after M, when the chain has read the previous
+    // chunk's.  Same operation order and rounding as the standalone front end:
     // y = round(silu(round(sum_tap w x))), the outer rounding being the io pack.
-    auto conv_stage_v = [&](int64_t cv) __attribute__((always_inline)) {
+    uint4 vo[VT];
+    auto conv_v = [&](int64_t cv) __attribute__((always_inline)) {
       if (!fv_thread) return;
       const int nv = valid_rows(cv);
       float win[3][8];
@@ -769,27 +730,42 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       for (int i = 0; i < VT; ++i)
 #pragma unroll
         for (int c = 0; c < 8; ++c) d[i][c] = __builtin_amdgcn_rcpf(1.0f + d[i][c]);
-      _Float16* vd = sV + (VT * fvtb) * LDV + 8 * fvdb;
 #pragma unroll
       for (int i = 0; i < VT; ++i) {
 #pragma unroll
         for (int c = 0; c < 8; ++c) y[i][c] *= d[i][c];  // fast_silu
         const uint4 o = to_f16x8<IOT>(pack8_io<IOT>(y[i]));
         const bool ok = VT * fvtb + i < nv;
-        *reinterpret_cast<uint4*>(vd + i * LDV) =
-            make_uint4(ok ? o.x : 0u, ok ? o.y : 0u, ok ? o.z : 0u, ok ? o.w : 0u);
+        vo[i] = make_uint4(ok ? o.x : 0u, ok ? o.y : 0u, ok ? o.z : 0u, ok ? o.w : 0u);
       }
     };
+    auto stage_fv = [&]() __attribute__((always_inline)) {
+      if (!fv_thread) return;
+      _Float16* vd = sV + (VT * fvtb) * LDV + 8 * fvdb;
+#pragma unroll
+      for (int i = 0; i < VT; ++i) *reinterpret_cast<uint4*>(vd + i * LDV) = vo[i];
+    };
 
-    // Waves 2-3 (inverses; fused v conv and gates after M) and 4-7 (tiles,
-    // K/Q staging) run separate loops with the same barrier sequence.  Staging
-    // and prefetches run unconditionally, also for chunks past the end (their
+    // Waves 4-5 (inverses), 6-9 (tiles, K/Q staging) and 10-11 (fused v conv,
+    // gates) run separate loops with the same barrier sequence.  Staging and
+    // prefetches run unconditionally, also for chunks past the end (their
     // loads are masked off or clamped and their LDS targets are free): a
     // skipped consumer would leave the prefetch registers "maybe pending" at
     // the loop head, and the next prefetch would then wait for every load in
     // flight.
     if (sw < 2) {
-      if (wave == 2) {
+      lds_barrier();  // P0
+      inv_first(0);
+      inv_second(0);
+      lds_barrier();  // B(0)
+      for (int64_t c = 0; c < nchunks; ++c) {
+        if (c + 1 < nchunks) inv_first(c + 1);
+        lds_barrier();  // M(c)
+        if (c + 1 < nchunks) inv_second(c + 1);
+        lds_barrier();  // B(c+1)
+      }
+    } else if (sw >= 6) {
+      if (wave == kGateWave) {
         prefetch_g(0);
         stage_g(0);
         prefetch_g(1);
@@ -798,29 +774,29 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       }
       if constexpr (FUSED) {
         prefetch_fv(0);
-        conv_stage_v(0);
+        conv_v(0);
+        stage_fv();
         prefetch_fv(1);
       }
       lds_barrier();  // P0
-      solve(0);
       lds_barrier();  // B(0)
       for (int64_t c = 0; c < nchunks; ++c) {
-        if (c + 1 < nchunks) solve(c + 1);
+        if constexpr (FUSED) conv_v(c + 1);
         lds_barrier();  // M(c)
         if constexpr (FUSED) {
-          conv_stage_v(c + 1);
+          stage_fv();
           prefetch_fv(c + 2);
         }
-        if (wave == 2) {
+        if (wave == kGateWave) {
           stage_g(c + 2);
           prefetch_g(c + 3);
         }
         lds_barrier();  // B(c+1)
       }
     } else {
-      const int st = tid - 256;       // staging thread index (waves 4-7)
+      const int st = tid - 384;       // staging thread index (waves 6-9)
       const bool kq_thread = st >= 0 && st < KBLK;
-      const bool v_thread = !FUSED && st >= 128;  // two-step path, waves 6, 7: 4 tokens x 8 columns of V
+      const bool v_thread = !FUSED && st >= 128;  // two-step path, waves 8, 9: 4 tokens x 8 columns of V
       // K/Q block: 16-byte column block fastest (conflict-free 16-byte LDS writes)
       const int ktb = st / DB, kdb = st % DB;
       const int vtb = (st - 128) >> 3, vdb = (st - 128) & 7;
@@ -857,9 +833,9 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
           _Float16* kd = sK + (ck % 3) * kC * LDK + (4 * ktb) * LDK + 8 * kdb;
           _Float16* qd = sQ + (ck & 1) * kC * LDQ + (4 * ktb) * LDQ + 8 * kdb;
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            *reinterpret_cast<uint4*>(kd + u * LDK) = to_f16x8<IOT>(pk[u]);
-            *reinterpret_cast<uint4*>(qd + u * LDQ) = to_f16x8<IOT>(pq[u]);
+          for (int u = 0; u < 4; ++u) {  // (fused: q and k arrive as f16 operands)
+            *reinterpret_cast<uint4*>(kd + u * LDK) = FUSED ? pk[u] : to_f16x8<IOT>(pk[u]);
+            *reinterpret_cast<uint4*>(qd + u * LDQ) = FUSED ? pq[u] : to_f16x8<IOT>(pq[u]);
           }
         }
       };
@@ -880,15 +856,17 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       stage_kq(1);
       prefetch_kq(2);
       lds_barrier();  // P0
-      solve(0);
+      tiles(0, false);
+      tiles(0, true);
       lds_barrier();  // B(0)
       for (int64_t c = 0; c < nchunks; ++c) {
-        if (c + 1 < nchunks) solve(c + 1);
+        if (c + 1 < nchunks) tiles(c + 1, false);
         lds_barrier();  // M(c)
         stage_v();
         stage_kq(c + 2);
         prefetch_kq(c + 3);
         prefetch_v(c + 2);
+        if (c + 1 < nchunks) tiles(c + 1, true);
         lds_barrier();  // B(c+1)
       }
     }
@@ -943,18 +921,16 @@ extern "C" int gdn_prefill_fused(const void* q, const void* k, const void* mixed
                                  const void* weight, int kernel_width, const void* cu_seqlens, int cu_dtype,
                                  int64_t num_seqs, int64_t total_tokens, int64_t H, int64_t HV, int64_t dk,
                                  int64_t dv, const void* conv_state, int64_t conv_slot_stride,
-                                 int64_t conv_layer_stride, const void* gate, int64_t gate_row_stride,
-                                 int64_t gate_head_stride, int gate_dtype, const void* beta, int64_t beta_row_stride,
-                                 int64_t beta_head_stride, int beta_dtype, const void* A_log, int a_dtype,
-                                 const void* dt_bias, int dt_dtype, void* state, int state_dtype,
+                                 int64_t conv_layer_stride, const float* g, const float* beta, void* state,
+                                 int state_dtype,
                                  int64_t slot_stride, int64_t layer_stride, int64_t head_stride, int64_t layer,
                                  const void* baseline_slots, int baseline_dtype, const void* chunk_write_slots,
                                  int chunk_write_dtype, const void* final_write_slots, int final_write_dtype,
                                  void* out, float scale, void* stream) {
   using namespace gdn;
   GDN_REQUIRE(num_seqs >= 1 && total_tokens >= 0 && H > 0 && HV > 0 && HV % H == 0, "gdn_prefill_fused: bad sizes");
-  GDN_REQUIRE(q && k && mixed && weight && cu_seqlens && conv_state && baseline_slots && gate && beta && A_log &&
-                  dt_bias && state && chunk_write_slots && out,
+  GDN_REQUIRE(q && k && mixed && weight && cu_seqlens && conv_state && baseline_slots && g && beta && state &&
+                  chunk_write_slots && out,
               "gdn_prefill_fused: null input");
   const bool covered = kernel_width == 4 && (io_dtype == GDN_BF16 || io_dtype == GDN_F16) && dv % 64 == 0 &&
                        (dk == 32 || dk == 64 || dk == 128) && row_stride % 8 == 0 && aligned16(mixed) &&
@@ -966,7 +942,7 @@ extern "C" int gdn_prefill_fused(const void* q, const void* k, const void* mixed
     return GDN_ERR_UNSUPPORTED;
   }
   ChunkParams p{};
-  p.q = q; p.k = k;
+  p.q = q; p.k = k; p.g = g; p.beta = beta;
   p.cu = cu_seqlens; p.cu_is64 = cu_dtype == GDN_I64;
   p.N = num_seqs; p.T = total_tokens; p.H = H; p.HV = HV; p.DV = dv;
   p.state = state; p.slot_stride = slot_stride; p.layer_stride = layer_stride; p.head_stride = head_stride;
@@ -981,8 +957,5 @@ extern "C" int gdn_prefill_fused(const void* q, const void* k, const void* mixed
   f.mixed = mixed; f.row_stride = row_stride; f.weight = weight;
   f.conv_state = conv_state; f.conv_slot_stride = conv_slot_stride; f.conv_layer_stride = conv_layer_stride;
   f.key_dim = H * dk;
-  f.gate = gate; f.gate_r = gate_row_stride; f.gate_h = gate_head_stride; f.gate_dtype = gate_dtype;
-  f.beta = beta; f.beta_r = beta_row_stride; f.beta_h = beta_head_stride; f.beta_dtype = beta_dtype;
-  f.A_log = A_log; f.a_dtype = a_dtype; f.dt_bias = dt_bias; f.dt_dtype = dt_dtype;
   return launch_chunk_chain_fused(p, dk, io_dtype, state_dtype, num_seqs * H, static_cast<hipStream_t>(stream));
 }

@@ -6,9 +6,8 @@
 
 namespace gdn {
 
-// Raw inputs of the prefill front end, for the chunk kernel variant that
-// computes conv + SiLU + q/k normalisation + gates itself (kernel/fused.py:53-117,
-// packed_conv.py:49-133) instead of reading q, k, v, g and beta.
+// Raw inputs of the v conv (packed_conv.py:49-133) for the chunk kernel
+// variant that computes its V tiles itself instead of reading v.
 struct FrontIn {
   const void* mixed;  // [T, conv_dim] projections, unit column stride
   int64_t row_stride;
@@ -16,16 +15,6 @@ struct FrontIn {
   const void* conv_state;  // [slots, layers, conv_dim, 3] conv history pool
   int64_t conv_slot_stride, conv_layer_stride;
   int64_t key_dim;  // H * d_k: q channels [0, key_dim), k, then v
-  const void* gate;
-  int64_t gate_r, gate_h;
-  int gate_dtype;
-  const void* beta;
-  int64_t beta_r, beta_h;
-  int beta_dtype;
-  const void* A_log;
-  int a_dtype;
-  const void* dt_bias;
-  int dt_dtype;
 };
 
 struct ChunkParams {
@@ -58,8 +47,8 @@ struct ChunkParams {
 // shapes or dtypes it does not cover, so the caller can use another kernel.
 int launch_chunk_chain(const ChunkParams& p, int64_t dk, int io_dtype, int state_dtype, int64_t groups,
                        hipStream_t stream);
-// The same kernel with the front end computed from p.front (conv width 4,
-// 16-byte aligned rows); p.q, p.k, p.v, p.g and p.beta are not read.
+// The same kernel with the V tiles computed from p.front (conv width 4,
+// 16-byte aligned rows) and q, k read as f16 operands; p.v is not read.
 int launch_chunk_chain_fused(const ChunkParams& p, int64_t dk, int io_dtype, int state_dtype, int64_t groups,
                              hipStream_t stream);
 

@@ -122,6 +122,17 @@ template <class IOT> __device__ __forceinline__ uint4 pack8_io(const float (&y)[
   return make_uint4(out_pack2<IOT>(y[0], y[1]), out_pack2<IOT>(y[2], y[3]), out_pack2<IOT>(y[4], y[5]),
                     out_pack2<IOT>(y[6], y[7]));
 }
+// 8 input halfs -> 8 f16 operand halfs (bf16 -> f16 is exact in range;
+// round-toward-zero saturates out-of-range values at +-65504).
+template <class IOT> __device__ __forceinline__ uint4 to_f16x8(uint4 raw);
+template <> __device__ __forceinline__ uint4 to_f16x8<f16>(uint4 raw) { return raw; }
+template <> __device__ __forceinline__ uint4 to_f16x8<bf16>(uint4 raw) {
+  auto cvt = [](uint32_t w) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(w << 16),
+                                                                   __uint_as_float(w & 0xffff0000u)));
+  };
+  return make_uint4(cvt(raw.x), cvt(raw.y), cvt(raw.z), cvt(raw.w));
+}
 template <int W> __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = W / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);

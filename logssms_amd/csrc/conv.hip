@@ -142,6 +142,7 @@ struct FrontParams {
   void* v_out;
   float* g_out;
   float* b_out;
+  int qk_f16;  // q_out / k_out as f16 MFMA operands (the bf16-rounded values, converted)
 };
 
 // grid: (token tiles, C / 256).  A 256-channel slab holds whole q/k heads
@@ -354,7 +355,8 @@ __global__ __launch_bounds__(256) void conv_vec_kernel(FrontParams fp) {
           for (int c = 0; c < 8; ++c) y[c] *= rn;
           T* dst = ch0 < key_dim ? static_cast<T*>(fp.q_out) + t * key_dim + ch0
                                  : static_cast<T*>(fp.k_out) + t * key_dim + ch0 - key_dim;
-          *reinterpret_cast<uint4*>(dst) = pack8_io<T>(y);
+          const uint4 packed = pack8_io<T>(y);
+          *reinterpret_cast<uint4*>(dst) = fp.qk_f16 ? to_f16x8<T>(packed) : packed;
         } else {
           *reinterpret_cast<uint4*>(static_cast<T*>(fp.v_out) + t * (fp.HV * fp.DV) + ch0 - 2 * key_dim) =
               pack8_io<T>(y);
@@ -677,11 +679,16 @@ extern "C" int gdn_prefill_qk(const void* mixed, int64_t row_stride, int io_dtyp
                               const void* cu_seqlens, int cu_dtype, int64_t num_seqs, int64_t total_tokens, int64_t H,
                               int64_t dk, const void* conv_state, int64_t conv_slot_stride, int64_t conv_layer_stride,
                               int64_t layer, const void* baseline_slots, int baseline_dtype, void* q_out, void* k_out,
-                              void* stream) {
+                              int out_dtype, int64_t HV, const void* gate, int64_t gate_row_stride,
+                              int64_t gate_head_stride, int gate_dtype, const void* beta, int64_t beta_row_stride,
+                              int64_t beta_head_stride, int beta_dtype, const void* A_log, int a_dtype,
+                              const void* dt_bias, int dt_dtype, float* g_out, float* beta_out, void* stream) {
   using namespace gdn;
-  GDN_REQUIRE(num_seqs >= 1 && total_tokens >= 0 && H > 0, "gdn_prefill_qk: bad sizes");
-  GDN_REQUIRE(mixed && weight && cu_seqlens && conv_state && baseline_slots && q_out && k_out,
+  GDN_REQUIRE(num_seqs >= 1 && total_tokens >= 0 && H > 0 && HV > 0, "gdn_prefill_qk: bad sizes");
+  GDN_REQUIRE(mixed && weight && cu_seqlens && conv_state && baseline_slots && q_out && k_out && gate && beta &&
+                  A_log && dt_bias && g_out && beta_out,
               "gdn_prefill_qk: null input");
+  GDN_REQUIRE(out_dtype == io_dtype || out_dtype == GDN_F16, "gdn_prefill_qk: out_dtype must be the io dtype or f16");
   auto al = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
   const bool covered = kernel_width == 4 && (io_dtype == GDN_BF16 || io_dtype == GDN_F16) &&
                        (dk == 32 || dk == 64 || dk == 128) && row_stride % 8 == 0 && al(mixed) && al(weight) &&
@@ -700,8 +707,13 @@ extern "C" int gdn_prefill_qk(const void* mixed, int64_t row_stride, int io_dtyp
   p.baseline = baseline_slots; p.baseline_is64 = baseline_dtype == GDN_I64;
   p.end0 = p.C; p.end1 = p.C; p.s0 = p.s1 = p.s2 = 1.f;
   FrontParams fp{};
-  fp.conv = p; fp.H = H; fp.HV = H; fp.DK = dk; fp.DV = dk;
-  fp.q_out = q_out; fp.k_out = k_out;  // no v_out, no gates: channels [0, 2 H dk) only
+  fp.conv = p; fp.H = H; fp.HV = HV; fp.DK = dk; fp.DV = 0;
+  fp.q_out = q_out; fp.k_out = k_out;  // no v_out: channels [0, 2 H dk) only
+  fp.qk_f16 = out_dtype == GDN_F16;
+  fp.gate = gate; fp.gate_r = gate_row_stride; fp.gate_h = gate_head_stride; fp.gate_dtype = gate_dtype;
+  fp.beta = beta; fp.beta_r = beta_row_stride; fp.beta_h = beta_head_stride; fp.beta_dtype = beta_dtype;
+  fp.A_log = A_log; fp.a_dtype = a_dtype; fp.dt_bias = dt_bias; fp.dt_dtype = dt_dtype;
+  fp.g_out = g_out; fp.b_out = beta_out;
   auto s = static_cast<hipStream_t>(stream);
   const int rc = io_dtype == GDN_BF16 ? launch_vec<bf16, true>(fp, static_cast<int>(dk), s)
                                       : launch_vec<f16, true>(fp, static_cast<int>(dk), s);

@@ -75,8 +75,8 @@ def prefill_fused(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, co
                   chunk_events=None):
     """``gdn.py:100-150`` in three launches: the q/k pass writes normalised
     q and k (their conv is shared by all the v heads and d_v slices of a key
-    head), the chunk kernel's staging waves compute the v conv + SiLU and
-    the gates of each 64-token chunk from ``mixed_qkv`` (no v/g/beta round
+    head) and the prepared gates, the chunk kernel's staging waves compute
+    the v conv + SiLU of each 64-token chunk from ``mixed_qkv`` (no v round
     trip through HBM), and the conv windows of ``snapshot_rows`` go to
     ``conv_state[snapshot_slots]`` last.  Conv history and initial state come
     from ``baseline_slots``; chunk-end states go to ``chunk_write_slots``.
@@ -101,8 +101,11 @@ def prefill_fused(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, co
     weight = conv_weight.contiguous()
     A_log = A_log.contiguous()
     dt_bias = dt_bias.contiguous()
-    q = torch.empty(T, config.num_k_heads, config.head_k_dim, device=mixed_qkv.device, dtype=mixed_qkv.dtype)
+    # q, k as the chunk kernel's f16 MFMA operands; prepared gates
+    q = torch.empty(T, config.num_k_heads, config.head_k_dim, device=mixed_qkv.device, dtype=torch.float16)
     k = torch.empty_like(q)
+    g = torch.empty(T, config.num_v_heads, device=mixed_qkv.device, dtype=torch.float32)
+    b = torch.empty_like(g)
     stream = _lib.stream_of(mixed_qkv)
     N = len(cu_seqlens) - 1
     try:
@@ -110,13 +113,17 @@ def prefill_fused(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, co
                   weight.data_ptr(), 4, cu_seqlens.data_ptr(), _lib.index_code(cu_seqlens), N, T,
                   config.num_k_heads, config.head_k_dim, conv_state.data_ptr(), conv_state.stride(0),
                   conv_state.stride(1), config.layer_idx, baseline_slots.data_ptr(), _lib.index_code(baseline_slots),
-                  q.data_ptr(), k.data_ptr(), stream)
+                  q.data_ptr(), k.data_ptr(), _lib.F16_CODE, config.num_v_heads,
+                  gate.data_ptr(), gate.stride(0), gate.stride(1), _lib.dtype_code(gate.dtype),
+                  beta.data_ptr(), beta.stride(0), beta.stride(1), _lib.dtype_code(beta.dtype),
+                  A_log.data_ptr(), _lib.dtype_code(A_log.dtype), dt_bias.data_ptr(), _lib.dtype_code(dt_bias.dtype),
+                  g.data_ptr(), b.data_ptr(), stream)
     except NotImplementedError:
         return None
     if chunk_events is not None:
         chunk_events[0].record()
-    prefill_chunk_fused(q, k, mixed_qkv, gate, beta, weight, A_log, dt_bias, config, conv_state, recurrent_state,
-                        cu_seqlens, baseline_slots, chunk_write_slots, out)
+    prefill_chunk_fused(q, k, g, b, mixed_qkv, weight, config, conv_state, recurrent_state, cu_seqlens,
+                        baseline_slots, chunk_write_slots, out)
     if chunk_events is not None:
         chunk_events[1].record()
     if snapshot_rows.numel():
@@ -128,20 +135,17 @@ def prefill_fused(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, co
     return out
 
 
-def prefill_chunk_fused(q, k, mixed_qkv, gate, beta, weight, A_log, dt_bias, config, conv_state, recurrent_state,
-                        cu_seqlens, baseline_slots, chunk_write_slots, out):
-    """The chunk-kernel launch of ``prefill_fused`` (q, k from the q/k pass;
-    v and the gates computed from ``mixed_qkv`` inside)."""
+def prefill_chunk_fused(q, k, g, b, mixed_qkv, weight, config, conv_state, recurrent_state, cu_seqlens,
+                        baseline_slots, chunk_write_slots, out):
+    """The chunk-kernel launch of ``prefill_fused`` (q, k, g, beta from the q/k
+    pass; v computed from ``mixed_qkv`` inside)."""
     T = mixed_qkv.shape[0]
     _lib.call(
         "gdn_prefill_fused",
         q.data_ptr(), k.data_ptr(), mixed_qkv.data_ptr(), mixed_qkv.stride(0), _lib.dtype_code(mixed_qkv.dtype),
         weight.data_ptr(), 4, cu_seqlens.data_ptr(), _lib.index_code(cu_seqlens), len(cu_seqlens) - 1, T,
         config.num_k_heads, config.num_v_heads, config.head_k_dim, config.head_v_dim,
-        conv_state.data_ptr(), conv_state.stride(0), conv_state.stride(1),
-        gate.data_ptr(), gate.stride(0), gate.stride(1), _lib.dtype_code(gate.dtype),
-        beta.data_ptr(), beta.stride(0), beta.stride(1), _lib.dtype_code(beta.dtype),
-        A_log.data_ptr(), _lib.dtype_code(A_log.dtype), dt_bias.data_ptr(), _lib.dtype_code(dt_bias.dtype),
+        conv_state.data_ptr(), conv_state.stride(0), conv_state.stride(1), g.data_ptr(), b.data_ptr(),
         recurrent_state.data_ptr(), _lib.dtype_code(recurrent_state.dtype), recurrent_state.stride(0),
         recurrent_state.stride(1), recurrent_state.stride(2), config.layer_idx,
         baseline_slots.data_ptr(), _lib.index_code(baseline_slots),

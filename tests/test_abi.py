@@ -97,11 +97,12 @@ def test_fused_prefill_reports_uncovered_shapes_without_launching():
     d = 0x10000  # 16-byte aligned dummy address
 
     def qk(width, dk, row_stride=8192):
-        return lib.gdn_prefill_qk(d, row_stride, 1, d, width, d, 1, 1, 64, 16, dk, d, 0, 0, 0, d, 1, d, d, None)
+        return lib.gdn_prefill_qk(d, row_stride, 1, d, width, d, 1, 1, 64, 16, dk, d, 0, 0, 0, d, 1, d, d, 2, 32,
+                                  d, 32, 1, 1, d, 32, 1, 1, d, 0, d, 0, d, d, None)
 
     def fused(width, dk, dv, row_stride=8192):
-        return lib.gdn_prefill_fused(d, d, d, row_stride, 1, d, width, d, 1, 1, 64, 16, 32, dk, dv, d, 0, 0, d, 32, 1,
-                                     1, d, 32, 1, 1, d, 0, d, 0, d, 0, 0, 0, 0, 0, d, 1, d, 1, None, 1, d, 0.1, None)
+        return lib.gdn_prefill_fused(d, d, d, row_stride, 1, d, width, d, 1, 1, 64, 16, 32, dk, dv, d, 0, 0, d, d, d,
+                                     0, 0, 0, 0, 0, d, 1, d, 1, None, 1, d, 0.1, None)
     assert qk(3, 128) == 2
     assert b"not covered" in lib.gdn_last_error()
     assert qk(4, 256) == 2
