@@ -288,9 +288,9 @@ def main():
         T = inp["T"]
         flops = FLOP_PER_TOKEN_HEAD * T * HV
         achieved = flops / (chunk_ms * 1e-3)
-        # HBM traffic of the fused chunk kernel (algorithmic): normalised q, k and the v columns of
-        # mixed_qkv in, the bf16 gate/beta projections in, o out, final states out
-        chunk_bytes = T * (2 * H * D + HV * D) * 2 + 2 * T * HV * 2 + T * HV * D * 2 + inp["N"] * S_BYTES
+        # HBM traffic of the fused chunk kernel (algorithmic): f16 q, k and the v columns of
+        # mixed_qkv in, prepared fp32 g/beta in, o out, final states out
+        chunk_bytes = T * (2 * H * D + HV * D) * 2 + 2 * T * HV * 4 + T * HV * D * 2 + inp["N"] * S_BYTES
         result.update(
             metric="GDN prefill tokens/s (Qwen3-Next layer, 4x4096 packed)",
             value=T / (ms * 1e-3),
