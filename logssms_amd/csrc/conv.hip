@@ -222,6 +222,23 @@ __global__ __launch_bounds__(kThreads) void frontend_kernel(FrontParams fp) {
 // lanes of the head with cross-lane shuffles (no LDS).
 constexpr int kVTok = 16;
 
+// Sum over aligned groups of L lanes, every lane of a group receiving the
+// group's sum, by DPP moves inside 16-lane rows (no LDS round trips): pair
+// swap, quad swap, half-row mirror, half-row rotation; 32 lanes add one
+// cross-row shuffle.  The additions pair up exactly as in the xor butterfly.
+template <int L> __device__ __forceinline__ float head_sum(float v) {
+  auto dpp = [](float x, auto ctrl) __attribute__((always_inline)) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), decltype(ctrl)::value, 0xf, 0xf, false));
+  };
+  if constexpr (L >= 2) v += dpp(v, std::integral_constant<int, 0xB1>{});   // quad_perm [1,0,3,2]
+  if constexpr (L >= 4) v += dpp(v, std::integral_constant<int, 0x4E>{});   // quad_perm [2,3,0,1]
+  if constexpr (L >= 8) v += dpp(v, std::integral_constant<int, 0x141>{});  // row_half_mirror
+  if constexpr (L >= 16) v += dpp(v, std::integral_constant<int, 0x128>{}); // row_ror:8
+  if constexpr (L >= 32) v += __shfl_xor(v, 16, 64);
+  static_assert(L <= 32, "at most 32 lanes per group");
+  return v;
+}
+
 // FRONT: fused front end (q/k normalised into q_out/k_out, v into v_out, history
 // from the pool); otherwise the plain packed conv into conv.out.
 template <class T, int W, int DK, bool FRONT>
@@ -346,11 +363,11 @@ __global__ __launch_bounds__(256) void conv_vec_kernel(FrontParams fp) {
       float ss = 0.f;
 #pragma unroll
       for (int c = 0; c < 8; ++c) ss = fmaf(y[c], y[c], ss);
-#pragma unroll
-      for (int off = 1; off < DK / 8; off <<= 1) ss += __shfl_xor(ss, off, 64);
+      ss = head_sum<DK / 8>(ss);
       if (active) {
         if (ch0 < 2 * key_dim) {
-          const float rn = rsqrtf(ss + 1e-6f);
+          // ss + 1e-6 is a normal float, so the hardware rsq needs no range scaling
+          const float rn = __builtin_amdgcn_rsqf(ss + 1e-6f);
 #pragma unroll
           for (int c = 0; c < 8; ++c) y[c] *= rn;
           T* dst = ch0 < key_dim ? static_cast<T*>(fp.q_out) + t * key_dim + ch0

@@ -186,7 +186,7 @@ def test_prepare_gdn_softplus_edges_and_empty():
 
 # ------------------------------------------------------------------ fused prefill front end
 
-@pytest.mark.parametrize("dk", [32, 64, 128])
+@pytest.mark.parametrize("dk", [32, 64, 128, 256])
 def test_prefill_frontend_matches_conv_then_prepare(dk):
     from logssms_amd.kernel.linear_attention.fused_backend import prefill_frontend
     g = gen(5 + dk)
