@@ -248,6 +248,21 @@ def verify_gpu(dev, B=64, T=8, slots=1024, seed=5):
     return step, commit
 
 
+def norm_gpu(dev, T=16384, seed=6):
+    """rms_norm_gated over the config 2 core output (T x HV rows of D channels)."""
+    from logssms_amd.kernel.norm import rms_norm_gated
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(T, HV, D, generator=g).to(torch.bfloat16).to(dev)
+    proj = torch.randn(T, 2 * HV * D, generator=g).to(torch.bfloat16).to(dev)
+    z = proj[:, HV * D:].view(T, HV, D)
+    w = torch.ones(D, device=dev)
+
+    def step():
+        rms_norm_gated(x, z, w, 1e-6)
+
+    return step, 3 * T * HV * D * 2
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -255,7 +270,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--only", choices=["all", "prefill", "decode", "verify", "copy"], default="all",
+    ap.add_argument("--only", choices=["all", "prefill", "decode", "verify", "norm", "copy"], default="all",
                     help="'copy' times a plain 512 MiB device copy (the calibration kernel for the "
                          "FETCH_SIZE / WRITE_SIZE counter passes)")
     args = ap.parse_args()
@@ -343,15 +358,22 @@ def main():
                            "frac_hbm": nb / (ms * 1e-3) / PEAK_HBM, "traffic": _traffic("fused_kernel_verify_cfg5"),
                            "commit_ms": cms, "commit_GB/s": cb / (cms * 1e-3) / 1e9,
                            "commit_traffic": _traffic("commit_kernel_cfg5")}
+    if args.only in ("all", "norm"):
+        step, nb = norm_gpu(dev)
+        ms = _time(step, max(args.steps, 20), args.warmup)
+        extra["rms_norm_gated"] = {"config": "config 2 core output: 16384 tokens x 32 v-heads x 128, bf16, "
+                                             "gate a column slice of a 2x wider projection output",
+                                   "ms": ms, "bytes": nb, "GB/s": nb / (ms * 1e-3) / 1e9,
+                                   "frac_hbm": nb / (ms * 1e-3) / PEAK_HBM}
     if not result:
-        key = "decode" if "decode" in extra else "verify"
+        key = "decode" if "decode" in extra else ("verify" if "verify" in extra else "rms_norm_gated")
         e = extra[key]
         result.update(metric=f"GDN {key} state-update GB/s", value=e["GB/s"], unit="GB/s", n_gpus=1,
                       steps=args.steps, warmup=args.warmup, ms_per_step=e["ms"], higher_is_better=True,
                       scaling="weak", vs_baseline=None, dtype="bf16 io / fp32 state", data="synthetic",
                       config={"workload": e["config"]},
                       roofline={"bound": "hbm", "achieved": e["GB/s"], "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                                "frac": e["frac_hbm"], "traffic": e["traffic"]})
+                                "frac": e["frac_hbm"], "traffic": e.get("traffic")})
     result["extra"] = extra
     print(json.dumps(result))
 

@@ -305,6 +305,26 @@ int gdn_commit_accepted(void* state, int64_t state_slot_stride_bytes, int64_t st
                         int64_t write_t_stride, int write_dtype, const void* accepted, int accepted_dtype,
                         int64_t batch, int64_t steps, void* stream);
 
+/* ------------------------------------------------------------------ output norm */
+
+/*
+ * Gated RMS normalisation of the core output, one row of `cols` channels at a
+ * time: out[r, c] = (x[r, c] * rsqrt(sum_c x[r, c]^2 / cols + eps)) * weight[c]
+ * * silu(gate(r, c)), computed in fp32 and stored in `dtype`.
+ * Replaces rms_norm_gated (python/logssms/kernel/norm.py:151-187) and its
+ * Triton kernel (:113-148), called by RMSNormGated.forward
+ * (python/logssms/layers/norm.py:42-53).
+ *   x, out: contiguous [rows, cols] of `dtype`.
+ *   gate(r, c) = gate[(r / gate_rows) * gate_group_stride
+ *                     + (r % gate_rows) * gate_row_stride + c * gate_col_stride]
+ *     (element strides of the reference's gate.reshape(-1, gate_rows, cols)).
+ *   weight: [cols] of `weight_dtype`.
+ */
+int gdn_rms_norm_gated(const void* x, int dtype, int64_t rows, int64_t cols, const void* gate, int gate_dtype,
+                       int64_t gate_rows, int64_t gate_group_stride, int64_t gate_row_stride,
+                       int64_t gate_col_stride, const void* weight, int weight_dtype, float eps, void* out,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

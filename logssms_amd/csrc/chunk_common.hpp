@@ -52,6 +52,5 @@ int launch_chunk_chain(const ChunkParams& p, int64_t dk, int io_dtype, int state
 int launch_chunk_chain_fused(const ChunkParams& p, int64_t dk, int io_dtype, int state_dtype, int64_t groups,
                              hipStream_t stream);
 
-inline bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
 }  // namespace gdn

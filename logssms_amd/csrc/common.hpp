@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <type_traits>
 
 #include "../../include/gdn_mi355x.h"
 
@@ -133,11 +134,32 @@ template <> __device__ __forceinline__ uint4 to_f16x8<bf16>(uint4 raw) {
   };
   return make_uint4(cvt(raw.x), cvt(raw.y), cvt(raw.z), cvt(raw.w));
 }
+// Sum over aligned groups of L lanes (L a power of two up to 64), every lane
+// of a group receiving the group's sum.  Inside a 16-lane row the moves are
+// DPP (no LDS round trip): pair swap, quad swap, half-row mirror, half-row
+// rotation; 32 and 64 lanes add cross-row shuffles.  The additions pair up
+// exactly as in the xor butterfly, so every lane holds the same bits.
+template <int L> __device__ __forceinline__ float head_sum(float v) {
+  static_assert(L >= 1 && L <= 64 && (L & (L - 1)) == 0, "a power of two up to 64 lanes");
+  auto dpp = [](float x, auto ctrl) __attribute__((always_inline)) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), decltype(ctrl)::value, 0xf, 0xf, false));
+  };
+  if constexpr (L >= 2) v += dpp(v, std::integral_constant<int, 0xB1>{});   // quad_perm [1,0,3,2]
+  if constexpr (L >= 4) v += dpp(v, std::integral_constant<int, 0x4E>{});   // quad_perm [2,3,0,1]
+  if constexpr (L >= 8) v += dpp(v, std::integral_constant<int, 0x141>{});  // row_half_mirror
+  if constexpr (L >= 16) v += dpp(v, std::integral_constant<int, 0x128>{}); // row_ror:8
+  if constexpr (L >= 32) v += __shfl_xor(v, 16, 64);
+  if constexpr (L >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
 template <int W> __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = W / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
   return v;
 }
+
+// ---------------------------------------------------------------- host helpers
+inline bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
 // ---------------------------------------------------------------- host errors
 void set_error(const char* fmt, ...);

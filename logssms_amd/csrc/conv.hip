@@ -222,22 +222,6 @@ __global__ __launch_bounds__(kThreads) void frontend_kernel(FrontParams fp) {
 // lanes of the head with cross-lane shuffles (no LDS).
 constexpr int kVTok = 16;
 
-// Sum over aligned groups of L lanes, every lane of a group receiving the
-// group's sum, by DPP moves inside 16-lane rows (no LDS round trips): pair
-// swap, quad swap, half-row mirror, half-row rotation; 32 lanes add one
-// cross-row shuffle.  The additions pair up exactly as in the xor butterfly.
-template <int L> __device__ __forceinline__ float head_sum(float v) {
-  auto dpp = [](float x, auto ctrl) __attribute__((always_inline)) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), decltype(ctrl)::value, 0xf, 0xf, false));
-  };
-  if constexpr (L >= 2) v += dpp(v, std::integral_constant<int, 0xB1>{});   // quad_perm [1,0,3,2]
-  if constexpr (L >= 4) v += dpp(v, std::integral_constant<int, 0x4E>{});   // quad_perm [2,3,0,1]
-  if constexpr (L >= 8) v += dpp(v, std::integral_constant<int, 0x141>{});  // row_half_mirror
-  if constexpr (L >= 16) v += dpp(v, std::integral_constant<int, 0x128>{}); // row_ror:8
-  if constexpr (L >= 32) v += __shfl_xor(v, 16, 64);
-  static_assert(L <= 32, "at most 32 lanes per group");
-  return v;
-}
 
 // FRONT: fused front end (q/k normalised into q_out/k_out, v into v_out, history
 // from the pool); otherwise the plain packed conv into conv.out.

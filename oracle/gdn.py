@@ -25,6 +25,13 @@ Pinning (what makes these functions trustworthy, see ``tests/test_oracle.py``):
   ``tests/layers/test_conv_decode.py:58-62``); window snapshots are compared
   bit-exactly with ``cat(history, x)[..., -3:]``.
 
+* ``rms_norm_gated`` -- ``torch.nn.functional.rms_norm`` and
+  ``torch.nn.functional.silu`` (library routines) in float64, the closed form
+  of ``tests/kernel/test_grouped_norm_gated.py:21-30`` (one group, norm before
+  the gate), and closed forms: a zero gate gives zero, a constant row ``c``
+  gives ``c / sqrt(c^2 + eps) * w * silu(z)``, positive row scaling leaves the
+  result unchanged (up to eps).
+
 Parity unpinned (documented, within tolerance only): the reference GPU path's
 intermediate bf16 roundings inside the chunk pipeline (A, W, U, h, v'
 stored in bf16 by ``chunk_fwd.py:319``, ``wy_fast.py:125-126``,
@@ -475,3 +482,20 @@ def single_pass_decode_output(state, q_hat, k_hat, v, g, beta, scale):
     decayed_q = math.exp(g) * (state * q_hat[:, None]).sum(0)
     delta = (v - decayed_k) * beta
     return scale * (decayed_q + delta * float((k_hat * q_hat).sum()))
+
+
+def rms_norm_gated(hidden_states, gate, weight, eps):
+    """``rms_norm_gated`` (``kernel/norm.py:151-187``; Triton kernel ``:113-148``):
+    per row of ``hidden_states.shape[-1]`` channels,
+    ``(x * rsqrt(sum(x^2) / n + eps)) * w * (z * sigmoid(z))`` in float32,
+    returned in the dtype of ``hidden_states``.  Row ``r`` of the flattened
+    hidden rows pairs with row ``r`` of ``gate.reshape(-1, n)``, as the
+    reference's ``gate.reshape(-1, gate.shape[-2], n)`` indexing does
+    (``:134-137``)."""
+    n = hidden_states.shape[-1]
+    assert hidden_states.shape == gate.shape and weight.numel() == n
+    x = hidden_states.reshape(-1, n).float()
+    z = gate.reshape(-1, n).float()
+    variance = (x * x).sum(-1, keepdim=True) / n
+    y = (x * torch.rsqrt(variance + eps)) * weight.float() * (z * torch.sigmoid(z))
+    return y.to(hidden_states.dtype).view(hidden_states.shape)

@@ -42,7 +42,8 @@ def test_header_declares_expected_entry_points():
     assert {"gdn_last_error", "gdn_abi_version", "gdn_chunk_gated_delta_rule", "gdn_fused_recurrent",
             "gdn_fused_conv_recurrent", "gdn_packed_causal_conv1d", "gdn_prepare", "gdn_prefill_frontend",
             "gdn_conv_decode", "gdn_store_state", "gdn_copy_rows", "gdn_zero_rows",
-            "gdn_commit_accepted", "gdn_prefill_qk", "gdn_prefill_fused", "gdn_conv_snapshots"} <= names
+            "gdn_commit_accepted", "gdn_prefill_qk", "gdn_prefill_fused", "gdn_conv_snapshots",
+            "gdn_rms_norm_gated"} <= names
 
 
 def test_ctypes_table_matches_header():
@@ -84,6 +85,12 @@ def test_invalid_arguments_report_errors_without_a_gpu():
     assert b"steps" in lib.gdn_last_error()
     # empty work is a no-op success
     assert lib.gdn_copy_rows(None, 0, None, 1, None, 0, None, 1, 0, 1, 16, 0, None) == 0
+    assert lib.gdn_rms_norm_gated(None, 1, 0, 128, None, 1, 32, 4096, 128, 1, None, 0, 1e-6, None, None) == 0
+    assert lib.gdn_rms_norm_gated(None, 1, 4, 0, None, 1, 32, 4096, 128, 1, None, 0, 1e-6, None, None) == 1
+    assert b"bad shape" in lib.gdn_last_error()
+    assert lib.gdn_rms_norm_gated(None, 7, 4, 128, None, 1, 32, 4096, 128, 1, None, 0, 1e-6, None, None) == 1
+    assert lib.gdn_rms_norm_gated(None, 1, 4, 128, None, 1, 32, 4096, 128, 1, None, 0, 1e-6, None, None) == 1
+    assert b"null" in lib.gdn_last_error()
 
 
 def test_fused_prefill_reports_uncovered_shapes_without_launching():

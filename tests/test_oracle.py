@@ -263,3 +263,38 @@ def test_verify_conv_matches_conv1d_and_unfold():
     torch.testing.assert_close(y, want, rtol=1e-12, atol=1e-12)
     unf = src.unfold(-1, W - 1, 1)[:, :, 1:].permute(0, 2, 1, 3)
     torch.testing.assert_close(windows, unf, rtol=0, atol=0)
+
+
+# ---------------------------------------------------------------- output norm
+
+def test_rms_norm_gated_matches_library_routines():
+    g = torch.Generator().manual_seed(40)
+    x = _normal(5, 3, 64, gen=g)
+    z = _normal(5, 3, 64 + 8, gen=g)[..., :64]  # strided gate view
+    w = _normal(64, gen=g)
+    got = gdn.rms_norm_gated(x, z, w, 1e-6)
+    want = F.rms_norm(x, (64,), eps=1e-6) * w * F.silu(z)
+    torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-6)
+    # the reference test's closed form (one group, norm before the gate; tests/kernel/test_grouped_norm_gated.py)
+    variance = x.square().mean(-1, keepdim=True)
+    torch.testing.assert_close(got, x * torch.rsqrt(variance + 1e-6) * w * F.silu(z), rtol=1e-5, atol=1e-6)
+
+
+def test_rms_norm_gated_closed_forms():
+    g = torch.Generator().manual_seed(41)
+    w = _normal(16, gen=g)
+    z = _normal(4, 16, gen=g)
+    # a zero gate zeroes the row (silu(0) = 0, not sigmoid(0) = 1/2)
+    x = _normal(4, 16, gen=g)
+    assert torch.equal(gdn.rms_norm_gated(x, torch.zeros_like(z), w, 1e-5), torch.zeros_like(x))
+    # a constant row c: c / sqrt(c^2 + eps) * w * silu(z) (eps inside the root)
+    for c in (1e-3, -0.5, 2.0):
+        xc = torch.full((4, 16), c, dtype=torch.float64)
+        want = c / math.sqrt(c * c + 1e-5) * w * z * torch.sigmoid(z)
+        torch.testing.assert_close(gdn.rms_norm_gated(xc, z, w, 1e-5), want, rtol=1e-5, atol=1e-7)
+    # positive row scaling cancels (eps = 0); rows stay paired with their own gate rows
+    scale = torch.tensor([0.5, 3.0, 7.0, 0.1], dtype=torch.float64)[:, None]
+    torch.testing.assert_close(gdn.rms_norm_gated(x * scale, z, w, 0.0), gdn.rms_norm_gated(x, z, w, 0.0),
+                               rtol=1e-5, atol=1e-6)
+    swapped = gdn.rms_norm_gated(x, z.flip(0), w, 1e-5)
+    assert not torch.allclose(swapped, gdn.rms_norm_gated(x, z, w, 1e-5))
