@@ -246,7 +246,7 @@ __device__ __forceinline__ void run_steps(const RecParams& p, Smem& s, float (&s
     for (int i = 0; i < RPT; ++i) {
       const float kr = kn[rg + RG * i];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) st[i][c] = fmaf(d, st[i][c], kr * dl[c]);
+      for (int c = 0; c < 4; ++c) st[i][c] = fmaf(kr, dl[c], d * st[i][c]);
     }
     // per-step state writes (verify / plain mode)
     ST* dst = nullptr;
