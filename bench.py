@@ -117,6 +117,42 @@ def make_prefill(seed=2, lengths=(4096, 4096, 4096, 4096)):
                 conv_tokens=conv_tokens, snap_rows=snap_rows, snap_slots=torch.arange(N, dtype=torch.int64), N=N, T=T)
 
 
+def make_prefill_cfg4(seed=4, n=64, median=1500, sigma=1.0, every=1024, hit_rate=0.5):
+    """64 packed sequences with lognormal lengths (median
+    1500, sigma 1.0, clipped to 16..16384); half of them (seeded choice)
+    start from a cached state and conv history in a random pool slot
+    (state ~N(0, 0.1), conv ~N(0, 1)); a checkpoint (state + conv window) is
+    written to a fresh slot at every multiple of 1024 tokens below the length
+    and at the length."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    lengths = np.clip(np.rint(rng.lognormal(np.log(median), sigma, n)), 16, 16384).astype(int).tolist()
+    inp = make_prefill(seed, lengths)
+    N, T = inp["N"], inp["T"]
+    hits = rng.permutation(N)[: int(round(hit_rate * N))]
+    nck = sum(len(range(every, m, every)) + 1 for m in lengths)
+    slots = rng.permutation(len(hits) + nck + 8)
+    baseline = torch.full((N,), -1, dtype=torch.int64)
+    baseline[torch.as_tensor(hits)] = torch.as_tensor(slots[: len(hits)], dtype=torch.int64)
+    fresh = iter(slots[len(hits):].tolist())
+    nchunks = [(m + C - 1) // C for m in lengths]
+    chunk_write = torch.full((sum(nchunks),), -1, dtype=torch.int64)
+    rows, snap_slots = [], []
+    c0 = t0 = 0
+    for m, nc in zip(lengths, nchunks):
+        for end in list(range(every, m, every)) + [m]:
+            slot = next(fresh)
+            chunk_write[c0 + (end - 1) // C] = slot
+            rows.append(t0 + end - 1)
+            snap_slots.append(slot)
+        c0 += nc
+        t0 += m
+    inp.update(baseline=baseline, chunk_write=chunk_write, snap_rows=torch.tensor(rows),
+               snap_slots=torch.tensor(snap_slots), slots=len(slots), random_pools=seed, lengths=lengths,
+               checkpoints=len(rows))
+    return inp
+
+
 def prefill_gpu(inp, dev, events=None, fused=True):
     """One backend prefill step.  fused: ``prefill_fused`` (q/k pass, then the
     chunk kernel computing the v conv + SiLU and the gates itself, then the
@@ -127,8 +163,13 @@ def prefill_gpu(inp, dev, events=None, fused=True):
     from logssms_amd.kernel.linear_attention.fused_backend import prefill_frontend, prefill_fused
     cfg = _config()
     d = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
-    conv_pool = torch.zeros(max(8, d["N"]), 1, CONV_DIM, W - 1, device=dev, dtype=torch.bfloat16)
-    state_pool = torch.zeros(max(8, d["N"]), 1, HV, D, D, device=dev, dtype=torch.float32)
+    slots = d.get("slots", max(8, d["N"]))
+    conv_pool = torch.zeros(slots, 1, CONV_DIM, W - 1, device=dev, dtype=torch.bfloat16)
+    state_pool = torch.zeros(slots, 1, HV, D, D, device=dev, dtype=torch.float32)
+    if d.get("random_pools") is not None:  # cached states / conv histories of the prefix hits
+        gd = torch.Generator(device=dev).manual_seed(int(d["random_pools"]))
+        state_pool.normal_(0.0, 0.1, generator=gd)
+        conv_pool.copy_(torch.randn(conv_pool.shape, device=dev, generator=gd).to(torch.bfloat16))
     out = torch.empty(1, d["T"], HV, D, device=dev, dtype=torch.bfloat16)
     io = ChunkStateIO(state_pool, d["baseline"], d["chunk_write"], layer=0)
 
@@ -339,6 +380,23 @@ def main():
                           f"tokens of sequence 0 at full head count; median of {len(times)} runs",
             }
             torch.set_num_threads(threads)
+        del step, inp
+        torch.cuda.empty_cache()
+        inp4 = make_prefill_cfg4()
+        ev4 = []
+        step4, _, _ = prefill_gpu(inp4, dev, ev4)
+        ms4 = _time(step4, max(args.steps // 2, 5), args.warmup, ev4)
+        chunk4 = _kernel_ms(ev4)
+        flops4 = FLOP_PER_TOKEN_HEAD * inp4["T"] * HV
+        extra["prefill_cfg4"] = {
+            "config": "BASELINE config 4: 64 seqs, lognormal lengths (median 1500, sigma 1.0, seed 4), "
+                      "half from cached pool states + conv histories, checkpoints every 1024 tokens and at the end",
+            "tokens": inp4["T"], "max_len": max(inp4["lengths"]), "checkpoints": inp4["checkpoints"],
+            "ms": ms4, "tokens/s": inp4["T"] / (ms4 * 1e-3), "chunk_kernel_ms": chunk4,
+            "chunk_tflops": flops4 / (chunk4 * 1e-3) / 1e12, "frac_mfma": flops4 / (chunk4 * 1e-3) / PEAK_MFMA_16BIT,
+            "checkpoint_bytes": inp4["checkpoints"] * (S_BYTES + SC_BYTES)}
+        del step4, inp4
+        torch.cuda.empty_cache()
 
     if args.only in ("all", "decode"):
         step = decode_gpu(dev)
