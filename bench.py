@@ -13,8 +13,10 @@ the algorithmic flop count (10 C d + 6 d^2 + 2/3 C^2 per token per v-head).
 ``extra.prefill_two_step_ms`` times the unfused path (``prefill_frontend``
 then the chunk kernel) on the same inputs.
 
-``extra`` reports the HBM-bound paths: decode (config 3) and spec-decode
-verify (config 5) in GB/s against 8 TB/s, from the canonical byte formulas.
+``extra`` reports the varlen prefill with prefix-cache hits and checkpoints
+(config 4), and the HBM-bound paths: decode (config 3), spec-decode verify
+(config 5) and the gated RMS norm of the config 2 output, in GB/s against
+8 TB/s, from the canonical byte formulas.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 """
@@ -394,7 +396,8 @@ def main():
             "tokens": inp4["T"], "max_len": max(inp4["lengths"]), "checkpoints": inp4["checkpoints"],
             "ms": ms4, "tokens/s": inp4["T"] / (ms4 * 1e-3), "chunk_kernel_ms": chunk4,
             "chunk_tflops": flops4 / (chunk4 * 1e-3) / 1e12, "frac_mfma": flops4 / (chunk4 * 1e-3) / PEAK_MFMA_16BIT,
-            "checkpoint_bytes": inp4["checkpoints"] * (S_BYTES + SC_BYTES)}
+            "checkpoint_bytes": inp4["checkpoints"] * (S_BYTES + SC_BYTES),
+            "chunk_traffic": _traffic("chunk_chain_kernel_fused_cfg4")}
         del step4, inp4
         torch.cuda.empty_cache()
 
@@ -422,7 +425,7 @@ def main():
         extra["rms_norm_gated"] = {"config": "config 2 core output: 16384 tokens x 32 v-heads x 128, bf16, "
                                              "gate a column slice of a 2x wider projection output",
                                    "ms": ms, "bytes": nb, "GB/s": nb / (ms * 1e-3) / 1e9,
-                                   "frac_hbm": nb / (ms * 1e-3) / PEAK_HBM}
+                                   "frac_hbm": nb / (ms * 1e-3) / PEAK_HBM, "traffic": _traffic("norm_vec_kernel_cfg2")}
     if not result:
         key = "decode" if "decode" in extra else ("verify" if "verify" in extra else "rms_norm_gated")
         e = extra[key]
