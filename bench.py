@@ -306,6 +306,43 @@ def norm_gpu(dev, T=16384, seed=6):
     return step, 3 * T * HV * D * 2
 
 
+def layer_gpu(dev, hidden=2048, seed=7):
+    """The whole GatedDeltaNet layer (Qwen3-Next shape, hidden 2048) on the
+    config 2 batch: merged projections (hipBLASLt GEMMs) whose column slices
+    feed the backend prefill as strided views, the gated RMS norm and the
+    output projection.  Returns (step, parts): parts times the three stages."""
+    from logssms_amd.cache import LinearStatePool
+    from logssms_amd.core import Batch, Context, Request, set_global_ctx
+    from logssms_amd.layers import GatedDeltaNet
+    g = torch.Generator(device=dev).manual_seed(seed)
+    net = GatedDeltaNet(hidden, H, HV, D, D, W, 1e-6, 0, device=dev, dtype=torch.bfloat16)
+    for t in (net.in_proj_qkvz_weight, net.in_proj_ba_weight, net.out_proj_weight):
+        t.normal_(0.0, 0.02, generator=g)
+    net.conv1d_weight.normal_(0.0, 0.02, generator=g)
+    net.A_log.uniform_(-1.0, 0.0, generator=g)
+    net.dt_bias.zero_()
+    lengths = [4096] * 4
+    pool = LinearStatePool(8, 1, CONV_DIM, W, HV, D, D, dev, torch.bfloat16)
+    table = torch.arange(8, device=dev, dtype=torch.int32)[:4, None].expand(4, 4096).contiguous()
+    ctx = Context(page_size=4096, linear_state=pool, state_table=table)
+    set_global_ctx(ctx)
+    batch = Batch(reqs=[Request(i, 0, n) for i, n in enumerate(lengths)], phase="prefill")
+    ctx.batch = batch
+    ctx.linear_attn_backend.prepare_metadata(batch)
+    x = torch.randn(sum(lengths), hidden, device=dev, generator=g).to(torch.bfloat16)
+
+    def step():
+        return net.forward(x)
+
+    def parts():
+        mixed, z, beta, gate = net.proj(x)
+        core = net.attend(mixed, beta, gate)
+        return {"proj": lambda: net.proj(x), "core": lambda: net.attend(mixed, beta, gate),
+                "output": lambda: net.output(core, z)}
+
+    return step, parts
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -313,7 +350,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--only", choices=["all", "prefill", "decode", "verify", "norm", "copy"], default="all",
+    ap.add_argument("--only", choices=["all", "prefill", "decode", "verify", "norm", "layer", "copy"],
+                    default="all",
                     help="'copy' times a plain 512 MiB device copy (the calibration kernel for the "
                          "FETCH_SIZE / WRITE_SIZE counter passes)")
     args = ap.parse_args()
@@ -426,10 +464,25 @@ def main():
                                              "gate a column slice of a 2x wider projection output",
                                    "ms": ms, "bytes": nb, "GB/s": nb / (ms * 1e-3) / 1e9,
                                    "frac_hbm": nb / (ms * 1e-3) / PEAK_HBM, "traffic": _traffic("norm_vec_kernel_cfg2")}
+    if args.only in ("all", "layer"):
+        step, parts = layer_gpu(dev)
+        ms = _time(step, max(args.steps // 2, 5), args.warmup)
+        stages = {k: _time(fn, max(args.steps // 2, 5), args.warmup) for k, fn in parts().items()}
+        T = 4 * 4096
+        extra["gated_delta_layer"] = {
+            "config": "GatedDeltaNet layer, hidden 2048, config 2 batch (4 x 4096): in_proj_qkvz/in_proj_ba GEMMs, "
+                      "GDN prefill on their strided column slices, gated RMS norm, out_proj GEMM",
+            "ms": ms, "tokens/s": T / (ms * 1e-3), "stage_ms": stages}
+        del step, parts
+        torch.cuda.empty_cache()
     if not result:
-        key = "decode" if "decode" in extra else ("verify" if "verify" in extra else "rms_norm_gated")
+        keys = [k for k in ("decode", "verify", "rms_norm_gated") if k in extra]
+        if not keys:  # --only layer
+            print(json.dumps({"extra": extra}))
+            return
+        key = keys[0]
         e = extra[key]
-        result.update(metric=f"GDN {key} state-update GB/s", value=e["GB/s"], unit="GB/s", n_gpus=1,
+        result.update(metric=f"GDN {key} GB/s", value=e["GB/s"], unit="GB/s", n_gpus=1,
                       steps=args.steps, warmup=args.warmup, ms_per_step=e["ms"], higher_is_better=True,
                       scaling="weak", vs_baseline=None, dtype="bf16 io / fp32 state", data="synthetic",
                       config={"workload": e["config"]},

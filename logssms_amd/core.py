@@ -69,6 +69,7 @@ class Context:
     linear_state: Any = None
     state_table: torch.Tensor | None = None
     work_state_table: torch.Tensor | None = None
+    batch: Any = None  # the batch being run (GatedDeltaNet.attend reads it)
     _backend: Any = field(default=None, repr=False)
 
     @property
