@@ -305,6 +305,31 @@ int gdn_commit_accepted(void* state, int64_t state_slot_stride_bytes, int64_t st
                         int64_t write_t_stride, int write_dtype, const void* accepted, int accepted_dtype,
                         int64_t batch, int64_t steps, void* stream);
 
+/* ------------------------------------------------------------------ graph metadata */
+
+/*
+ * Batched copy of `fields` small integer tensors in one launch:
+ * dsts[i][j * dst_strides[i]] = srcs[i][j * src_strides[i]] for j < lengths[i]
+ * (elem_sizes[i] bytes per element: 1, 2, 4 or 8; strides in elements).
+ * The pointer and size tables are host arrays read at the call.  Replaces
+ * copy_metadata (python/logssms/kernel/metadata.py:108-134), which
+ * MixedLinearCopyPlan uses to refresh captured metadata before a replay
+ * (layers/linear_attention_backend/mixed.py:127-197).
+ */
+int gdn_metadata_copy(const void* const* srcs, void* const* dsts, const int64_t* lengths, const int64_t* src_strides,
+                      const int64_t* dst_strides, const int* elem_sizes, int fields, void* stream);
+
+/*
+ * Batched padding of contiguous integer tensors to fixed capacities in one
+ * launch: dsts[i][j] = srcs[i][j] for j < lengths[i]; for lengths[i] <= j <
+ * capacities[i] the value fills[i], or, when tails[i] >= 0 (a flattened pair
+ * table), 0 at even and tails[i] at odd positions.  Replaces pad_metadata
+ * (python/logssms/kernel/metadata.py:137-150), used by
+ * prepare_mixed_linear_metadata (layers/linear_attention_backend/mixed.py:23-120).
+ */
+int gdn_metadata_pad(const void* const* srcs, void* const* dsts, const int64_t* lengths, const int64_t* capacities,
+                     const int64_t* fills, const int64_t* tails, const int* elem_sizes, int fields, void* stream);
+
 /* ------------------------------------------------------------------ output norm */
 
 /*

@@ -33,14 +33,40 @@ class MarconiCacheMetadata:
 @dataclass
 class Batch:
     reqs: list[Request]
-    phase: Literal["prefill", "decode", "verify"]
+    phase: Literal["prefill", "decode", "verify", "mixed"]
     padded_reqs: list[Request] | None = None
     cache_metadata: Any = None
     linear_attn_metadata: Any = None
+    # mixed batches (core.py:117-127): the prefill requests first, then the decode
+    # ones; mixed_parts = (prefill batch, decode batch); the prefill inputs take
+    # prefill_token_capacity rows (0: exactly the prefill tokens)
+    num_prefill_reqs: int = 0
+    mixed_parts: tuple | None = None
+    prefill_token_capacity: int = 0
 
     def __post_init__(self):
         if self.padded_reqs is None:
             self.padded_reqs = self.reqs
+
+    @property
+    def is_mixed(self) -> bool:
+        return self.phase == "mixed"
+
+    @property
+    def prefill_count(self) -> int:
+        return self.size if self.is_prefill else self.num_prefill_reqs
+
+    @property
+    def prefill_reqs(self) -> list[Request]:
+        return self.reqs[:self.prefill_count]
+
+    @property
+    def decode_reqs(self) -> list[Request]:
+        return self.reqs[self.prefill_count:] if not self.is_verify else []
+
+    @property
+    def prefill_tokens(self) -> int:
+        return sum(req.extend_len for req in self.prefill_reqs)
 
     @property
     def is_prefill(self) -> bool:

@@ -27,6 +27,15 @@ __device__ __forceinline__ int64_t find_sequence(const void* cu, int cu_is64, in
   return lo;
 }
 
+// End of the packed tokens, cu[N]: rows at or past it (the padding of a
+// fixed-capacity input) belong to no sequence and are neither read nor written.
+__device__ __forceinline__ int64_t tile_end(const void* cu, int cu_is64, int64_t n, int64_t rows, int64_t t0,
+                                            int64_t tile) {
+  const int64_t packed = load_index(cu, n, cu_is64);
+  const int64_t lim = packed < rows ? packed : rows;
+  return t0 + tile < lim ? t0 + tile : lim;
+}
+
 struct ConvParams {
   const void* x;
   int64_t xr, xc;
@@ -118,7 +127,8 @@ __global__ __launch_bounds__(kThreads) void packed_conv_kernel(ConvParams p) {
   const int64_t ch = static_cast<int64_t>(blockIdx.y) * kThreads + threadIdx.x;
   if (ch >= p.C) return;
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kTile;
-  const int64_t t1 = t0 + kTile < p.T ? t0 + kTile : p.T;
+  const int64_t t1 = tile_end(p.cu, p.cu_is64, p.N, p.T, t0, kTile);
+  if (t0 >= t1) return;
   T* out = static_cast<T*>(p.out);
   conv_channel<T>(p, ch, t0, t1, [&](int64_t t, float y) { out[t * p.C + ch] = from_f32<T>(y); });
 }
@@ -153,7 +163,8 @@ __global__ __launch_bounds__(kThreads) void frontend_kernel(FrontParams fp) {
   const ConvParams& p = fp.conv;
   const int64_t ch = static_cast<int64_t>(blockIdx.y) * kThreads + threadIdx.x;
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kTile;
-  const int64_t t1 = t0 + kTile < p.T ? t0 + kTile : p.T;
+  const int64_t t1 = tile_end(p.cu, p.cu_is64, p.N, p.T, t0, kTile);
+  if (t0 >= t1) return;  // whole block: padding rows only
   const int n = static_cast<int>(t1 - t0);
   const int64_t key_dim = fp.H * DK;
   const bool active = ch < p.C;
@@ -232,7 +243,8 @@ __global__ __launch_bounds__(256) void conv_vec_kernel(FrontParams fp) {
   const int64_t ch0 = (static_cast<int64_t>(blockIdx.y) * 256 + threadIdx.x) * 8;
   const bool active = ch0 < p.C;
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kVTok;
-  const int64_t t1 = t0 + kVTok < p.T ? t0 + kVTok : p.T;
+  const int64_t t1 = tile_end(p.cu, p.cu_is64, p.N, p.T, t0, kVTok);
+  if (t0 >= t1) return;  // whole block: padding rows only
   const int64_t key_dim = FRONT ? fp.H * DK : 0;
   float w[W][8], bias[8];
   float win[S > 0 ? S : 1][8];

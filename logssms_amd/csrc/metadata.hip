@@ -1,0 +1,143 @@
+// Batched metadata copies for fixed-capacity graph replay: one launch moves a
+// group of small index tensors (python/logssms/kernel/metadata.py:77-150,
+// copy_metadata / pad_metadata, used by the mixed prefill/decode graph
+// buckets of layers/linear_attention_backend/mixed.py).
+//
+// Roofline: launch latency.  A group holds a few hundred to a few thousand
+// indices; one launch per group replaces one copy_/fill_ launch per tensor.
+// The field table travels in the kernel arguments, so a captured graph
+// replays the same pointers.
+#include "common.hpp"
+
+namespace gdn {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxFields = 16;
+
+struct Field {
+  const char* src;
+  char* dst;
+  int64_t length;    // source elements
+  int64_t capacity;  // destination elements (pad) or = length (copy)
+  int64_t src_stride, dst_stride;  // in elements (copy)
+  int64_t fill, tail;              // pad values
+  int elem;                        // bytes per element: 1, 2, 4 or 8
+};
+
+struct FieldTable {
+  Field f[kMaxFields];
+};
+
+__device__ __forceinline__ int64_t load_int(const char* p, int elem) {
+  switch (elem) {
+    case 8: return *reinterpret_cast<const int64_t*>(p);
+    case 4: return *reinterpret_cast<const int32_t*>(p);
+    case 2: return *reinterpret_cast<const int16_t*>(p);
+    default: return *reinterpret_cast<const int8_t*>(p);
+  }
+}
+__device__ __forceinline__ void store_int(char* p, int elem, int64_t v) {
+  switch (elem) {
+    case 8: *reinterpret_cast<int64_t*>(p) = v; break;
+    case 4: *reinterpret_cast<int32_t*>(p) = static_cast<int32_t>(v); break;
+    case 2: *reinterpret_cast<int16_t*>(p) = static_cast<int16_t>(v); break;
+    default: *reinterpret_cast<int8_t*>(p) = static_cast<int8_t>(v); break;
+  }
+}
+
+// grid (element blocks, fields): dst[i * dst_stride] = src[i * src_stride], i < length.
+__global__ __launch_bounds__(kThreads) void metadata_copy_kernel(FieldTable t) {
+  const Field& f = t.f[blockIdx.y];
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= f.length) return;
+  store_int(f.dst + i * f.dst_stride * f.elem, f.elem, load_int(f.src + i * f.src_stride * f.elem, f.elem));
+}
+
+// grid (element blocks, fields): dst[i] = src[i] for i < length; beyond it the
+// fill value, or for a pair table (tail >= 0) the pair (0, tail).
+__global__ __launch_bounds__(kThreads) void metadata_pad_kernel(FieldTable t) {
+  const Field& f = t.f[blockIdx.y];
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= f.capacity) return;
+  int64_t v;
+  if (i < f.length) v = load_int(f.src + i * f.elem, f.elem);
+  else v = f.tail >= 0 ? (i % 2 == 1 ? f.tail : 0) : f.fill;
+  store_int(f.dst + i * f.elem, f.elem, v);
+}
+
+int launch_fields(bool pad, const Field* fields, int n, hipStream_t s) {
+  for (int base = 0; base < n; base += kMaxFields) {
+    const int m = n - base < kMaxFields ? n - base : kMaxFields;
+    FieldTable t{};
+    int64_t most = 0;
+    for (int j = 0; j < m; ++j) {
+      t.f[j] = fields[base + j];
+      const int64_t count = pad ? t.f[j].capacity : t.f[j].length;
+      most = count > most ? count : most;
+    }
+    if (most == 0) continue;
+    const int64_t blocks = (most + kThreads - 1) / kThreads;
+    GDN_REQUIRE(blocks <= 0x7fffffff, "metadata: too many elements");
+    if (pad)
+      hipLaunchKernelGGL(metadata_pad_kernel, dim3(static_cast<unsigned>(blocks), m), dim3(kThreads), 0, s, t);
+    else
+      hipLaunchKernelGGL(metadata_copy_kernel, dim3(static_cast<unsigned>(blocks), m), dim3(kThreads), 0, s, t);
+    const int rc = GDN_LAUNCH_CHECK(pad ? "gdn_metadata_pad launch" : "gdn_metadata_copy launch");
+    if (rc != GDN_OK) return rc;
+  }
+  return GDN_OK;
+}
+
+bool elem_ok(int e) { return e == 1 || e == 2 || e == 4 || e == 8; }
+
+}  // namespace
+}  // namespace gdn
+
+extern "C" int gdn_metadata_copy(const void* const* srcs, void* const* dsts, const int64_t* lengths,
+                                 const int64_t* src_strides, const int64_t* dst_strides, const int* elem_sizes,
+                                 int fields, void* stream) {
+  using namespace gdn;
+  GDN_REQUIRE(fields >= 0, "gdn_metadata_copy: negative field count");
+  if (fields == 0) return GDN_OK;
+  GDN_REQUIRE(srcs && dsts && lengths && src_strides && dst_strides && elem_sizes, "gdn_metadata_copy: null table");
+  Field table[64];
+  for (int base = 0; base < fields; base += 64) {
+    const int m = fields - base < 64 ? fields - base : 64;
+    for (int j = 0; j < m; ++j) {
+      const int i = base + j;
+      GDN_REQUIRE(elem_ok(elem_sizes[i]) && lengths[i] >= 0, "gdn_metadata_copy: field %d: bad size", i);
+      GDN_REQUIRE(lengths[i] == 0 || (srcs[i] && dsts[i]), "gdn_metadata_copy: field %d: null pointer", i);
+      table[j] = Field{static_cast<const char*>(srcs[i]), static_cast<char*>(dsts[i]), lengths[i], lengths[i],
+                       src_strides[i], dst_strides[i], 0, -1, elem_sizes[i]};
+    }
+    const int rc = launch_fields(false, table, m, static_cast<hipStream_t>(stream));
+    if (rc != GDN_OK) return rc;
+  }
+  return GDN_OK;
+}
+
+extern "C" int gdn_metadata_pad(const void* const* srcs, void* const* dsts, const int64_t* lengths,
+                                const int64_t* capacities, const int64_t* fills, const int64_t* tails,
+                                const int* elem_sizes, int fields, void* stream) {
+  using namespace gdn;
+  GDN_REQUIRE(fields >= 0, "gdn_metadata_pad: negative field count");
+  if (fields == 0) return GDN_OK;
+  GDN_REQUIRE(srcs && dsts && lengths && capacities && fills && tails && elem_sizes, "gdn_metadata_pad: null table");
+  Field table[64];
+  for (int base = 0; base < fields; base += 64) {
+    const int m = fields - base < 64 ? fields - base : 64;
+    for (int j = 0; j < m; ++j) {
+      const int i = base + j;
+      GDN_REQUIRE(elem_ok(elem_sizes[i]) && lengths[i] >= 0 && capacities[i] >= lengths[i],
+                  "gdn_metadata_pad: field %d: source longer than its capacity", i);
+      GDN_REQUIRE(capacities[i] == 0 || dsts[i], "gdn_metadata_pad: field %d: null destination", i);
+      GDN_REQUIRE(lengths[i] == 0 || srcs[i], "gdn_metadata_pad: field %d: null source", i);
+      table[j] = Field{static_cast<const char*>(srcs[i]), static_cast<char*>(dsts[i]), lengths[i], capacities[i],
+                       1, 1, fills[i], tails[i], elem_sizes[i]};
+    }
+    const int rc = launch_fields(true, table, m, static_cast<hipStream_t>(stream));
+    if (rc != GDN_OK) return rc;
+  }
+  return GDN_OK;
+}

@@ -1,6 +1,7 @@
 """Layer-level mirrors of ``logssms.layers`` for the GDN path."""
 
 from .gated_delta import GatedDeltaConfig, GatedDeltaNet
+from .linear_attention_mixed import MixedLinearCopyPlan, prepare_mixed_linear_metadata
 from .norm import RMSNormGated
 
-__all__ = ["GatedDeltaConfig", "GatedDeltaNet", "RMSNormGated"]
+__all__ = ["GatedDeltaConfig", "GatedDeltaNet", "MixedLinearCopyPlan", "RMSNormGated", "prepare_mixed_linear_metadata"]

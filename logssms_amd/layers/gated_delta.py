@@ -94,12 +94,16 @@ class GatedDeltaNet:
         return mixed_qkv, z, beta, gate
 
     def attend(self, mixed_qkv: torch.Tensor, beta: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
-        """``:107-131``: the backend of the global context on the context's batch."""
+        """``:107-131``: the backend of the global context on the context's batch
+        (a mixed batch through ``forward_mixed``)."""
         from ..core import get_global_ctx
 
         ctx = get_global_ctx()
-        if getattr(ctx.batch, "is_mixed", False):
-            raise NotImplementedError("mixed prefill/decode batches are not supported by this backend")
+        if ctx.batch.is_mixed:
+            return ctx.linear_attn_backend.forward_mixed(
+                ctx.batch, {"mixed_qkv": mixed_qkv, "gate": gate, "beta": beta},
+                conv_weight=self.conv1d_weight, A_log=self.A_log, dt_bias=self.dt_bias, config=self._config,
+            )
         return ctx.linear_attn_backend.forward(
             mixed_qkv=mixed_qkv, gate=gate, beta=beta, conv_weight=self.conv1d_weight, A_log=self.A_log,
             dt_bias=self.dt_bias, config=self._config, batch=ctx.batch,

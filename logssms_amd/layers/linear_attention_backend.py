@@ -239,6 +239,21 @@ class GatedDeltaBackend:
         self.capture.slots[:bs].copy_(metadata.slots)
 
     # ------------------------------------------------------------ forward
+    def forward_mixed(self, batch, token_inputs: dict[str, torch.Tensor], **kwargs) -> torch.Tensor:
+        """base.py:20-42: a mixed batch's prefill part (its first
+        ``prefill_token_capacity`` rows, or the prefill tokens) and decode part
+        (the remaining rows), each through ``forward`` into slices of one output."""
+        assert batch.mixed_parts is not None
+        split = batch.prefill_token_capacity or batch.prefill_tokens
+        example = next(iter(token_inputs.values()))
+        config = kwargs["config"]
+        output = torch.empty(len(example), config.num_v_heads, config.head_v_dim, dtype=example.dtype,
+                             device=example.device)
+        for part, begin, end in ((batch.mixed_parts[0], 0, split), (batch.mixed_parts[1], split, len(example))):
+            self.forward(**{name: tensor[begin:end] for name, tensor in token_inputs.items()}, **kwargs,
+                         batch=part, out=output[begin:end])
+        return output
+
     def forward(self, mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, batch, out=None):
         """gdn.py:20-49."""
         metadata = batch.linear_attn_metadata

@@ -43,7 +43,7 @@ def test_header_declares_expected_entry_points():
             "gdn_fused_conv_recurrent", "gdn_packed_causal_conv1d", "gdn_prepare", "gdn_prefill_frontend",
             "gdn_conv_decode", "gdn_store_state", "gdn_copy_rows", "gdn_zero_rows",
             "gdn_commit_accepted", "gdn_prefill_qk", "gdn_prefill_fused", "gdn_conv_snapshots",
-            "gdn_rms_norm_gated"} <= names
+            "gdn_rms_norm_gated", "gdn_metadata_copy", "gdn_metadata_pad"} <= names
 
 
 def test_ctypes_table_matches_header():
@@ -91,6 +91,10 @@ def test_invalid_arguments_report_errors_without_a_gpu():
     assert lib.gdn_rms_norm_gated(None, 7, 4, 128, None, 1, 32, 4096, 128, 1, None, 0, 1e-6, None, None) == 1
     assert lib.gdn_rms_norm_gated(None, 1, 4, 128, None, 1, 32, 4096, 128, 1, None, 0, 1e-6, None, None) == 1
     assert b"null" in lib.gdn_last_error()
+    assert lib.gdn_metadata_copy(None, None, None, None, None, None, 0, None) == 0  # nothing to move
+    assert lib.gdn_metadata_pad(None, None, None, None, None, None, None, 0, None) == 0
+    assert lib.gdn_metadata_pad(None, None, None, None, None, None, None, 2, None) == 1
+    assert b"null table" in lib.gdn_last_error()
 
 
 def test_fused_prefill_reports_uncovered_shapes_without_launching():
