@@ -64,11 +64,21 @@ typedef short s4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 to_uint4(u4_t v) { return make_uint4(v[0], v[1], v[2], v[3]); }
 
-// LDS row strides (halfs).  K rows: 76 dwords, so both the 8-byte row reads
-// of the left operands and the 4-row transpose reads avoid bank conflicts.
-constexpr int LDK = 152;
+// LDS row strides (halfs).  The LDS serves a 64-bit access 16 lanes at a
+// time over 32 four-byte banks (the layouts below measure zero bank-conflict
+// cycles on the K/Q tiles, against 44 % of all LDS-busy cycles with padded
+// rows alone).
+//
+// K and Q tiles: rows of d_k + 16 halfs (a stride of 8 mod 32 dwords), and
+// 8-byte chunk q of row r stored at chunk q ^ ((r / 4) mod 4).  The 16 rows of
+// a left-operand read (one chunk each) then fall on 4 row phases x 4 chunk
+// swizzles = 16 distinct bank pairs, and so do the 4 rows x 4 chunks of a
+// transpose read; the swizzle keeps chunks q and q + 4 16 halfs apart.
 constexpr int LDV = 80;      // V rows (64 columns)
-constexpr int LDA = kC + 8;  // A and M rows
+// A and M rows: 34 dwords.  The LDS serves a 64-bit access 16 lanes at a time
+// over 32 four-byte banks; 16 rows at a stride of 2 mod 4 dwords hit all 32
+// banks once (a stride of 0 mod 4 pairs rows r and r + 8 on one bank).
+constexpr int LDA = kC + 4;
 // Gate table per chunk (floats): G, 2^G, 2^(G_last - G) (0 past the end),
 // beta, then 2^G_last.
 constexpr int GTS = 264;
@@ -90,6 +100,13 @@ __device__ __forceinline__ h8_t afrag(const _Float16* base, int ld, int row, int
   const _Float16* p = base + row * ld + k0 + 4 * g;
   return cat(*reinterpret_cast<const h4_t*>(p), *reinterpret_cast<const h4_t*>(p + 16));
 }
+// afrag of a swizzled K / Q tile: k0 is a multiple of 32 and g < 4, so chunk
+// k0 / 4 + g lands on k0 / 4 + (g ^ a), a = (row / 4) mod 4, and chunk + 4 16
+// halfs after it.
+__device__ __forceinline__ h8_t kqfrag(const _Float16* base, int ld, int row, int k0, int g) {
+  const _Float16* p = base + row * ld + k0 + 4 * (g ^ ((row >> 2) & 3));
+  return cat(*reinterpret_cast<const h4_t*>(p), *reinterpret_cast<const h4_t*>(p + 16));
+}
 // LDS transpose read: the 16 lanes of a group read a 4-row x 16-column block
 // (lane r: row r / 4, columns 4 (r % 4)..+3) and lane r receives column r.
 __device__ __forceinline__ h4_t tr_read(const _Float16* p) {
@@ -100,6 +117,13 @@ __device__ __forceinline__ h4_t tr_read(const _Float16* p) {
 // of X, k block = rows t0..t0+31 of X in the k order above.
 __device__ __forceinline__ h8_t tfrag(const _Float16* X, int ld, int t0, int c0, int lr, int lg) {
   const _Float16* p = X + (t0 + 4 * lg + (lr >> 2)) * ld + c0 + 4 * (lr & 3);
+  return cat(tr_read(p), tr_read(p + 16 * ld));
+}
+// tfrag of a swizzled K tile (t0 a multiple of 32, c0 of 16): the row phase
+// (r / 4) mod 4 is the same for rows r and r + 16.
+__device__ __forceinline__ h8_t kq_tfrag(const _Float16* X, int ld, int t0, int c0, int lr, int lg) {
+  const int r = t0 + 4 * lg + (lr >> 2);
+  const _Float16* p = X + r * ld + c0 + 4 * ((lr & 3) ^ ((r >> 2) & 3));
   return cat(tr_read(p), tr_read(p + 16 * ld));
 }
 // Right operand from two C-layout accumulator tiles (rows 0-15, rows 16-31).
@@ -191,7 +215,8 @@ template <int DK, class IOT, class ST, bool FUSED>
 __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p) {
   constexpr int HT = DK / 16;    // 16-row state tiles
   constexpr int KS = DK / 32;    // 32-deep k steps over d_k
-  constexpr int LDQ = DK + 8;    // Q row stride (halfs)
+  constexpr int LDK = DK + 16;   // K / Q row strides (halfs; swizzled tiles)
+  constexpr int LDQ = DK + 16;
   constexpr int DB = DK / 8;     // 8-column blocks of a K row
   constexpr int KBLK = 16 * DB;  // K (Q) staging blocks (4 tokens x 8 columns) per chunk
   static_assert(KS >= 1 && KBLK <= 256, "d_k in {32, 64, 128}");
@@ -310,7 +335,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         for (int m = 0; m < KS; ++m) {
           h8_t kf[4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) kf[i] = afrag(K, LDK, 16 * i + lr, 32 * m, lg);
+          for (int i = 0; i < 4; ++i) kf[i] = kqfrag(K, LDK, 16 * i + lr, 32 * m, lg);
           const h8_t hb = bfrag(hT[2 * m], hT[2 * m + 1]);
 #pragma unroll
           for (int i = 0; i < 4; ++i) P[i] = mma(kf[i], hb, P[i]);
@@ -332,7 +357,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       for (int m = 0; m < KS; ++m) {
         h8_t qf[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) qf[i] = afrag(Q, LDQ, 16 * i + lr, 32 * m, lg);
+        for (int i = 0; i < 4; ++i) qf[i] = kqfrag(Q, LDQ, 16 * i + lr, 32 * m, lg);
         const h8_t hb = bfrag(hT[2 * m], hT[2 * m + 1]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) Ot[i] = mma(hb, qf[i], Ot[i]);
@@ -408,8 +433,8 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         const float gl = gt[G_LAST];
 #pragma unroll
         for (int ti = 0; ti < HT; ++ti) {
-          const h8_t k0 = tfrag(K, LDK, 0, 16 * ti, lr, lg);
-          const h8_t k1 = tfrag(K, LDK, 32, 16 * ti, lr, lg);
+          const h8_t k0 = kq_tfrag(K, LDK, 0, 16 * ti, lr, lg);
+          const h8_t k1 = kq_tfrag(K, LDK, 32, 16 * ti, lr, lg);
           hT[ti] = mma(k1, db1, mma(k0, db0, hT[ti] * gl));
         }
       }
@@ -454,8 +479,8 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       h8_t k0[KS], k1[KS];
 #pragma unroll
       for (int m = 0; m < KS; ++m) {
-        k0[m] = afrag(K, LDK, r0 + lr, 32 * m, lg);
-        k1[m] = afrag(K, LDK, r0 + 16 + lr, 32 * m, lg);
+        k0[m] = kqfrag(K, LDK, r0 + lr, 32 * m, lg);
+        k1[m] = kqfrag(K, LDK, r0 + 16 + lr, 32 * m, lg);
       }
 #pragma unroll
       for (int m = 0; m < KS; ++m) {
@@ -533,8 +558,8 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         h8_t a[KS], b[KS];
 #pragma unroll
         for (int m = 0; m < KS; ++m) {
-          a[m] = afrag(K, LDK, 16 * tj + lr, 32 * m, lg);
-          b[m] = afrag(X, ldx, 16 * ti + lr, 32 * m, lg);
+          a[m] = kqfrag(K, LDK, 16 * tj + lr, 32 * m, lg);
+          b[m] = kqfrag(X, ldx, 16 * ti + lr, 32 * m, lg);
         }
         f4_t acc = zero4();
 #pragma unroll
@@ -830,12 +855,20 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       };
       auto stage_kq = [&](int64_t ck) __attribute__((always_inline)) {
         if (kq_thread) {
-          _Float16* kd = sK + (ck % 3) * kC * LDK + (4 * ktb) * LDK + 8 * kdb;
-          _Float16* qd = sQ + (ck & 1) * kC * LDQ + (4 * ktb) * LDQ + 8 * kdb;
+          // rows 4 ktb + u share the swizzle a = ktb mod 4: chunks 2 kdb and
+          // 2 kdb + 1 go to (2 kdb) ^ a and (2 kdb + 1) ^ a, as two 8-byte writes
+          const int a = ktb & 3;
+          const int o0 = 4 * ((2 * kdb) ^ a), o1 = 4 * ((2 * kdb + 1) ^ a);
+          _Float16* kd = sK + (ck % 3) * kC * LDK + (4 * ktb) * LDK;
+          _Float16* qd = sQ + (ck & 1) * kC * LDQ + (4 * ktb) * LDQ;
 #pragma unroll
           for (int u = 0; u < 4; ++u) {  // (fused: q and k arrive as f16 operands)
-            *reinterpret_cast<uint4*>(kd + u * LDK) = FUSED ? pk[u] : to_f16x8<IOT>(pk[u]);
-            *reinterpret_cast<uint4*>(qd + u * LDQ) = FUSED ? pq[u] : to_f16x8<IOT>(pq[u]);
+            const uint4 kv = FUSED ? pk[u] : to_f16x8<IOT>(pk[u]);
+            const uint4 qv = FUSED ? pq[u] : to_f16x8<IOT>(pq[u]);
+            *reinterpret_cast<uint2*>(kd + u * LDK + o0) = make_uint2(kv.x, kv.y);
+            *reinterpret_cast<uint2*>(kd + u * LDK + o1) = make_uint2(kv.z, kv.w);
+            *reinterpret_cast<uint2*>(qd + u * LDQ + o0) = make_uint2(qv.x, qv.y);
+            *reinterpret_cast<uint2*>(qd + u * LDQ + o1) = make_uint2(qv.z, qv.w);
           }
         }
       };
