@@ -144,7 +144,9 @@ int gdn_chunk_gated_delta_rule(const void* q, const void* k, const void* v, int 
  *   in out_dtype: the io dtype, or GDN_F16 for the f16 MFMA operands that
  *   gdn_prefill_fused reads (the io-rounded values, converted toward zero);
  *   gate, beta [T, HV] (row/head strides, any float dtype), A_log, dt_bias
- *   [HV] -> g_out, beta_out [T, HV] fp32 (prepare_gdn, kernel/fused.py:105-117).
+ *   [HV] -> g_out, beta_out [HV, T] fp32, head-major so that the chunk
+ *   kernel's per-head gate loads are contiguous (prepare_gdn,
+ *   kernel/fused.py:105-117).
  */
 int gdn_prefill_qk(const void* mixed, int64_t row_stride, int io_dtype, const void* weight, int kernel_width,
                    const void* cu_seqlens, int cu_dtype, int64_t num_seqs, int64_t total_tokens, int64_t H,
@@ -156,7 +158,7 @@ int gdn_prefill_qk(const void* mixed, int64_t row_stride, int io_dtype, const vo
                    float* beta_out, void* stream);
 
 /*
- * gdn_prefill_fused: q, k (f16), g, beta from gdn_prefill_qk; mixed, weight,
+ * gdn_prefill_fused: q, k (f16), g, beta ([HV, T]) from gdn_prefill_qk; mixed, weight,
  * conv_state and baseline_slots as there (the v channels' history, and the
  * initial recurrent state, come from baseline_slots); state pool,
  * chunk/final write slots and out as in gdn_chunk_gated_delta_rule.

@@ -623,9 +623,11 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     float pgate = 0.f, pbeta = 0.f;
     auto prefetch_g = [&](int64_t ck) __attribute__((always_inline)) {
       const bool ok = lane < valid_rows(ck);
-      const int64_t t = bos + (ok ? ck * kC + lane : 0);  // a valid row for every chunk index
-      pgate = p.g[t * p.HV + h];
-      pbeta = p.beta[t * p.HV + h];
+      const int64_t t = len > 0 ? bos + (ok ? ck * kC + lane : 0) : 0;  // a valid row for every chunk index
+      // fused: head-major [HV, T] gates from the q/k pass (contiguous per head)
+      const int64_t gi = FUSED ? h * p.T + t : t * p.HV + h;
+      pgate = p.g[gi];
+      pbeta = p.beta[gi];
     };
     auto stage_g = [&](int64_t ck) __attribute__((always_inline)) {
       const bool ok = lane < valid_rows(ck);
@@ -638,6 +640,9 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     // tokens before, or the conv history at the sequence start).
     constexpr int VT = 4, VNR = VT + 3;
     const int fst = tid - 640;
+    // (waves 10-11 only; prefetch_fv, conv_v and stage_fv are called from that
+    // role alone and run unconditionally, so no prefetch register is left
+    // maybe-pending on a skipped path)
     const bool fv_thread = FUSED && fst >= 0 && fst < 128;
     const int fvtb = fst >> 3, fvdb = fst & 7;
     const uint16_t* mixed = static_cast<const uint16_t*>(f.mixed);
@@ -646,7 +651,6 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     const int64_t ch0 = vch + 8 * fvdb;
     u4_t vraw[VNR];
     float vw[4][8];
-    uint32_t vlo = 0;
     const uint16_t* hist = nullptr;
     if constexpr (FUSED) {
       if (fv_thread) {
@@ -664,46 +668,22 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
 #pragma unroll
           for (int tap = 0; tap < 4; ++tap) vw[tap][c] = wv[c * 4 + tap];
       }
-      vlo = static_cast<uint32_t>((VT * fvtb * rs + 8 * fvdb) * 2);
-      asm volatile("" : "+v"(vlo));
       const int64_t bslot = uniform_index(p.read_slots, n, p.read_is64);
       if (bslot >= 0)
         hist = static_cast<const uint16_t*>(f.conv_state) + bslot * f.conv_slot_stride + p.layer * f.conv_layer_stride;
     }
+    // Every row of the window is a clamped row of the sequence, loaded with
+    // no select on the data, so nothing waits for these loads before the next
+    // chunk's conv.  Rows past the end only feed output rows that conv_v
+    // zeroes; the rows before the start (first chunk) are the conv history or
+    // zero, which conv_v substitutes.
     auto prefetch_fv = [&](int64_t cv) __attribute__((always_inline)) {
-      if (!fv_thread) return;
-      if (cv > 0 && (cv + 1) * kC <= len) {
-        // a uniform row pointer stepped per row (kept opaque so that the row
-        // addresses are not precomputed and held across the loop)
-        int64_t step = rs * 2;
-        asm volatile("" : "+s"(step));
-        const char* rp = reinterpret_cast<const char*>(mixed + (bos + cv * kC) * rs + vch) - 3 * step;
+      const int64_t t0 = cv * kC + VT * fvtb - 3;
 #pragma unroll
-        for (int i = 0; i < VNR; ++i) {
-          vraw[i] = *reinterpret_cast<const u4_t*>(rp + vlo);
-          rp += step;
-        }
-      } else {
-        // first, last or past-the-end chunk: rows outside the sequence read a
-        // clamped (valid) row and are zeroed; the rows before it are the history
-        const int64_t t0 = cv * kC + VT * fvtb - 3;
-        const u4_t zero = {0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int i = 0; i < VNR; ++i) {
-          const int64_t t = t0 + i;
-          const int64_t tc = t < 0 ? 0 : (t >= len ? len - 1 : t);
-          const u4_t v = *reinterpret_cast<const u4_t*>(mixed + (bos + tc) * rs + ch0);
-          vraw[i] = (t >= 0 && t < len) ? v : zero;
-        }
-        if (cv == 0) {  // conv history: [channel][3] layout, 48 contiguous bytes
-          const bool hl = fvtb == 0 && hist != nullptr;
-          const uint16_t* hp = hl ? hist + ch0 * 3 : mixed + bos * rs + ch0;
-#pragma unroll
-          for (int i = 0; i < 3; ++i) {
-            const u4_t v = *reinterpret_cast<const u4_t*>(hp + (hl ? 8 * i : 0));
-            vraw[i] = hl ? v : vraw[i];
-          }
-        }
+      for (int i = 0; i < VNR; ++i) {
+        const int64_t t = t0 + i;
+        const int64_t row = len > 0 ? bos + (t < 0 ? 0 : (t >= len ? len - 1 : t)) : 0;
+        vraw[i] = *reinterpret_cast<const u4_t*>(mixed + row * rs + ch0);
       }
     };
     // conv of chunk cv into registers, stage by stage over all VT x 8 values
@@ -713,15 +693,18 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     // y = round(silu(round(sum_tap w x))), the outer rounding being the io pack.
     uint4 vo[VT];
     auto conv_v = [&](int64_t cv) __attribute__((always_inline)) {
-      if (!fv_thread) return;
       const int nv = valid_rows(cv);
       float win[3][8];
 #pragma unroll
       for (int j = 0; j < 3; ++j) unpack8<IOT>(to_uint4(vraw[j]), win[j]);
-      if (cv == 0 && fvtb == 0) {  // history rows hold [channel][tap]
+      if (cv == 0 && fvtb == 0) {  // the 3 inputs before the sequence: history ([channel][tap]) or zero
         float e[3][8];
 #pragma unroll
-        for (int j = 0; j < 3; ++j) unpack8<IOT>(to_uint4(vraw[j]), e[j]);
+        for (int j = 0; j < 3; ++j) {
+          uint4 hv = make_uint4(0, 0, 0, 0);
+          if (hist != nullptr) hv = *reinterpret_cast<const uint4*>(hist + ch0 * 3 + 8 * j);
+          unpack8<IOT>(hv, e[j]);
+        }
 #pragma unroll
         for (int c = 0; c < 8; ++c)
 #pragma unroll
@@ -765,7 +748,6 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       }
     };
     auto stage_fv = [&]() __attribute__((always_inline)) {
-      if (!fv_thread) return;
       _Float16* vd = sV + (VT * fvtb) * LDV + 8 * fvdb;
 #pragma unroll
       for (int i = 0; i < VT; ++i) *reinterpret_cast<uint4*>(vd + i * LDV) = vo[i];
@@ -808,10 +790,11 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       for (int64_t c = 0; c < nchunks; ++c) {
         if constexpr (FUSED) conv_v(c + 1);
         lds_barrier();  // M(c)
-        if constexpr (FUSED) {
-          stage_fv();
-          prefetch_fv(c + 2);
-        }
+        // The row loads for the conv of c + 2 go out first, so they have the
+        // whole phase to arrive before that conv (right after the next
+        // barrier); the gate loads consumed here are older than them.
+        if constexpr (FUSED) prefetch_fv(c + 2);
+        if constexpr (FUSED) stage_fv();
         if (wave == kGateWave) {
           stage_g(c + 2);
           prefetch_g(c + 3);

@@ -152,6 +152,7 @@ struct FrontParams {
   void* v_out;
   float* g_out;
   float* b_out;
+  int64_t g_ld;  // 0: g_out / b_out [T, HV]; else head-major [HV, g_ld]
   int qk_f16;  // q_out / k_out as f16 MFMA operands (the bf16-rounded values, converted)
 };
 
@@ -394,14 +395,16 @@ __global__ __launch_bounds__(256) void conv_vec_kernel(FrontParams fp) {
   if (FRONT && blockIdx.y == 0 && fp.g_out) {
     const int n = static_cast<int>(t1 - t0);
     for (int idx = threadIdx.x; idx < n * fp.HV; idx += 256) {
-      const int64_t t = t0 + idx / fp.HV;
-      const int64_t h = idx % fp.HV;
+      // head-major output: consecutive threads take consecutive tokens of a head
+      const int64_t t = t0 + (fp.g_ld ? idx % n : idx / fp.HV);
+      const int64_t h = fp.g_ld ? idx / n : idx % fp.HV;
+      const int64_t o = fp.g_ld ? h * fp.g_ld + t : t * fp.HV + h;
       const float a = load_any(fp.A_log, h, fp.a_dtype);
       const float b = load_any(fp.dt_bias, h, fp.dt_dtype);
       const float gv = load_any(fp.gate, t * fp.gate_r + h * fp.gate_h, fp.gate_dtype) + b;
       const float bv = load_any(fp.beta, t * fp.beta_r + h * fp.beta_h, fp.beta_dtype);
-      fp.g_out[t * fp.HV + h] = -expf(a) * softplus_prefill(gv);
-      fp.b_out[t * fp.HV + h] = sigmoid(bv);
+      fp.g_out[o] = -expf(a) * softplus_prefill(gv);
+      fp.b_out[o] = sigmoid(bv);
     }
   }
 }
@@ -726,7 +729,7 @@ extern "C" int gdn_prefill_qk(const void* mixed, int64_t row_stride, int io_dtyp
   fp.gate = gate; fp.gate_r = gate_row_stride; fp.gate_h = gate_head_stride; fp.gate_dtype = gate_dtype;
   fp.beta = beta; fp.beta_r = beta_row_stride; fp.beta_h = beta_head_stride; fp.beta_dtype = beta_dtype;
   fp.A_log = A_log; fp.a_dtype = a_dtype; fp.dt_bias = dt_bias; fp.dt_dtype = dt_dtype;
-  fp.g_out = g_out; fp.b_out = beta_out;
+  fp.g_out = g_out; fp.b_out = beta_out; fp.g_ld = total_tokens;  // [HV, T]
   auto s = static_cast<hipStream_t>(stream);
   const int rc = io_dtype == GDN_BF16 ? launch_vec<bf16, true>(fp, static_cast<int>(dk), s)
                                       : launch_vec<f16, true>(fp, static_cast<int>(dk), s);

@@ -104,7 +104,7 @@ def prefill_fused(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, co
     # q, k as the chunk kernel's f16 MFMA operands; prepared gates
     q = torch.empty(T, config.num_k_heads, config.head_k_dim, device=mixed_qkv.device, dtype=torch.float16)
     k = torch.empty_like(q)
-    g = torch.empty(T, config.num_v_heads, device=mixed_qkv.device, dtype=torch.float32)
+    g = torch.empty(config.num_v_heads, T, device=mixed_qkv.device, dtype=torch.float32)  # head-major
     b = torch.empty_like(g)
     stream = _lib.stream_of(mixed_qkv)
     N = len(cu_seqlens) - 1
@@ -138,7 +138,7 @@ def prefill_fused(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, co
 def prefill_chunk_fused(q, k, g, b, mixed_qkv, weight, config, conv_state, recurrent_state, cu_seqlens,
                         baseline_slots, chunk_write_slots, out):
     """The chunk-kernel launch of ``prefill_fused`` (q, k, g, beta from the q/k
-    pass; v computed from ``mixed_qkv`` inside)."""
+    pass, g and beta head-major ``[HV, T]``; v computed from ``mixed_qkv`` inside)."""
     T = mixed_qkv.shape[0]
     _lib.call(
         "gdn_prefill_fused",
