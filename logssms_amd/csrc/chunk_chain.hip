@@ -595,9 +595,9 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
           mtile(3, 1);
         }
       } else {
-        if (w == 2) {
+        if (w == 0) {
           mtile(3, 2);
-        } else if (w == 3) {
+        } else if (w == 1) {
           mtile(3, 3);
         }
       }
@@ -777,7 +777,6 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         stage_g(0);
         prefetch_g(1);
         stage_g(1);
-        prefetch_g(2);
       }
       if constexpr (FUSED) {
         prefetch_fv(0);
@@ -785,6 +784,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         stage_fv();
         prefetch_fv(1);
       }
+      prefetch_g(2);
       lds_barrier();  // P0
       lds_barrier();  // B(0)
       for (int64_t c = 0; c < nchunks; ++c) {
@@ -792,13 +792,13 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         lds_barrier();  // M(c)
         // The row loads for the conv of c + 2 go out first, so they have the
         // whole phase to arrive before that conv (right after the next
-        // barrier); the gate loads consumed here are older than them.
+        // barrier).  Both waves issue the gate loads, after the row loads:
+        // the loads in flight at the conv are then the same on either
+        // wave, and the conv's waits never cover the younger gate loads.
         if constexpr (FUSED) prefetch_fv(c + 2);
         if constexpr (FUSED) stage_fv();
-        if (wave == kGateWave) {
-          stage_g(c + 2);
-          prefetch_g(c + 3);
-        }
+        if (wave == kGateWave) stage_g(c + 2);
+        prefetch_g(c + 3);
         lds_barrier();  // B(c+1)
       }
     } else {
