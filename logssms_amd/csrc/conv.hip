@@ -232,7 +232,7 @@ __global__ __launch_bounds__(kThreads) void frontend_kernel(FrontParams fp) {
 // 16-byte load and one 16-byte store per token, the W-1 previous inputs in
 // registers, and the per-head q/k sum of squares reduced across the DK/8
 // lanes of the head with cross-lane shuffles (no LDS).
-constexpr int kVTok = 16;
+constexpr int kVTok = 32;
 
 
 // FRONT: fused front end (q/k normalised into q_out/k_out, v into v_out, history
