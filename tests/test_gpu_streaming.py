@@ -410,6 +410,61 @@ def test_verify_group_matches_oracle(permute_rows):
     assert_state_close(state, state_ref)
 
 
+def _wide_pools(conv, state):
+    """Device views of `conv` / `state` whose element offsets pass 2**31 bytes:
+    a 1 GiB slot stride for the state pool and the reference's conv layer
+    stride of 1,487,011,840 elements (tests/layers/test_conv_decode.py:25-55)."""
+    slots, layers, C, S = conv.shape
+    _, _, HV, dk, dv = state.shape
+    ls = 1487011840
+    cbuf = torch.empty(ls * (layers - 1) + slots * C * S, device=DEV, dtype=conv.dtype)
+    wide_conv = cbuf.as_strided(conv.shape, (C * S, ls, S, 1))
+    ss = 1 << 28
+    sbuf = torch.empty(ss * (slots - 1) + layers * HV * dk * dv, device=DEV, dtype=state.dtype)
+    wide_state = sbuf.as_strided(state.shape, (ss, HV * dk * dv, dk * dv, dv, 1))
+    wide_conv.copy_(conv.to(DEV))
+    wide_state.copy_(state.to(DEV))
+    return wide_conv, wide_state
+
+
+def test_decode_and_verify_pool_offsets_beyond_2gib():
+    """Slot and layer offsets above 2**31 bytes address the right rows: the
+    layer-1 conv windows sit 2.97 GB into their buffer and slots >= 2 of the
+    state pool past 2 GiB; outputs, windows and states equal the oracle on the
+    compact pools."""
+    from logssms_amd.kernel.linear_attention.fused_backend import decode_step, verify_group
+    g = gen(31)
+    H, HV, d = 2, 4, 64
+    cfg = _cfg(H=H, HV=HV, dk=d, dv=d, layer=1)
+    B, T, slots = 3, 2, 10
+    inp = _backend_inputs(g, cfg, B * T, slots)
+    reads = torch.tensor([1, 6, 3])
+    writes = torch.tensor([7, 6, 2])  # one in place
+    conv_ref, state_ref = inp["conv"].clone(), inp["state"].clone()
+    want = ref.forward_decode(inp["mixed"][:B], inp["gate"][:B], inp["beta"][:B], inp["weight"], inp["A_log"],
+                              inp["dt_bias"], conv_ref, state_ref, 1, reads, writes, H, d, HV, d)
+    conv, state = _wide_pools(inp["conv"], inp["state"])
+    got = decode_step(inp["mixed"][:B].to(DEV), inp["gate"][:B].to(DEV), inp["beta"][:B].to(DEV),
+                      inp["weight"].to(DEV), inp["A_log"].to(DEV), inp["dt_bias"].to(DEV), cfg, conv, state,
+                      reads.to(DEV), writes.to(DEV))
+    assert_bf16_close(got, want)
+    torch.testing.assert_close(conv.cpu(), conv_ref, rtol=0, atol=0)
+    assert_state_close(state, state_ref)
+    # verify from the decoded pools: per-step windows and states to far slots
+    # (written slots disjoint from every baseline slot)
+    base = torch.tensor([7, 2, 0])
+    vwrites = torch.tensor([[5, 4], [1, 3], [8, 9]])
+    want = ref.forward_verify(inp["mixed"], inp["gate"], inp["beta"], inp["weight"], inp["A_log"],
+                              inp["dt_bias"], conv_ref, state_ref, 1, base, vwrites, H, d, HV, d)
+    out = torch.zeros(B * T, HV, d, device=DEV, dtype=torch.bfloat16)
+    verify_group(inp["mixed"].to(DEV), inp["gate"].to(DEV), inp["beta"].to(DEV), inp["weight"].to(DEV),
+                 inp["A_log"].to(DEV), inp["dt_bias"].to(DEV), cfg, conv, state, None, base.to(DEV),
+                 vwrites.to(DEV), out)
+    assert_bf16_close(out, want)
+    torch.testing.assert_close(conv.cpu(), conv_ref, rtol=0, atol=0)
+    assert_state_close(state, state_ref)
+
+
 # ------------------------------------------------------------------ state rows
 
 @pytest.mark.parametrize("index_dtype", [torch.int32, torch.int64])
