@@ -120,6 +120,38 @@ def test_fused_prefill_equals_two_step_path(case):
     assert not torch.equal(pool.recurrent_state[written], state0[written])
 
 
+def test_prefill_pool_offsets_beyond_2gib():
+    """Both prefill paths on pool views whose offsets pass 2**31 bytes (the
+    reference's conv layer stride of 1,487,011,840 elements, a 512 MiB state
+    slot stride) give bit for bit what the fused path gives on compact pools:
+    baseline states and conv histories are read from, and checkpoints and
+    snapshots written to, the far rows."""
+    from types import SimpleNamespace
+    cfg = _cfg(2, 4, 128, 128)
+    pool, w, meta = _setup(cfg, [70, 3, 130], gen(77), slots=8)
+    conv0, state0 = pool.conv_state.clone(), pool.recurrent_state.clone()
+    want = _fused(cfg, pool, w, meta).clone()
+    conv_want, state_want = pool.conv_state.clone(), pool.recurrent_state.clone()
+    slots, layers, C, S = conv0.shape
+    ls = 1487011840
+    conv_buf = torch.empty(ls * (layers - 1) + slots * C * S, device=DEV, dtype=conv0.dtype)
+    ss = (1 << 27) + 64
+    per_slot = state0[0].numel()
+    state_buf = torch.empty(ss * (slots - 1) + per_slot, device=DEV, dtype=state0.dtype)
+    wide = SimpleNamespace(conv_state=conv_buf.as_strided(conv0.shape, (C * S, ls, S, 1)),
+                           recurrent_state=state_buf.as_strided(state0.shape, (ss,) + state0.stride()[1:]))
+    used = torch.cat([meta["baseline"], meta["chunk_write"]])
+    assert int(used.max()) * ss * state0.element_size() >= 1 << 31, "no state slot past 2 GiB is used"
+    for path in (_fused, _two_step):
+        wide.conv_state.copy_(conv0)
+        wide.recurrent_state.copy_(state0)
+        got = path(cfg, wide, w, meta)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"{path.__name__}: output differs"
+        assert torch.equal(wide.recurrent_state, state_want), f"{path.__name__}: states differ"
+        assert torch.equal(wide.conv_state, conv_want), f"{path.__name__}: conv windows differ"
+
+
 def test_fused_prefill_declines_uncovered_shapes():
     """dv = 32 is outside the fused kernel: the wrapper returns None (the
     backend then takes the two-step path) and writes nothing."""
