@@ -357,7 +357,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the GDN path shards by heads/sequences with no collective; see DESIGN.md)", file=sys.stderr)
+              "(the GDN path would shard by sequences and v-heads, one process per GPU, with no "
+              "collective on the path)", file=sys.stderr)
         sys.exit(2)
     dev = "cuda:0"
     torch.cuda.set_device(0)
