@@ -125,6 +125,80 @@ def test_packed_conv_input_scales():
     assert len(lengths) == 2
 
 
+def test_packed_conv_graph_replay_reads_current_slots():
+    """One capture, replays with new token and final snapshot slots: the
+    windows land where the slot tensors say at replay time
+    (tests/kernel/test_gdn_prefill_direct.py:271-283)."""
+    from logssms_amd.kernel.linear_attention import PackedConvStateIO, packed_causal_conv1d
+    g = gen(41)
+    C, W = 256, 4
+    cu = [0, 5, 70, 71]
+    T, N = cu[-1], len(cu) - 1
+    x = randn(T, C, g=g, dtype=torch.bfloat16)
+    weight = randn(C, 1, W, g=g, dtype=torch.bfloat16, std=0.2)
+    history = randn(N, C, W - 1, g=g, dtype=torch.bfloat16)
+    y_ref, windows = ref.packed_causal_conv1d(x, weight, history, cu)
+    storage = torch.zeros(12, 2, C, W - 1, device=DEV, dtype=torch.bfloat16)
+    slots = torch.full((T,), -1, device=DEV, dtype=torch.int64)
+    final = torch.full((N,), -1, device=DEV, dtype=torch.int64)
+    io = PackedConvStateIO(storage, slots, final_slots=final, layer=1)
+    args = (x.to(DEV), weight.to(DEV), history.to(DEV), torch.tensor(cu, device=DEV), None)
+    out = packed_causal_conv1d(*args, state_io=io)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = packed_causal_conv1d(*args, state_io=io)
+    plans = [({3: 0, 40: 1}, [2, 3, 4]), ({0: 5, 63: 6, 69: 7}, [-1, 8, 9]), ({}, [10, -1, 11])]
+    for rows, fin in plans:
+        storage.zero_()
+        slots.fill_(-1)
+        for r, s in rows.items():
+            slots[r] = s
+        final.copy_(torch.tensor(fin, device=DEV))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert_bf16_close(out, y_ref, rel=1e-2, atol=1e-2)
+        got = storage.cpu()
+        want = torch.zeros_like(got)
+        for r, s in rows.items():
+            want[s, 1] = windows[r]
+        for n, s in enumerate(fin):
+            if s >= 0:
+                want[s, 1] = windows[cu[n + 1] - 1]
+        torch.testing.assert_close(got, want, rtol=0, atol=0)
+
+
+def test_conv_decode_graph_replay_reads_current_slots():
+    """One capture of the single-token conv, replays with new read/write
+    slots, including in-place updates (tests/layers/test_conv_decode.py:143-159)."""
+    from logssms_amd.kernel.linear_attention import conv_decode
+    g = gen(42)
+    cfg = _cfg(width=4)
+    C = cfg.conv_dim
+    x = randn(3, C, g=g, dtype=torch.bfloat16)
+    weight = randn(C, 1, 4, g=g, dtype=torch.bfloat16, std=0.2)
+    state = randn(8, 2, C, 3, g=g, dtype=torch.bfloat16)
+    dev_state = state.to(DEV)
+    reads = torch.tensor([0, 1, 2], device=DEV)
+    writes = torch.tensor([3, 4, 5], device=DEV)
+    args = (x.to(DEV), weight.to(DEV), cfg)
+    conv_decode(*args, read_slots=reads, write_slots=writes, standard_state=dev_state)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y = conv_decode(*args, read_slots=reads, write_slots=writes, standard_state=dev_state)
+    # (a slot written by one sequence is never read by another in the same step)
+    for r, w in [([7, 6, 5], [0, 1, 2]), ([1, 3, 5], [1, 3, 5]), ([2, 0, 4], [6, 7, 3])]:
+        reads.copy_(torch.tensor(r, device=DEV))
+        writes.copy_(torch.tensor(w, device=DEV))
+        expected_state = dev_state.cpu()
+        want = ref.conv_decode(x, weight, expected_state, 1, r, w)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert_bf16_close(y, want, rel=1e-2, atol=1e-2)
+        torch.testing.assert_close(dev_state.cpu(), expected_state, rtol=0, atol=0)
+
+
 # ------------------------------------------------------------------ prepare_gdn
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
