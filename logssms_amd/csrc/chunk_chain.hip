@@ -113,13 +113,9 @@ __device__ __forceinline__ h4_t tr_read(const _Float16* p) {
   typedef __attribute__((address_space(3))) s4_t lds_s4;
   return __builtin_bit_cast(h4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p)));
 }
-// Left operand of X^T for a row-major X: rows of X^T = columns c0 + lane % 16
-// of X, k block = rows t0..t0+31 of X in the k order above.
-__device__ __forceinline__ h8_t tfrag(const _Float16* X, int ld, int t0, int c0, int lr, int lg) {
-  const _Float16* p = X + (t0 + 4 * lg + (lr >> 2)) * ld + c0 + 4 * (lr & 3);
-  return cat(tr_read(p), tr_read(p + 16 * ld));
-}
-// tfrag of a swizzled K tile (t0 a multiple of 32, c0 of 16): the row phase
+// Left operand of K^T for a token-major, swizzled K tile: rows of K^T =
+// columns c0 + lane % 16 of K (c0 a multiple of 16), k block = tokens
+// t0..t0+31 (t0 a multiple of 32) in the k order above; the row phase
 // (r / 4) mod 4 is the same for rows r and r + 16.
 __device__ __forceinline__ h8_t kq_tfrag(const _Float16* X, int ld, int t0, int c0, int lr, int lg) {
   const int r = t0 + 4 * lg + (lr >> 2);
@@ -753,6 +749,31 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       for (int i = 0; i < VT; ++i) *reinterpret_cast<uint4*>(vd + i * LDV) = vo[i];
     };
 
+    // Two-step path: waves 10-11 stage the V rows (4 tokens x 8 columns per
+    // lane, the fv lane mapping), converted to f16 operands.  Rows past the
+    // end are clamped loads, zeroed when staged.
+    uint4 pv[4];
+    auto prefetch_v = [&](int64_t cv) __attribute__((always_inline)) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t t = cv * kC + VT * fvtb + u;
+        const int64_t row = len > 0 ? bos + (t < len ? t : len - 1) : 0;  // a row of the sequence
+        pv[u] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.v) + (row * p.HV + h) * p.DV +
+                                                col_base + 8 * fvdb);
+      }
+    };
+    auto stage_v = [&](int64_t cv) __attribute__((always_inline)) {
+      const int nk = valid_rows(cv);
+      _Float16* vd = sV + (VT * fvtb) * LDV + 8 * fvdb;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint4 o = to_f16x8<IOT>(pv[u]);
+        const bool ok = VT * fvtb + u < nk;
+        *reinterpret_cast<uint4*>(vd + u * LDV) = make_uint4(ok ? o.x : 0u, ok ? o.y : 0u, ok ? o.z : 0u,
+                                                             ok ? o.w : 0u);
+      }
+    };
+
     // Waves 4-5 (inverses), 6-9 (tiles, K/Q staging) and 10-11 (fused v conv,
     // gates) run separate loops with the same barrier sequence.  Staging and
     // prefetches run unconditionally, also for chunks past the end (their
@@ -783,6 +804,10 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         conv_v(0);
         stage_fv();
         prefetch_fv(1);
+      } else {
+        prefetch_v(0);
+        stage_v(0);
+        prefetch_v(1);
       }
       prefetch_g(2);
       lds_barrier();  // P0
@@ -795,8 +820,13 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         // barrier).  Both waves issue the gate loads, after the row loads:
         // the loads in flight at the conv are then the same on either
         // wave, and the conv's waits never cover the younger gate loads.
-        if constexpr (FUSED) prefetch_fv(c + 2);
-        if constexpr (FUSED) stage_fv();
+        if constexpr (FUSED) {
+          prefetch_fv(c + 2);
+          stage_fv();
+        } else {
+          stage_v(c + 1);
+          prefetch_v(c + 2);
+        }
         if (wave == kGateWave) stage_g(c + 2);
         prefetch_g(c + 3);
         lds_barrier();  // B(c+1)
@@ -804,18 +834,12 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     } else {
       const int st = tid - 384;       // staging thread index (waves 6-9)
       const bool kq_thread = st >= 0 && st < KBLK;
-      const bool v_thread = !FUSED && st >= 128;  // two-step path, waves 8, 9: 4 tokens x 8 columns of V
       // K/Q block: 16-byte column block fastest (conflict-free 16-byte LDS writes)
       const int ktb = st / DB, kdb = st % DB;
-      const int vtb = (st - 128) >> 3, vdb = (st - 128) & 7;
       const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + ((bos + 4 * ktb) * p.H + kh) * DK + 8 * kdb;
       const uint16_t* qbase = static_cast<const uint16_t*>(p.q) + ((bos + 4 * ktb) * p.H + kh) * DK + 8 * kdb;
       const int64_t krow = p.H * DK, kstride = kC * krow;
-      uint4 pk[4], pq[4], pv[4];
-      const uint16_t* vbase = FUSED ? nullptr
-                                    : static_cast<const uint16_t*>(p.v) + ((bos + 4 * vtb) * p.HV + h) * p.DV +
-                                          col_base + 8 * vdb;
-      const int64_t vrow = p.HV * p.DV, vstride = kC * vrow;
+      uint4 pk[4], pq[4];
 
       auto prefetch_kq = [&](int64_t ck) __attribute__((always_inline)) {
         const int nk = valid_rows(ck);
@@ -826,14 +850,6 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
             pk[u] = *reinterpret_cast<const uint4*>(kbase + ck * kstride + u * krow);
             pq[u] = *reinterpret_cast<const uint4*>(qbase + ck * kstride + u * krow);
           }
-        }
-      };
-      auto prefetch_v = [&](int64_t cv) __attribute__((always_inline)) {
-        const int nk = valid_rows(cv);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          pv[u] = make_uint4(0, 0, 0, 0);
-          if (v_thread && 4 * vtb + u < nk) pv[u] = *reinterpret_cast<const uint4*>(vbase + cv * vstride + u * vrow);
         }
       };
       auto stage_kq = [&](int64_t ck) __attribute__((always_inline)) {
@@ -855,20 +871,10 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
           }
         }
       };
-      auto stage_v = [&]() __attribute__((always_inline)) {
-        if (!v_thread) return;
-        _Float16* vd = sV + (4 * vtb) * LDV + 8 * vdb;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) *reinterpret_cast<uint4*>(vd + u * LDV) = to_f16x8<IOT>(pv[u]);
-      };
-
       // ---- prologue: chunks 0 and 1 staged, chunk 0 solved
       prefetch_kq(0);
-      prefetch_v(0);
       stage_kq(0);
-      stage_v();
       prefetch_kq(1);
-      prefetch_v(1);
       stage_kq(1);
       prefetch_kq(2);
       lds_barrier();  // P0
@@ -878,10 +884,8 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       for (int64_t c = 0; c < nchunks; ++c) {
         if (c + 1 < nchunks) tiles(c + 1, false);
         lds_barrier();  // M(c)
-        stage_v();
         stage_kq(c + 2);
         prefetch_kq(c + 3);
-        prefetch_v(c + 2);
         if (c + 1 < nchunks) tiles(c + 1, true);
         lds_barrier();  // B(c+1)
       }
