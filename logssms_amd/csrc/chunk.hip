@@ -783,11 +783,10 @@ extern "C" int gdn_chunk_gated_delta_rule(const void* q, const void* k, const vo
   if (dv % 64 == 0) {
     p.nvs = static_cast<int>(dv / 64);
     p.members = static_cast<int>(r * p.nvs);
+    // the 12-wave kernel covers every (d_k, io, state) combination this entry
+    // accepts; anything it declines is unsupported here as well
     const int rc = launch_chunk_chain(p, dk, io_dtype, state_dtype, groups, s);
     if (rc != GDN_ERR_UNSUPPORTED) return rc;
-    if (dk == 128) return dispatch_types<128, 64>(p, io_dtype, state_dtype, groups, s);
-    if (dk == 64) return dispatch_types<64, 64>(p, io_dtype, state_dtype, groups, s);
-    if (dk == 32) return dispatch_types<32, 64>(p, io_dtype, state_dtype, groups, s);
   } else if (dv == 32) {
     p.nvs = 1;
     p.members = static_cast<int>(r);
