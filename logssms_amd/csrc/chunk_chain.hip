@@ -631,7 +631,8 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     };
 
     // ---- fused path: V rows are the conv + SiLU of the projections
-    // (packed_conv.py:49-133), computed by waves 10-11 after the M barrier.  A
+    // (packed_conv.py:49-133), computed by waves 10-11 before the M barrier and
+    // staged after it.  A
     // lane convolves VT tokens x 8 channels with the 3 inputs before them (the
     // tokens before, or the conv history at the sequence start).
     constexpr int VT = 4, VNR = VT + 3;
@@ -774,8 +775,9 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       }
     };
 
-    // Waves 4-5 (inverses), 6-9 (tiles, K/Q staging) and 10-11 (fused v conv,
-    // gates) run separate loops with the same barrier sequence.  Staging and
+    // Waves 4-5 (inverses), 6-9 (tiles, K/Q staging) and 10-11 (v conv on the
+    // fused path or V staging on the two-step path, gates) run separate loops
+    // with the same barrier sequence.  Staging and
     // prefetches run unconditionally, also for chunks past the end (their
     // loads are masked off or clamped and their LDS targets are free): a
     // skipped consumer would leave the prefetch registers "maybe pending" at
