@@ -22,14 +22,14 @@ def _cfg(H, HV, dk, dv, layer=1):
                             conv_dim=2 * H * dk + HV * dv, state_len=3, layer_idx=layer)
 
 
-def _setup(cfg, lengths, g, state_dtype=torch.float32, slots=96, layers=2):
+def _setup(cfg, lengths, g, state_dtype=torch.float32, slots=96, layers=2, io=torch.bfloat16):
     """Random pools and inputs; per sequence a baseline (or none), checkpoint
     slots at some chunk ends and at the end, and conv snapshots at the same
     rows plus one skipped (negative) snapshot."""
     from logssms_amd.cache import LinearStatePool
     pool = LinearStatePool(slots, layers, cfg.conv_dim, 4, cfg.num_v_heads, cfg.head_k_dim, cfg.head_v_dim, DEV,
-                           torch.bfloat16, state_dtype=state_dtype)
-    pool.conv_state.copy_(randn(*pool.conv_state.shape, g=g, dtype=torch.bfloat16))
+                           io, state_dtype=state_dtype)
+    pool.conv_state.copy_(randn(*pool.conv_state.shape, g=g, dtype=io))
     pool.recurrent_state.copy_(randn(*pool.recurrent_state.shape, g=g, std=0.1).to(state_dtype))
     T = sum(lengths)
     free = torch.randperm(slots, generator=g).tolist()
@@ -52,10 +52,10 @@ def _setup(cfg, lengths, g, state_dtype=torch.float32, slots=96, layers=2):
     snap_slots.append(-1)
     cu = torch.tensor([0] + torch.tensor(lengths).cumsum(0).tolist(), dtype=torch.int32)
     w = dict(
-        mixed=randn(T, cfg.conv_dim, g=g, dtype=torch.bfloat16),
-        gate=randn(T, cfg.num_v_heads, g=g, dtype=torch.bfloat16),
-        beta=randn(T, cfg.num_v_heads, g=g, dtype=torch.bfloat16),
-        weight=randn(cfg.conv_dim, 1, 4, g=g, dtype=torch.bfloat16, std=0.3),
+        mixed=randn(T, cfg.conv_dim, g=g, dtype=io),
+        gate=randn(T, cfg.num_v_heads, g=g, dtype=io),
+        beta=randn(T, cfg.num_v_heads, g=g, dtype=io),
+        weight=randn(cfg.conv_dim, 1, 4, g=g, dtype=io, std=0.3),
         A_log=-rand(cfg.num_v_heads, g=g),
         dt_bias=randn(cfg.num_v_heads, g=g, std=0.5),
     )
@@ -88,21 +88,24 @@ def _fused(cfg, pool, w, meta):
 
 
 CASES = [
-    # H, HV, dk, dv, lengths, state dtype
-    (2, 4, 128, 128, [1, 2, 3, 63, 64, 65, 130, 257], torch.float32),
-    (2, 2, 128, 64, [200, 5, 64, 129], torch.float32),
-    (2, 4, 64, 64, [1, 70, 64, 191, 2], torch.float32),
-    (4, 4, 32, 64, [33, 128, 3, 100], torch.float32),
-    (2, 4, 128, 128, [96, 1, 300], torch.bfloat16),
+    # H, HV, dk, dv, lengths, state dtype, io dtype
+    (2, 4, 128, 128, [1, 2, 3, 63, 64, 65, 130, 257], torch.float32, torch.bfloat16),
+    (2, 2, 128, 64, [200, 5, 64, 129], torch.float32, torch.bfloat16),
+    (2, 4, 64, 64, [1, 70, 64, 191, 2], torch.float32, torch.bfloat16),
+    (4, 4, 32, 64, [33, 128, 3, 100], torch.float32, torch.bfloat16),
+    (2, 4, 128, 128, [96, 1, 300], torch.bfloat16, torch.bfloat16),
+    (2, 4, 128, 128, [1, 63, 64, 65, 200], torch.float32, torch.float16),
+    (2, 4, 64, 64, [70, 3, 129], torch.float16, torch.float16),
 ]
 
 
-@pytest.mark.parametrize("case", CASES, ids=[f"H{c[0]}_HV{c[1]}_dk{c[2]}_dv{c[3]}_{str(c[5])[6:]}" for c in CASES])
+@pytest.mark.parametrize("case", CASES, ids=[f"H{c[0]}_HV{c[1]}_dk{c[2]}_dv{c[3]}_{str(c[5])[6:]}_{str(c[6])[6:]}"
+                                             for c in CASES])
 def test_fused_prefill_equals_two_step_path(case):
-    H, HV, dk, dv, lengths, sdt = case
-    print(f"fused prefill case H={H} HV={HV} dk={dk} dv={dv} lengths={lengths} state={sdt}", flush=True)
+    H, HV, dk, dv, lengths, sdt, io = case
+    print(f"fused prefill case H={H} HV={HV} dk={dk} dv={dv} lengths={lengths} state={sdt} io={io}", flush=True)
     cfg = _cfg(H, HV, dk, dv)
-    pool, w, meta = _setup(cfg, lengths, gen(100 + dk + dv + len(lengths)), sdt)
+    pool, w, meta = _setup(cfg, lengths, gen(100 + dk + dv + len(lengths)), sdt, io=io)
     conv0, state0 = pool.conv_state.clone(), pool.recurrent_state.clone()
     want = _two_step(cfg, pool, w, meta).clone()
     conv_want, state_want = pool.conv_state.clone(), pool.recurrent_state.clone()
