@@ -390,29 +390,30 @@ def test_plain_recurrence_keeps_every_state(T):
 
 # ------------------------------------------------------------------ fused decode / verify
 
-def _backend_inputs(g, cfg, rows, slots):
+def _backend_inputs(g, cfg, rows, slots, io=torch.bfloat16):
     C = cfg.conv_dim
     return dict(
-        mixed=randn(rows, C, g=g, dtype=torch.bfloat16),
-        gate=randn(rows, cfg.num_v_heads, g=g, dtype=torch.bfloat16),
-        beta=randn(rows, cfg.num_v_heads, g=g, dtype=torch.bfloat16),
-        weight=randn(C, 1, cfg.state_len + 1, g=g, dtype=torch.bfloat16, std=0.3),
+        mixed=randn(rows, C, g=g, dtype=io),
+        gate=randn(rows, cfg.num_v_heads, g=g, dtype=io),
+        beta=randn(rows, cfg.num_v_heads, g=g, dtype=io),
+        weight=randn(C, 1, cfg.state_len + 1, g=g, dtype=io, std=0.3),
         A_log=-rand(cfg.num_v_heads, g=g),
         dt_bias=torch.zeros(cfg.num_v_heads),
-        conv=randn(slots, 2, C, cfg.state_len, g=g, dtype=torch.bfloat16),
+        conv=randn(slots, 2, C, cfg.state_len, g=g, dtype=io),
         state=randn(slots, 2, cfg.num_v_heads, cfg.head_k_dim, cfg.head_v_dim, g=g, std=0.1),
     )
 
 
 @pytest.mark.parametrize("in_place", [True, False])
 @pytest.mark.parametrize("shape", [(2, 4, 64), (16, 32, 128)])
-def test_decode_step_matches_oracle(in_place, shape):
+@pytest.mark.parametrize("io", [torch.bfloat16, torch.float16])
+def test_decode_step_matches_oracle(in_place, shape, io):
     from logssms_amd.kernel.linear_attention.fused_backend import decode_step
     H, HV, d = shape
     g = gen(3)
     cfg = _cfg(H=H, HV=HV, dk=d, dv=d, layer=1)
     B, slots = 16, 40
-    inp = _backend_inputs(g, cfg, B, slots)
+    inp = _backend_inputs(g, cfg, B, slots, io)
     perm = torch.randperm(slots, generator=g)
     reads = perm[:B]
     writes = reads.clone() if in_place else perm[B:2 * B]
