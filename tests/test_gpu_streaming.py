@@ -460,14 +460,15 @@ def test_decode_step_graph_replay_reads_current_slots():
 
 
 @pytest.mark.parametrize("permute_rows", [False, True])
-def test_verify_group_matches_oracle(permute_rows):
+@pytest.mark.parametrize("io", [torch.bfloat16, torch.float16])
+def test_verify_group_matches_oracle(permute_rows, io):
     from logssms_amd.kernel.linear_attention.fused_backend import verify_group
     g = gen(12)
     H, HV, d = 16, 32, 128
     cfg = _cfg(H=H, HV=HV, dk=d, dv=d, layer=1)
     B, T, slots = 3, 8, 40
     rows = B * T
-    inp = _backend_inputs(g, cfg, rows + 5, slots)
+    inp = _backend_inputs(g, cfg, rows + 5, slots, io)
     perm = torch.randperm(slots, generator=g)
     baseline = perm[:B]
     writes = perm[B:B + B * T].view(B, T)
@@ -476,7 +477,7 @@ def test_verify_group_matches_oracle(permute_rows):
     want = ref.forward_verify(inp["mixed"][row_idx], inp["gate"][row_idx], inp["beta"][row_idx], inp["weight"],
                               inp["A_log"], inp["dt_bias"], conv_ref, state_ref, 1, baseline, writes, H, d, HV, d)
     conv, state = inp["conv"].to(DEV), inp["state"].to(DEV)
-    out = torch.zeros(rows + 5, HV, d, device=DEV, dtype=torch.bfloat16)
+    out = torch.zeros(rows + 5, HV, d, device=DEV, dtype=io)
     verify_group(inp["mixed"].to(DEV), inp["gate"].to(DEV), inp["beta"].to(DEV), inp["weight"].to(DEV),
                  inp["A_log"].to(DEV), inp["dt_bias"].to(DEV), cfg, conv, state,
                  row_idx.to(DEV) if permute_rows else None, baseline.to(DEV), writes.to(DEV), out)
