@@ -92,14 +92,21 @@ def _kernel_ms(events):
 
 # ---------------------------------------------------------------- prefill (config 2)
 
-def make_prefill(seed=2, lengths=(4096, 4096, 4096, 4096)):
+def make_prefill(seed=2, lengths=(4096, 4096, 4096, 4096), draw_device="cpu"):
+    """Config 2's inputs (host tensors).  The projections (``mixed``, the
+    largest tensor) are drawn on ``draw_device`` with a generator of that
+    device seeded with ``seed`` and copied to the host, so a GPU box draws
+    config 4's 1.2 G values in milliseconds; the rest come from a CPU
+    generator.  Every consumer (bench, parity tests, CPU baseline) reads the
+    same host copy."""
     g = torch.Generator().manual_seed(seed)
     T = sum(lengths)
     N = len(lengths)
     cu = [0]
     for n in lengths:
         cu.append(cu[-1] + n)
-    mixed = torch.randn(T, CONV_DIM, generator=g).to(torch.bfloat16)
+    gm = torch.Generator(device=draw_device).manual_seed(seed)
+    mixed = torch.randn(T, CONV_DIM, generator=gm, device=draw_device).to(torch.bfloat16).cpu()
     weight = (torch.randn(CONV_DIM, 1, W, generator=g) * 0.02).to(torch.bfloat16)
     gate = torch.randn(T, HV, generator=g).to(torch.bfloat16)
     beta = torch.randn(T, HV, generator=g).to(torch.bfloat16)
@@ -119,7 +126,7 @@ def make_prefill(seed=2, lengths=(4096, 4096, 4096, 4096)):
                 conv_tokens=conv_tokens, snap_rows=snap_rows, snap_slots=torch.arange(N, dtype=torch.int64), N=N, T=T)
 
 
-def make_prefill_cfg4(seed=4, n=64, median=1500, sigma=1.0, every=1024, hit_rate=0.5):
+def make_prefill_cfg4(seed=4, n=64, median=1500, sigma=1.0, every=1024, hit_rate=0.5, draw_device="cpu"):
     """64 packed sequences with lognormal lengths (median
     1500, sigma 1.0, clipped to 16..16384); half of them (seeded choice)
     start from a cached state and conv history in a random pool slot
@@ -129,7 +136,7 @@ def make_prefill_cfg4(seed=4, n=64, median=1500, sigma=1.0, every=1024, hit_rate
     import numpy as np
     rng = np.random.default_rng(seed)
     lengths = np.clip(np.rint(rng.lognormal(np.log(median), sigma, n)), 16, 16384).astype(int).tolist()
-    inp = make_prefill(seed, lengths)
+    inp = make_prefill(seed, lengths, draw_device)
     N, T = inp["N"], inp["T"]
     hits = rng.permutation(N)[: int(round(hit_rate * N))]
     nck = sum(len(range(every, m, every)) + 1 for m in lengths)
@@ -149,29 +156,40 @@ def make_prefill_cfg4(seed=4, n=64, median=1500, sigma=1.0, every=1024, hit_rate
             snap_slots.append(slot)
         c0 += nc
         t0 += m
+    conv_tokens = torch.full((T,), -1, dtype=torch.int64)
+    conv_tokens[torch.tensor(rows)] = torch.tensor(snap_slots)
     inp.update(baseline=baseline, chunk_write=chunk_write, snap_rows=torch.tensor(rows),
-               snap_slots=torch.tensor(snap_slots), slots=len(slots), random_pools=seed, lengths=lengths,
-               checkpoints=len(rows))
+               snap_slots=torch.tensor(snap_slots), conv_tokens=conv_tokens, slots=len(slots), random_pools=seed,
+               lengths=lengths, checkpoints=len(rows))
     return inp
 
 
-def prefill_gpu(inp, dev, events=None, fused=True):
+def make_prefill_pools(inp, dev):
+    """The conv-window and fp32 state pools of a prefill workload: zeros, or
+    for config 4 (``random_pools`` = seed) N(0, 1) windows and N(0, 0.1)
+    states, the cached prefixes the hits resume from."""
+    slots = inp.get("slots", max(8, inp["N"]))
+    conv_pool = torch.zeros(slots, 1, CONV_DIM, W - 1, device=dev, dtype=torch.bfloat16)
+    state_pool = torch.zeros(slots, 1, HV, D, D, device=dev, dtype=torch.float32)
+    if inp.get("random_pools") is not None:
+        gd = torch.Generator(device=dev).manual_seed(int(inp["random_pools"]))
+        state_pool.normal_(0.0, 0.1, generator=gd)
+        conv_pool.copy_(torch.randn(conv_pool.shape, device=dev, generator=gd).to(torch.bfloat16))
+    return conv_pool, state_pool
+
+
+def prefill_gpu(inp, dev, events=None, fused=True, pools=None):
     """One backend prefill step.  fused: ``prefill_fused`` (q/k pass, then the
     chunk kernel computing the v conv + SiLU and the gates itself, then the
     conv-snapshot launch); otherwise the two-step path (``prefill_frontend``
-    writing q, k, v, g, beta, then the chunk kernel).  `events` collects a
-    (start, end) event pair around each chunk-kernel launch."""
+    writing q, k, v, g, beta and then the windows, then the chunk kernel).
+    `events` collects a (start, end) event pair around each chunk-kernel
+    launch; `pools` = (conv_pool, state_pool) to run on, else fresh ones."""
     from logssms_amd.kernel.linear_attention import ChunkStateIO, chunk_gated_delta_rule_to_cache
     from logssms_amd.kernel.linear_attention.fused_backend import prefill_frontend, prefill_fused
     cfg = _config()
     d = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
-    slots = d.get("slots", max(8, d["N"]))
-    conv_pool = torch.zeros(slots, 1, CONV_DIM, W - 1, device=dev, dtype=torch.bfloat16)
-    state_pool = torch.zeros(slots, 1, HV, D, D, device=dev, dtype=torch.float32)
-    if d.get("random_pools") is not None:  # cached states / conv histories of the prefix hits
-        gd = torch.Generator(device=dev).manual_seed(int(d["random_pools"]))
-        state_pool.normal_(0.0, 0.1, generator=gd)
-        conv_pool.copy_(torch.randn(conv_pool.shape, device=dev, generator=gd).to(torch.bfloat16))
+    conv_pool, state_pool = pools if pools is not None else make_prefill_pools(inp, dev)
     out = torch.empty(1, d["T"], HV, D, device=dev, dtype=torch.bfloat16)
     io = ChunkStateIO(state_pool, d["baseline"], d["chunk_write"], layer=0)
 
@@ -195,7 +213,8 @@ def prefill_gpu(inp, dev, events=None, fused=True):
             return out
         else:
             q, k, v, g, b = prefill_frontend(d["mixed"], d["gate"], d["beta"], d["weight"], d["A_log"],
-                                             d["dt_bias"], cfg, conv_pool, d["cu"], d["baseline"], d["conv_tokens"])
+                                             d["dt_bias"], cfg, conv_pool, d["cu"], d["baseline"], d["snap_rows"],
+                                             d["snap_slots"])
             s = mark()
             chunk_gated_delta_rule_to_cache(q, k, v, g, b, io, d["cu"], out=out, return_v_new=False)
             if events is not None:
@@ -374,7 +393,7 @@ def main():
         return
 
     if args.only in ("all", "prefill"):
-        inp = make_prefill()
+        inp = make_prefill(draw_device=dev)
         events = []
         step, state_pool, out = prefill_gpu(inp, dev, events)
         ms = _time(step, args.steps, args.warmup, events)
@@ -423,7 +442,7 @@ def main():
             torch.set_num_threads(threads)
         del step, inp
         torch.cuda.empty_cache()
-        inp4 = make_prefill_cfg4()
+        inp4 = make_prefill_cfg4(draw_device=dev)
         ev4 = []
         step4, _, _ = prefill_gpu(inp4, dev, ev4)
         ms4 = _time(step4, max(args.steps // 2, 5), args.warmup, ev4)

@@ -81,21 +81,23 @@ int gdn_prepare(const void* query, const int64_t* qs, const void* key, const int
 /*
  * Fused prefill front end (one pass over mixed_qkv): conv-history gather from
  * the conv pool (layers/linear_attention_backend/gdn.py:107-113), packed conv +
- * SiLU + window snapshots (packed_conv.py), q/k/v split (gdn.py:51-72) and
- * prepare_gdn (fused.py).  Bitwise the same rounding chain as running the two
- * reference ops back to back.
+ * SiLU (packed_conv.py), q/k/v split (gdn.py:51-72) and prepare_gdn
+ * (fused.py).  Bitwise the same rounding chain as running the two reference
+ * ops back to back.  The conv windows are not written here: a window slot may
+ * be the baseline slot another workgroup of this launch still reads its
+ * history from (a prefill resuming mid-page), so the caller writes them with
+ * gdn_conv_snapshots after this launch, as the reference gathers the history
+ * before its conv writes any window (gdn.py:107-112).
  *   mixed [T, C] strided, C = 2*H*dk + HV*dv; gate/beta [T, HV] strided (2 strides).
- *   conv_state [slots, L, C, W-1]; baseline_slots[N] (<0: zero history);
- *   token_slots[T] or NULL (snapshot destinations).
+ *   conv_state [slots, L, C, W-1] (read only); baseline_slots[N] (<0: zero history).
  *   Outputs: q_out/k_out [T, H, dk], v_out [T, HV, dv] (dtype), g_out/beta_out [T, HV] fp32.
  */
 int gdn_prefill_frontend(const void* mixed, int64_t row_stride, int64_t col_stride, int dtype,
                          const void* weight, const void* bias, int kernel_width, const void* cu_seqlens,
                          int cu_dtype, int64_t num_seqs, int64_t total_tokens, int64_t H, int64_t HV,
-                         int64_t dk, int64_t dv, void* conv_state, int64_t state_slot_stride,
+                         int64_t dk, int64_t dv, const void* conv_state, int64_t state_slot_stride,
                          int64_t state_layer_stride, int64_t layer, const void* baseline_slots,
-                         int baseline_dtype, const void* token_slots, int token_slots_dtype,
-                         const void* gate, int64_t gate_row_stride, int64_t gate_head_stride,
+                         int baseline_dtype, const void* gate, int64_t gate_row_stride, int64_t gate_head_stride,
                          int gate_dtype, const void* beta, int64_t beta_row_stride,
                          int64_t beta_head_stride, int beta_dtype, const void* A_log, int a_dtype,
                          const void* dt_bias, int dt_dtype, void* q_out, void* k_out, void* v_out,

@@ -29,7 +29,7 @@ SIGNATURES = {
     "gdn_prepare": [P, PI64, P, PI64, P, PI64, I32, P, PI64, I32, P, PI64, I32, P, I64, I32, P, I64, I32,
                     I64, I64, I64, I64, I64, I64, P, P, P, P, P, P],
     "gdn_prefill_frontend": [P, I64, I64, I32, P, P, I32, P, I32, I64, I64, I64, I64, I64, I64, P, I64, I64,
-                             I64, P, I32, P, I32, P, I64, I64, I32, P, I64, I64, I32, P, I32, P, I32, P, P,
+                             I64, P, I32, P, I64, I64, I32, P, I64, I64, I32, P, I32, P, I32, P, P,
                              P, P, P, P],
     "gdn_prefill_qk": [P, I64, I32, P, I32, P, I32, I64, I64, I64, I64, P, I64, I64, I64, P, I32, P, P, I32, I64,
                        P, I64, I64, I32, P, I64, I64, I32, P, I32, P, I32, P, P, P],

@@ -607,10 +607,9 @@ extern "C" int gdn_packed_causal_conv1d(const void* x, int64_t x_row_stride, int
 extern "C" int gdn_prefill_frontend(const void* mixed, int64_t row_stride, int64_t col_stride, int dtype,
                                     const void* weight, const void* bias, int kernel_width, const void* cu_seqlens,
                                     int cu_dtype, int64_t num_seqs, int64_t total_tokens, int64_t H, int64_t HV,
-                                    int64_t dk, int64_t dv, void* conv_state, int64_t state_slot_stride,
+                                    int64_t dk, int64_t dv, const void* conv_state, int64_t state_slot_stride,
                                     int64_t state_layer_stride, int64_t layer, const void* baseline_slots,
-                                    int baseline_dtype, const void* token_slots, int token_slots_dtype,
-                                    const void* gate, int64_t gate_row_stride, int64_t gate_head_stride,
+                                    int baseline_dtype, const void* gate, int64_t gate_row_stride, int64_t gate_head_stride,
                                     int gate_dtype, const void* beta, int64_t beta_row_stride,
                                     int64_t beta_head_stride, int beta_dtype, const void* A_log, int a_dtype,
                                     const void* dt_bias, int dt_dtype, void* q_out, void* k_out, void* v_out,
@@ -627,9 +626,11 @@ extern "C" int gdn_prefill_frontend(const void* mixed, int64_t row_stride, int64
   ConvParams p{};
   p.x = mixed; p.xr = row_stride; p.xc = col_stride; p.w = weight; p.bias = bias; p.history = nullptr;
   p.cu = cu_seqlens; p.cu_is64 = cu_dtype == GDN_I64; p.N = num_seqs; p.T = total_tokens; p.C = channels;
-  p.W = kernel_width; p.out = nullptr; p.state = conv_state; p.slot_stride = state_slot_stride;
-  p.layer_stride = state_layer_stride; p.layer = layer; p.token_slots = token_slots;
-  p.token_is64 = token_slots_dtype == GDN_I64; p.final_slots = nullptr; p.final_is64 = 0;
+  // conv_state is only read (history); token_slots / final_slots stay null so
+  // no window is written in this launch
+  p.W = kernel_width; p.out = nullptr; p.state = const_cast<void*>(conv_state); p.slot_stride = state_slot_stride;
+  p.layer_stride = state_layer_stride; p.layer = layer; p.token_slots = nullptr;
+  p.token_is64 = 0; p.final_slots = nullptr; p.final_is64 = 0;
   p.baseline = baseline_slots; p.baseline_is64 = baseline_dtype == GDN_I64;
   p.end0 = channels; p.end1 = channels; p.s0 = p.s1 = p.s2 = 1.f;
   FrontParams fp{};

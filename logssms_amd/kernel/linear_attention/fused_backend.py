@@ -6,9 +6,9 @@ smallest number of gfx950 kernels.
 * ``prefill_fused`` -- the whole prefill (``gdn.py:100-150``): a q/k pass,
   the chunk kernel computing the v conv + SiLU and the gates in its staging
   waves, and a small conv-snapshot launch.
-* ``prefill_frontend`` -- conv-history gather + packed conv + snapshots + split
-  + ``prepare_gdn`` in one pass over ``mixed_qkv`` (``gdn.py:100-132``), for
-  shapes outside the fused kernel.
+* ``prefill_frontend`` -- conv-history gather + packed conv + split +
+  ``prepare_gdn`` in one pass over ``mixed_qkv`` (``gdn.py:100-132``), then
+  the window snapshots, for shapes outside the fused kernel.
 * ``decode_step`` -- ``conv_decode`` + slotted recurrent update in one kernel
   (``gdn.py:222-265``).
 * ``verify_group`` -- one verify length group: conv over the drafts, conv
@@ -34,15 +34,22 @@ def _check_pools(conv_state: torch.Tensor, recurrent_state: torch.Tensor | None,
 
 
 def prefill_frontend(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, conv_state, cu_seqlens,
-                     baseline_slots, conv_token_slots=None):
+                     baseline_slots, snapshot_rows=None, snapshot_slots=None):
     """Returns ``(q [1,T,H,dk], k, v [1,T,HV,dv], g [1,T,HV] fp32, beta fp32)``
     exactly as ``prepare_gdn(split(packed_causal_conv1d(...)))`` would, with
     the conv history read from ``conv_state[baseline_slots, layer]`` (zeros for
-    negative slots) and windows written to ``conv_state[conv_token_slots[t]]``."""
+    negative slots).  The window of packed row ``snapshot_rows[i]`` then goes
+    to ``conv_state[snapshot_slots[i]]`` (negative slots skipped) in a second
+    launch, after every history has been read: a window slot may equal a
+    baseline slot (a prefill resuming mid-page writes its checkpoint to the
+    page it resumed from), and the reference reads all histories before any
+    window is written (``gdn.py:107-112`` gathers them with ``index_select``)."""
     T, C = mixed_qkv.shape
     assert C == config.conv_dim == 2 * config.key_dim + config.value_dim
     assert gate.shape == beta.shape == (T, config.num_v_heads)
     _check_pools(conv_state, None, config)
+    if snapshot_rows is not None:
+        assert snapshot_slots is not None and snapshot_rows.shape == snapshot_slots.shape and snapshot_rows.ndim == 1
     dev, dt = mixed_qkv.device, mixed_qkv.dtype
     q = torch.empty(1, T, config.num_k_heads, config.head_k_dim, device=dev, dtype=dt)
     k = torch.empty_like(q)
@@ -61,13 +68,48 @@ def prefill_frontend(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config,
         len(cu_seqlens) - 1, T, config.num_k_heads, config.num_v_heads, config.head_k_dim, config.head_v_dim,
         conv_state.data_ptr(), conv_state.stride(0), conv_state.stride(1), config.layer_idx,
         baseline_slots.data_ptr(), _lib.index_code(baseline_slots),
-        _lib.ptr(conv_token_slots), _lib.index_code(conv_token_slots) if conv_token_slots is not None else 0,
         gate.data_ptr(), gate.stride(0), gate.stride(1), _lib.dtype_code(gate.dtype),
         beta.data_ptr(), beta.stride(0), beta.stride(1), _lib.dtype_code(beta.dtype),
         A_log.data_ptr(), _lib.dtype_code(A_log.dtype), dt_bias.data_ptr(), _lib.dtype_code(dt_bias.dtype),
         q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), b.data_ptr(), _lib.stream_of(mixed_qkv),
     )
+    if snapshot_rows is not None:
+        conv_snapshots(mixed_qkv, config, conv_state, cu_seqlens, baseline_slots, snapshot_rows, snapshot_slots)
     return q, k, v, g, b
+
+
+def conv_snapshots(mixed_qkv, config, conv_state, cu_seqlens, baseline_slots, rows, slots):
+    """``conv_state[slots[i], layer] <- `` the raw conv window ending at packed
+    row ``rows[i]`` (history from ``baseline_slots`` before the sequence start;
+    negative slots skipped).  16-bit inputs with unit column stride."""
+    if not rows.numel():
+        return
+    assert mixed_qkv.stride(1) == 1 and mixed_qkv.dtype in (torch.bfloat16, torch.float16)
+    _lib.call("gdn_conv_snapshots", mixed_qkv.data_ptr(), mixed_qkv.stride(0), _lib.dtype_code(mixed_qkv.dtype),
+              cu_seqlens.data_ptr(), _lib.index_code(cu_seqlens), len(cu_seqlens) - 1, mixed_qkv.shape[0],
+              mixed_qkv.shape[1], config.state_len + 1, conv_state.data_ptr(), conv_state.stride(0),
+              conv_state.stride(1), config.layer_idx, baseline_slots.data_ptr(), _lib.index_code(baseline_slots),
+              rows.data_ptr(), _lib.index_code(rows), slots.data_ptr(), _lib.index_code(slots), rows.numel(),
+              _lib.stream_of(mixed_qkv))
+
+
+def _aligned16(t: torch.Tensor) -> bool:
+    return t.data_ptr() % 16 == 0
+
+
+def _fused_covered(mixed_qkv, config, conv_state, recurrent_state) -> bool:
+    """The shapes ``gdn_prefill_qk`` and ``gdn_prefill_fused`` take (checked
+    before the first launch, so an uncovered shape launches nothing and the
+    two-step path runs instead): conv width 4, d_k in {32, 64, 128}, d_v a
+    multiple of 64, 16-bit io with unit-stride 16-byte-aligned rows, a
+    16-byte-aligned conv pool whose slot and layer strides keep that
+    alignment, and an fp32 or io-typed state pool."""
+    return (config.state_len == 3 and config.head_k_dim in (32, 64, 128) and config.head_v_dim % 64 == 0
+            and mixed_qkv.dtype in (torch.bfloat16, torch.float16) and mixed_qkv.stride(1) == 1
+            and mixed_qkv.stride(0) % 8 == 0 and _aligned16(mixed_qkv) and _aligned16(conv_state)
+            and conv_state.stride(0) % 8 == 0 and conv_state.stride(1) % 8 == 0
+            and conv_state.dtype == mixed_qkv.dtype
+            and recurrent_state.dtype in (torch.float32, mixed_qkv.dtype))
 
 
 def prefill_fused(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, conv_state, recurrent_state,
@@ -91,14 +133,12 @@ def prefill_fused(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, co
     assert gate.shape == beta.shape == (T, config.num_v_heads)
     _check_pools(conv_state, recurrent_state, config)
     assert snapshot_rows.shape == snapshot_slots.shape and snapshot_rows.ndim == 1
-    if (mixed_qkv.stride(1) != 1 or config.state_len != 3 or config.head_v_dim % 64
-            or config.head_k_dim not in (32, 64, 128) or mixed_qkv.dtype not in (torch.bfloat16, torch.float16)
-            or recurrent_state.dtype not in (torch.float32, mixed_qkv.dtype)):
+    weight = conv_weight.contiguous()
+    if not (_fused_covered(mixed_qkv, config, conv_state, recurrent_state) and _aligned16(weight)):
         return None
     if out is None:
         out = torch.empty(T, config.num_v_heads, config.head_v_dim, device=mixed_qkv.device, dtype=mixed_qkv.dtype)
     assert out.shape == (T, config.num_v_heads, config.head_v_dim) and out.is_contiguous()
-    weight = conv_weight.contiguous()
     A_log = A_log.contiguous()
     dt_bias = dt_bias.contiguous()
     # q, k as the chunk kernel's f16 MFMA operands; prepared gates
@@ -126,12 +166,7 @@ def prefill_fused(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, co
                         baseline_slots, chunk_write_slots, out)
     if chunk_events is not None:
         chunk_events[1].record()
-    if snapshot_rows.numel():
-        _lib.call("gdn_conv_snapshots", mixed_qkv.data_ptr(), mixed_qkv.stride(0), _lib.dtype_code(mixed_qkv.dtype),
-                  cu_seqlens.data_ptr(), _lib.index_code(cu_seqlens), N, T, C, 4, conv_state.data_ptr(),
-                  conv_state.stride(0), conv_state.stride(1), config.layer_idx, baseline_slots.data_ptr(),
-                  _lib.index_code(baseline_slots), snapshot_rows.data_ptr(), _lib.index_code(snapshot_rows),
-                  snapshot_slots.data_ptr(), _lib.index_code(snapshot_slots), snapshot_rows.numel(), stream)
+    conv_snapshots(mixed_qkv, config, conv_state, cu_seqlens, baseline_slots, snapshot_rows, snapshot_slots)
     return out
 
 
@@ -217,4 +252,4 @@ def verify_group(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, con
     return output
 
 
-__all__ = ["decode_step", "prefill_chunk_fused", "prefill_frontend", "prefill_fused", "verify_group"]
+__all__ = ["conv_snapshots", "decode_step", "prefill_chunk_fused", "prefill_frontend", "prefill_fused", "verify_group"]

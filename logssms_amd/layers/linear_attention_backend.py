@@ -277,7 +277,8 @@ class GatedDeltaBackend:
         if o is not None:
             return o
         q, k, v, g, b = prefill_frontend(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, pool.conv_state,
-                                         idx.cu_seqlens, metadata.baseline_slots, metadata.conv_token_slots)
+                                         idx.cu_seqlens, metadata.baseline_slots, metadata.snapshot_rows,
+                                         metadata.checkpoint_slots)
         io = ChunkStateIO(storage=pool.recurrent_state, read_slots=metadata.baseline_slots,
                           chunk_write_slots=metadata.chunk_write_slots, layer=config.layer_idx)
         o, _ = chunk_gated_delta_rule_to_cache(q, k, v, g, b, io, idx.cu_seqlens, out=None if out is None else

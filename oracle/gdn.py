@@ -107,13 +107,15 @@ def _scale_inputs(values: torch.Tensor, channels: torch.Tensor, boundaries, scal
 
 
 def packed_causal_conv1d(x, weight, history, cu_seqlens, bias=None, *,
-                         input_boundaries=None, input_scales=(1.0, 1.0, 1.0)):
+                         input_boundaries=None, input_scales=(1.0, 1.0, 1.0), window_rows=None):
     """kernel/linear_attention/packed_conv.py:53-140 (wrapper :143-192).
 
     x [T, C] (any dtype), weight [C, 1, W], history [N, C, W-1].
     Returns (y [T, C] in x.dtype, windows [T, C, W-1]) where ``windows[t]`` is
     the raw (scaled) input window ``[x_{t-W+2}, ..., x_t]`` that the kernel
-    scatters to ``slots[t] >= 0`` (``:112-123``).
+    scatters to ``slots[t] >= 0`` (``:112-123``).  With ``window_rows`` (a
+    list of packed rows) only those windows are kept: ``windows[i]`` is the
+    window of row ``window_rows[i]`` (large inputs need not hold all T).
     """
     T, C = x.shape
     K = weight.shape[-1]
@@ -123,7 +125,8 @@ def packed_causal_conv1d(x, weight, history, cu_seqlens, bias=None, *,
         input_boundaries = (C, C)
     xs = _scale_inputs(x, channels[None, :], input_boundaries, input_scales)
     y = torch.empty(T, C, dtype=x.dtype)
-    windows = torch.empty(T, C, S, dtype=x.dtype)
+    rows = list(range(T)) if window_rows is None else [int(t) for t in window_rows]
+    windows = torch.empty(len(rows), C, S, dtype=x.dtype)
     acc_t = _acc_dtype(x.dtype)
     w = weight.reshape(C, K).to(acc_t)
     cu = [int(v) for v in cu_seqlens]
@@ -131,15 +134,21 @@ def packed_causal_conv1d(x, weight, history, cu_seqlens, bias=None, *,
         b, e = cu[r], cu[r + 1]
         src = torch.cat([history[r].T.to(x.dtype), xs[b:e]], 0)  # [S + L, C]
         L = e - b
+        src_acc = src.to(acc_t)
         acc = torch.zeros(L, C, dtype=acc_t)
         for tap in range(K):
-            acc = acc + src[tap:tap + L].to(acc_t) * w[None, :, tap]
+            acc = acc + src_acc[tap:tap + L] * w[None, :, tap]
         if bias is not None:
             acc = acc + bias.to(acc_t)[None, :]
         acc = acc.to(x.dtype).to(acc_t)
         y[b:e] = silu(acc).to(x.dtype)
-        for tap in range(1, K):
-            windows[b:e, :, tap - 1] = src[tap:tap + L]
+        if window_rows is None:
+            for tap in range(1, K):
+                windows[b:e, :, tap - 1] = src[tap:tap + L]
+            continue
+        for i, t in enumerate(rows):
+            if b <= t < e:  # src row (t - b) + tap holds x_{t - S + tap}
+                windows[i] = src[t - b + 1:t - b + K].T
     return y, windows
 
 
@@ -238,7 +247,7 @@ def naive_recurrence(q, k, v, g, beta, scale, state0, *, checkpoint_every=None):
     return out, state, checkpoints
 
 
-def chunk_gdn(q, k, v, g, beta, scale, state0, chunk_size=64, rcp_ln2=RCP_LN2):
+def chunk_gdn(q, k, v, g, beta, scale, state0, chunk_size=64, rcp_ln2=RCP_LN2, on_chunk_end=None):
     """The chunked (WY/UT) gated delta rule of one sequence, restating the
     reference pipeline ``vendor/fla/gated_delta.py:15-82``:
 
@@ -252,15 +261,18 @@ def chunk_gdn(q, k, v, g, beta, scale, state0, chunk_size=64, rcp_ln2=RCP_LN2):
     Shapes as in ``naive_recurrence``.  Returns (o, v_new, chunk_end_states
     [NT, HV, dk, dv], final state).  ``rcp_ln2`` defaults to the reference's
     truncated constant (relative exponent error 1.3e-8 against ``1/ln 2``).
+    With ``on_chunk_end(i, h)`` each chunk-end state is handed to the callback
+    instead and ``chunk_end_states`` comes back empty.
     """
     dt = state0.dtype
     T = q.shape[0]
     HV = v.shape[1]
-    qe = _expand_heads(q.to(dt), HV).transpose(0, 1)  # [HV, T, dk]
-    ke = _expand_heads(k.to(dt), HV).transpose(0, 1)
-    ve = v.to(dt).transpose(0, 1)  # [HV, T, dv]
-    ge = g.to(dt).transpose(0, 1)  # [HV, T]
-    be = beta.to(dt).transpose(0, 1)
+    # head-major copies, so every chunk below is a contiguous slab
+    qe = _expand_heads(q.to(dt), HV).transpose(0, 1).contiguous()  # [HV, T, dk]
+    ke = _expand_heads(k.to(dt), HV).transpose(0, 1).contiguous()
+    ve = v.to(dt).transpose(0, 1).contiguous()  # [HV, T, dv]
+    ge = g.to(dt).transpose(0, 1).contiguous()  # [HV, T]
+    be = beta.to(dt).transpose(0, 1).contiguous()
     h = state0.clone()
     o = torch.empty(HV, T, v.shape[-1], dtype=dt)
     v_new = torch.empty_like(o)
@@ -287,7 +299,10 @@ def chunk_gdn(q, k, v, g, beta, scale, state0, chunk_size=64, rcp_ln2=RCP_LN2):
         g_last = G[:, -1]
         h = torch.exp2(g_last)[:, None, None] * h + kc.transpose(1, 2) @ (
             torch.exp2(g_last[:, None] - G)[:, :, None] * vn)
-        ends.append(h.clone())
+        if on_chunk_end is not None:
+            on_chunk_end(c0 // chunk_size, h)
+        else:
+            ends.append(h.clone())
     end_states = torch.stack(ends) if ends else torch.empty(0, *h.shape, dtype=dt)
     return o.transpose(0, 1), v_new.transpose(0, 1), end_states, h
 
@@ -324,15 +339,17 @@ def chunk_gated_delta_rule_to_cache(query, key, value, gate, beta, storage, read
             s0 = storage[slot, layer].to(dtype)
         else:
             s0 = torch.zeros(HV, dk, dv, dtype=dtype)
-        on, vn, ends, final = chunk_gdn(query[0, b:e], key[0, b:e], value[0, b:e],
-                                         gate[0, b:e], beta[0, b:e], scale, s0, chunk_size)
+        def write_end(i, h, first=chunk):
+            ws = int(chunk_write_slots[first + i])
+            if ws >= 0:
+                storage[ws, layer] = h.to(storage.dtype)
+
+        on, vn, _, final = chunk_gdn(query[0, b:e], key[0, b:e], value[0, b:e],
+                                     gate[0, b:e], beta[0, b:e], scale, s0, chunk_size,
+                                     on_chunk_end=write_end)
         o[0, b:e] = on.to(value.dtype)
         v_new[0, b:e] = vn.to(value.dtype)
-        for i in range(ends.shape[0]):
-            ws = int(chunk_write_slots[chunk + i])
-            if ws >= 0:
-                storage[ws, layer] = ends[i].to(storage.dtype)
-        chunk += ends.shape[0]
+        chunk += (e - b + chunk_size - 1) // chunk_size
         if final_write_slots is not None and int(final_write_slots[n]) >= 0:
             storage[int(final_write_slots[n]), layer] = final.to(storage.dtype)
     return o, v_new
@@ -425,10 +442,11 @@ def forward_prefill(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, conv_sta
         s = int(baseline_slots[n])
         if s >= 0:
             history[n] = conv_state[s, layer]
-    y, windows = packed_causal_conv1d(mixed_qkv, conv_weight, history, cu_seqlens)
-    for t, s in enumerate(int(x) for x in conv_token_slots):
-        if s >= 0:
-            conv_state[s, layer] = windows[t]
+    token_slots = [int(x) for x in conv_token_slots]
+    rows = [t for t, s in enumerate(token_slots) if s >= 0]
+    y, windows = packed_causal_conv1d(mixed_qkv, conv_weight, history, cu_seqlens, window_rows=rows)
+    for i, t in enumerate(rows):
+        conv_state[token_slots[t], layer] = windows[i]
     q, k, v = split_qkv(y[None], num_k_heads, head_k_dim, num_v_heads, head_v_dim)
     q, k, v, g, b = prepare_gdn(q, k, v, gate[None], beta[None], A_log, dt_bias)
     o, _ = chunk_gated_delta_rule_to_cache(q, k, v, g, b, recurrent_state, baseline_slots,

@@ -297,3 +297,37 @@ def test_marconi_backend_prefill_matches_standard_pool():
                                    rtol=0, atol=0)
         torch.testing.assert_close(hybrid.conv_state[blk, lane], plain.conv_state[s, cfg.layer_idx], rtol=0, atol=0)
         assert hybrid.recurrent_state[blk, lane].abs().sum() > 0
+
+
+@pytest.mark.parametrize("dims", [(128, 128), (32, 32)], ids=["fused_dv128", "two_step_dv32"])
+def test_prefill_resuming_mid_page_writes_windows_after_reading_history(dims):
+    """Page size 256 with prefixes cached to 64 and 192 tokens: a short
+    extension's only checkpoint lands on the page the prefill resumed from,
+    so its window slot is the baseline slot whose history the same prefill
+    reads (``gdn.py:107-112`` gathers every history before any window is
+    written).  d_v = 128 runs the fused path, d_v = 32 the two-step path."""
+    from logssms_amd.core import Batch, Context, Request
+    dk, dv = dims
+    g = gen(77 + dk)
+    cfg = _cfg(H=2, HV=4, dk=dk, dv=dv, layer=1)
+    page = 256
+    reqs = [(0, 64, 100), (1, 128, 200), (2, 0, 70), (3, 192, 64), (4, 64, 1)]
+    slots = 32
+    perm = torch.randperm(slots, generator=g).tolist()
+    table = [[perm[(3 * i + p // page) % slots] for p in range(1024)] for i in range(5)]
+    meta = md.prefill_metadata(table, reqs, page)
+    aliased = [n for n, (t, c, e) in enumerate(reqs) if c and table[t][c - 1] == table[t][c + e - 1]]
+    assert aliased == [0, 3, 4]
+    T = sum(e for _, _, e in reqs)
+    w = _weights(g, cfg, T)
+    pool = _pool(cfg, slots, g=g)
+    conv_ref, state_ref = pool.conv_state.cpu(), pool.recurrent_state.cpu()
+    cu = md.from_lengths([e for _, _, e in reqs])["cu_seqlens"]
+    want = ref.forward_prefill(w["mixed"], w["gate"], w["beta"], w["weight"], w["A_log"], w["dt_bias"], conv_ref,
+                               state_ref, 1, torch.tensor(cu), meta["baseline_slots"], meta["chunk_write_slots"],
+                               meta["conv_token_slots"], 2, dk, 4, dv)
+    ctx = Context(page_size=page, linear_state=pool, state_table=torch.tensor(table, device=DEV))
+    got = _forward(ctx, Batch(reqs=[Request(t, c, c + e) for t, c, e in reqs], phase="prefill"), w, cfg)
+    assert_bf16_close(got, want)
+    torch.testing.assert_close(pool.conv_state.cpu(), conv_ref, rtol=0, atol=0)
+    assert_state_close(pool.recurrent_state, state_ref)

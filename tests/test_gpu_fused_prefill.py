@@ -68,12 +68,8 @@ def _two_step(cfg, pool, w, meta):
     from logssms_amd.kernel.linear_attention.fused_backend import prefill_frontend
     from logssms_amd.kernel.linear_attention.gdn import chunk_gated_delta_rule_to_cache
     from logssms_amd.kernel.linear_attention.state_io import ChunkStateIO
-    T = w["mixed"].shape[0]
-    token_slots = torch.full((T,), -1, dtype=torch.int64, device=DEV)
-    keep = meta["snap_slots"] >= 0
-    token_slots[meta["rows"][keep]] = meta["snap_slots"][keep]
     q, k, v, g, b = prefill_frontend(w["mixed"], w["gate"], w["beta"], w["weight"], w["A_log"], w["dt_bias"], cfg,
-                                     pool.conv_state, meta["cu"], meta["baseline"], token_slots)
+                                     pool.conv_state, meta["cu"], meta["baseline"], meta["rows"], meta["snap_slots"])
     io = ChunkStateIO(storage=pool.recurrent_state, read_slots=meta["baseline"], chunk_write_slots=meta["chunk_write"],
                       layer=cfg.layer_idx)
     o, _ = chunk_gated_delta_rule_to_cache(q, k, v, g, b, io, meta["cu"], return_v_new=False)

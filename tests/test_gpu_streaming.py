@@ -293,9 +293,10 @@ def test_prefill_frontend_matches_conv_then_prepare(dk):
         if s >= 0:
             expected_pool[s, 1] = windows[t]
     pool = conv_state.to(DEV)
+    rows = (token_slots >= 0).nonzero().flatten()
     got = prefill_frontend(mixed.to(DEV), gate.to(DEV), beta.to(DEV), weight.to(DEV), A_log.to(DEV),
                            dt_bias.to(DEV), cfg, pool, torch.tensor(cu, device=DEV), baseline.to(DEV),
-                           token_slots.to(DEV))
+                           rows.to(DEV), token_slots[rows].to(DEV))
     for x, w in zip(got[:3], want[:3]):
         assert_bf16_close(x, w, rel=1e-2, atol=1e-2)
     for x, w in zip(got[3:], want[3:]):

@@ -298,3 +298,205 @@ def test_rms_norm_gated_closed_forms():
                                rtol=1e-5, atol=1e-6)
     swapped = gdn.rms_norm_gated(x, z.flip(0), w, 1e-5)
     assert not torch.allclose(swapped, gdn.rms_norm_gated(x, z, w, 1e-5))
+
+
+def test_packed_conv_window_rows_select_the_same_windows():
+    gen = torch.Generator().manual_seed(32)
+    cu = [0, 3, 70, 72]
+    C, W = 24, 4
+    x = torch.randn(cu[-1], C, generator=gen).to(torch.bfloat16)
+    weight = (torch.randn(C, 1, W, generator=gen) * 0.2).to(torch.bfloat16)
+    history = torch.randn(3, C, W - 1, generator=gen).to(torch.bfloat16)
+    y, windows = gdn.packed_causal_conv1d(x, weight, history, cu)
+    rows = [71, 0, 2, 63, 3]
+    y2, some = gdn.packed_causal_conv1d(x, weight, history, cu, window_rows=rows)
+    assert torch.equal(y, y2)
+    assert torch.equal(some, windows[rows])
+
+
+# ---------------------------------------------------------------- slot I/O and compositions
+
+def test_store_state_matches_index_copy():
+    """kernel/store.py:69-83: ``pool[idx[i]] = states[i]`` for idx >= 0,
+    pinned by ``Tensor.index_copy_`` (a library routine)."""
+    gen = torch.Generator().manual_seed(50)
+    pool = torch.randn(7, 2, 3, 5, generator=gen)
+    states = torch.randn(4, 2, 3, 5, generator=gen)
+    for dtype in (torch.int64, torch.int32):
+        idx = torch.tensor([5, -1, 0, 3], dtype=dtype)
+        got = pool.clone()
+        gdn.store_state(got, idx, states)
+        keep = idx >= 0
+        want = pool.clone().view(7, -1).index_copy_(0, idx[keep].long(), states.view(4, -1)[keep]).view(pool.shape)
+        assert torch.equal(got, want)
+
+
+def test_fused_recurrent_to_slots_equals_gather_recurrence_scatter():
+    """``fused_recurrent.py:396-458`` slotted mode: gather the read slots
+    (``index_select``), one token recurrence per sequence (pinned by closed
+    forms above), normalisation with ``sqrt`` and division, softplus from
+    ``math.log1p``, then scatter to the write slots (``index_copy_``); an
+    in-place slot, a shared read slot and untouched slots included."""
+    gen = torch.Generator().manual_seed(51)
+    B, H, HV, dk, dv, layer = 3, 2, 4, 8, 6, 1
+    q = _normal(B, 1, H, dk, gen=gen)
+    k = _normal(B, 1, H, dk, gen=gen)
+    v = _normal(B, 1, HV, dv, gen=gen)
+    gate = _normal(B, 1, HV, gen=gen)
+    beta = _normal(B, 1, HV, gen=gen)
+    A_log = _normal(HV, gen=gen) * 0.3
+    dt_bias = _normal(HV, gen=gen) * 0.3
+    pool = _normal(6, 2, HV, dk, dv, gen=gen)
+    reads, writes = torch.tensor([1, 3, 3]), torch.tensor([1, 4, 0])
+    before = pool.clone()
+    o = gdn.fused_recurrent_to_slots(q, k, v, gate, beta, A_log, dt_bias, pool, reads, writes, layer,
+                                     dtype=torch.float64)
+    init = before.index_select(0, reads)[:, layer]
+    expected = before.clone()
+    for b in range(B):
+        qn = q[b, 0] / torch.sqrt((q[b, 0] ** 2).sum(-1, keepdim=True) + 1e-6)
+        kn = k[b, 0] / torch.sqrt((k[b, 0] ** 2).sum(-1, keepdim=True) + 1e-6)
+        sp = torch.tensor([math.log1p(math.exp(float(x))) for x in gate[b, 0] + dt_bias], dtype=torch.float64)
+        g = -torch.exp(A_log) * sp
+        o_ref, s_ref, _ = gdn.naive_recurrence(qn[None], kn[None], v[b], g[None],
+                                               (1.0 / (1.0 + torch.exp(-beta[b, 0])))[None], dk ** -0.5, init[b])
+        torch.testing.assert_close(o[b, 0], o_ref[0], rtol=1e-12, atol=1e-12)
+        expected[:, layer].index_copy_(0, writes[b:b + 1], s_ref[None])
+    torch.testing.assert_close(pool, expected, rtol=1e-12, atol=1e-12)
+    assert torch.equal(pool[2], before[2]) and torch.equal(pool[5], before[5])
+    assert torch.equal(pool[:, 0], before[:, 0])
+
+
+@pytest.mark.parametrize("decode", [False, True])
+def test_partitioned_input_scales_closed_form(decode):
+    """``_scale_inputs`` against the closed form of the reference's
+    ``tests/layers/test_conv_decode.py:185-222``: each channel range scaled
+    (and rounded to the input dtype) once, then ``silu(conv1d(...))`` with
+    bias; snapshots are the scaled raw windows."""
+    gen = torch.Generator().manual_seed(87)
+    scales, widths = (0.7, 0.8, 0.9), (256, 128, 128)
+    C = sum(widths)
+    bounds = (256, 384)
+    lengths = [1, 1] if decode else [7, 16]
+    raw = (torch.randn(sum(lengths), C + 32, generator=gen).to(torch.bfloat16))[:, :C]
+    scaled = torch.cat([part * s for part, s in zip(raw.split(widths, -1), scales)], -1)
+    history = torch.randn(2, C, 3, generator=gen).to(torch.bfloat16)
+    weight = (torch.randn(C, 1, 4, generator=gen) * 0.2).to(torch.bfloat16)
+    bias = (torch.randn(C, generator=gen) * 0.1).to(torch.bfloat16)
+    expected, snapshots, begin = [], [], 0
+    for i, length in enumerate(lengths):
+        source = torch.cat((history[i:i + 1], scaled[begin:begin + length].T[None]), -1)
+        expected.append(F.silu(F.conv1d(source.float(), weight.float(), bias.float(), groups=C))[0].T)
+        snapshots.append(source[0, :, -3:])
+        begin += length
+    if decode:
+        storage = torch.zeros(4, 1, C, 3, dtype=torch.bfloat16)
+        storage[:2, 0] = history
+        got = gdn.conv_decode(raw, weight, storage, 0, [0, 1], [2, 3], bias=bias, round_conv=True,
+                              input_boundaries=bounds, input_scales=scales)
+        windows = storage[2:, 0]
+    else:
+        got, windows = gdn.packed_causal_conv1d(raw, weight, history, [0, 7, 23], bias, input_boundaries=bounds,
+                                                input_scales=scales, window_rows=[6, 22])
+    torch.testing.assert_close(got.float(), torch.cat(expected), rtol=2e-2, atol=2e-2)
+    assert torch.equal(windows, torch.stack(snapshots))
+    # unscaled inputs would miss the closed form: the scales are applied
+    plain = gdn.packed_causal_conv1d(raw, weight, history, [0, 7, 23] if not decode else [0, 1, 2], bias)[0]
+    assert not torch.allclose(plain.float(), torch.cat(expected), rtol=2e-2, atol=2e-2)
+
+
+def test_conv_decode_round_conv_rounds_the_pre_activation():
+    """``conv_decode(round_conv=True)`` rounds the conv sum to the io dtype
+    before SiLU (``conv_decode.py:276-278``): its bf16 outputs equal
+    ``silu(round_bf16(conv1d))`` from a float64 ``F.conv1d``, except where the
+    fp32 sum and the float64 sum straddle a bf16 rounding boundary, and they
+    differ from the unrounded chain in many elements."""
+    gen = torch.Generator().manual_seed(94)
+    B, C = 64, 512
+    x = torch.randn(B, C, generator=gen).to(torch.bfloat16)
+    weight = (torch.randn(C, 1, 4, generator=gen) * 0.5).to(torch.bfloat16)
+    state = torch.randn(B, 1, C, 3, generator=gen).to(torch.bfloat16)
+    src = torch.cat([state[:, 0], x[:, :, None]], -1).double()  # [B, C, 4]
+    pre = F.conv1d(src.reshape(1, B * C, 4), weight.double().repeat(B, 1, 1), groups=B * C).reshape(B, C)
+    rounded = F.silu(pre.to(torch.bfloat16).double()).to(torch.bfloat16)
+    unrounded = F.silu(pre).to(torch.bfloat16)
+    got = gdn.conv_decode(x, weight, state.clone(), 0, list(range(B)), list(range(B)), round_conv=True)
+    assert (got != rounded).float().mean() < 1e-3
+    assert (got != unrounded).float().mean() > 0.05
+    plain = gdn.conv_decode(x, weight, state.clone(), 0, list(range(B)), list(range(B)))
+    assert (plain != unrounded).float().mean() < 1e-3
+
+
+def _composition_inputs(gen, T, H, HV, dk, dv, C):
+    return dict(
+        mixed=torch.randn(T, C, generator=gen),
+        gate=torch.randn(T, HV, generator=gen),
+        beta=torch.randn(T, HV, generator=gen),
+        weight=torch.randn(C, 1, 4, generator=gen) * 0.3,
+        A_log=-torch.rand(HV, generator=gen),
+        dt_bias=torch.randn(HV, generator=gen) * 0.3,
+    )
+
+
+def test_forward_prefill_equals_successive_decode_steps():
+    """In fp32 io the prefill composition (conv with history, windows,
+    split, prepare, chunked rule with pool I/O, ``gdn.py:74-149``) and T
+    decode steps (``gdn.py:222-265``, each reading the slot the previous step
+    wrote) are two independent paths to the same outputs, checkpoint state,
+    final state and conv window."""
+    gen = torch.Generator().manual_seed(60)
+    H, HV, dk, dv, T, layer = 2, 4, 16, 8, 70, 1
+    C = 2 * H * dk + HV * dv
+    w = _composition_inputs(gen, T, H, HV, dk, dv, C)
+    slots = T + 4
+    conv0 = torch.randn(slots, 2, C, 3, generator=gen)
+    state0 = torch.randn(slots, 2, HV, dk, dv, generator=gen) * 0.1
+    conv_p, state_p = conv0.clone(), state0.clone()
+    chunk_writes = torch.tensor([slots - 2, slots - 1])  # checkpoint after token 64, final state
+    token_slots = torch.full((T,), -1)
+    token_slots[63], token_slots[T - 1] = slots - 2, slots - 1
+    o_p = gdn.forward_prefill(w["mixed"], w["gate"], w["beta"], w["weight"], w["A_log"], w["dt_bias"], conv_p,
+                              state_p, layer, [0, T], [0], chunk_writes, token_slots, H, dk, HV, dv)
+    conv_d, state_d = conv0.clone(), state0.clone()
+    outs = []
+    for t in range(T):  # slot 0 -> 1 -> ... -> T
+        outs.append(gdn.forward_decode(w["mixed"][t:t + 1], w["gate"][t:t + 1], w["beta"][t:t + 1], w["weight"],
+                                       w["A_log"], w["dt_bias"], conv_d, state_d, layer, [t], [t + 1], H, dk, HV,
+                                       dv))
+    torch.testing.assert_close(o_p, torch.cat(outs), rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(state_p[slots - 2, layer], state_d[64, layer], rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(state_p[slots - 1, layer], state_d[T, layer], rtol=1e-4, atol=1e-5)
+    assert torch.equal(conv_p[slots - 2, layer], conv_d[64, layer])
+    assert torch.equal(conv_p[slots - 1, layer], conv_d[T, layer])
+    assert torch.equal(state_p[:slots - 2], state0[:slots - 2]) and torch.equal(conv_p[:slots - 2], conv0[:slots - 2])
+
+
+def test_forward_verify_equals_decode_steps_with_per_step_slots():
+    """One verify length group (``gdn.py:151-220``): B sequences of T drafts
+    from their baseline slots, step t's window and state to
+    ``write_slots[b, t]``; equal to T decode steps per sequence whose step t
+    reads step t-1's slot and writes ``write_slots[b, t]``."""
+    gen = torch.Generator().manual_seed(61)
+    H, HV, dk, dv, B, T, layer = 2, 4, 16, 8, 3, 5, 0
+    C = 2 * H * dk + HV * dv
+    w = _composition_inputs(gen, B * T, H, HV, dk, dv, C)
+    slots = 4 + B * T
+    conv0 = torch.randn(slots, 1, C, 3, generator=gen)
+    state0 = torch.randn(slots, 1, HV, dk, dv, generator=gen) * 0.1
+    base = torch.tensor([2, 0, 3])
+    writes = torch.arange(4, 4 + B * T).view(B, T)
+    conv_v, state_v = conv0.clone(), state0.clone()
+    o_v = gdn.forward_verify(w["mixed"], w["gate"], w["beta"], w["weight"], w["A_log"], w["dt_bias"], conv_v,
+                             state_v, layer, base, writes, H, dk, HV, dv)
+    conv_d, state_d = conv0.clone(), state0.clone()
+    for b in range(B):
+        read = int(base[b])
+        for t in range(T):
+            r = b * T + t
+            o = gdn.forward_decode(w["mixed"][r:r + 1], w["gate"][r:r + 1], w["beta"][r:r + 1], w["weight"],
+                                   w["A_log"], w["dt_bias"], conv_d, state_d, layer, [read], [int(writes[b, t])], H,
+                                   dk, HV, dv)
+            torch.testing.assert_close(o_v[r:r + 1], o, rtol=1e-5, atol=1e-6)
+            read = int(writes[b, t])
+    torch.testing.assert_close(state_v, state_d, rtol=1e-5, atol=1e-6)
+    assert torch.equal(conv_v, conv_d)
