@@ -354,6 +354,38 @@ int gdn_rms_norm_gated(const void* x, int dtype, int64_t rows, int64_t cols, con
                        int64_t gate_col_stride, const void* weight, int weight_dtype, float eps, void* out,
                        void* stream);
 
+/*
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops or harnesses that
+ * forbid hipMalloc): the fused prefill of gdn_prefill_qk + gdn_prefill_fused
+ * + gdn_conv_snapshots in one call, with the staging the first launch hands
+ * to the second (f16 q/k operands, head-major g/beta) kept in a 64 MiB
+ * file-scope device array of the library, one per GPU, instead of
+ * caller-allocated buffers.  It allocates nothing.  Inputs, pools, slots and
+ * `out` [T, HV, dv] as in those three entry points (snapshot_rows/slots[count]
+ * as gdn_conv_snapshots' rows/slots; no final write slots).
+ * Returns GDN_ERR_INVALID when the staging, 2 * align256(T * H * dk * 2) +
+ * 2 * align256(T * HV * 4) bytes, exceeds gdn_prefill_noalloc_scratch_bytes()
+ * (7,943 tokens at Qwen3-Next shape, H = 16, HV = 32, dk = 128), and
+ * GDN_ERR_UNSUPPORTED for shapes outside the fused kernel.  Calls on one GPU
+ * share the array: calls that overlap on one GPU (unordered streams) race.
+ * The device must be current on the calling thread.
+ */
+int gdn_prefill_fused_noalloc(const void* mixed, int64_t row_stride, int io_dtype, const void* weight,
+                              int kernel_width, const void* cu_seqlens, int cu_dtype, int64_t num_seqs,
+                              int64_t total_tokens, int64_t H, int64_t HV, int64_t dk, int64_t dv, void* conv_state,
+                              int64_t conv_slot_stride, int64_t conv_layer_stride, const void* gate,
+                              int64_t gate_row_stride, int64_t gate_head_stride, int gate_dtype, const void* beta,
+                              int64_t beta_row_stride, int64_t beta_head_stride, int beta_dtype, const void* A_log,
+                              int a_dtype, const void* dt_bias, int dt_dtype, void* state, int state_dtype,
+                              int64_t slot_stride, int64_t layer_stride, int64_t head_stride, int64_t layer,
+                              const void* baseline_slots, int baseline_dtype, const void* chunk_write_slots,
+                              int chunk_write_dtype, const void* snapshot_rows, int snapshot_rows_dtype,
+                              const void* snapshot_slots, int snapshot_slots_dtype, int64_t snapshot_count, void* out,
+                              float scale, void* stream);
+/* Bytes of gdn_prefill_fused_noalloc's per-GPU staging array. */
+int64_t gdn_prefill_noalloc_scratch_bytes(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -53,6 +53,9 @@ SIGNATURES = {
     "gdn_store_state": [P, I64, P, I32, P, I64, I64, I64, P],
     "gdn_copy_rows": [P, I64, P, I32, P, I64, P, I32, I64, I64, I64, I64, P],
     "gdn_zero_rows": [P, I64, P, I32, I64, I64, I64, I64, P],
+    "gdn_prefill_fused_noalloc": [P, I64, I32, P, I32, P, I32, I64, I64, I64, I64, I64, I64, P, I64, I64, P, I64,
+                                  I64, I32, P, I64, I64, I32, P, I32, P, I32, P, I32, I64, I64, I64, I64, P, I32,
+                                  P, I32, P, I32, P, I32, I64, P, F32, P],
     "gdn_commit_accepted": [P, I64, I64, I64, P, I64, I64, I64, P, I32, P, I64, I64, I32, P, I32, I64, I64, P],
 }
 
@@ -81,6 +84,8 @@ def lib() -> ctypes.CDLL:
         handle.gdn_last_error.restype = ctypes.c_char_p
         handle.gdn_abi_version.argtypes = []
         handle.gdn_abi_version.restype = ctypes.c_int
+        handle.gdn_prefill_noalloc_scratch_bytes.argtypes = []
+        handle.gdn_prefill_noalloc_scratch_bytes.restype = ctypes.c_int64
         _lib = handle
     return _lib
 

@@ -170,6 +170,41 @@ def prefill_fused(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, co
     return out
 
 
+def prefill_fused_noalloc(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, conv_state, recurrent_state,
+                          cu_seqlens, baseline_slots, chunk_write_slots, snapshot_rows, snapshot_slots, out):
+    """``prefill_fused`` through ``gdn_prefill_fused_noalloc``: the same
+    three launches, with the q/k operands and prepared gates staged in the
+    library's per-GPU device array, so nothing is allocated (``out`` [T, HV,
+    dv] is the caller's).  Raises ``RuntimeError`` when T exceeds what the
+    array holds and ``NotImplementedError`` for shapes outside the fused
+    kernel; calls that overlap on one GPU race on the shared array."""
+    T, C = mixed_qkv.shape
+    assert C == config.conv_dim == 2 * config.key_dim + config.value_dim
+    assert gate.shape == beta.shape == (T, config.num_v_heads)
+    _check_pools(conv_state, recurrent_state, config)
+    assert snapshot_rows.shape == snapshot_slots.shape and snapshot_rows.ndim == 1
+    assert out.shape == (T, config.num_v_heads, config.head_v_dim) and out.is_contiguous()
+    assert conv_weight.is_contiguous() and A_log.is_contiguous() and dt_bias.is_contiguous()
+    _lib.call(
+        "gdn_prefill_fused_noalloc",
+        mixed_qkv.data_ptr(), mixed_qkv.stride(0), _lib.dtype_code(mixed_qkv.dtype), conv_weight.data_ptr(),
+        config.state_len + 1, cu_seqlens.data_ptr(), _lib.index_code(cu_seqlens), len(cu_seqlens) - 1, T,
+        config.num_k_heads, config.num_v_heads, config.head_k_dim, config.head_v_dim,
+        conv_state.data_ptr(), conv_state.stride(0), conv_state.stride(1),
+        gate.data_ptr(), gate.stride(0), gate.stride(1), _lib.dtype_code(gate.dtype),
+        beta.data_ptr(), beta.stride(0), beta.stride(1), _lib.dtype_code(beta.dtype),
+        A_log.data_ptr(), _lib.dtype_code(A_log.dtype), dt_bias.data_ptr(), _lib.dtype_code(dt_bias.dtype),
+        recurrent_state.data_ptr(), _lib.dtype_code(recurrent_state.dtype), recurrent_state.stride(0),
+        recurrent_state.stride(1), recurrent_state.stride(2), config.layer_idx,
+        baseline_slots.data_ptr(), _lib.index_code(baseline_slots),
+        chunk_write_slots.data_ptr(), _lib.index_code(chunk_write_slots),
+        snapshot_rows.data_ptr(), _lib.index_code(snapshot_rows), snapshot_slots.data_ptr(),
+        _lib.index_code(snapshot_slots), snapshot_rows.numel(),
+        out.data_ptr(), float(config.head_k_dim) ** -0.5, _lib.stream_of(mixed_qkv),
+    )
+    return out
+
+
 def prefill_chunk_fused(q, k, g, b, mixed_qkv, weight, config, conv_state, recurrent_state, cu_seqlens,
                         baseline_slots, chunk_write_slots, out):
     """The chunk-kernel launch of ``prefill_fused`` (q, k, g, beta from the q/k
@@ -252,4 +287,5 @@ def verify_group(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, con
     return output
 
 
-__all__ = ["conv_snapshots", "decode_step", "prefill_chunk_fused", "prefill_frontend", "prefill_fused", "verify_group"]
+__all__ = ["conv_snapshots", "decode_step", "prefill_chunk_fused", "prefill_frontend", "prefill_fused",
+           "prefill_fused_noalloc", "verify_group"]

@@ -16,7 +16,7 @@ def _declarations():
     src = open(HEADER).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
     out = {}
-    for m in re.finditer(r"(?:int|const char\*)\s+(gdn_\w+)\s*\(([^;]*?)\);", src, re.S):
+    for m in re.finditer(r"(?:int64_t|int|const char\*)\s+(gdn_\w+)\s*\(([^;]*?)\);", src, re.S):
         params = [p.strip() for p in m.group(2).split(",") if p.strip() and p.strip() != "void"]
         out[m.group(1)] = params
     return out
@@ -43,14 +43,15 @@ def test_header_declares_expected_entry_points():
             "gdn_fused_conv_recurrent", "gdn_packed_causal_conv1d", "gdn_prepare", "gdn_prefill_frontend",
             "gdn_conv_decode", "gdn_store_state", "gdn_copy_rows", "gdn_zero_rows",
             "gdn_commit_accepted", "gdn_prefill_qk", "gdn_prefill_fused", "gdn_conv_snapshots",
-            "gdn_rms_norm_gated", "gdn_metadata_copy", "gdn_metadata_pad"} <= names
+            "gdn_rms_norm_gated", "gdn_metadata_copy", "gdn_metadata_pad", "gdn_prefill_fused_noalloc",
+            "gdn_prefill_noalloc_scratch_bytes"} <= names
 
 
 def test_ctypes_table_matches_header():
     from logssms_amd import _lib
     decls = _declarations()
     for name, params in decls.items():
-        if name in ("gdn_last_error", "gdn_abi_version"):
+        if name in ("gdn_last_error", "gdn_abi_version", "gdn_prefill_noalloc_scratch_bytes"):
             assert params == []
             continue
         assert name in _lib.SIGNATURES, name
@@ -65,7 +66,8 @@ def test_library_loads_and_exports_every_symbol():
     lib = _lib.lib()
     for name in _declarations():
         assert hasattr(lib, name), name
-    assert lib.gdn_abi_version() == 2
+    assert lib.gdn_abi_version() == 3
+    assert lib.gdn_prefill_noalloc_scratch_bytes() == 64 << 20
     assert lib.gdn_last_error() in (b"",) or isinstance(lib.gdn_last_error(), bytes)
 
 
