@@ -35,8 +35,13 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
-PEAK_MFMA_16BIT = 2.5e15  # MI355X dense bf16/fp16 FLOP/s
-PEAK_HBM = 8.0e12  # MI355X HBM3E bytes/s
+PEAK_MFMA_16BIT = 2.5e15  # MI355X dense bf16/fp16 FLOP/s (published)
+PEAK_HBM = 8.0e12  # MI355X HBM3E bytes/s (published)
+MFMA_16BIT_FLOP_PER_CLK_PER_CU = 4096  # dense 16-bit MFMA issue of one CDNA4 CU
+
+# hipDeviceAttribute_t values of this ROCm's hip_runtime_api.h: peak engine
+# clock (kHz), peak memory clock (kHz), memory bus width (bits), compute units
+_HIP_ATTRS = {"engine_clock_khz": 5, "memory_clock_khz": 60, "memory_bus_bits": 59, "compute_units": 63}
 
 H, HV, D, W = 16, 32, 128, 4
 CONV_DIM = 2 * H * D + HV * D  # 8192
@@ -60,6 +65,56 @@ def _traffic(name):
     except OSError:
         pass
     return None
+
+
+def device_peaks(index=0):
+    """The clocks the HIP runtime reports for the device and the peaks they
+    imply: 16-bit MFMA = CUs x engine clock x 4096 FLOP/clk/CU, HBM = bus
+    width x 4 transfers per reported memory clock (the HBM3/HBM3E pin rate
+    is 4x the clock the runtime reports: 2 GHz x 4 x 8192 bits = 8.2 TB/s
+    here).  The roofline fractions use the published peaks; these are
+    printed beside them."""
+    import ctypes
+    out = {}
+    try:
+        hip = ctypes.CDLL("libamdhip64.so")
+        for name, attr in _HIP_ATTRS.items():
+            value = ctypes.c_int(0)
+            out[name] = value.value if hip.hipDeviceGetAttribute(ctypes.byref(value), attr, index) == 0 else None
+    except OSError:
+        return out
+    if out.get("compute_units") and out.get("engine_clock_khz"):
+        out["mfma_16bit_peak_tflops"] = (out["compute_units"] * out["engine_clock_khz"] * 1e3
+                                         * MFMA_16BIT_FLOP_PER_CLK_PER_CU / 1e12)
+    if out.get("memory_clock_khz") and out.get("memory_bus_bits"):
+        out["hbm_peak_gbps"] = 4 * out["memory_clock_khz"] * 1e3 * out["memory_bus_bits"] / 8 / 1e9
+    out["published"] = {"mfma_16bit_tflops": PEAK_MFMA_16BIT / 1e12, "hbm_gbps": PEAK_HBM / 1e9}
+    return out
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def _median_time(fn, budget_s, max_runs=50):
+    """Median wall time of fn over as many runs as fit in ``budget_s`` (at
+    least one, after one untimed warm-up run)."""
+    fn()
+    times = []
+    t_start = time.perf_counter()
+    while not times or (time.perf_counter() - t_start < budget_s and len(times) < max_runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
 
 
 def _config(layer=0):
@@ -224,21 +279,40 @@ def prefill_gpu(inp, dev, events=None, fused=True, pools=None):
     return step, state_pool, out
 
 
-def prefill_cpu_sample(inp, tokens, threads):
-    """Times the oracle's chunked restatement (conv + prepare + chunk rule) on
-    the first `tokens` tokens of sequence 0 at full head count."""
+def prefill_cpu_legs(inp, chunk_tokens, naive_tokens, budget_s):
+    """The prefill CPU baseline on config 2's inputs, all host threads:
+    (ii) the oracle's chunked restatement (conv + prepare + chunk rule,
+    ``forward_prefill``) on the first ``chunk_tokens`` tokens of sequence 0 at
+    full head count; (i) the naive token recurrence (the reference test's
+    semantics) on the first ``naive_tokens`` of them, from the same prepared
+    q, k, v, g, beta.  Returns the two cpu_baseline-style dicts."""
     from oracle import gdn as ref
-    torch.set_num_threads(threads)
-    mixed = inp["mixed"][:tokens]
-    gate = inp["gate"][:tokens]
-    beta = inp["beta"][:tokens]
-    conv = torch.zeros(1, 1, CONV_DIM, W - 1, dtype=torch.bfloat16)
-    state = torch.zeros(1, 1, HV, D, D)
-    nc = (tokens + C - 1) // C
-    t0 = time.perf_counter()
-    ref.forward_prefill(mixed, gate, beta, inp["weight"], inp["A_log"], inp["dt_bias"], conv, state, 0,
-                        [0, tokens], [-1], [-1] * nc, [-1] * tokens, H, D, HV, D)
-    return time.perf_counter() - t0
+    mixed, gate, beta = inp["mixed"][:chunk_tokens], inp["gate"][:chunk_tokens], inp["beta"][:chunk_tokens]
+    nc = (chunk_tokens + C - 1) // C
+
+    def chunked():
+        conv = torch.zeros(1, 1, CONV_DIM, W - 1, dtype=torch.bfloat16)
+        state = torch.zeros(1, 1, HV, D, D)
+        ref.forward_prefill(mixed, gate, beta, inp["weight"], inp["A_log"], inp["dt_bias"], conv, state, 0,
+                            [0, chunk_tokens], [-1], [-1] * nc, [-1] * chunk_tokens, H, D, HV, D)
+
+    t_chunk, runs = _median_time(chunked, budget_s)
+    n = naive_tokens
+    y, _ = ref.packed_causal_conv1d(inp["mixed"][:n], inp["weight"], torch.zeros(1, CONV_DIM, W - 1,
+                                                                                  dtype=torch.bfloat16), [0, n],
+                                    window_rows=[])
+    q, k, v = ref.split_qkv(y[None], H, D, HV, D)
+    q, k, v, g, b = ref.prepare_gdn(q, k, v, inp["gate"][None, :n], inp["beta"][None, :n], inp["A_log"],
+                                    inp["dt_bias"])
+    t_naive, runs_naive = _median_time(
+        lambda: ref.naive_recurrence(q[0], k[0], v[0], g[0], b[0], D ** -0.5, torch.zeros(HV, D, D)), budget_s / 3)
+    return ({"value": chunk_tokens / t_chunk, "unit": "tokens/s",
+             "sample": f"(ii) oracle forward_prefill (conv + prepare + chunked rule, fp32 torch) on the first "
+                       f"{chunk_tokens} tokens of sequence 0 at full head count; median of {runs} runs"},
+            {"value": n / t_naive, "unit": "tokens/s",
+             "sample": f"(i) naive token recurrence (oracle naive_recurrence, the reference test's semantics, "
+                       f"fp32 torch, 32 v-heads) on the first {n} tokens of sequence 0, truncated from 4096 to "
+                       f"keep the run short; median of {runs_naive} runs"})
 
 
 # ---------------------------------------------------------------- decode (config 3) / verify (config 5)
@@ -277,7 +351,28 @@ def decode_gpu(dev, B=256, slots=1024, seed=3, events=None):
     def step():
         decode_step(mixed, gate, beta, weight, A_log, dt_bias, cfg, conv, state, slot_idx, slot_idx, out=out)
 
-    return step
+    tensors = dict(mixed=mixed, gate=gate, beta=beta, weight=weight, A_log=A_log, dt_bias=dt_bias, conv=conv,
+                   state=state, reads=slot_idx, writes=slot_idx)
+    return step, tensors
+
+
+def decode_cpu_leg(t, budget_s):
+    """Config 3 on the host: the oracle's vectorised decode step
+    (``forward_decode_batched``: index_select / index_copy_ pool I/O, the
+    recurrence batched over the 256 sequences) on a host copy of the GPU
+    run's pools and inputs, all host threads."""
+    from oracle import gdn as ref
+    h = {k: v.cpu() for k, v in t.items()}
+
+    def run():
+        ref.forward_decode_batched(h["mixed"], h["gate"], h["beta"], h["weight"], h["A_log"], h["dt_bias"],
+                                   h["conv"], h["state"], 0, h["reads"], h["writes"], H, D, HV, D)
+
+    sec, runs = _median_time(run, budget_s, max_runs=10)
+    nb = decode_bytes(h["mixed"].shape[0])
+    return {"value": nb / sec / 1e9, "unit": "GB/s", "ms": sec * 1e3,
+            "sample": f"oracle forward_decode_batched on config 3 in full (256 sequences, host copy of the GPU "
+                      f"pools), fp32 torch; median of {runs} runs"}
 
 
 def verify_gpu(dev, B=64, T=8, slots=1024, seed=5):
@@ -307,7 +402,29 @@ def verify_gpu(dev, B=64, T=8, slots=1024, seed=5):
                   conv.stride(0) * 2, 0, SC_BYTES, live.data_ptr(), 1, writes.data_ptr(), T, 1, 1,
                   accepted.data_ptr(), 1, B, T, _lib.stream_of(state))
 
-    return step, commit
+    tensors = dict(mixed=mixed, gate=gate, beta=beta, weight=weight, A_log=A_log, dt_bias=dt_bias, conv=conv,
+                   state=state, live=live, writes=writes)
+    return step, commit, tensors
+
+
+def verify_cpu_leg(t, budget_s):
+    """Config 5 on the host: the oracle's batched verify
+    (``forward_verify_batched``: 8 steps, each vectorised over the 64
+    sequences, every per-step state and window written with index_copy_) on a
+    host copy of the GPU run's pools and inputs, all host threads."""
+    from oracle import gdn as ref
+    h = {k: v.cpu() for k, v in t.items()}
+
+    def run():
+        ref.forward_verify_batched(h["mixed"], h["gate"], h["beta"], h["weight"], h["A_log"], h["dt_bias"],
+                                   h["conv"], h["state"], 0, h["live"], h["writes"], H, D, HV, D)
+
+    sec, runs = _median_time(run, budget_s, max_runs=10)
+    B, T = h["writes"].shape
+    nb = verify_bytes(B, T)
+    return {"value": nb / sec / 1e9, "unit": "GB/s", "ms": sec * 1e3,
+            "sample": f"oracle forward_verify_batched on config 5 in full ({B} sequences x {T} drafts, host copy "
+                      f"of the GPU pools), fp32 torch; median of {runs} runs"}
 
 
 def norm_gpu(dev, T=16384, seed=6):
@@ -368,7 +485,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0,
+                    help="time budget of each CPU baseline leg (chunked prefill; naive prefill, decode and "
+                         "verify get a share of it)")
     ap.add_argument("--only", choices=["all", "prefill", "decode", "verify", "norm", "layer", "copy"],
                     default="all",
                     help="'copy' times a plain 512 MiB device copy (the calibration kernel for the "
@@ -381,8 +500,11 @@ def main():
         sys.exit(2)
     dev = "cuda:0"
     torch.cuda.set_device(0)
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
     result = {}
-    extra = {}
+    extra = {"peaks": device_peaks(0)}
+    cpu_info = {"cores": threads, "cpu_model": cpu_model()}
     if args.only == "copy":
         nbytes = 512 << 20
         src = torch.ones(nbytes // 4, device=dev)
@@ -408,7 +530,7 @@ def main():
         # mixed_qkv in, prepared fp32 g/beta in, o out, final states out
         chunk_bytes = T * (2 * H * D + HV * D) * 2 + 2 * T * HV * 4 + T * HV * D * 2 + inp["N"] * S_BYTES
         result.update(
-            metric="GDN prefill tokens/s (Qwen3-Next layer, 4x4096 packed)",
+            metric="GDN prefill tokens/s (% MFMA peak); decode state-update GB/s (% HBM peak)",
             value=T / (ms * 1e-3),
             unit="tokens/s",
             n_gpus=1, steps=args.steps, warmup=args.warmup, ms_per_step=ms,
@@ -426,20 +548,8 @@ def main():
         )
         extra["prefill_qk_and_snapshot_ms"] = ms - chunk_ms
         if not args.no_cpu_baseline:
-            threads = len(os.sched_getaffinity(0))
-            sample = 4096
-            times = []
-            t_start = time.perf_counter()
-            while not times or (time.perf_counter() - t_start < args.cpu_seconds and len(times) < 50):
-                times.append(prefill_cpu_sample(inp, sample, threads))
-            times.sort()
-            med = times[len(times) // 2]
-            result["cpu_baseline"] = {
-                "value": sample / med, "unit": "tokens/s", "cores": threads, "kind": "port",
-                "sample": f"oracle forward_prefill (conv+prepare+chunked rule, fp32 torch) on the first {sample} "
-                          f"tokens of sequence 0 at full head count; median of {len(times)} runs",
-            }
-            torch.set_num_threads(threads)
+            chunked, naive = prefill_cpu_legs(inp, 4096, 256, args.cpu_seconds)
+            result["cpu_baseline"] = {**chunked, **cpu_info, "kind": "port", "naive_recurrence": naive}
         del step, inp
         torch.cuda.empty_cache()
         inp4 = make_prefill_cfg4(draw_device=dev)
@@ -460,14 +570,19 @@ def main():
         torch.cuda.empty_cache()
 
     if args.only in ("all", "decode"):
-        step = decode_gpu(dev)
+        step, tensors = decode_gpu(dev)
         ms = _time(step, max(args.steps, 20), args.warmup)
         nb = decode_bytes(256)
         extra["decode"] = {"config": "BASELINE config 3 (256 seqs, in-place RMW of randperm pool slots)",
                            "ms": ms, "bytes": nb, "GB/s": nb / (ms * 1e-3) / 1e9,
                            "frac_hbm": nb / (ms * 1e-3) / PEAK_HBM, "traffic": _traffic("fused_kernel_decode_cfg3")}
+        if not args.no_cpu_baseline:
+            extra["decode"]["cpu_baseline"] = {**decode_cpu_leg(tensors, args.cpu_seconds / 2), **cpu_info,
+                                               "kind": "port"}
+        del step, tensors
+        torch.cuda.empty_cache()
     if args.only in ("all", "verify"):
-        step, commit = verify_gpu(dev)
+        step, commit, tensors = verify_gpu(dev)
         ms = _time(step, max(args.steps, 20), args.warmup)
         nb = verify_bytes(64, 8)
         cms = _time(commit, max(args.steps, 20), args.warmup)
@@ -477,6 +592,11 @@ def main():
                            "frac_hbm": nb / (ms * 1e-3) / PEAK_HBM, "traffic": _traffic("fused_kernel_verify_cfg5"),
                            "commit_ms": cms, "commit_GB/s": cb / (cms * 1e-3) / 1e9,
                            "commit_traffic": _traffic("commit_kernel_cfg5")}
+        if not args.no_cpu_baseline:
+            extra["verify"]["cpu_baseline"] = {**verify_cpu_leg(tensors, args.cpu_seconds / 2), **cpu_info,
+                                               "kind": "port"}
+        del step, commit, tensors
+        torch.cuda.empty_cache()
     if args.only in ("all", "norm"):
         step, nb = norm_gpu(dev)
         ms = _time(step, max(args.steps, 20), args.warmup)

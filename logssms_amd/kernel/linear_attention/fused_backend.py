@@ -248,6 +248,35 @@ def _fused(mixed, row_index, gate, beta, conv_weight, A_log, dt_bias, config, co
     )
 
 
+# limits of gdn_fused_conv_recurrent: drafts per launch, v-heads per key head
+_MAX_FUSED_STEPS = 16
+_MAX_FUSED_GROUP = 4
+
+
+def _stepwise(mixed, row_index, gate, beta, conv_weight, A_log, dt_bias, config, conv_state, recurrent_state,
+              read_slots, write_slots, batch, steps, out):
+    """Decode/verify for head groups wider than the fused kernel takes (more
+    than 4 v-heads per key head): per step, ``conv_decode`` (split, rounded
+    before SiLU for verify as in its torch conv) then the slotted recurrence
+    (``fused_recurrent_gated_delta_rule_to_slots``); step t reads the conv
+    window and state step t-1 wrote, step 0 those of ``read_slots``."""
+    from .conv_decode import conv_decode
+    from .gdn import fused_recurrent_gated_delta_rule_to_slots
+    dev = mixed.device
+    rows = (row_index.view(batch, steps).long() if row_index is not None
+            else torch.arange(batch * steps, device=dev).view(batch, steps))
+    writes = write_slots.view(batch, 1) if write_slots.ndim == 1 else write_slots
+    for t in range(steps):
+        r = rows[:, t]
+        read = read_slots if t == 0 else writes[:, t - 1]
+        q, k, v = conv_decode(mixed.index_select(0, r), conv_weight, config, split_qkv=True, round_conv=steps > 1,
+                              read_slots=read, write_slots=writes[:, t], standard_state=conv_state)
+        o = fused_recurrent_gated_delta_rule_to_slots(q, k, v, gate.index_select(0, r)[:, None],
+                                                      beta.index_select(0, r)[:, None], A_log, dt_bias,
+                                                      recurrent_state, read, writes[:, t], config.layer_idx)
+        out.index_copy_(0, r, o[:, 0])
+
+
 def decode_step(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, conv_state, recurrent_state,
                 read_slots, write_slots, out=None):
     """``gdn.py:222-265`` in one kernel: conv window of ``read_slots`` -> SiLU
@@ -261,7 +290,10 @@ def decode_step(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, conv
     if out is None:
         out = torch.empty(B, config.num_v_heads, config.head_v_dim, device=mixed_qkv.device, dtype=mixed_qkv.dtype)
     assert out.shape == (B, config.num_v_heads, config.head_v_dim) and out.is_contiguous()
-    if B:
+    if B and config.num_v_heads // config.num_k_heads > _MAX_FUSED_GROUP:
+        _stepwise(mixed_qkv, None, gate, beta, conv_weight, A_log, dt_bias, config, conv_state, recurrent_state,
+                  read_slots, write_slots, B, 1, out)
+    elif B:
         _fused(mixed_qkv, None, gate, beta, conv_weight, A_log, dt_bias, config, conv_state, recurrent_state,
                read_slots, write_slots, B, 1, write_slots.stride(0), 0, out)
     return out
@@ -272,15 +304,31 @@ def verify_group(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, con
     """One verify length group (``gdn.py:165-218``): B sequences of T drafts at
     rows ``row_indices`` (``[B*T]``, or None for rows ``0..B*T-1``) of
     ``mixed_qkv``/``gate``/``beta``.  Step t's conv window and state go to
-    ``write_slots[b, t]``; outputs land in ``output[row]`` ([rows, HV, dv])."""
+    ``write_slots[b, t]``; outputs land in ``output[row]`` ([rows, HV, dv]).
+    Groups of more than 16 drafts run as 16-step segments (each resuming from
+    the slot the previous segment's last step wrote, so those write slots must
+    be valid); more than 4 v-heads per key head take ``_stepwise``."""
     B, T = write_slots.shape
     assert baseline_slots.shape == (B,)
-    assert 1 <= T <= 16
+    assert T >= 1
     _check_pools(conv_state, recurrent_state, config)
     assert output.is_contiguous() and output.shape[1:] == (config.num_v_heads, config.head_v_dim)
     if row_indices is not None:
         assert row_indices.shape == (B * T,)
-    if B:
+    if B and config.num_v_heads // config.num_k_heads > _MAX_FUSED_GROUP:
+        _stepwise(mixed_qkv, row_indices, gate, beta, conv_weight, A_log, dt_bias, config, conv_state,
+                  recurrent_state, baseline_slots, write_slots, B, T, output)
+    elif B and T > _MAX_FUSED_STEPS:
+        # segments of at most 16 drafts; each resumes from the conv window and
+        # state the previous segment's last step wrote
+        rows = (row_indices.view(B, T) if row_indices is not None
+                else torch.arange(B * T, device=mixed_qkv.device).view(B, T))
+        for s0 in range(0, T, _MAX_FUSED_STEPS):
+            s1 = min(s0 + _MAX_FUSED_STEPS, T)
+            base = baseline_slots if s0 == 0 else write_slots[:, s0 - 1]
+            verify_group(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, conv_state, recurrent_state,
+                         rows[:, s0:s1].reshape(-1), base, write_slots[:, s0:s1], output)
+    elif B:
         _fused(mixed_qkv, row_indices, gate, beta, conv_weight, A_log, dt_bias, config, conv_state,
                recurrent_state, baseline_slots, write_slots, B, T, write_slots.stride(0), write_slots.stride(1),
                output)

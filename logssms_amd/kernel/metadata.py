@@ -1,8 +1,9 @@
-"""``copy_metadata`` / ``pad_metadata`` (drop-ins for the reference's
-``python/logssms/kernel/metadata.py:108-150``): one launch moves a group of
-small index tensors (``gdn_metadata_copy`` / ``gdn_metadata_pad``,
-``csrc/metadata.hip``).  CPU tensors take the same plain torch path as the
-reference's host branch."""
+"""``copy_metadata`` / ``pad_metadata``: the interface of the reference's
+``python/logssms/kernel/metadata.py:108-150`` (same arguments, results and
+``ValueError`` conditions).  On the device a whole group of small index
+tensors moves in one launch (``gdn_metadata_copy`` / ``gdn_metadata_pad``,
+``csrc/metadata.hip``): the per-field pointers, lengths and strides travel as
+a kernel argument table.  Host tensors take plain torch copies."""
 
 from __future__ import annotations
 
@@ -13,72 +14,71 @@ import torch
 from .. import _lib
 
 
-def _ptrs(values):
-    arr = (ctypes.c_void_p * len(values))(*values)
+def _table(ctype, values):
+    """A ctypes array of ``values`` and a pointer to it (keep both alive)."""
+    arr = (ctype * len(values))(*values)
     return ctypes.cast(arr, ctypes.c_void_p), arr
 
 
-def _i64(values):
-    return (ctypes.c_int64 * len(values))(*[int(v) for v in values])
-
-
-def _i32(values):
-    arr = (ctypes.c_int * len(values))(*[int(v) for v in values])
-    return ctypes.cast(arr, ctypes.c_void_p), arr
+def _element_stride(t: torch.Tensor) -> int:
+    """Stride of a tensor read as a flat vector: 1 when contiguous, its own
+    stride when it is 1-D; anything else cannot be read that way."""
+    if t.is_contiguous():
+        return 1
+    if t.ndim == 1:
+        return t.stride(0)
+    raise ValueError("metadata copies require contiguous tensors or strided vectors")
 
 
 def copy_metadata(sources, outputs) -> None:
-    """``outputs[i][:] = sources[i]`` for equally sized tensors; contiguous
-    tensors or strided vectors (``metadata.py:108-134``)."""
-    if not outputs or len(sources) != len(outputs):
+    """``outputs[i][...] = sources[i]`` for each pair of equally long tensors
+    (contiguous, or vectors of any stride)."""
+    pairs = list(zip(sources, outputs))
+    if not outputs or len(pairs) != len(sources) or len(pairs) != len(outputs):
         raise ValueError("metadata copies require equally sized nonempty source/output groups")
-    counts = tuple(output.numel() for output in outputs)
-    if any(source.numel() != count for source, count in zip(sources, counts)):
+    lengths = [dst.numel() for dst in outputs]
+    if any(src.numel() != n for (src, _), n in zip(pairs, lengths)):
         raise ValueError("metadata copies require matching source/output tensor lengths")
-    if max(counts) == 0:
+    if not any(lengths):
         return
     if not outputs[0].is_cuda:
-        for source, output in zip(sources, outputs, strict=True):
-            output.copy_(source)
+        for src, dst in pairs:
+            dst.copy_(src)
         return
-
-    def stride(tensor):
-        if tensor.is_contiguous():
-            return 1
-        if tensor.ndim == 1:
-            return tensor.stride(0)
-        raise ValueError("metadata copies require contiguous tensors or strided vectors")
-
-    for src, dst in zip(sources, outputs):
-        if src.dtype != dst.dtype or src.device != dst.device:
-            raise ValueError("metadata copies require matching dtypes and devices")
-    srcs, dsts = _ptrs([s.data_ptr() for s in sources]), _ptrs([d.data_ptr() for d in outputs])
-    sizes = _i32([d.element_size() for d in outputs])
-    _lib.call("gdn_metadata_copy", srcs[0], dsts[0], _i64(counts), _i64([stride(s) for s in sources]),
-              _i64([stride(d) for d in outputs]), sizes[0], len(outputs), _lib.stream_of(outputs[0]))
+    src_strides = [_element_stride(src) for src, _ in pairs]
+    dst_strides = [_element_stride(dst) for _, dst in pairs]
+    if any(src.dtype != dst.dtype or src.device != dst.device for src, dst in pairs):
+        raise ValueError("metadata copies require matching dtypes and devices")
+    src_ptrs = _table(ctypes.c_void_p, [src.data_ptr() for src, _ in pairs])
+    dst_ptrs = _table(ctypes.c_void_p, [dst.data_ptr() for _, dst in pairs])
+    sizes = _table(ctypes.c_int, [dst.element_size() for _, dst in pairs])
+    _lib.call("gdn_metadata_copy", src_ptrs[0], dst_ptrs[0], _lib.i64_array(lengths), _lib.i64_array(src_strides),
+              _lib.i64_array(dst_strides), sizes[0], len(pairs), _lib.stream_of(outputs[0]))
 
 
 def pad_metadata(sources, outputs, fills, chunk_tails) -> None:
-    """``outputs[i][:len(sources[i])] = sources[i]``, the rest ``fills[i]``, or
-    for a flattened pair table (``chunk_tails[i] >= 0``) the pairs
-    ``(0, chunk_tails[i])`` (``metadata.py:137-150``)."""
+    """``outputs[i][:len(sources[i])] = sources[i]``; the rows after it get
+    ``fills[i]``, or, for a flattened (request, chunk) pair table
+    (``chunk_tails[i] >= 0``), the pair ``(0, chunk_tails[i])``."""
     if not outputs:
         return
+    jobs = list(zip(sources, outputs, fills, chunk_tails))
     if not outputs[0].is_cuda:
-        for src, dst, fill, tail in zip(sources, outputs, fills, chunk_tails):
-            dst.fill_(fill)
+        for src, dst, fill, tail in jobs:
             if tail >= 0:
-                dst[:, 1] = tail
-            dst[:len(src)].copy_(src)
+                dst.view(-1, 2).copy_(torch.tensor([0, tail], dtype=dst.dtype))
+            else:
+                dst.fill_(fill)
+            dst[:src.shape[0]] = src
         return
-    for src, dst in zip(sources, outputs):
-        if src.dtype != dst.dtype or not src.is_contiguous() or not dst.is_contiguous():
-            raise ValueError("metadata padding requires contiguous tensors of one dtype")
-    srcs, dsts = _ptrs([s.data_ptr() for s in sources]), _ptrs([d.data_ptr() for d in outputs])
-    sizes = _i32([d.element_size() for d in outputs])
-    _lib.call("gdn_metadata_pad", srcs[0], dsts[0], _i64([s.numel() for s in sources]),
-              _i64([d.numel() for d in outputs]), _i64(fills), _i64(chunk_tails), sizes[0], len(outputs),
-              _lib.stream_of(outputs[0]))
+    if any(src.dtype != dst.dtype or not (src.is_contiguous() and dst.is_contiguous()) for src, dst, _, _ in jobs):
+        raise ValueError("metadata padding requires contiguous tensors of one dtype")
+    src_ptrs = _table(ctypes.c_void_p, [src.data_ptr() for src, _, _, _ in jobs])
+    dst_ptrs = _table(ctypes.c_void_p, [dst.data_ptr() for _, dst, _, _ in jobs])
+    sizes = _table(ctypes.c_int, [dst.element_size() for _, dst, _, _ in jobs])
+    _lib.call("gdn_metadata_pad", src_ptrs[0], dst_ptrs[0], _lib.i64_array([src.numel() for src, _, _, _ in jobs]),
+              _lib.i64_array([dst.numel() for _, dst, _, _ in jobs]), _lib.i64_array([f for _, _, f, _ in jobs]),
+              _lib.i64_array([t for _, _, _, t in jobs]), sizes[0], len(jobs), _lib.stream_of(outputs[0]))
 
 
 __all__ = ["copy_metadata", "pad_metadata"]

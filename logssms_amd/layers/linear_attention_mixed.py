@@ -1,15 +1,25 @@
-"""Fixed-capacity metadata for mixed prefill/decode graph buckets (reference
-``python/logssms/layers/linear_attention_backend/mixed.py:1-197``).
+"""Fixed-capacity metadata for mixed prefill/decode graph buckets.
 
-Ordinary metadata is prepared with the actual token lengths first and then
-normalised outside capture: the per-chunk and per-token tables are padded to
-the bucket's capacity (padded chunk pairs point past the packed tokens,
-padded write slots are -1, so padded entries write nothing), decode slots
-become int64.  ``MixedLinearCopyPlan`` then copies fresh metadata into the
-tensors a graph captured, after checking that nothing but tensor contents
-changed.  No device tensor is read on the host.  Only the standard
-(radix-pool) metadata is handled; the LogState variant is not part of this
-build."""
+Interface of the reference's
+``python/logssms/layers/linear_attention_backend/mixed.py:59-197``
+(``prepare_mixed_linear_metadata``, ``MixedLinearCopyPlan``): the same names,
+arguments, padding rules and errors; the bodies are this library's own.
+
+A bucket fixes the prefill request count and token capacity.  Metadata is
+first prepared at the actual lengths and then normalised, outside capture,
+to shapes that depend on the bucket only:
+
+* per-token tables are ``capacity`` rows long, per-chunk tables
+  ``chunk_capacity(requests, capacity)`` rows long;
+* padded write slots are -1 (the kernels skip them), padded index entries are
+  0 (they read the first real row), padded chunk pairs are ``(0, capacity)``
+  (a chunk starting past the packed tokens, which the kernels clamp away);
+* decode slot tables become int64.
+
+All padding of one bucket is one ``gdn_metadata_pad`` launch; no device
+tensor is read on the host.  Only the standard (radix-pool) metadata is
+handled -- the LogState variant is not part of this library.
+"""
 
 from __future__ import annotations
 
@@ -18,153 +28,166 @@ from dataclasses import fields, is_dataclass, replace
 import torch
 
 from ..kernel.metadata import copy_metadata, pad_metadata
-from .linear_attention_backend import LinearAttnMetadata, PackedLinearIndices
+from .linear_attention_backend import LinearAttnMetadata
+
+# prefill tables padded to the bucket's chunk capacity, and their fill values
+_CHUNK_TABLE_FILLS = {"chunk_write_slots": -1, "checkpoint_slots": -1, "checkpoint_chunks": 0,
+                      "snapshot_rows": 0, "snapshot_reqs": 0}
+_DECODE_SLOT_TABLES = ("slots", "read_slots", "write_slots")
 
 
-class _MetadataPadding:
-    """Collects (source, padded output, fill, pair tail) and pads them all in
-    one launch (``mixed.py:23-38``)."""
+def chunk_capacity(requests: int, capacity: int, chunk: int = 64) -> int:
+    """Most chunks ``requests`` positive lengths summing to at most
+    ``capacity`` can need: a length l takes ceil(l / chunk) = 1 + (l - 1) //
+    chunk chunks, and the (l - 1) sum to at most capacity - requests."""
+    return requests + (capacity - requests) // chunk
+
+
+class _Padding:
+    """Pending padded copies, run together in one launch by ``flush``."""
 
     def __init__(self):
-        self.copies = []
+        self._jobs: list[tuple[torch.Tensor, torch.Tensor, int, int]] = []
 
-    def __call__(self, tensor, capacity, value=0, *, chunk_tail=-1):
-        if tensor.shape[0] > capacity:
+    def add(self, tensor: torch.Tensor, rows: int, fill: int = 0, pair_tail: int = -1) -> torch.Tensor:
+        if tensor.shape[0] > rows:
             raise ValueError("metadata exceeds mixed graph capacity")
-        output = tensor.new_empty((capacity, *tensor.shape[1:]))
-        self.copies.append((tensor.contiguous(), output, value, chunk_tail))
-        return output
+        padded = torch.empty((rows, *tensor.shape[1:]), dtype=tensor.dtype, device=tensor.device)
+        self._jobs.append((tensor.contiguous(), padded, fill, pair_tail))
+        return padded
 
-    def finish(self):
-        if self.copies:
-            sources, outputs, fills, tails = zip(*self.copies)
-            pad_metadata(sources, outputs, fills, tails)
-
-
-def _packed_pad(indices: PackedLinearIndices, capacity: int, requests: int, chunk_size: int,
-                pad: _MetadataPadding) -> PackedLinearIndices:
-    """``mixed.py:41-56``: the most chunks positive lengths summing to
-    ``capacity`` can have, for the chunk and conv-chunk pair tables."""
-    chunks = requests + (capacity - requests) // chunk_size
-    conv_chunks = requests + (capacity - requests) // 64
-
-    def pad_chunks(source: torch.Tensor, count: int) -> torch.Tensor:
-        return pad(source, count, chunk_tail=capacity)
-
-    return replace(indices, chunk_indices=pad_chunks(indices.chunk_indices, chunks),
-                   conv_chunks=pad_chunks(indices.conv_chunks, conv_chunks))
+    def flush(self) -> None:
+        if self._jobs:
+            pad_metadata(*(list(column) for column in zip(*self._jobs)))
+            self._jobs = []
 
 
 def prepare_mixed_linear_metadata(prefill, decode, prefill_capacity: int):
-    """Normalise already-prepared metadata, install it, and return both
-    (``mixed.py:59-124``).  The prefill forward then takes exactly
-    ``prefill_capacity`` input rows, of which the first
-    ``sum(req.extend_len)`` are meaningful; request-level arrays and
-    ``cu_seqlens`` keep their actual values and shapes."""
+    """Normalise the actual-length metadata of ``prefill`` and ``decode`` to
+    the bucket of ``prefill_capacity`` tokens, install the results on the two
+    batches and return them.  The prefill forward then reads exactly
+    ``prefill_capacity`` input rows, of which the first ``sum(extend_len)``
+    are real; ``cu_seqlens`` and request-level arrays keep their actual
+    values.  The input metadata objects are left unmodified."""
     pm, dm = prefill.linear_attn_metadata, decode.linear_attn_metadata
     if not isinstance(pm, LinearAttnMetadata):
         raise TypeError("mixed prefill requires prepared linear metadata")
-    if type(dm) is not type(pm) or pm.phase != "prefill" or dm.phase != "decode":
+    if type(dm) is not type(pm) or (pm.phase, dm.phase) != ("prefill", "decode"):
         raise ValueError("mixed metadata requires matching prefill/decode backends")
     lengths = [req.extend_len for req in prefill.reqs]
-    if not lengths or any(length <= 0 for length in lengths):
+    if not lengths or min(lengths) <= 0:
         raise ValueError("mixed prefill requires nonempty positive request lengths")
-    if prefill_capacity < sum(lengths):
+    if sum(lengths) > prefill_capacity:
         raise ValueError("actual prefill length exceeds mixed graph capacity")
     indices = pm.prefill_indices
-    if indices is None or len(indices.cu_seqlens) != len(lengths) + 1:
+    if indices is None or indices.cu_seqlens.shape[0] != len(lengths) + 1:
         raise ValueError("prepare ordinary actual-length metadata before normalization")
-    pad = _MetadataPadding()
-    packed = _packed_pad(indices, prefill_capacity, len(lengths), 64, pad)
-    chunk_capacity = len(packed.chunk_indices)
     if pm.chunk_write_slots is None or pm.conv_token_slots is None:
         raise ValueError("mixed prefill requires direct-write metadata")
-    updates = dict(
-        prefill_indices=packed,
-        chunk_write_slots=pad(pm.chunk_write_slots, chunk_capacity, -1),
-        conv_token_slots=pad(pm.conv_token_slots, prefill_capacity, -1),
-    )
-    # at most one checkpoint per chunk; padded entries read the first real
-    # row and write nothing (slot -1)
-    for name in ("checkpoint_slots", "checkpoint_chunks", "snapshot_rows", "snapshot_reqs"):
-        tensor = getattr(pm, name)
-        if tensor is None:
-            raise ValueError(f"missing prefill {name}")
-        updates[name] = pad(tensor, chunk_capacity, -1 if name == "checkpoint_slots" else 0)
-    decode_updates = {}
-    for name in ("slots", "read_slots", "write_slots"):
-        tensor = getattr(dm, name)
-        if tensor is not None:
-            decode_updates[name] = tensor.to(torch.int64)
-    pad.finish()
-    normalized = replace(pm, **updates), replace(dm, **decode_updates)
+    missing = [name for name in _CHUNK_TABLE_FILLS if getattr(pm, name) is None]
+    if missing:
+        raise ValueError(f"missing prefill {missing[0]}")
+
+    chunks = chunk_capacity(len(lengths), prefill_capacity)
+    padding = _Padding()
+    packed = replace(
+        indices,
+        chunk_indices=padding.add(indices.chunk_indices, chunks, pair_tail=prefill_capacity),
+        conv_chunks=padding.add(indices.conv_chunks, chunk_capacity(len(lengths), prefill_capacity, 64),
+                                pair_tail=prefill_capacity))
+    prefill_tables = {name: padding.add(getattr(pm, name), chunks, fill) for name, fill in _CHUNK_TABLE_FILLS.items()}
+    prefill_tables["conv_token_slots"] = padding.add(pm.conv_token_slots, prefill_capacity, -1)
+    decode_tables = {name: getattr(dm, name).to(torch.int64) for name in _DECODE_SLOT_TABLES
+                     if getattr(dm, name) is not None}
+    padding.flush()
+    normalized = (replace(pm, prefill_indices=packed, **prefill_tables), replace(dm, **decode_tables))
     prefill.linear_attn_metadata, decode.linear_attn_metadata = normalized
     return normalized
 
 
+def _leaves(obj, path=()):
+    """Flattens a metadata structure into (kind, path, payload) entries in a
+    fixed order: ("tensor", path, tensor), ("node", path, shape signature)
+    for dataclasses / dicts / lists / tuples, ("const", path, value) for
+    anything else."""
+    if isinstance(obj, torch.Tensor):
+        yield "tensor", path, obj
+    elif is_dataclass(obj) and not isinstance(obj, type):
+        yield "node", path, (type(obj), None)
+        for f in fields(obj):
+            yield from _leaves(getattr(obj, f.name), path + (f.name,))
+    elif isinstance(obj, dict):
+        yield "node", path, (dict, tuple(obj))
+        for key, value in obj.items():
+            yield from _leaves(value, path + (key,))
+    elif isinstance(obj, (list, tuple)):
+        yield "node", path, (type(obj), len(obj))
+        for i, value in enumerate(obj):
+            yield from _leaves(value, path + (i,))
+    else:
+        yield "const", path, obj
+
+
+def _layout(t: torch.Tensor):
+    return t.shape, t.dtype, t.device
+
+
+def _vector_or_dense(t: torch.Tensor) -> bool:
+    return t.is_contiguous() or t.ndim == 1
+
+
 class MixedLinearCopyPlan:
-    """Copies fresh normalised metadata into the tensors of ``destination``
-    (the structure a graph captured), after validating that only tensor
-    contents changed (``mixed.py:127-197``).  Contiguous device tensors (and
-    strided vectors) go in one batched launch per device; the rest use
-    ``copy_``.  Nothing is written if validation fails."""
+    """Refreshes the tensors a graph captured (``destination``) from fresh
+    normalised metadata of the same structure.  ``copy`` first checks that
+    nothing but tensor contents changed -- same dataclass / container types,
+    keys and lengths, equal non-tensor values, same tensor shapes, dtypes and
+    devices -- and writes nothing if any check fails.  Device tensors that
+    are contiguous or vectors (any stride) are refreshed in one launch per
+    device; the rest with ``copy_``."""
 
     def __init__(self, destination):
-        self.tensors = []
-        self.constants = []
-        self.structures = []
-
-        def visit(dst, getter):
-            if isinstance(dst, torch.Tensor):
-                self.tensors.append((getter, dst, (dst.shape, dst.dtype, dst.device)))
-            elif is_dataclass(dst):
-                self.structures.append((getter, type(dst), None))
-                for field in fields(dst):
-                    visit(getattr(dst, field.name), lambda root, get=getter, name=field.name: getattr(get(root), name))
-            elif isinstance(dst, (tuple, list, dict)):
-                keys = tuple(dst) if isinstance(dst, dict) else tuple(range(len(dst)))
-                self.structures.append((getter, type(dst), keys if isinstance(dst, dict) else len(dst)))
-                for key in keys:
-                    visit(dst[key], lambda root, get=getter, key=key: get(root)[key])
-            else:
-                self.constants.append((getter, dst))
-
-        visit(destination, lambda root: root)
-        groups = {}
-        self.fallback = []
-        for index, (_, dst, _) in enumerate(self.tensors):
-            if dst.numel() == 0:
+        entries = list(_leaves(destination))
+        self._structure = [(kind, path, payload) for kind, path, payload in entries if kind != "tensor"]
+        self._targets = [(path, tensor, _layout(tensor)) for kind, path, tensor in entries if kind == "tensor"]
+        by_device: dict[torch.device, list[int]] = {}
+        self._eager: list[int] = []
+        for i, (_, tensor, _) in enumerate(self._targets):
+            if tensor.numel() == 0:
                 continue
-            if dst.is_cuda and (dst.is_contiguous() or dst.ndim == 1):
-                groups.setdefault(dst.device, []).append(index)
+            if tensor.is_cuda and _vector_or_dense(tensor):
+                by_device.setdefault(tensor.device, []).append(i)
             else:
-                self.fallback.append(index)
-        self.groups = [(tuple(indices), tuple(self.tensors[i][1] for i in indices)) for indices in groups.values()]
+                self._eager.append(i)
+        self._launches = list(by_device.values())
+
+    def _sources(self, source) -> list[torch.Tensor]:
+        entries = list(_leaves(source))
+        structure = [(kind, path, payload) for kind, path, payload in entries if kind != "tensor"]
+        tensors = [(path, tensor) for kind, path, tensor in entries if kind == "tensor"]
+        if len(structure) != len(self._structure) or len(tensors) != len(self._targets):
+            raise ValueError("mixed metadata structure changed")
+        for (kind, path, payload), (want_kind, want_path, want) in zip(structure, self._structure):
+            if (kind, path) != (want_kind, want_path):
+                raise ValueError("mixed metadata structure changed")
+            if kind == "node" and payload != want:
+                raise ValueError("mixed metadata sequence/dictionary changed")
+            if kind == "const" and payload != want:
+                raise ValueError("mixed metadata non-tensor value changed")
+        for (path, tensor), (want_path, _, layout) in zip(tensors, self._targets):
+            if path != want_path or _layout(tensor) != layout:
+                raise ValueError("mixed metadata tensor shape/dtype/device changed")
+        sources = [tensor for _, tensor in tensors]
+        for group in self._launches:
+            if not all(_vector_or_dense(sources[i]) for i in group):
+                raise ValueError("mixed metadata source strides changed")
+        return sources
 
     def copy(self, source) -> None:
-        try:
-            for get, kind, size in self.structures:
-                value = get(source)
-                if type(value) is not kind:
-                    raise ValueError("mixed metadata structure changed")
-                if size is not None and (tuple(value) if kind is dict else len(value)) != size:
-                    raise ValueError("mixed metadata sequence/dictionary changed")
-            for get, expected in self.constants:
-                if get(source) != expected:
-                    raise ValueError("mixed metadata non-tensor value changed")
-            sources = tuple(get(source) for get, _, _ in self.tensors)
-            for src, (_, _, layout) in zip(sources, self.tensors):
-                if not isinstance(src, torch.Tensor) or (src.shape, src.dtype, src.device) != layout:
-                    raise ValueError("mixed metadata tensor shape/dtype/device changed")
-            for indices, _ in self.groups:
-                if any(not sources[i].is_contiguous() and sources[i].ndim != 1 for i in indices):
-                    raise ValueError("mixed metadata source strides changed")
-        except (AttributeError, KeyError, IndexError, TypeError) as error:
-            raise ValueError("mixed metadata structure changed") from error
-        for indices, outputs in self.groups:
-            copy_metadata(tuple(sources[i] for i in indices), outputs)
-        for i in self.fallback:
-            self.tensors[i][1].copy_(sources[i])
+        sources = self._sources(source)  # validates everything before any write
+        for group in self._launches:
+            copy_metadata([sources[i] for i in group], [self._targets[i][1] for i in group])
+        for i in self._eager:
+            self._targets[i][1].copy_(sources[i])
 
 
-__all__ = ["MixedLinearCopyPlan", "prepare_mixed_linear_metadata"]
+__all__ = ["MixedLinearCopyPlan", "chunk_capacity", "prepare_mixed_linear_metadata"]

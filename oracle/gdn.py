@@ -492,6 +492,67 @@ def forward_verify(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, conv_stat
     return o.flatten(0, 1)
 
 
+def _batched_step(conv_state, recurrent_state, layer, x, gate, beta, conv_weight, A_log, dt_bias, reads,
+                  writes, round_conv, H, dk, HV, dv, dtype):
+    """One token for every sequence at once: conv window of ``reads`` ->
+    ``writes``, split, normalise, gate, recurrence of ``reads`` -> ``writes``
+    (pool I/O through ``index_select`` / ``index_copy_``).  Returns o [B, HV, dv]."""
+    B, C = x.shape
+    K = conv_weight.shape[-1]
+    conv_layer = conv_state[:, layer]
+    windows = conv_layer.index_select(0, reads)  # [B, C, K-1]
+    acc = (torch.cat([windows, x[:, :, None]], -1).to(dtype) * conv_weight.reshape(C, K).to(dtype)[None]).sum(-1)
+    if round_conv:
+        acc = acc.to(x.dtype).to(dtype)
+    y = silu(acc).to(x.dtype)
+    conv_layer.index_copy_(0, writes, torch.cat([windows[:, :, 1:], x[:, :, None]], -1))
+    q, k, v = split_qkv(y, H, dk, HV, dv)
+    q = _expand_heads(l2norm(q.to(dtype)), HV) * dk ** -0.5  # [B, HV, dk]
+    k = _expand_heads(l2norm(k.to(dtype)), HV)
+    g = -torch.exp(A_log.to(dtype))[None] * softplus_decode(gate.to(dtype) + dt_bias.to(dtype))
+    b = torch.sigmoid(beta.to(dtype))
+    pool_layer = recurrent_state[:, layer]
+    S = pool_layer.index_select(0, reads).to(dtype) * torch.exp(g)[:, :, None, None]
+    delta = (v.to(dtype) - (S * k[..., None]).sum(2)) * b[..., None]
+    S = S + k[..., None] * delta[:, :, None, :]
+    o = (S * q[..., None]).sum(2)
+    pool_layer.index_copy_(0, writes, S.to(recurrent_state.dtype))
+    return o.to(x.dtype)
+
+
+def forward_decode_batched(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, conv_state,
+                           recurrent_state, layer, read_slots, write_slots, num_k_heads, head_k_dim,
+                           num_v_heads, head_v_dim, dtype=torch.float32):
+    """``forward_decode`` vectorised over sequences, with the pool I/O as
+    ``index_select`` / ``index_copy_`` (the CPU baseline form for decode).
+    Read and write slot sets must each be free of repeats."""
+    reads = torch.as_tensor(read_slots, dtype=torch.long)
+    writes = torch.as_tensor(write_slots, dtype=torch.long)
+    return _batched_step(conv_state, recurrent_state, layer, mixed_qkv, gate, beta, conv_weight, A_log, dt_bias,
+                         reads, writes, False, num_k_heads, head_k_dim, num_v_heads, head_v_dim, dtype)
+
+
+def forward_verify_batched(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, conv_state,
+                           recurrent_state, layer, baseline_slots, write_slots, num_k_heads,
+                           head_k_dim, num_v_heads, head_v_dim, dtype=torch.float32):
+    """``forward_verify`` as T batched steps (the CPU baseline form for
+    verify): step t reads the window and state step t-1 wrote to
+    ``write_slots[:, t-1]`` (the baseline slots for t = 0), with the conv
+    pre-activation rounded to the io dtype as the verify torch conv does."""
+    B, T = write_slots.shape
+    writes = torch.as_tensor(write_slots, dtype=torch.long)
+    x = mixed_qkv.view(B, T, -1)
+    gv, bv = gate.view(B, T, -1), beta.view(B, T, -1)
+    out = torch.empty(B, T, num_v_heads, head_v_dim, dtype=mixed_qkv.dtype)
+    read = torch.as_tensor(baseline_slots, dtype=torch.long)
+    for t in range(T):
+        out[:, t] = _batched_step(conv_state, recurrent_state, layer, x[:, t], gv[:, t], bv[:, t], conv_weight,
+                                  A_log, dt_bias, read, writes[:, t], True, num_k_heads, head_k_dim, num_v_heads,
+                                  head_v_dim, dtype)
+        read = writes[:, t]
+    return out.flatten(0, 1)
+
+
 def single_pass_decode_output(state, q_hat, k_hat, v, g, beta, scale):
     """The one-read decode identity of ``fused_recurrent.py:219-222`` /
     ``gdn_replay.py``: with ``S' = e^g S + k delta^T``,

@@ -259,3 +259,59 @@ def test_linear_state_pool_layout():
     assert pool.recurrent_state.shape == (3, 2, 2, 8, 16) and pool.recurrent_state.dtype == torch.float32
     single = LinearStatePool(3, 2, 40, 4, 2, 8, 16, "cpu", torch.bfloat16, state_dtype=None)
     assert single.recurrent_state.dtype == torch.bfloat16
+
+
+def _planner(page):
+    from logssms_amd.cache import MarconiCheckpointer
+    return MarconiCheckpointer(pool=None, page_size=page)
+
+
+def test_marconi_checkpoint_plan_matches_oracle():
+    """``cache/marconi/manager.py:248-270`` placement against the oracle's
+    restatement on random requests: planned checkpoints inside and at both
+    ends of the extension, page boundaries with and without a checkpoint."""
+    from logssms_amd.cache import MarconiRequestState
+    rng = random.Random(11)
+    for trial in range(400):
+        page = rng.choice([64, 128, 256])
+        cached = rng.randrange(0, 6) * page
+        device = cached + rng.randrange(1, 4 * page)
+        candidates = sorted({rng.randrange(cached, device + page) // 64 * 64 for _ in range(rng.randrange(0, 4))})
+        checkpoints = {e: 1000 + i for i, e in enumerate(candidates) if e > 0}
+        if rng.random() < 0.3:
+            checkpoints[device] = 2000
+        states = (rng.randrange(0, 50), rng.randrange(50, 100))
+        writes, copies = _planner(page).plan(MarconiRequestState(states, dict(checkpoints)), cached, device)
+        want_writes, want_copies = md.marconi_checkpoint_writes(
+            [dict(cached_len=cached, device_len=device, states=states, checkpoints=dict(checkpoints))], page)
+        assert writes == want_writes[0], trial
+        assert copies == want_copies, trial
+
+
+def test_marconi_branch_checkpoint_known_answer():
+    """tests/hybrid/test_marconi.py:226-268: a request of ps + 12 tokens with
+    a branch checkpoint planned at ps writes [ps, ps + 12] to the two live
+    states, and the branch slot receives a copy of the state at ps."""
+    from logssms_amd.cache import MarconiRequestState
+    from logssms_amd.core import Batch, Request
+    ps = 64
+    planner = _planner(ps)
+    planner.requests[0] = MarconiRequestState(states=(7, 9), checkpoints={ps: 3})
+    batch = Batch([Request(0, 0, ps + 12)], "prefill")
+    planner.prepare_batch(batch)
+    assert batch.cache_metadata.checkpoint_writes == [[(ps, 7), (ps + 12, 9)]]
+    assert batch.cache_metadata.checkpoint_copies == [(7, 3)]
+    decode = Batch([Request(0, ps + 12, ps + 13)], "decode")
+    planner.prepare_batch(decode)
+    assert decode.cache_metadata is None
+
+
+def test_marconi_copy_blocks_rejects_aliasing():
+    pool = _small_pool()
+    with pytest.raises(ValueError):
+        pool.copy_blocks([1, 2], [3, 3])
+    with pytest.raises(ValueError):
+        pool.copy_blocks([1, 2], [2, 4])
+    with pytest.raises(ValueError):
+        pool.copy_blocks([1], [2, 4])
+    pool.copy_blocks([], [])

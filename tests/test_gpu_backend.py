@@ -331,3 +331,48 @@ def test_prefill_resuming_mid_page_writes_windows_after_reading_history(dims):
     assert_bf16_close(got, want)
     torch.testing.assert_close(pool.conv_state.cpu(), conv_ref, rtol=0, atol=0)
     assert_state_close(pool.recurrent_state, state_ref)
+
+
+def test_marconi_checkpointer_writes_live_states_and_copies_the_branch():
+    """``cache/marconi/manager.py:248-278`` end to end on the block pool: a
+    prefill of ps + 12 tokens with a branch checkpoint planned at ps writes
+    the states at ps and ps + 12 into the two live slots, and
+    ``after_forward`` copies the live state at ps (state and conv window,
+    every lane) into the branch slot in one launch.  The live states equal a
+    plain slot pool run with the same writes bit for bit."""
+    from logssms_amd.cache import MarconiCheckpointer, MarconiRequestState
+    from logssms_amd.core import Batch, Context, MarconiCacheMetadata, Request
+    g = gen(48)
+    cfg = _cfg(H=2, HV=4, dk=64, dv=64, layer=2)
+    hybrid = _hybrid(cfg, 4, 48, dtype=torch.bfloat16)
+    hybrid.storage.copy_(randn(*hybrid.storage.shape, g=g, std=0.1).to(torch.bfloat16))
+    s0, s1, branch = (hybrid.allocate_state() for _ in range(3))
+    ps = hybrid.layout.block_size
+    planner = MarconiCheckpointer(hybrid, ps)
+    planner.requests[0] = MarconiRequestState((s0, s1), {ps: branch})
+    T = ps + 12
+    w = _weights(g, cfg, T)
+    table = torch.zeros(1, 256, dtype=torch.int64, device=DEV)
+    batch = Batch([Request(0, 0, T)], "prefill")
+    planner.prepare_batch(batch)
+    assert batch.cache_metadata.checkpoint_writes == [[(ps, s0), (T, s1)]]
+    out_h = _forward(Context(page_size=ps, linear_state=hybrid, state_table=table), batch, w, cfg).clone()
+    planner.after_forward(batch)
+    plain = _pool(cfg, 48, layers=4, state_dtype=torch.bfloat16)
+    sparse = MarconiCacheMetadata(checkpoint_writes=batch.cache_metadata.checkpoint_writes)
+    out_p = _forward(Context(page_size=ps, linear_state=plain, state_table=table),
+                     Batch([Request(0, 0, T)], "prefill", cache_metadata=sparse), w, cfg)
+    torch.testing.assert_close(out_h, out_p, rtol=0, atol=0)
+    group, lane = divmod(cfg.layer_idx, hybrid.layout.layers_per_group)
+    blk = {s: int(hybrid.group_table[s, group]) for s in (s0, s1, branch)}
+    for s in (s0, s1):
+        torch.testing.assert_close(hybrid.recurrent_state[blk[s], lane], plain.recurrent_state[s, cfg.layer_idx],
+                                   rtol=0, atol=0)
+        torch.testing.assert_close(hybrid.conv_state[blk[s], lane], plain.conv_state[s, cfg.layer_idx], rtol=0, atol=0)
+    for other_lane in range(hybrid.layout.layers_per_group):
+        for g_ in range(hybrid.layout.state_groups):
+            a, b = int(hybrid.group_table[s0, g_]), int(hybrid.group_table[branch, g_])
+            torch.testing.assert_close(hybrid.recurrent_state[b, other_lane], hybrid.recurrent_state[a, other_lane],
+                                       rtol=0, atol=0)
+            torch.testing.assert_close(hybrid.conv_state[b, other_lane], hybrid.conv_state[a, other_lane],
+                                       rtol=0, atol=0)

@@ -487,6 +487,59 @@ def test_verify_group_matches_oracle(permute_rows, io):
     assert_state_close(state, state_ref)
 
 
+@pytest.mark.parametrize("shape", [(2, 4, 64, 21), (1, 8, 64, 5), (2, 16, 64, 18)],
+                         ids=["T21_segments", "group8_stepwise", "group8_T18"])
+def test_verify_beyond_fused_limits_matches_oracle(shape):
+    """Verify groups of more than 16 drafts (16-step segments, each resuming
+    from the previous segment's last write slot) and head groups of more than
+    4 v-heads per key head (conv_decode + slotted recurrence per step) against
+    the oracle's verify (the reference's fused_recurrent takes any T and head
+    ratio, ``fused_recurrent.py:461-550``)."""
+    from logssms_amd.kernel.linear_attention.fused_backend import verify_group
+    H, HV, d, T = shape
+    g = gen(13 + T)
+    cfg = _cfg(H=H, HV=HV, dk=d, dv=d, layer=1)
+    B = 3
+    slots = B * (T + 1) + 4
+    rows = B * T
+    inp = _backend_inputs(g, cfg, rows + 3, slots)
+    perm = torch.randperm(slots, generator=g)
+    baseline = perm[:B]
+    writes = perm[B:B + B * T].view(B, T)
+    row_idx = torch.randperm(rows + 3, generator=g)[:rows]
+    conv_ref, state_ref = inp["conv"].clone(), inp["state"].clone()
+    want = ref.forward_verify(inp["mixed"][row_idx], inp["gate"][row_idx], inp["beta"][row_idx], inp["weight"],
+                              inp["A_log"], inp["dt_bias"], conv_ref, state_ref, 1, baseline, writes, H, d, HV, d)
+    conv, state = inp["conv"].to(DEV), inp["state"].to(DEV)
+    out = torch.zeros(rows + 3, HV, d, device=DEV, dtype=torch.bfloat16)
+    verify_group(inp["mixed"].to(DEV), inp["gate"].to(DEV), inp["beta"].to(DEV), inp["weight"].to(DEV),
+                 inp["A_log"].to(DEV), inp["dt_bias"].to(DEV), cfg, conv, state, row_idx.to(DEV), baseline.to(DEV),
+                 writes.to(DEV), out)
+    assert_bf16_close(out[row_idx.to(DEV)], want)
+    torch.testing.assert_close(conv.cpu(), conv_ref, rtol=0, atol=0)
+    assert_state_close(state, state_ref)
+
+
+def test_decode_step_wide_head_group_matches_oracle():
+    from logssms_amd.kernel.linear_attention.fused_backend import decode_step
+    H, HV, d = 2, 16, 64
+    g = gen(14)
+    cfg = _cfg(H=H, HV=HV, dk=d, dv=d, layer=1)
+    B, slots = 5, 12
+    inp = _backend_inputs(g, cfg, B, slots)
+    perm = torch.randperm(slots, generator=g)
+    reads, writes = perm[:B], torch.cat([perm[:2], perm[B:B + 3]])
+    conv_ref, state_ref = inp["conv"].clone(), inp["state"].clone()
+    want = ref.forward_decode(inp["mixed"], inp["gate"], inp["beta"], inp["weight"], inp["A_log"], inp["dt_bias"],
+                              conv_ref, state_ref, 1, reads, writes, H, d, HV, d)
+    conv, state = inp["conv"].to(DEV), inp["state"].to(DEV)
+    got = decode_step(inp["mixed"].to(DEV), inp["gate"].to(DEV), inp["beta"].to(DEV), inp["weight"].to(DEV),
+                      inp["A_log"].to(DEV), inp["dt_bias"].to(DEV), cfg, conv, state, reads.to(DEV), writes.to(DEV))
+    assert_bf16_close(got, want)
+    torch.testing.assert_close(conv.cpu(), conv_ref, rtol=0, atol=0)
+    assert_state_close(state, state_ref)
+
+
 def _wide_pools(conv, state):
     """Device views of `conv` / `state` whose element offsets pass 2**31 bytes:
     a 1 GiB slot stride for the state pool and the reference's conv layer

@@ -500,3 +500,33 @@ def test_forward_verify_equals_decode_steps_with_per_step_slots():
             read = int(writes[b, t])
     torch.testing.assert_close(state_v, state_d, rtol=1e-5, atol=1e-6)
     assert torch.equal(conv_v, conv_d)
+
+
+def test_batched_decode_and_verify_equal_the_per_sequence_forms():
+    """The vectorised CPU-baseline forms (index_select / index_copy_ pool I/O)
+    against ``forward_decode`` / ``forward_verify``."""
+    gen = torch.Generator().manual_seed(62)
+    H, HV, dk, dv, B, T = 2, 4, 16, 8, 4, 3
+    C = 2 * H * dk + HV * dv
+    w = _composition_inputs(gen, B * T, H, HV, dk, dv, C)
+    w["mixed"] = w["mixed"].to(torch.bfloat16)
+    conv0 = torch.randn(20, 2, C, 3, generator=gen).to(torch.bfloat16)
+    state0 = torch.randn(20, 2, HV, dk, dv, generator=gen) * 0.1
+    reads, writes = torch.tensor([3, 7, 1, 0]), torch.tensor([3, 9, 11, 12])
+    a = (conv0.clone(), state0.clone())
+    b = (conv0.clone(), state0.clone())
+    args = (w["gate"][:B], w["beta"][:B], w["weight"].to(torch.bfloat16), w["A_log"], w["dt_bias"])
+    o1 = gdn.forward_decode(w["mixed"][:B], *args, *a, 1, reads, writes, H, dk, HV, dv)
+    o2 = gdn.forward_decode_batched(w["mixed"][:B], *args, *b, 1, reads, writes, H, dk, HV, dv)
+    torch.testing.assert_close(o2.float(), o1.float(), rtol=1e-2, atol=1e-2)
+    assert torch.equal(a[0], b[0])
+    torch.testing.assert_close(a[1], b[1], rtol=1e-5, atol=1e-6)
+    base, wt = torch.tensor([3, 7, 1, 0]), torch.arange(8, 8 + B * T).view(B, T)
+    a = (conv0.clone(), state0.clone())
+    b = (conv0.clone(), state0.clone())
+    args = (w["gate"], w["beta"], w["weight"].to(torch.bfloat16), w["A_log"], w["dt_bias"])
+    o1 = gdn.forward_verify(w["mixed"], *args, *a, 0, base, wt, H, dk, HV, dv)
+    o2 = gdn.forward_verify_batched(w["mixed"], *args, *b, 0, base, wt, H, dk, HV, dv)
+    torch.testing.assert_close(o2.float(), o1.float(), rtol=1e-2, atol=1e-2)
+    assert torch.equal(a[0], b[0])
+    torch.testing.assert_close(a[1], b[1], rtol=1e-5, atol=1e-6)
