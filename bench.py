@@ -479,6 +479,29 @@ def layer_gpu(dev, hidden=2048, seed=7):
     return step, parts
 
 
+def rmw_sweep(dev, steps, warmup, nbytes=2 << 30):
+    """The box's 1-read:1-write HBM ceiling: ``gdn_probe_rmw`` (an in-place
+    x <- 1.0 x stream over 16-byte vectors) over a 2 GiB buffer, the size of
+    config 3's state pool, for block sizes and loads in flight per lane.
+    GB/s counts the bytes read plus the bytes written."""
+    from logssms_amd import _lib
+    buf = torch.ones(nbytes // 4, device=dev)
+    stream = _lib.stream_of(buf)
+    runs = []
+    for block_kib in (64, 1024):
+        for loads in (1, 4, 16):
+            for nt in (0, 1):
+                ms = _time(lambda: _lib.call("gdn_probe_rmw", buf.data_ptr(), nbytes, block_kib << 10, loads, nt,
+                                             stream), steps, warmup)
+                runs.append({"block_kib": block_kib, "loads_in_flight": loads, "nontemporal": nt, "ms": ms,
+                             "GB/s": 2 * nbytes / (ms * 1e-3) / 1e9})
+    best = max(runs, key=lambda r: r["GB/s"])
+    del buf
+    torch.cuda.empty_cache()
+    return {"config": "gdn_probe_rmw over 2 GiB in place (1 read : 1 write, 16-byte vectors)", "best": best,
+            "frac_hbm": best["GB/s"] * 1e9 / PEAK_HBM, "runs": runs}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -488,10 +511,11 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="time budget of each CPU baseline leg (chunked prefill; naive prefill, decode and "
                          "verify get a share of it)")
-    ap.add_argument("--only", choices=["all", "prefill", "decode", "verify", "norm", "layer", "copy"],
+    ap.add_argument("--only", choices=["all", "prefill", "decode", "verify", "norm", "layer", "copy", "rmw"],
                     default="all",
                     help="'copy' times a plain 512 MiB device copy (the calibration kernel for the "
-                         "FETCH_SIZE / WRITE_SIZE counter passes)")
+                         "FETCH_SIZE / WRITE_SIZE counter passes); 'rmw' the in-place read-modify-write "
+                         "ceiling sweep")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -569,6 +593,9 @@ def main():
         del step4, inp4
         torch.cuda.empty_cache()
 
+    if args.only == "rmw":
+        print(json.dumps({"rmw": rmw_sweep(dev, max(args.steps, 10), args.warmup)}))
+        return
     if args.only in ("all", "decode"):
         step, tensors = decode_gpu(dev)
         ms = _time(step, max(args.steps, 20), args.warmup)
@@ -581,6 +608,8 @@ def main():
                                                "kind": "port"}
         del step, tensors
         torch.cuda.empty_cache()
+    if args.only == "all":
+        extra["rmw_ceiling"] = rmw_sweep(dev, 10, 2)
     if args.only in ("all", "verify"):
         step, commit, tensors = verify_gpu(dev)
         ms = _time(step, max(args.steps, 20), args.warmup)

@@ -386,6 +386,17 @@ int gdn_prefill_fused_noalloc(const void* mixed, int64_t row_stride, int io_dtyp
 /* Bytes of gdn_prefill_fused_noalloc's per-GPU staging array. */
 int64_t gdn_prefill_noalloc_scratch_bytes(void);
 
+/*
+ * Measurement probe, no counterpart in the reference: buf[i] <- buf[i] * 1.0
+ * in place over `bytes` (16-byte vectors), each block owning `block_bytes`
+ * consecutive bytes and each lane keeping `loads_in_flight` (1, 2, 4, 8, 16)
+ * 16-byte loads in flight before its stores, optionally non-temporal.  The
+ * 1-read:1-write HBM ceiling the decode / verify state updates are read
+ * against (bench.py --only rmw).
+ */
+int gdn_probe_rmw(void* buf, int64_t bytes, int64_t block_bytes, int loads_in_flight, int nontemporal,
+                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif

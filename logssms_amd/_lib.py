@@ -56,6 +56,7 @@ SIGNATURES = {
     "gdn_prefill_fused_noalloc": [P, I64, I32, P, I32, P, I32, I64, I64, I64, I64, I64, I64, P, I64, I64, P, I64,
                                   I64, I32, P, I64, I64, I32, P, I32, P, I32, P, I32, I64, I64, I64, I64, P, I32,
                                   P, I32, P, I32, P, I32, I64, P, F32, P],
+    "gdn_probe_rmw": [P, I64, I64, I32, I32, P],
     "gdn_commit_accepted": [P, I64, I64, I64, P, I64, I64, I64, P, I32, P, I64, I64, I32, P, I32, I64, I64, P],
 }
 

@@ -91,9 +91,10 @@ __device__ __forceinline__ f4_t mma(h8_t a, h8_t b, f4_t c) {
 }
 __device__ __forceinline__ f4_t zero4() { return f4_t{0.f, 0.f, 0.f, 0.f}; }
 
-__device__ __forceinline__ _Float16 to_op(float x) {
-  return static_cast<_Float16>(__builtin_amdgcn_fmed3f(x, -65504.f, 65504.f));
-}
+// f16 MFMA operand, round to nearest even (pairs become one v_cvt_pk_f16_f32).
+// Magnitudes beyond the f16 range (65504) become +-inf, which then shows in
+// the outputs and states rather than passing as a saturated value.
+__device__ __forceinline__ _Float16 to_op(float x) { return static_cast<_Float16>(x); }
 __device__ __forceinline__ h8_t cat(h4_t lo, h4_t hi) { return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7); }
 // Left operand, row `row` of a row-major f16 matrix, k block at column k0.
 __device__ __forceinline__ h8_t afrag(const _Float16* base, int ld, int row, int k0, int g) {
@@ -453,7 +454,10 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const bool keep = strict ? t > s0 + e : t >= s0 + e;
-        s[e] = keep ? bt * s[e] * fast_exp2(fminf(gti - gs[e], 0.f)) : 0.f;
+        // G is a running sum of log-decays, so kept entries (t >= s) have a
+        // non-positive exponent; a dropped entry's exponent may overflow to
+        // inf, which the select discards.
+        s[e] = keep ? bt * s[e] * fast_exp2(gti - gs[e]) : 0.f;
       }
       return s;
     };
@@ -493,7 +497,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         const float gsc = gt[sc + lr];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          s[e] = (t0 + 4 * lg + e > sc + lr) ? bt4[e] * s[e] * fast_exp2(fminf(gt4[e] - gsc, 0.f)) : 0.f;
+          s[e] = (t0 + 4 * lg + e > sc + lr) ? bt4[e] * s[e] * fast_exp2(gt4[e] - gsc) : 0.f;
         return s;
       };
       auto lmask_t = [&](f4_t s, int tc, int s0) {  // entries (tc + c, s0 + 4g + e)
@@ -570,8 +574,9 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         const int t = 16 * ti + lr, s0 = 16 * tj + 4 * lg;
         store_row4(A, t, s0, -masked(gt, tile(K, LDK, ti, tj), t, s0, true, true));
       };
-      const int w = sw - 2;  // 0..3
-      // waves 6-7 share SIMDs with the v conv waves, 8-9 with the inverse waves
+      const int w = sw - 2;  // 0..3 tile waves; -2, -1 the inverse waves (phase B only)
+      // waves 6-7 share SIMDs with the v conv waves, 8-9 with the inverse waves;
+      // the inverse waves, done early in the second phase, take its two tiles
       if (!second) {
         if (w == 0) {
           ltile(2, 0);
@@ -591,9 +596,9 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
           mtile(3, 1);
         }
       } else {
-        if (w == 0) {
+        if (w == -2) {
           mtile(3, 2);
-        } else if (w == 1) {
+        } else if (w == -1) {
           mtile(3, 3);
         }
       }
@@ -671,16 +676,25 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     }
     // Every row of the window is a clamped row of the sequence, loaded with
     // no select on the data, so nothing waits for these loads before the next
-    // chunk's conv.  Rows past the end only feed output rows that conv_v
-    // zeroes; the rows before the start (first chunk) are the conv history or
-    // zero, which conv_v substitutes.
+    // chunk's conv.  Rows past the end only feed V rows that beta = 0 removes
+    // from the chain; the rows before the start (first chunk) are the conv
+    // history or zero, which conv_v substitutes.
+    // Addressing: a wave-uniform row base plus a 32-bit lane offset.  The
+    // rows a chunk's lanes read lie in [cv kC - 3, cv kC + 63] clamped to the
+    // sequence [0, len), so their offsets from the lowest clamped row are
+    // small and non-negative (row_stride < 2^24 elements keeps them in 32 bits).
     auto prefetch_fv = [&](int64_t cv) __attribute__((always_inline)) {
-      const int64_t t0 = cv * kC + VT * fvtb - 3;
+      const int64_t c0 = cv * kC;
+      const int hi = static_cast<int>(len - 1 - c0);            // last row, relative to the chunk start
+      const int lo = c0 >= 3 ? -3 : -static_cast<int>(c0);      // first row the window may reach
+      const int base = lo < hi ? lo : hi;
+      const uint16_t* cb = mixed + (bos + c0 + base) * rs + vch;
 #pragma unroll
       for (int i = 0; i < VNR; ++i) {
-        const int64_t t = t0 + i;
-        const int64_t row = len > 0 ? bos + (t < 0 ? 0 : (t >= len ? len - 1 : t)) : 0;
-        vraw[i] = *reinterpret_cast<const u4_t*>(mixed + row * rs + ch0);
+        const int t = VT * fvtb + i - 3;
+        const int r = (t < lo ? lo : t) < hi ? (t < lo ? lo : t) : hi;
+        const uint32_t off = static_cast<uint32_t>((r - base) * static_cast<int>(rs) + 8 * fvdb);
+        vraw[i] = *reinterpret_cast<const u4_t*>(cb + off);
       }
     };
     // conv of chunk cv into registers, stage by stage over all VT x 8 values
@@ -690,7 +704,6 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     // y = round(silu(round(sum_tap w x))), the outer rounding being the io pack.
     uint4 vo[VT];
     auto conv_v = [&](int64_t cv) __attribute__((always_inline)) {
-      const int nv = valid_rows(cv);
       float win[3][8];
 #pragma unroll
       for (int j = 0; j < 3; ++j) unpack8<IOT>(to_uint4(vraw[j]), win[j]);
@@ -739,9 +752,9 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       for (int i = 0; i < VT; ++i) {
 #pragma unroll
         for (int c = 0; c < 8; ++c) y[i][c] *= d[i][c];  // fast_silu
-        const uint4 o = to_f16x8<IOT>(pack8_io<IOT>(y[i]));
-        const bool ok = VT * fvtb + i < nv;
-        vo[i] = make_uint4(ok ? o.x : 0u, ok ? o.y : 0u, ok ? o.z : 0u, ok ? o.w : 0u);
+        // rows past the end hold the conv of clamped (real, finite) rows; the
+        // chain scales them by beta = 0 there
+        vo[i] = to_f16x8<IOT>(pack8_io<IOT>(y[i]));
       }
     };
     auto stage_fv = [&]() __attribute__((always_inline)) {
@@ -787,11 +800,15 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       lds_barrier();  // P0
       inv_first(0);
       inv_second(0);
+      tiles(0, true);
       lds_barrier();  // B(0)
       for (int64_t c = 0; c < nchunks; ++c) {
         if (c + 1 < nchunks) inv_first(c + 1);
         lds_barrier();  // M(c)
-        if (c + 1 < nchunks) inv_second(c + 1);
+        if (c + 1 < nchunks) {
+          inv_second(c + 1);
+          tiles(c + 1, true);
+        }
         lds_barrier();  // B(c+1)
       }
     } else if (sw >= 6) {
@@ -815,7 +832,13 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       lds_barrier();  // P0
       lds_barrier();  // B(0)
       for (int64_t c = 0; c < nchunks; ++c) {
-        if constexpr (FUSED) conv_v(c + 1);
+        if constexpr (FUSED) {
+          conv_v(c + 1);
+          // keep the conv in this phase: the scheduler would otherwise sink
+          // it past the barrier into the busier second phase
+#pragma unroll
+          for (int i = 0; i < VT; ++i) asm volatile("" ::"v"(vo[i].x), "v"(vo[i].y), "v"(vo[i].z), "v"(vo[i].w));
+        }
         lds_barrier();  // M(c)
         // The row loads for the conv of c + 2 go out first, so they have the
         // whole phase to arrive before that conv (right after the next
@@ -881,14 +904,12 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       prefetch_kq(2);
       lds_barrier();  // P0
       tiles(0, false);
-      tiles(0, true);
       lds_barrier();  // B(0)
       for (int64_t c = 0; c < nchunks; ++c) {
         if (c + 1 < nchunks) tiles(c + 1, false);
         lds_barrier();  // M(c)
         stage_kq(c + 2);
         prefetch_kq(c + 3);
-        if (c + 1 < nchunks) tiles(c + 1, true);
         lds_barrier();  // B(c+1)
       }
     }
@@ -955,12 +976,13 @@ extern "C" int gdn_prefill_fused(const void* q, const void* k, const void* mixed
                   chunk_write_slots && out,
               "gdn_prefill_fused: null input");
   const bool covered = kernel_width == 4 && (io_dtype == GDN_BF16 || io_dtype == GDN_F16) && dv % 64 == 0 &&
-                       (dk == 32 || dk == 64 || dk == 128) && row_stride % 8 == 0 && aligned16(mixed) &&
+                       (dk == 32 || dk == 64 || dk == 128) && row_stride % 8 == 0 && row_stride > 0 &&
+                       row_stride < (int64_t(1) << 24) && aligned16(mixed) &&
                        aligned16(weight) && aligned16(conv_state) && conv_slot_stride % 8 == 0 &&
                        conv_layer_stride % 8 == 0 && (state_dtype == GDN_F32 || state_dtype == io_dtype);
   if (!covered) {
     set_error("gdn_prefill_fused: not covered (needs conv width 4, 16-bit io, dk in {32, 64, 128}, dv %% 64 == 0, "
-              "16-byte aligned rows and conv pool, fp32 or io-typed state)");
+              "16-byte aligned rows shorter than 2^24 elements and conv pool, fp32 or io-typed state)");
     return GDN_ERR_UNSUPPORTED;
   }
   ChunkParams p{};

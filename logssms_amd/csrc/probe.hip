@@ -1,0 +1,75 @@
+// Bandwidth probe for the HBM-bound kernels: an in-place read-modify-write
+// stream (x <- a x over 16-byte vectors), the access mix of the decode state
+// update (each 64 KiB of state read once and written back once).  Not part of
+// the GDN path; bench.py --only rmw uses it to measure the 1-read:1-write
+// ceiling of the box that the decode / verify fractions are read against.
+#include "common.hpp"
+
+namespace gdn {
+namespace {
+
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// Each block owns `per_block` consecutive vectors; each lane keeps U loads in
+// flight before its stores.
+template <int U, bool NT>
+__global__ __launch_bounds__(256) void rmw_kernel(f4v* buf, int64_t n_vec, int64_t per_block, float a) {
+  const int64_t begin = static_cast<int64_t>(blockIdx.x) * per_block;
+  const int64_t end = begin + per_block < n_vec ? begin + per_block : n_vec;
+  for (int64_t i0 = begin + threadIdx.x; i0 < end; i0 += 256 * U) {
+    f4v v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + 256 * u;
+      if (i < end) v[u] = NT ? __builtin_nontemporal_load(buf + i) : buf[i];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + 256 * u;
+      if (i < end) {
+        if (NT) __builtin_nontemporal_store(v[u] * a, buf + i);
+        else buf[i] = v[u] * a;
+      }
+    }
+  }
+}
+
+template <int U>
+int launch_rmw(f4v* buf, int64_t n_vec, int64_t per_block, int nontemporal, hipStream_t s) {
+  const int64_t blocks = (n_vec + per_block - 1) / per_block;
+  if (blocks > 0x7fffffff) {
+    set_error("gdn_probe_rmw: grid too large");
+    return GDN_ERR_INVALID;
+  }
+  if (nontemporal)
+    hipLaunchKernelGGL((rmw_kernel<U, true>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, buf, n_vec,
+                       per_block, 1.0f);
+  else
+    hipLaunchKernelGGL((rmw_kernel<U, false>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, buf, n_vec,
+                       per_block, 1.0f);
+  return GDN_LAUNCH_CHECK("gdn_probe_rmw launch");
+}
+
+}  // namespace
+}  // namespace gdn
+
+extern "C" int gdn_probe_rmw(void* buf, int64_t bytes, int64_t block_bytes, int loads_in_flight, int nontemporal,
+                             void* stream) {
+  using namespace gdn;
+  GDN_REQUIRE(buf && bytes > 0 && bytes % 16 == 0 && block_bytes >= 16 && block_bytes % 16 == 0,
+              "gdn_probe_rmw: bad sizes");
+  GDN_REQUIRE((reinterpret_cast<uintptr_t>(buf) & 15) == 0, "gdn_probe_rmw: buffer not 16-byte aligned");
+  auto* v = static_cast<f4v*>(buf);
+  const int64_t n = bytes / 16, per = block_bytes / 16;
+  auto s = static_cast<hipStream_t>(stream);
+  switch (loads_in_flight) {
+    case 1: return launch_rmw<1>(v, n, per, nontemporal, s);
+    case 2: return launch_rmw<2>(v, n, per, nontemporal, s);
+    case 4: return launch_rmw<4>(v, n, per, nontemporal, s);
+    case 8: return launch_rmw<8>(v, n, per, nontemporal, s);
+    case 16: return launch_rmw<16>(v, n, per, nontemporal, s);
+    default:
+      set_error("gdn_probe_rmw: loads_in_flight %d not in {1, 2, 4, 8, 16}", loads_in_flight);
+      return GDN_ERR_UNSUPPORTED;
+  }
+}

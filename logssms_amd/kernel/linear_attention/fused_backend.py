@@ -101,12 +101,14 @@ def _fused_covered(mixed_qkv, config, conv_state, recurrent_state) -> bool:
     """The shapes ``gdn_prefill_qk`` and ``gdn_prefill_fused`` take (checked
     before the first launch, so an uncovered shape launches nothing and the
     two-step path runs instead): conv width 4, d_k in {32, 64, 128}, d_v a
-    multiple of 64, 16-bit io with unit-stride 16-byte-aligned rows, a
+    multiple of 64, 16-bit io with unit-stride 16-byte-aligned rows (row
+    stride below 2^24 elements), a
     16-byte-aligned conv pool whose slot and layer strides keep that
     alignment, and an fp32 or io-typed state pool."""
     return (config.state_len == 3 and config.head_k_dim in (32, 64, 128) and config.head_v_dim % 64 == 0
             and mixed_qkv.dtype in (torch.bfloat16, torch.float16) and mixed_qkv.stride(1) == 1
-            and mixed_qkv.stride(0) % 8 == 0 and _aligned16(mixed_qkv) and _aligned16(conv_state)
+            and mixed_qkv.stride(0) % 8 == 0 and 0 < mixed_qkv.stride(0) < (1 << 24)
+            and _aligned16(mixed_qkv) and _aligned16(conv_state)
             and conv_state.stride(0) % 8 == 0 and conv_state.stride(1) % 8 == 0
             and conv_state.dtype == mixed_qkv.dtype
             and recurrent_state.dtype in (torch.float32, mixed_qkv.dtype))

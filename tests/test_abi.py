@@ -44,7 +44,7 @@ def test_header_declares_expected_entry_points():
             "gdn_conv_decode", "gdn_store_state", "gdn_copy_rows", "gdn_zero_rows",
             "gdn_commit_accepted", "gdn_prefill_qk", "gdn_prefill_fused", "gdn_conv_snapshots",
             "gdn_rms_norm_gated", "gdn_metadata_copy", "gdn_metadata_pad", "gdn_prefill_fused_noalloc",
-            "gdn_prefill_noalloc_scratch_bytes"} <= names
+            "gdn_prefill_noalloc_scratch_bytes", "gdn_probe_rmw"} <= names
 
 
 def test_ctypes_table_matches_header():
