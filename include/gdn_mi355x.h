@@ -104,17 +104,30 @@ int gdn_prefill_frontend(const void* mixed, int64_t row_stride, int64_t col_stri
                          float* g_out, float* beta_out, void* stream);
 
 /*
- * Chunked gated delta rule over packed varlen sequences with state-pool I/O
- * (chunk size 64).  Replaces vendor/fla/gated_delta.py:15-82
+ * Chunked gated delta rule over packed varlen sequences with state-pool I/O.
+ * Replaces vendor/fla/gated_delta.py:15-82
  * (chunk_gated_delta_rule_to_cache -> cumsum, kkt/solve, wy, fwd_h, fwd_o
- * kernels) and kernel/linear_attention/state_io.py:15-28 (ChunkStateIO).
+ * kernels) and kernel/linear_attention/state_io.py:15-80 (ChunkStateIO,
+ * _chunk_state_pointer, _store_chunk_state_tile).
  *   q, k [T, H, dk], v [T, HV, dv] contiguous, io dtype (bf16 or f16);
  *   g, beta [T, HV] fp32 contiguous (prepared: natural-log decay, beta in [0,1]).
  *   state pool [slots, L, HV, dk, dv] (slot/layer/head strides, inner
  *   contiguous), state_dtype; read_slots[N] (<0: zero initial state);
- *   chunk_write_slots[NT] indexed by global 64-token chunk (<0: skip);
+ *   chunk_write_slots[NT] indexed by global checkpoint interval: one per
+ *   chunk_size (16, 32 or 64) tokens of each sequence, the last one of a
+ *   sequence possibly shorter (<0: skip);
  *   final_write_slots[N] or NULL.
  *   out [T, HV, dv] io dtype; v_new [T, HV, dv] or NULL (u - w h of the reference).
+ * Frame-table state (LogState payload frames, kernel/linear_attention/
+ * layout.py:11-26) when frames != NULL: state is the frame storage
+ * (num_frames frames of frame_bytes), the strides are ignored, and head h of
+ * layer `layer` in slot s starts at logical byte (layer HV + h) head_bytes of
+ * the slot; logical byte x lies in frame frames[s frames_per_slot + x /
+ * frame_bytes] at offset x % frame_bytes.  head_bytes >= dk dv elt, and either
+ * divides frame_bytes or is a multiple of it (then frame_bytes must be a
+ * multiple of 16 state rows, 16 dv elt).  A frame entry < 0 or >= num_frames reads as zero state
+ * and takes no write.  Granularities below 64 and frame tables need
+ * dv % 64 == 0.
  */
 int gdn_chunk_gated_delta_rule(const void* q, const void* k, const void* v, int io_dtype, const float* g,
                                const float* beta, const void* cu_seqlens, int cu_dtype, int64_t num_seqs,
@@ -122,8 +135,10 @@ int gdn_chunk_gated_delta_rule(const void* q, const void* k, const void* v, int 
                                void* state, int state_dtype, int64_t slot_stride, int64_t layer_stride,
                                int64_t head_stride, int64_t layer, const void* read_slots, int read_dtype,
                                const void* chunk_write_slots, int chunk_write_dtype,
-                               const void* final_write_slots, int final_write_dtype, void* out,
-                               void* v_new, float scale, void* stream);
+                               const void* final_write_slots, int final_write_dtype, int64_t chunk_size,
+                               const void* frames, int frames_dtype, int64_t frames_per_slot, int64_t frame_bytes,
+                               int64_t head_bytes, int64_t num_frames, void* out, void* v_new, float scale,
+                               void* stream);
 
 /*
  * The GDN prefill of one layer (layers/linear_attention_backend/gdn.py:100-150:

@@ -754,16 +754,53 @@ int dispatch_types(const ChunkParams& p, int io, int st, int64_t groups, hipStre
 
 using namespace gdn;
 
+namespace gdn {
+
+int set_frame_layout(ChunkParams& p, int64_t dk, int state_dtype, const void* frames, int frames_dtype,
+                     int64_t frames_per_slot, int64_t frame_bytes, int64_t head_bytes, int64_t num_frames) {
+  const int64_t elt = state_dtype == GDN_F32 ? 4 : 2;
+  const int64_t state_bytes = dk * p.DV * elt;
+  GDN_REQUIRE(frames_per_slot > 0 && frame_bytes > 0 && num_frames > 0 && head_bytes >= state_bytes &&
+                  frame_bytes % elt == 0 && head_bytes % elt == 0,
+              "gdn_chunk_gated_delta_rule: bad frame layout (frames_per_slot %lld, frame_bytes %lld, head_bytes "
+              "%lld, num_frames %lld, state %lld bytes per head)",
+              (long long)frames_per_slot, (long long)frame_bytes, (long long)head_bytes, (long long)num_frames,
+              (long long)state_bytes);
+  const bool inside = head_bytes <= frame_bytes;
+  GDN_REQUIRE(inside ? frame_bytes % head_bytes == 0
+                     : head_bytes % frame_bytes == 0 && frame_bytes % (16 * p.DV * elt) == 0,
+              "gdn_chunk_gated_delta_rule: head_bytes %lld must divide frame_bytes %lld, or be a multiple of it "
+              "with frames holding whole 16-row state tiles",
+              (long long)head_bytes, (long long)frame_bytes);
+  GDN_REQUIRE((p.layer + 1) * p.HV * head_bytes <= frames_per_slot * frame_bytes,
+              "gdn_chunk_gated_delta_rule: layer %lld of %lld heads x %lld bytes lies past the %lld frames of a slot",
+              (long long)p.layer, (long long)p.HV, (long long)head_bytes, (long long)frames_per_slot);
+  p.frames = frames;
+  p.frames_is64 = frames_dtype == GDN_I64;
+  p.frame_rows = inside ? 0 : 1;
+  p.fps = frames_per_slot;
+  p.frame_bytes = frame_bytes;
+  p.head_bytes = head_bytes;
+  p.num_frames = num_frames;
+  return GDN_OK;
+}
+
+}  // namespace gdn
+
 extern "C" int gdn_chunk_gated_delta_rule(const void* q, const void* k, const void* v, int io_dtype, const float* g,
                                           const float* beta, const void* cu_seqlens, int cu_dtype, int64_t num_seqs,
                                           int64_t total_tokens, int64_t H, int64_t HV, int64_t dk, int64_t dv,
                                           void* state, int state_dtype, int64_t slot_stride, int64_t layer_stride,
                                           int64_t head_stride, int64_t layer, const void* read_slots, int read_dtype,
                                           const void* chunk_write_slots, int chunk_write_dtype,
-                                          const void* final_write_slots, int final_write_dtype, void* out,
+                                          const void* final_write_slots, int final_write_dtype, int64_t chunk_size,
+                                          const void* frames, int frames_dtype, int64_t frames_per_slot,
+                                          int64_t frame_bytes, int64_t head_bytes, int64_t num_frames, void* out,
                                           void* v_new, float scale, void* stream) {
-  GDN_REQUIRE(num_seqs >= 0 && total_tokens >= 0 && H > 0 && HV > 0 && HV % H == 0,
+  GDN_REQUIRE(num_seqs >= 0 && total_tokens >= 0 && H > 0 && HV > 0 && HV % H == 0 && layer >= 0,
               "gdn_chunk_gated_delta_rule: bad sizes");
+  GDN_REQUIRE(chunk_size == 16 || chunk_size == 32 || chunk_size == 64,
+              "gdn_chunk_gated_delta_rule: chunk_size %lld not in {16, 32, 64}", (long long)chunk_size);
   if (num_seqs == 0) return GDN_OK;
   GDN_REQUIRE(q && k && v && g && beta && cu_seqlens && state && read_slots && chunk_write_slots && out,
               "gdn_chunk_gated_delta_rule: null input");
@@ -777,6 +814,12 @@ extern "C" int gdn_chunk_gated_delta_rule(const void* q, const void* k, const vo
   p.cw_slots = chunk_write_slots; p.cw_is64 = chunk_write_dtype == GDN_I64;
   p.fw_slots = final_write_slots; p.fw_is64 = final_write_dtype == GDN_I64;
   p.out = out; p.v_new = v_new; p.scale = scale;
+  p.gran = static_cast<int>(chunk_size);
+  if (frames) {
+    const int rc = set_frame_layout(p, dk, state_dtype, frames, frames_dtype, frames_per_slot, frame_bytes, head_bytes,
+                                    num_frames);
+    if (rc != GDN_OK) return rc;
+  }
   auto s = static_cast<hipStream_t>(stream);
   const int64_t groups = num_seqs * H;
   const int64_t r = HV / H;
@@ -788,6 +831,10 @@ extern "C" int gdn_chunk_gated_delta_rule(const void* q, const void* k, const vo
     const int rc = launch_chunk_chain(p, dk, io_dtype, state_dtype, groups, s);
     if (rc != GDN_ERR_UNSUPPORTED) return rc;
   } else if (dv == 32) {
+    if (chunk_size != 64 || frames) {
+      set_error("gdn_chunk_gated_delta_rule: dv = 32 takes chunk_size 64 and a plain state pool only");
+      return GDN_ERR_UNSUPPORTED;
+    }
     p.nvs = 1;
     p.members = static_cast<int>(r);
     if (dk == 128) return dispatch_types<128, 32>(p, io_dtype, state_dtype, groups, s);

@@ -208,7 +208,9 @@ __device__ __forceinline__ Tri tri_mul_add(const Tri& P, const Tri& Y) {
   return Z;
 }
 
-template <int DK, class IOT, class ST, bool FUSED>
+// EXT: checkpoint granularities below 64 and frame-table states (a separate
+// instantiation, so that the plain path carries none of their registers).
+template <int DK, class IOT, class ST, bool FUSED, bool EXT>
 __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p) {
   constexpr int HT = DK / 16;    // 16-row state tiles
   constexpr int KS = DK / 32;    // 32-deep k steps over d_k
@@ -250,6 +252,8 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
   ST* pool = static_cast<ST*>(p.state);
   const int64_t head_off = p.layer * p.layer_stride + h * p.head_stride + col_base;
   const int j = wave;  // chain wave: state columns 16j..16j+15
+  constexpr int64_t kRowBytes = sizeof(ST);
+  const int64_t row_bytes = p.DV * kRowBytes;
   f4_t hT[HT];
   // State slice rows 16 ti + 4 lg + e, column 16 j + lr: a wave-uniform base
   // plus a 32-bit lane offset (kept opaque so the per-element offsets are not
@@ -259,24 +263,59 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     asm volatile("" : "+v"(o));
     return o;
   };
-  auto load_state = [&]() {
-    const int64_t rs = uniform_index(p.read_slots, n, p.read_is64);
-    const char* src = rs >= 0 ? reinterpret_cast<const char*>(pool + rs * p.slot_stride + head_off) : nullptr;
-    const uint32_t o = state_lane_off();
-#pragma unroll
-    for (int ti = 0; ti < HT; ++ti)
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        hT[ti][e] = src ? load_st(reinterpret_cast<const ST*>(src + (16 * ti + e) * p.DV * sizeof(ST) + o)) : 0.f;
+  // Byte address of element (0, col_base) of the slice in slot s, or null for
+  // a negative slot or an unmapped frame (entry < 0 or past the storage).
+  // Rows follow every row_bytes (plain pools and heads inside one frame).
+  auto slice_base = [&](int64_t s) __attribute__((always_inline)) -> char* {
+    if (s < 0) return nullptr;
+    if (!EXT || !p.frames) return reinterpret_cast<char*>(pool + s * p.slot_stride + head_off);
+    const int64_t logical = (p.layer * p.HV + h) * p.head_bytes;
+    const int64_t fr = uniform_index(p.frames, s * p.fps + logical / p.frame_bytes, p.frames_is64);
+    if (fr < 0 || fr >= p.num_frames) return nullptr;
+    return static_cast<char*>(p.state) + fr * p.frame_bytes + logical % p.frame_bytes + col_base * kRowBytes;
   };
-  auto store_state = [&](int64_t slot_idx) {
-    char* dst = reinterpret_cast<char*>(pool + slot_idx * p.slot_stride + head_off);
+  // Heads spanning several frames (each frame holds whole 16-row tiles):
+  // byte address of element (16 ti, col_base) of slot s, or null.
+  auto frame_tile = [&](int64_t s, int ti) __attribute__((always_inline)) -> char* {
+    const int64_t logical = (p.layer * p.HV + h) * p.head_bytes + 16 * ti * row_bytes;
+    const int64_t fr = uniform_index(p.frames, s * p.fps + logical / p.frame_bytes, p.frames_is64);
+    if (fr < 0 || fr >= p.num_frames) return nullptr;
+    return static_cast<char*>(p.state) + fr * p.frame_bytes + logical % p.frame_bytes + col_base * kRowBytes;
+  };
+  // Row 16 ti of the slice in slot s (slice = slice_base(s)), or null.
+  auto tile_at = [&](char* slice, int64_t s, int ti) __attribute__((always_inline)) -> char* {
+    if (EXT && p.frame_rows) return s >= 0 ? frame_tile(s, ti) : nullptr;
+    return slice ? slice + 16 * ti * row_bytes : nullptr;
+  };
+  auto load_state = [&]() __attribute__((always_inline)) {
+    const int64_t rs = uniform_index(p.read_slots, n, p.read_is64);
+    char* src = EXT && p.frame_rows ? nullptr : slice_base(rs);
     const uint32_t o = state_lane_off();
 #pragma unroll
-    for (int ti = 0; ti < HT; ++ti)
+    for (int ti = 0; ti < HT; ++ti) {
+      const char* tile = tile_at(src, rs, ti);
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        store_st(reinterpret_cast<ST*>(dst + (16 * ti + e) * p.DV * sizeof(ST) + o), hT[ti][e]);
+        hT[ti][e] = tile ? load_st(reinterpret_cast<const ST*>(tile + e * row_bytes + o)) : 0.f;
+    }
+  };
+  // Stores tile(ti) (rows 16 ti.., this wave's columns) for every ti to slot s >= 0.
+  auto store_tiles = [&](int64_t s, auto&& tile) __attribute__((always_inline)) {
+    char* dst = EXT && p.frame_rows ? nullptr : slice_base(s);
+    if (!(EXT && p.frame_rows) && !dst) return;
+    const uint32_t o = state_lane_off();
+#pragma unroll
+    for (int ti = 0; ti < HT; ++ti) {
+      const f4_t v = tile(ti);
+      char* t = tile_at(dst, s, ti);
+      if (t) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) store_st(reinterpret_cast<ST*>(t + e * row_bytes + o), v[e]);
+      }
+    }
+  };
+  auto store_state = [&](int64_t s) __attribute__((always_inline)) {
+    store_tiles(s, [&](int ti) __attribute__((always_inline)) { return hT[ti]; });
   };
 
   if (nchunks == 0) {  // empty sequence: the final state is the initial state
@@ -289,10 +328,12 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     }
     return;
   }
+  // checkpoint slots before this sequence: one per `gran` tokens of each earlier sequence
+  const int gran = EXT ? p.gran : kC;
   int64_t chunk_base = 0;
   for (int64_t m = 0; m < n; ++m) {
     const int64_t lm = uniform_index(p.cu, m + 1, p.cu_is64) - uniform_index(p.cu, m, p.cu_is64);
-    chunk_base += (lm + kC - 1) / kC;
+    chunk_base += (lm + gran - 1) / gran;
   }
 
   // A and M start zero: their upper blocks are never written.
@@ -316,7 +357,9 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     lds_barrier();  // B(0)
     for (int64_t c = 0; c < nchunks; ++c) {
       const int nv = valid_rows(c);
-      const int64_t cw = uniform_index(p.cw_slots, chunk_base + c, p.cw_is64);  // checkpoint slot
+      const int nsub = (nv + gran - 1) / gran;  // checkpoint intervals in this chunk
+      const int64_t sub0 = chunk_base + c * (kC / gran);
+      const int64_t cw = uniform_index(p.cw_slots, sub0 + nsub - 1, p.cw_is64);  // checkpoint slot
       const _Float16* K = sK + (c % 3) * kC * LDK;
       const _Float16* Q = sQ + (c & 1) * kC * LDQ;
       const float* gt = sG + (c % 3) * GTS;
@@ -418,6 +461,29 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
           for (int e = 0; e < 4; ++e)
             if (16 * i + 4 * lg + e < nv)
               *reinterpret_cast<uint16_t*>(vb + (16 * i + e) * tok_stride * 2 + ov) = out_bits<IOT>(V[i][e]);
+      }
+      // ---- checkpoints inside the chunk (granularity 16 or 32): the state after
+      // token te = (s + 1) gran - 1 is 2^G_te h + K^T (2^(G_te - G) v'), the
+      // decay taken over tokens t <= te only.
+      for (int sc = 0; EXT && sc + 1 < nsub; ++sc) {
+        const int64_t ws = uniform_index(p.cw_slots, sub0 + sc, p.cw_is64);
+        if (ws < 0) continue;
+        const int te = (sc + 1) * gran - 1;
+        const float Ge = gt[te], ge = gt[G_EXP + te];
+        f4_t dm[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const f4_t g4 = *reinterpret_cast<const f4_t*>(gt + 16 * i + 4 * lg);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            dm[i][e] = 16 * i + 4 * lg + e <= te ? V[i][e] * fast_exp2(Ge - g4[e]) : 0.f;
+        }
+        const h8_t m0 = bfrag(dm[0], dm[1]), m1 = bfrag(dm[2], dm[3]);
+        store_tiles(ws, [&](int ti) __attribute__((always_inline)) {
+          f4_t r = mma(kq_tfrag(K, LDK, 0, 16 * ti, lr, lg), m0, hT[ti] * ge);
+          if (te >= 32) r = mma(kq_tfrag(K, LDK, 32, 16 * ti, lr, lg), m1, r);
+          return r;
+        });
       }
       // ---- S3b: h <- 2^G_last h + K^T (2^(G_last - G) v')
       {
@@ -923,8 +989,14 @@ int launch_typed(const ChunkParams& p, int64_t groups, hipStream_t stream) {
     set_error("gdn_chunk_gated_delta_rule: grid too large");
     return GDN_ERR_INVALID;
   }
-  hipLaunchKernelGGL((chunk_chain_kernel<DK, IOT, ST, FUSED>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads),
-                     0, stream, p);
+  const dim3 grid(static_cast<unsigned>(blocks));
+  if constexpr (FUSED) {  // the fused prefill takes 64-token checkpoints into a plain pool
+    hipLaunchKernelGGL((chunk_chain_kernel<DK, IOT, ST, true, false>), grid, dim3(kThreads), 0, stream, p);
+  } else if (p.gran < kC || p.frames) {
+    hipLaunchKernelGGL((chunk_chain_kernel<DK, IOT, ST, false, true>), grid, dim3(kThreads), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((chunk_chain_kernel<DK, IOT, ST, false, false>), grid, dim3(kThreads), 0, stream, p);
+  }
   return GDN_LAUNCH_CHECK("gdn_chunk_gated_delta_rule launch");
 }
 
@@ -995,6 +1067,7 @@ extern "C" int gdn_prefill_fused(const void* q, const void* k, const void* mixed
   p.cw_slots = chunk_write_slots; p.cw_is64 = chunk_write_dtype == GDN_I64;
   p.fw_slots = final_write_slots; p.fw_is64 = final_write_dtype == GDN_I64;
   p.out = out; p.v_new = nullptr; p.scale = scale;
+  p.gran = kC;
   p.nvs = static_cast<int>(dv / 64);
   p.members = static_cast<int>((HV / H) * p.nvs);
   FrontIn& f = p.front;

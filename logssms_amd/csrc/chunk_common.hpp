@@ -40,7 +40,26 @@ struct ChunkParams {
   int nvs;      // 64-column v slices per head
   int members;  // workgroups per (sequence, key head)
   FrontIn front;
+  // Checkpoint granularity: cw_slots holds one slot per `gran` tokens of each
+  // sequence (16, 32 or 64; the kernels work in 64-token chunks throughout).
+  int gran;
+  // Frame-table state addressing (LogState payload frames,
+  // kernel/linear_attention/layout.py:11-26) when `frames` is set: `state` is
+  // the frame storage, head (layer, h) of slot s starts at logical byte
+  // (layer HV + h) head_bytes of the slot, and logical byte x of slot s lies in
+  // frame frames[s fps + x / frame_bytes] at offset x % frame_bytes.  With
+  // head_bytes <= frame_bytes a head sits inside one frame; otherwise each
+  // 16-row tile of it is looked up on its own (frame_rows).
+  const void* frames;
+  int frames_is64;
+  int frame_rows;
+  int64_t fps, frame_bytes, head_bytes, num_frames;
 };
+
+// Host-side validation of a frame-table state layout; returns GDN_OK or sets
+// the error and returns GDN_ERR_INVALID.  Fills the frame fields of p.
+int set_frame_layout(ChunkParams& p, int64_t dk, int state_dtype, const void* frames, int frames_dtype,
+                     int64_t frames_per_slot, int64_t frame_bytes, int64_t head_bytes, int64_t num_frames);
 
 // Register-chain kernel (chunk_chain.hip) for d_k in {32, 64, 128} and d_v a
 // multiple of 64.  Returns GDN_ERR_UNSUPPORTED (without setting an error) for

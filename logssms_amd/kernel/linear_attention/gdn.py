@@ -40,32 +40,52 @@ def chunk_gated_delta_rule_to_cache(
 ) -> tuple[torch.Tensor, torch.Tensor | None]:
     """Chunked gated delta rule over packed sequences with pool I/O
     (``gated_delta.py:15-82``): initial state of sequence n from
-    ``storage[read_slots[n], layer]`` (zero if negative), chunk-end states to
-    ``storage[chunk_write_slots[c], layer]`` for every 64-token chunk ``c``
-    with a non-negative slot, optional final states to ``final_write_slots``.
-    ``gate`` is the natural-log decay and ``beta`` the prepared write strength
+    ``storage[read_slots[n], layer]`` (zero if negative), checkpoint states to
+    ``storage[chunk_write_slots[c], layer]`` for every ``chunk_size``-token
+    interval ``c`` (global numbering, the last interval of a sequence possibly
+    shorter) with a non-negative slot, optional final states to
+    ``final_write_slots``.  With ``state_io.payload_frames`` the same states
+    live in the LogState frame storage (``state_io.py:42-80``).  ``gate`` is
+    the natural-log decay and ``beta`` the prepared write strength
     (``prepare_gdn`` outputs).  Returns ``(o, v_new)``; ``v_new`` is
     ``u - w h`` (None when ``return_v_new=False``).
 
-    ``chunk_indices``/``chunk_offsets`` are accepted for signature
-    compatibility (the kernel derives chunk boundaries from ``cu_seqlens``).
+    The kernel always solves 64-token chunks; ``chunk_size`` 16 or 32 sets
+    where checkpoints are taken (the results do not depend on it beyond
+    rounding).  ``chunk_indices``/``chunk_offsets`` are accepted for signature
+    compatibility (the kernel derives interval boundaries from
+    ``cu_seqlens``); ``log_io`` (the LogState token log) is not supported.
     """
     del chunk_offsets
     assert query.shape[0] == key.shape[0] == value.shape[0] == 1
     assert chunk_size in (16, 32, 64)
     assert cu_seqlens.ndim == 1
     assert len(cu_seqlens) == len(state_io.read_slots) + 1
-    if chunk_size != 64:
-        raise NotImplementedError("the MI355X chunk kernel is specialised for chunk_size=64")
-    if log_io is not None or state_io.payload_frames is not None:
-        raise NotImplementedError("LogState state I/O is not supported by the MI355X backend")
+    if log_io is not None:
+        raise NotImplementedError("the LogState token log (ChunkLogIO) is not supported by the MI355X backend")
     _, T, H, dk = query.shape
     HV, dv = value.shape[2:]
     assert key.shape == query.shape and value.shape[:2] == query.shape[:2]
     assert HV % H == 0
     assert gate.shape == beta.shape == (1, T, HV)
     storage = state_io.storage
-    _check_state_storage(storage, HV, dk, dv)
+    frames = state_io.payload_frames
+    if frames is None:
+        _check_state_storage(storage, HV, dk, dv)
+        strides = (storage.stride(0), storage.stride(1), storage.stride(2))
+        frame_args = (None, 0, 0, 0, 0, 0)
+    else:
+        assert storage.ndim == 2 and storage.is_contiguous()
+        assert state_io.frame_bytes > 0 and state_io.head_payload_bytes > 0
+        assert storage.shape[1] * storage.element_size() == state_io.frame_bytes
+        assert frames.ndim == 2 and frames.is_contiguous() and frames.device == storage.device
+        if dv % 64:
+            raise NotImplementedError("frame-table states need head_v_dim % 64 == 0 on the MI355X backend")
+        strides = (0, 0, 0)
+        frame_args = (frames, _lib.index_code(frames), frames.shape[1], state_io.frame_bytes,
+                      state_io.head_payload_bytes, storage.shape[0])
+    if chunk_size != 64 and dv % 64:
+        raise NotImplementedError("chunk_size 16/32 needs head_v_dim % 64 == 0 on the MI355X backend")
     assert storage.device == query.device
     if chunk_indices is not None:
         assert state_io.chunk_write_slots.shape == (len(chunk_indices),)
@@ -84,11 +104,11 @@ def chunk_gated_delta_rule_to_cache(
             query.data_ptr(), key.data_ptr(), value.data_ptr(), _lib.dtype_code(value.dtype),
             gate.data_ptr(), beta.data_ptr(), cu_seqlens.data_ptr(), _lib.index_code(cu_seqlens),
             len(cu_seqlens) - 1, T, H, HV, dk, dv,
-            storage.data_ptr(), _lib.dtype_code(storage.dtype), storage.stride(0), storage.stride(1),
-            storage.stride(2), state_io.layer,
+            storage.data_ptr(), _lib.dtype_code(storage.dtype), *strides, state_io.layer,
             state_io.read_slots.data_ptr(), _lib.index_code(state_io.read_slots),
             state_io.chunk_write_slots.data_ptr(), _lib.index_code(state_io.chunk_write_slots),
-            _lib.ptr(fw), _lib.index_code(fw) if fw is not None else 0,
+            _lib.ptr(fw), _lib.index_code(fw) if fw is not None else 0, chunk_size,
+            _lib.ptr(frame_args[0]), *frame_args[1:],
             o.data_ptr(), _lib.ptr(v_new), float(dk) ** -0.5, _lib.stream_of(query),
         )
     return o, v_new

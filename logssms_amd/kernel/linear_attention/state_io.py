@@ -11,9 +11,13 @@ import torch
 @dataclass(frozen=True)
 class ChunkStateIO:
     """state_io.py:15-28.  ``storage`` is ``[slots, layers, HV, dk, dv]``
-    (any slot/layer/head strides, inner dims contiguous).  ``payload_frames``
-    and the frame/log fields describe the LogState layout and are rejected
-    with ``NotImplementedError`` when set."""
+    (any slot/layer/head strides, inner dims contiguous), or, with
+    ``payload_frames`` set (the LogState layout), the frame storage
+    ``[num_frames, frame_bytes / itemsize]`` in the state dtype: head h of
+    layer ``layer`` in slot s starts at logical byte ``(layer HV + h)
+    head_payload_bytes`` of the slot, and logical byte x lies in frame
+    ``payload_frames[s, x // frame_bytes]`` at offset ``x % frame_bytes``
+    (``layout.py:11-26``)."""
 
     storage: torch.Tensor
     read_slots: torch.Tensor

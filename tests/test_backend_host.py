@@ -315,3 +315,28 @@ def test_marconi_copy_blocks_rejects_aliasing():
     with pytest.raises(ValueError):
         pool.copy_blocks([1], [2, 4])
     pool.copy_blocks([], [])
+
+
+def test_chunk_entry_rejects_what_it_does_not_cover():
+    """The LogState token log and frame tables / granularities below 64 with
+    head_v_dim 32 raise NotImplementedError before anything is launched."""
+    from logssms_amd.kernel.linear_attention import ChunkLogIO, ChunkStateIO, chunk_gated_delta_rule_to_cache
+    T, H, dk, dv = 4, 1, 32, 32
+    q = torch.zeros(1, T, H, dk, dtype=torch.bfloat16)
+    v = torch.zeros(1, T, H, dv, dtype=torch.bfloat16)
+    g = torch.zeros(1, T, H)
+    cu = torch.tensor([0, T])
+    slots = torch.tensor([-1])
+    pool = torch.zeros(1, 1, H, dk, dv)
+    io = ChunkStateIO(pool, slots, torch.tensor([-1]))
+    log = ChunkLogIO(slots, torch.zeros(T, dtype=torch.int64), torch.zeros(1, 2, dtype=torch.int32), g, 64, 4, H)
+    with pytest.raises(NotImplementedError):
+        chunk_gated_delta_rule_to_cache(q, q, v, g, g, io, cu, log_io=log)
+    with pytest.raises(NotImplementedError):
+        chunk_gated_delta_rule_to_cache(q, q, v, g, g, ChunkStateIO(pool, slots, torch.tensor([-1])), cu,
+                                        chunk_size=32)
+    frames = ChunkStateIO(torch.zeros(4, 1024, dtype=torch.bfloat16), slots, torch.tensor([-1]),
+                          payload_frames=torch.zeros(1, 1, dtype=torch.int32), frame_bytes=2048,
+                          head_payload_bytes=2048)
+    with pytest.raises(NotImplementedError):
+        chunk_gated_delta_rule_to_cache(q, q, v, g, g, frames, cu)

@@ -1,0 +1,119 @@
+"""Pins the LogState frame-table addressing of the oracle (``oracle/frames.py``).
+
+With the identity table (slot s owns frames s fps .. s fps + fps - 1) the frame
+storage is one contiguous pool, so every read must equal a plain reshape of
+the storage; relabelling frames must not change what a slot reads; the chunk
+pipeline on frames must equal the plain-pool pipeline bit for bit.  An index
+slip (frame vs element units, a head offset off by one, the wrong table
+column) fails one of these.
+"""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import frames as fr
+from oracle import gdn
+
+# (dk, dv, frame_bytes, head_bytes): heads inside a frame, heads spanning two
+# frames, a padded head (48 state bytes in a 64-byte payload)
+LAYOUTS = [(8, 4, 128, 64), (8, 4, 32, 64), (6, 4, 128, 64), (4, 4, 64, 32)]
+
+
+def _identity(slots, fps):
+    return (torch.arange(slots)[:, None] * fps + torch.arange(fps)[None, :]).to(torch.int32)
+
+
+def _setup(dk, dv, frame_bytes, head_bytes, layers=2, HV=3, slots=4, dtype=torch.bfloat16, seed=0):
+    itemsize = torch.tensor([], dtype=dtype).element_size()
+    fps = -(-layers * HV * head_bytes // frame_bytes)
+    g = torch.Generator().manual_seed(seed)
+    storage = torch.randn(slots * fps, frame_bytes // itemsize, generator=g).to(dtype)
+    return storage, _identity(slots, fps), fps, itemsize
+
+
+def _as_pool(storage, slots, layers, HV, dk, dv, head_bytes, itemsize):
+    """The identity-table storage read as a plain [slots, layers, HV, dk, dv] pool."""
+    head = head_bytes // itemsize
+    per_slot = storage.reshape(slots, -1)[:, :layers * HV * head]
+    return per_slot.reshape(slots, layers, HV, head)[..., :dk * dv].reshape(slots, layers, HV, dk, dv)
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_identity_table_reads_a_contiguous_pool(layout):
+    dk, dv, frame_bytes, head_bytes = layout
+    storage, frames, _, itemsize = _setup(dk, dv, frame_bytes, head_bytes)
+    pool = _as_pool(storage, 4, 2, 3, dk, dv, head_bytes, itemsize)
+    for layer in range(2):
+        got = fr.read_frame_states(storage, frames, [3, 0, 2], layer, 3, dk, dv, frame_bytes, head_bytes)
+        torch.testing.assert_close(got, pool[[3, 0, 2], layer], rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_relabelled_frames_read_and_write_the_same(layout):
+    dk, dv, frame_bytes, head_bytes = layout
+    storage, frames, _, _ = _setup(dk, dv, frame_bytes, head_bytes, seed=1)
+    perm = torch.randperm(storage.shape[0], generator=torch.Generator().manual_seed(2))
+    moved = torch.empty_like(storage)
+    moved[perm] = storage
+    table = perm[frames.long()].to(torch.int32)
+    for layer in range(2):
+        a = fr.read_frame_states(storage, frames, [0, 1, 2, 3], layer, 3, dk, dv, frame_bytes, head_bytes)
+        b = fr.read_frame_states(moved, table, [0, 1, 2, 3], layer, 3, dk, dv, frame_bytes, head_bytes)
+        torch.testing.assert_close(a, b, rtol=0, atol=0)
+    values = torch.randn(2, 3, dk, dv, generator=torch.Generator().manual_seed(3)).to(storage.dtype)
+    fr.write_frame_states(storage, frames, [2, 1], 1, values, frame_bytes, head_bytes)
+    fr.write_frame_states(moved, table, [2, 1], 1, values, frame_bytes, head_bytes)
+    torch.testing.assert_close(moved[perm], storage, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_write_touches_only_the_named_states(layout):
+    dk, dv, frame_bytes, head_bytes = layout
+    storage, frames, _, itemsize = _setup(dk, dv, frame_bytes, head_bytes, seed=4)
+    before = storage.clone()
+    values = torch.randn(3, 3, dk, dv, generator=torch.Generator().manual_seed(5)).to(storage.dtype)
+    fr.write_frame_states(storage, frames, [2, -1, 0], 1, values, frame_bytes, head_bytes)
+    got = fr.read_frame_states(storage, frames, [2, 0], 1, 3, dk, dv, frame_bytes, head_bytes)
+    torch.testing.assert_close(got, values[[0, 2]], rtol=0, atol=0)
+    expected = _as_pool(before.clone(), 4, 2, 3, dk, dv, head_bytes, itemsize)
+    expected[[2, 0], 1] = values[[0, 2]]
+    torch.testing.assert_close(_as_pool(storage, 4, 2, 3, dk, dv, head_bytes, itemsize), expected, rtol=0, atol=0)
+    # padding bytes of the payload and the unused tail of the last frame stay as they were
+    mask = torch.ones(storage.numel(), dtype=torch.bool)
+    mask[fr.frame_state_index(frames, [2, 0], 1, 3, dk, dv, itemsize, frame_bytes, head_bytes).reshape(-1)] = False
+    assert torch.equal(storage.reshape(-1)[mask], before.reshape(-1)[mask])
+
+
+@pytest.mark.parametrize("chunk_size", [16, 32])
+def test_chunk_on_frames_equals_the_plain_pool(chunk_size):
+    dk = dv = 8
+    H, HV, layers, slots = 1, 2, 2, 6
+    head_bytes = dk * dv * 2
+    frame_bytes = 2 * head_bytes
+    storage, frames, _, itemsize = _setup(dk, dv, frame_bytes, head_bytes, layers=layers, HV=HV, slots=slots, seed=6)
+    storage.mul_(0.1)
+    g = torch.Generator().manual_seed(7)
+    lengths = [40, 17]
+    cu = [0, 40, 57]
+    T = cu[-1]
+    q = F.normalize(torch.randn(1, T, H, dk, generator=g), dim=-1)
+    k = F.normalize(torch.randn(1, T, H, dk, generator=g), dim=-1)
+    v = torch.randn(1, T, HV, dv, generator=g)
+    gate = -torch.rand(1, T, HV, generator=g) * 0.2
+    beta = torch.sigmoid(torch.randn(1, T, HV, generator=g))
+    n_int = sum(-(-n // chunk_size) for n in lengths)
+    reads = torch.tensor([0, -1])
+    writes = torch.full((n_int,), -1)
+    writes[0], writes[-1] = 2, 3
+    finals = torch.tensor([4, 5])
+    pool = _as_pool(storage.clone(), slots, layers, HV, dk, dv, head_bytes, itemsize).contiguous()
+    o_a, vn_a = gdn.chunk_gated_delta_rule_to_cache(q, k, v, gate, beta, pool, reads, writes, cu, layer=1,
+                                                    final_write_slots=finals, chunk_size=chunk_size)
+    o_b, vn_b = fr.chunk_gated_delta_rule_to_frames(q, k, v, gate, beta, storage, frames, frame_bytes, head_bytes,
+                                                    reads, writes, cu, layer=1, final_write_slots=finals,
+                                                    chunk_size=chunk_size)
+    torch.testing.assert_close(o_b, o_a, rtol=0, atol=0)
+    torch.testing.assert_close(vn_b, vn_a, rtol=0, atol=0)
+    torch.testing.assert_close(_as_pool(storage, slots, layers, HV, dk, dv, head_bytes, itemsize), pool,
+                               rtol=0, atol=0)
