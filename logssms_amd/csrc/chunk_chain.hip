@@ -116,12 +116,17 @@ __device__ __forceinline__ h4_t tr_read(const _Float16* p) {
 }
 // Left operand of K^T for a token-major, swizzled K tile: rows of K^T =
 // columns c0 + lane % 16 of K (c0 a multiple of 16), k block = tokens
-// t0..t0+31 (t0 a multiple of 32) in the k order above; the row phase
-// (r / 4) mod 4 is the same for rows r and r + 16.
-__device__ __forceinline__ h8_t kq_tfrag(const _Float16* X, int ld, int t0, int c0, int lr, int lg) {
-  const int r = t0 + 4 * lg + (lr >> 2);
-  const _Float16* p = X + r * ld + c0 + 4 * ((lr & 3) ^ ((r >> 2) & 3));
-  return cat(tr_read(p), tr_read(p + 16 * ld));
+// t0..t0+31 (t0 a multiple of 32) in the k order above.  Lane (lr, lg) reads
+// rows r = t0 + 4 lg + lr / 4 and r + 16, whose row phase (r / 4) mod 4 is lg
+// for every t0 in {0, 32}: the lane part of the address is the byte offset
+// lane_tr_offset(...) from the tile, computed once, and the rest a constant.
+__device__ __forceinline__ uint32_t lane_tr_offset(int ld, int lr, int lg) {
+  return static_cast<uint32_t>(((4 * lg + (lr >> 2)) * ld + 4 * ((lr & 3) ^ lg)) * 2);
+}
+template <int LD>
+__device__ __forceinline__ h8_t kq_tfrag(const char* lane_tile, int t0, int c0) {
+  const char* p = lane_tile + (t0 * LD + c0) * 2;
+  return cat(tr_read(reinterpret_cast<const _Float16*>(p)), tr_read(reinterpret_cast<const _Float16*>(p + 16 * LD * 2)));
 }
 // Right operand from two C-layout accumulator tiles (rows 0-15, rows 16-31).
 __device__ __forceinline__ h8_t bfrag(f4_t a, f4_t b) {
@@ -347,6 +352,8 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     uint16_t* og = static_cast<uint16_t*>(p.out) + (bos * p.HV + h) * p.DV + col_base + 16 * j;
     uint16_t* vng = p.v_new ? static_cast<uint16_t*>(p.v_new) + (bos * p.HV + h) * p.DV + col_base + 16 * j : nullptr;
     const int64_t tok_stride = p.HV * p.DV;
+    uint32_t ktr = lane_tr_offset(LDK, lr, lg);
+    asm volatile("" : "+v"(ktr));
     load_state();
     // No vector-memory load may be outstanding at the loop head (a wait there
     // would also wait for the previous chunk's output stores): consume the
@@ -364,21 +371,26 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       const _Float16* Q = sQ + (c & 1) * kC * LDQ;
       const float* gt = sG + (c % 3) * GTS;
       // ---- S1: P = K h -> R = beta (v - 2^G P);  O^T = h^T Q^T (token columns).
-      // The 4 fragments of a 32-deep k step are read together; the converted
-      // state is the right operand of K h and the left operand of h^T Q^T.
+      // Per 32-deep k step the K and Q fragments are read together and the
+      // converted state is both the right operand of K h and the left operand
+      // of h^T Q^T: eight independent accumulations in flight.
       f4_t R[4], Ot[4];
       {
         f4_t P[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) P[i] = zero4();
+        for (int i = 0; i < 4; ++i) P[i] = Ot[i] = zero4();
 #pragma unroll
         for (int m = 0; m < KS; ++m) {
-          h8_t kf[4];
+          h8_t kf[4], qf[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) kf[i] = kqfrag(K, LDK, 16 * i + lr, 32 * m, lg);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) qf[i] = kqfrag(Q, LDQ, 16 * i + lr, 32 * m, lg);
           const h8_t hb = bfrag(hT[2 * m], hT[2 * m + 1]);
 #pragma unroll
           for (int i = 0; i < 4; ++i) P[i] = mma(kf[i], hb, P[i]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) Ot[i] = mma(hb, qf[i], Ot[i]);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -390,17 +402,6 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
 #pragma unroll
           for (int e = 0; e < 4; ++e) R[i][e] = b4[e] * (static_cast<float>(v4[e]) - e4[e] * P[i][e]);
         }
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) Ot[i] = zero4();
-#pragma unroll
-      for (int m = 0; m < KS; ++m) {
-        h8_t qf[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) qf[i] = kqfrag(Q, LDQ, 16 * i + lr, 32 * m, lg);
-        const h8_t hb = bfrag(hT[2 * m], hT[2 * m + 1]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) Ot[i] = mma(hb, qf[i], Ot[i]);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) Ot[i] *= gt[G_EXP + 16 * i + lr];
@@ -480,8 +481,9 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         }
         const h8_t m0 = bfrag(dm[0], dm[1]), m1 = bfrag(dm[2], dm[3]);
         store_tiles(ws, [&](int ti) __attribute__((always_inline)) {
-          f4_t r = mma(kq_tfrag(K, LDK, 0, 16 * ti, lr, lg), m0, hT[ti] * ge);
-          if (te >= 32) r = mma(kq_tfrag(K, LDK, 32, 16 * ti, lr, lg), m1, r);
+          const char* kl = reinterpret_cast<const char*>(K) + ktr;
+          f4_t r = mma(kq_tfrag<LDK>(kl, 0, 16 * ti), m0, hT[ti] * ge);
+          if (te >= 32) r = mma(kq_tfrag<LDK>(kl, 32, 16 * ti), m1, r);
           return r;
         });
       }
@@ -496,8 +498,9 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         const float gl = gt[G_LAST];
 #pragma unroll
         for (int ti = 0; ti < HT; ++ti) {
-          const h8_t k0 = kq_tfrag(K, LDK, 0, 16 * ti, lr, lg);
-          const h8_t k1 = kq_tfrag(K, LDK, 32, 16 * ti, lr, lg);
+          const char* kl = reinterpret_cast<const char*>(K) + ktr;
+          const h8_t k0 = kq_tfrag<LDK>(kl, 0, 16 * ti);
+          const h8_t k1 = kq_tfrag<LDK>(kl, 32, 16 * ti);
           hT[ti] = mma(k1, db1, mma(k0, db0, hT[ti] * gl));
         }
       }
