@@ -141,6 +141,32 @@ int gdn_chunk_gated_delta_rule(const void* q, const void* k, const void* v, int 
                                void* stream);
 
 /*
+ * LogState token log of the chunked prefill: replaces the log stores of
+ * kernel/linear_attention/state_io.py:83-126 (_store_chunk_log, called from
+ * vendor/fla/chunk_delta_h.py:183-192 when a ChunkLogIO is given), with the
+ * log layout of kernel/linear_attention/layout.py:29-80 (log_pointer).
+ * For every token t with log_slots[t] >= 0 and 0 <= token_offsets[t] <
+ * page_size, and every value head h:
+ *   v_new[t, h, :] -> the value row (h, position) of the slot's log;
+ *   key[t, h / (HV / H), :] -> key row (h / (HV / key_heads), position) when
+ *     h % (HV / key_heads) == 0;
+ *   gate[t, h] (fp32) -> float (layer page_size + position) HV + h of the
+ *     decay record decay_frames[slot] = {frame, record}.
+ * The log of a slot holds, in 16-bit elements from logical byte 0, granule
+ * (position / granularity), layer, then keys [key_heads, granularity, dk]
+ * and values [HV, granularity, dv]; logical byte x lies in frame
+ * frames[slot frames_per_slot + x / frame_bytes] at offset x % frame_bytes
+ * (storage = num_frames frames).  Frame entries < 0 or >= num_frames take no
+ * write.  v_new and key [T, ., d] contiguous in the storage's 16-bit dtype.
+ */
+int gdn_store_chunk_log(void* storage, const void* frames, int frames_dtype, int64_t frames_per_slot,
+                        int64_t frame_bytes, int64_t num_frames, const void* log_slots, int slots_dtype,
+                        const void* token_offsets, int offsets_dtype, int64_t T, const void* v_new, const void* key,
+                        int64_t H, int64_t HV, int64_t dk, int64_t dv, int64_t key_heads, const float* gate,
+                        const void* decay_frames, int decay_dtype, int64_t decay_record_bytes, int64_t layer,
+                        int64_t num_layers, int64_t granularity, int64_t page_size, void* stream);
+
+/*
  * The GDN prefill of one layer (layers/linear_attention_backend/gdn.py:100-150:
  * history gather, packed_causal_conv1d, split, prepare_gdn,
  * chunk_gated_delta_rule_to_cache) as three launches whose results equal

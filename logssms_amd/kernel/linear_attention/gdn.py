@@ -54,15 +54,15 @@ def chunk_gated_delta_rule_to_cache(
     where checkpoints are taken (the results do not depend on it beyond
     rounding).  ``chunk_indices``/``chunk_offsets`` are accepted for signature
     compatibility (the kernel derives interval boundaries from
-    ``cu_seqlens``); ``log_io`` (the LogState token log) is not supported.
+    ``cu_seqlens``).  With ``log_io`` (frame storage only) every logged
+    token's v' rows, key rows and gates then go into its log slot
+    (``state_io.py:83-126``, ``gdn_store_chunk_log``).
     """
     del chunk_offsets
     assert query.shape[0] == key.shape[0] == value.shape[0] == 1
     assert chunk_size in (16, 32, 64)
     assert cu_seqlens.ndim == 1
     assert len(cu_seqlens) == len(state_io.read_slots) + 1
-    if log_io is not None:
-        raise NotImplementedError("the LogState token log (ChunkLogIO) is not supported by the MI355X backend")
     _, T, H, dk = query.shape
     HV, dv = value.shape[2:]
     assert key.shape == query.shape and value.shape[:2] == query.shape[:2]
@@ -86,6 +86,13 @@ def chunk_gated_delta_rule_to_cache(
                       state_io.head_payload_bytes, storage.shape[0])
     if chunk_size != 64 and dv % 64:
         raise NotImplementedError("chunk_size 16/32 needs head_v_dim % 64 == 0 on the MI355X backend")
+    if log_io is not None:
+        assert frames is not None, "the token log lives in the LogState frame storage"
+        assert log_io.slots.shape == log_io.token_offsets.shape == (T,)
+        assert log_io.gate.numel() == T * HV and log_io.num_key_heads > 0
+        assert H % log_io.num_key_heads == 0 and HV % log_io.num_key_heads == 0
+        assert storage.dtype == value.dtype, "log rows are stored in the io dtype"
+        return_v_new = True
     assert storage.device == query.device
     if chunk_indices is not None:
         assert state_io.chunk_write_slots.shape == (len(chunk_indices),)
@@ -111,6 +118,19 @@ def chunk_gated_delta_rule_to_cache(
             _lib.ptr(frame_args[0]), *frame_args[1:],
             o.data_ptr(), _lib.ptr(v_new), float(dk) ** -0.5, _lib.stream_of(query),
         )
+        if log_io is not None:
+            log_gate = log_io.gate.float().contiguous()
+            _lib.call(
+                "gdn_store_chunk_log",
+                storage.data_ptr(), frames.data_ptr(), _lib.index_code(frames), frames.shape[1],
+                state_io.frame_bytes, storage.shape[0],
+                log_io.slots.data_ptr(), _lib.index_code(log_io.slots),
+                log_io.token_offsets.data_ptr(), _lib.index_code(log_io.token_offsets), T,
+                v_new.data_ptr(), key.data_ptr(), H, HV, dk, dv, log_io.num_key_heads,
+                log_gate.data_ptr(), log_io.decay_frames.data_ptr(), _lib.index_code(log_io.decay_frames),
+                log_io.decay_record_bytes, state_io.layer, state_io.num_layers, state_io.granularity,
+                log_io.page_size, _lib.stream_of(query),
+            )
     return o, v_new
 
 

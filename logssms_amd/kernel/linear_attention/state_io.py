@@ -34,7 +34,11 @@ class ChunkStateIO:
 
 @dataclass(frozen=True)
 class ChunkLogIO:
-    """state_io.py:31-39 (LogState only; accepted for signature compatibility)."""
+    """state_io.py:31-39: the LogState token log.  ``slots`` / ``token_offsets``
+    [T] give each token's log slot (-1: none) and position in its page;
+    ``gate`` [1, T, HV] is the prepared (natural-log) gate; ``decay_frames``
+    [slots, 2] the {frame, record} of each slot's decay record of
+    ``decay_record_bytes``; ``num_key_heads`` the key heads the log keeps."""
 
     slots: torch.Tensor
     token_offsets: torch.Tensor

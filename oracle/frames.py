@@ -12,14 +12,20 @@ starts at logical byte ``(l HV + h) head_bytes`` of the slot; logical byte
 ``cache/logstate/frame_pool.py:181-199``).  ``head_bytes`` is the state size
 or its power-of-two padding (``cache/logstate/layout.py:64-71``).
 
-Pinning (``tests/test_oracle.py``): with the identity table
+The token log of the chunked prefill (``store_chunk_log``) uses the same
+frame tables for its rows and a per-slot decay record for the gates
+(``kernel/linear_attention/state_io.py:83-126``, ``layout.py:29-80``).
+
+Pinning (``tests/test_oracle_frames.py``): with the identity table
 ``payload_frames[s, i] = s fps + i`` the storage is one contiguous pool, so
 ``read_frame_states`` must equal a plain reshape of the storage (heads inside
-one frame, heads spanning frames, padded heads); relabelling frames (moving
-frame f's bytes to frame p(f) and the table entries with them) leaves every
-read unchanged; and ``chunk_gated_delta_rule_to_frames`` on the identity
-table must equal ``gdn.chunk_gated_delta_rule_to_cache`` on the reshaped
-pool bit for bit.
+one frame, heads spanning frames, padded heads), and ``store_chunk_log`` must
+write each row where a reshape of the slot's log payload as
+``[granule, layer, keys | values]`` puts it; relabelling frames (moving frame
+f's bytes to frame p(f) and the table entries with them) leaves every read
+and write unchanged; and ``chunk_gated_delta_rule_to_frames`` on the identity
+table must equal ``gdn.chunk_gated_delta_rule_to_cache`` on the reshaped pool
+bit for bit.
 """
 
 from __future__ import annotations
@@ -105,3 +111,59 @@ def chunk_gated_delta_rule_to_frames(query, key, value, gate, beta, storage, fra
         write_frame_states(storage, frames, [used[i] for i in written], layer, pool[written, 0], frame_bytes,
                            head_bytes)
     return o, v_new
+
+
+def log_element_index(frames, slots, positions, index, columns, layer, layers, granularity, key_heads, HV, dk, dv,
+                      frame_bytes, value):
+    """Flat 16-bit element indices into the frame storage of log rows
+    (``kernel/linear_attention/layout.py:29-80``, ``log_pointer``): slot
+    ``slots[i]``, page position ``positions[i]``, row ``index[i]`` (a value
+    head, or a logged key head), element ``columns``.  The slot's log holds,
+    from logical byte 0, granule (position // granularity), layer, keys
+    ``[key_heads, granularity, dk]`` then values ``[HV, granularity, dv]``.
+    Every element is placed through its own byte offset, which equals the
+    reference's per-row placement whenever a row fits one frame."""
+    slots = torch.as_tensor(slots, dtype=torch.int64)[:, None]
+    positions = torch.as_tensor(positions, dtype=torch.int64)[:, None]
+    index = torch.as_tensor(index, dtype=torch.int64)[:, None]
+    columns = torch.as_tensor(columns, dtype=torch.int64)[None, :]
+    key_size = granularity * key_heads * dk
+    layer_size = key_size + granularity * HV * dv
+    dim = dv if value else dk
+    elem = ((positions // granularity * layers + layer) * layer_size + (key_size if value else 0)
+            + (index * granularity + positions % granularity) * dim + columns)
+    byte = 2 * elem
+    fr = frames.to(torch.int64)[slots, byte // frame_bytes]
+    return (fr * frame_bytes + byte % frame_bytes) // 2
+
+
+def store_chunk_log(storage, frames, frame_bytes, log_slots, token_offsets, v_new, key, gate, decay_frames,
+                    decay_record_bytes, *, layer, layers, granularity, page_size, key_heads):
+    """The token-log stores of the chunked prefill (``state_io.py:83-126``):
+    for every token t with ``log_slots[t] >= 0`` and every value head h,
+    ``v_new[t, h]`` goes to value row h, ``key[t, h // (HV // H)]`` to key row
+    ``h // (HV // key_heads)`` when ``h % (HV // key_heads) == 0``, and
+    ``gate[t, h]`` (fp32) to float ``(layer page_size + position) HV + h`` of
+    the slot's decay record.  ``storage`` ([num_frames, frame_bytes / 2],
+    16-bit) is modified in place; v_new [T, HV, dv], key [T, H, dk] in its
+    dtype, gate [T, HV]."""
+    T, HV, dv = v_new.shape
+    H, dk = key.shape[1:]
+    flat = storage.view(-1)
+    as_bytes = storage.view(torch.uint8).view(-1)
+    group = HV // key_heads
+    for t in range(T):
+        slot, pos = int(log_slots[t]), int(token_offsets[t])
+        if slot < 0 or not 0 <= pos < page_size:
+            continue
+        heads = list(range(HV))
+        idx = log_element_index(frames, [slot] * HV, [pos] * HV, heads, range(dv), layer, layers, granularity,
+                                key_heads, HV, dk, dv, frame_bytes, True)
+        flat[idx.reshape(-1)] = v_new[t].reshape(-1).to(storage.dtype)
+        logged = [h for h in heads if h % group == 0]
+        kidx = log_element_index(frames, [slot] * len(logged), [pos] * len(logged), [h // group for h in logged],
+                                 range(dk), layer, layers, granularity, key_heads, HV, dk, dv, frame_bytes, False)
+        flat[kidx.reshape(-1)] = key[t, [h // (HV // H) for h in logged]].reshape(-1).to(storage.dtype)
+        frame, record = int(decay_frames[slot, 0]), int(decay_frames[slot, 1])
+        base = frame * frame_bytes + record * decay_record_bytes + 4 * ((layer * page_size + pos) * HV)
+        as_bytes[base:base + 4 * HV] = gate[t].to(torch.float32).contiguous().view(torch.uint8)

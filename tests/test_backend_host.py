@@ -318,8 +318,9 @@ def test_marconi_copy_blocks_rejects_aliasing():
 
 
 def test_chunk_entry_rejects_what_it_does_not_cover():
-    """The LogState token log and frame tables / granularities below 64 with
-    head_v_dim 32 raise NotImplementedError before anything is launched."""
+    """A token log without frame storage is rejected, and frame tables /
+    granularities below 64 with head_v_dim 32 raise NotImplementedError,
+    before anything is launched."""
     from logssms_amd.kernel.linear_attention import ChunkLogIO, ChunkStateIO, chunk_gated_delta_rule_to_cache
     T, H, dk, dv = 4, 1, 32, 32
     q = torch.zeros(1, T, H, dk, dtype=torch.bfloat16)
@@ -330,7 +331,7 @@ def test_chunk_entry_rejects_what_it_does_not_cover():
     pool = torch.zeros(1, 1, H, dk, dv)
     io = ChunkStateIO(pool, slots, torch.tensor([-1]))
     log = ChunkLogIO(slots, torch.zeros(T, dtype=torch.int64), torch.zeros(1, 2, dtype=torch.int32), g, 64, 4, H)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(AssertionError):
         chunk_gated_delta_rule_to_cache(q, q, v, g, g, io, cu, log_io=log)
     with pytest.raises(NotImplementedError):
         chunk_gated_delta_rule_to_cache(q, q, v, g, g, ChunkStateIO(pool, slots, torch.tensor([-1])), cu,

@@ -117,3 +117,88 @@ def test_chunk_on_frames_equals_the_plain_pool(chunk_size):
     torch.testing.assert_close(vn_b, vn_a, rtol=0, atol=0)
     torch.testing.assert_close(_as_pool(storage, slots, layers, HV, dk, dv, head_bytes, itemsize), pool,
                                rtol=0, atol=0)
+
+
+def _log_case(frame_bytes, seed, key_heads=2):
+    """A small token log: 2 layers, granularity 4, page 8, H = 2, HV = 4."""
+    H, HV, dk, dv, layers, gran, page = 2, 4, 6, 8, 2, 4, 8
+    log_elems = page * layers * (key_heads * dk + HV * dv)
+    fps = -(-2 * log_elems // frame_bytes)
+    slots = 3
+    record = 4 * layers * page * HV
+    g = torch.Generator().manual_seed(seed)
+    T = 10
+    frames = _identity(slots, fps)
+    decay = torch.tensor([[slots * fps + s, 0] for s in range(slots)], dtype=torch.int32)
+    storage = torch.randn(slots * fps + slots, frame_bytes // 2, generator=g).to(torch.bfloat16)
+    log_slots = torch.tensor([0, 2, -1, 0, 2, 2, 0, -1, 2, 0])
+    offsets = torch.tensor([0, 1, 3, 5, 7, 2, 3, 4, 6, 7])
+    v_new = torch.randn(T, HV, dv, generator=g).to(torch.bfloat16)
+    key = torch.randn(T, H, dk, generator=g).to(torch.bfloat16)
+    gate = -torch.rand(T, HV, generator=g)
+    kw = dict(layer=1, layers=layers, granularity=gran, page_size=page, key_heads=key_heads)
+    return storage, frames, decay, record, log_slots, offsets, v_new, key, gate, kw, fps
+
+
+@pytest.mark.parametrize("frame_bytes", [512, 264, 260])
+@pytest.mark.parametrize("key_heads", [2, 1])
+def test_identity_table_log_lands_in_the_reshaped_payload(frame_bytes, key_heads):
+    """Rows within one frame (512 bytes), value rows straddling frames (264),
+    key and value rows straddling frames (260); a decay record (256 bytes)
+    always fits one frame."""
+    storage, frames, decay, record, slots, offsets, v_new, key, gate, kw, fps = _log_case(frame_bytes, 8, key_heads)
+    before = storage.clone()
+    fr.store_chunk_log(storage, frames, frame_bytes, slots, offsets, v_new, key, gate, decay, record, **kw)
+    H, HV, dk, dv = 2, 4, 6, 8
+    gran, page, layers, layer = kw["granularity"], kw["page_size"], kw["layers"], kw["layer"]
+    KH = key_heads
+    n_slots = 3
+    per_layer = gran * (KH * dk + HV * dv)
+    payload = storage[:n_slots * fps].reshape(n_slots, -1)[:, :page * layers * (KH * dk + HV * dv)]
+    payload = payload.reshape(n_slots, page // gran, layers, per_layer)
+    keys = payload[..., :gran * KH * dk].reshape(n_slots, page // gran, layers, KH, gran, dk)
+    values = payload[..., gran * KH * dk:].reshape(n_slots, page // gran, layers, HV, gran, dv)
+    decay_view = storage[n_slots * fps:].view(torch.uint8)[:, :record].contiguous().view(torch.float32)
+    decay_view = decay_view.reshape(n_slots, layers, page, HV)
+    last = {}
+    for t in range(len(slots)):
+        if int(slots[t]) >= 0:
+            last[(int(slots[t]), int(offsets[t]))] = t
+    for (s, pos), t in last.items():
+        assert torch.equal(values[s, pos // gran, layer, :, pos % gran], v_new[t])
+        for kh in range(KH):
+            h = kh * (HV // KH)
+            assert torch.equal(keys[s, pos // gran, layer, kh, pos % gran], key[t, h // (HV // H)])
+        assert torch.equal(decay_view[s, layer, pos], gate[t])
+    # nothing else moved: restore the logged rows from `before` and compare
+    restored = storage.clone()
+    rv = restored[:n_slots * fps].reshape(n_slots, -1)[:, :page * layers * (KH * dk + HV * dv)]
+    rv = rv.reshape(n_slots, page // gran, layers, per_layer)
+    bv = before[:n_slots * fps].reshape(n_slots, -1)[:, :page * layers * (KH * dk + HV * dv)]
+    bv = bv.reshape(n_slots, page // gran, layers, per_layer)
+    rd = restored[n_slots * fps:].view(torch.uint8)
+    bd = before[n_slots * fps:].view(torch.uint8)
+    for (s, pos), _ in last.items():
+        for kh in range(KH):
+            o = (kh * gran + pos % gran) * dk
+            rv[s, pos // gran, layer, o:o + dk] = bv[s, pos // gran, layer, o:o + dk]
+        for h in range(HV):
+            o = gran * KH * dk + (h * gran + pos % gran) * dv
+            rv[s, pos // gran, layer, o:o + dv] = bv[s, pos // gran, layer, o:o + dv]
+        b = 4 * ((layer * page + pos) * HV)
+        rd[s, b:b + 4 * HV] = bd[s, b:b + 4 * HV]
+    assert torch.equal(restored.view(torch.int16), before.view(torch.int16))
+
+
+def test_relabelled_frames_log_the_same():
+    storage, frames, decay, record, slots, offsets, v_new, key, gate, kw, _ = _log_case(260, 9)
+    perm = torch.randperm(storage.shape[0], generator=torch.Generator().manual_seed(10))
+    moved = torch.empty_like(storage)
+    moved[perm] = storage
+    table = perm[frames.long()].to(torch.int32)
+    dtable = decay.clone()
+    dtable[:, 0] = perm[decay[:, 0].long()].to(torch.int32)
+    fr.store_chunk_log(storage, frames, 260, slots, offsets, v_new, key, gate, decay, record, **kw)
+    fr.store_chunk_log(moved, table, 260, slots, offsets, v_new, key, gate, dtable, record, **kw)
+    # bit patterns (decay floats written into 16-bit storage may read as NaN)
+    assert torch.equal(moved[perm].view(torch.int16), storage.view(torch.int16))
