@@ -14,8 +14,9 @@
 //   (I + L)^-1 = (I - L + L^2 - L^3)(I + L^4)(I + L^8)(I + L^16)
 // (L is nilpotent), evaluated with MFMA products in registers.
 //
-// Mapping: one workgroup per (sequence, v-head, 64-column slice of d_v); 8 waves.
-//   * Chain waves 0-1: wave j owns state columns 32j..32j+31 for the whole
+// Mapping: one workgroup per (sequence, v-head, 64-column slice of d_v); 12
+// waves, waves i, i + 4 and i + 8 on SIMD i.
+//   * Chain waves 0-3: wave j owns state columns 16j..16j+15 for the whole
 //     sequence as fp32 MFMA accumulator tiles.  Every product of the chain
 //     takes its right operand straight from accumulator registers: the k index
 //     of each 32-deep product is ordered so that lane group g (= lane / 16)
@@ -24,21 +25,24 @@
 //     LDS) is read in that same order; K^T rows come from the token-major K
 //     tile through the LDS transpose read.  Per chunk: P = K h and o^T = h^T
 //     q^T, R, v', o^T += v'^T M^T (stored directly: a lane holds 4 consecutive
-//     output columns of one token), h update.
-//   * Side waves 2-7 prepare chunk c+1 while the chain runs chunk c: waves 2
-//     and 3 form A11 and A22 (k k^T tiles, masks, product-form inverse, all
-//     in registers), waves 4-7 the masked q k^T tiles (M) and -L21, and stage
-//     / prefetch later chunks (K, Q, V tiles and the gate table).
-//   * Waves i and i + 4 share a SIMD (chain waves with waves 4-5, inverse
-//     waves with waves 6-7).
+//     output columns of one token), h update, checkpoint stores.
+//   * Side waves prepare chunk c+1 while the chain runs chunk c: waves 4-5
+//     form A11 and A22 (k k^T tiles, masks, product-form inverse, all in
+//     registers) and two masked tiles; waves 6-9 the other masked q k^T tiles
+//     (M) and -L21, and stage / prefetch later chunks (K, Q tiles); waves
+//     10-11 the V tiles (staged, or on the fused path computed) and wave 10
+//     the gate table.
 //   * Fused variant (FUSED): the V tiles are the conv + SiLU of the raw
-//     projections, computed by waves 4-5 before the M barrier, and the gate
+//     projections, computed by waves 10-11 before the M barrier, and the gate
 //     table is prepared from the raw gate / beta projections; q and k come
 //     normalised from a separate pass (their conv is shared by every
 //     workgroup of a key head).
+//   * EXT variant: checkpoints every 16 or 32 tokens (the states at interval
+//     ends inside a chunk, formed from the chunk's K and v') and frame-table
+//     state addressing (LogState payload frames).
 // Two workgroup barriers per chunk (LDS-only waits, so global prefetches stay
-// in flight).  MFMA operands are f16 (bf16 inputs convert exactly; values
-// saturate at +-65504) with fp32 accumulation.
+// in flight).  MFMA operands are f16 (bf16 inputs convert exactly; magnitudes
+// beyond 65504 become +-inf) with fp32 accumulation.
 //
 // Roofline: MFMA (16-bit).  Algorithmic flops per token per v-head:
 // 10 C d + 6 d^2 + 2/3 C^2 (C = 64, d = 128).
