@@ -167,6 +167,60 @@ int gdn_store_chunk_log(void* storage, const void* frames, int frames_dtype, int
                         int64_t num_layers, int64_t granularity, int64_t page_size, void* stream);
 
 /*
+ * LogState conv decode: replaces conv_decode (kernel/linear_attention/
+ * conv_decode.py:293-352) with pool= (the conv snapshots of
+ * cache/logstate/frame_pool.py in frames).  For sequence b the window of
+ * channel ch is elements layer C (W-1) + ch (W-1) + s of the snapshot of
+ * (read_slots[b], read_granules[b]); element e of snapshot (slot, granule) is
+ * conv_frames[(slot G + granule) F + e / frame_elems] * frame_elems + e %
+ * frame_elems of the storage (F = frames_per_granule; with F == 1,
+ * conv_frames[slot G + granule] * frame_elems + e; layout.py:104-112).  The
+ * shifted window goes to (write_slots[b], write_granules[b]) and to granule 0
+ * of work_slots[b].  A negative slot or an unmapped frame reads zeros and
+ * takes no write.  Outputs as gdn_conv_decode; bf16 or f16 storage.
+ */
+int gdn_conv_decode_logstate(const void* x, int64_t x_row_stride, int64_t x_col_stride, int dtype,
+                             const void* weight, const void* bias, int kernel_width, int64_t batch, int64_t channels,
+                             void* storage, const void* conv_frames, int frames_dtype, int64_t num_granules,
+                             int64_t frames_per_granule, int64_t frame_bytes, int64_t num_frames, int64_t layer,
+                             const void* read_slots, int read_dtype, const void* read_granules,
+                             int read_granules_dtype, const void* write_slots, int write_dtype,
+                             const void* write_granules, int write_granules_dtype, const void* work_slots,
+                             int work_dtype, void* q_out, void* k_out, void* v_out, int64_t key_dim, int split_qkv,
+                             int round_conv, void* stream);
+
+/*
+ * LogState decode step: replaces fused_recurrent_gated_delta_rule_to_logstate
+ * (vendor/fla/fused_recurrent.py:292-394 -> _fused_recurrent_gated_delta_kernel
+ * with DIRECT_STORE, :31-288, and _gdn_replay_kernel, gdn_replay.py:17-148).
+ * Per sequence b (work slot w, log slot l, page position p, replay count n <= 16):
+ *   state = the work slot's state (frame-table addressed as in
+ *   gdn_chunk_gated_delta_rule), plus, unless eager, the n tokens logged at
+ *   positions p-n..p-1 of l replayed onto it (S = e^{sum g} S_w + sum_i k_i
+ *   (e^{sum_{j>i} g_j} v'_i)^T, the scaled v' rounded to the io dtype);
+ *   raw q, k [B, H, dk], v [B, HV, dv] (io dtype), gate/beta [B, HV] strided,
+ *   A_log/dt_bias [HV]: q, k L2-normalised, g = -exp(A_log) softplus(gate +
+ *   dt_bias), beta = sigmoid(beta); eager: the fused_recurrent step; else
+ *   delta = (v - e^g S^T k) beta, o = e^g S^T q + delta (k.q);
+ *   log rows at p of l: v' = delta, key (v-heads h with h % (HV/H) == 0) =
+ *   normalised k, decay record float (layer page + p) HV + h = g;
+ *   the new state goes to w every step (eager) or when (p + 1) % 16 == 0.
+ * The log layout and decay records are those of gdn_store_chunk_log with
+ * key_heads = H.  out [B, HV, dv] io dtype.
+ */
+int gdn_recurrent_logstate(const void* q, const void* k, const void* v, int io_dtype, const void* gate,
+                           int64_t gate_b_stride, int64_t gate_h_stride, int gate_dtype, const void* beta,
+                           int64_t beta_b_stride, int64_t beta_h_stride, int beta_dtype, const void* A_log,
+                           int a_dtype, const void* dt_bias, int dt_dtype, int64_t batch, int64_t H, int64_t HV,
+                           int64_t dk, int64_t dv, void* storage, const void* payload_frames, int frames_dtype,
+                           int64_t frames_per_slot, int64_t frame_bytes, int64_t head_bytes, int64_t num_frames,
+                           const void* decay_frames, int decay_dtype, int64_t decay_record_bytes,
+                           const void* work_slots, int work_dtype, const void* log_slots, int log_dtype,
+                           const void* token_offsets, int offsets_dtype, const void* replay_counts, int counts_dtype,
+                           int64_t layer, int64_t num_layers, int64_t granularity, int64_t page_size, int eager,
+                           void* out, float scale, void* stream);
+
+/*
  * The GDN prefill of one layer (layers/linear_attention_backend/gdn.py:100-150:
  * history gather, packed_causal_conv1d, split, prepare_gdn,
  * chunk_gated_delta_rule_to_cache) as three launches whose results equal

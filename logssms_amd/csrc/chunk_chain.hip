@@ -41,8 +41,11 @@
 //     ends inside a chunk, formed from the chunk's K and v') and frame-table
 //     state addressing (LogState payload frames).
 // Two workgroup barriers per chunk (LDS-only waits, so global prefetches stay
-// in flight).  MFMA operands are f16 (bf16 inputs convert exactly; magnitudes
-// beyond 65504 become +-inf) with fp32 accumulation.
+// in flight).  MFMA operands are f16 with fp32 accumulation: bf16 values
+// convert exactly within f16's normal range, magnitudes below 2^-14 keep
+// fewer bits (f16 subnormals; at most 2^-25 absolute error) and magnitudes
+// beyond 65504 become +-inf.  The operands are normalised q / k, decays and
+// beta <= 1, the solve's A, v / v' and the state slices.
 //
 // Roofline: MFMA (16-bit).  Algorithmic flops per token per v-head:
 // 10 C d + 6 d^2 + 2/3 C^2 (C = 64, d = 128).

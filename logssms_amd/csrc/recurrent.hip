@@ -484,9 +484,13 @@ __global__ __launch_bounds__(kThreads) void conv_decode_kernel(
   if (ch >= C) return;
   const int64_t rs = load_index(reads, b * read_stride, read_is64);
   const int64_t ws = load_index(writes, b * write_stride, write_is64);
-  const IOT* src = state + rs * slot_stride + layer * layer_stride + ch * (W - 1);
   float win[8];
-  for (int i = 0; i < W - 1; ++i) win[i] = to_f32(src[i]);
+  if (rs >= 0) {  // a negative read slot is a zero history
+    const IOT* src = state + rs * slot_stride + layer * layer_stride + ch * (W - 1);
+    for (int i = 0; i < W - 1; ++i) win[i] = to_f32(src[i]);
+  } else {
+    for (int i = 0; i < W - 1; ++i) win[i] = 0.f;
+  }
   float xv = to_f32(x[b * xr + ch * xc]);
   if (s0 != 1.f || s1 != 1.f || s2 != 1.f) {
     const float sc = ch < end0 ? s0 : (ch < end1 ? s1 : s2);
@@ -498,9 +502,11 @@ __global__ __launch_bounds__(kThreads) void conv_decode_kernel(
   if (bias) acc += to_f32(bias[ch]);
   if (round_conv) acc = round_to<IOT>(acc);
   const IOT y = from_f32<IOT>(silu(acc));
-  IOT* dst = state + ws * slot_stride + layer * layer_stride + ch * (W - 1);
-  for (int i = 0; i + 1 < W - 1; ++i) dst[i] = from_f32<IOT>(win[i + 1]);
-  dst[W - 2] = from_f32<IOT>(xv);
+  if (ws >= 0) {  // a negative write slot takes no write
+    IOT* dst = state + ws * slot_stride + layer * layer_stride + ch * (W - 1);
+    for (int i = 0; i + 1 < W - 1; ++i) dst[i] = from_f32<IOT>(win[i + 1]);
+    dst[W - 2] = from_f32<IOT>(xv);
+  }
   if (!split) {
     q[b * C + ch] = y;
   } else if (ch < key_dim) {

@@ -5,6 +5,7 @@ from .conv_decode import conv_decode
 from .gdn import (
     chunk_gated_delta_rule_to_cache,
     fused_recurrent_gated_delta_rule,
+    fused_recurrent_gated_delta_rule_to_logstate,
     fused_recurrent_gated_delta_rule_to_slots,
 )
 from .packed_conv import PackedConvStateIO, packed_causal_conv1d
@@ -17,6 +18,7 @@ __all__ = [
     "chunk_gated_delta_rule_to_cache",
     "conv_decode",
     "fused_recurrent_gated_delta_rule",
+    "fused_recurrent_gated_delta_rule_to_logstate",
     "fused_recurrent_gated_delta_rule_to_slots",
     "packed_causal_conv1d",
 ]

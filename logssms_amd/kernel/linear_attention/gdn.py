@@ -235,10 +235,79 @@ def fused_recurrent_gated_delta_rule(
     return output, states
 
 
+@torch.compiler.disable
+def fused_recurrent_gated_delta_rule_to_logstate(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    gate: torch.Tensor,
+    beta: torch.Tensor,
+    A_log: torch.Tensor,
+    dt_bias: torch.Tensor,
+    pool,
+    work_slots: torch.Tensor,
+    log_slots: torch.Tensor,
+    token_offsets: torch.Tensor,
+    layer: int,
+    replay_counts: torch.Tensor,
+    enable_eager_state: bool = False,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """fused_recurrent.py:292-394: one LogState decode step per sequence.
+    The state is the work slot's state in the pool's frame storage plus,
+    unless ``enable_eager_state``, the ``replay_counts[b]`` (<= 16) tokens
+    logged since it, replayed from the log (``gdn_replay.py:17-148``); the
+    step's v' row, key row and gate go into the log at ``token_offsets[b]`` of
+    ``log_slots[b]``; the new state goes to the work slot every step (eager) or
+    at the end of each 16-token replay window.  Raw inputs as
+    ``fused_recurrent_gated_delta_rule_to_slots``.  ``pool`` carries
+    ``storage``, ``payload_frame_table``, ``decay_frame_table``,
+    ``frame_bytes``, ``head_payload_bytes``, ``page_size`` and ``layout``
+    (``head_k_dim``, ``head_v_dim``, ``num_value_heads``,
+    ``num_linear_layers``, ``granularity``, ``log_decay_bytes``), as
+    ``cache/logstate/frame_pool.py``'s pool does."""
+    batch_size, seq_len, num_k_heads, head_k_dim = query.shape
+    num_v_heads, head_v_dim = value.shape[2:]
+    layout = pool.layout
+    assert seq_len == 1
+    assert head_k_dim == layout.head_k_dim and head_v_dim == layout.head_v_dim
+    assert num_v_heads == layout.num_value_heads and num_v_heads % num_k_heads == 0
+    assert replay_counts.shape == work_slots.shape == log_slots.shape == token_offsets.shape == (batch_size,)
+    assert pool.frame_bytes % pool.head_payload_bytes == 0 or pool.head_payload_bytes % pool.frame_bytes == 0
+    output = torch.empty_like(value) if out is None else out
+    assert output.shape == value.shape and output.dtype == value.dtype and output.is_contiguous()
+    if batch_size == 0:
+        return output
+    storage = pool.storage
+    frames = pool.payload_frame_table.contiguous()
+    decay = pool.decay_frame_table.contiguous()
+    assert storage.is_contiguous() and storage.device == query.device
+    num_frames = storage.numel() * storage.element_size() // pool.frame_bytes
+    query, key, value = query.contiguous(), key.contiguous(), value.contiguous()
+    gate, beta, A_log, dt_bias = _gates(gate, beta, A_log, dt_bias)
+    slots = [t.contiguous() for t in (work_slots, log_slots, token_offsets, replay_counts)]
+    _lib.call(
+        "gdn_recurrent_logstate",
+        query.data_ptr(), key.data_ptr(), value.data_ptr(), _lib.dtype_code(value.dtype),
+        gate.data_ptr(), gate.stride(0), gate.stride(2), _lib.dtype_code(gate.dtype),
+        beta.data_ptr(), beta.stride(0), beta.stride(2), _lib.dtype_code(beta.dtype),
+        A_log.data_ptr(), _lib.dtype_code(A_log.dtype), dt_bias.data_ptr(), _lib.dtype_code(dt_bias.dtype),
+        batch_size, num_k_heads, num_v_heads, head_k_dim, head_v_dim,
+        storage.data_ptr(), frames.data_ptr(), _lib.index_code(frames), frames.shape[1], pool.frame_bytes,
+        pool.head_payload_bytes, num_frames, decay.data_ptr(), _lib.index_code(decay), layout.log_decay_bytes,
+        slots[0].data_ptr(), _lib.index_code(slots[0]), slots[1].data_ptr(), _lib.index_code(slots[1]),
+        slots[2].data_ptr(), _lib.index_code(slots[2]), slots[3].data_ptr(), _lib.index_code(slots[3]),
+        layer, layout.num_linear_layers, layout.granularity, pool.page_size, int(enable_eager_state),
+        output.data_ptr(), float(head_k_dim) ** -0.5, _lib.stream_of(query),
+    )
+    return output
+
+
 __all__ = [
     "ChunkLogIO",
     "ChunkStateIO",
     "chunk_gated_delta_rule_to_cache",
     "fused_recurrent_gated_delta_rule",
+    "fused_recurrent_gated_delta_rule_to_logstate",
     "fused_recurrent_gated_delta_rule_to_slots",
 ]

@@ -32,7 +32,7 @@ from __future__ import annotations
 
 import torch
 
-from .gdn import chunk_gated_delta_rule_to_cache
+from .gdn import chunk_gated_delta_rule_to_cache, l2norm, softplus_decode
 
 
 def frame_state_index(frames, slots, layer, HV, dk, dv, itemsize, frame_bytes, head_bytes):
@@ -114,7 +114,7 @@ def chunk_gated_delta_rule_to_frames(query, key, value, gate, beta, storage, fra
 
 
 def log_element_index(frames, slots, positions, index, columns, layer, layers, granularity, key_heads, HV, dk, dv,
-                      frame_bytes, value):
+                      frame_bytes, value, itemsize=2):
     """Flat 16-bit element indices into the frame storage of log rows
     (``kernel/linear_attention/layout.py:29-80``, ``log_pointer``): slot
     ``slots[i]``, page position ``positions[i]``, row ``index[i]`` (a value
@@ -122,7 +122,9 @@ def log_element_index(frames, slots, positions, index, columns, layer, layers, g
     from logical byte 0, granule (position // granularity), layer, keys
     ``[key_heads, granularity, dk]`` then values ``[HV, granularity, dv]``.
     Every element is placed through its own byte offset, which equals the
-    reference's per-row placement whenever a row fits one frame."""
+    reference's per-row placement whenever a row fits one frame.  The
+    reference's log elements are 16-bit (``itemsize`` 2); other sizes serve
+    the oracle's own fp32 checks."""
     slots = torch.as_tensor(slots, dtype=torch.int64)[:, None]
     positions = torch.as_tensor(positions, dtype=torch.int64)[:, None]
     index = torch.as_tensor(index, dtype=torch.int64)[:, None]
@@ -132,9 +134,9 @@ def log_element_index(frames, slots, positions, index, columns, layer, layers, g
     dim = dv if value else dk
     elem = ((positions // granularity * layers + layer) * layer_size + (key_size if value else 0)
             + (index * granularity + positions % granularity) * dim + columns)
-    byte = 2 * elem
+    byte = itemsize * elem
     fr = frames.to(torch.int64)[slots, byte // frame_bytes]
-    return (fr * frame_bytes + byte % frame_bytes) // 2
+    return (fr * frame_bytes + byte % frame_bytes) // itemsize
 
 
 def store_chunk_log(storage, frames, frame_bytes, log_slots, token_offsets, v_new, key, gate, decay_frames,
@@ -167,3 +169,142 @@ def store_chunk_log(storage, frames, frame_bytes, log_slots, token_offsets, v_ne
         frame, record = int(decay_frames[slot, 0]), int(decay_frames[slot, 1])
         base = frame * frame_bytes + record * decay_record_bytes + 4 * ((layer * page_size + pos) * HV)
         as_bytes[base:base + 4 * HV] = gate[t].to(torch.float32).contiguous().view(torch.uint8)
+
+
+# ----------------------------------------------------------------- LogState decode
+
+def conv_element_index(conv_frames, slots, granules, layer, C, S, frame_elems):
+    """Flat element indices ``[len(slots), C S]`` of the conv windows of
+    (slot, granule) at ``layer`` (``layout.py:104-112``, ``conv_pointer``):
+    element ``layer C S + ch S + s`` of the (slot, granule) snapshot lies in
+    frame ``conv_frames[slot, granule, e // frame_elems]`` at ``e % frame_elems``
+    (one frame per snapshot: ``conv_frames[slot, granule, 0]`` plus e)."""
+    slots = torch.as_tensor(slots, dtype=torch.int64)[:, None]
+    granules = torch.as_tensor(granules, dtype=torch.int64)[:, None]
+    elem = layer * C * S + torch.arange(C * S, dtype=torch.int64)[None, :]
+    table = conv_frames.to(torch.int64)
+    if table.shape[2] == 1:
+        return table[slots, granules, 0] * frame_elems + elem
+    return table[slots, granules, elem // frame_elems] * frame_elems + elem % frame_elems
+
+
+def conv_decode_logstate(x, weight, storage, conv_frames, frame_bytes, layer, read_slots, read_granules,
+                         write_slots, write_granules, work_slots, *, round_conv=False):
+    """``conv_decode`` with the LogState pool (``conv_decode.py:293-352`` with
+    ``pool=``, kernel ``:25-289``): the window is read from (read slot, read
+    granule), and the shifted window goes to (write slot, write granule) and to
+    granule 0 of the work slot.  ``storage`` ([num_frames, frame elements], the
+    io dtype) is modified in place.  Returns y [B, C]."""
+    B, C = x.shape
+    W = weight.shape[-1]
+    S = W - 1
+    fe = frame_bytes // storage.element_size()
+    flat = storage.view(-1)
+    idx = conv_element_index(conv_frames, read_slots, read_granules, layer, C, S, fe)
+    windows = flat[idx].view(B, C, S)
+    acc_t = torch.float64 if x.dtype == torch.float64 else torch.float32
+    full = torch.cat([windows, x[:, :, None]], -1).to(acc_t)
+    acc = (full * weight.reshape(C, W).to(acc_t)[None]).sum(-1)
+    if round_conv:
+        acc = acc.to(x.dtype).to(acc_t)
+    y = (acc / (1.0 + torch.exp(-acc))).to(x.dtype)
+    new = torch.cat([windows[:, :, 1:], x[:, :, None]], -1).to(storage.dtype).reshape(B, C * S)
+    for slots, granules in ((write_slots, write_granules), (work_slots, torch.zeros(B, dtype=torch.int64))):
+        out = conv_element_index(conv_frames, slots, granules, layer, C, S, fe)
+        flat[out.reshape(-1)] = new.reshape(-1)
+    return y
+
+
+def fused_recurrent_to_logstate(query, key, value, gate, beta, A_log, dt_bias, storage, payload_frames,
+                                decay_frames, frame_bytes, head_bytes, record_bytes, work_slots, log_slots,
+                                token_offsets, replay_counts, *, layer, layers, granularity, page_size,
+                                eager=False, window=16, dtype=torch.float32):
+    """LogState decode (``vendor/fla/fused_recurrent.py:292-394``, kernels
+    ``:31-288`` with DIRECT_STORE and ``gdn_replay.py:17-148``).  Per sequence
+    b with work slot w, log slot l, page position p and replay count n:
+
+    * state: the work slot's state, and unless ``eager`` the n tokens logged
+      since it (positions p - n .. p - 1) replayed onto it,
+      S = e^{sum g} S_w + sum_i k_i (e^{sum_{j > i} g_j} v'_i)^T, the scaled
+      logged values rounded to the io dtype (``replay.py``);
+    * step (raw inputs, q / k L2-normalised, g = -exp(A_log) softplus(gate +
+      dt_bias), beta = sigmoid(beta)): eager as ``fused_recurrent``; otherwise
+      delta = (v - e^g S^T k) beta, o = e^g S^T q + delta (k . q);
+    * logs at position p of slot l: v' row = delta, key row = k (for v-heads
+      h with h % (HV / H) == 0), decay = g;
+    * the work slot receives the new state every step when ``eager``, else
+      only when (p + 1) % window == 0.
+
+    query/key [B, 1, H, dk], value [B, 1, HV, dv], gate/beta [B, 1, HV].
+    ``storage`` ([num_frames, frame elements], the io dtype) is modified in
+    place.  Returns o [B, 1, HV, dv]."""
+    B, _, H, dk = query.shape
+    HV, dv = value.shape[2:]
+    group = HV // H
+    io = value.dtype
+    item = storage.element_size()
+    flat = storage.view(-1)
+    as_bytes = storage.view(torch.uint8).view(-1)
+    scale = dk ** -0.5
+    q_all = l2norm(query[:, 0].to(dtype)) * scale
+    k_all = l2norm(key[:, 0].to(dtype))
+    g_all = -torch.exp(A_log.to(dtype))[None] * softplus_decode(gate[:, 0].to(dtype) + dt_bias.to(dtype))
+    b_all = torch.sigmoid(beta[:, 0].to(dtype))
+    out = torch.empty(B, 1, HV, dv, dtype=io)
+    for b in range(B):
+        w, lslot, pos, n = int(work_slots[b]), int(log_slots[b]), int(token_offsets[b]), int(replay_counts[b])
+        state = read_frame_states(storage, payload_frames, [w], layer, HV, dk, dv, frame_bytes,
+                                  head_bytes)[0].to(dtype)
+        frame, record = int(decay_frames[lslot, 0]), int(decay_frames[lslot, 1])
+        rec = frame * frame_bytes + record * record_bytes
+        if not eager and n > 0:
+            positions = list(range(pos - n, pos))
+            g_log = torch.stack([as_bytes[rec + 4 * (layer * page_size + t) * HV:
+                                          rec + 4 * ((layer * page_size + t) * HV + HV)].view(torch.float32)
+                                 for t in positions]).to(dtype)  # [n, HV]
+            heads = list(range(HV))
+            keys = torch.stack([flat[log_element_index(payload_frames, [lslot] * HV, [t] * HV,
+                                                       [h // group for h in heads], range(dk), layer, layers,
+                                                       granularity, H, HV, dk, dv, frame_bytes, False, item)]
+                                for t in positions]).to(dtype)  # [n, HV, dk]
+            vals = torch.stack([flat[log_element_index(payload_frames, [lslot] * HV, [t] * HV, heads, range(dv),
+                                                       layer, layers, granularity, H, HV, dk, dv, frame_bytes,
+                                                       True, item)]
+                                for t in positions]).to(dtype)  # [n, HV, dv]
+            total = g_log.sum(0)
+            suffix = torch.exp(total[None] - torch.cumsum(g_log, 0))
+            scaled = (vals * suffix[..., None]).to(io).to(dtype)
+            state = state * torch.exp(total)[:, None, None] + torch.einsum('thk,thv->hkv', keys, scaled)
+        q = q_all[b].repeat_interleave(group, 0)  # [HV, dk]
+        k = k_all[b].repeat_interleave(group, 0)
+        g, bt = g_all[b], b_all[b]
+        v = value[b, 0].to(dtype)
+        decay = torch.exp(g)
+        if eager:
+            state = state * decay[:, None, None]
+            delta = (v - (state * k[:, :, None]).sum(1)) * bt[:, None]
+            state = state + k[:, :, None] * delta[:, None, :]
+            o = (state * q[:, :, None]).sum(1)
+            new_state = state
+        else:
+            sk = (state * k[:, :, None]).sum(1) * decay[:, None]
+            sq = (state * q[:, :, None]).sum(1) * decay[:, None]
+            delta = (v - sk) * bt[:, None]
+            o = sq + delta * (k * q).sum(-1, keepdim=True)
+            new_state = state * decay[:, None, None] + k[:, :, None] * delta[:, None, :]
+        out[b, 0] = o.to(io)
+        if lslot >= 0 and 0 <= pos < page_size:
+            heads = list(range(HV))
+            vidx = log_element_index(payload_frames, [lslot] * HV, [pos] * HV, heads, range(dv), layer, layers,
+                                     granularity, H, HV, dk, dv, frame_bytes, True, item)
+            flat[vidx.reshape(-1)] = delta.to(io).reshape(-1)
+            logged = [h for h in heads if h % group == 0]
+            kidx = log_element_index(payload_frames, [lslot] * len(logged), [pos] * len(logged),
+                                     [h // group for h in logged], range(dk), layer, layers, granularity, H, HV, dk,
+                                     dv, frame_bytes, False, item)
+            flat[kidx.reshape(-1)] = k[logged].to(io).reshape(-1)
+            base = rec + 4 * (layer * page_size + pos) * HV
+            as_bytes[base:base + 4 * HV] = g.to(torch.float32).contiguous().view(torch.uint8)
+        if w >= 0 and (eager or (pos + 1) % window == 0):
+            write_frame_states(storage, payload_frames, [w], layer, new_state[None], frame_bytes, head_bytes)
+    return out

@@ -228,3 +228,111 @@ def test_chunk_token_log():
     a, e = host.view(torch.int16).reshape(-1), expected.view(torch.int16).reshape(-1)
     bad = (a != e) & mask
     assert not bad.any(), f"{int(bad.sum())} bytes differ outside the v' rows and states"
+
+
+def _decode_pool(g, slots, H, HV, dk, dv, layers, page, gran, conv_dim, W, frame_bytes, head_bytes):
+    """A fragmented LogState frame storage: payload frames (states and logs),
+    one decay record per slot, conv snapshots per (slot, granule)."""
+    from types import SimpleNamespace
+    fps = max(-(-layers * HV * head_bytes // frame_bytes), -(-2 * page * layers * (H * dk + HV * dv) // frame_bytes))
+    record = 4 * layers * page * HV
+    per_frame = frame_bytes // record
+    n_dec = -(-slots // per_frame)
+    granules = page // gran
+    conv_bytes = 2 * layers * conv_dim * (W - 1)
+    cf = -(-conv_bytes // frame_bytes)
+    total = slots * fps + n_dec + slots * granules * cf + 3
+    order = torch.randperm(total, generator=g)
+    payload = order[:slots * fps].reshape(slots, fps).to(torch.int32)
+    dec = order[slots * fps:slots * fps + n_dec]
+    decay = torch.tensor([[int(dec[s // per_frame]), s % per_frame] for s in range(slots)], dtype=torch.int32)
+    conv = order[slots * fps + n_dec:slots * fps + n_dec + slots * granules * cf].reshape(slots, granules, cf)
+    storage = (torch.randn(total, frame_bytes // 2, generator=g) * 0.05).to(torch.bfloat16)
+    layout = SimpleNamespace(head_k_dim=dk, head_v_dim=dv, num_value_heads=HV, num_linear_layers=layers,
+                             granularity=gran, log_decay_bytes=record, num_granules=granules)
+    pool = SimpleNamespace(storage=None, payload_frame_table=None, decay_frame_table=None,
+                           conv_frame_table=None, frame_bytes=frame_bytes, head_payload_bytes=head_bytes,
+                           page_size=page, layout=layout, dtype=torch.bfloat16)
+    return storage, payload, decay, conv.to(torch.int32), record, pool
+
+
+@pytest.mark.parametrize("eager", [False, True])
+def test_logstate_decode_steps(eager):
+    """34 LogState decode steps (conv through the conv frame table, the
+    recurrence from the work state plus the replayed log) against the oracle:
+    outputs every step, then the work states, the log rows, the gates and the
+    conv windows (fused_recurrent.py:292-394, gdn_replay.py:17-148,
+    conv_decode.py:293-352)."""
+    from types import SimpleNamespace
+    from logssms_amd.kernel.linear_attention import conv_decode, fused_recurrent_gated_delta_rule_to_logstate
+    g = gen(91 + int(eager))
+    B, H, HV, dk, dv, layers, layer, page, gran, W = 3, 2, 4, 128, 128, 2, 1, 64, 16, 4
+    conv_dim = 2 * H * dk + HV * dv
+    frame_bytes, head_bytes = 65536, 32768
+    slots = 6
+    storage, payload, decay, conv, record, pool = _decode_pool(g, slots, H, HV, dk, dv, layers, page, gran, conv_dim,
+                                                               W, frame_bytes, head_bytes)
+    works, logs = torch.tensor([0, 2, 4]), torch.tensor([1, 3, 5])
+    weight = (torch.randn(conv_dim, 1, W, generator=g) * 0.3).to(torch.bfloat16)
+    A_log, dt_bias = torch.randn(HV, generator=g) * 0.3, torch.randn(HV, generator=g) * 0.3
+    cfg = SimpleNamespace(state_len=W - 1, conv_dim=conv_dim, num_k_heads=H, head_k_dim=dk, num_v_heads=HV,
+                          head_v_dim=dv, key_dim=H * dk, layer_idx=layer)
+    expected = storage.clone()
+    dev_u8 = storage.view(torch.uint8).to(DEV)
+    pool.storage = dev_u8
+    pool.payload_frame_table, pool.decay_frame_table, pool.conv_frame_table = payload.to(DEV), decay.to(DEV), conv.to(DEV)
+    T = 34
+    print(f"LogState decode, eager={eager}: {T} steps x {B} sequences", flush=True)
+    for t in range(T):
+        mixed = (torch.randn(B, conv_dim, generator=g)).to(torch.bfloat16)
+        a, bt = torch.randn(B, HV, generator=g), torch.randn(B, HV, generator=g)
+        pos = torch.full((B,), t)
+        counts = torch.zeros(B, dtype=torch.int64) if eager else pos % 16
+        zeros = torch.zeros(B, dtype=torch.int64)
+        # oracle
+        y = ofr.conv_decode_logstate(mixed, weight, expected, conv, frame_bytes, layer, works, zeros, logs,
+                                     pos // gran, works)
+        q, k, v = (y[:, :H * dk].reshape(B, 1, H, dk), y[:, H * dk:2 * H * dk].reshape(B, 1, H, dk),
+                   y[:, 2 * H * dk:].reshape(B, 1, HV, dv))
+        o_ref = ofr.fused_recurrent_to_logstate(q, k, v, a[:, None], bt[:, None], A_log, dt_bias, expected, payload,
+                                                decay, frame_bytes, head_bytes, record, works, logs, pos, counts,
+                                                layer=layer, layers=layers, granularity=gran, page_size=page,
+                                                eager=eager)
+        # device
+        dq, dk_, dvv = conv_decode(mixed.to(DEV), weight.to(DEV), cfg, split_qkv=True, read_slots=works.to(DEV),
+                                   write_slots=logs.to(DEV), pool=pool, read_granules=zeros.to(DEV),
+                                   write_granules=(pos // gran).to(DEV), work_slots=works.to(DEV))
+        o = fused_recurrent_gated_delta_rule_to_logstate(dq, dk_, dvv, a[:, None].to(DEV), bt[:, None].to(DEV),
+                                                         A_log.to(DEV), dt_bias.to(DEV), pool, works.to(DEV),
+                                                         logs.to(DEV), pos.to(DEV), layer, counts.to(DEV),
+                                                         enable_eager_state=eager)
+        assert_bf16_close(dq.reshape(B, -1), q.reshape(B, -1))
+        assert_bf16_close(o, o_ref)
+    torch.cuda.synchronize()
+    host = dev_u8.cpu().view(torch.bfloat16).reshape(storage.shape)
+    _report("out (last step)", o, o_ref)
+    got = ofr.read_frame_states(host, payload, works, layer, HV, dk, dv, frame_bytes, head_bytes)
+    want = ofr.read_frame_states(expected, payload, works, layer, HV, dk, dv, frame_bytes, head_bytes)
+    _report("work states", got, want)
+    assert_state16_close(got, want)
+    # log rows (v' to the output bar, keys within one bf16 rounding step), gates, conv windows
+    for b in range(B):
+        vidx = torch.cat([ofr.log_element_index(payload, [int(logs[b])] * HV, [t] * HV, range(HV), range(dv), layer,
+                                                layers, gran, H, HV, dk, dv, frame_bytes, True) for t in range(T)])
+        assert_bf16_close(host.reshape(-1)[vidx], expected.reshape(-1)[vidx])
+        kidx = torch.cat([ofr.log_element_index(payload, [int(logs[b])] * H, [t] * H, range(H), range(dk), layer,
+                                                layers, gran, H, HV, dk, dv, frame_bytes, False) for t in range(T)])
+        ka, ke = host.reshape(-1)[kidx].float(), expected.reshape(-1)[kidx].float()
+        assert ((ka - ke).abs() <= ke.abs() * 2.0 ** -7 + 1e-6).all()
+    hb, eb = host.view(torch.uint8).reshape(-1), expected.view(torch.uint8).reshape(-1)
+    for b in range(B):
+        fr_, ri = int(decay[int(logs[b]), 0]), int(decay[int(logs[b]), 1])
+        base = fr_ * frame_bytes + ri * record + 4 * (layer * page) * HV
+        ga = hb[base:base + 4 * T * HV].view(torch.float32)
+        ge = eb[base:base + 4 * T * HV].view(torch.float32)
+        torch.testing.assert_close(ga, ge, rtol=1e-5, atol=1e-6)
+    fe = frame_bytes // 2
+    for slot, gr in [(int(works[b]), 0) for b in range(B)] + [(int(logs[b]), t // gran) for b in range(B)
+                                                                for t in (0, T - 1)]:
+        idx = ofr.conv_element_index(conv, [slot], [gr], layer, conv_dim, W - 1, fe)
+        assert torch.equal(host.reshape(-1)[idx].view(torch.int16), expected.reshape(-1)[idx].view(torch.int16))

@@ -202,3 +202,117 @@ def test_relabelled_frames_log_the_same():
     fr.store_chunk_log(moved, table, 260, slots, offsets, v_new, key, gate, dtable, record, **kw)
     # bit patterns (decay floats written into 16-bit storage may read as NaN)
     assert torch.equal(moved[perm].view(torch.int16), storage.view(torch.int16))
+
+
+# ---------------------------------------------------------------- LogState decode
+
+def _decode_pool(seed, dtype=torch.float32, dk=8, dv=8, H=2, HV=4, layers=2, page=32, slots=4, conv_dim=12, W=4,
+                 granules=2):
+    """Frame storage with identity payload tables (state head in one frame of
+    two heads), log payloads, decay records and identity conv tables."""
+    g = torch.Generator().manual_seed(seed)
+    item = torch.tensor([], dtype=dtype).element_size()
+    head_bytes = dk * dv * item
+    record = 4 * layers * page * HV
+    frame_bytes = max(4 * head_bytes, record)
+    log_bytes = item * page * layers * (H * dk + HV * dv)
+    fps = max(-(-layers * HV * head_bytes // frame_bytes), -(-log_bytes // frame_bytes))
+    conv_elems = layers * conv_dim * (W - 1)
+    cf = -(-conv_elems * item // frame_bytes)
+    n_payload = slots * fps
+    n_decay = slots
+    n_conv = slots * granules * cf
+    storage = (torch.randn(n_payload + n_decay + n_conv, frame_bytes // item, generator=g) * 0.1).to(dtype)
+    payload = _identity(slots, fps)
+    decay = torch.tensor([[n_payload + s, 0] for s in range(slots)], dtype=torch.int32)
+    conv = (n_payload + n_decay + torch.arange(slots * granules * cf).reshape(slots, granules, cf)).to(torch.int32)
+    return dict(storage=storage, payload=payload, decay=decay, conv=conv, frame_bytes=frame_bytes,
+                head_bytes=head_bytes, record=record, fps=fps, cf=cf, gen=g, dk=dk, dv=dv, H=H, HV=HV,
+                layers=layers, page=page, slots=slots, conv_dim=conv_dim, W=W, granules=granules)
+
+
+def test_logstate_conv_decode_equals_plain_conv_decode():
+    P = _decode_pool(11)
+    C, W, S, G = P["conv_dim"], P["W"], P["W"] - 1, P["granules"]
+    fe = P["frame_bytes"] // P["storage"].element_size()
+    g = P["gen"]
+    B = 3
+    x = torch.randn(B, C, generator=g)
+    weight = torch.randn(C, 1, W, generator=g) * 0.3
+    reads, rgran = torch.tensor([0, 3, 1]), torch.tensor([1, 0, 1])
+    writes, wgran = torch.tensor([2, 1, 3]), torch.tensor([1, 1, 0])
+    works = torch.tensor([0, 2, 1])
+    # the plain pool of (slot, granule) windows that the identity conv table lays out
+    base = P["slots"] * P["fps"] + P["slots"]
+    before = P["storage"].clone()
+    block = before[base:].reshape(P["slots"] * G, -1)[:, :P["layers"] * C * S].reshape(P["slots"] * G, P["layers"], C, S)
+    plain = block.clone()
+    y_ref = gdn.conv_decode(x, weight, plain, 1, reads * G + rgran, writes * G + wgran)
+    y = fr.conv_decode_logstate(x, weight, P["storage"], P["conv"], P["frame_bytes"], 1, reads, rgran, writes, wgran,
+                                works)
+    torch.testing.assert_close(y, y_ref, rtol=0, atol=0)
+    after = P["storage"][base:].reshape(P["slots"] * G, -1)[:, :P["layers"] * C * S].reshape(P["slots"] * G,
+                                                                                             P["layers"], C, S)
+    for b in range(B):
+        torch.testing.assert_close(after[int(writes[b]) * G + int(wgran[b]), 1], plain[int(writes[b]) * G + int(wgran[b]), 1],
+                                   rtol=0, atol=0)
+        torch.testing.assert_close(after[int(works[b]) * G, 1], plain[int(writes[b]) * G + int(wgran[b]), 1],
+                                   rtol=0, atol=0)
+    assert torch.equal(P["storage"][:base], before[:base])
+
+
+def _raw_step(g, B, H, HV, dk, dv):
+    q = torch.randn(B, 1, H, dk, generator=g)
+    k = torch.randn(B, 1, H, dk, generator=g)
+    v = torch.randn(B, 1, HV, dv, generator=g) * 0.5
+    a = torch.randn(B, 1, HV, generator=g)
+    bt = torch.randn(B, 1, HV, generator=g)
+    return q, k, v, a, bt
+
+
+def test_eager_logstate_step_equals_slotted_decode():
+    P = _decode_pool(12)
+    g = P["gen"]
+    B, H, HV, dk, dv = 2, P["H"], P["HV"], P["dk"], P["dv"]
+    A_log, dt_bias = torch.randn(HV, generator=g) * 0.3, torch.randn(HV, generator=g) * 0.3
+    q, k, v, a, bt = _raw_step(g, B, H, HV, dk, dv)
+    works, logs = torch.tensor([1, 3]), torch.tensor([0, 2])
+    payload = P["storage"][:P["slots"] * P["fps"]].clone()
+    pool = _as_pool(payload, P["slots"], P["layers"], HV, dk, dv, P["head_bytes"], 4).contiguous()
+    o_ref = gdn.fused_recurrent_to_slots(q, k, v, a, bt, A_log, dt_bias, pool, works, works, 1)
+    o = fr.fused_recurrent_to_logstate(q, k, v, a, bt, A_log, dt_bias, P["storage"], P["payload"], P["decay"],
+                                       P["frame_bytes"], P["head_bytes"], P["record"], works, logs,
+                                       torch.tensor([5, 9]), torch.tensor([0, 0]), layer=1, layers=P["layers"],
+                                       granularity=8, page_size=P["page"], eager=True)
+    torch.testing.assert_close(o, o_ref, rtol=0, atol=0)
+    got = fr.read_frame_states(P["storage"], P["payload"], works, 1, HV, dk, dv, P["frame_bytes"], P["head_bytes"])
+    torch.testing.assert_close(got, pool[works, 1], rtol=0, atol=0)
+
+
+def test_replayed_logstate_decode_equals_eager_decode():
+    """The replay form (state written every 16 tokens, the tokens since
+    rebuilt from the log) equals the eager recurrence over 40 steps: outputs,
+    and the work states once both have written them (after step 31)."""
+    T = 40
+    runs = {}
+    for eager in (True, False):
+        P = _decode_pool(13, page=64)
+        g = torch.Generator().manual_seed(14)
+        B, H, HV, dk, dv = 2, P["H"], P["HV"], P["dk"], P["dv"]
+        A_log, dt_bias = torch.randn(HV, generator=g) * 0.3, torch.randn(HV, generator=g) * 0.3
+        works, logs = torch.tensor([1, 3]), torch.tensor([0, 2])
+        outs, mid = [], None
+        for t in range(T):
+            q, k, v, a, bt = _raw_step(g, B, H, HV, dk, dv)
+            counts = torch.tensor([0, 0]) if eager else torch.tensor([t % 16] * B)
+            outs.append(fr.fused_recurrent_to_logstate(q, k, v, a, bt, A_log, dt_bias, P["storage"], P["payload"],
+                                                       P["decay"], P["frame_bytes"], P["head_bytes"], P["record"],
+                                                       works, logs, torch.tensor([t, t]), counts, layer=1,
+                                                       layers=P["layers"], granularity=8, page_size=P["page"],
+                                                       eager=eager))
+            if t == 31:
+                mid = fr.read_frame_states(P["storage"], P["payload"], works, 1, HV, dk, dv, P["frame_bytes"],
+                                           P["head_bytes"])
+        runs[eager] = (torch.cat(outs, 1), mid)
+    torch.testing.assert_close(runs[False][0], runs[True][0], rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(runs[False][1], runs[True][1], rtol=1e-5, atol=1e-5)
