@@ -167,6 +167,26 @@ int gdn_store_chunk_log(void* storage, const void* frames, int frames_dtype, int
                         int64_t num_layers, int64_t granularity, int64_t page_size, void* stream);
 
 /*
+ * LogState conv windows of a packed prefill: replaces the state stores of
+ * packed_causal_conv1d (kernel/linear_attention/packed_conv.py:53-133) with a
+ * PackedConvStateIO that carries granules and a conv frame table.  For each
+ * packed row t < cu[N] of sequence n, the raw window of the kernel_width - 1
+ * inputs ending at t (rows before the sequence start from history[n], [N, C,
+ * W-1]) goes to the snapshot (token_slots[t], token_granules[t]) when that
+ * slot is >= 0, and the last row's window also to granule 0 of
+ * final_slots[n] (when final_slots is non-NULL and the slot >= 0).
+ * Snapshot addressing as in gdn_conv_decode_logstate.  The conv output
+ * itself comes from gdn_packed_causal_conv1d (without state I/O).
+ */
+int gdn_conv_windows_logstate(const void* x, int64_t x_row_stride, int64_t x_col_stride, int dtype,
+                              const void* history, const void* cu_seqlens, int cu_dtype, int64_t num_seqs,
+                              int64_t total_tokens, int64_t channels, int kernel_width, void* storage,
+                              const void* conv_frames, int frames_dtype, int64_t num_granules,
+                              int64_t frames_per_granule, int64_t frame_bytes, int64_t num_frames, int64_t layer,
+                              const void* token_slots, int slots_dtype, const void* token_granules,
+                              int granules_dtype, const void* final_slots, int finals_dtype, void* stream);
+
+/*
  * LogState conv decode: replaces conv_decode (kernel/linear_attention/
  * conv_decode.py:293-352) with pool= (the conv snapshots of
  * cache/logstate/frame_pool.py in frames).  For sequence b the window of

@@ -60,6 +60,17 @@ __device__ __forceinline__ int64_t load_index(const void* p, int64_t i, int is64
   return is64 ? static_cast<const int64_t*>(p)[i] : static_cast<int64_t>(static_cast<const int32_t*>(p)[i]);
 }
 
+// Sequence of packed row t: the largest r < n with cu[r] <= t (cu is
+// non-decreasing with cu[0] = 0, so empty sequences are skipped).
+__device__ __forceinline__ int64_t find_sequence(const void* cu, int cu_is64, int64_t n, int64_t t) {
+  int64_t lo = 0, hi = n - 1;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) >> 1;
+    if (load_index(cu, mid, cu_is64) <= t) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
 // ---------------------------------------------------------------- math
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float exp_f(float x) { return __expf(x); }

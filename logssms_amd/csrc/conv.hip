@@ -17,16 +17,6 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kTile = 32;  // tokens per thread
 
-__device__ __forceinline__ int64_t find_sequence(const void* cu, int cu_is64, int64_t n, int64_t t) {
-  // largest r with cu[r] <= t (cu is non-decreasing, cu[0] = 0)
-  int64_t lo = 0, hi = n - 1;
-  while (lo < hi) {
-    const int64_t mid = (lo + hi + 1) >> 1;
-    if (load_index(cu, mid, cu_is64) <= t) lo = mid; else hi = mid - 1;
-  }
-  return lo;
-}
-
 // End of the packed tokens, cu[N]: rows at or past it (the padding of a
 // fixed-capacity input) belong to no sequence and are neither read nor written.
 __device__ __forceinline__ int64_t tile_end(const void* cu, int cu_is64, int64_t n, int64_t rows, int64_t t0,

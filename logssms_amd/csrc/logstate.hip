@@ -182,6 +182,52 @@ __global__ __launch_bounds__(kDecodeThreads) void conv_decode_frames_kernel(Conv
   }
 }
 
+// ---- LogState prefill conv windows (packed_conv.py:53-133 with LOGSTATE):
+// the raw window ending at packed row t goes to (token_slots[t],
+// token_granules[t]) when that slot is >= 0, and a sequence's last window to
+// granule 0 of final_slots[seq]; window rows before the sequence start come
+// from history [N, C, W-1].
+struct ConvWindowParams {
+  const void* x;
+  int64_t xr, xc;
+  const void* history;
+  const void* cu; int cu_is64;
+  int64_t N, T, C;
+  int S;
+  void* storage;
+  const void* table; int table_is64;
+  int64_t granules, cf, fe, num_frames, layer;
+  const void* slots; int slots_is64;
+  const void* gran; int gran_is64;
+  const void* finals; int finals_is64;
+};
+
+// grid (T, channel blocks)
+template <class T>
+__global__ __launch_bounds__(kDecodeThreads) void conv_windows_frames_kernel(ConvWindowParams p) {
+  const int64_t t = blockIdx.x;
+  const int64_t ch = static_cast<int64_t>(blockIdx.y) * kDecodeThreads + threadIdx.x;
+  if (ch >= p.C || t >= load_index(p.cu, p.N, p.cu_is64)) return;
+  const int64_t slot = load_index(p.slots, t, p.slots_is64);
+  const int64_t n = find_sequence(p.cu, p.cu_is64, p.N, t);
+  const int64_t begin = load_index(p.cu, n, p.cu_is64), end = load_index(p.cu, n + 1, p.cu_is64);
+  const int64_t fin = p.finals && t == end - 1 ? load_index(p.finals, n, p.finals_is64) : -1;
+  if (slot < 0 && fin < 0) return;
+  const int64_t granule = slot >= 0 ? load_index(p.gran, t, p.gran_is64) : 0;
+  const T* x = static_cast<const T*>(p.x);
+  const T* hist = static_cast<const T*>(p.history) + (n * p.C + ch) * p.S;
+  T* st = static_cast<T*>(p.storage);
+  const int64_t e0 = p.layer * p.C * p.S + ch * p.S;
+  for (int j = 0; j < p.S; ++j) {
+    const int64_t pos = t - (p.S - 1) + j;
+    const T v = pos >= begin ? x[pos * p.xr + ch * p.xc] : hist[pos - begin + p.S];
+    T* d0 = conv_element(st, p.table, p.table_is64, slot, granule, e0 + j, p.granules, p.cf, p.fe, p.num_frames);
+    T* d1 = conv_element(st, p.table, p.table_is64, fin, 0, e0 + j, p.granules, p.cf, p.fe, p.num_frames);
+    if (d0) *d0 = v;
+    if (d1) *d1 = v;
+  }
+}
+
 struct LogDecodeParams {
   const void* q; const void* k; const void* v;
   const void* gate; int64_t gate_b, gate_h; int gate_dtype;
@@ -613,4 +659,51 @@ extern "C" int gdn_recurrent_logstate(
   if (dk == 64 && dv == 128) return launch(I64{}, I128{});
   set_error("gdn_recurrent_logstate: unsupported head dims dk=%lld dv=%lld", (long long)dk, (long long)dv);
   return GDN_ERR_UNSUPPORTED;
+}
+
+extern "C" int gdn_conv_windows_logstate(const void* x, int64_t x_row_stride, int64_t x_col_stride, int dtype,
+                                         const void* history, const void* cu_seqlens, int cu_dtype, int64_t num_seqs,
+                                         int64_t total_tokens, int64_t channels, int kernel_width, void* storage,
+                                         const void* conv_frames, int frames_dtype, int64_t num_granules,
+                                         int64_t frames_per_granule, int64_t frame_bytes, int64_t num_frames,
+                                         int64_t layer, const void* token_slots, int slots_dtype,
+                                         const void* token_granules, int granules_dtype, const void* final_slots,
+                                         int finals_dtype, void* stream) {
+  using namespace gdn;
+  GDN_REQUIRE(num_seqs >= 1 && total_tokens >= 0 && channels > 0 && layer >= 0,
+              "gdn_conv_windows_logstate: bad sizes");
+  if (total_tokens == 0) return GDN_OK;
+  GDN_REQUIRE(kernel_width >= 2 && kernel_width <= 8, "gdn_conv_windows_logstate: kernel width %d not in [2, 8]",
+              kernel_width);
+  GDN_REQUIRE(x && history && cu_seqlens && storage && conv_frames && token_slots && token_granules,
+              "gdn_conv_windows_logstate: null input");
+  GDN_REQUIRE(num_granules > 0 && frames_per_granule > 0 && num_frames > 0 && frame_bytes > 0 && frame_bytes % 2 == 0,
+              "gdn_conv_windows_logstate: bad conv frame table");
+  const int64_t fe = frame_bytes / 2;
+  const int64_t span = (layer + 1) * channels * (kernel_width - 1);
+  GDN_REQUIRE(frames_per_granule == 1 ? span <= fe : span <= frames_per_granule * fe,
+              "gdn_conv_windows_logstate: layer %lld's conv windows exceed the snapshot's frames", (long long)layer);
+  GDN_REQUIRE(total_tokens <= 0x7fffffff && (channels + kDecodeThreads - 1) / kDecodeThreads <= 65535,
+              "gdn_conv_windows_logstate: grid too large");
+  ConvWindowParams p{};
+  p.x = x; p.xr = x_row_stride; p.xc = x_col_stride; p.history = history;
+  p.cu = cu_seqlens; p.cu_is64 = cu_dtype == GDN_I64;
+  p.N = num_seqs; p.T = total_tokens; p.C = channels; p.S = kernel_width - 1;
+  p.storage = storage; p.table = conv_frames; p.table_is64 = frames_dtype == GDN_I64;
+  p.granules = num_granules; p.cf = frames_per_granule; p.fe = fe; p.num_frames = num_frames; p.layer = layer;
+  p.slots = token_slots; p.slots_is64 = slots_dtype == GDN_I64;
+  p.gran = token_granules; p.gran_is64 = granules_dtype == GDN_I64;
+  p.finals = final_slots; p.finals_is64 = finals_dtype == GDN_I64;
+  const dim3 grid(static_cast<unsigned>(total_tokens), static_cast<unsigned>((channels + kDecodeThreads - 1) /
+                                                                            kDecodeThreads));
+  auto s = static_cast<hipStream_t>(stream);
+  if (dtype == GDN_BF16) {
+    hipLaunchKernelGGL(conv_windows_frames_kernel<bf16>, grid, dim3(kDecodeThreads), 0, s, p);
+  } else if (dtype == GDN_F16) {
+    hipLaunchKernelGGL(conv_windows_frames_kernel<f16>, grid, dim3(kDecodeThreads), 0, s, p);
+  } else {
+    set_error("gdn_conv_windows_logstate: unsupported dtype %d (bf16 or f16)", dtype);
+    return GDN_ERR_UNSUPPORTED;
+  }
+  return GDN_LAUNCH_CHECK("gdn_conv_windows_logstate launch");
 }

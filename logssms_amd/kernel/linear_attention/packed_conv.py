@@ -13,9 +13,11 @@ from ... import _lib
 
 @dataclass(frozen=True)
 class PackedConvStateIO:
-    """packed_conv.py:11-20.  Standard slot mode only: ``granules``,
-    ``frame_table`` and ``frame_bytes`` belong to the LogState cache and raise
-    ``NotImplementedError`` when set."""
+    """packed_conv.py:11-20.  Standard mode: ``storage [slots, layers, C,
+    W-1]`` indexed by ``slots``.  LogState mode (``frame_table`` set): the
+    windows go to the (slot, granule) conv snapshots of the frame storage
+    ``[num_frames, frame_bytes / itemsize]`` in the io dtype, with
+    ``frame_table [slots, granules, frames per snapshot]``."""
 
     storage: torch.Tensor
     slots: torch.Tensor
@@ -63,9 +65,10 @@ def packed_causal_conv1d(
     assert history.shape == (len(cu_seqlens) - 1, channels, state_len)
     assert weight.shape == (channels, 1, kernel_size)
     direct = state_io is not None
+    if direct and state_io.frame_table is not None:
+        return _packed_conv_logstate(x, weight, history, cu_seqlens, bias, state_io, input_boundaries, input_scales)
     if direct:
-        if state_io.frame_table is not None or state_io.granules is not None:
-            raise NotImplementedError("LogState conv frames are not supported by the MI355X backend")
+        assert state_io.granules is None, "conv granules need a frame table"
         assert state_io.slots.shape == (total_tokens,)
         assert state_io.storage.dtype == x.dtype and state_io.storage.device == x.device
         assert state_io.storage.ndim == 4 and state_io.storage.shape[2:] == (channels, state_len)
@@ -94,6 +97,42 @@ def packed_causal_conv1d(
         _lib.index_code(state_io.slots) if direct else 0,
         _lib.ptr(final), _lib.index_code(final) if final is not None else 0,
         *scale_args, _lib.stream_of(x),
+    )
+    return output
+
+
+def _packed_conv_logstate(x, weight, history, cu_seqlens, bias, state_io, input_boundaries, input_scales):
+    """LogState mode of ``packed_causal_conv1d`` (``packed_conv.py:160-189``):
+    the conv itself, then the windows through the conv frame table
+    (``gdn_conv_windows_logstate``)."""
+    if input_boundaries is not None or tuple(input_scales) != (1.0, 1.0, 1.0):
+        raise NotImplementedError("input scales are not supported with LogState conv frames")
+    total_tokens, channels = x.shape
+    kernel_size = weight.shape[-1]
+    table = state_io.frame_table
+    assert state_io.granules is not None and state_io.granules.shape == (total_tokens,)
+    assert state_io.slots.shape == (total_tokens,)
+    assert state_io.frame_bytes % x.element_size() == 0
+    assert table.ndim == 3 and table.is_contiguous()
+    storage = state_io.storage
+    assert storage.dtype == x.dtype and storage.device == x.device and storage.is_contiguous()
+    if state_io.final_slots is not None:
+        assert state_io.final_slots.shape == (len(cu_seqlens) - 1,)
+    output = packed_causal_conv1d(x, weight, history, cu_seqlens, None, bias)
+    if total_tokens == 0:
+        return output
+    history = history.to(x.dtype).contiguous()
+    slots, granules = state_io.slots.contiguous(), state_io.granules.contiguous()
+    final = state_io.final_slots.contiguous() if state_io.final_slots is not None else None
+    num_frames = storage.numel() * storage.element_size() // state_io.frame_bytes
+    _lib.call(
+        "gdn_conv_windows_logstate",
+        x.data_ptr(), x.stride(0), x.stride(1), _lib.dtype_code(x.dtype), history.data_ptr(),
+        cu_seqlens.data_ptr(), _lib.index_code(cu_seqlens), len(cu_seqlens) - 1, total_tokens, channels,
+        kernel_size, storage.data_ptr(), table.data_ptr(), _lib.index_code(table), table.shape[1], table.shape[2],
+        state_io.frame_bytes, num_frames, state_io.layer, slots.data_ptr(), _lib.index_code(slots),
+        granules.data_ptr(), _lib.index_code(granules), _lib.ptr(final),
+        _lib.index_code(final) if final is not None else 0, _lib.stream_of(x),
     )
     return output
 

@@ -308,3 +308,62 @@ def fused_recurrent_to_logstate(query, key, value, gate, beta, A_log, dt_bias, s
         if w >= 0 and (eager or (pos + 1) % window == 0):
             write_frame_states(storage, payload_frames, [w], layer, new_state[None], frame_bytes, head_bytes)
     return out
+
+
+def read_conv_windows(storage, conv_frames, frame_bytes, slots, granules, layer, C, S):
+    """The pool's ``read_conv`` (``cache/logstate/frame_pool.py:229-257``):
+    windows [len(slots), C, S] of the (slot, granule) snapshots; a negative
+    slot reads zeros."""
+    slots = torch.as_tensor(slots, dtype=torch.int64)
+    granules = torch.as_tensor(granules, dtype=torch.int64)
+    out = torch.zeros(len(slots), C, S, dtype=storage.dtype)
+    keep = slots >= 0
+    if keep.any():
+        idx = conv_element_index(conv_frames, slots[keep], granules[keep], layer, C, S,
+                                 frame_bytes // storage.element_size())
+        out[keep] = storage.reshape(-1)[idx].view(-1, C, S)
+    return out
+
+
+def forward_prefill_logstate(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, storage, payload_frames,
+                             decay_frames, conv_frames, frame_bytes, head_bytes, record_bytes, *, layer, layers,
+                             granularity, page_size, cu_seqlens, work_slots, conv_read_slots, conv_read_granules,
+                             conv_token_slots, conv_token_granules, chunk_write_slots, log_write_slots,
+                             token_offsets, num_k_heads, head_k_dim, num_v_heads, head_v_dim, dtype=torch.float32):
+    """The LogState prefill (``layers/linear_attention_backend/gdn_logstate.py:85-172``):
+    conv history from the (read slot, read granule) snapshots, packed conv
+    with windows to (``conv_token_slots``, ``conv_token_granules``) and each
+    sequence's last window to granule 0 of its work slot, ``prepare_gdn``, the
+    chunked rule from and to the work slots with checkpoints every
+    ``granularity`` tokens, and the token log.  ``storage`` (the io dtype) is
+    modified in place; returns o [T, HV, dv]."""
+    from .gdn import packed_causal_conv1d, prepare_gdn, split_qkv
+    N = len(cu_seqlens) - 1
+    C = mixed_qkv.shape[1]
+    S = conv_weight.shape[-1] - 1
+    fe = frame_bytes // storage.element_size()
+    flat = storage.view(-1)
+    history = read_conv_windows(storage, conv_frames, frame_bytes, conv_read_slots, conv_read_granules, layer, C, S)
+    cu = [int(v) for v in cu_seqlens]
+    token_slots = [int(x) for x in conv_token_slots]
+    rows = sorted({t for t, s in enumerate(token_slots) if s >= 0} | {cu[n + 1] - 1 for n in range(N)
+                                                                      if cu[n + 1] > cu[n]})
+    y, windows = packed_causal_conv1d(mixed_qkv, conv_weight, history, cu_seqlens, window_rows=rows)
+    where = {t: i for i, t in enumerate(rows)}
+    for t, s in enumerate(token_slots):
+        if s >= 0:
+            idx = conv_element_index(conv_frames, [s], [int(conv_token_granules[t])], layer, C, S, fe)
+            flat[idx.reshape(-1)] = windows[where[t]].reshape(-1).to(storage.dtype)
+    for n in range(N):
+        if cu[n + 1] > cu[n] and int(work_slots[n]) >= 0:
+            idx = conv_element_index(conv_frames, [int(work_slots[n])], [0], layer, C, S, fe)
+            flat[idx.reshape(-1)] = windows[where[cu[n + 1] - 1]].reshape(-1).to(storage.dtype)
+    q, k, v = split_qkv(y[None], num_k_heads, head_k_dim, num_v_heads, head_v_dim)
+    q, k, v, g, b = prepare_gdn(q, k, v, gate[None], beta[None], A_log, dt_bias)
+    o, v_new = chunk_gated_delta_rule_to_frames(q, k, v, g, b, storage, payload_frames, frame_bytes, head_bytes,
+                                                work_slots, chunk_write_slots, cu_seqlens, layer=layer,
+                                                final_write_slots=work_slots, chunk_size=granularity, dtype=dtype)
+    store_chunk_log(storage, payload_frames, frame_bytes, log_write_slots, token_offsets, v_new[0], k[0], g[0],
+                    decay_frames, record_bytes, layer=layer, layers=layers, granularity=granularity,
+                    page_size=page_size, key_heads=num_k_heads)
+    return o[0]

@@ -336,3 +336,121 @@ def test_logstate_decode_steps(eager):
                                                                 for t in (0, T - 1)]:
         idx = ofr.conv_element_index(conv, [slot], [gr], layer, conv_dim, W - 1, fe)
         assert torch.equal(host.reshape(-1)[idx].view(torch.int16), expected.reshape(-1)[idx].view(torch.int16))
+
+
+@pytest.mark.parametrize("eager", [False, True])
+def test_logstate_backend_prefill_then_decode(eager):
+    """GatedDeltaLogStateBackend (gdn_logstate.py:18-224): a packed prefill of
+    two sequences from their work slots (conv history, initial state), with
+    conv snapshots at granule ends, two mid-sequence checkpoints and the token
+    log, then 18 decode steps each, replaying the log between write-backs;
+    against the oracle's LogState prefill and decode."""
+    from types import SimpleNamespace
+    from logssms_amd.core import Batch
+    from logssms_amd.layers import GatedDeltaLogStateBackend, LogStateLinearAttnMetadata
+    from logssms_amd.layers.linear_attention_backend import PackedLinearIndices
+    g = gen(101 + int(eager))
+    H, HV, dk, dv, layers, layer, page, gran, W = 2, 4, 128, 128, 2, 1, 64, 16, 4
+    C = 2 * H * dk + HV * dv
+    frame_bytes, head_bytes = 65536, 32768
+    slots = 8  # 0, 1 work slots; 2, 3, 4 log pages; 5, 6 checkpoints; 7 spare
+    storage, payload, decay, conv, record, pool = _decode_pool(g, slots, H, HV, dk, dv, layers, page, gran, C, W,
+                                                               frame_bytes, head_bytes)
+    pool.layout.num_key_heads = H
+    fe = frame_bytes // 2
+
+    def read_conv(s, gr, lay):
+        idx = ofr.conv_element_index(conv, s.cpu(), gr.cpu(), lay, C, W - 1, fe).to(DEV)
+        return pool.storage.view(torch.bfloat16).reshape(-1)[idx].view(len(s), C, W - 1)
+
+    pool.read_conv = read_conv
+    dev_u8 = storage.view(torch.uint8).to(DEV)
+    pool.storage = dev_u8
+    pool.payload_frame_table, pool.decay_frame_table, pool.conv_frame_table = payload.to(DEV), decay.to(DEV), conv.to(DEV)
+    backend = GatedDeltaLogStateBackend(ctx=SimpleNamespace(linear_state=pool), enable_eager_state=eager)
+    cfg = SimpleNamespace(key_dim=H * dk, value_dim=HV * dv, head_k_dim=dk, head_v_dim=dv, layer_idx=layer,
+                          state_len=W - 1, conv_dim=C, num_k_heads=H, num_v_heads=HV)
+    weight = (torch.randn(C, 1, W, generator=g) * 0.3).to(torch.bfloat16)
+    A_log, dt_bias = torch.randn(HV, generator=g) * 0.3, torch.randn(HV, generator=g) * 0.3
+    expected = storage.clone()
+
+    # ---- prefill
+    lengths = [100, 37]
+    cu = [0, 100, 137]
+    T = cu[-1]
+    works = torch.tensor([0, 1])
+    pages = {0: [2, 3], 1: [4]}  # log slot of each page
+    log_slots, offsets, tok_slots, tok_gran = [], [], [], []
+    for n, length in enumerate(lengths):
+        for pos in range(length):
+            ls = pages[n][pos // page]
+            log_slots.append(ls)
+            offsets.append(pos % page)
+            end_of_granule = (pos % page) % gran == gran - 1
+            tok_slots.append(ls if end_of_granule else -1)
+            tok_gran.append((pos % page) // gran)
+    n_int = sum(-(-n // gran) for n in lengths)
+    chunk_writes = torch.full((n_int,), -1)
+    chunk_writes[2], chunk_writes[7 + 1] = 5, 6
+    mixed = torch.randn(T, C, generator=g).to(torch.bfloat16)
+    gate, beta = torch.randn(T, HV, generator=g).to(torch.bfloat16), torch.randn(T, HV, generator=g).to(torch.bfloat16)
+    o_ref = ofr.forward_prefill_logstate(mixed, gate, beta, weight, A_log, dt_bias, expected, payload, decay, conv,
+                                         frame_bytes, head_bytes, record, layer=layer, layers=layers,
+                                         granularity=gran, page_size=page, cu_seqlens=cu, work_slots=works,
+                                         conv_read_slots=works, conv_read_granules=[0, 0],
+                                         conv_token_slots=torch.tensor(tok_slots),
+                                         conv_token_granules=torch.tensor(tok_gran), chunk_write_slots=chunk_writes,
+                                         log_write_slots=torch.tensor(log_slots), token_offsets=torch.tensor(offsets),
+                                         num_k_heads=H, head_k_dim=dk, num_v_heads=HV, head_v_dim=dv)
+    meta = LogStateLinearAttnMetadata(
+        phase="prefill", work_slots=works.to(DEV), log_slots=torch.tensor(log_slots, device=DEV),
+        token_offsets=torch.tensor(offsets, device=DEV), conv_read_slots=works.to(DEV),
+        conv_read_granules=torch.zeros(2, dtype=torch.int64, device=DEV),
+        replay_counts=torch.zeros(2, dtype=torch.int64, device=DEV), cu_seqlens=torch.tensor(cu, device=DEV),
+        prefill_indices=PackedLinearIndices.from_lengths(lengths, DEV, gran), chunk_write_slots=chunk_writes.to(DEV),
+        log_write_slots=torch.tensor(log_slots, device=DEV), conv_token_slots=torch.tensor(tok_slots, device=DEV),
+        conv_token_granules=torch.tensor(tok_gran, device=DEV))
+    print(f"LogState backend, eager={eager}: prefill {lengths}", flush=True)
+    o = backend.forward(mixed.to(DEV), gate.to(DEV), beta.to(DEV), weight.to(DEV), A_log.to(DEV), dt_bias.to(DEV),
+                        cfg, Batch(reqs=[None, None], phase="prefill", linear_attn_metadata=meta))
+    torch.cuda.synchronize()
+    _report("prefill out", o, o_ref)
+    assert_bf16_close(o, o_ref)
+
+    # ---- decode: 18 steps; the replay count is the tokens logged since the last write-back
+    pos = torch.tensor(lengths)
+    since = [0, 0]
+    for step in range(18):
+        off = pos % page
+        ls = torch.tensor([pages[n][int(pos[n]) // page] for n in range(2)])
+        counts = torch.tensor([0, 0]) if eager else torch.tensor(since)
+        x = torch.randn(2, C, generator=g).to(torch.bfloat16)
+        a, bt = torch.randn(2, HV, generator=g).to(torch.bfloat16), torch.randn(2, HV, generator=g).to(torch.bfloat16)
+        y = ofr.conv_decode_logstate(x, weight, expected, conv, frame_bytes, layer, works, torch.zeros(2, dtype=torch.int64),
+                                     ls, off // gran, works)
+        q, k, v = (y[:, :H * dk].reshape(2, 1, H, dk), y[:, H * dk:2 * H * dk].reshape(2, 1, H, dk),
+                   y[:, 2 * H * dk:].reshape(2, 1, HV, dv))
+        o_ref = ofr.fused_recurrent_to_logstate(q, k, v, a[:, None], bt[:, None], A_log, dt_bias, expected, payload,
+                                                decay, frame_bytes, head_bytes, record, works, ls, off, counts,
+                                                layer=layer, layers=layers, granularity=gran, page_size=page,
+                                                eager=eager)
+        meta = LogStateLinearAttnMetadata(
+            phase="decode", work_slots=works.to(DEV), log_slots=ls.to(DEV), token_offsets=off.to(DEV),
+            conv_read_slots=works.to(DEV), conv_read_granules=torch.zeros(2, dtype=torch.int64, device=DEV),
+            replay_counts=counts.to(DEV))
+        o = backend.forward(x.to(DEV), a.to(DEV), bt.to(DEV), weight.to(DEV), A_log.to(DEV), dt_bias.to(DEV), cfg,
+                            Batch(reqs=[None, None], phase="decode", linear_attn_metadata=meta))
+        assert_bf16_close(o, o_ref[:, 0])
+        since = [0 if (int(off[n]) + 1) % 16 == 0 else since[n] + 1 for n in range(2)]
+        pos = pos + 1
+    torch.cuda.synchronize()
+    _report("decode out (last step)", o, o_ref[:, 0])
+    host = dev_u8.cpu().view(torch.bfloat16).reshape(storage.shape)
+    for name, s in (("work", works.tolist()), ("checkpoints", [5, 6])):
+        got = ofr.read_frame_states(host, payload, s, layer, HV, dk, dv, frame_bytes, head_bytes)
+        want = ofr.read_frame_states(expected, payload, s, layer, HV, dk, dv, frame_bytes, head_bytes)
+        _report(f"{name} states", got, want)
+        assert_state16_close(got, want)
+    for slot, gr in [(0, 0), (1, 0), (2, 3), (3, 1), (4, 1)]:
+        idx = ofr.conv_element_index(conv, [slot], [gr], layer, C, W - 1, fe)
+        assert torch.equal(host.reshape(-1)[idx].view(torch.int16), expected.reshape(-1)[idx].view(torch.int16))

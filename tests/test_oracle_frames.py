@@ -316,3 +316,52 @@ def test_replayed_logstate_decode_equals_eager_decode():
         runs[eager] = (torch.cat(outs, 1), mid)
     torch.testing.assert_close(runs[False][0], runs[True][0], rtol=1e-5, atol=1e-5)
     torch.testing.assert_close(runs[False][1], runs[True][1], rtol=1e-5, atol=1e-5)
+
+
+def test_logstate_prefill_equals_the_plain_pipeline():
+    """Identity tables: the LogState prefill's output, work-slot states and
+    conv windows equal the plain pipeline (packed conv from the same history,
+    prepare, the chunked rule at the same granularity into a plain pool)."""
+    H, HV, dk, dv, W = 2, 4, 8, 8, 4
+    C = 2 * H * dk + HV * dv
+    P = _decode_pool(15, dtype=torch.float32, page=32, conv_dim=C, H=H, HV=HV, dk=dk, dv=dv, W=W)
+    g = P["gen"]
+    layers, G, S, gran = P["layers"], P["granules"], W - 1, 16
+    lengths, cu = [21, 9], [0, 21, 30]
+    T = cu[-1]
+    mixed = torch.randn(T, C, generator=g)
+    weight = torch.randn(C, 1, W, generator=g) * 0.3
+    gate, beta = torch.randn(T, HV, generator=g), torch.randn(T, HV, generator=g)
+    A_log, dt_bias = torch.randn(HV, generator=g) * 0.3, torch.randn(HV, generator=g) * 0.3
+    works = torch.tensor([1, 3])
+    conv_token = torch.full((T,), -1)
+    conv_token[15], conv_token[26] = 0, 2
+    conv_gran = torch.zeros(T, dtype=torch.int64)
+    conv_gran[15] = 1
+    chunk_writes = torch.full((sum(-(-n // gran) for n in lengths),), -1)
+    logs = torch.tensor([0] * 21 + [2] * 9)
+    offsets = torch.tensor(list(range(21)) + list(range(9)))
+    storage = P["storage"]
+    history = fr.read_conv_windows(storage, P["conv"], P["frame_bytes"], works, [0, 0], 1, C, S)
+    y, win = gdn.packed_causal_conv1d(mixed, weight, history, cu, window_rows=[15, 26, 20, 29])
+    q, k, v = gdn.split_qkv(y[None], H, dk, HV, dv)
+    q, k, v, gg, bb = gdn.prepare_gdn(q, k, v, gate[None], beta[None], A_log, dt_bias)
+    pool = _as_pool(storage[:P["slots"] * P["fps"]].clone(), P["slots"], layers, HV, dk, dv, P["head_bytes"],
+                    4).contiguous()
+    o_ref, _ = gdn.chunk_gated_delta_rule_to_cache(q, k, v, gg, bb, pool, works, chunk_writes, cu, layer=1,
+                                                   final_write_slots=works, chunk_size=gran)
+    o = fr.forward_prefill_logstate(mixed, gate, beta, weight, A_log, dt_bias, storage, P["payload"], P["decay"],
+                                    P["conv"], P["frame_bytes"], P["head_bytes"], P["record"], layer=1,
+                                    layers=layers, granularity=gran, page_size=P["page"], cu_seqlens=cu,
+                                    work_slots=works, conv_read_slots=works, conv_read_granules=[0, 0],
+                                    conv_token_slots=conv_token, conv_token_granules=conv_gran,
+                                    chunk_write_slots=chunk_writes, log_write_slots=logs, token_offsets=offsets,
+                                    num_k_heads=H, head_k_dim=dk, num_v_heads=HV, head_v_dim=dv)
+    torch.testing.assert_close(o, o_ref[0], rtol=0, atol=0)
+    got = fr.read_frame_states(storage, P["payload"], works, 1, HV, dk, dv, P["frame_bytes"], P["head_bytes"])
+    torch.testing.assert_close(got, pool[works, 1], rtol=0, atol=0)
+    # windows: token 15 -> (slot 0, granule 1), token 26 -> (2, 0), each last token -> its work slot's granule 0
+    base = P["slots"] * P["fps"] + P["slots"]
+    after = storage[base:].reshape(P["slots"] * G, -1)[:, :layers * C * S].reshape(P["slots"] * G, layers, C, S)
+    for (slot, gr), w in zip([(0, 1), (2, 0), (1, 0), (3, 0)], win):
+        torch.testing.assert_close(after[slot * G + gr, 1], w, rtol=0, atol=0)
