@@ -241,6 +241,36 @@ int gdn_recurrent_logstate(const void* q, const void* k, const void* v, int io_d
                            void* out, float scale, void* stream);
 
 /*
+ * LogState state reconstruction: replaces restore_log_state_chains
+ * (kernel/linear_attention/logstate.py:59-88 -> csrc/jit/logstate_construction.cu
+ * restore).  Task i: the state of base_slots[i] (< 0: zero) for every layer
+ * and value head, then for each segment j in [segment_offsets[i],
+ * segment_offsets[i+1]) the tokens at positions log_begins[j] ..
+ * log_ends[j] - 1 of log slot log_slots[j] in order, S <- e^g S + k v'^T
+ * (the log layout and decay records of gdn_store_chunk_log, key_heads log
+ * key heads); the result goes to output_slots[i].  Slot states use the frame
+ * layout of gdn_chunk_gated_delta_rule; dtype bf16 or f16.  Outputs must not
+ * be read by another task of the same call.
+ */
+int gdn_logstate_restore(void* storage, const void* payload_frames, int frames_dtype, int64_t frames_per_slot,
+                         int64_t frame_bytes, int64_t head_bytes, int64_t num_frames, const void* decay_frames,
+                         int decay_dtype, int64_t decay_record_bytes, int64_t num_layers, int64_t HV,
+                         int64_t key_heads, int64_t dk, int64_t dv, int64_t granularity, int64_t page_size, int dtype,
+                         const int32_t* base_slots, const int32_t* segment_offsets, const int32_t* log_slots,
+                         const int32_t* log_begins, const int32_t* log_ends, const int32_t* output_slots,
+                         int64_t num_tasks, void* stream);
+
+/*
+ * LogState state copy: replaces copy_states (kernel/linear_attention/logstate.py:118-128
+ * -> logstate_construction.cu copy): the states of every layer and value
+ * head of sources[i] to destinations[i].
+ */
+int gdn_logstate_copy_states(void* storage, const void* payload_frames, int frames_dtype, int64_t frames_per_slot,
+                             int64_t frame_bytes, int64_t head_bytes, int64_t num_frames, int64_t num_layers,
+                             int64_t HV, int64_t dk, int64_t dv, int dtype, const int32_t* sources,
+                             const int32_t* destinations, int64_t count, void* stream);
+
+/*
  * The GDN prefill of one layer (layers/linear_attention_backend/gdn.py:100-150:
  * history gather, packed_causal_conv1d, split, prepare_gdn,
  * chunk_gated_delta_rule_to_cache) as three launches whose results equal

@@ -484,6 +484,162 @@ __global__ __launch_bounds__(kDecodeThreads) void logstate_decode_kernel(LogDeco
   }
 }
 
+// ---- restore / copy of LogState slot states (kernel/linear_attention/logstate.py:59-128)
+struct RestoreParams {
+  char* storage;
+  const void* frames; int frames_is64;
+  int64_t fps, frame_bytes, head_bytes, num_frames;
+  const void* decay; int decay_is64;
+  int64_t record_bytes;
+  int64_t layers, HV, KH, gran, page;
+  const int32_t* base;      // [tasks], -1: zero state
+  const int32_t* offsets;   // [tasks + 1] into the segments
+  const int32_t* seg_slots; // [segments] log slot
+  const int32_t* seg_begin; // [segments] first position
+  const int32_t* seg_end;   // [segments] end position
+  const int32_t* output;    // [tasks]
+};
+
+// State row of (slot, layer, head) in a frame storage (the layout of
+// gdn_chunk_gated_delta_rule's frame tables), or null.
+template <class T>
+__device__ __forceinline__ T* slot_row(const RestoreParams& p, int64_t s, int64_t layer, int64_t h, int64_t row,
+                                       int DV) {
+  if (s < 0) return nullptr;
+  const int64_t x = (layer * p.HV + h) * p.head_bytes + row * DV * static_cast<int64_t>(sizeof(T));
+  const int64_t fr = load_index(p.frames, s * p.fps + x / p.frame_bytes, p.frames_is64);
+  if (fr < 0 || fr >= p.num_frames) return nullptr;
+  return reinterpret_cast<T*>(p.storage + fr * p.frame_bytes + x % p.frame_bytes);
+}
+
+template <class T>
+__device__ __forceinline__ const T* restore_log(const RestoreParams& p, int64_t slot, int64_t layer, int64_t pos,
+                                                int64_t index, int64_t col, bool value, int DK, int DV) {
+  const int64_t key_size = p.gran * p.KH * DK;
+  const int64_t layer_size = key_size + p.gran * p.HV * DV;
+  const int64_t elem = (pos / p.gran * p.layers + layer) * layer_size + (value ? key_size : 0) +
+                       (index * p.gran + pos % p.gran) * (value ? DV : DK) + col;
+  const int64_t byte = 2 * elem;
+  const int64_t fr = load_index(p.frames, slot * p.fps + byte / p.frame_bytes, p.frames_is64);
+  if (fr < 0 || fr >= p.num_frames) return nullptr;
+  return reinterpret_cast<const T*>(p.storage + fr * p.frame_bytes + byte % p.frame_bytes);
+}
+
+// grid (tasks x layers x HV): the state of the task's base slot (or zero),
+// then each segment of logged tokens t = b .. e-1 in one step,
+// S <- e^{sum_t g_t} S + sum_t k_t (e^{sum_{j>t} g_j} v'_t)^T with the scaled
+// v' rounded to the state dtype (logstate_construction.cuh:329-393), taken
+// 16 tokens at a time; written to the output slot.
+template <int DK, int DV, class T>
+__global__ __launch_bounds__(kDecodeThreads) void restore_kernel(RestoreParams p) {
+  constexpr int CG = DV / 4, RG = kDecodeThreads / CG, RPT = DK / RG;
+  static_assert(RPT >= 1 && DK % RG == 0, "state split");
+  const int64_t task = blockIdx.x / (p.layers * p.HV);
+  const int64_t layer = (blockIdx.x / p.HV) % p.layers;
+  const int64_t h = blockIdx.x % p.HV;
+  const int64_t kh = h / (p.HV / p.KH);
+  const int tid = threadIdx.x, c0 = 4 * (tid % CG), r0 = (tid / CG) * RPT;
+  __shared__ float s_keys[kReplayWindow][DK];
+  __shared__ float s_vals[kReplayWindow][DV];
+  __shared__ float s_suffix[kReplayWindow];
+  __shared__ float s_part[kDecodeThreads / 64];
+  __shared__ float s_rest;
+  float S[RPT][4];
+  const int64_t base = p.base[task];
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const T* row = slot_row<T>(p, base, layer, h, r0 + r, DV);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) S[r][c] = row ? to_f32(row[c0 + c]) : 0.f;
+  }
+  for (int64_t seg = p.offsets[task]; seg < p.offsets[task + 1]; ++seg) {
+    const int64_t ls = p.seg_slots[seg];
+    int64_t fr = -1, ri = -1;
+    if (ls >= 0) {
+      fr = load_index(p.decay, 2 * ls, p.decay_is64);
+      ri = load_index(p.decay, 2 * ls + 1, p.decay_is64);
+    }
+    const bool ok = fr >= 0 && fr < p.num_frames && ri >= 0 && (ri + 1) * p.record_bytes <= p.frame_bytes;
+    const int64_t begin = p.seg_begin[seg] < 0 ? 0 : p.seg_begin[seg];
+    const int64_t end = p.seg_end[seg] < p.page ? p.seg_end[seg] : p.page;
+    if (!ok || begin >= end) continue;
+    const float* rec =
+        reinterpret_cast<const float*>(p.storage + fr * p.frame_bytes + ri * p.record_bytes) + layer * p.page * p.HV + h;
+    // gate sum over the segment
+    float part = 0.f;
+    for (int64_t t = begin + tid; t < end; t += kDecodeThreads) part += rec[t * p.HV];
+    part = wave_sum(part);
+    __syncthreads();  // the previous segment's last group is consumed
+    if ((tid & 63) == 0) s_part[tid >> 6] = part;
+    if (tid == 0) s_rest = 0.f;
+    __syncthreads();
+    float total = 0.f;
+#pragma unroll
+    for (int w = 0; w < kDecodeThreads / 64; ++w) total += s_part[w];
+    const float decay = expf(total);
+#pragma unroll
+    for (int r = 0; r < RPT; ++r)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) S[r][c] *= decay;
+    for (int64_t t0 = begin; t0 < end; t0 += kReplayWindow) {
+      const int n = static_cast<int>(end - t0 < kReplayWindow ? end - t0 : kReplayWindow);
+      __syncthreads();  // the previous group's rows are consumed
+      if (tid == 0) {
+        // s_rest: the gates of the segment's tokens before this group
+        float prefix = s_rest;
+        for (int i = 0; i < n; ++i) {
+          prefix += rec[(t0 + i) * p.HV];
+          s_suffix[i] = expf(total - prefix);
+        }
+        s_rest = prefix;
+      }
+      for (int idx = tid; idx < n * DK; idx += kDecodeThreads) {
+        const T* e = restore_log<T>(p, ls, layer, t0 + idx / DK, kh, idx % DK, false, DK, DV);
+        s_keys[idx / DK][idx % DK] = e ? to_f32(*e) : 0.f;
+      }
+      __syncthreads();
+      for (int idx = tid; idx < n * DV; idx += kDecodeThreads) {
+        const T* e = restore_log<T>(p, ls, layer, t0 + idx / DV, h, idx % DV, true, DK, DV);
+        s_vals[idx / DV][idx % DV] = e ? to_f32(from_f32<T>(to_f32(*e) * s_suffix[idx / DV])) : 0.f;
+      }
+      __syncthreads();
+      for (int i = 0; i < n; ++i) {
+#pragma unroll
+        for (int r = 0; r < RPT; ++r) {
+          const float kr = s_keys[i][r0 + r];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) S[r][c] = fmaf(kr, s_vals[i][c0 + c], S[r][c]);
+        }
+      }
+    }
+  }
+  const int64_t out = p.output[task];
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    T* row = slot_row<T>(p, out, layer, h, r0 + r, DV);
+    if (!row) continue;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) row[c0 + c] = from_f32<T>(S[r][c]);
+  }
+}
+
+// grid (pairs x layers x HV): the state of (source, layer, head) to destination.
+template <int DK, int DV, class T>
+__global__ __launch_bounds__(kDecodeThreads) void copy_states_kernel(RestoreParams p) {
+  const int64_t pair = blockIdx.x / (p.layers * p.HV);
+  const int64_t layer = (blockIdx.x / p.HV) % p.layers;
+  const int64_t h = blockIdx.x % p.HV;
+  const int64_t src = p.base[pair], dst = p.output[pair];
+  for (int idx = threadIdx.x; idx < DK * (DV / 4); idx += kDecodeThreads) {
+    const int row = idx / (DV / 4), c0 = 4 * (idx % (DV / 4));
+    const T* a = slot_row<T>(p, src, layer, h, row, DV);
+    T* b = slot_row<T>(p, dst, layer, h, row, DV);
+    if (!a || !b) continue;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) b[c0 + c] = a[c0 + c];
+  }
+}
+
 }  // namespace
 }  // namespace gdn
 
@@ -706,4 +862,129 @@ extern "C" int gdn_conv_windows_logstate(const void* x, int64_t x_row_stride, in
     return GDN_ERR_UNSUPPORTED;
   }
   return GDN_LAUNCH_CHECK("gdn_conv_windows_logstate launch");
+}
+
+namespace gdn {
+namespace {
+
+int restore_setup(RestoreParams& p, void* storage, const void* payload_frames, int frames_dtype,
+                  int64_t frames_per_slot, int64_t frame_bytes, int64_t head_bytes, int64_t num_frames,
+                  const void* decay_frames, int decay_dtype, int64_t record_bytes, int64_t layers, int64_t HV,
+                  int64_t KH, int64_t dk, int64_t dv, int64_t granularity, int64_t page_size, const char* who) {
+  GDN_REQUIRE(layers > 0 && HV > 0 && KH > 0 && HV % KH == 0 && granularity > 0 && page_size > 0 &&
+                  page_size % granularity == 0,
+              "%s: bad layout", who);
+  const int64_t row = dv * 2;
+  GDN_REQUIRE(frames_per_slot > 0 && frame_bytes > 0 && num_frames > 0 && frame_bytes % 8 == 0 &&
+                  head_bytes >= dk * row && head_bytes % 8 == 0,
+              "%s: bad frame layout", who);
+  GDN_REQUIRE(head_bytes <= frame_bytes ? frame_bytes % head_bytes == 0
+                                        : head_bytes % frame_bytes == 0 && frame_bytes % row == 0,
+              "%s: head_bytes %lld must divide frame_bytes %lld, or be a multiple of it with frames holding whole "
+              "state rows",
+              who, (long long)head_bytes, (long long)frame_bytes);
+  GDN_REQUIRE(layers * HV * head_bytes <= frames_per_slot * frame_bytes &&
+                  2 * page_size * layers * (KH * dk + HV * dv) <= frames_per_slot * frame_bytes,
+              "%s: the states or the log exceed a slot's frames", who);
+  GDN_REQUIRE(record_bytes % 4 == 0 && record_bytes >= 4 * layers * page_size * HV && record_bytes <= frame_bytes,
+              "%s: bad decay record size", who);
+  p.storage = static_cast<char*>(storage);
+  p.frames = payload_frames; p.frames_is64 = frames_dtype == GDN_I64;
+  p.fps = frames_per_slot; p.frame_bytes = frame_bytes; p.head_bytes = head_bytes; p.num_frames = num_frames;
+  p.decay = decay_frames; p.decay_is64 = decay_dtype == GDN_I64; p.record_bytes = record_bytes;
+  p.layers = layers; p.HV = HV; p.KH = KH; p.gran = granularity; p.page = page_size;
+  return GDN_OK;
+}
+
+// RESTORE: restore_kernel, else copy_states_kernel.
+template <bool RESTORE>
+int launch_state_kernel(const RestoreParams& p, int64_t blocks, int64_t dk, int64_t dv, int dtype, hipStream_t s,
+                        const char* who) {
+  if (blocks > 0x7fffffff) {
+    set_error("%s: grid too large", who);
+    return GDN_ERR_INVALID;
+  }
+  auto launch = [&](auto dkc, auto dvc) {
+    constexpr int DK = decltype(dkc)::value, DV = decltype(dvc)::value;
+    const dim3 grid(static_cast<unsigned>(blocks));
+    if constexpr (RESTORE) {
+      if (dtype == GDN_BF16)
+        hipLaunchKernelGGL((restore_kernel<DK, DV, bf16>), grid, dim3(kDecodeThreads), 0, s, p);
+      else
+        hipLaunchKernelGGL((restore_kernel<DK, DV, f16>), grid, dim3(kDecodeThreads), 0, s, p);
+    } else {
+      if (dtype == GDN_BF16)
+        hipLaunchKernelGGL((copy_states_kernel<DK, DV, bf16>), grid, dim3(kDecodeThreads), 0, s, p);
+      else
+        hipLaunchKernelGGL((copy_states_kernel<DK, DV, f16>), grid, dim3(kDecodeThreads), 0, s, p);
+    }
+    return GDN_LAUNCH_CHECK(who);
+  };
+  if (dtype != GDN_BF16 && dtype != GDN_F16) {
+    set_error("%s: state dtype must be bf16 or f16", who);
+    return GDN_ERR_UNSUPPORTED;
+  }
+  using I128 = std::integral_constant<int, 128>;
+  using I64 = std::integral_constant<int, 64>;
+  using I32 = std::integral_constant<int, 32>;
+  if (dk == 128 && dv == 128) return launch(I128{}, I128{});
+  if (dk == 64 && dv == 64) return launch(I64{}, I64{});
+  if (dk == 32 && dv == 32) return launch(I32{}, I32{});
+  if (dk == 128 && dv == 64) return launch(I128{}, I64{});
+  if (dk == 64 && dv == 128) return launch(I64{}, I128{});
+  set_error("%s: unsupported head dims dk=%lld dv=%lld", who, (long long)dk, (long long)dv);
+  return GDN_ERR_UNSUPPORTED;
+}
+
+}  // namespace
+}  // namespace gdn
+
+extern "C" int gdn_logstate_restore(void* storage, const void* payload_frames, int frames_dtype,
+                                    int64_t frames_per_slot, int64_t frame_bytes, int64_t head_bytes,
+                                    int64_t num_frames, const void* decay_frames, int decay_dtype,
+                                    int64_t decay_record_bytes, int64_t num_layers, int64_t HV, int64_t key_heads,
+                                    int64_t dk, int64_t dv, int64_t granularity, int64_t page_size, int dtype,
+                                    const int32_t* base_slots, const int32_t* segment_offsets,
+                                    const int32_t* log_slots, const int32_t* log_begins, const int32_t* log_ends,
+                                    const int32_t* output_slots, int64_t num_tasks, void* stream) {
+  using namespace gdn;
+  GDN_REQUIRE(num_tasks >= 0, "gdn_logstate_restore: bad sizes");
+  if (num_tasks == 0) return GDN_OK;
+  GDN_REQUIRE(storage && payload_frames && decay_frames && base_slots && segment_offsets && log_slots &&
+                  log_begins && log_ends && output_slots,
+              "gdn_logstate_restore: null input");
+  RestoreParams p{};
+  int rc = restore_setup(p, storage, payload_frames, frames_dtype, frames_per_slot, frame_bytes, head_bytes,
+                         num_frames, decay_frames, decay_dtype, decay_record_bytes, num_layers, HV, key_heads, dk, dv,
+                         granularity, page_size, "gdn_logstate_restore");
+  if (rc != GDN_OK) return rc;
+  p.base = base_slots; p.offsets = segment_offsets; p.seg_slots = log_slots; p.seg_begin = log_begins;
+  p.seg_end = log_ends; p.output = output_slots;
+  return launch_state_kernel<true>(p, num_tasks * num_layers * HV, dk, dv, dtype,
+                                             static_cast<hipStream_t>(stream), "gdn_logstate_restore");
+}
+
+extern "C" int gdn_logstate_copy_states(void* storage, const void* payload_frames, int frames_dtype,
+                                        int64_t frames_per_slot, int64_t frame_bytes, int64_t head_bytes,
+                                        int64_t num_frames, int64_t num_layers, int64_t HV, int64_t dk, int64_t dv,
+                                        int dtype, const int32_t* sources, const int32_t* destinations,
+                                        int64_t count, void* stream) {
+  using namespace gdn;
+  GDN_REQUIRE(count >= 0, "gdn_logstate_copy_states: bad sizes");
+  if (count == 0) return GDN_OK;
+  GDN_REQUIRE(storage && payload_frames && sources && destinations, "gdn_logstate_copy_states: null input");
+  GDN_REQUIRE(num_layers > 0 && HV > 0 && frames_per_slot > 0 && frame_bytes > 0 && num_frames > 0 &&
+                  head_bytes >= dk * dv * 2 &&
+                  (head_bytes <= frame_bytes ? frame_bytes % head_bytes == 0
+                                             : head_bytes % frame_bytes == 0 && frame_bytes % (dv * 2) == 0) &&
+                  num_layers * HV * head_bytes <= frames_per_slot * frame_bytes,
+              "gdn_logstate_copy_states: bad frame layout");
+  RestoreParams p{};
+  p.storage = static_cast<char*>(storage);
+  p.frames = payload_frames; p.frames_is64 = frames_dtype == GDN_I64;
+  p.fps = frames_per_slot; p.frame_bytes = frame_bytes; p.head_bytes = head_bytes; p.num_frames = num_frames;
+  p.layers = num_layers; p.HV = HV; p.KH = 1;
+  p.base = sources; p.output = destinations;
+  return launch_state_kernel<false>(p, count * num_layers * HV, dk, dv, dtype,
+                                                 static_cast<hipStream_t>(stream), "gdn_logstate_copy_states");
 }

@@ -8,6 +8,7 @@ from .gdn import (
     fused_recurrent_gated_delta_rule_to_logstate,
     fused_recurrent_gated_delta_rule_to_slots,
 )
+from .logstate import copy_states, restore_log_state_chains, store_log_states
 from .packed_conv import PackedConvStateIO, packed_causal_conv1d
 from .state_io import ChunkLogIO, ChunkStateIO
 
@@ -17,8 +18,11 @@ __all__ = [
     "PackedConvStateIO",
     "chunk_gated_delta_rule_to_cache",
     "conv_decode",
+    "copy_states",
     "fused_recurrent_gated_delta_rule",
     "fused_recurrent_gated_delta_rule_to_logstate",
     "fused_recurrent_gated_delta_rule_to_slots",
     "packed_causal_conv1d",
+    "restore_log_state_chains",
+    "store_log_states",
 ]

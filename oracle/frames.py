@@ -25,7 +25,12 @@ write each row where a reshape of the slot's log payload as
 f's bytes to frame p(f) and the table entries with them) leaves every read
 and write unchanged; and ``chunk_gated_delta_rule_to_frames`` on the identity
 table must equal ``gdn.chunk_gated_delta_rule_to_cache`` on the reshaped pool
-bit for bit.
+bit for bit.  ``restore_log_state_chains`` must rebuild, from a copied base
+state and the rows that eager decode steps logged, the state those steps left
+in the work slot (any split into segments or chained restores), a None base
+must equal a zeroed one, and a bf16 restore must round the suffix-scaled v'
+before the product; ``copy_states`` must move every layer of the named slots
+and no other byte.
 """
 
 from __future__ import annotations
@@ -367,3 +372,71 @@ def forward_prefill_logstate(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias,
                     decay_frames, record_bytes, layer=layer, layers=layers, granularity=granularity,
                     page_size=page_size, key_heads=num_k_heads)
     return o[0]
+
+
+# ----------------------------------------------------------------- LogState construction
+
+def read_log_segment(storage, payload_frames, decay_frames, frame_bytes, record_bytes, slot, begin, end, *, layer,
+                     layers, granularity, page_size, key_heads, HV, dk, dv):
+    """The logged tokens ``begin .. end - 1`` of log slot ``slot`` at
+    ``layer``: gates [n, HV] (fp32), key rows [n, HV, dk] (value head h reads
+    key row h // (HV / key_heads)) and v' rows [n, HV, dv], in the storage
+    dtype (``logstate_construction.cuh:137-190``)."""
+    flat = storage.view(-1)
+    as_bytes = storage.view(torch.uint8).view(-1)
+    item = storage.element_size()
+    group = HV // key_heads
+    positions = list(range(begin, end))
+    frame, record = int(decay_frames[slot, 0]), int(decay_frames[slot, 1])
+    rec = frame * frame_bytes + record * record_bytes
+    gates = torch.stack([as_bytes[rec + 4 * (layer * page_size + t) * HV:rec + 4 * ((layer * page_size + t) * HV + HV)]
+                         .view(torch.float32) for t in positions])
+    heads = list(range(HV))
+    keys = torch.stack([flat[log_element_index(payload_frames, [slot] * HV, [t] * HV, [h // group for h in heads],
+                                               range(dk), layer, layers, granularity, key_heads, HV, dk, dv,
+                                               frame_bytes, False, item)] for t in positions])
+    vals = torch.stack([flat[log_element_index(payload_frames, [slot] * HV, [t] * HV, heads, range(dv), layer, layers,
+                                               granularity, key_heads, HV, dk, dv, frame_bytes, True, item)]
+                        for t in positions])
+    return gates, keys, vals
+
+
+def restore_log_state_chains(storage, payload_frames, decay_frames, frame_bytes, head_bytes, record_bytes, chains, *,
+                             layers, HV, key_heads, dk, dv, granularity, page_size, dtype=torch.float32):
+    """``restore_log_state_chains`` (``kernel/linear_attention/logstate.py:59-88``,
+    kernel ``logstate_construction.cuh:290-393``): for each ``(base, segments,
+    output)`` and every layer and value head, S = the state of slot ``base``
+    (zero for None), then per segment ``(slot, begin, end)``
+    S <- e^{sum g} S + sum_t k_t (e^{sum_{j > t} g_j} v'_t)^T over its tokens,
+    the scaled v' rounded to the storage dtype; S goes to slot ``output``.
+    Chains are taken in order; ``storage`` is modified in place."""
+    io = storage.dtype
+    for base, segments, output in chains:
+        for layer in range(layers):
+            if base is None:
+                state = torch.zeros(HV, dk, dv, dtype=dtype)
+            else:
+                state = read_frame_states(storage, payload_frames, [base], layer, HV, dk, dv, frame_bytes,
+                                          head_bytes)[0].to(dtype)
+            for slot, begin, end in segments:
+                if end <= begin:
+                    continue
+                g, keys, vals = read_log_segment(storage, payload_frames, decay_frames, frame_bytes, record_bytes,
+                                                 slot, begin, end, layer=layer, layers=layers,
+                                                 granularity=granularity, page_size=page_size, key_heads=key_heads,
+                                                 HV=HV, dk=dk, dv=dv)
+                g = g.to(dtype)
+                total = g.sum(0)
+                suffix = torch.exp(total[None] - torch.cumsum(g, 0))
+                scaled = (vals.to(dtype) * suffix[..., None]).to(io).to(dtype)
+                state = state * torch.exp(total)[:, None, None] + torch.einsum('thk,thv->hkv', keys.to(dtype), scaled)
+            write_frame_states(storage, payload_frames, [output], layer, state[None], frame_bytes, head_bytes)
+
+
+def copy_states(storage, payload_frames, frame_bytes, head_bytes, sources, destinations, *, layers, HV, dk, dv):
+    """``copy_states`` (``logstate.py:118-128``, ``logstate_construction.cuh:397-414``):
+    every layer's states of ``sources[i]`` to ``destinations[i]``."""
+    for src, dst in zip(sources, destinations):
+        for layer in range(layers):
+            state = read_frame_states(storage, payload_frames, [src], layer, HV, dk, dv, frame_bytes, head_bytes)
+            write_frame_states(storage, payload_frames, [dst], layer, state, frame_bytes, head_bytes)

@@ -248,8 +248,8 @@ def _decode_pool(g, slots, H, HV, dk, dv, layers, page, gran, conv_dim, W, frame
     decay = torch.tensor([[int(dec[s // per_frame]), s % per_frame] for s in range(slots)], dtype=torch.int32)
     conv = order[slots * fps + n_dec:slots * fps + n_dec + slots * granules * cf].reshape(slots, granules, cf)
     storage = (torch.randn(total, frame_bytes // 2, generator=g) * 0.05).to(torch.bfloat16)
-    layout = SimpleNamespace(head_k_dim=dk, head_v_dim=dv, num_value_heads=HV, num_linear_layers=layers,
-                             granularity=gran, log_decay_bytes=record, num_granules=granules)
+    layout = SimpleNamespace(head_k_dim=dk, head_v_dim=dv, num_value_heads=HV, num_key_heads=H,
+                             num_linear_layers=layers, granularity=gran, log_decay_bytes=record, num_granules=granules)
     pool = SimpleNamespace(storage=None, payload_frame_table=None, decay_frame_table=None,
                            conv_frame_table=None, frame_bytes=frame_bytes, head_payload_bytes=head_bytes,
                            page_size=page, layout=layout, dtype=torch.bfloat16)
@@ -454,3 +454,71 @@ def test_logstate_backend_prefill_then_decode(eager):
     for slot, gr in [(0, 0), (1, 0), (2, 3), (3, 1), (4, 1)]:
         idx = ofr.conv_element_index(conv, [slot], [gr], layer, C, W - 1, fe)
         assert torch.equal(host.reshape(-1)[idx].view(torch.int16), expected.reshape(-1)[idx].view(torch.int16))
+
+
+# (H, frame_bytes, head_bytes, granularity): state heads inside a frame and
+# spanning two frames, one and two key heads
+RESTORE_CASES = [(1, 65536, 32768, 16), (2, 16384, 32768, 32), (2, 65536, 32768, 64)]
+
+
+@pytest.mark.parametrize("case", RESTORE_CASES)
+def test_logstate_store_copy_restore(case):
+    """store_log_states, copy_states and restore_log_state_chains
+    (kernel/linear_attention/logstate.py:59-128, logstate.cu:11-228,
+    logstate_construction.cuh:265-416) on a fragmented frame storage against
+    the oracle: the log bytes bit-exact after the stores, the copied states
+    bit-exact, the restored states to the state bar (fp32 1e-3 plus one bf16
+    rounding); no other byte changes.  Chains: a full page from a base, a None
+    base over two segments of two log slots, and a copied base over three
+    segments one of which is empty (tests/kernel/test_logstate_granules.py:24-49
+    is the model)."""
+    from logssms_amd.kernel.linear_attention.logstate import copy_states, restore_log_state_chains, store_log_states
+    H, frame_bytes, head_bytes, gran = case
+    g = gen(101 + gran + H)
+    HV, dk, dv, layers, page, slots = 4, 128, 128, 2, 64, 7
+    storage, payload, decay, conv, record, pool = _decode_pool(g, slots, H, HV, dk, dv, layers, page, gran, 16, 4,
+                                                               frame_bytes, head_bytes)
+    expected = storage.clone()
+    dev_u8 = storage.view(torch.uint8).to(DEV)
+    pool.storage = dev_u8
+    pool.payload_frame_table, pool.decay_frame_table = payload.to(DEV), decay.to(DEV)
+    print(f"store/copy/restore H={H} frame_bytes={frame_bytes} granularity={gran}", flush=True)
+    for slot in (1, 3):
+        for layer in range(layers):
+            heads = H if layer == 0 else HV  # keys per key head, then one row per value head
+            keys = F.normalize(torch.randn(page, heads, dk, generator=g), dim=-1).to(torch.bfloat16)
+            if heads == HV:
+                keys = keys[:, ::HV // H].repeat_interleave(HV // H, 1)
+            values = (torch.randn(page, HV, dv, generator=g) * 0.1).to(torch.bfloat16)
+            decays = -torch.rand(page, HV, generator=g) * 0.3
+            offsets = torch.randperm(page, generator=g)
+            token_slots = torch.full((page,), slot)
+            token_slots[5] = -1
+            ofr.store_chunk_log(expected, payload, frame_bytes, token_slots, offsets, values, keys, decays, decay,
+                                record, layer=layer, layers=layers, granularity=gran, page_size=page, key_heads=H)
+            store_log_states(pool, token_slots.to(torch.int32).to(DEV), offsets.to(torch.int32).to(DEV),
+                             keys.to(DEV), values.to(DEV), decays.to(DEV), layer)
+    torch.cuda.synchronize()
+    host = dev_u8.cpu().view(torch.bfloat16).reshape(storage.shape)
+    assert torch.equal(host.view(torch.int16), expected.view(torch.int16)), "log stores differ"
+    copy_states(pool, [0], [5])
+    ofr.copy_states(expected, payload, frame_bytes, head_bytes, [0], [5], layers=layers, HV=HV, dk=dk, dv=dv)
+    torch.cuda.synchronize()
+    host = dev_u8.cpu().view(torch.bfloat16).reshape(storage.shape)
+    assert torch.equal(host.view(torch.int16), expected.view(torch.int16)), "copied states differ"
+    chains = [(0, [(1, 0, page)], 2), (None, [(1, 5, 40), (3, 0, 17)], 4),
+              (5, [(3, 16, page), (1, 63, page), (1, 10, 10)], 6)]
+    restore_log_state_chains(pool, chains)
+    ofr.restore_log_state_chains(expected, payload, decay, frame_bytes, head_bytes, record, chains, layers=layers,
+                                 HV=HV, key_heads=H, dk=dk, dv=dv, granularity=gran, page_size=page)
+    torch.cuda.synchronize()
+    host = dev_u8.cpu().view(torch.bfloat16).reshape(storage.shape)
+    mask = torch.ones(host.numel(), dtype=torch.bool)
+    for layer in range(layers):
+        got = ofr.read_frame_states(host, payload, [2, 4, 6], layer, HV, dk, dv, frame_bytes, head_bytes)
+        want = ofr.read_frame_states(expected, payload, [2, 4, 6], layer, HV, dk, dv, frame_bytes, head_bytes)
+        _report(f"restored states, layer {layer}", got, want)
+        assert_state16_close(got, want)
+        mask[ofr.frame_state_index(payload, [2, 4, 6], layer, HV, dk, dv, 2, frame_bytes, head_bytes).reshape(-1)] = False
+    a, e = host.view(torch.int16).reshape(-1), expected.view(torch.int16).reshape(-1)
+    assert not ((a != e) & mask).any(), "restore wrote outside its output states"

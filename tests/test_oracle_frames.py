@@ -365,3 +365,98 @@ def test_logstate_prefill_equals_the_plain_pipeline():
     after = storage[base:].reshape(P["slots"] * G, -1)[:, :layers * C * S].reshape(P["slots"] * G, layers, C, S)
     for (slot, gr), w in zip([(0, 1), (2, 0), (1, 0), (3, 0)], win):
         torch.testing.assert_close(after[slot * G + gr, 1], w, rtol=0, atol=0)
+
+
+# ---------------------------------------------------------------- LogState construction
+
+def _decoded_log(seed, T=21, eager=True):
+    """T eager LogState decode steps of one sequence (work slot 1, log slot
+    0, layer 1) on an fp32 pool; the work state before them is copied to
+    slot 2 first.  Returns the pool and the work state after the steps."""
+    P = _decode_pool(seed, page=32)
+    g = P["gen"]
+    H, HV, dk, dv = P["H"], P["HV"], P["dk"], P["dv"]
+    A_log, dt_bias = torch.randn(HV, generator=g) * 0.3, torch.randn(HV, generator=g) * 0.3
+    fr.copy_states(P["storage"], P["payload"], P["frame_bytes"], P["head_bytes"], [1], [2], layers=P["layers"],
+                   HV=HV, dk=dk, dv=dv)
+    for t in range(T):
+        q, k, v, a, bt = _raw_step(g, 1, H, HV, dk, dv)
+        fr.fused_recurrent_to_logstate(q, k, v, a, bt, A_log, dt_bias, P["storage"], P["payload"], P["decay"],
+                                       P["frame_bytes"], P["head_bytes"], P["record"], torch.tensor([1]),
+                                       torch.tensor([0]), torch.tensor([t]), torch.tensor([0]), layer=1,
+                                       layers=P["layers"], granularity=8, page_size=P["page"], eager=eager)
+    final = fr.read_frame_states(P["storage"], P["payload"], [1], 1, HV, dk, dv, P["frame_bytes"], P["head_bytes"])
+    return P, final
+
+
+def _restore(P, chains):
+    fr.restore_log_state_chains(P["storage"], P["payload"], P["decay"], P["frame_bytes"], P["head_bytes"], P["record"],
+                                chains, layers=P["layers"], HV=P["HV"], key_heads=P["H"], dk=P["dk"], dv=P["dv"],
+                                granularity=8, page_size=P["page"])
+    return fr.read_frame_states(P["storage"], P["payload"], [3], 1, P["HV"], P["dk"], P["dv"], P["frame_bytes"],
+                                P["head_bytes"])
+
+
+@pytest.mark.parametrize("segments", [[(0, 0, 21)], [(0, 0, 7), (0, 7, 21)], [(0, 0, 8), (0, 8, 9), (0, 9, 21)]])
+def test_restore_replays_the_decode(segments):
+    """The state rebuilt from the copied base and the logged tokens (v' rows,
+    keys, gates written by 21 eager decode steps) equals the state the decode
+    left in the work slot, however the tokens split into segments."""
+    P, final = _decoded_log(16)
+    got = _restore(P, [(2, segments, 3)])
+    torch.testing.assert_close(got, final, rtol=1e-5, atol=1e-5)
+
+
+def test_restore_chains_compose_and_zero_base():
+    """Restoring the first 10 tokens into slot 3 and then the rest from slot
+    3 equals one restore; a None base equals a zeroed base slot."""
+    P, final = _decoded_log(17)
+    _restore(P, [(2, [(0, 0, 10)], 3)])
+    got = _restore(P, [(3, [(0, 10, 21)], 3)])
+    torch.testing.assert_close(got, final, rtol=1e-5, atol=1e-5)
+    zero = torch.zeros(1, P["HV"], P["dk"], P["dv"])
+    for layer in range(P["layers"]):
+        fr.write_frame_states(P["storage"], P["payload"], [2], layer, zero, P["frame_bytes"], P["head_bytes"])
+    a = _restore(P, [(2, [(0, 3, 21)], 3)])
+    b = _restore(P, [(None, [(0, 3, 21)], 3)])
+    assert torch.equal(a, b) and a.abs().sum() > 0
+
+
+def test_restore_rounds_scaled_values_to_the_storage_dtype():
+    """A bf16 pool: the one-token restore is e^g S + k round(v') exactly (the
+    suffix of the last token is e^0), and a two-token restore rounds
+    e^{g_2} v'_1 to bf16 before the product."""
+    P = _decode_pool(18, dtype=torch.bfloat16, page=32)
+    HV, dk, dv, H = P["HV"], P["dk"], P["dv"], P["H"]
+    g_bytes = P["storage"].view(torch.uint8).view(-1)
+    fr_, ri = int(P["decay"][0, 0]), int(P["decay"][0, 1])
+    base = fr_ * P["frame_bytes"] + ri * P["record"]
+    gates = -torch.rand(P["layers"] * P["page"] * HV, generator=P["gen"]) * 0.5
+    g_bytes[base:base + 4 * gates.numel()] = gates.view(torch.uint8)
+    s0 = fr.read_frame_states(P["storage"], P["payload"], [2], 1, HV, dk, dv, P["frame_bytes"], P["head_bytes"])[0]
+    gl, keys, vals = fr.read_log_segment(P["storage"], P["payload"], P["decay"], P["frame_bytes"], P["record"], 0, 4, 6,
+                                         layer=1, layers=P["layers"], granularity=8, page_size=P["page"], key_heads=H,
+                                         HV=HV, dk=dk, dv=dv)
+    got = _restore(P, [(2, [(0, 4, 6)], 3)])[0].float()
+    total = gl[0] + gl[1]
+    scaled1 = (vals[0].float() * torch.exp(total - gl[0])[:, None]).to(torch.bfloat16).float()
+    want = (s0.float() * torch.exp(total)[:, None, None] + keys[0].float()[:, :, None] * scaled1[:, None, :]
+            + keys[1].float()[:, :, None] * vals[1].float()[:, None, :])
+    torch.testing.assert_close(got, want.to(torch.bfloat16).float(), rtol=0, atol=0)
+
+
+def test_copy_states_moves_every_layer_and_nothing_else():
+    P = _decode_pool(19)
+    before = P["storage"].clone()
+    fr.copy_states(P["storage"], P["payload"], P["frame_bytes"], P["head_bytes"], [3, 0], [1, 2], layers=P["layers"],
+                   HV=P["HV"], dk=P["dk"], dv=P["dv"])
+    args = (P["HV"], P["dk"], P["dv"], P["frame_bytes"], P["head_bytes"])
+    for layer in range(P["layers"]):
+        for src, dst in [(3, 1), (0, 2)]:
+            assert torch.equal(fr.read_frame_states(P["storage"], P["payload"], [dst], layer, *args),
+                               fr.read_frame_states(before, P["payload"], [src], layer, *args))
+    mask = torch.ones(P["storage"].numel(), dtype=torch.bool)
+    for layer in range(P["layers"]):
+        mask[fr.frame_state_index(P["payload"], [1, 2], layer, P["HV"], P["dk"], P["dv"], 4, P["frame_bytes"],
+                                  P["head_bytes"]).reshape(-1)] = False
+    assert torch.equal(P["storage"].reshape(-1)[mask], before.reshape(-1)[mask])
