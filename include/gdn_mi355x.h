@@ -271,6 +271,46 @@ int gdn_logstate_copy_states(void* storage, const void* payload_frames, int fram
                              const int32_t* destinations, int64_t count, void* stream);
 
 /*
+ * LogState conv snapshot copy: replaces copy_conv_snapshots
+ * (kernel/linear_attention/conv_copy.py:31-52).  The snapshot_bytes of
+ * (source_slots[i], source_granules[i]) to (output_slots[i],
+ * output_granules[i]); conv_frames is the [table_rows, granules,
+ * frames_per_snapshot] frame table, snapshot byte x in frame
+ * conv_frames[slot, granule, x / frame_bytes] at x % frame_bytes.  Pairs with
+ * a negative or out-of-range slot or granule are skipped.
+ */
+int gdn_logstate_copy_conv(void* storage, const void* conv_frames, int frames_dtype, int64_t table_rows,
+                           int64_t granules, int64_t frames_per_snapshot, int64_t frame_bytes, int64_t num_frames,
+                           int64_t snapshot_bytes, const void* source_slots, int source_slots_dtype,
+                           const void* source_granules, int source_granules_dtype, const void* output_slots,
+                           int output_slots_dtype, const void* output_granules, int output_granules_dtype,
+                           int64_t count, void* stream);
+
+/*
+ * LogState masked conv store: replaces store_conv
+ * (kernel/linear_attention/masked_store.py:58-72).  Row i of values (row_bytes,
+ * one layer's conv window) to bytes [layer row_bytes, (layer + 1) row_bytes)
+ * of the (slots[i], slot_granules[i]) snapshot; rows with a negative slot are
+ * skipped.
+ */
+int gdn_logstate_store_conv(void* storage, const void* conv_frames, int frames_dtype, int64_t table_rows,
+                            int64_t granules, int64_t frames_per_snapshot, int64_t frame_bytes, int64_t num_frames,
+                            const void* slots, int slots_dtype, const void* slot_granules, int granules_dtype,
+                            int64_t count, int64_t layer, int64_t row_bytes, const void* values, void* stream);
+
+/*
+ * LogState masked state store: replaces store_states
+ * (kernel/linear_attention/masked_store.py:45-55).  values [count, HV,
+ * state_bytes] to head h of layer `layer` of slots[i] (logical byte
+ * (layer HV + h) head_bytes of the slot's payload frames); rows with a
+ * negative slot are skipped.
+ */
+int gdn_logstate_store_states(void* storage, const void* payload_frames, int frames_dtype, int64_t table_rows,
+                              int64_t frames_per_slot, int64_t frame_bytes, int64_t head_bytes, int64_t num_frames,
+                              const void* slots, int slots_dtype, int64_t count, int64_t layer, int64_t HV,
+                              int64_t state_bytes, const void* values, void* stream);
+
+/*
  * The GDN prefill of one layer (layers/linear_attention_backend/gdn.py:100-150:
  * history gather, packed_causal_conv1d, split, prepare_gdn,
  * chunk_gated_delta_rule_to_cache) as three launches whose results equal

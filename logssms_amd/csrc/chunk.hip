@@ -76,14 +76,7 @@ __device__ __forceinline__ uint16_t op_bits(float x) { return bits_of<f16>(x); }
 __device__ __forceinline__ uint32_t op_pack(float a, float b) {
   return op_bits(a) | (static_cast<uint32_t>(op_bits(b)) << 16);
 }
-template <class T> __device__ __forceinline__ float from_bits(uint16_t b);
-template <> __device__ __forceinline__ float from_bits<bf16>(uint16_t b) {
-  return __uint_as_float(static_cast<uint32_t>(b) << 16);
-}
-template <> __device__ __forceinline__ float from_bits<f16>(uint16_t b) {
-  return static_cast<float>(*reinterpret_cast<f16*>(&b));
-}
-__device__ __forceinline__ float op_val(uint16_t b) { return from_bits<f16>(b); }
+__device__ __forceinline__ float op_val(uint16_t b) { return static_cast<float>(*reinterpret_cast<f16*>(&b)); }
 
 // 8 input halfs (bf16 or f16) -> 8 operand halfs (f16).
 template <class IOT> __device__ __forceinline__ uint4 to_operands(uint4 raw);

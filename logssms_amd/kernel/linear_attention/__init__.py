@@ -1,6 +1,7 @@
 """Linear-attention operators mirroring ``logssms.kernel.linear_attention``
 (packed conv, conv decode) and its vendored FLA entry points."""
 
+from .conv_copy import copy_conv_snapshots
 from .conv_decode import conv_decode
 from .gdn import (
     chunk_gated_delta_rule_to_cache,
@@ -18,6 +19,7 @@ __all__ = [
     "PackedConvStateIO",
     "chunk_gated_delta_rule_to_cache",
     "conv_decode",
+    "copy_conv_snapshots",
     "copy_states",
     "fused_recurrent_gated_delta_rule",
     "fused_recurrent_gated_delta_rule_to_logstate",

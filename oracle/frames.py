@@ -440,3 +440,40 @@ def copy_states(storage, payload_frames, frame_bytes, head_bytes, sources, desti
         for layer in range(layers):
             state = read_frame_states(storage, payload_frames, [src], layer, HV, dk, dv, frame_bytes, head_bytes)
             write_frame_states(storage, payload_frames, [dst], layer, state, frame_bytes, head_bytes)
+
+
+def store_states(storage, payload_frames, frame_bytes, head_bytes, slots, layer, values):
+    """``store_states`` (``kernel/linear_attention/masked_store.py:11-55``):
+    ``values[i]`` [HV, dk, dv] to layer ``layer`` of ``slots[i]``, negative
+    slots skipped; the values are rounded to the storage dtype."""
+    write_frame_states(storage, payload_frames, slots, layer, values, frame_bytes, head_bytes)
+
+
+def store_conv(storage, conv_frames, frame_bytes, slots, granules, layer, values):
+    """``store_conv`` (``masked_store.py:34-72``): ``values[i]`` [C, S] to
+    layer ``layer`` of the (slots[i], granules[i]) conv snapshot, negative
+    slots skipped."""
+    n, C, S = values.shape
+    flat = storage.view(-1)
+    fe = frame_bytes // storage.element_size()
+    for i in range(n):
+        if int(slots[i]) < 0:
+            continue
+        idx = conv_element_index(conv_frames, [int(slots[i])], [int(granules[i])], layer, C, S, fe)
+        flat[idx.reshape(-1)] = values[i].reshape(-1).to(storage.dtype)
+
+
+def copy_conv_snapshots(storage, conv_frames, frame_bytes, source_slots, source_granules, output_slots,
+                        output_granules, *, layers, C, S):
+    """``copy_conv_snapshots`` (``kernel/linear_attention/conv_copy.py:7-52``):
+    every layer's window of (source slot, granule) to (output slot, granule),
+    pairs with a negative slot skipped (the pairs must not overlap)."""
+    flat = storage.view(-1)
+    fe = frame_bytes // storage.element_size()
+    for s, sg, o, og in zip(source_slots, source_granules, output_slots, output_granules):
+        if int(s) < 0 or int(o) < 0:
+            continue
+        for layer in range(layers):
+            src = conv_element_index(conv_frames, [int(s)], [int(sg)], layer, C, S, fe).reshape(-1)
+            dst = conv_element_index(conv_frames, [int(o)], [int(og)], layer, C, S, fe).reshape(-1)
+            flat[dst] = flat[src].clone()

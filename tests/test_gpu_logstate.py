@@ -522,3 +522,42 @@ def test_logstate_store_copy_restore(case):
         mask[ofr.frame_state_index(payload, [2, 4, 6], layer, HV, dk, dv, 2, frame_bytes, head_bytes).reshape(-1)] = False
     a, e = host.view(torch.int16).reshape(-1), expected.view(torch.int16).reshape(-1)
     assert not ((a != e) & mask).any(), "restore wrote outside its output states"
+
+
+@pytest.mark.parametrize("frame_bytes", [65536, 4096])
+def test_logstate_masked_stores_and_conv_copy(frame_bytes):
+    """store_states, store_conv (masked_store.py:11-72) and
+    copy_conv_snapshots (conv_copy.py:7-52) on a fragmented frame storage
+    against the oracle, bit-exact over the whole storage; negative slots are
+    skipped.  frame_bytes 4096: state heads and conv snapshots span frames."""
+    from logssms_amd.kernel.linear_attention.conv_copy import copy_conv_snapshots
+    from logssms_amd.kernel.linear_attention.masked_store import store_conv, store_states
+    g = gen(111 + frame_bytes % 1000)
+    H, HV, dk, dv, layers, page, gran, W, slots = 2, 4, 128, 128, 2, 64, 16, 4, 5
+    conv_dim = 2 * H * dk + HV * dv
+    storage, payload, decay, conv, record, pool = _decode_pool(g, slots, H, HV, dk, dv, layers, page, gran, conv_dim,
+                                                               W, max(frame_bytes, 4 * layers * page * HV), 32768)
+    frame_bytes = pool.frame_bytes
+    pool.layout.conv_dim, pool.layout.state_len = conv_dim, W - 1
+    expected = storage.clone()
+    dev_u8 = storage.view(torch.uint8).to(DEV)
+    pool.storage = dev_u8
+    pool.payload_frame_table, pool.conv_frame_table = payload.to(DEV), conv.to(DEV)
+    print(f"masked stores / conv copy frame_bytes={frame_bytes}", flush=True)
+    state_slots = torch.tensor([3, -1, 0], dtype=torch.int32)
+    states = torch.randn(3, HV, dk, dv, generator=g)
+    ofr.store_states(expected, payload, frame_bytes, 32768, state_slots.long(), 1, states)
+    store_states(pool, state_slots.to(DEV), 1, states.to(DEV))
+    conv_slots, conv_gran = torch.tensor([1, 4, -1, 2]), torch.tensor([3, 0, 1, 2])
+    windows = torch.randn(4, conv_dim, W - 1, generator=g).to(torch.bfloat16)
+    ofr.store_conv(expected, conv, frame_bytes, conv_slots, conv_gran, 0, windows)
+    store_conv(pool, conv_slots.to(DEV), conv_gran.to(DEV), 0, windows.to(DEV))
+    src, sg = torch.tensor([1, 2, -1], dtype=torch.int32), torch.tensor([3, 2, 0], dtype=torch.int32)
+    dst, dg = torch.tensor([0, 3, 4], dtype=torch.int32), torch.tensor([1, 0, 1], dtype=torch.int32)
+    ofr.copy_conv_snapshots(expected, conv, frame_bytes, src, sg, dst, dg, layers=layers, C=conv_dim, S=W - 1)
+    copy_conv_snapshots(pool, src.to(DEV), sg.to(DEV), dst.to(DEV), dg.to(DEV))
+    torch.cuda.synchronize()
+    host = dev_u8.cpu().view(torch.bfloat16).reshape(storage.shape)
+    diff = host.view(torch.int16) != expected.view(torch.int16)
+    assert not diff.any(), f"{int(diff.sum())} elements differ"
+    assert not torch.equal(expected, storage), "the stores changed nothing"

@@ -460,3 +460,28 @@ def test_copy_states_moves_every_layer_and_nothing_else():
         mask[fr.frame_state_index(P["payload"], [1, 2], layer, P["HV"], P["dk"], P["dv"], 4, P["frame_bytes"],
                                   P["head_bytes"]).reshape(-1)] = False
     assert torch.equal(P["storage"].reshape(-1)[mask], before.reshape(-1)[mask])
+
+
+def test_conv_store_and_copy_on_the_identity_table():
+    """Identity conv tables: store_conv writes layer l of the reshaped
+    [slot, granule, layer, C, S] block, copy_conv_snapshots copies whole
+    blocks, and nothing else changes."""
+    P = _decode_pool(20)
+    C, S, G, L = P["conv_dim"], P["W"] - 1, P["granules"], P["layers"]
+    base = P["slots"] * P["fps"] + P["slots"]
+    g = P["gen"]
+
+    def block(storage):
+        return storage[base:].reshape(P["slots"] * G, -1)[:, :L * C * S].reshape(P["slots"], G, L, C, S)
+
+    before = P["storage"].clone()
+    values = torch.randn(3, C, S, generator=g)
+    fr.store_conv(P["storage"], P["conv"], P["frame_bytes"], [2, -1, 0], [1, 0, 0], 1, values)
+    want = block(before).clone()
+    want[2, 1, 1], want[0, 0, 1] = values[0], values[2]
+    assert torch.equal(block(P["storage"]), want)
+    fr.copy_conv_snapshots(P["storage"], P["conv"], P["frame_bytes"], [2, 1], [1, 0], [3, -1], [0, 1], layers=L, C=C,
+                           S=S)
+    want[3, 0] = want[2, 1]
+    assert torch.equal(block(P["storage"]), want)
+    assert torch.equal(P["storage"][:base], before[:base])
