@@ -519,6 +519,18 @@ int gdn_metadata_copy(const void* const* srcs, void* const* dsts, const int64_t*
 int gdn_metadata_pad(const void* const* srcs, void* const* dsts, const int64_t* lengths, const int64_t* capacities,
                      const int64_t* fills, const int64_t* tails, const int* elem_sizes, int fields, void* stream);
 
+/*
+ * LogState prefill write plan: replaces make_logstate_prefill_writes
+ * (python/logssms/kernel/metadata.py:150-178), called by the LogState
+ * backend's prefill metadata (layers/linear_attention_backend/logstate.py:214-272).
+ * plan = int32 [conv slot | conv granule | log enabled] of `count` tokens;
+ * out ([3, count], the dtype of log_slots) = [log_slots where enabled else -1 |
+ * log_slots where conv slot == -2 else conv slot | token_offsets /
+ * granularity where conv slot == -2 else conv granule].
+ */
+int gdn_logstate_prefill_writes(const void* log_slots, int slots_dtype, const void* token_offsets, int offsets_dtype,
+                                const int32_t* plan, void* out, int64_t count, int64_t granularity, void* stream);
+
 /* ------------------------------------------------------------------ output norm */
 
 /*

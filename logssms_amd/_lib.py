@@ -50,6 +50,7 @@ SIGNATURES = {
     "gdn_logstate_copy_conv": [P, P, I32, I64, I64, I64, I64, I64, I64, P, I32, P, I32, P, I32, P, I32, I64, P],
     "gdn_logstate_store_conv": [P, P, I32, I64, I64, I64, I64, I64, P, I32, P, I32, I64, I64, I64, P, P],
     "gdn_logstate_store_states": [P, P, I32, I64, I64, I64, I64, I64, P, I32, I64, I64, I64, I64, P, P],
+    "gdn_logstate_prefill_writes": [P, I32, P, I32, P, P, I64, I64, P],
     "gdn_logstate_restore": [P, P, I32, I64, I64, I64, I64, P, I32, I64, I64, I64, I64, I64, I64, I64, I64, I32, P,
                              P, P, P, P, P, I64, P],
     "gdn_logstate_copy_states": [P, P, I32, I64, I64, I64, I64, I64, I64, I64, I64, I32, P, P, I64, P],

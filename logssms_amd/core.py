@@ -31,6 +31,19 @@ class MarconiCacheMetadata:
 
 
 @dataclass
+class LogStateCacheMetadata:
+    """cache/logstate/metadata.py:6-10 (with cache/metadata.py:5-6): the
+    replay count of each decode request, the page offset of each prefill
+    request's first token, the checkpoint writes (global token row, slot) and
+    the (request, begin, end) position ranges whose tokens are not logged."""
+
+    replay_counts: list[int] | None = None
+    first_offsets: list[int] | None = None
+    checkpoint_writes: list[tuple[int, int]] = field(default_factory=list)
+    checkpoint_ranges: list[tuple[int, int, int]] = field(default_factory=list)
+
+
+@dataclass
 class Batch:
     reqs: list[Request]
     phase: Literal["prefill", "decode", "verify", "mixed"]
@@ -43,6 +56,10 @@ class Batch:
     num_prefill_reqs: int = 0
     mixed_parts: tuple | None = None
     prefill_token_capacity: int = 0
+    # token positions and KV locations of the batch rows (core.py Batch.positions
+    # / out_loc), read by the LogState metadata
+    positions: torch.Tensor | None = None
+    out_loc: torch.Tensor | None = None
 
     def __post_init__(self):
         if self.padded_reqs is None:
@@ -95,6 +112,7 @@ class Context:
     linear_state: Any = None
     state_table: torch.Tensor | None = None
     work_state_table: torch.Tensor | None = None
+    page_table: torch.Tensor | None = None
     batch: Any = None  # the batch being run (GatedDeltaNet.attend reads it)
     _backend: Any = field(default=None, repr=False)
 
@@ -126,5 +144,5 @@ def get_global_ctx() -> Context:
     return _GLOBAL_CTX
 
 
-__all__ = ["Batch", "Context", "MarconiCacheMetadata", "Request", "clear_global_ctx", "get_global_ctx",
-           "set_global_ctx"]
+__all__ = ["Batch", "Context", "LogStateCacheMetadata", "MarconiCacheMetadata", "Request", "clear_global_ctx",
+           "get_global_ctx", "set_global_ctx"]

@@ -141,3 +141,50 @@ extern "C" int gdn_metadata_pad(const void* const* srcs, void* const* dsts, cons
   }
   return GDN_OK;
 }
+
+// LogState prefill write plan (python/logssms/kernel/metadata.py:150-178,
+// make_logstate_prefill_writes): from the per-token log slots, page offsets
+// and the host plan [conv slot | conv granule | log enabled] (conv slot -2:
+// the token's own log slot at granule offset / granularity) build
+// [log write slots | conv token slots | conv token granules].
+namespace gdn {
+namespace {
+
+__global__ __launch_bounds__(kThreads) void logstate_prefill_writes_kernel(const void* logs, const void* offsets,
+                                                                          int offsets_is64, const int32_t* plan,
+                                                                          void* out, int out_is64, int64_t count,
+                                                                          int64_t granularity) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (r >= count) return;
+  const int64_t slot = load_index(logs, r, out_is64);
+  const int64_t conv = plan[r];
+  const int64_t values[3] = {plan[2 * count + r] != 0 ? slot : -1, conv == -2 ? slot : conv,
+                             conv == -2 ? load_index(offsets, r, offsets_is64) / granularity : plan[count + r]};
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    if (out_is64)
+      static_cast<int64_t*>(out)[j * count + r] = values[j];
+    else
+      static_cast<int32_t*>(out)[j * count + r] = static_cast<int32_t>(values[j]);
+  }
+}
+
+}  // namespace
+}  // namespace gdn
+
+extern "C" int gdn_logstate_prefill_writes(const void* log_slots, int slots_dtype, const void* token_offsets,
+                                           int offsets_dtype, const int32_t* plan, void* out, int64_t count,
+                                           int64_t granularity, void* stream) {
+  using namespace gdn;
+  GDN_REQUIRE(count >= 0 && granularity > 0, "gdn_logstate_prefill_writes: bad sizes");
+  if (count == 0) return GDN_OK;
+  GDN_REQUIRE(log_slots && token_offsets && plan && out, "gdn_logstate_prefill_writes: null input");
+  GDN_REQUIRE((slots_dtype == GDN_I32 || slots_dtype == GDN_I64) && (offsets_dtype == GDN_I32 || offsets_dtype == GDN_I64),
+              "gdn_logstate_prefill_writes: index tensors must be int32 or int64");
+  const int64_t blocks = (count + kThreads - 1) / kThreads;
+  GDN_REQUIRE(blocks <= 0x7fffffff, "gdn_logstate_prefill_writes: too many tokens");
+  hipLaunchKernelGGL(logstate_prefill_writes_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), log_slots, token_offsets, offsets_dtype == GDN_I64, plan, out,
+                     slots_dtype == GDN_I64, count, granularity);
+  return GDN_LAUNCH_CHECK("gdn_logstate_prefill_writes");
+}

@@ -81,4 +81,27 @@ def pad_metadata(sources, outputs, fills, chunk_tails) -> None:
               _lib.i64_array([t for _, _, _, t in jobs]), sizes[0], len(jobs), _lib.stream_of(outputs[0]))
 
 
-__all__ = ["copy_metadata", "pad_metadata"]
+def make_logstate_prefill_writes(logs: torch.Tensor, offsets: torch.Tensor, plan: torch.Tensor, granularity: int):
+    """metadata.py:150-178: from the per-token log slots ``logs``, page
+    offsets ``offsets`` and the int32 host plan ``[conv slot | conv granule |
+    log enabled]`` (conv slot -2: the token's own log slot), the
+    ``(log write slots, conv token slots, conv token granules)`` of a LogState
+    prefill (``gdn_logstate_prefill_writes`` on the device; host tensors take
+    the same torch expressions)."""
+    count = logs.numel()
+    output = torch.empty((3, count), dtype=logs.dtype, device=logs.device)
+    if not logs.is_cuda:
+        conv, granules, enabled = plan[:3 * count].view(3, count)
+        output[0] = torch.where(enabled != 0, logs, -1)
+        output[1] = torch.where(conv == -2, logs, conv)
+        output[2] = torch.where(conv == -2, offsets // granularity, granules)
+        return output.unbind(0)
+    assert plan.dtype == torch.int32 and plan.is_contiguous() and plan.numel() >= 3 * count
+    logs, offsets = logs.contiguous(), offsets.contiguous()
+    _lib.call("gdn_logstate_prefill_writes", logs.data_ptr(), _lib.index_code(logs), offsets.data_ptr(),
+              _lib.index_code(offsets), plan.data_ptr(), output.data_ptr(), count, granularity,
+              _lib.stream_of(logs))
+    return output.unbind(0)
+
+
+__all__ = ["copy_metadata", "make_logstate_prefill_writes", "pad_metadata"]

@@ -21,9 +21,13 @@ construction) and must provide what ``cache/logstate/frame_pool.py``'s pool
 provides: ``storage`` (uint8 frames), ``dtype``, ``frame_bytes``,
 ``head_payload_bytes``, ``page_size``, ``payload_frame_table``,
 ``decay_frame_table``, ``conv_frame_table``, ``layout`` and ``read_conv``.
-Building the metadata is the LogState cache manager's work (its page and
-work-slot tables); the backend takes it from ``batch.linear_attn_metadata``.
-Speculative verify raises ``NotImplementedError``, as in the reference.
+``prepare_metadata`` (``logstate.py:92-272``) builds the metadata from the
+context's ``state_table`` (the log slot of each position), ``work_state_table``
+and ``page_table``, the batch's ``positions`` / ``out_loc`` and its
+``LogStateCacheMetadata`` (replay counts, checkpoint writes and unlogged
+ranges, which the LogState cache manager plans); the pool's ``allocator``
+tells work slots from others.  Speculative verify raises
+``NotImplementedError``, as in the reference.
 """
 
 from __future__ import annotations
@@ -32,8 +36,9 @@ from dataclasses import dataclass
 
 import torch
 
-from ..core import get_global_ctx
+from ..core import LogStateCacheMetadata, get_global_ctx
 from ..kernel.fused import prepare_gdn
+from ..kernel.metadata import copy_metadata, make_logstate_prefill_writes
 from ..kernel.linear_attention.conv_decode import conv_decode
 from ..kernel.linear_attention.gdn import (
     chunk_gated_delta_rule_to_cache,
@@ -94,29 +99,145 @@ class GatedDeltaLogStateBackend:
     def ctx(self):
         return self._ctx if self._ctx is not None else get_global_ctx()
 
+    # ------------------------------------------------------------ metadata
+    def prepare_metadata(self, batch) -> None:
+        """logstate.py:92-212 (the table path; the reference's prepared-packet
+        shortcut gathers the same slots)."""
+        if batch.cache_metadata is None:
+            batch.cache_metadata = LogStateCacheMetadata()
+        assert isinstance(batch.cache_metadata, LogStateCacheMetadata)
+        if batch.is_verify:
+            raise NotImplementedError("LogState speculative verify is not implemented yet.")
+        ctx = self.ctx
+        pool = ctx.linear_state
+        state_table, work_table = ctx.state_table, ctx.work_state_table
+        assert state_table is not None and work_table is not None and ctx.page_table is not None
+        assert work_table.shape[1] == 1
+        assert batch.positions is not None and batch.out_loc is not None
+        device = pool.storage.device
+        reqs = batch.padded_reqs if batch.is_decode else batch.reqs
+        table_indices = torch.tensor([r.table_idx for r in reqs], dtype=torch.int64, device=state_table.device)
+        if batch.is_decode:
+            row_table_indices = table_indices
+        else:
+            row_table_indices = torch.tensor([r.table_idx for r in reqs for _ in range(r.extend_len)],
+                                             dtype=torch.int64, device=state_table.device)
+        work_slots = work_table[table_indices, 0]
+        positions = batch.positions
+        assert len(positions) == len(row_table_indices)
+        log_slots = state_table[row_table_indices, positions.long()]
+        token_offsets = batch.out_loc.remainder(pool.page_size).to(torch.int32)
+        if batch.is_decode:
+            counts = batch.cache_metadata.replay_counts
+            if counts is None:
+                counts = [0] * len(reqs)
+            assert len(counts) == len(reqs)
+            replay_counts = torch.tensor(counts, dtype=torch.int32, device=device)
+            conv_read_slots = work_slots
+            conv_read_granules = torch.zeros_like(work_slots)
+        else:
+            replay_counts = torch.empty(0, dtype=torch.int32, device=device)
+            previous = torch.tensor([r.cached_len - 1 for r in reqs], dtype=torch.int64, device=state_table.device)
+            previous_slots = state_table[table_indices, previous.clamp_min(0)]
+            previous_kv = ctx.page_table[table_indices, previous.clamp_min(0)]
+            mapped = (previous >= 0) & (previous_slots >= 0)
+            conv_read_slots = torch.where(mapped, previous_slots, work_slots)
+            conv_read_granules = torch.where(
+                mapped, previous_kv.remainder(pool.page_size) // pool.layout.granularity, 0).to(torch.int32)
+        metadata = LogStateLinearAttnMetadata(
+            phase=batch.phase, work_slots=work_slots, log_slots=log_slots, token_offsets=token_offsets,
+            conv_read_slots=conv_read_slots, conv_read_granules=conv_read_granules, replay_counts=replay_counts)
+        if batch.is_prefill:
+            self._prepare_direct_prefill(batch, metadata, pool)
+        batch.linear_attn_metadata = metadata
+
+    @staticmethod
+    def _prepare_direct_prefill(batch, metadata, pool) -> None:
+        """logstate.py:214-272: the packed-sequence indices, the chunk
+        checkpoint slots, and per token the log write slot (none inside an
+        unlogged range) and the conv snapshot target: the token's own log
+        slot and granule at each granule end and at the sequence end, or a
+        checkpoint slot (granule 0 of a work slot, else the last granule)."""
+        lengths = [r.extend_len for r in batch.reqs]
+        granularity = pool.layout.granularity
+        device = pool.storage.device
+        metadata.prefill_indices = PackedLinearIndices.from_lengths(lengths, device, granularity)
+        metadata.cu_seqlens = metadata.prefill_indices.cu_seqlens
+        first_offsets = batch.cache_metadata.first_offsets
+        if first_offsets is None:
+            first_offsets = metadata.token_offsets.index_select(0, metadata.cu_seqlens[:-1]).tolist()
+        total = sum(lengths)
+        chunks = len(metadata.prefill_indices.chunk_indices)
+        host = torch.empty(3 * total + chunks, dtype=torch.int32, pin_memory=device.type == "cuda")
+        conv_slots, conv_granules, log_mask = host[:3 * total].view(3, total).numpy()
+        chunk_writes = host[3 * total:].numpy()
+        conv_slots.fill(-1)
+        conv_granules.fill(0)
+        log_mask.fill(1)
+        chunk_writes.fill(-1)
+        checkpoints = iter(sorted(batch.cache_metadata.checkpoint_writes))
+        checkpoint = next(checkpoints, None)
+        ranges: dict[int, list[tuple[int, int]]] = {}
+        for req, begin, end in batch.cache_metadata.checkpoint_ranges:
+            ranges.setdefault(req, []).append((begin, end))
+        token_begin = chunk_begin = 0
+        for i, req in enumerate(batch.reqs):
+            length, first = lengths[i], first_offsets[i]
+            token_end = token_begin + length
+            conv_slots[token_begin + granularity - 1 - first % granularity:token_end:granularity] = -2
+            if length:
+                conv_slots[token_end - 1] = -2
+            for begin, end in ranges.get(i, ()):
+                begin = max(0, begin - req.cached_len)
+                end = min(length, end - req.cached_len)
+                if begin < end:
+                    log_mask[token_begin + begin:token_begin + end] = 0
+                    conv_slots[token_begin + begin:token_begin + end] = -1
+            while checkpoint is not None and checkpoint[0] < token_end:
+                global_row, slot = checkpoint
+                row = global_row - token_begin
+                assert row >= 0
+                if (first + row + 1) % granularity == 0 or row + 1 == length:
+                    conv_slots[global_row] = slot
+                    conv_granules[global_row] = (
+                        0 if pool.allocator.slot(slot).kind == "work" else pool.layout.num_granules - 1)
+                    chunk_writes[chunk_begin + row // granularity] = slot
+                checkpoint = next(checkpoints, None)
+            token_begin += length
+            chunk_begin += (length + granularity - 1) // granularity
+        packet = host.to(device, non_blocking=device.type == "cuda")
+        metadata.chunk_write_slots = packet[3 * total:]
+        metadata.log_write_slots, metadata.conv_token_slots, metadata.conv_token_granules = (
+            make_logstate_prefill_writes(metadata.log_slots, metadata.token_offsets, packet, granularity))
+
     # ------------------------------------------------------------ decode graphs
     def init_capture_graph(self, max_seq_len: int, bs_list: list[int]) -> None:
         del max_seq_len
+        assert self.capture is None, "Capture already initialized."
         self.capture_bs = sorted(bs_list)
         self.capture = LogStateLinearAttnCaptureData.make(max(bs_list), self.ctx.linear_state.storage.device)
 
     def prepare_for_capture(self, batch) -> None:
-        """The captured decode reads the capture buffers (their first
-        ``batch.size`` entries)."""
-        assert self.capture is not None and batch.is_decode
-        bs = batch.size
-        cap = self.capture
-        batch.linear_attn_metadata = LogStateLinearAttnMetadata(
-            phase="decode", **{name: getattr(cap, name)[:bs] for name in _CAPTURED})
+        """logstate.py:285-292: the batch's metadata, copied into the capture
+        buffers, which the captured decode then reads."""
+        assert self.capture is not None and batch.size in self.capture_bs
+        self.prepare_metadata(batch)
+        batch.linear_attn_metadata = self._copy_to_capture(batch.linear_attn_metadata, batch.size)
 
     def prepare_for_replay(self, batch) -> None:
-        """Copies the fresh metadata of ``batch`` into the capture buffers
-        (padding entries keep what they held)."""
-        assert self.capture is not None
-        metadata = batch.linear_attn_metadata
-        for name in _CAPTURED:
-            src = getattr(metadata, name)
-            getattr(self.capture, name)[:src.shape[0]].copy_(src)
+        """logstate.py:294-299: the fresh metadata of ``batch`` into the
+        capture buffers."""
+        bs = batch.padded_size
+        assert self.capture is not None and bs in self.capture_bs
+        self._copy_to_capture(batch.linear_attn_metadata, bs)
+
+    def _copy_to_capture(self, metadata, bs: int) -> "LogStateLinearAttnMetadata":
+        """logstate.py:301-329: one batched copy of the six decode fields."""
+        assert self.capture is not None and isinstance(metadata, LogStateLinearAttnMetadata)
+        copy_metadata(tuple(getattr(metadata, name).to(torch.int32) for name in _CAPTURED),
+                      tuple(getattr(self.capture, name)[:bs] for name in _CAPTURED))
+        return LogStateLinearAttnMetadata(phase="decode",
+                                          **{name: getattr(self.capture, name)[:bs] for name in _CAPTURED})
 
     # ------------------------------------------------------------ forward
     def forward(self, mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, batch, out=None):

@@ -561,3 +561,143 @@ def test_logstate_masked_stores_and_conv_copy(frame_bytes):
     diff = host.view(torch.int16) != expected.view(torch.int16)
     assert not diff.any(), f"{int(diff.sum())} elements differ"
     assert not torch.equal(expected, storage), "the stores changed nothing"
+
+
+def test_logstate_metadata_then_prefill_and_captured_decode():
+    """GatedDeltaLogStateBackend.prepare_metadata (logstate.py:92-272) from
+    the state / work / page tables and a LogStateCacheMetadata: request A
+    (no cached prefix, 100 tokens) and request B (32 cached tokens in log slot
+    7, 37 new ones).  Checkpoint writes at granule ends (a work-kind slot takes
+    granule 0, others the last granule), one that is not at a granule end
+    (ignored), and an unlogged range.  The built fields are checked against a
+    per-token statement of the same plan, then the prefill runs on them
+    against the oracle, then one decode step through prepare_for_capture's
+    capture buffers."""
+    from types import SimpleNamespace
+    from logssms_amd.core import Batch, Context, LogStateCacheMetadata, Request
+    from logssms_amd.layers import GatedDeltaLogStateBackend
+    g = gen(121)
+    H, HV, dk, dv, layers, layer, page, gran, W = 2, 4, 128, 128, 2, 1, 64, 16, 4
+    C = 2 * H * dk + HV * dv
+    frame_bytes, head_bytes = 65536, 32768
+    slots = 10  # 0, 1 work; 2, 3, 4, 7 log pages; 5, 6, 9 checkpoints; 8 a work-kind checkpoint
+    storage, payload, decay, conv, record, pool = _decode_pool(g, slots, H, HV, dk, dv, layers, page, gran, C, W,
+                                                               frame_bytes, head_bytes)
+    fe = frame_bytes // 2
+
+    def read_conv(s, gr, lay):
+        idx = ofr.conv_element_index(conv, s.cpu(), gr.cpu(), lay, C, W - 1, fe).to(DEV)
+        return pool.storage.view(torch.bfloat16).reshape(-1)[idx].view(len(s), C, W - 1)
+
+    pool.read_conv = read_conv
+    pool.allocator = SimpleNamespace(slot=lambda s: SimpleNamespace(kind="work" if s in (0, 1, 8) else "log"))
+    dev_u8 = storage.view(torch.uint8).to(DEV)
+    pool.storage = dev_u8
+    pool.payload_frame_table, pool.decay_frame_table, pool.conv_frame_table = payload.to(DEV), decay.to(DEV), conv.to(DEV)
+    # tables: row 0 = request A (log pages 2, 3), row 1 = request B (log pages 7, 4)
+    width = 4 * page
+    state_table = torch.full((2, width), -1, dtype=torch.int32)
+    page_table = torch.zeros(2, width, dtype=torch.int64)
+    log_pages = {0: [2, 3], 1: [7, 4]}
+    kv_pages = {0: [5, 1], 1: [2, 7]}
+    for row in (0, 1):
+        for p in range(2):
+            state_table[row, p * page:(p + 1) * page] = log_pages[row][p]
+            page_table[row, p * page:(p + 1) * page] = kv_pages[row][p] * page + torch.arange(page)
+    ctx = Context(page_size=page, linear_state=pool, state_table=state_table.to(DEV),
+                  work_state_table=torch.tensor([[0], [1]], dtype=torch.int32, device=DEV), page_table=page_table.to(DEV))
+    backend = GatedDeltaLogStateBackend(ctx=ctx)
+    reqs = [Request(table_idx=0, cached_len=0, device_len=100), Request(table_idx=1, cached_len=32, device_len=69)]
+    lengths, cu = [100, 37], [0, 100, 137]
+    T = cu[-1]
+    rows = [0] * 100 + [1] * 37
+    positions = torch.tensor(list(range(100)) + list(range(32, 69)), dtype=torch.int32)
+    out_loc = page_table[torch.tensor(rows), positions.long()]
+    cache = LogStateCacheMetadata(checkpoint_writes=[(136, 6), (47, 5), (63, 8), (50, 9)],
+                                  checkpoint_ranges=[(0, 80, 90)])
+    batch = Batch(reqs=reqs, phase="prefill", cache_metadata=cache, positions=positions.to(DEV),
+                  out_loc=out_loc.to(DEV))
+    backend.prepare_metadata(batch)
+    meta = batch.linear_attn_metadata
+    # ---- the plan, token by token
+    offsets = (out_loc % page).tolist()
+    log_slots = [int(state_table[rows[t], int(positions[t])]) for t in range(T)]
+    want_log = [-1 if 80 <= t < 90 else log_slots[t] for t in range(T)]
+    want_conv, want_gran = [-1] * T, [0] * T
+    for n in range(2):
+        for r in range(lengths[n]):
+            t = cu[n] + r
+            if (offsets[t] + 1) % gran == 0 or r + 1 == lengths[n]:
+                want_conv[t], want_gran[t] = log_slots[t], offsets[t] // gran
+    for t in range(80, 90):
+        want_conv[t] = -1
+    for t, s, gr in [(136, 6, 3), (47, 5, 3), (63, 8, 0)]:
+        want_conv[t], want_gran[t] = s, gr
+    want_chunks = [-1] * (7 + 3)
+    want_chunks[2], want_chunks[3], want_chunks[7 + 2] = 5, 8, 6
+    assert meta.work_slots.tolist() == [0, 1]
+    assert meta.log_slots.tolist() == log_slots and meta.token_offsets.tolist() == offsets
+    assert meta.conv_read_slots.tolist() == [0, 7] and meta.conv_read_granules.tolist() == [0, 1]
+    assert meta.log_write_slots.tolist() == want_log
+    assert meta.conv_token_slots.tolist() == want_conv and meta.conv_token_granules.tolist() == want_gran
+    assert meta.chunk_write_slots.tolist() == want_chunks
+    assert meta.cu_seqlens.tolist() == cu
+    # ---- the prefill on that metadata
+    cfg = SimpleNamespace(key_dim=H * dk, value_dim=HV * dv, head_k_dim=dk, head_v_dim=dv, layer_idx=layer,
+                          state_len=W - 1, conv_dim=C, num_k_heads=H, num_v_heads=HV)
+    weight = (torch.randn(C, 1, W, generator=g) * 0.3).to(torch.bfloat16)
+    A_log, dt_bias = torch.randn(HV, generator=g) * 0.3, torch.randn(HV, generator=g) * 0.3
+    expected = storage.clone()
+    mixed = torch.randn(T, C, generator=g).to(torch.bfloat16)
+    gate, beta = torch.randn(T, HV, generator=g).to(torch.bfloat16), torch.randn(T, HV, generator=g).to(torch.bfloat16)
+    o_ref = ofr.forward_prefill_logstate(mixed, gate, beta, weight, A_log, dt_bias, expected, payload, decay, conv,
+                                         frame_bytes, head_bytes, record, layer=layer, layers=layers,
+                                         granularity=gran, page_size=page, cu_seqlens=cu,
+                                         work_slots=torch.tensor([0, 1]), conv_read_slots=torch.tensor([0, 7]),
+                                         conv_read_granules=[0, 1], conv_token_slots=torch.tensor(want_conv),
+                                         conv_token_granules=torch.tensor(want_gran),
+                                         chunk_write_slots=torch.tensor(want_chunks),
+                                         log_write_slots=torch.tensor(want_log), token_offsets=torch.tensor(offsets),
+                                         num_k_heads=H, head_k_dim=dk, num_v_heads=HV, head_v_dim=dv)
+    print("LogState metadata: prefill [100, 37 after 32 cached]", flush=True)
+    o = backend.forward(mixed.to(DEV), gate.to(DEV), beta.to(DEV), weight.to(DEV), A_log.to(DEV), dt_bias.to(DEV),
+                        cfg, batch)
+    torch.cuda.synchronize()
+    _report("prefill out", o, o_ref)
+    assert_bf16_close(o, o_ref)
+    # ---- one decode step through the capture buffers
+    backend.init_capture_graph(256, [2, 4])
+    dpos = torch.tensor([100, 69], dtype=torch.int32)
+    dloc = page_table[torch.tensor([0, 1]), dpos.long()]
+    dreqs = [Request(table_idx=0, cached_len=100, device_len=101), Request(table_idx=1, cached_len=69, device_len=70)]
+    dbatch = Batch(reqs=dreqs, phase="decode", cache_metadata=LogStateCacheMetadata(replay_counts=[0, 0]),
+                   positions=dpos.to(DEV), out_loc=dloc.to(DEV))
+    backend.prepare_for_capture(dbatch)
+    dmeta = dbatch.linear_attn_metadata
+    assert dmeta.work_slots.data_ptr() == backend.capture.work_slots.data_ptr()
+    dlogs = [int(state_table[0, 100]), int(state_table[1, 69])]
+    assert dmeta.log_slots.tolist() == dlogs and dmeta.token_offsets.tolist() == (dloc % page).tolist()
+    assert dmeta.conv_read_slots.tolist() == [0, 1] and dmeta.conv_read_granules.tolist() == [0, 0]
+    assert dmeta.replay_counts.tolist() == [0, 0]
+    x = torch.randn(2, C, generator=g).to(torch.bfloat16)
+    a, bt = torch.randn(2, HV, generator=g).to(torch.bfloat16), torch.randn(2, HV, generator=g).to(torch.bfloat16)
+    off = dloc % page
+    y = ofr.conv_decode_logstate(x, weight, expected, conv, frame_bytes, layer, torch.tensor([0, 1]),
+                                 torch.zeros(2, dtype=torch.int64), torch.tensor(dlogs), off // gran,
+                                 torch.tensor([0, 1]))
+    q, k, v = (y[:, :H * dk].reshape(2, 1, H, dk), y[:, H * dk:2 * H * dk].reshape(2, 1, H, dk),
+               y[:, 2 * H * dk:].reshape(2, 1, HV, dv))
+    o_ref = ofr.fused_recurrent_to_logstate(q, k, v, a[:, None], bt[:, None], A_log, dt_bias, expected, payload, decay,
+                                            frame_bytes, head_bytes, record, torch.tensor([0, 1]), torch.tensor(dlogs),
+                                            off, torch.tensor([0, 0]), layer=layer, layers=layers, granularity=gran,
+                                            page_size=page)
+    o = backend.forward(x.to(DEV), a.to(DEV), bt.to(DEV), weight.to(DEV), A_log.to(DEV), dt_bias.to(DEV), cfg, dbatch)
+    torch.cuda.synchronize()
+    _report("decode out", o, o_ref[:, 0])
+    assert_bf16_close(o, o_ref[:, 0])
+    host = dev_u8.cpu().view(torch.bfloat16).reshape(storage.shape)
+    for name, s in (("work", [0, 1]), ("checkpoints", [5, 6, 8])):
+        got = ofr.read_frame_states(host, payload, s, layer, HV, dk, dv, frame_bytes, head_bytes)
+        want = ofr.read_frame_states(expected, payload, s, layer, HV, dk, dv, frame_bytes, head_bytes)
+        _report(f"{name} states", got, want)
+        assert_state16_close(got, want)
