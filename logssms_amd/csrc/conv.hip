@@ -238,7 +238,11 @@ __global__ __launch_bounds__(256) void conv_vec_kernel(FrontParams fp) {
   if (t0 >= t1) return;  // whole block: padding rows only
   const int64_t key_dim = FRONT ? fp.H * DK : 0;
   float w[W][8], bias[8];
-  float win[S > 0 ? S : 1][8];
+  // The last S inputs live in a ring of W rows: at phase PH (the token's
+  // index mod W inside the tile, known at compile time through the unrolled
+  // loop below) tap i is row (PH + i) % W and the token's own input goes to
+  // row (PH + S) % W, so the window never moves between registers.
+  float ring[W][8];
   const bool scaled = !FRONT && (p.s0 != 1.f || p.s1 != 1.f || p.s2 != 1.f);
   float sc[8];
   if (active) {
@@ -269,24 +273,28 @@ __global__ __launch_bounds__(256) void conv_vec_kernel(FrontParams fp) {
     }
   }
   const T* x = static_cast<const T*>(p.x);
-  auto x_at = [&](int64_t t, float (&v)[8]) {
-    unpack8<T>(*reinterpret_cast<const uint4*>(x + t * p.xr + ch0), v);
+  auto x_raw = [&](int64_t t) { return *reinterpret_cast<const uint4*>(x + t * p.xr + ch0); };
+  auto x_unpack = [&](uint4 raw, float (&v)[8]) {
+    unpack8<T>(raw, v);
     if (scaled) {
 #pragma unroll
       for (int c = 0; c < 8; ++c) v[c] = round_to<T>(v[c] * sc[c]);
     }
   };
+  auto x_at = [&](int64_t t, float (&v)[8]) { x_unpack(x_raw(t), v); };
   int64_t r = find_sequence(p.cu, p.cu_is64, p.N, t0);
   int64_t begin = load_index(p.cu, r, p.cu_is64);
   int64_t end = load_index(p.cu, r + 1, p.cu_is64);
-  auto load_window = [&](int64_t t) {
+  auto load_window = [&](int64_t t, auto ph) {
+    constexpr int PH = decltype(ph)::value;
+#pragma unroll
     for (int i = 0; i < S; ++i) {
       const int64_t pos = t - S + i;
       if (pos >= begin) {
         float v[8];
         x_at(pos, v);
 #pragma unroll
-        for (int c = 0; c < 8; ++c) win[i][c] = v[c];
+        for (int c = 0; c < 8; ++c) ring[(PH + i) % W][c] = v[c];
       } else {
         const int j = static_cast<int>(pos - begin + S);
         const T* src;
@@ -299,21 +307,20 @@ __global__ __launch_bounds__(256) void conv_vec_kernel(FrontParams fp) {
                           : nullptr;
         }
 #pragma unroll
-        for (int c = 0; c < 8; ++c) win[i][c] = src ? to_f32(src[c * S]) : 0.f;
+        for (int c = 0; c < 8; ++c) ring[(PH + i) % W][c] = src ? to_f32(src[c * S]) : 0.f;
       }
     }
   };
-  // One token: conv of the window + current input, SiLU, snapshots, window
-  // shift, outputs.
-  auto token = [&](int64_t t, const float (&xv)[8]) __attribute__((always_inline)) {
-    // y = round(silu(round(sum_tap w x + b))), each stage over all 8 channels
-    // (independent exp / reciprocal latencies overlap)
-    float y[8], d[8];
+  // y = round(silu(round(sum_tap w x + b))) of the token at phase PH, each
+  // stage over all 8 channels (independent exp / reciprocal latencies overlap)
+  auto conv_silu = [&](const float (&xv)[8], float (&y)[8], auto ph) __attribute__((always_inline)) {
+    constexpr int PH = decltype(ph)::value;
+    float d[8];
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       float acc = bias[c];
 #pragma unroll
-      for (int i = 0; i < S; ++i) acc = fmaf(win[i][c], w[i][c], acc);
+      for (int i = 0; i < S; ++i) acc = fmaf(ring[(PH + i) % W][c], w[i][c], acc);
       y[c] = fmaf(xv[c], w[S][c], acc);
     }
     round8<T>(y);
@@ -324,34 +331,18 @@ __global__ __launch_bounds__(256) void conv_vec_kernel(FrontParams fp) {
 #pragma unroll
     for (int c = 0; c < 8; ++c) y[c] *= d[c];  // fast_silu
     round8<T>(y);
-    if (active && p.state) {  // window snapshots (raw inputs, oldest first)
-      const int64_t slot = p.token_slots ? load_index(p.token_slots, t, p.token_is64) : -1;
-      const int64_t fslot = (!FRONT && p.final_slots && t == end - 1) ? load_index(p.final_slots, r, p.final_is64) : -1;
-      for (int k = 0; k < 2; ++k) {
-        const int64_t s_ = k == 0 ? slot : fslot;
-        if (s_ < 0) continue;
-        T* dst = static_cast<T*>(p.state) + s_ * p.slot_stride + p.layer * p.layer_stride + ch0 * S;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-#pragma unroll
-          for (int i = 0; i + 1 < S; ++i) dst[c * S + i] = from_f32<T>(win[i + 1][c]);
-          dst[c * S + S - 1] = from_f32<T>(xv[c]);
-        }
-      }
-    }
-#pragma unroll
-    for (int i = 0; i + 1 < S; ++i)
-#pragma unroll
-      for (int c = 0; c < 8; ++c) win[i][c] = win[i + 1][c];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) win[S - 1][c] = xv[c];
+  };
+  // The outputs of token t (ALL: every lane of the block is active).
+  auto emit = [&](int64_t t, float (&y)[8], auto all) __attribute__((always_inline)) {
+    constexpr bool ALL = decltype(all)::value;
+    const bool on = ALL || active;
     if (FRONT) {
       // per-head sum of squares over DK / 8 lanes (heads start at multiples of DK)
       float ss = 0.f;
 #pragma unroll
       for (int c = 0; c < 8; ++c) ss = fmaf(y[c], y[c], ss);
       ss = head_sum<DK / 8>(ss);
-      if (active) {
+      if (on) {
         if (ch0 < 2 * key_dim) {
           // ss + 1e-6 is a normal float, so the hardware rsq needs no range scaling
           const float rn = __builtin_amdgcn_rsqf(ss + 1e-6f);
@@ -366,22 +357,66 @@ __global__ __launch_bounds__(256) void conv_vec_kernel(FrontParams fp) {
               pack8_io<T>(y);
         }
       }
-    } else if (active) {
+    } else if (on) {
       *reinterpret_cast<uint4*>(static_cast<T*>(p.out) + t * p.C + ch0) = pack8_io<T>(y);
     }
   };
-  if (active) load_window(t0);
-  for (int64_t t = t0; t < t1; ++t) {
+  // One token in general: sequence starts, snapshots, outputs.
+  auto token = [&](int64_t t, const float (&xv)[8], auto ph) __attribute__((always_inline)) {
+    constexpr int PH = decltype(ph)::value;
+    float y[8];
+    conv_silu(xv, y, ph);
+    if (active && p.state) {  // window snapshots (raw inputs, oldest first)
+      const int64_t slot = p.token_slots ? load_index(p.token_slots, t, p.token_is64) : -1;
+      const int64_t fslot = (!FRONT && p.final_slots && t == end - 1) ? load_index(p.final_slots, r, p.final_is64) : -1;
+      for (int k = 0; k < 2; ++k) {
+        const int64_t s_ = k == 0 ? slot : fslot;
+        if (s_ < 0) continue;
+        T* dst = static_cast<T*>(p.state) + s_ * p.slot_stride + p.layer * p.layer_stride + ch0 * S;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+#pragma unroll
+          for (int i = 0; i + 1 < S; ++i) dst[c * S + i] = from_f32<T>(ring[(PH + i + 1) % W][c]);
+          dst[c * S + S - 1] = from_f32<T>(xv[c]);
+        }
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) ring[(PH + S) % W][c] = xv[c];
+    emit(t, y, std::false_type{});
+  };
+  if (active) load_window(t0, std::integral_constant<int, 0>{});
+  // the input row of the next token is loaded one token ahead, so its HBM
+  // latency overlaps this token's arithmetic (inactive lanes keep zeros)
+  uint4 next = active ? x_raw(t0) : make_uint4(0, 0, 0, 0);
+  int64_t t = t0;
+  auto step = [&](auto ph) __attribute__((always_inline)) {
     while (t >= end) {  // next sequence (skips empty ones)
       ++r;
       begin = end;
       end = load_index(p.cu, r + 1, p.cu_is64);
-      if (t < end && active) load_window(t);
+      if (t < end && active) load_window(t, ph);
     }
-    float xv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (active) x_at(t, xv);
-    token(t, xv);
-  }
+    const uint4 cur = next;
+    if (active && t + 1 < t1) next = x_raw(t + 1);
+    float xv[8];
+    x_unpack(cur, xv);
+    token(t, xv, ph);
+    ++t;
+  };
+  // tokens go in groups of W, one per phase of the window ring
+  auto group = [&](auto... ph) __attribute__((always_inline)) { (step(ph), ...); };
+  auto tail = [&](auto... ph) __attribute__((always_inline)) { ((t < t1 ? step(ph) : void()), ...); };
+  auto phases = [&](auto f) __attribute__((always_inline)) {
+    if constexpr (W == 2) f(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
+    else if constexpr (W == 3)
+      f(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}, std::integral_constant<int, 2>{});
+    else
+      f(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}, std::integral_constant<int, 2>{},
+        std::integral_constant<int, 3>{});
+  };
+  while (t + W <= t1) phases(group);
+  phases(tail);
   if (FRONT && blockIdx.y == 0 && fp.g_out) {
     const int n = static_cast<int>(t1 - t0);
     for (int idx = threadIdx.x; idx < n * fp.HV; idx += 256) {
