@@ -502,6 +502,172 @@ def rmw_sweep(dev, steps, warmup, nbytes=2 << 30):
             "frac_hbm": best["GB/s"] * 1e9 / PEAK_HBM, "runs": runs}
 
 
+# ---------------------------------------------------------------- LogState
+
+LS_PAGE, LS_GRAN, LS_FRAME = 256, 32, 65536
+LS_HEAD = D * D * 2  # bf16 state head
+
+
+def make_frame_pool(dev, slots, seed=8):
+    """A LogState frame storage at Qwen3-Next shape (one linear layer, bf16):
+    64 KiB frames drawn at random for every slot's payload (states and the
+    page's token log), one decay record per slot, one conv snapshot frame per
+    (slot, granule); page 256, granularity 32."""
+    from types import SimpleNamespace
+    g = torch.Generator().manual_seed(seed)
+    layers = 1
+    fps = max(-(-layers * HV * LS_HEAD // LS_FRAME), -(-2 * LS_PAGE * layers * (H * D + HV * D) // LS_FRAME))
+    record = 4 * layers * LS_PAGE * HV
+    per = LS_FRAME // record
+    n_dec = -(-slots // per)
+    granules = LS_PAGE // LS_GRAN
+    cf = -(-2 * layers * CONV_DIM * (W - 1) // LS_FRAME)
+    total = slots * fps + n_dec + slots * granules * cf
+    order = torch.randperm(total, generator=g)
+    payload = order[:slots * fps].reshape(slots, fps).to(torch.int32)
+    dec = order[slots * fps:slots * fps + n_dec]
+    decay = torch.tensor([[int(dec[s // per]), s % per] for s in range(slots)], dtype=torch.int32)
+    conv = order[slots * fps + n_dec:].reshape(slots, granules, cf).to(torch.int32)
+    storage = torch.empty(total, LS_FRAME, dtype=torch.uint8, device=dev)
+    storage.view(torch.bfloat16).normal_(0.0, 0.05, generator=torch.Generator(device=dev).manual_seed(seed))
+    # decay records hold gates (natural-log decays <= 0)
+    rec = storage[dec.to(dev)].view(torch.float32)
+    rec.copy_(-torch.rand(rec.shape, device=dev) * 0.1)
+    storage[dec.to(dev)] = rec.view(torch.uint8)
+    layout = SimpleNamespace(head_k_dim=D, head_v_dim=D, num_value_heads=HV, num_key_heads=H, num_linear_layers=layers,
+                             granularity=LS_GRAN, log_decay_bytes=record, num_granules=granules,
+                             conv_dim=CONV_DIM, state_len=W - 1)
+    return SimpleNamespace(storage=storage, dtype=torch.bfloat16, frame_bytes=LS_FRAME, head_payload_bytes=LS_HEAD,
+                           page_size=LS_PAGE, payload_frame_table=payload.to(dev), decay_frame_table=decay.to(dev),
+                           conv_frame_table=conv.to(dev), layout=layout)
+
+
+def logstate_decode_bytes(counts, flush):
+    """Algorithmic HBM bytes of one LogState recurrence launch: per sequence
+    the bf16 work state, the replayed log rows (v' and gate per v-head, key
+    per key head), the step's log row, the state write-back on flush steps,
+    the q/k/v/gate/beta inputs and the output."""
+    row = HV * (2 * D + 4) + H * 2 * D
+    total = 0
+    for n, f in zip(counts, flush):
+        total += HV * LS_HEAD + n * row + row + (HV * LS_HEAD if f else 0)
+        total += 2 * (2 * H * D + HV * D) + 2 * 2 * HV + 2 * HV * D
+    return total
+
+
+def logstate_gpu(dev, steps, warmup, B=256):
+    """LogState decode (config 3 batch, replay counts pos % 16), the LogState
+    chunked prefill (config 2 lengths at granularity 32 with frame-table
+    states and the token log) and state reconstruction from logged pages."""
+    from types import SimpleNamespace
+    from logssms_amd.kernel.linear_attention import (
+        ChunkLogIO, ChunkStateIO, chunk_gated_delta_rule_to_cache, conv_decode,
+        fused_recurrent_gated_delta_rule_to_logstate, restore_log_state_chains)
+    out = {}
+    g = torch.Generator().manual_seed(9)
+    pool = make_frame_pool(dev, 2 * B)
+    cfg = SimpleNamespace(state_len=W - 1, conv_dim=CONV_DIM, num_k_heads=H, head_k_dim=D, num_v_heads=HV,
+                          head_v_dim=D, key_dim=H * D, layer_idx=0)
+    works = torch.arange(B, dtype=torch.int32, device=dev)
+    logs = torch.arange(B, 2 * B, dtype=torch.int32, device=dev)
+    pos = torch.randint(0, LS_PAGE, (B,), generator=g, dtype=torch.int32)
+    counts = pos % 16
+    flush = ((pos + 1) % 16 == 0).tolist()
+    pos_d, counts_d = pos.to(dev), counts.to(dev)
+    zeros = torch.zeros(B, dtype=torch.int32, device=dev)
+    gran = (pos // LS_GRAN).to(dev)
+    mixed = torch.randn(B, CONV_DIM, generator=g).to(torch.bfloat16).to(dev)
+    gate = torch.randn(B, 1, HV, generator=g).to(torch.bfloat16).to(dev)
+    beta = torch.randn(B, 1, HV, generator=g).to(torch.bfloat16).to(dev)
+    weight = (torch.randn(CONV_DIM, 1, W, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    A_log = (-torch.rand(HV, generator=g)).to(dev)
+    dt_bias = torch.zeros(HV, device=dev)
+    o = torch.empty(B, 1, HV, D, dtype=torch.bfloat16, device=dev)
+    qkv = conv_decode(mixed, weight, cfg, split_qkv=True, read_slots=works, write_slots=logs, pool=pool,
+                      read_granules=zeros, write_granules=gran, work_slots=works)
+
+    def conv_step():
+        conv_decode(mixed, weight, cfg, split_qkv=True, read_slots=works, write_slots=logs, pool=pool,
+                    read_granules=zeros, write_granules=gran, work_slots=works)
+
+    def rec_step():
+        fused_recurrent_gated_delta_rule_to_logstate(*qkv, gate, beta, A_log, dt_bias, pool, works, logs, pos_d, 0,
+                                                      counts_d, out=o)
+
+    conv_ms = _time(conv_step, max(steps, 20), warmup)
+    rec_ms = _time(rec_step, max(steps, 20), warmup)
+    rb = logstate_decode_bytes(counts.tolist(), flush)
+    cb = B * (CONV_DIM * 2 + 3 * (W - 1) * CONV_DIM * 2 + CONV_DIM * 2) + CONV_DIM * W * 2
+    out["decode"] = {
+        "config": f"{B} seqs at random page positions (replay counts pos % 16, mean {float(counts.float().mean()):.1f}), "
+                  "bf16 frame storage, 64 KiB frames drawn at random, page 256, granularity 32",
+        "ms": conv_ms + rec_ms, "recurrence_ms": rec_ms, "recurrence_bytes": rb,
+        "recurrence_GB/s": rb / (rec_ms * 1e-3) / 1e9, "recurrence_frac_hbm": rb / (rec_ms * 1e-3) / PEAK_HBM,
+        "conv_ms": conv_ms, "conv_bytes": cb, "conv_GB/s": cb / (conv_ms * 1e-3) / 1e9}
+    del qkv, o
+    # state reconstruction: one task per sequence, base = its work slot, one full logged page
+    tasks = [(int(works[i]), [(int(logs[i]), 0, LS_PAGE)], int(works[(i + 1) % B])) for i in range(0, B, 2)]
+    rs_ms = _time(lambda: restore_log_state_chains(pool, tasks), max(steps // 2, 5), warmup)
+    heads = len(tasks) * HV
+    rs_bytes = heads * (2 * LS_HEAD + LS_PAGE * (2 * D + 4)) + len(tasks) * H * LS_PAGE * 2 * D
+    rs_flop = heads * LS_PAGE * 2 * D * D
+    out["restore"] = {"config": f"{len(tasks)} chains, base state + one logged page of {LS_PAGE} tokens, 32 v-heads",
+                      "ms": rs_ms, "bytes": rs_bytes, "GB/s": rs_bytes / (rs_ms * 1e-3) / 1e9,
+                      "flop": rs_flop, "TFLOP/s": rs_flop / (rs_ms * 1e-3) / 1e12}
+    del pool
+    torch.cuda.empty_cache()
+    # prefill: config 2 lengths, frame-table states read from and written to work slots,
+    # checkpoints every 1024 tokens, every token logged into its page's log slot
+    lengths = [4096] * 4
+    T = sum(lengths)
+    pages = T // LS_PAGE
+    n_int = T // LS_GRAN
+    ppool = make_frame_pool(dev, 4 + pages + 16, seed=10)
+    q = torch.nn.functional.normalize(torch.randn(1, T, H, D, generator=g), dim=-1).to(torch.bfloat16).to(dev)
+    k = torch.nn.functional.normalize(torch.randn(1, T, H, D, generator=g), dim=-1).to(torch.bfloat16).to(dev)
+    v = torch.randn(1, T, HV, D, generator=g).to(torch.bfloat16).to(dev)
+    gg = (-torch.rand(1, T, HV, generator=g) * 0.1).to(dev)
+    bb = torch.rand(1, T, HV, generator=g).to(dev)
+    cu = torch.tensor([0, 4096, 8192, 12288, 16384], dtype=torch.int32, device=dev)
+    work = torch.arange(4, dtype=torch.int32, device=dev)
+    chunk_writes = torch.full((n_int,), -1, dtype=torch.int32)
+    per_seq = 4096 // LS_GRAN
+    for n in range(4):
+        for j in range(1, 4):
+            chunk_writes[n * per_seq + j * (1024 // LS_GRAN) - 1] = 4 + pages + 4 * n + j - 1
+    tok = torch.arange(T)
+    log_slots = (4 + tok // LS_PAGE).to(torch.int32).to(dev)
+    offsets = (tok % LS_PAGE).to(torch.int32).to(dev)
+    io = ChunkStateIO(storage=ppool.storage.view(torch.bfloat16), read_slots=work,
+                      chunk_write_slots=chunk_writes.to(dev), final_write_slots=work,
+                      payload_frames=ppool.payload_frame_table, frame_bytes=LS_FRAME, head_payload_bytes=LS_HEAD,
+                      layer=0, num_layers=1, granularity=LS_GRAN, page_size=LS_PAGE)
+    log = ChunkLogIO(slots=log_slots, token_offsets=offsets, decay_frames=ppool.decay_frame_table, gate=gg,
+                     page_size=LS_PAGE, decay_record_bytes=ppool.layout.log_decay_bytes, num_key_heads=H)
+    ev = []
+
+    def prefill_step():
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        chunk_gated_delta_rule_to_cache(q, k, v, gg, bb, io, cu, chunk_size=LS_GRAN, log_io=log)
+        b.record()
+        ev.append((a, b))
+
+    pf_ms = _time(prefill_step, max(steps // 2, 5), warmup)
+    pf_kernel = _kernel_ms(ev)
+    flops = FLOP_PER_TOKEN_HEAD * T * HV
+    out["prefill"] = {
+        "config": "BASELINE config 2 lengths (4 x 4096), bf16 frame-table states in and out of work slots, "
+                  "checkpoints every 1024 tokens, granularity 32, every token logged (v', key, gate)",
+        "ms": pf_ms, "tokens/s": T / (pf_ms * 1e-3), "chunk_and_log_ms": pf_kernel,
+        "chunk_tflops": flops / (pf_kernel * 1e-3) / 1e12,
+        "frac_mfma": flops / (pf_kernel * 1e-3) / PEAK_MFMA_16BIT}
+    del ppool, io, log
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -511,7 +677,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="time budget of each CPU baseline leg (chunked prefill; naive prefill, decode and "
                          "verify get a share of it)")
-    ap.add_argument("--only", choices=["all", "prefill", "decode", "verify", "norm", "layer", "copy", "rmw"],
+    ap.add_argument("--only", choices=["all", "prefill", "decode", "verify", "norm", "layer", "logstate", "copy",
+                                       "rmw"],
                     default="all",
                     help="'copy' times a plain 512 MiB device copy (the calibration kernel for the "
                          "FETCH_SIZE / WRITE_SIZE counter passes); 'rmw' the in-place read-modify-write "
@@ -644,9 +811,11 @@ def main():
             "ms": ms, "tokens/s": T / (ms * 1e-3), "stage_ms": stages}
         del step, parts
         torch.cuda.empty_cache()
+    if args.only in ("all", "logstate"):
+        extra["logstate"] = logstate_gpu(dev, args.steps, args.warmup)
     if not result:
         keys = [k for k in ("decode", "verify", "rms_norm_gated") if k in extra]
-        if not keys:  # --only layer
+        if not keys:  # --only layer / logstate
             print(json.dumps({"extra": extra}))
             return
         key = keys[0]

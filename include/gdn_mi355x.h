@@ -11,7 +11,8 @@
  *     gdn_last_error() (thread-local).  Nothing throws across the ABI.
  *
  * Index arrays (slots, cu_seqlens, ...) may be int32 or int64 (GDN_I32 /
- * GDN_I64).  Negative slots are sentinels: a negative read slot means "zero
+ * GDN_I64); int64 entries must lie in the int32 range (the kernels read
+ * their low word).  Negative slots are sentinels: a negative read slot means "zero
  * state" where the reference does so, a negative write slot means "skip".
  * Element types are GDN_F32, GDN_BF16 or GDN_F16.
  *

@@ -56,9 +56,30 @@ __device__ __forceinline__ float load_any(const void* p, int64_t i, int dtype) {
   }
 }
 
+// Entry i of an int32 or int64 index array.  An int64 entry is read as its
+// low (little-endian) word, sign-extended: one 4-byte load either way, with
+// no branch on the width, so consecutive index loads issue back to back
+// instead of each waiting behind a branch.  int64 entries must therefore lie
+// in the int32 range (slots, frames, token offsets and sentinels do).
 __device__ __forceinline__ int64_t load_index(const void* p, int64_t i, int is64) {
-  return is64 ? static_cast<const int64_t*>(p)[i] : static_cast<int64_t>(static_cast<const int32_t*>(p)[i]);
+  return static_cast<int64_t>(static_cast<const int32_t*>(p)[is64 ? 2 * i : i]);
 }
+
+// x / d and x % d for 0 <= x < 2^32: a shift and a mask when d is a power of
+// two (frame sizes, granularities), a 32-bit division otherwise -- never the
+// long 64-bit division sequence.  The host checks that the offsets fit.
+struct Div32 {
+  uint32_t d;
+  int32_t shift;  // >= 0: d == 1 << shift; -1: general divisor
+  __device__ __forceinline__ uint32_t div(uint32_t x) const { return shift >= 0 ? x >> shift : x / d; }
+  __device__ __forceinline__ uint32_t mod(uint32_t x) const { return shift >= 0 ? x & (d - 1) : x % d; }
+};
+inline Div32 make_div32(int64_t d) {
+  Div32 v{static_cast<uint32_t>(d > 0 ? d : 1), -1};
+  if (d > 0 && (d & (d - 1)) == 0) v.shift = __builtin_ctzll(static_cast<unsigned long long>(d));
+  return v;
+}
+constexpr int64_t kMaxOffset32 = int64_t{1} << 32;
 
 // Sequence of packed row t: the largest r < n with cu[r] <= t (cu is
 // non-decreasing with cu[0] = 0, so empty sequences are skipped).

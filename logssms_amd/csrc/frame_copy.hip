@@ -42,19 +42,22 @@ struct FrameCopyParams {
   int64_t length;                  // bytes per task
   int64_t layer, HV, head_bytes;
   int64_t tasks, spans;            // spans of kSpanBytes per task
+  Div32 fdiv;                      // frame_bytes
 };
 
 // Frame byte address of logical byte x of table row `row`, or null.
 __device__ __forceinline__ char* frame_byte(const FrameCopyParams& p, int64_t row, int64_t per_row, int64_t x) {
-  const int64_t fr = load_index(p.table, row * per_row + x / p.frame_bytes, p.table_is64);
+  const uint32_t x32 = static_cast<uint32_t>(x);  // < per_row frame_bytes < 2^32 (checked by the host)
+  const int64_t fr = load_index(p.table, row * per_row + p.fdiv.div(x32), p.table_is64);
   if (fr < 0 || fr >= p.num_frames) return nullptr;
-  return p.storage + fr * p.frame_bytes + x % p.frame_bytes;
+  return p.storage + fr * p.frame_bytes + p.fdiv.mod(x32);
 }
 
 template <class U>
 __global__ __launch_bounds__(kCopyThreads) void frame_copy_kernel(FrameCopyParams p, int mode) {
-  const int64_t task = blockIdx.x / p.spans;
-  const int64_t span = blockIdx.x % p.spans;
+  const uint32_t bid = blockIdx.x, nspans = static_cast<uint32_t>(p.spans);
+  const int64_t task = bid / nspans;
+  const int64_t span = bid % nspans;
   // destination row / start, and source (frames or linear rows)
   int64_t dst_row, dst_start, per_row;
   int64_t src_row = -1;
@@ -95,6 +98,9 @@ __global__ __launch_bounds__(kCopyThreads) void frame_copy_kernel(FrameCopyParam
 }
 
 int launch_frame_copy(FrameCopyParams& p, int mode, bool aligned16, hipStream_t stream, const char* who) {
+  GDN_REQUIRE((mode == kStoreStates ? p.fps : p.CF) * p.frame_bytes < kMaxOffset32, "%s: a row's frames exceed 4 GiB",
+              who);
+  p.fdiv = make_div32(p.frame_bytes);
   p.spans = (p.length + kSpanBytes - 1) / kSpanBytes;
   const int64_t blocks = p.tasks * p.spans;
   if (blocks == 0) return GDN_OK;

@@ -53,6 +53,7 @@ struct LogParams {
   int decay_is64;
   int64_t record_bytes;
   int64_t layer, layers, gran, page;
+  Div32 fdiv, gdiv;  // frame_bytes, gran
 };
 
 // Address of element `col` of log row `index` (a value head, or a logged key
@@ -62,12 +63,13 @@ __device__ __forceinline__ uint16_t* log_element(const LogParams& p, int64_t slo
   const int64_t key_size = p.gran * p.KH * p.K;
   const int64_t layer_size = key_size + p.gran * p.HV * p.V;
   const int64_t dim = value ? p.V : p.K;
-  const int64_t elem = (pos / p.gran * p.layers + p.layer) * layer_size + (value ? key_size : 0) +
-                       (index * p.gran + pos % p.gran) * dim + col;
-  const int64_t byte = 2 * elem;
-  const int64_t fr = load_index(p.frames, slot * p.fps + byte / p.frame_bytes, p.frames_is64);
+  const uint32_t ps = static_cast<uint32_t>(pos);
+  const int64_t elem = (p.gdiv.div(ps) * p.layers + p.layer) * layer_size + (value ? key_size : 0) +
+                       (index * p.gran + p.gdiv.mod(ps)) * dim + col;
+  const uint32_t byte = static_cast<uint32_t>(2 * elem);
+  const int64_t fr = load_index(p.frames, slot * p.fps + p.fdiv.div(byte), p.frames_is64);
   if (fr < 0 || fr >= p.num_frames) return nullptr;
-  return reinterpret_cast<uint16_t*>(p.storage + fr * p.frame_bytes + byte % p.frame_bytes);
+  return reinterpret_cast<uint16_t*>(p.storage + fr * p.frame_bytes + p.fdiv.mod(byte));
 }
 
 // grid (T, HV)
@@ -99,6 +101,36 @@ __global__ __launch_bounds__(kThreads) void chunk_log_kernel(LogParams p) {
   }
 }
 
+// grid (T): one 256-thread block per token moves all its log rows in 16-byte
+// pieces (v' rows of every value head, the logged key rows) and its gates.
+// Needs dk, dv multiples of 8, frames a multiple of 16 bytes and 16-byte
+// aligned sources (checked by the host); a piece never straddles two frames.
+constexpr int kLogThreads = 256;
+__global__ __launch_bounds__(kLogThreads) void chunk_log_vec_kernel(LogParams p) {
+  const int64_t t = blockIdx.x;
+  const int64_t slot = load_index(p.slots, t, p.slots_is64);
+  const int64_t pos = load_index(p.offsets, t, p.offsets_is64);
+  if (slot < 0 || pos < 0 || pos >= p.page) return;
+  const int64_t vv = p.V / 8, kv = p.K / 8;
+  const int64_t group = p.HV / p.KH;  // value heads per logged key head
+  const int64_t nval = p.HV * vv, total = nval + p.KH * kv;
+  for (int64_t i = threadIdx.x; i < total; i += kLogThreads) {
+    const bool value = i < nval;
+    const int64_t j = value ? i : i - nval;
+    const int64_t row = j / (value ? vv : kv), col = 8 * (j % (value ? vv : kv));
+    const uint16_t* src = value ? p.v_new + (t * p.HV + row) * p.V + col
+                                : p.key + (t * p.H + row * group / (p.HV / p.H)) * p.K + col;
+    uint16_t* d = log_element(p, slot, pos, row, col, value);
+    if (d) *reinterpret_cast<uint4*>(d) = *reinterpret_cast<const uint4*>(src);
+  }
+  const int64_t fr = load_index(p.decay, 2 * slot, p.decay_is64);
+  const int64_t rec = load_index(p.decay, 2 * slot + 1, p.decay_is64);
+  if (fr >= 0 && fr < p.num_frames && rec >= 0 && (rec + 1) * p.record_bytes <= p.frame_bytes) {
+    float* d = reinterpret_cast<float*>(p.storage + fr * p.frame_bytes + rec * p.record_bytes);
+    for (int64_t h = threadIdx.x; h < p.HV; h += kLogThreads) d[(p.layer * p.page + pos) * p.HV + h] = p.gate[t * p.HV + h];
+  }
+}
+
 // ---------------------------------------------------------------- LogState decode
 
 constexpr int kReplayWindow = 16;  // cache/logstate/layout.py:8
@@ -111,9 +143,16 @@ __device__ __forceinline__ T* conv_element(T* storage, const void* table, int is
                                            int64_t e, int64_t granules, int64_t cf, int64_t fe, int64_t num_frames) {
   if (slot < 0) return nullptr;
   const int64_t row = slot * granules + granule;
-  const int64_t fr = cf == 1 ? load_index(table, row, is64) : load_index(table, row * cf + e / fe, is64);
+  if (cf == 1) {
+    const int64_t fr = load_index(table, row, is64);
+    if (fr < 0 || fr >= num_frames) return nullptr;
+    return storage + fr * fe + e;
+  }
+  // e < layers C S and fe fit 32 bits (checked by the host)
+  const uint32_t e32 = static_cast<uint32_t>(e), fe32 = static_cast<uint32_t>(fe);
+  const int64_t fr = load_index(table, row * cf + e32 / fe32, is64);
   if (fr < 0 || fr >= num_frames) return nullptr;
-  return storage + fr * fe + (cf == 1 ? e : e % fe);
+  return storage + fr * fe + e32 % fe32;
 }
 
 struct ConvFrameParams {
@@ -248,6 +287,7 @@ struct LogDecodeParams {
   int eager;
   void* out;
   float scale;
+  Div32 fdiv, gdiv;  // frame_bytes, gran
 };
 
 // Element (row, col) of the state of value head h in slot s: logical byte
@@ -256,10 +296,10 @@ struct LogDecodeParams {
 template <class T>
 __device__ __forceinline__ T* state_row(const LogDecodeParams& p, int64_t s, int64_t h, int64_t row, int DV) {
   if (s < 0) return nullptr;
-  const int64_t x = (p.layer * p.HV + h) * p.head_bytes + row * DV * static_cast<int64_t>(sizeof(T));
-  const int64_t fr = load_index(p.frames, s * p.fps + x / p.frame_bytes, p.frames_is64);
+  const uint32_t x = static_cast<uint32_t>((p.layer * p.HV + h) * p.head_bytes + row * DV * static_cast<int64_t>(sizeof(T)));
+  const int64_t fr = load_index(p.frames, s * p.fps + p.fdiv.div(x), p.frames_is64);
   if (fr < 0 || fr >= p.num_frames) return nullptr;
-  return reinterpret_cast<T*>(p.storage + fr * p.frame_bytes + x % p.frame_bytes);
+  return reinterpret_cast<T*>(p.storage + fr * p.frame_bytes + p.fdiv.mod(x));
 }
 
 // 16-bit log element (the log layout of chunk_log_kernel, key heads = H).
@@ -268,12 +308,13 @@ __device__ __forceinline__ T* decode_log(const LogDecodeParams& p, int64_t slot,
                                          int64_t col, bool value, int DK, int DV) {
   const int64_t key_size = p.gran * p.H * DK;
   const int64_t layer_size = key_size + p.gran * p.HV * DV;
-  const int64_t elem = (pos / p.gran * p.layers + p.layer) * layer_size + (value ? key_size : 0) +
-                       (index * p.gran + pos % p.gran) * (value ? DV : DK) + col;
-  const int64_t byte = 2 * elem;
-  const int64_t fr = load_index(p.frames, slot * p.fps + byte / p.frame_bytes, p.frames_is64);
+  const uint32_t ps = static_cast<uint32_t>(pos);
+  const int64_t elem = (p.gdiv.div(ps) * p.layers + p.layer) * layer_size + (value ? key_size : 0) +
+                       (index * p.gran + p.gdiv.mod(ps)) * (value ? DV : DK) + col;
+  const uint32_t byte = static_cast<uint32_t>(2 * elem);
+  const int64_t fr = load_index(p.frames, slot * p.fps + p.fdiv.div(byte), p.frames_is64);
   if (fr < 0 || fr >= p.num_frames) return nullptr;
-  return reinterpret_cast<T*>(p.storage + fr * p.frame_bytes + byte % p.frame_bytes);
+  return reinterpret_cast<T*>(p.storage + fr * p.frame_bytes + p.fdiv.mod(byte));
 }
 
 __device__ __forceinline__ float wave_sum(float x) {
@@ -282,23 +323,64 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-// grid (batch x HV); 256 threads hold the dk x dv state as RPT rows x 4
-// columns each (columns 4 (tid % (dv / 4)) .. + 3).
-template <int DK, int DV, class T>
-__global__ __launch_bounds__(kDecodeThreads) void logstate_decode_kernel(LogDecodeParams p) {
-  constexpr int CG = DV / 4, RG = kDecodeThreads / CG, RPT = DK / RG;
-  static_assert(RPT >= 1 && DK % RG == 0, "state split");
-  const int64_t b = blockIdx.x / p.HV, h = blockIdx.x % p.HV;
+// Barrier for LDS traffic only: global loads in flight stay in flight.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Two 16-bit values of a dword as floats, and back (round to nearest even).
+template <class T> __device__ __forceinline__ void split2(uint32_t w, float& a, float& b);
+template <> __device__ __forceinline__ void split2<bf16>(uint32_t w, float& a, float& b) {
+  a = __uint_as_float(w << 16);
+  b = __uint_as_float(w & 0xffff0000u);
+}
+template <> __device__ __forceinline__ void split2<f16>(uint32_t w, float& a, float& b) {
+  const f16* h = reinterpret_cast<const f16*>(&w);
+  a = static_cast<float>(h[0]);
+  b = static_cast<float>(h[1]);
+}
+
+// N = 4 or 8 consecutive 16-bit values as N / 2 dwords.
+template <int N> __device__ __forceinline__ void load_words(const void* src, uint32_t (&w)[N / 2]) {
+  if constexpr (N == 8) {
+    const uint4 v = *reinterpret_cast<const uint4*>(src);
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+  } else {
+    const uint2 v = *reinterpret_cast<const uint2*>(src);
+    w[0] = v.x; w[1] = v.y;
+  }
+}
+template <int N> __device__ __forceinline__ void store_words(void* dst, const uint32_t (&w)[N / 2]) {
+  if constexpr (N == 8)
+    *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+  else
+    *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
+}
+
+// grid (batch x HV); NT threads hold the dk x dv state as RPT rows x CPT
+// columns each (columns CPT (tid % (dv / CPT)) .. + CPT - 1), moved with 8- or
+// 16-byte accesses.  Every global load (state rows, q / k, gates, replayed
+// gates and rows) is issued before the first wait, so one HBM latency covers
+// them all; values the whole block needs (norms, gates, suffix decays) are
+// computed redundantly per wave instead of broadcast through LDS, and the
+// column reductions run inside each wave before one LDS exchange across
+// waves.  Only the LDS exchanges need barriers (lgkmcnt only).
+template <int DK, int DV, class T, int NT>
+__global__ __launch_bounds__(NT) void logstate_decode_kernel(LogDecodeParams p) {
+  constexpr int CPT = DK * DV >= 8 * NT ? 8 : 4;
+  constexpr int CG = DV / CPT, RG = NT / CG, RPT = DK / RG, NW = CPT / 2;
+  constexpr int WAVES = NT / 64;
+  constexpr int KV = DK / 8, VV = DV / 8;        // 16-byte pieces per row
+  constexpr int PIECES = (kReplayWindow * (KV + VV) + NT - 1) / NT;
+  static_assert(RPT >= 1 && DK % RG == 0 && DV % CPT == 0 && 64 % CG == 0, "state split");
+  static_assert((DK <= 128 && DK % 64 == 0) || DK == 32, "q/k norm lanes");
+  const uint32_t bid = blockIdx.x, nhv = static_cast<uint32_t>(p.HV);
+  const int64_t b = bid / nhv, h = bid % nhv;
   const int64_t group = p.HV / p.H, kh = h / group;
-  const int tid = threadIdx.x, cg = tid % CG, rg = tid / CG;
-  const int c0 = 4 * cg, r0 = rg * RPT;
-  __shared__ float s_q[DK], s_k[DK], s_delta[DV];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, cg = tid % CG, rg = tid / CG;
+  const int c0 = CPT * cg, r0 = rg * RPT;
+  __shared__ float s_delta[DV];
   __shared__ float s_keys[kReplayWindow][DK];
   __shared__ float s_vals[kReplayWindow][DV];
-  __shared__ float s_red[2][RG][DV];
-  __shared__ float s_part[4][3];
-  __shared__ float s_suffix[kReplayWindow];
-  __shared__ float s_scal[6];  // kq, g, decay, beta, e^{sum g}, replay count
+  __shared__ float s_red[2][WAVES][DV];
 
   const int64_t w = load_index(p.work, b, p.work_is64);
   const int64_t ls = load_index(p.logs, b, p.logs_is64);
@@ -307,8 +389,7 @@ __global__ __launch_bounds__(kDecodeThreads) void logstate_decode_kernel(LogDeco
   int64_t n = p.eager || !in_page ? 0 : load_index(p.counts, b, p.counts_is64);
   n = n < 0 ? 0 : (n > kReplayWindow ? kReplayWindow : n);
   n = n > pos ? pos : n;  // the logged tokens precede the position within the page
-  // decay record of the log slot
-  float* rec = nullptr;
+  float* rec = nullptr;  // decay record of the log slot
   if (in_page) {
     const int64_t fr = load_index(p.decay, 2 * ls, p.decay_is64);
     const int64_t ri = load_index(p.decay, 2 * ls + 1, p.decay_is64);
@@ -316,158 +397,237 @@ __global__ __launch_bounds__(kDecodeThreads) void logstate_decode_kernel(LogDeco
       rec = reinterpret_cast<float*>(p.storage + fr * p.frame_bytes + ri * p.record_bytes);
   }
   if (!rec) n = 0;
+  // Loads go to a valid address whatever the slot (an unmapped row reads the
+  // storage's first bytes and is discarded), so no branch separates them.
+  const T* const safe = reinterpret_cast<const T*>(p.storage);
 
-  // ---- q, k (L2 norm), the gates
-  {
-    float qv = 0.f, kv = 0.f;
-    if (tid < DK) {
-      qv = to_f32(static_cast<const T*>(p.q)[(b * p.H + kh) * DK + tid]);
-      kv = to_f32(static_cast<const T*>(p.k)[(b * p.H + kh) * DK + tid]);
-    }
-    const float qq = wave_sum(qv * qv), kk = wave_sum(kv * kv), qk = wave_sum(qv * kv);
-    if ((tid & 63) == 0) {
-      s_part[tid >> 6][0] = qq;
-      s_part[tid >> 6][1] = kk;
-      s_part[tid >> 6][2] = qk;
-    }
-    __syncthreads();
-    const float sqq = s_part[0][0] + s_part[1][0] + s_part[2][0] + s_part[3][0];
-    const float skk = s_part[0][1] + s_part[1][1] + s_part[2][1] + s_part[3][1];
-    const float sqk = s_part[0][2] + s_part[1][2] + s_part[2][2] + s_part[3][2];
-    const float rq = rsqrtf(sqq + 1e-6f) * p.scale, rk = rsqrtf(skk + 1e-6f);
-    if (tid < DK) {
-      s_q[tid] = qv * rq;
-      s_k[tid] = kv * rk;
-    }
-    if (tid == 0) {
-      const float a = load_any(p.A_log, h, p.a_dtype);
-      const float bias = load_any(p.dt_bias, h, p.dt_dtype);
-      const float gv = load_any(p.gate, b * p.gate_b + h * p.gate_h, p.gate_dtype);
-      const float bv = load_any(p.beta, b * p.beta_b + h * p.beta_h, p.beta_dtype);
-      const float g = -expf(a) * softplus_decode(gv + bias);
-      s_scal[0] = sqk * rq * rk;
-      s_scal[1] = g;
-      s_scal[2] = expf(g);
-      s_scal[3] = sigmoid(bv);
-      // replay decays: e^{sum g} and the suffix factors e^{sum_{j > i} g_j}
-      float total = 0.f;
-      for (int i = 0; i < n; ++i) total += rec[(p.layer * p.page + pos - n + i) * p.HV + h];
-      float prefix = 0.f;
-      for (int i = 0; i < n; ++i) {
-        prefix += rec[(p.layer * p.page + pos - n + i) * p.HV + h];
-        s_suffix[i] = expf(total - prefix);
-      }
-      s_scal[4] = expf(total);
-    }
-    __syncthreads();
-  }
-  // ---- stage the replayed rows: keys, and values scaled by their suffix decay
-  for (int64_t idx = tid; idx < n * DK; idx += kDecodeThreads) {
-    const int64_t i = idx / DK, col = idx % DK;
-    const T* e = decode_log<T>(p, ls, pos - n + i, kh, col, false, DK, DV);
-    s_keys[i][col] = e ? to_f32(*e) : 0.f;
-  }
-  for (int64_t idx = tid; idx < n * DV; idx += kDecodeThreads) {
-    const int64_t i = idx / DV, col = idx % DV;
-    const T* e = decode_log<T>(p, ls, pos - n + i, h, col, true, DK, DV);
-    s_vals[i][col] = e ? round_to<T>(to_f32(*e) * s_suffix[i]) : 0.f;
-  }
-  __syncthreads();
-
-  // ---- the state: work slot, replayed
-  float S[RPT][4];
-  const float total_decay = s_scal[4];
+  // ---- every global load
+  uint32_t raw[RPT][NW];  // the work state's rows
+  bool row_ok[RPT];
 #pragma unroll
   for (int r = 0; r < RPT; ++r) {
     const T* row = state_row<T>(p, w, h, r0 + r, DV);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) S[r][c] = row ? to_f32(row[c0 + c]) * total_decay : 0.f;
+    row_ok[r] = row != nullptr;
+    load_words<CPT>(row ? row + c0 : safe, raw[r]);
   }
+  const T* qrow = static_cast<const T*>(p.q) + (b * p.H + kh) * DK;
+  const T* krow = static_cast<const T*>(p.k) + (b * p.H + kh) * DK;
+  constexpr int QL = DK / 64 > 0 ? DK / 64 : 1;  // q/k elements per lane for the norms
+  float qn[QL], kn[QL];
+#pragma unroll
+  for (int e = 0; e < QL; ++e) {
+    const int i = lane + 64 * e;
+    qn[e] = i < DK ? to_f32(qrow[i < DK ? i : 0]) : 0.f;
+    kn[e] = i < DK ? to_f32(krow[i < DK ? i : 0]) : 0.f;
+  }
+  float qr[RPT], kr[RPT];  // this thread's rows of q and k
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    qr[r] = to_f32(qrow[r0 + r]);
+    kr[r] = to_f32(krow[r0 + r]);
+  }
+  const float a_log = load_any(p.A_log, h, p.a_dtype);
+  const float dt = load_any(p.dt_bias, h, p.dt_dtype);
+  const float graw = load_any(p.gate, b * p.gate_b + h * p.gate_h, p.gate_dtype);
+  const float braw = load_any(p.beta, b * p.beta_b + h * p.beta_h, p.beta_dtype);
+  const float vin = tid < DV ? to_f32(static_cast<const T*>(p.v)[(b * p.HV + h) * DV + (tid < DV ? tid : 0)]) : 0.f;
+  const int64_t gbase = (p.layer * p.page + pos - n) * p.HV + h;
+  const float glane = lane < n ? rec[gbase + (lane < n ? lane : 0) * p.HV] : 0.f;  // replayed gate of token `lane`
+  uint32_t wv[PIECES][4];  // replayed rows: piece j of token i (j < KV a key piece, else a value piece)
+  bool live[PIECES];
+#pragma unroll
+  for (int k = 0; k < PIECES; ++k) {
+    const int idx = tid + k * NT, i = idx / (KV + VV), j = idx % (KV + VV);
+    const bool value = j >= KV;
+    const int col = 8 * (value ? j - KV : j);
+    const T* e = i < n ? decode_log<T>(p, ls, pos - n + i, value ? h : kh, col, value, DK, DV) : nullptr;
+    live[k] = e != nullptr;
+    load_words<8>(e ? e : safe, wv[k]);
+  }
+
+  // ---- norms, gates and the replay decays (every wave computes them)
+  float qq = 0.f, kk = 0.f, qk = 0.f;
+#pragma unroll
+  for (int e = 0; e < QL; ++e) {
+    qq = fmaf(qn[e], qn[e], qq);
+    kk = fmaf(kn[e], kn[e], kk);
+    qk = fmaf(qn[e], kn[e], qk);
+  }
+  qq = wave_sum(qq);
+  kk = wave_sum(kk);
+  qk = wave_sum(qk);
+  const float rq = rsqrtf(qq + 1e-6f) * p.scale, rk = rsqrtf(kk + 1e-6f);
+  const float kq = qk * rq * rk;
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    qr[r] *= rq;
+    kr[r] *= rk;
+  }
+  const float g = -expf(a_log) * softplus_decode(graw + dt);
+  const float decay = expf(g), beta = sigmoid(braw);
+  // inclusive scan of the replayed gates over lanes 0 .. n-1; suffix_i = e^{total - prefix_i}
+  float scan = glane;
+#pragma unroll
+  for (int off = 1; off < kReplayWindow; off <<= 1) {
+    const float y = __shfl_up(scan, off, 64);
+    if (lane >= off) scan += y;
+  }
+  const float total = __shfl(scan, kReplayWindow - 1, 64);
+  const float suffix = expf(total - scan);  // lanes < n
+  const float total_decay = expf(total);
+
+  // ---- stage the replayed rows: keys, and values scaled by their suffix decay
+#pragma unroll
+  for (int k = 0; k < PIECES; ++k) {
+    const int idx = tid + k * NT, i = idx / (KV + VV), j = idx % (KV + VV);
+    const float sfx = __shfl(suffix, i < kReplayWindow ? i : 0, 64);
+    if (i >= n) continue;
+    const bool value = j >= KV;
+    const int col = 8 * (value ? j - KV : j);
+    float x[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) split2<T>(live[k] ? wv[k][q] : 0u, x[2 * q], x[2 * q + 1]);
+    if (value) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) s_vals[i][col + q] = round_to<T>(x[q] * sfx);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) s_keys[i][col + q] = x[q];
+    }
+  }
+  if (n > 0) lds_barrier();
+
+  // ---- the state: work slot, replayed
+  float S[RPT][CPT];
+#pragma unroll
+  for (int r = 0; r < RPT; ++r)
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+      split2<T>(row_ok[r] ? raw[r][j] : 0u, S[r][2 * j], S[r][2 * j + 1]);
+      S[r][2 * j] *= total_decay;
+      S[r][2 * j + 1] *= total_decay;
+    }
   for (int i = 0; i < n; ++i) {
 #pragma unroll
     for (int r = 0; r < RPT; ++r) {
-      const float kr = s_keys[i][r0 + r];
+      const float key = s_keys[i][r0 + r];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) S[r][c] = fmaf(kr, s_vals[i][c0 + c], S[r][c]);
+      for (int c = 0; c < CPT; ++c) S[r][c] = fmaf(key, s_vals[i][c0 + c], S[r][c]);
     }
   }
 
-  const float kq = s_scal[0], g = s_scal[1], decay = s_scal[2], beta = s_scal[3];
-  const T* vin = static_cast<const T*>(p.v) + (b * p.HV + h) * DV;
+  // Column sums of x[c] over the block: inside the wave over its RGW row
+  // groups (lanes CG apart), then across waves through s_red[slot].
+  auto wave_cols = [&](float (&x)[CPT]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int m = CG; m < 64; m <<= 1)
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) x[c] += __shfl_xor(x[c], m, 64);
+  };
   float out_c = 0.f;
   if (p.eager) {
     // S <- e^g S; delta = (v - S^T k) beta; S <- S + k delta^T; o = S^T q
+    float ak[CPT];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      float acc = 0.f;
+    for (int c = 0; c < CPT; ++c) {
+      ak[c] = 0.f;
 #pragma unroll
       for (int r = 0; r < RPT; ++r) {
         S[r][c] *= decay;
-        acc = fmaf(S[r][c], s_k[r0 + r], acc);
+        ak[c] = fmaf(S[r][c], kr[r], ak[c]);
       }
-      s_red[0][rg][c0 + c] = acc;
     }
-    __syncthreads();
+    wave_cols(ak);
+    if (lane < CG) {
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) s_red[0][wave][c0 + c] = ak[c];
+    }
+    lds_barrier();
     if (tid < DV) {
       float sk = 0.f;
-      for (int i = 0; i < RG; ++i) sk += s_red[0][i][tid];
-      s_delta[tid] = (to_f32(vin[tid]) - sk) * beta;
-    }
-    __syncthreads();
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      float acc = 0.f;
+      for (int i = 0; i < WAVES; ++i) sk += s_red[0][i][tid];
+      s_delta[tid] = (vin - sk) * beta;
+    }
+    lds_barrier();
+    float aq[CPT];
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      aq[c] = 0.f;
 #pragma unroll
       for (int r = 0; r < RPT; ++r) {
-        S[r][c] = fmaf(s_k[r0 + r], s_delta[c0 + c], S[r][c]);
-        acc = fmaf(S[r][c], s_q[r0 + r], acc);
+        S[r][c] = fmaf(kr[r], s_delta[c0 + c], S[r][c]);
+        aq[c] = fmaf(S[r][c], qr[r], aq[c]);
       }
-      s_red[1][rg][c0 + c] = acc;
     }
-    __syncthreads();
+    wave_cols(aq);
+    if (lane < CG) {
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) s_red[1][wave][c0 + c] = aq[c];
+    }
+    lds_barrier();
     if (tid < DV) {
-      for (int i = 0; i < RG; ++i) out_c += s_red[1][i][tid];
+#pragma unroll
+      for (int i = 0; i < WAVES; ++i) out_c += s_red[1][i][tid];
     }
   } else {
     // delta = (v - e^g S^T k) beta; o = e^g S^T q + delta (k . q)
+    float ak[CPT], aq[CPT];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      float ak = 0.f, aq = 0.f;
+    for (int c = 0; c < CPT; ++c) {
+      ak[c] = 0.f;
+      aq[c] = 0.f;
 #pragma unroll
       for (int r = 0; r < RPT; ++r) {
-        ak = fmaf(S[r][c], s_k[r0 + r], ak);
-        aq = fmaf(S[r][c], s_q[r0 + r], aq);
+        ak[c] = fmaf(S[r][c], kr[r], ak[c]);
+        aq[c] = fmaf(S[r][c], qr[r], aq[c]);
       }
-      s_red[0][rg][c0 + c] = ak;
-      s_red[1][rg][c0 + c] = aq;
     }
-    __syncthreads();
+    wave_cols(ak);
+    wave_cols(aq);
+    if (lane < CG) {
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) {
+        s_red[0][wave][c0 + c] = ak[c];
+        s_red[1][wave][c0 + c] = aq[c];
+      }
+    }
+    lds_barrier();
     if (tid < DV) {
       float sk = 0.f, sq = 0.f;
-      for (int i = 0; i < RG; ++i) {
+#pragma unroll
+      for (int i = 0; i < WAVES; ++i) {
         sk += s_red[0][i][tid];
         sq += s_red[1][i][tid];
       }
-      const float delta = (to_f32(vin[tid]) - sk * decay) * beta;
+      const float delta = (vin - sk * decay) * beta;
       s_delta[tid] = delta;
       out_c = sq * decay + delta * kq;
     }
-    __syncthreads();
+    lds_barrier();
   }
 
-  // ---- output and the step's log rows
-  if (tid < DV) {
-    static_cast<T*>(p.out)[(b * p.HV + h) * DV + tid] = from_f32<T>(out_c);
-    if (in_page) {
-      T* e = decode_log<T>(p, ls, pos, h, tid, true, DK, DV);
-      if (e) *e = from_f32<T>(s_delta[tid]);
+  // ---- output and the step's log rows (16-byte pieces)
+  if (tid < DV) static_cast<T*>(p.out)[(b * p.HV + h) * DV + tid] = from_f32<T>(out_c);
+  if (in_page) {
+    const bool key_row = h % group == 0;
+    if (tid < VV || (key_row && tid >= VV && tid < VV + KV)) {
+      const bool value = tid < VV;
+      const int col = 8 * (value ? tid : tid - VV);
+      T* e = decode_log<T>(p, ls, pos, value ? h : kh, col, value, DK, DV);
+      if (e) {
+        uint32_t pk[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float a = value ? s_delta[col + 2 * q] : to_f32(krow[col + 2 * q]) * rk;
+          const float c = value ? s_delta[col + 2 * q + 1] : to_f32(krow[col + 2 * q + 1]) * rk;
+          pk[q] = out_pack2<T>(a, c);
+        }
+        store_words<8>(e, pk);
+      }
     }
+    if (rec && tid == 0) rec[(p.layer * p.page + pos) * p.HV + h] = g;
   }
-  if (in_page && h % group == 0 && tid < DK) {
-    T* e = decode_log<T>(p, ls, pos, kh, tid, false, DK, DV);
-    if (e) *e = from_f32<T>(s_k[tid]);
-  }
-  if (in_page && rec && tid == 0) rec[(p.layer * p.page + pos) * p.HV + h] = g;
 
   // ---- the work state: every step (eager), else at the end of a replay window
   if (p.eager || (pos + 1) % kReplayWindow == 0) {
@@ -475,11 +635,18 @@ __global__ __launch_bounds__(kDecodeThreads) void logstate_decode_kernel(LogDeco
     for (int r = 0; r < RPT; ++r) {
       T* row = state_row<T>(p, w, h, r0 + r, DV);
       if (!row) continue;
+      uint32_t pk[NW];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const float val = p.eager ? S[r][c] : fmaf(s_k[r0 + r], s_delta[c0 + c], S[r][c] * decay);
-        row[c0 + c] = from_f32<T>(val);
+      for (int j = 0; j < NW; ++j) {
+        float v2[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const int c = 2 * j + q;
+          v2[q] = p.eager ? S[r][c] : fmaf(kr[r], s_delta[c0 + c], S[r][c] * decay);
+        }
+        pk[j] = out_pack2<T>(v2[0], v2[1]);
       }
+      store_words<CPT>(row + c0, pk);
     }
   }
 }
@@ -498,6 +665,7 @@ struct RestoreParams {
   const int32_t* seg_begin; // [segments] first position
   const int32_t* seg_end;   // [segments] end position
   const int32_t* output;    // [tasks]
+  Div32 fdiv, gdiv;         // frame_bytes, gran
 };
 
 // State row of (slot, layer, head) in a frame storage (the layout of
@@ -506,10 +674,10 @@ template <class T>
 __device__ __forceinline__ T* slot_row(const RestoreParams& p, int64_t s, int64_t layer, int64_t h, int64_t row,
                                        int DV) {
   if (s < 0) return nullptr;
-  const int64_t x = (layer * p.HV + h) * p.head_bytes + row * DV * static_cast<int64_t>(sizeof(T));
-  const int64_t fr = load_index(p.frames, s * p.fps + x / p.frame_bytes, p.frames_is64);
+  const uint32_t x = static_cast<uint32_t>((layer * p.HV + h) * p.head_bytes + row * DV * static_cast<int64_t>(sizeof(T)));
+  const int64_t fr = load_index(p.frames, s * p.fps + p.fdiv.div(x), p.frames_is64);
   if (fr < 0 || fr >= p.num_frames) return nullptr;
-  return reinterpret_cast<T*>(p.storage + fr * p.frame_bytes + x % p.frame_bytes);
+  return reinterpret_cast<T*>(p.storage + fr * p.frame_bytes + p.fdiv.mod(x));
 }
 
 template <class T>
@@ -517,41 +685,89 @@ __device__ __forceinline__ const T* restore_log(const RestoreParams& p, int64_t 
                                                 int64_t index, int64_t col, bool value, int DK, int DV) {
   const int64_t key_size = p.gran * p.KH * DK;
   const int64_t layer_size = key_size + p.gran * p.HV * DV;
-  const int64_t elem = (pos / p.gran * p.layers + layer) * layer_size + (value ? key_size : 0) +
-                       (index * p.gran + pos % p.gran) * (value ? DV : DK) + col;
-  const int64_t byte = 2 * elem;
-  const int64_t fr = load_index(p.frames, slot * p.fps + byte / p.frame_bytes, p.frames_is64);
+  const uint32_t ps = static_cast<uint32_t>(pos);
+  const int64_t elem = (p.gdiv.div(ps) * p.layers + layer) * layer_size + (value ? key_size : 0) +
+                       (index * p.gran + p.gdiv.mod(ps)) * (value ? DV : DK) + col;
+  const uint32_t byte = static_cast<uint32_t>(2 * elem);
+  const int64_t fr = load_index(p.frames, slot * p.fps + p.fdiv.div(byte), p.frames_is64);
   if (fr < 0 || fr >= p.num_frames) return nullptr;
-  return reinterpret_cast<const T*>(p.storage + fr * p.frame_bytes + byte % p.frame_bytes);
+  return reinterpret_cast<const T*>(p.storage + fr * p.frame_bytes + p.fdiv.mod(byte));
 }
 
-// grid (tasks x layers x HV): the state of the task's base slot (or zero),
-// then each segment of logged tokens t = b .. e-1 in one step,
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// 16 x 16 x 32 products with fp32 accumulation on 16-bit operands of the state
+// dtype.  Operand fragments: lane l holds row (A) or column (B) l % 16 and the
+// 8 consecutive k elements 8 (l / 16) .. + 7; the result tile gives lane l
+// column l % 16, rows 4 (l / 16) .. + 3.
+template <class T> struct RestoreMma;
+template <> struct RestoreMma<bf16> {
+  static __device__ __forceinline__ f32x4 run(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+  }
+};
+template <> struct RestoreMma<f16> {
+  static __device__ __forceinline__ f32x4 run(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b),
+                                                  c, 0, 0, 0);
+  }
+};
+
+constexpr int kRestoreGroup = 64;               // tokens staged per step (two 32-deep products)
+constexpr int kRestoreLd = kRestoreGroup + 8;   // LDS row of one feature over a group, padded
+constexpr int kRestoreSpan = kDecodeThreads;    // tokens whose suffix decays one block scan yields
+
+// grid (tasks x layers x HV), 4 waves: the state of the task's base slot (or
+// zero), then each segment of logged tokens t = b .. e-1 in one step,
 // S <- e^{sum_t g_t} S + sum_t k_t (e^{sum_{j>t} g_j} v'_t)^T with the scaled
-// v' rounded to the state dtype (logstate_construction.cuh:329-393), taken
-// 16 tokens at a time; written to the output slot.
+// v' rounded to the state dtype (logstate_construction.cuh:329-393); written
+// to the output slot.  The sum runs on MFMA, 64 tokens per step: the step's
+// keys and scaled v' rows are staged feature-major in LDS (token index
+// contiguous: the k dimension of both operands), and each wave owns the
+// state's columns of DV / 64 (at least one) 16-wide tiles over all DK rows in
+// fp32 accumulators.  The suffix decays of 256 tokens come from one block
+// scan of their gates.
 template <int DK, int DV, class T>
 __global__ __launch_bounds__(kDecodeThreads) void restore_kernel(RestoreParams p) {
-  constexpr int CG = DV / 4, RG = kDecodeThreads / CG, RPT = DK / RG;
-  static_assert(RPT >= 1 && DK % RG == 0, "state split");
-  const int64_t task = blockIdx.x / (p.layers * p.HV);
-  const int64_t layer = (blockIdx.x / p.HV) % p.layers;
-  const int64_t h = blockIdx.x % p.HV;
+  constexpr int RT = DK / 16, CTT = DV / 16, CT = CTT >= 4 ? CTT / 4 : 1;
+  constexpr int KV = DK / 8, VV = DV / 8;  // 16-byte pieces per row
+  constexpr int PIECES = kRestoreGroup * (KV + VV) / kDecodeThreads;
+  static_assert(DK % 16 == 0 && DV % 16 == 0, "tile split");
+  static_assert(kRestoreGroup * (KV + VV) % kDecodeThreads == 0, "piece split");
+  const uint32_t bid = blockIdx.x, nhv = static_cast<uint32_t>(p.HV), nl = static_cast<uint32_t>(p.layers);
+  const int64_t task = bid / (nl * nhv);
+  const int64_t layer = (bid / nhv) % nl;
+  const int64_t h = bid % nhv;
   const int64_t kh = h / (p.HV / p.KH);
-  const int tid = threadIdx.x, c0 = 4 * (tid % CG), r0 = (tid / CG) * RPT;
-  __shared__ float s_keys[kReplayWindow][DK];
-  __shared__ float s_vals[kReplayWindow][DV];
-  __shared__ float s_suffix[kReplayWindow];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lq = lane >> 4;
+  const bool owner = wave * CT < CTT;  // this wave holds column tiles
+  __shared__ uint16_t s_kt[DK * kRestoreLd];
+  __shared__ uint16_t s_vt[DV * kRestoreLd];
+  __shared__ float s_suffix[kRestoreSpan];
   __shared__ float s_part[kDecodeThreads / 64];
-  __shared__ float s_rest;
-  float S[RPT][4];
+  f32x4 acc[RT][CT];
   const int64_t base = p.base[task];
+  // Loads go to a valid address whatever the slot (an unmapped row reads the
+  // storage's first element and is then discarded), so every load is issued
+  // before the first wait: a select or branch on each freshly loaded value
+  // would wait for it alone.
+  const T* const safe = reinterpret_cast<const T*>(p.storage);
 #pragma unroll
-  for (int r = 0; r < RPT; ++r) {
-    const T* row = slot_row<T>(p, base, layer, h, r0 + r, DV);
+  for (int i = 0; i < RT; ++i)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) S[r][c] = row ? to_f32(row[c0 + c]) : 0.f;
-  }
+    for (int c = 0; c < CT; ++c) {
+      const int col = (wave * CT + c) * 16 + lr;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const T* row = owner ? slot_row<T>(p, base, layer, h, i * 16 + 4 * lq + e, DV) : nullptr;
+        const T* src = row ? row + col : safe;
+        const float x = to_f32(*src);
+        acc[i][c][e] = row ? x : 0.f;
+      }
+    }
   for (int64_t seg = p.offsets[task]; seg < p.offsets[task + 1]; ++seg) {
     const int64_t ls = p.seg_slots[seg];
     int64_t fr = -1, ri = -1;
@@ -569,58 +785,111 @@ __global__ __launch_bounds__(kDecodeThreads) void restore_kernel(RestoreParams p
     float part = 0.f;
     for (int64_t t = begin + tid; t < end; t += kDecodeThreads) part += rec[t * p.HV];
     part = wave_sum(part);
-    __syncthreads();  // the previous segment's last group is consumed
-    if ((tid & 63) == 0) s_part[tid >> 6] = part;
-    if (tid == 0) s_rest = 0.f;
-    __syncthreads();
+    lds_barrier();  // the previous segment's last step is consumed
+    if (lane == 0) s_part[wave] = part;
+    lds_barrier();
     float total = 0.f;
 #pragma unroll
     for (int w = 0; w < kDecodeThreads / 64; ++w) total += s_part[w];
     const float decay = expf(total);
 #pragma unroll
-    for (int r = 0; r < RPT; ++r)
+    for (int i = 0; i < RT; ++i)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) S[r][c] *= decay;
-    for (int64_t t0 = begin; t0 < end; t0 += kReplayWindow) {
-      const int n = static_cast<int>(end - t0 < kReplayWindow ? end - t0 : kReplayWindow);
-      __syncthreads();  // the previous group's rows are consumed
-      if (tid == 0) {
-        // s_rest: the gates of the segment's tokens before this group
-        float prefix = s_rest;
-        for (int i = 0; i < n; ++i) {
-          prefix += rec[(t0 + i) * p.HV];
-          s_suffix[i] = expf(total - prefix);
+      for (int c = 0; c < CT; ++c) acc[i][c] *= decay;
+    float rest = 0.f;  // the gates of the segment's tokens before the span
+    for (int64_t sb = begin; sb < end; sb += kRestoreSpan) {
+      // suffix decays of the span: one block inclusive scan of its gates
+      float x = sb + tid < end ? rec[(sb + tid) * p.HV] : 0.f;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+      }
+      lds_barrier();  // s_part and the previous span's suffixes are consumed
+      if (lane == 63) s_part[wave] = x;
+      lds_barrier();
+      float before = rest, span = 0.f;
+#pragma unroll
+      for (int w = 0; w < kDecodeThreads / 64; ++w) {
+        before += w < wave ? s_part[w] : 0.f;
+        span += s_part[w];
+      }
+      s_suffix[tid] = expf(total - (before + x));
+      rest += span;
+      const int64_t span_end = sb + kRestoreSpan < end ? sb + kRestoreSpan : end;
+      for (int64_t g0 = sb; g0 < span_end; g0 += kRestoreGroup) {
+        const int n = static_cast<int>(span_end - g0 < kRestoreGroup ? span_end - g0 : kRestoreGroup);
+        // the step's pieces: piece j of token t (consecutive threads take consecutive tokens)
+        uint4 raw[PIECES];
+        bool live[PIECES];
+#pragma unroll
+        for (int k = 0; k < PIECES; ++k) {
+          const int idx = tid + k * kDecodeThreads, t = idx % kRestoreGroup, piece = idx / kRestoreGroup;
+          const bool value = piece >= KV;
+          const int col = 8 * (value ? piece - KV : piece);
+          const T* e = restore_log<T>(p, ls, layer, g0 + (t < n ? t : 0), value ? h : kh, col, value, DK, DV);
+          live[k] = t < n && e;
+          raw[k] = *reinterpret_cast<const uint4*>(e ? e : safe);
         }
-        s_rest = prefix;
-      }
-      for (int idx = tid; idx < n * DK; idx += kDecodeThreads) {
-        const T* e = restore_log<T>(p, ls, layer, t0 + idx / DK, kh, idx % DK, false, DK, DV);
-        s_keys[idx / DK][idx % DK] = e ? to_f32(*e) : 0.f;
-      }
-      __syncthreads();
-      for (int idx = tid; idx < n * DV; idx += kDecodeThreads) {
-        const T* e = restore_log<T>(p, ls, layer, t0 + idx / DV, h, idx % DV, true, DK, DV);
-        s_vals[idx / DV][idx % DV] = e ? to_f32(from_f32<T>(to_f32(*e) * s_suffix[idx / DV])) : 0.f;
-      }
-      __syncthreads();
-      for (int i = 0; i < n; ++i) {
+        lds_barrier();  // suffixes written; the previous step's operands are consumed
 #pragma unroll
-        for (int r = 0; r < RPT; ++r) {
-          const float kr = s_keys[i][r0 + r];
+        for (int k = 0; k < PIECES; ++k) {
+          const int idx = tid + k * kDecodeThreads, t = idx % kRestoreGroup, piece = idx / kRestoreGroup;
+          const bool value = piece >= KV;
+          const int col = 8 * (value ? piece - KV : piece);
+          const uint32_t wv[4] = {live[k] ? raw[k].x : 0u, live[k] ? raw[k].y : 0u, live[k] ? raw[k].z : 0u,
+                                  live[k] ? raw[k].w : 0u};
+          uint16_t* dst = (value ? s_vt : s_kt) + col * kRestoreLd + t;
+          if (value) {
+            const float sfx = s_suffix[g0 - sb + t];
 #pragma unroll
-          for (int c = 0; c < 4; ++c) S[r][c] = fmaf(kr, s_vals[i][c0 + c], S[r][c]);
+            for (int q = 0; q < 4; ++q) {
+              float a, b;
+              split2<T>(wv[q], a, b);
+              const uint32_t packed = out_pack2<T>(a * sfx, b * sfx);
+              dst[(2 * q) * kRestoreLd] = static_cast<uint16_t>(packed & 0xffffu);
+              dst[(2 * q + 1) * kRestoreLd] = static_cast<uint16_t>(packed >> 16);
+            }
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              dst[(2 * q) * kRestoreLd] = static_cast<uint16_t>(wv[q] & 0xffffu);
+              dst[(2 * q + 1) * kRestoreLd] = static_cast<uint16_t>(wv[q] >> 16);
+            }
+          }
+        }
+        lds_barrier();
+        if (owner) {
+#pragma unroll
+          for (int ks = 0; ks < kRestoreGroup / 32; ++ks)
+#pragma unroll
+            for (int c = 0; c < CT; ++c) {
+              const uint4 bfrag = *reinterpret_cast<const uint4*>(
+                  s_vt + ((wave * CT + c) * 16 + lr) * kRestoreLd + 32 * ks + 8 * lq);
+#pragma unroll
+              for (int i = 0; i < RT; ++i) {
+                const uint4 afrag =
+                    *reinterpret_cast<const uint4*>(s_kt + (i * 16 + lr) * kRestoreLd + 32 * ks + 8 * lq);
+                acc[i][c] = RestoreMma<T>::run(afrag, bfrag, acc[i][c]);
+              }
+            }
         }
       }
     }
   }
   const int64_t out = p.output[task];
+  if (!owner) return;
 #pragma unroll
-  for (int r = 0; r < RPT; ++r) {
-    T* row = slot_row<T>(p, out, layer, h, r0 + r, DV);
-    if (!row) continue;
+  for (int i = 0; i < RT; ++i)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) row[c0 + c] = from_f32<T>(S[r][c]);
-  }
+    for (int c = 0; c < CT; ++c) {
+      const int col = (wave * CT + c) * 16 + lr;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        T* row = slot_row<T>(p, out, layer, h, i * 16 + 4 * lq + e, DV);
+        if (row) row[col] = from_f32<T>(acc[i][c][e]);
+      }
+    }
 }
 
 // grid (pairs x layers x HV): the state of (source, layer, head) to destination.
@@ -662,6 +931,7 @@ extern "C" int gdn_store_chunk_log(void* storage, const void* frames, int frames
   GDN_REQUIRE(frames_per_slot > 0 && frame_bytes > 0 && frame_bytes % 4 == 0 && num_frames > 0,
               "gdn_store_chunk_log: bad frame table");
   const int64_t log_bytes = 2 * page_size * num_layers * (key_heads * dk + HV * dv);
+  GDN_REQUIRE(frames_per_slot * frame_bytes < kMaxOffset32, "gdn_store_chunk_log: a slot's frames exceed 4 GiB");
   GDN_REQUIRE(log_bytes <= frames_per_slot * frame_bytes,
               "gdn_store_chunk_log: a slot's log (%lld bytes) exceeds its %lld frames", (long long)log_bytes,
               (long long)frames_per_slot);
@@ -686,8 +956,15 @@ extern "C" int gdn_store_chunk_log(void* storage, const void* frames, int frames
   p.decay = decay_frames; p.decay_is64 = decay_dtype == GDN_I64;
   p.record_bytes = decay_record_bytes;
   p.layer = layer; p.layers = num_layers; p.gran = granularity; p.page = page_size;
-  hipLaunchKernelGGL(chunk_log_kernel, dim3(static_cast<unsigned>(T), static_cast<unsigned>(HV)), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream), p);
+  p.fdiv = make_div32(frame_bytes); p.gdiv = make_div32(granularity);
+  const bool vec = dk % 8 == 0 && dv % 8 == 0 && frame_bytes % 16 == 0 && aligned16(storage) && aligned16(v_new) &&
+                   aligned16(key);
+  if (vec)
+    hipLaunchKernelGGL(chunk_log_vec_kernel, dim3(static_cast<unsigned>(T)), dim3(kLogThreads), 0,
+                       static_cast<hipStream_t>(stream), p);
+  else
+    hipLaunchKernelGGL(chunk_log_kernel, dim3(static_cast<unsigned>(T), static_cast<unsigned>(HV)), dim3(kThreads), 0,
+                       static_cast<hipStream_t>(stream), p);
   return GDN_LAUNCH_CHECK("gdn_store_chunk_log launch");
 }
 
@@ -719,6 +996,7 @@ extern "C" int gdn_conv_decode_logstate(const void* x, int64_t x_row_stride, int
   const int64_t span = (layer + 1) * channels * (kernel_width - 1);
   GDN_REQUIRE(frames_per_granule == 1 ? span <= fe : span <= frames_per_granule * fe,
               "gdn_conv_decode_logstate: layer %lld's conv windows exceed the snapshot's frames", (long long)layer);
+  GDN_REQUIRE(span < kMaxOffset32 && fe < kMaxOffset32, "gdn_conv_decode_logstate: snapshot offsets exceed 32 bits");
   GDN_REQUIRE(batch <= 65535, "gdn_conv_decode_logstate: batch too large");
   ConvFrameParams p{};
   p.x = x; p.xr = x_row_stride; p.xc = x_col_stride; p.weight = weight; p.bias = bias; p.W = kernel_width;
@@ -764,14 +1042,16 @@ extern "C" int gdn_recurrent_logstate(
                   page_size % granularity == 0,
               "gdn_recurrent_logstate: bad layout");
   const int64_t row = dv * 2;
-  GDN_REQUIRE(frames_per_slot > 0 && frame_bytes > 0 && num_frames > 0 && frame_bytes % 8 == 0 &&
-                  head_bytes >= dk * row && head_bytes % 8 == 0,
-              "gdn_recurrent_logstate: bad frame layout");
+  GDN_REQUIRE(frames_per_slot > 0 && frame_bytes > 0 && num_frames > 0 && frame_bytes % 16 == 0 &&
+                  head_bytes >= dk * row && head_bytes % 16 == 0 && aligned16(storage),
+              "gdn_recurrent_logstate: bad frame layout (frame and head bytes must be multiples of 16, the "
+              "storage 16-byte aligned)");
   GDN_REQUIRE(head_bytes <= frame_bytes ? frame_bytes % head_bytes == 0
                                         : head_bytes % frame_bytes == 0 && frame_bytes % row == 0,
               "gdn_recurrent_logstate: head_bytes %lld must divide frame_bytes %lld, or be a multiple of it with "
               "frames holding whole state rows",
               (long long)head_bytes, (long long)frame_bytes);
+  GDN_REQUIRE(frames_per_slot * frame_bytes < kMaxOffset32, "gdn_recurrent_logstate: a slot's frames exceed 4 GiB");
   GDN_REQUIRE((layer + 1) * HV * head_bytes <= frames_per_slot * frame_bytes &&
                   2 * page_size * num_layers * (H * dk + HV * dv) <= frames_per_slot * frame_bytes,
               "gdn_recurrent_logstate: the states or the log exceed a slot's frames");
@@ -794,15 +1074,18 @@ extern "C" int gdn_recurrent_logstate(
   p.offsets = token_offsets; p.offsets_is64 = offsets_dtype == GDN_I64;
   p.counts = replay_counts; p.counts_is64 = counts_dtype == GDN_I64;
   p.layer = layer; p.layers = num_layers; p.gran = granularity; p.page = page_size;
+  p.fdiv = make_div32(frame_bytes); p.gdiv = make_div32(granularity);
   p.eager = eager; p.out = out; p.scale = scale;
   const dim3 grid(static_cast<unsigned>(batch * HV));
   auto s = static_cast<hipStream_t>(stream);
   auto launch = [&](auto dkc, auto dvc) {
     constexpr int DK = decltype(dkc)::value, DV = decltype(dvc)::value;
+    // 512 threads for the largest heads keep the per-thread state at 32 floats
+    constexpr int NT = DK * DV >= 128 * 128 ? 512 : kDecodeThreads;
     if (io_dtype == GDN_BF16)
-      hipLaunchKernelGGL((logstate_decode_kernel<DK, DV, bf16>), grid, dim3(kDecodeThreads), 0, s, p);
+      hipLaunchKernelGGL((logstate_decode_kernel<DK, DV, bf16, NT>), grid, dim3(NT), 0, s, p);
     else
-      hipLaunchKernelGGL((logstate_decode_kernel<DK, DV, f16>), grid, dim3(kDecodeThreads), 0, s, p);
+      hipLaunchKernelGGL((logstate_decode_kernel<DK, DV, f16, NT>), grid, dim3(NT), 0, s, p);
     return GDN_LAUNCH_CHECK("gdn_recurrent_logstate launch");
   };
   using I128 = std::integral_constant<int, 128>;
@@ -839,6 +1122,7 @@ extern "C" int gdn_conv_windows_logstate(const void* x, int64_t x_row_stride, in
   const int64_t span = (layer + 1) * channels * (kernel_width - 1);
   GDN_REQUIRE(frames_per_granule == 1 ? span <= fe : span <= frames_per_granule * fe,
               "gdn_conv_windows_logstate: layer %lld's conv windows exceed the snapshot's frames", (long long)layer);
+  GDN_REQUIRE(span < kMaxOffset32 && fe < kMaxOffset32, "gdn_conv_windows_logstate: snapshot offsets exceed 32 bits");
   GDN_REQUIRE(total_tokens <= 0x7fffffff && (channels + kDecodeThreads - 1) / kDecodeThreads <= 65535,
               "gdn_conv_windows_logstate: grid too large");
   ConvWindowParams p{};
@@ -875,14 +1159,16 @@ int restore_setup(RestoreParams& p, void* storage, const void* payload_frames, i
                   page_size % granularity == 0,
               "%s: bad layout", who);
   const int64_t row = dv * 2;
-  GDN_REQUIRE(frames_per_slot > 0 && frame_bytes > 0 && num_frames > 0 && frame_bytes % 8 == 0 &&
-                  head_bytes >= dk * row && head_bytes % 8 == 0,
-              "%s: bad frame layout", who);
+  GDN_REQUIRE(frames_per_slot > 0 && frame_bytes > 0 && num_frames > 0 && frame_bytes % 16 == 0 &&
+                  head_bytes >= dk * row && head_bytes % 16 == 0 && aligned16(storage),
+              "%s: bad frame layout (frame and head bytes must be multiples of 16, the storage 16-byte aligned)",
+              who);
   GDN_REQUIRE(head_bytes <= frame_bytes ? frame_bytes % head_bytes == 0
                                         : head_bytes % frame_bytes == 0 && frame_bytes % row == 0,
               "%s: head_bytes %lld must divide frame_bytes %lld, or be a multiple of it with frames holding whole "
               "state rows",
               who, (long long)head_bytes, (long long)frame_bytes);
+  GDN_REQUIRE(frames_per_slot * frame_bytes < kMaxOffset32, "%s: a slot's frames exceed 4 GiB", who);
   GDN_REQUIRE(layers * HV * head_bytes <= frames_per_slot * frame_bytes &&
                   2 * page_size * layers * (KH * dk + HV * dv) <= frames_per_slot * frame_bytes,
               "%s: the states or the log exceed a slot's frames", who);
@@ -893,6 +1179,7 @@ int restore_setup(RestoreParams& p, void* storage, const void* payload_frames, i
   p.fps = frames_per_slot; p.frame_bytes = frame_bytes; p.head_bytes = head_bytes; p.num_frames = num_frames;
   p.decay = decay_frames; p.decay_is64 = decay_dtype == GDN_I64; p.record_bytes = record_bytes;
   p.layers = layers; p.HV = HV; p.KH = KH; p.gran = granularity; p.page = page_size;
+  p.fdiv = make_div32(frame_bytes); p.gdiv = make_div32(granularity);
   return GDN_OK;
 }
 
@@ -977,13 +1264,15 @@ extern "C" int gdn_logstate_copy_states(void* storage, const void* payload_frame
                   head_bytes >= dk * dv * 2 &&
                   (head_bytes <= frame_bytes ? frame_bytes % head_bytes == 0
                                              : head_bytes % frame_bytes == 0 && frame_bytes % (dv * 2) == 0) &&
-                  num_layers * HV * head_bytes <= frames_per_slot * frame_bytes,
+                  num_layers * HV * head_bytes <= frames_per_slot * frame_bytes &&
+                  frames_per_slot * frame_bytes < kMaxOffset32,
               "gdn_logstate_copy_states: bad frame layout");
   RestoreParams p{};
   p.storage = static_cast<char*>(storage);
   p.frames = payload_frames; p.frames_is64 = frames_dtype == GDN_I64;
   p.fps = frames_per_slot; p.frame_bytes = frame_bytes; p.head_bytes = head_bytes; p.num_frames = num_frames;
   p.layers = num_layers; p.HV = HV; p.KH = 1;
+  p.fdiv = make_div32(frame_bytes); p.gdiv = make_div32(1);
   p.base = sources; p.output = destinations;
   return launch_state_kernel<false>(p, count * num_layers * HV, dk, dv, dtype,
                                                  static_cast<hipStream_t>(stream), "gdn_logstate_copy_states");
