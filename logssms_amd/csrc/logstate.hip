@@ -355,32 +355,53 @@ template <int N> __device__ __forceinline__ void store_words(void* dst, const ui
     *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
 }
 
-// grid (batch x HV); NT threads hold the dk x dv state as RPT rows x CPT
-// columns each (columns CPT (tid % (dv / CPT)) .. + CPT - 1), moved with 8- or
-// 16-byte accesses.  Every global load (state rows, q / k, gates, replayed
-// gates and rows) is issued before the first wait, so one HBM latency covers
-// them all; values the whole block needs (norms, gates, suffix decays) are
-// computed redundantly per wave instead of broadcast through LDS, and the
-// column reductions run inside each wave before one LDS exchange across
-// waves.  Only the LDS exchanges need barriers (lgkmcnt only).
-template <int DK, int DV, class T, int NT>
-__global__ __launch_bounds__(NT) void logstate_decode_kernel(LogDecodeParams p) {
-  constexpr int CPT = DK * DV >= 8 * NT ? 8 : 4;
-  constexpr int CG = DV / CPT, RG = NT / CG, RPT = DK / RG, NW = CPT / 2;
-  constexpr int WAVES = NT / 64;
+typedef short s4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+// 16 x 16 x 16 products on 16-bit operands, fp32 accumulation: lane l holds
+// row (A) / column (B) l % 16 and k = 4 (l / 16) .. + 3; the result gives lane
+// l column l % 16, rows 4 (l / 16) .. + 3.
+template <class T> __device__ __forceinline__ f4_t mma16(uint2 a, uint2 b, f4_t c);
+template <> __device__ __forceinline__ f4_t mma16<bf16>(uint2 a, uint2 b, f4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s4_t, a), __builtin_bit_cast(s4_t, b), c, 0, 0, 0);
+}
+template <> __device__ __forceinline__ f4_t mma16<f16>(uint2 a, uint2 b, f4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4_t, a), __builtin_bit_cast(h4_t, b), c, 0, 0, 0);
+}
+
+// Sum over the 16 lanes of a row (every lane of the row receives it).
+__device__ __forceinline__ float row16_sum(float v) { return head_sum<16>(v); }
+
+constexpr int kReplayLd = kReplayWindow + 4;  // LDS row of one feature over the replay window
+
+// grid (batch x HV), DV / (16 TPW) waves.  The state is held transposed,
+// T = S^T (dv x dk), in 16 x 16 MFMA result tiles: wave w owns the TPW dv row
+// tiles TPW w .. and every dk column, lane l the dk column 16 it + l % 16 of
+// tile it and the dv rows 16 jt + 4 (l / 16) .. + 3 of row tile jt -- four
+// consecutive elements of one state row in memory, moved as 8 bytes.  Two
+// row tiles per wave (d_v = 128) keep 4 waves per block and 32 KiB of state
+// in flight per 4 waves, which sets the block's share of HBM bandwidth.  The replayed tokens' rank-n update
+// T += V'^T K runs as one 16-deep MFMA per tile from keys and scaled v' rows
+// staged feature-major in LDS; S^T k and S^T q are per-lane FMAs and a
+// 16-lane DPP sum, complete inside each wave.  Every global load is issued
+// before the first wait; the only barrier guards the staged replay rows.
+template <int DK, int DV, class T>
+__global__ __launch_bounds__(DV * 4 / (DV >= 128 ? 2 : 1)) __attribute__((amdgpu_waves_per_eu(3))) void logstate_decode_kernel(LogDecodeParams p) {
+  constexpr int TPW = DV >= 128 ? 2 : 1;         // dv row tiles per wave
+  constexpr int NT = DV * 4 / TPW, RT = DK / 16;  // threads; dk tiles per wave
   constexpr int KV = DK / 8, VV = DV / 8;        // 16-byte pieces per row
   constexpr int PIECES = (kReplayWindow * (KV + VV) + NT - 1) / NT;
-  static_assert(RPT >= 1 && DK % RG == 0 && DV % CPT == 0 && 64 % CG == 0, "state split");
-  static_assert((DK <= 128 && DK % 64 == 0) || DK == 32, "q/k norm lanes");
+  static_assert(DK % 16 == 0 && DV % 16 == 0, "tile split");
   const uint32_t bid = blockIdx.x, nhv = static_cast<uint32_t>(p.HV);
   const int64_t b = bid / nhv, h = bid % nhv;
   const int64_t group = p.HV / p.H, kh = h / group;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, cg = tid % CG, rg = tid / CG;
-  const int c0 = CPT * cg, r0 = rg * RPT;
-  __shared__ float s_delta[DV];
-  __shared__ float s_keys[kReplayWindow][DK];
-  __shared__ float s_vals[kReplayWindow][DV];
-  __shared__ float s_red[2][WAVES][DV];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+  int j0[TPW];  // this lane's dv rows j0[u] .. j0[u] + 3 of row tile TPW wave + u
+#pragma unroll
+  for (int u = 0; u < TPW; ++u) j0[u] = 16 * (TPW * wave + u) + 4 * lg;
+  __shared__ uint16_t s_kt[DK * kReplayLd];
+  __shared__ uint16_t s_vt[DV * kReplayLd];
 
   const int64_t w = load_index(p.work, b, p.work_is64);
   const int64_t ls = load_index(p.logs, b, p.logs_is64);
@@ -402,38 +423,37 @@ __global__ __launch_bounds__(NT) void logstate_decode_kernel(LogDecodeParams p) 
   const T* const safe = reinterpret_cast<const T*>(p.storage);
 
   // ---- every global load
-  uint32_t raw[RPT][NW];  // the work state's rows
-  bool row_ok[RPT];
+  uint2 raw[TPW][RT];  // S[16 it + lr][j0[u] .. j0[u] + 3]
+  bool row_ok[RT];
+  // a head inside one frame: one (uniform) frame lookup for all its rows
+  const T* head = p.head_bytes <= p.frame_bytes ? state_row<T>(p, w, h, 0, DV) : nullptr;
 #pragma unroll
-  for (int r = 0; r < RPT; ++r) {
-    const T* row = state_row<T>(p, w, h, r0 + r, DV);
-    row_ok[r] = row != nullptr;
-    load_words<CPT>(row ? row + c0 : safe, raw[r]);
+  for (int it = 0; it < RT; ++it) {
+    const T* row = p.head_bytes <= p.frame_bytes ? (head ? head + (16 * it + lr) * DV : nullptr)
+                                                 : state_row<T>(p, w, h, 16 * it + lr, DV);
+    row_ok[it] = row != nullptr;
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) raw[u][it] = *reinterpret_cast<const uint2*>(row ? row + j0[u] : safe);
   }
   const T* qrow = static_cast<const T*>(p.q) + (b * p.H + kh) * DK;
   const T* krow = static_cast<const T*>(p.k) + (b * p.H + kh) * DK;
-  constexpr int QL = DK / 64 > 0 ? DK / 64 : 1;  // q/k elements per lane for the norms
-  float qn[QL], kn[QL];
+  float qv[RT], kv[RT];  // q, k at this lane's dk columns
 #pragma unroll
-  for (int e = 0; e < QL; ++e) {
-    const int i = lane + 64 * e;
-    qn[e] = i < DK ? to_f32(qrow[i < DK ? i : 0]) : 0.f;
-    kn[e] = i < DK ? to_f32(krow[i < DK ? i : 0]) : 0.f;
+  for (int it = 0; it < RT; ++it) {
+    qv[it] = to_f32(qrow[16 * it + lr]);
+    kv[it] = to_f32(krow[16 * it + lr]);
   }
-  float qr[RPT], kr[RPT];  // this thread's rows of q and k
+  uint2 vraw[TPW];
 #pragma unroll
-  for (int r = 0; r < RPT; ++r) {
-    qr[r] = to_f32(qrow[r0 + r]);
-    kr[r] = to_f32(krow[r0 + r]);
-  }
+  for (int u = 0; u < TPW; ++u)
+    vraw[u] = *reinterpret_cast<const uint2*>(static_cast<const T*>(p.v) + (b * p.HV + h) * DV + j0[u]);
   const float a_log = load_any(p.A_log, h, p.a_dtype);
   const float dt = load_any(p.dt_bias, h, p.dt_dtype);
   const float graw = load_any(p.gate, b * p.gate_b + h * p.gate_h, p.gate_dtype);
   const float braw = load_any(p.beta, b * p.beta_b + h * p.beta_h, p.beta_dtype);
-  const float vin = tid < DV ? to_f32(static_cast<const T*>(p.v)[(b * p.HV + h) * DV + (tid < DV ? tid : 0)]) : 0.f;
   const int64_t gbase = (p.layer * p.page + pos - n) * p.HV + h;
   const float glane = lane < n ? rec[gbase + (lane < n ? lane : 0) * p.HV] : 0.f;  // replayed gate of token `lane`
-  uint32_t wv[PIECES][4];  // replayed rows: piece j of token i (j < KV a key piece, else a value piece)
+  uint4 pw[PIECES];  // replayed rows: piece j of token i (j < KV a key piece, else a value piece)
   bool live[PIECES];
 #pragma unroll
   for (int k = 0; k < PIECES; ++k) {
@@ -442,26 +462,26 @@ __global__ __launch_bounds__(NT) void logstate_decode_kernel(LogDecodeParams p) 
     const int col = 8 * (value ? j - KV : j);
     const T* e = i < n ? decode_log<T>(p, ls, pos - n + i, value ? h : kh, col, value, DK, DV) : nullptr;
     live[k] = e != nullptr;
-    load_words<8>(e ? e : safe, wv[k]);
+    pw[k] = *reinterpret_cast<const uint4*>(e ? e : safe);
   }
 
   // ---- norms, gates and the replay decays (every wave computes them)
   float qq = 0.f, kk = 0.f, qk = 0.f;
 #pragma unroll
-  for (int e = 0; e < QL; ++e) {
-    qq = fmaf(qn[e], qn[e], qq);
-    kk = fmaf(kn[e], kn[e], kk);
-    qk = fmaf(qn[e], kn[e], qk);
+  for (int it = 0; it < RT; ++it) {
+    qq = fmaf(qv[it], qv[it], qq);
+    kk = fmaf(kv[it], kv[it], kk);
+    qk = fmaf(qv[it], kv[it], qk);
   }
-  qq = wave_sum(qq);
-  kk = wave_sum(kk);
-  qk = wave_sum(qk);
+  qq = row16_sum(qq);
+  kk = row16_sum(kk);
+  qk = row16_sum(qk);
   const float rq = rsqrtf(qq + 1e-6f) * p.scale, rk = rsqrtf(kk + 1e-6f);
   const float kq = qk * rq * rk;
 #pragma unroll
-  for (int r = 0; r < RPT; ++r) {
-    qr[r] *= rq;
-    kr[r] *= rk;
+  for (int it = 0; it < RT; ++it) {
+    qv[it] *= rq;
+    kv[it] *= rk;
   }
   const float g = -expf(a_log) * softplus_decode(graw + dt);
   const float decay = expf(g), beta = sigmoid(braw);
@@ -476,153 +496,121 @@ __global__ __launch_bounds__(NT) void logstate_decode_kernel(LogDecodeParams p) 
   const float suffix = expf(total - scan);  // lanes < n
   const float total_decay = expf(total);
 
-  // ---- stage the replayed rows: keys, and values scaled by their suffix decay
+  // ---- the state, decayed over the replayed tokens
+  f4_t Tt[TPW][RT];
 #pragma unroll
-  for (int k = 0; k < PIECES; ++k) {
-    const int idx = tid + k * NT, i = idx / (KV + VV), j = idx % (KV + VV);
-    const float sfx = __shfl(suffix, i < kReplayWindow ? i : 0, 64);
-    if (i >= n) continue;
-    const bool value = j >= KV;
-    const int col = 8 * (value ? j - KV : j);
-    float x[8];
+  for (int u = 0; u < TPW; ++u)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) split2<T>(live[k] ? wv[k][q] : 0u, x[2 * q], x[2 * q + 1]);
-    if (value) {
+    for (int it = 0; it < RT; ++it) {
+      float a, c2, d, e;
+      split2<T>(row_ok[it] ? raw[u][it].x : 0u, a, c2);
+      split2<T>(row_ok[it] ? raw[u][it].y : 0u, d, e);
+      Tt[u][it] = f4_t{a, c2, d, e} * total_decay;
+    }
+  if (n > 0) {
+    // stage the replayed rows feature-major (token index contiguous): keys,
+    // and values scaled by their suffix decay and rounded to the state dtype
 #pragma unroll
-      for (int q = 0; q < 8; ++q) s_vals[i][col + q] = round_to<T>(x[q] * sfx);
+    for (int k = 0; k < PIECES; ++k) {
+      const int idx = tid + k * NT, i = idx / (KV + VV), j = idx % (KV + VV);
+      const float sfx = __shfl(suffix, i < kReplayWindow ? i : 0, 64);
+      if (i >= kReplayWindow) continue;
+      const bool value = j >= KV;
+      const int col = 8 * (value ? j - KV : j);
+      const bool keep = live[k] && i < n;  // tokens i >= n stage zeros
+      const uint32_t wv[4] = {keep ? pw[k].x : 0u, keep ? pw[k].y : 0u, keep ? pw[k].z : 0u, keep ? pw[k].w : 0u};
+      uint16_t* dst = (value ? s_vt : s_kt) + col * kReplayLd + i;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint32_t word = wv[q];
+        if (value) {
+          float a, c2;
+          split2<T>(word, a, c2);
+          word = out_pack2<T>(a * sfx, c2 * sfx);
+        }
+        dst[(2 * q) * kReplayLd] = static_cast<uint16_t>(word & 0xffffu);
+        dst[(2 * q + 1) * kReplayLd] = static_cast<uint16_t>(word >> 16);
+      }
+    }
+    lds_barrier();
+    // T += V'^T K over the replayed tokens (zero rows past n)
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) {
+      const uint2 af = *reinterpret_cast<const uint2*>(s_vt + (16 * (TPW * wave + u) + lr) * kReplayLd + 4 * lg);
+#pragma unroll
+      for (int it = 0; it < RT; ++it) {
+        const uint2 bf = *reinterpret_cast<const uint2*>(s_kt + (16 * it + lr) * kReplayLd + 4 * lg);
+        Tt[u][it] = mma16<T>(af, bf, Tt[u][it]);
+      }
+    }
+  }
+
+  // ---- one step: row sums of T against k and q (S^T k, S^T q) for rows j0 + e
+  float delta[TPW][4], out[TPW][4];
+#pragma unroll
+  for (int u = 0; u < TPW; ++u) {
+    float vin[4];
+    split2<T>(vraw[u].x, vin[0], vin[1]);
+    split2<T>(vraw[u].y, vin[2], vin[3]);
+    if (p.eager) {
+      // S <- e^g S; delta = (v - S^T k) beta; S <- S + k delta^T; o = S^T q
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float acc = 0.f;
+#pragma unroll
+        for (int it = 0; it < RT; ++it) {
+          Tt[u][it][e] *= decay;
+          acc = fmaf(Tt[u][it][e], kv[it], acc);
+        }
+        delta[u][e] = (vin[e] - row16_sum(acc)) * beta;
+        float accq = 0.f;
+#pragma unroll
+        for (int it = 0; it < RT; ++it) {
+          Tt[u][it][e] = fmaf(delta[u][e], kv[it], Tt[u][it][e]);
+          accq = fmaf(Tt[u][it][e], qv[it], accq);
+        }
+        out[u][e] = row16_sum(accq);
+      }
     } else {
+      // delta = (v - e^g S^T k) beta; o = e^g S^T q + delta (k . q)
 #pragma unroll
-      for (int q = 0; q < 8; ++q) s_keys[i][col + q] = x[q];
-    }
-  }
-  if (n > 0) lds_barrier();
-
-  // ---- the state: work slot, replayed
-  float S[RPT][CPT];
+      for (int e = 0; e < 4; ++e) {
+        float ak = 0.f, aq = 0.f;
 #pragma unroll
-  for (int r = 0; r < RPT; ++r)
-#pragma unroll
-    for (int j = 0; j < NW; ++j) {
-      split2<T>(row_ok[r] ? raw[r][j] : 0u, S[r][2 * j], S[r][2 * j + 1]);
-      S[r][2 * j] *= total_decay;
-      S[r][2 * j + 1] *= total_decay;
-    }
-  for (int i = 0; i < n; ++i) {
-#pragma unroll
-    for (int r = 0; r < RPT; ++r) {
-      const float key = s_keys[i][r0 + r];
-#pragma unroll
-      for (int c = 0; c < CPT; ++c) S[r][c] = fmaf(key, s_vals[i][c0 + c], S[r][c]);
+        for (int it = 0; it < RT; ++it) {
+          ak = fmaf(Tt[u][it][e], kv[it], ak);
+          aq = fmaf(Tt[u][it][e], qv[it], aq);
+        }
+        delta[u][e] = (vin[e] - row16_sum(ak) * decay) * beta;
+        out[u][e] = row16_sum(aq) * decay + delta[u][e] * kq;
+      }
     }
   }
 
-  // Column sums of x[c] over the block: inside the wave over its RGW row
-  // groups (lanes CG apart), then across waves through s_red[slot].
-  auto wave_cols = [&](float (&x)[CPT]) __attribute__((always_inline)) {
+  // ---- output and the step's log rows
+  if (lr == 0) {
 #pragma unroll
-    for (int m = CG; m < 64; m <<= 1)
-#pragma unroll
-      for (int c = 0; c < CPT; ++c) x[c] += __shfl_xor(x[c], m, 64);
-  };
-  float out_c = 0.f;
-  if (p.eager) {
-    // S <- e^g S; delta = (v - S^T k) beta; S <- S + k delta^T; o = S^T q
-    float ak[CPT];
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      ak[c] = 0.f;
-#pragma unroll
-      for (int r = 0; r < RPT; ++r) {
-        S[r][c] *= decay;
-        ak[c] = fmaf(S[r][c], kr[r], ak[c]);
-      }
-    }
-    wave_cols(ak);
-    if (lane < CG) {
-#pragma unroll
-      for (int c = 0; c < CPT; ++c) s_red[0][wave][c0 + c] = ak[c];
-    }
-    lds_barrier();
-    if (tid < DV) {
-      float sk = 0.f;
-#pragma unroll
-      for (int i = 0; i < WAVES; ++i) sk += s_red[0][i][tid];
-      s_delta[tid] = (vin - sk) * beta;
-    }
-    lds_barrier();
-    float aq[CPT];
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      aq[c] = 0.f;
-#pragma unroll
-      for (int r = 0; r < RPT; ++r) {
-        S[r][c] = fmaf(kr[r], s_delta[c0 + c], S[r][c]);
-        aq[c] = fmaf(S[r][c], qr[r], aq[c]);
-      }
-    }
-    wave_cols(aq);
-    if (lane < CG) {
-#pragma unroll
-      for (int c = 0; c < CPT; ++c) s_red[1][wave][c0 + c] = aq[c];
-    }
-    lds_barrier();
-    if (tid < DV) {
-#pragma unroll
-      for (int i = 0; i < WAVES; ++i) out_c += s_red[1][i][tid];
-    }
-  } else {
-    // delta = (v - e^g S^T k) beta; o = e^g S^T q + delta (k . q)
-    float ak[CPT], aq[CPT];
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      ak[c] = 0.f;
-      aq[c] = 0.f;
-#pragma unroll
-      for (int r = 0; r < RPT; ++r) {
-        ak[c] = fmaf(S[r][c], kr[r], ak[c]);
-        aq[c] = fmaf(S[r][c], qr[r], aq[c]);
-      }
-    }
-    wave_cols(ak);
-    wave_cols(aq);
-    if (lane < CG) {
-#pragma unroll
-      for (int c = 0; c < CPT; ++c) {
-        s_red[0][wave][c0 + c] = ak[c];
-        s_red[1][wave][c0 + c] = aq[c];
-      }
-    }
-    lds_barrier();
-    if (tid < DV) {
-      float sk = 0.f, sq = 0.f;
-#pragma unroll
-      for (int i = 0; i < WAVES; ++i) {
-        sk += s_red[0][i][tid];
-        sq += s_red[1][i][tid];
-      }
-      const float delta = (vin - sk * decay) * beta;
-      s_delta[tid] = delta;
-      out_c = sq * decay + delta * kq;
-    }
-    lds_barrier();
+    for (int u = 0; u < TPW; ++u)
+      *reinterpret_cast<uint2*>(static_cast<T*>(p.out) + (b * p.HV + h) * DV + j0[u]) =
+          make_uint2(out_pack2<T>(out[u][0], out[u][1]), out_pack2<T>(out[u][2], out[u][3]));
   }
-
-  // ---- output and the step's log rows (16-byte pieces)
-  if (tid < DV) static_cast<T*>(p.out)[(b * p.HV + h) * DV + tid] = from_f32<T>(out_c);
   if (in_page) {
-    const bool key_row = h % group == 0;
-    if (tid < VV || (key_row && tid >= VV && tid < VV + KV)) {
-      const bool value = tid < VV;
-      const int col = 8 * (value ? tid : tid - VV);
-      T* e = decode_log<T>(p, ls, pos, value ? h : kh, col, value, DK, DV);
+    if (lr == 0) {
+#pragma unroll
+      for (int u = 0; u < TPW; ++u) {
+        T* e = decode_log<T>(p, ls, pos, h, j0[u], true, DK, DV);
+        if (e) *reinterpret_cast<uint2*>(e) =
+            make_uint2(out_pack2<T>(delta[u][0], delta[u][1]), out_pack2<T>(delta[u][2], delta[u][3]));
+      }
+    }
+    if (h % group == 0 && tid < KV) {
+      const int col = 8 * tid;
+      T* e = decode_log<T>(p, ls, pos, kh, col, false, DK, DV);
       if (e) {
         uint32_t pk[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float a = value ? s_delta[col + 2 * q] : to_f32(krow[col + 2 * q]) * rk;
-          const float c = value ? s_delta[col + 2 * q + 1] : to_f32(krow[col + 2 * q + 1]) * rk;
-          pk[q] = out_pack2<T>(a, c);
-        }
+        for (int q = 0; q < 4; ++q)
+          pk[q] = out_pack2<T>(to_f32(krow[col + 2 * q]) * rk, to_f32(krow[col + 2 * q + 1]) * rk);
         store_words<8>(e, pk);
       }
     }
@@ -632,21 +620,19 @@ __global__ __launch_bounds__(NT) void logstate_decode_kernel(LogDecodeParams p) 
   // ---- the work state: every step (eager), else at the end of a replay window
   if (p.eager || (pos + 1) % kReplayWindow == 0) {
 #pragma unroll
-    for (int r = 0; r < RPT; ++r) {
-      T* row = state_row<T>(p, w, h, r0 + r, DV);
+    for (int it = 0; it < RT; ++it) {
+      T* row = p.head_bytes <= p.frame_bytes ? (head ? const_cast<T*>(head) + (16 * it + lr) * DV : nullptr)
+                                             : state_row<T>(p, w, h, 16 * it + lr, DV);
       if (!row) continue;
-      uint32_t pk[NW];
 #pragma unroll
-      for (int j = 0; j < NW; ++j) {
-        float v2[2];
+      for (int u = 0; u < TPW; ++u) {
+        float v4[4];
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const int c = 2 * j + q;
-          v2[q] = p.eager ? S[r][c] : fmaf(kr[r], s_delta[c0 + c], S[r][c] * decay);
-        }
-        pk[j] = out_pack2<T>(v2[0], v2[1]);
+        for (int e = 0; e < 4; ++e)
+          v4[e] = p.eager ? Tt[u][it][e] : fmaf(delta[u][e], kv[it], Tt[u][it][e] * decay);
+        *reinterpret_cast<uint2*>(row + j0[u]) =
+            make_uint2(out_pack2<T>(v4[0], v4[1]), out_pack2<T>(v4[2], v4[3]));
       }
-      store_words<CPT>(row + c0, pk);
     }
   }
 }
@@ -731,7 +717,7 @@ constexpr int kRestoreSpan = kDecodeThreads;    // tokens whose suffix decays on
 // fp32 accumulators.  The suffix decays of 256 tokens come from one block
 // scan of their gates.
 template <int DK, int DV, class T>
-__global__ __launch_bounds__(kDecodeThreads) void restore_kernel(RestoreParams p) {
+__global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(2))) void restore_kernel(RestoreParams p) {
   constexpr int RT = DK / 16, CTT = DV / 16, CT = CTT >= 4 ? CTT / 4 : 1;
   constexpr int KV = DK / 8, VV = DV / 8;  // 16-byte pieces per row
   constexpr int PIECES = kRestoreGroup * (KV + VV) / kDecodeThreads;
@@ -748,26 +734,34 @@ __global__ __launch_bounds__(kDecodeThreads) void restore_kernel(RestoreParams p
   __shared__ uint16_t s_vt[DV * kRestoreLd];
   __shared__ float s_suffix[kRestoreSpan];
   __shared__ float s_part[kDecodeThreads / 64];
+  // acc[i][c] is the transposed tile T = S^T: lane l holds dk column
+  // i 16 + l % 16 and dv rows (wave CT + c) 16 + 4 (l / 16) .. + 3, i.e. four
+  // consecutive elements of one state row, moved as 8 bytes.
   f32x4 acc[RT][CT];
   const int64_t base = p.base[task];
   // Loads go to a valid address whatever the slot (an unmapped row reads the
-  // storage's first element and is then discarded), so every load is issued
-  // before the first wait: a select or branch on each freshly loaded value
-  // would wait for it alone.
+  // storage's first elements and is then discarded), so every load is issued
+  // before the first wait.
   const T* const safe = reinterpret_cast<const T*>(p.storage);
+  // state row r of slot s (a head inside one frame: one uniform lookup)
+  auto row_of = [&](int64_t s, const T* head, int r) __attribute__((always_inline)) -> const T* {
+    if (p.head_bytes <= p.frame_bytes) return head ? head + r * DV : nullptr;
+    return slot_row<T>(p, s, layer, h, r, DV);
+  };
+  const T* base_head = p.head_bytes <= p.frame_bytes ? slot_row<T>(p, base, layer, h, 0, DV) : nullptr;
 #pragma unroll
-  for (int i = 0; i < RT; ++i)
+  for (int i = 0; i < RT; ++i) {
+    const T* row = owner ? row_of(base, base_head, 16 * i + lr) : nullptr;
 #pragma unroll
     for (int c = 0; c < CT; ++c) {
-      const int col = (wave * CT + c) * 16 + lr;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const T* row = owner ? slot_row<T>(p, base, layer, h, i * 16 + 4 * lq + e, DV) : nullptr;
-        const T* src = row ? row + col : safe;
-        const float x = to_f32(*src);
-        acc[i][c][e] = row ? x : 0.f;
-      }
+      const int col = (wave * CT + c) * 16 + 4 * lq;
+      const uint2 w2 = *reinterpret_cast<const uint2*>(row ? row + col : safe);
+      float a, b2, c2, d;
+      split2<T>(row ? w2.x : 0u, a, b2);
+      split2<T>(row ? w2.y : 0u, c2, d);
+      acc[i][c] = f32x4{a, b2, c2, d};
     }
+  }
   for (int64_t seg = p.offsets[task]; seg < p.offsets[task + 1]; ++seg) {
     const int64_t ls = p.seg_slots[seg];
     int64_t fr = -1, ri = -1;
@@ -868,9 +862,9 @@ __global__ __launch_bounds__(kDecodeThreads) void restore_kernel(RestoreParams p
                   s_vt + ((wave * CT + c) * 16 + lr) * kRestoreLd + 32 * ks + 8 * lq);
 #pragma unroll
               for (int i = 0; i < RT; ++i) {
-                const uint4 afrag =
+                const uint4 kfrag =
                     *reinterpret_cast<const uint4*>(s_kt + (i * 16 + lr) * kRestoreLd + 32 * ks + 8 * lq);
-                acc[i][c] = RestoreMma<T>::run(afrag, bfrag, acc[i][c]);
+                acc[i][c] = RestoreMma<T>::run(bfrag, kfrag, acc[i][c]);  // T += V'^T K
               }
             }
         }
@@ -879,17 +873,18 @@ __global__ __launch_bounds__(kDecodeThreads) void restore_kernel(RestoreParams p
   }
   const int64_t out = p.output[task];
   if (!owner) return;
+  const T* out_head = p.head_bytes <= p.frame_bytes ? slot_row<T>(p, out, layer, h, 0, DV) : nullptr;
 #pragma unroll
-  for (int i = 0; i < RT; ++i)
+  for (int i = 0; i < RT; ++i) {
+    T* row = const_cast<T*>(row_of(out, out_head, 16 * i + lr));
+    if (!row) continue;
 #pragma unroll
     for (int c = 0; c < CT; ++c) {
-      const int col = (wave * CT + c) * 16 + lr;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        T* row = slot_row<T>(p, out, layer, h, i * 16 + 4 * lq + e, DV);
-        if (row) row[col] = from_f32<T>(acc[i][c][e]);
-      }
+      const int col = (wave * CT + c) * 16 + 4 * lq;
+      *reinterpret_cast<uint2*>(row + col) =
+          make_uint2(out_pack2<T>(acc[i][c][0], acc[i][c][1]), out_pack2<T>(acc[i][c][2], acc[i][c][3]));
     }
+  }
 }
 
 // grid (pairs x layers x HV): the state of (source, layer, head) to destination.
@@ -1080,12 +1075,10 @@ extern "C" int gdn_recurrent_logstate(
   auto s = static_cast<hipStream_t>(stream);
   auto launch = [&](auto dkc, auto dvc) {
     constexpr int DK = decltype(dkc)::value, DV = decltype(dvc)::value;
-    // 512 threads for the largest heads keep the per-thread state at 32 floats
-    constexpr int NT = DK * DV >= 128 * 128 ? 512 : kDecodeThreads;
     if (io_dtype == GDN_BF16)
-      hipLaunchKernelGGL((logstate_decode_kernel<DK, DV, bf16, NT>), grid, dim3(NT), 0, s, p);
+      hipLaunchKernelGGL((logstate_decode_kernel<DK, DV, bf16>), grid, dim3(DV * 4 / (DV >= 128 ? 2 : 1)), 0, s, p);
     else
-      hipLaunchKernelGGL((logstate_decode_kernel<DK, DV, f16, NT>), grid, dim3(NT), 0, s, p);
+      hipLaunchKernelGGL((logstate_decode_kernel<DK, DV, f16>), grid, dim3(DV * 4 / (DV >= 128 ? 2 : 1)), 0, s, p);
     return GDN_LAUNCH_CHECK("gdn_recurrent_logstate launch");
   };
   using I128 = std::integral_constant<int, 128>;
