@@ -24,8 +24,14 @@ import torch
 from ... import _lib
 
 
-def _vector(values, device) -> torch.Tensor:
-    return torch.tensor(list(values), dtype=torch.int32, device=device)
+def _vectors(groups, device) -> list[torch.Tensor]:
+    """The int32 vectors of ``groups`` on ``device`` from one packed host
+    copy (one transfer instead of one per vector)."""
+    sizes = [len(g) for g in groups]
+    host = torch.tensor([v for g in groups for v in g], dtype=torch.int32)
+    if torch.device(device).type == "cuda":
+        host = host.pin_memory()
+    return list(host.to(device, non_blocking=True).split(sizes))
 
 
 def _common(pool):
@@ -52,13 +58,14 @@ def restore_log_state_chains(pool, chains: Sequence[tuple[int | None, Sequence[t
     offsets = [0]
     for _base, logs, _out in chains:
         offsets.append(offsets[-1] + len(logs))
-    device = storage.device
-    base = _vector([-1 if b is None else b for b, _logs, _out in chains], device)
-    seg_offsets = _vector(offsets, device)
-    seg_slots = _vector([slot for slot, _b, _e in segments] or [0], device)
-    seg_begin = _vector([b for _s, b, _e in segments] or [0], device)
-    seg_end = _vector([e for _s, _b, e in segments] or [0], device)
-    outputs = _vector([out for _b, _logs, out in chains], device)
+    base, seg_offsets, seg_slots, seg_begin, seg_end, outputs = _vectors([
+        [-1 if b is None else b for b, _logs, _out in chains],
+        offsets,
+        [slot for slot, _b, _e in segments] or [0],
+        [b for _s, b, _e in segments] or [0],
+        [e for _s, _b, e in segments] or [0],
+        [out for _b, _logs, out in chains],
+    ], storage.device)
     decay = pool.decay_frame_table.contiguous()
     _lib.call(
         "gdn_logstate_restore",
@@ -107,8 +114,7 @@ def copy_states(pool, sources: Sequence[int], destinations: Sequence[int]) -> No
     assert len(sources) == len(destinations)
     storage, frames, num_frames = _common(pool)
     layout = pool.layout
-    src = _vector(sources, storage.device)
-    dst = _vector(destinations, storage.device)
+    src, dst = _vectors([list(sources), list(destinations)], storage.device)
     _lib.call(
         "gdn_logstate_copy_states",
         storage.data_ptr(), frames.data_ptr(), _lib.index_code(frames), frames.shape[1], pool.frame_bytes,
