@@ -256,8 +256,13 @@ def _decode_pool(g, slots, H, HV, dk, dv, layers, page, gran, conv_dim, W, frame
     return storage, payload, decay, conv.to(torch.int32), record, pool
 
 
-@pytest.mark.parametrize("eager", [False, True])
-def test_logstate_decode_steps(eager):
+# (eager, dk, dv): both modes at Qwen3-Next shape, the replay form at the other head shapes
+DECODE_CASES = [(False, 128, 128), (True, 128, 128), (False, 64, 64), (False, 32, 32), (False, 128, 64),
+                (True, 64, 128)]
+
+
+@pytest.mark.parametrize("case", DECODE_CASES)
+def test_logstate_decode_steps(case):
     """34 LogState decode steps (conv through the conv frame table, the
     recurrence from the work state plus the replayed log) against the oracle:
     outputs every step, then the work states, the log rows, the gates and the
@@ -265,10 +270,11 @@ def test_logstate_decode_steps(eager):
     conv_decode.py:293-352)."""
     from types import SimpleNamespace
     from logssms_amd.kernel.linear_attention import conv_decode, fused_recurrent_gated_delta_rule_to_logstate
-    g = gen(91 + int(eager))
-    B, H, HV, dk, dv, layers, layer, page, gran, W = 3, 2, 4, 128, 128, 2, 1, 64, 16, 4
+    eager, dk, dv = case
+    g = gen(91 + int(eager) + dk + 3 * dv)
+    B, H, HV, layers, layer, page, gran, W = 3, 2, 4, 2, 1, 64, 16, 4
     conv_dim = 2 * H * dk + HV * dv
-    frame_bytes, head_bytes = 65536, 32768
+    frame_bytes, head_bytes = 65536, dk * dv * 2
     slots = 6
     storage, payload, decay, conv, record, pool = _decode_pool(g, slots, H, HV, dk, dv, layers, page, gran, conv_dim,
                                                                W, frame_bytes, head_bytes)
@@ -282,7 +288,7 @@ def test_logstate_decode_steps(eager):
     pool.storage = dev_u8
     pool.payload_frame_table, pool.decay_frame_table, pool.conv_frame_table = payload.to(DEV), decay.to(DEV), conv.to(DEV)
     T = 34
-    print(f"LogState decode, eager={eager}: {T} steps x {B} sequences", flush=True)
+    print(f"LogState decode, eager={eager} dk={dk} dv={dv}: {T} steps x {B} sequences", flush=True)
     for t in range(T):
         mixed = (torch.randn(B, conv_dim, generator=g)).to(torch.bfloat16)
         a, bt = torch.randn(B, HV, generator=g), torch.randn(B, HV, generator=g)
@@ -458,7 +464,10 @@ def test_logstate_backend_prefill_then_decode(eager):
 
 # (H, frame_bytes, head_bytes, granularity): state heads inside a frame and
 # spanning two frames, one and two key heads
-RESTORE_CASES = [(1, 65536, 32768, 16), (2, 16384, 32768, 32), (2, 65536, 32768, 64)]
+# (H, frame_bytes, head_bytes, granularity, dk, dv)
+RESTORE_CASES = [(1, 65536, 32768, 16, 128, 128), (2, 16384, 32768, 32, 128, 128), (2, 65536, 32768, 64, 128, 128),
+                 (2, 65536, 8192, 32, 64, 64), (1, 65536, 2048, 16, 32, 32), (2, 65536, 16384, 32, 128, 64),
+                 (2, 16384, 16384, 32, 64, 128)]
 
 
 @pytest.mark.parametrize("case", RESTORE_CASES)
@@ -473,16 +482,16 @@ def test_logstate_store_copy_restore(case):
     segments one of which is empty (tests/kernel/test_logstate_granules.py:24-49
     is the model)."""
     from logssms_amd.kernel.linear_attention.logstate import copy_states, restore_log_state_chains, store_log_states
-    H, frame_bytes, head_bytes, gran = case
-    g = gen(101 + gran + H)
-    HV, dk, dv, layers, page, slots = 4, 128, 128, 2, 64, 7
+    H, frame_bytes, head_bytes, gran, dk, dv = case
+    g = gen(101 + gran + H + dk + dv)
+    HV, layers, page, slots = 4, 2, 64, 7
     storage, payload, decay, conv, record, pool = _decode_pool(g, slots, H, HV, dk, dv, layers, page, gran, 16, 4,
                                                                frame_bytes, head_bytes)
     expected = storage.clone()
     dev_u8 = storage.view(torch.uint8).to(DEV)
     pool.storage = dev_u8
     pool.payload_frame_table, pool.decay_frame_table = payload.to(DEV), decay.to(DEV)
-    print(f"store/copy/restore H={H} frame_bytes={frame_bytes} granularity={gran}", flush=True)
+    print(f"store/copy/restore H={H} frame_bytes={frame_bytes} granularity={gran} dk={dk} dv={dv}", flush=True)
     for slot in (1, 3):
         for layer in range(layers):
             heads = H if layer == 0 else HV  # keys per key head, then one row per value head
