@@ -417,9 +417,10 @@ __global__ __launch_bounds__(256) void conv_vec_kernel(FrontParams fp) {
   };
   while (t + W <= t1) phases(group);
   phases(tail);
-  if (FRONT && blockIdx.y == 0 && fp.g_out) {
+  if (FRONT && fp.g_out) {
+    // the tile's gates, split over the blocks of its channel groups
     const int n = static_cast<int>(t1 - t0);
-    for (int idx = threadIdx.x; idx < n * fp.HV; idx += 256) {
+    for (int idx = threadIdx.x + 256 * static_cast<int>(blockIdx.y); idx < n * fp.HV; idx += 256 * gridDim.y) {
       // head-major output: consecutive threads take consecutive tokens of a head
       const int64_t t = t0 + (fp.g_ld ? idx % n : idx / fp.HV);
       const int64_t h = fp.g_ld ? idx / n : idx % fp.HV;
