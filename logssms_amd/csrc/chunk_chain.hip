@@ -146,12 +146,6 @@ __device__ __forceinline__ h8_t bfrag(f4_t a, f4_t b) {
   return o;
 }
 
-template <class IOT> __device__ __forceinline__ uint16_t out_bits(float x);
-template <> __device__ __forceinline__ uint16_t out_bits<bf16>(float x) { return f32_to_bf16_bits(x); }
-template <> __device__ __forceinline__ uint16_t out_bits<f16>(float x) {
-  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
-}
-
 // Inclusive prefix sum over the 64 lanes of a wave with DPP moves (no LDS):
 // a scan within each 16-lane row (row_shr 1, 2, 4, 8), then the row totals
 // carried upwards (row_bcast 15 into rows 1 and 3, row_bcast 31 into rows 2
@@ -431,6 +425,25 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         V[2] = mma(a2, rb1, zero4());
         V[3] = mma(a3, rb1, zero4());
         vb1 = bfrag(V[2], V[3]);
+        if (vng) {
+          // v'^T = R^T A^T: the same fragments with the operands swapped (a
+          // B fragment of R is an A fragment of R^T), so lane (g, c) holds
+          // columns 4g..4g+3 of token 16 i + c and writes them as 8 bytes.
+          const f4_t vt[4] = {mma(rb0, a0, zero4()), mma(rb0, a1, zero4()), mma(rb1, a2, zero4()),
+                              mma(rb1, a3, zero4())};
+          char* vb = reinterpret_cast<char*>(vng + c * kC * tok_stride);
+          uint32_t ov = static_cast<uint32_t>((lr * tok_stride + 4 * lg) * 2);
+          asm volatile("" : "+v"(ov));
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (16 * i + lr < nv) {
+              uint2 w;
+              w.x = out_pack2<IOT>(vt[i][0], vt[i][1]);
+              w.y = out_pack2<IOT>(vt[i][2], vt[i][3]);
+              *reinterpret_cast<uint2*>(vb + 16 * i * tok_stride * 2 + ov) = w;
+            }
+          }
+        }
       }
       // ---- S3a: o^T += v'^T M^T; a lane holds 4 consecutive output columns of one token
       {
@@ -458,17 +471,6 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
             *reinterpret_cast<uint2*>(ob + 16 * i * tok_stride * 2 + o) = w;
           }
         }
-      }
-      if (vng) {  // v' (u - w h of the reference): uniform row base plus an opaque 32-bit lane offset
-        char* vb = reinterpret_cast<char*>(vng + c * kC * tok_stride);
-        uint32_t ov = static_cast<uint32_t>((4 * lg * tok_stride + lr) * 2);
-        asm volatile("" : "+v"(ov));
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (16 * i + 4 * lg + e < nv)
-              *reinterpret_cast<uint16_t*>(vb + (16 * i + e) * tok_stride * 2 + ov) = out_bits<IOT>(V[i][e]);
       }
       // ---- checkpoints inside the chunk (granularity 16 or 32): the state after
       // token te = (s + 1) gran - 1 is 2^G_te h + K^T (2^(G_te - G) v'), the
