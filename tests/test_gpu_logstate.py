@@ -268,17 +268,29 @@ def test_logstate_decode_steps(case):
     outputs every step, then the work states, the log rows, the gates and the
     conv windows (fused_recurrent.py:292-394, gdn_replay.py:17-148,
     conv_decode.py:293-352)."""
+    eager, dk, dv = case
+    _decode_steps(eager, dk, dv, seed=91 + int(eager) + dk + 3 * dv)
+
+
+@pytest.mark.parametrize("B", [64, 128])
+def test_logstate_decode_wide_batches(B):
+    """64 and 128 sequences at 16 key / 32 value heads (2048 and 4096 decode
+    blocks over 512 and 1024 slots): 18 steps against the oracle, with a
+    write-back at position 15 and replays of up to 15 logged tokens."""
+    _decode_steps(False, 64, 64, seed=7 + B, B=B, H=16, HV=32, layers=1, layer=0, page=32, gran=16, T=18)
+
+
+def _decode_steps(eager, dk, dv, seed, B=3, H=2, HV=4, layers=2, layer=1, page=64, gran=16, T=34):
     from types import SimpleNamespace
     from logssms_amd.kernel.linear_attention import conv_decode, fused_recurrent_gated_delta_rule_to_logstate
-    eager, dk, dv = case
-    g = gen(91 + int(eager) + dk + 3 * dv)
-    B, H, HV, layers, layer, page, gran, W = 3, 2, 4, 2, 1, 64, 16, 4
+    g = gen(seed)
+    W = 4
     conv_dim = 2 * H * dk + HV * dv
     frame_bytes, head_bytes = 65536, dk * dv * 2
-    slots = 6
+    slots = 2 * B
     storage, payload, decay, conv, record, pool = _decode_pool(g, slots, H, HV, dk, dv, layers, page, gran, conv_dim,
                                                                W, frame_bytes, head_bytes)
-    works, logs = torch.tensor([0, 2, 4]), torch.tensor([1, 3, 5])
+    works, logs = torch.arange(0, 2 * B, 2), torch.arange(1, 2 * B, 2)
     weight = (torch.randn(conv_dim, 1, W, generator=g) * 0.3).to(torch.bfloat16)
     A_log, dt_bias = torch.randn(HV, generator=g) * 0.3, torch.randn(HV, generator=g) * 0.3
     cfg = SimpleNamespace(state_len=W - 1, conv_dim=conv_dim, num_k_heads=H, head_k_dim=dk, num_v_heads=HV,
@@ -287,8 +299,7 @@ def test_logstate_decode_steps(case):
     dev_u8 = storage.view(torch.uint8).to(DEV)
     pool.storage = dev_u8
     pool.payload_frame_table, pool.decay_frame_table, pool.conv_frame_table = payload.to(DEV), decay.to(DEV), conv.to(DEV)
-    T = 34
-    print(f"LogState decode, eager={eager} dk={dk} dv={dv}: {T} steps x {B} sequences", flush=True)
+    print(f"LogState decode, eager={eager} dk={dk} dv={dv} HV={HV}: {T} steps x {B} sequences", flush=True)
     for t in range(T):
         mixed = (torch.randn(B, conv_dim, generator=g)).to(torch.bfloat16)
         a, bt = torch.randn(B, HV, generator=g), torch.randn(B, HV, generator=g)
@@ -321,7 +332,9 @@ def test_logstate_decode_steps(case):
     want = ofr.read_frame_states(expected, payload, works, layer, HV, dk, dv, frame_bytes, head_bytes)
     _report("work states", got, want)
     assert_state16_close(got, want)
-    # log rows (v' to the output bar, keys within one bf16 rounding step), gates, conv windows
+    # log rows (v' to the output bar; keys within two bf16 rounding steps: the
+    # conv output the key is normalised from may differ from the oracle's by
+    # one step, and the logged key is rounded again), gates, conv windows
     for b in range(B):
         vidx = torch.cat([ofr.log_element_index(payload, [int(logs[b])] * HV, [t] * HV, range(HV), range(dv), layer,
                                                 layers, gran, H, HV, dk, dv, frame_bytes, True) for t in range(T)])
@@ -329,7 +342,12 @@ def test_logstate_decode_steps(case):
         kidx = torch.cat([ofr.log_element_index(payload, [int(logs[b])] * H, [t] * H, range(H), range(dk), layer,
                                                 layers, gran, H, HV, dk, dv, frame_bytes, False) for t in range(T)])
         ka, ke = host.reshape(-1)[kidx].float(), expected.reshape(-1)[kidx].float()
-        assert ((ka - ke).abs() <= ke.abs() * 2.0 ** -7 + 1e-6).all()
+        bad = ~((ka - ke).abs() <= ke.abs() * 2.0 ** -6 + 1e-6)
+        if bad.any():
+            row, col = bad.nonzero()[0].tolist()
+            raise AssertionError(f"sequence {b}: {int(bad.sum())} logged key elements differ, first at token "
+                                 f"{row // H}, key head {row % H}, column {col}: {float(ka[row, col])} vs "
+                                 f"{float(ke[row, col])}")
     hb, eb = host.view(torch.uint8).reshape(-1), expected.view(torch.uint8).reshape(-1)
     for b in range(B):
         fr_, ri = int(decay[int(logs[b]), 0]), int(decay[int(logs[b]), 1])
