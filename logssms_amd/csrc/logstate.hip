@@ -285,6 +285,8 @@ struct LogDecodeParams {
   const void* counts; int counts_is64;
   int64_t layer, layers, gran, page;
   int eager;
+  int hpb;    // value heads per block (divides HV)
+  int group;  // value heads per key head
   void* out;
   float scale;
   Div32 fdiv, gdiv;  // frame_bytes, gran
@@ -300,21 +302,6 @@ __device__ __forceinline__ T* state_row(const LogDecodeParams& p, int64_t s, int
   const int64_t fr = load_index(p.frames, s * p.fps + p.fdiv.div(x), p.frames_is64);
   if (fr < 0 || fr >= p.num_frames) return nullptr;
   return reinterpret_cast<T*>(p.storage + fr * p.frame_bytes + p.fdiv.mod(x));
-}
-
-// 16-bit log element (the log layout of chunk_log_kernel, key heads = H).
-template <class T>
-__device__ __forceinline__ T* decode_log(const LogDecodeParams& p, int64_t slot, int64_t pos, int64_t index,
-                                         int64_t col, bool value, int DK, int DV) {
-  const int64_t key_size = p.gran * p.H * DK;
-  const int64_t layer_size = key_size + p.gran * p.HV * DV;
-  const uint32_t ps = static_cast<uint32_t>(pos);
-  const int64_t elem = (p.gdiv.div(ps) * p.layers + p.layer) * layer_size + (value ? key_size : 0) +
-                       (index * p.gran + p.gdiv.mod(ps)) * (value ? DV : DK) + col;
-  const uint32_t byte = static_cast<uint32_t>(2 * elem);
-  const int64_t fr = load_index(p.frames, slot * p.fps + p.fdiv.div(byte), p.frames_is64);
-  if (fr < 0 || fr >= p.num_frames) return nullptr;
-  return reinterpret_cast<T*>(p.storage + fr * p.frame_bytes + p.fdiv.mod(byte));
 }
 
 __device__ __forceinline__ float wave_sum(float x) {
@@ -373,267 +360,510 @@ template <> __device__ __forceinline__ f4_t mma16<f16>(uint2 a, uint2 b, f4_t c)
 // Sum over the 16 lanes of a row (every lane of the row receives it).
 __device__ __forceinline__ float row16_sum(float v) { return head_sum<16>(v); }
 
-constexpr int kReplayLd = kReplayWindow + 4;  // LDS row of one feature over the replay window
+// grid (batch x HV / hpb); a block takes hpb value heads of one sequence in
+// turn with NCW compute waves and one loading wave.
+//
+// The loading wave issues every global load of the block.  One head ahead of
+// the compute waves it resolves the head's frame-table entries and moves the
+// state (row-major, 16-byte chunks XOR-swizzled by row), the replayed log rows
+// (token-major, zero past the replay count), the q / k / v rows and the
+// step's store addresses into LDS -- the state and rows by direct-to-LDS
+// loads into a double buffer -- and waits for its own loads only.  The
+// compute waves read LDS, compute and store; they issue no global load, so no
+// wait of theirs covers a store, and a head's loads are in flight while the
+// previous head computes.  Two barriers per head: MID (the replayed rows are
+// consumed, the single row buffer may be refilled) and END (the next head is
+// resident).
+//
+// Compute wave w owns the TPW d_v row tiles TPW w .. of T = S^T (dv x dk),
+// held as 16 x 16 MFMA result tiles: lane l has the dk column 16 it + l % 16
+// of tile it and the dv rows 16 jt + 4 (l / 16) .. + 3 of row tile jt, four
+// consecutive elements of a state row.  The replay T += V'^T K is one 16-deep
+// MFMA per tile, its operands read from the token-major rows by LDS transpose
+// reads; S^T k and S^T q are per-lane FMAs and a 16-lane DPP sum.
+template <int DK, int DV>
+struct DecodeShape {
+  static constexpr int TPW = DV >= 128 ? 4 : 1;           // dv row tiles per compute wave
+  static constexpr int NCW = DV / (16 * TPW);             // compute waves
+  static constexpr int NT = 64 * (NCW + 1);               // threads (the last wave loads)
+  static constexpr int RT = DK / 16;                      // dk tiles
+  static constexpr int KV = DK / 8, VV = DV / 8;          // 16-byte chunks of a key / value row
+  static constexpr int SCH = DK * VV;                     // 16-byte chunks of a state
+  static constexpr int PCH = kReplayWindow * (KV + VV);   // 16-byte chunks of the replayed rows
+  static constexpr int QCH = 2 * KV + VV;                 // 16-byte chunks of q, k and v
+  static_assert(QCH <= 64 && SCH % 64 == 0 && PCH % 64 == 0, "chunk split");
+};
 
-// grid (batch x HV), DV / (16 TPW) waves.  The state is held transposed,
-// T = S^T (dv x dk), in 16 x 16 MFMA result tiles: wave w owns the TPW dv row
-// tiles TPW w .. and every dk column, lane l the dk column 16 it + l % 16 of
-// tile it and the dv rows 16 jt + 4 (l / 16) .. + 3 of row tile jt -- four
-// consecutive elements of one state row in memory, moved as 8 bytes.  Two
-// row tiles per wave (d_v = 128) keep 4 waves per block and 32 KiB of state
-// in flight per 4 waves, which sets the block's share of HBM bandwidth.  The replayed tokens' rank-n update
-// T += V'^T K runs as one 16-deep MFMA per tile from keys and scaled v' rows
-// staged feature-major in LDS; S^T k and S^T q are per-lane FMAs and a
-// 16-lane DPP sum, complete inside each wave.  Every global load is issued
-// before the first wait; the only barrier guards the staged replay rows.
+constexpr int kMaxHeadsPerBlock = 8;
+// A head's scalars, computed by the loading wave when the block starts.
+struct HeadScalars {
+  float g, decay, beta;
+  int state;  // frame-table entry of the work state (a head inside one frame)
+};
+template <int DK, int DV>
+struct HeadSlot {
+  int ok;                             // the work state is mapped
+  // byte offsets into the frame storage (-1: none); offsets rather than
+  // pointers, so that stores through them are known to be global stores
+  int64_t head;                       // work state (a head inside one frame)
+  int64_t vlog[DV / 8];               // the step's value row, per 16-byte chunk
+  int64_t klog[DK / 8];               // the step's key row
+  int64_t grec;                       // the step's gate record
+};
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef short s4v_t __attribute__((ext_vector_type(4)));
+// LDS transpose read: the 16 lanes of a group read a 4-row x 16-column block of
+// 16-bit values (lane r: row r / 4, columns 4 (r % 4)..+3) and lane r receives
+// column r of the 4 rows.
+__device__ __forceinline__ uint2 tr_read16(const uint16_t* p) {
+  typedef __attribute__((address_space(3))) s4v_t lds_s4;
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p)));
+}
+// Direct-to-LDS load of 16 bytes per active lane: lane l lands at lds + 16 l.
+__device__ __forceinline__ void dma16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (lds_void*)(lds), 16, 0, 0);
+}
+// x of the lane CTRL names inside the lane's 16-lane row (row_shr:k), 0 past the row start.
+template <int CTRL> __device__ __forceinline__ float dpp_shr(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, true));
+}
+// s_waitcnt vmcnt(0) lgkmcnt(0) as the builtin, so that the compiler knows
+// that every earlier load has landed and adds no wait of its own for them.
+__device__ __forceinline__ void wait_all() {
+  __builtin_amdgcn_s_waitcnt(0x0070);  // gfx9 encoding: vmcnt 0, expcnt 7 (no wait), lgkmcnt 0
+  asm volatile("" ::: "memory");
+}
+// Chunk position of logical chunk c in row r of a swizzled row-major array
+// with `chunks` 16-byte chunks per row (a power of two).
+__device__ __forceinline__ int swz_state(int r, int c, int chunks) { return c ^ (r & (chunks - 1)); }
+__device__ __forceinline__ int swz_rows(int t, int c, int chunks) { return c ^ ((2 * (t & 3)) & (chunks - 1)); }
+
 template <int DK, int DV, class T>
-__global__ __launch_bounds__(DV * 4 / (DV >= 128 ? 2 : 1)) __attribute__((amdgpu_waves_per_eu(3))) void logstate_decode_kernel(LogDecodeParams p) {
-  constexpr int TPW = DV >= 128 ? 2 : 1;         // dv row tiles per wave
-  constexpr int NT = DV * 4 / TPW, RT = DK / 16;  // threads; dk tiles per wave
-  constexpr int KV = DK / 8, VV = DV / 8;        // 16-byte pieces per row
-  constexpr int PIECES = (kReplayWindow * (KV + VV) + NT - 1) / NT;
-  static_assert(DK % 16 == 0 && DV % 16 == 0, "tile split");
-  const uint32_t bid = blockIdx.x, nhv = static_cast<uint32_t>(p.HV);
-  const int64_t b = bid / nhv, h = bid % nhv;
-  const int64_t group = p.HV / p.H, kh = h / group;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
-  int j0[TPW];  // this lane's dv rows j0[u] .. j0[u] + 3 of row tile TPW wave + u
-#pragma unroll
-  for (int u = 0; u < TPW; ++u) j0[u] = 16 * (TPW * wave + u) + 4 * lg;
-  __shared__ uint16_t s_kt[DK * kReplayLd];
-  __shared__ uint16_t s_vt[DV * kReplayLd];
+__global__ __launch_bounds__((DecodeShape<DK, DV>::NT)) __attribute__((amdgpu_waves_per_eu(2))) void logstate_decode_kernel(LogDecodeParams p) {
+  using S = DecodeShape<DK, DV>;
+  constexpr int TPW = S::TPW, NCW = S::NCW, RT = S::RT, KV = S::KV, VV = S::VV;
+  constexpr uint32_t kRow = DV * 2;  // bytes of a state row
+  static_assert(sizeof(T) == 2, "16-bit frames");
+  __shared__ __align__(16) uint16_t sS[2][DK * DV];                      // states
+  __shared__ __align__(16) uint16_t sP[kReplayWindow * (DK + DV)];       // replayed key rows, then value rows
+  __shared__ __align__(16) uint16_t sQ[2][2 * DK + DV];                  // q, k, v rows
+  __shared__ HeadSlot<DK, DV> sH[2];
+  __shared__ HeadScalars sHS[kMaxHeadsPerBlock];
+  __shared__ float sGt[kMaxHeadsPerBlock][kReplayWindow];  // replayed tokens' gates per head
+  __shared__ float sSfx[NCW][kReplayWindow];
+  uint16_t* const sPk = sP;
+  uint16_t* const sPv = sP + kReplayWindow * DK;
 
-  const int64_t w = load_index(p.work, b, p.work_is64);
-  const int64_t ls = load_index(p.logs, b, p.logs_is64);
-  const int64_t pos = load_index(p.offsets, b, p.offsets_is64);
+  const uint32_t nhv = static_cast<uint32_t>(p.HV), hpb = static_cast<uint32_t>(p.hpb);
+  const uint32_t group = static_cast<uint32_t>(p.group);
+  const uint32_t ngroups = nhv / hpb, bid = blockIdx.x;
+  const uint32_t b = bid / ngroups, h0 = (bid % ngroups) * hpb;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+
+  // ---- the sequence's slots, read by every wave (uniform)
+  const int w = static_cast<int>(load_index(p.work, b, p.work_is64));
+  const int ls = static_cast<int>(load_index(p.logs, b, p.logs_is64));
+  const int pos = static_cast<int>(load_index(p.offsets, b, p.offsets_is64));
   const bool in_page = ls >= 0 && pos >= 0 && pos < p.page;
-  int64_t n = p.eager || !in_page ? 0 : load_index(p.counts, b, p.counts_is64);
+  int n = p.eager || !in_page ? 0 : static_cast<int>(load_index(p.counts, b, p.counts_is64));
   n = n < 0 ? 0 : (n > kReplayWindow ? kReplayWindow : n);
   n = n > pos ? pos : n;  // the logged tokens precede the position within the page
-  float* rec = nullptr;  // decay record of the log slot
+  float* rec = nullptr;   // decay record of the log slot
   if (in_page) {
-    const int64_t fr = load_index(p.decay, 2 * ls, p.decay_is64);
-    const int64_t ri = load_index(p.decay, 2 * ls + 1, p.decay_is64);
+    const int64_t fr = load_index(p.decay, 2 * static_cast<int64_t>(ls), p.decay_is64);
+    const int64_t ri = load_index(p.decay, 2 * static_cast<int64_t>(ls) + 1, p.decay_is64);
     if (fr >= 0 && fr < p.num_frames && ri >= 0 && (ri + 1) * p.record_bytes <= p.frame_bytes)
       rec = reinterpret_cast<float*>(p.storage + fr * p.frame_bytes + ri * p.record_bytes);
   }
   if (!rec) n = 0;
-  // Loads go to a valid address whatever the slot (an unmapped row reads the
-  // storage's first bytes and is discarded), so no branch separates them.
-  const T* const safe = reinterpret_cast<const T*>(p.storage);
+  const bool one_frame = p.head_bytes <= p.frame_bytes;  // a head inside one frame
+  const uint32_t layer = static_cast<uint32_t>(p.layer), gran = static_cast<uint32_t>(p.gran);
 
-  // ---- every global load
-  uint2 raw[TPW][RT];  // S[16 it + lr][j0[u] .. j0[u] + 3]
-  bool row_ok[RT];
-  // a head inside one frame: one (uniform) frame lookup for all its rows
-  const T* head = p.head_bytes <= p.frame_bytes ? state_row<T>(p, w, h, 0, DV) : nullptr;
+  if (wave == NCW) {
+    // ==================================================================== loading wave
+    // The loading wave issues before the compute waves of its SIMD, and its
+    // frame arithmetic is shifts and masks for power-of-two frames.
+    __builtin_amdgcn_s_setprio(3);
+    auto loader = [&](auto pow2) __attribute__((always_inline)) {
+    constexpr bool POW2 = decltype(pow2)::value;
+    auto fdivv = [&](uint32_t x) -> uint32_t {
+      if constexpr (POW2) return x >> p.fdiv.shift;
+      else return x / p.fdiv.d;
+    };
+    auto fmodv = [&](uint32_t x) -> uint32_t {
+      if constexpr (POW2) return x & (p.fdiv.d - 1);
+      else return x % p.fdiv.d;
+    };
+    auto fbase = [&](int64_t fr) -> int64_t {
+      if constexpr (POW2) return fr << p.fdiv.shift;
+      else return fr * p.frame_bytes;
+    };
+    const int64_t wrow = static_cast<int64_t>(w >= 0 ? w : 0) * p.fps;   // frame-table rows of the slots
+    const int64_t lrow = static_cast<int64_t>(ls >= 0 ? ls : 0) * p.fps;
+    auto frame_at = [&](int64_t fr, uint32_t byte) -> char* {  // null for an unmapped entry
+      return fr >= 0 && fr < p.num_frames ? p.storage + fbase(fr) + fmodv(byte) : nullptr;
+    };
+    const uint32_t key_size = gran * static_cast<uint32_t>(p.H) * DK;
+    const uint32_t layer_size = key_size + gran * nhv * DV;
+    auto log_byte = [&](uint32_t t, uint32_t index, uint32_t col, bool value) -> uint32_t {
+      const uint32_t elem = (p.gdiv.div(t) * static_cast<uint32_t>(p.layers) + layer) * layer_size +
+                            (value ? key_size : 0u) + (index * gran + p.gdiv.mod(t)) * (value ? DV : DK) + col;
+      return 2u * elem;
+    };
+    auto state_byte = [&](uint32_t h) { return static_cast<uint32_t>((layer * nhv + h) * p.head_bytes); };
+    // log positions outside the page are never read or written; they look up position 0
+    const uint32_t tp = in_page ? static_cast<uint32_t>(pos) : 0u;
+    // replayed chunk k * 64 + lane: token t, chunk position c of its key or value
+    // row; its byte offset in the slot's log without the head term (per block)
+    constexpr int PK = S::PCH / 64;
+    bool pval[PK], plive[PK];
+    uint32_t pbase[PK];
 #pragma unroll
-  for (int it = 0; it < RT; ++it) {
-    const T* row = p.head_bytes <= p.frame_bytes ? (head ? head + (16 * it + lr) * DV : nullptr)
-                                                 : state_row<T>(p, w, h, 16 * it + lr, DV);
-    row_ok[it] = row != nullptr;
+    for (int k = 0; k < PK; ++k) {
+      const int P = k * 64 + lane;
+      const bool value = P >= kReplayWindow * KV;
+      const int Q = value ? P - kReplayWindow * KV : P;
+      const int per = value ? VV : KV;
+      const int t = Q / per, c = swz_rows(t, Q % per, per);  // logical chunk stored at this position
+      const uint32_t tok = in_page ? static_cast<uint32_t>(pos - n + (t < n ? t : 0)) : 0u;
+      pval[k] = value;
+      plive[k] = t < n;
+      pbase[k] = log_byte(tok, 0, 8u * c, value);
+    }
+    const uint32_t vhead = 2u * gran * DV, khead = 2u * gran * DK;  // log bytes per value / key head
+    const uint32_t vbase = log_byte(tp, 0, 8u * (lane < VV ? lane : 0), true);
+    const uint32_t kbase = log_byte(tp, 0, 8u * (lane < KV ? lane : 0), false);
+    // head h's frame-table entries and scalars, loaded one head ahead
+    struct Entries {
+      int piece[PK], vrow, krow;
+    };
+    auto entries = [&](uint32_t h) {
+      Entries e;
+      const uint32_t kh = h / group;
 #pragma unroll
-    for (int u = 0; u < TPW; ++u) raw[u][it] = *reinterpret_cast<const uint2*>(row ? row + j0[u] : safe);
-  }
-  const T* qrow = static_cast<const T*>(p.q) + (b * p.H + kh) * DK;
-  const T* krow = static_cast<const T*>(p.k) + (b * p.H + kh) * DK;
-  float qv[RT], kv[RT];  // q, k at this lane's dk columns
+      for (int k = 0; k < PK; ++k)
+        e.piece[k] = static_cast<int>(load_index(
+            p.frames, lrow + fdivv(pbase[k] + (pval[k] ? h * vhead : kh * khead)), p.frames_is64));
+      e.vrow = static_cast<int>(load_index(p.frames, lrow + fdivv(vbase + h * vhead), p.frames_is64));
+      e.krow = static_cast<int>(load_index(p.frames, lrow + fdivv(kbase + kh * khead), p.frames_is64));
+      return e;
+    };
+    // state rows: instruction k = 4 kk + j moves rows RPI k .. of the state; the
+    // lane part of its source offset depends on j only
+    constexpr int NI = S::SCH / 64, RPI = 64 / VV;
+    uint32_t soff[4];
 #pragma unroll
-  for (int it = 0; it < RT; ++it) {
-    qv[it] = to_f32(qrow[16 * it + lr]);
-    kv[it] = to_f32(krow[16 * it + lr]);
-  }
-  uint2 vraw[TPW];
+    for (int j = 0; j < 4; ++j) {
+      const int r = RPI * j + lane / VV;
+      soff[j] = r * kRow + 16 * swz_state(r, lane % VV, VV);
+    }
+    // state, q / k / v rows and the head's scalars and store addresses into slot s
+    auto fill_main = [&](uint32_t h, int s, const Entries& e) {
+      const uint32_t kh = h / group;
+      char* head = one_frame && w >= 0 ? frame_at(sHS[h - h0].state, state_byte(h)) : nullptr;
+      const bool ok = one_frame ? head != nullptr : w >= 0;
+      if (one_frame) {
+        if (head) {  // else the compute waves take a zero state
+#pragma unroll 1
+          for (int kk = 0; kk < (NI + 3) / 4; ++kk) {
 #pragma unroll
-  for (int u = 0; u < TPW; ++u)
-    vraw[u] = *reinterpret_cast<const uint2*>(static_cast<const T*>(p.v) + (b * p.HV + h) * DV + j0[u]);
-  const float a_log = load_any(p.A_log, h, p.a_dtype);
-  const float dt = load_any(p.dt_bias, h, p.dt_dtype);
-  const float graw = load_any(p.gate, b * p.gate_b + h * p.gate_h, p.gate_dtype);
-  const float braw = load_any(p.beta, b * p.beta_b + h * p.beta_h, p.beta_dtype);
-  const int64_t gbase = (p.layer * p.page + pos - n) * p.HV + h;
-  const float glane = lane < n ? rec[gbase + (lane < n ? lane : 0) * p.HV] : 0.f;  // replayed gate of token `lane`
-  uint4 pw[PIECES];  // replayed rows: piece j of token i (j < KV a key piece, else a value piece)
-  bool live[PIECES];
+            for (int j = 0; j < 4; ++j) {
+              const int k = 4 * kk + j;
+              if (k < NI) dma16(head + kk * 4 * RPI * kRow + soff[j], &sS[s][k * 64 * 8]);
+            }
+          }
+        }
+      } else if (w >= 0) {  // a head over several frames: a lookup per row, unmapped rows zero
+#pragma unroll 1
+        for (int k = 0; k < NI; ++k) {
+          const int P = k * 64 + lane, r = P / VV, c = swz_state(r, P % VV, VV);
+          const T* row = state_row<T>(p, w, h, r, DV);
+          if (row) dma16(reinterpret_cast<const char*>(row) + 16 * c, &sS[s][k * 64 * 8]);
+          else *reinterpret_cast<uint4*>(&sS[s][P * 8]) = make_uint4(0, 0, 0, 0);
+        }
+      }
+      // q, k, v rows
+      {
+        const T* q = static_cast<const T*>(p.q) + (static_cast<int64_t>(b) * p.H + kh) * DK;
+        const T* k = static_cast<const T*>(p.k) + (static_cast<int64_t>(b) * p.H + kh) * DK;
+        const T* v = static_cast<const T*>(p.v) + (static_cast<int64_t>(b) * nhv + h) * DV;
+        const int c = lane < KV ? lane : (lane < 2 * KV ? lane - KV : lane - 2 * KV);
+        const T* src = lane < KV ? q : (lane < 2 * KV ? k : v);
+        if (lane < S::QCH) dma16(src + 8 * c, &sQ[s][0]);
+      }
+      // scalars and addresses
+      HeadSlot<DK, DV>& hs = sH[s];
+      auto off = [&](const char* q) -> int64_t { return q ? q - p.storage : -1; };
+      if (lane < VV) hs.vlog[lane] = in_page ? off(frame_at(e.vrow, vbase + h * vhead)) : -1;
+      if (lane < KV) hs.klog[lane] = in_page && h % group == 0 ? off(frame_at(e.krow, kbase + kh * khead)) : -1;
+      if (lane == 0) {
+        hs.ok = ok ? 1 : 0;
+        hs.head = off(head);
+        hs.grec = in_page && rec ? off(reinterpret_cast<const char*>(
+                                       rec + (layer * static_cast<uint32_t>(p.page) + static_cast<uint32_t>(pos)) * nhv + h))
+                                 : -1;
+      }
+    };
+    // the replayed rows of head h into registers (issued early), then into LDS
+    // (zeros past n and for unmapped chunks)
+    struct Rows {
+      uint4 v[PK];
+      bool live[PK];
+    };
+    auto load_rows = [&](uint32_t h, const Entries& e) {
+      Rows r;
+      const uint32_t kh = h / group;
 #pragma unroll
-  for (int k = 0; k < PIECES; ++k) {
-    const int idx = tid + k * NT, i = idx / (KV + VV), j = idx % (KV + VV);
-    const bool value = j >= KV;
-    const int col = 8 * (value ? j - KV : j);
-    const T* e = i < n ? decode_log<T>(p, ls, pos - n + i, value ? h : kh, col, value, DK, DV) : nullptr;
-    live[k] = e != nullptr;
-    pw[k] = *reinterpret_cast<const uint4*>(e ? e : safe);
+      for (int k = 0; k < PK; ++k) {
+        const char* src = plive[k] ? frame_at(e.piece[k], pbase[k] + (pval[k] ? h * vhead : kh * khead)) : nullptr;
+        r.live[k] = src != nullptr;
+        r.v[k] = *reinterpret_cast<const uint4*>(src ? src : p.storage);
+      }
+      return r;
+    };
+    auto store_rows = [&](const Rows& r) {
+#pragma unroll
+      for (int k = 0; k < PK; ++k)
+        *reinterpret_cast<uint4*>(&sP[(k * 64 + lane) * 8]) = r.live[k] ? r.v[k] : make_uint4(0, 0, 0, 0);
+    };
+    // every head's scalars and work-state entry, and the replayed gates
+    if (lane < static_cast<int>(hpb)) {
+      const uint32_t h = h0 + lane;
+      const float a_log = load_any(p.A_log, h, p.a_dtype);
+      const float dt = load_any(p.dt_bias, h, p.dt_dtype);
+      const float graw = load_any(p.gate, b * p.gate_b + h * p.gate_h, p.gate_dtype);
+      const float braw = load_any(p.beta, b * p.beta_b + h * p.beta_h, p.beta_dtype);
+      const float g = -expf(a_log) * softplus_decode(graw + dt);
+      sHS[lane] = HeadScalars{g, expf(g), sigmoid(braw),
+                              static_cast<int>(load_index(p.frames, wrow + fdivv(state_byte(h)), p.frames_is64))};
+    }
+    for (int i = lane; i < static_cast<int>(hpb) * kReplayWindow; i += 64) {
+      const int hh = i / kReplayWindow, t = i % kReplayWindow;
+      const uint32_t gbase = (layer * static_cast<uint32_t>(p.page) + static_cast<uint32_t>(pos - n)) * nhv + h0 + hh;
+      sGt[hh][t] = t < n ? rec[gbase + (t < n ? t : 0) * nhv] : 0.f;
+    }
+    wait_all();
+    Entries cur = entries(h0);
+    fill_main(h0, 0, cur);
+    store_rows(load_rows(h0, cur));
+    cur = entries(hpb > 1 ? h0 + 1 : h0);
+    wait_all();
+    lds_barrier();  // head 0 resident
+    for (uint32_t hi = 0; hi < hpb; ++hi) {
+      const bool more = hi + 1 < hpb;
+      Rows rows;
+      Entries nxt = cur;
+      if (more) {
+        fill_main(h0 + hi + 1, (hi + 1) & 1, cur);
+        rows = load_rows(h0 + hi + 1, cur);
+        nxt = entries(hi + 2 < hpb ? h0 + hi + 2 : h0 + hi + 1);
+      }
+      lds_barrier();  // MID: the compute waves have read the replayed rows
+      if (more) store_rows(rows);
+      cur = nxt;
+      wait_all();
+      lds_barrier();  // END: the next head is resident
+    }
+    };
+    if (p.fdiv.shift >= 0) loader(std::true_type{});
+    else loader(std::false_type{});
+    return;
   }
 
-  // ---- norms, gates and the replay decays (every wave computes them)
-  float qq = 0.f, kk = 0.f, qk = 0.f;
+  // ====================================================================== compute waves
+  int j0[TPW];  // this lane's dv rows j0[u] .. j0[u] + 3 of row tile TPW wave + u
 #pragma unroll
-  for (int it = 0; it < RT; ++it) {
-    qq = fmaf(qv[it], qv[it], qq);
-    kk = fmaf(kv[it], kv[it], kk);
-    qk = fmaf(qv[it], kv[it], qk);
-  }
-  qq = row16_sum(qq);
-  kk = row16_sum(kk);
-  qk = row16_sum(qk);
-  const float rq = rsqrtf(qq + 1e-6f) * p.scale, rk = rsqrtf(kk + 1e-6f);
-  const float kq = qk * rq * rk;
-#pragma unroll
-  for (int it = 0; it < RT; ++it) {
-    qv[it] *= rq;
-    kv[it] *= rk;
-  }
-  const float g = -expf(a_log) * softplus_decode(graw + dt);
-  const float decay = expf(g), beta = sigmoid(braw);
-  // inclusive scan of the replayed gates over lanes 0 .. n-1; suffix_i = e^{total - prefix_i}
-  float scan = glane;
-#pragma unroll
-  for (int off = 1; off < kReplayWindow; off <<= 1) {
-    const float y = __shfl_up(scan, off, 64);
-    if (lane >= off) scan += y;
-  }
-  const float total = __shfl(scan, kReplayWindow - 1, 64);
-  const float suffix = expf(total - scan);  // lanes < n
-  const float total_decay = expf(total);
-
-  // ---- the state, decayed over the replayed tokens
-  f4_t Tt[TPW][RT];
-#pragma unroll
-  for (int u = 0; u < TPW; ++u)
+  for (int u = 0; u < TPW; ++u) j0[u] = 16 * (TPW * wave + u) + 4 * lg;
+  lds_barrier();  // head 0 resident
+  for (uint32_t hi = 0; hi < hpb; ++hi) {
+    const uint32_t h = h0 + hi;
+    const int s = hi & 1;
+    const HeadSlot<DK, DV>& hs = sH[s];
+    const uint16_t* q = &sQ[s][0];
+    const uint16_t* k = q + DK;
+    const uint16_t* v = k + DK;
+    float qv[RT], kv[RT];  // q, k at this lane's dk columns
 #pragma unroll
     for (int it = 0; it < RT; ++it) {
-      float a, c2, d, e;
-      split2<T>(row_ok[it] ? raw[u][it].x : 0u, a, c2);
-      split2<T>(row_ok[it] ? raw[u][it].y : 0u, d, e);
-      Tt[u][it] = f4_t{a, c2, d, e} * total_decay;
+      qv[it] = to_f32(__builtin_bit_cast(T, q[16 * it + lr]));
+      kv[it] = to_f32(__builtin_bit_cast(T, k[16 * it + lr]));
     }
-  if (n > 0) {
-    // stage the replayed rows feature-major (token index contiguous): keys,
-    // and values scaled by their suffix decay and rounded to the state dtype
+    // ---- norms, gates and the replay decays (every wave computes them)
+    float qq = 0.f, kk = 0.f, qk = 0.f;
 #pragma unroll
-    for (int k = 0; k < PIECES; ++k) {
-      const int idx = tid + k * NT, i = idx / (KV + VV), j = idx % (KV + VV);
-      const float sfx = __shfl(suffix, i < kReplayWindow ? i : 0, 64);
-      if (i >= kReplayWindow) continue;
-      const bool value = j >= KV;
-      const int col = 8 * (value ? j - KV : j);
-      const bool keep = live[k] && i < n;  // tokens i >= n stage zeros
-      const uint32_t wv[4] = {keep ? pw[k].x : 0u, keep ? pw[k].y : 0u, keep ? pw[k].z : 0u, keep ? pw[k].w : 0u};
-      uint16_t* dst = (value ? s_vt : s_kt) + col * kReplayLd + i;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        uint32_t word = wv[q];
-        if (value) {
-          float a, c2;
-          split2<T>(word, a, c2);
-          word = out_pack2<T>(a * sfx, c2 * sfx);
-        }
-        dst[(2 * q) * kReplayLd] = static_cast<uint16_t>(word & 0xffffu);
-        dst[(2 * q + 1) * kReplayLd] = static_cast<uint16_t>(word >> 16);
-      }
+    for (int it = 0; it < RT; ++it) {
+      qq = fmaf(qv[it], qv[it], qq);
+      kk = fmaf(kv[it], kv[it], kk);
+      qk = fmaf(qv[it], kv[it], qk);
     }
-    lds_barrier();
-    // T += V'^T K over the replayed tokens (zero rows past n)
+    qq = row16_sum(qq);
+    kk = row16_sum(kk);
+    qk = row16_sum(qk);
+    const float rq = rsqrtf(qq + 1e-6f) * p.scale, rk = rsqrtf(kk + 1e-6f);
+    const float kq = qk * rq * rk;
 #pragma unroll
-    for (int u = 0; u < TPW; ++u) {
-      const uint2 af = *reinterpret_cast<const uint2*>(s_vt + (16 * (TPW * wave + u) + lr) * kReplayLd + 4 * lg);
-#pragma unroll
-      for (int it = 0; it < RT; ++it) {
-        const uint2 bf = *reinterpret_cast<const uint2*>(s_kt + (16 * it + lr) * kReplayLd + 4 * lg);
-        Tt[u][it] = mma16<T>(af, bf, Tt[u][it]);
-      }
+    for (int it = 0; it < RT; ++it) {
+      qv[it] *= rq;
+      kv[it] *= rk;
     }
-  }
+    const float decay = sHS[hi].decay, beta = sHS[hi].beta;
+    // inclusive scan of the replayed gates over lanes 0 .. n-1 (DPP shifts
+    // inside the first 16-lane row); suffix_i = e^{total - prefix_i}
+    float scan = lane < n ? sGt[hi][lane & (kReplayWindow - 1)] : 0.f;
+    scan += dpp_shr<0x111>(scan);
+    scan += dpp_shr<0x112>(scan);
+    scan += dpp_shr<0x114>(scan);
+    scan += dpp_shr<0x118>(scan);
+    const float total = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(scan), kReplayWindow - 1));
+    const float total_decay = expf(total);
+    if (lane < kReplayWindow) {
+      int l = lane;  // opaque, so that no address is held in a register across heads
+      asm volatile("" : "+v"(l));
+      (&sSfx[0][0])[wave * kReplayWindow + l] = expf(total - scan);
+    }
 
-  // ---- one step: row sums of T against k and q (S^T k, S^T q) for rows j0 + e
-  float delta[TPW][4], out[TPW][4];
-#pragma unroll
-  for (int u = 0; u < TPW; ++u) {
-    float vin[4];
-    split2<T>(vraw[u].x, vin[0], vin[1]);
-    split2<T>(vraw[u].y, vin[2], vin[3]);
-    if (p.eager) {
-      // S <- e^g S; delta = (v - S^T k) beta; S <- S + k delta^T; o = S^T q
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float acc = 0.f;
-#pragma unroll
-        for (int it = 0; it < RT; ++it) {
-          Tt[u][it][e] *= decay;
-          acc = fmaf(Tt[u][it][e], kv[it], acc);
-        }
-        delta[u][e] = (vin[e] - row16_sum(acc)) * beta;
-        float accq = 0.f;
-#pragma unroll
-        for (int it = 0; it < RT; ++it) {
-          Tt[u][it][e] = fmaf(delta[u][e], kv[it], Tt[u][it][e]);
-          accq = fmaf(Tt[u][it][e], qv[it], accq);
-        }
-        out[u][e] = row16_sum(accq);
-      }
-    } else {
-      // delta = (v - e^g S^T k) beta; o = e^g S^T q + delta (k . q)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float ak = 0.f, aq = 0.f;
-#pragma unroll
-        for (int it = 0; it < RT; ++it) {
-          ak = fmaf(Tt[u][it][e], kv[it], ak);
-          aq = fmaf(Tt[u][it][e], qv[it], aq);
-        }
-        delta[u][e] = (vin[e] - row16_sum(ak) * decay) * beta;
-        out[u][e] = row16_sum(aq) * decay + delta[u][e] * kq;
-      }
-    }
-  }
-
-  // ---- output and the step's log rows
-  if (lr == 0) {
+    // ---- the state, decayed over the replayed tokens
+    f4_t Tt[TPW][RT];
 #pragma unroll
     for (int u = 0; u < TPW; ++u)
-      *reinterpret_cast<uint2*>(static_cast<T*>(p.out) + (b * p.HV + h) * DV + j0[u]) =
-          make_uint2(out_pack2<T>(out[u][0], out[u][1]), out_pack2<T>(out[u][2], out[u][3]));
-  }
-  if (in_page) {
-    if (lr == 0) {
+#pragma unroll
+      for (int it = 0; it < RT; ++it) {
+        const int r = 16 * it + lr, c = j0[u] >> 3;
+        const uint2 raw = *reinterpret_cast<const uint2*>(&sS[s][r * DV + 8 * swz_state(r, c, VV) + (j0[u] & 7)]);
+        float a, c2, d, e;
+        split2<T>(hs.ok ? raw.x : 0u, a, c2);
+        split2<T>(hs.ok ? raw.y : 0u, d, e);
+        Tt[u][it] = f4_t{a, c2, d, e} * total_decay;
+      }
+    if (n > 0) {
+      // T += V'^T K: values scaled by their suffix decay and rounded to the
+      // state dtype (tokens past n are zero rows)
+      f4_t sfx;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sfx[e] = sSfx[wave][4 * lg + e];
+      auto row_addr = [&](const uint16_t* base, int per, int col) {  // lane's transpose-read address
+        const int t = 4 * lg + (lr >> 2), cc = (col >> 3), half = (col & 7);
+        return base + t * per * 8 + 8 * swz_rows(t, cc, per) + half;
+      };
 #pragma unroll
       for (int u = 0; u < TPW; ++u) {
-        T* e = decode_log<T>(p, ls, pos, h, j0[u], true, DK, DV);
-        if (e) *reinterpret_cast<uint2*>(e) =
-            make_uint2(out_pack2<T>(delta[u][0], delta[u][1]), out_pack2<T>(delta[u][2], delta[u][3]));
-      }
-    }
-    if (h % group == 0 && tid < KV) {
-      const int col = 8 * tid;
-      T* e = decode_log<T>(p, ls, pos, kh, col, false, DK, DV);
-      if (e) {
-        uint32_t pk[4];
+        const uint2 raw = tr_read16(row_addr(sPv, VV, 16 * (TPW * wave + u) + 4 * (lr & 3)));
+        float a, c2, d, e;
+        split2<T>(raw.x, a, c2);
+        split2<T>(raw.y, d, e);
+        const uint2 af = make_uint2(out_pack2<T>(a * sfx[0], c2 * sfx[1]), out_pack2<T>(d * sfx[2], e * sfx[3]));
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          pk[q] = out_pack2<T>(to_f32(krow[col + 2 * q]) * rk, to_f32(krow[col + 2 * q + 1]) * rk);
-        store_words<8>(e, pk);
+        for (int it = 0; it < RT; ++it) {
+          const uint2 bf = tr_read16(row_addr(sPk, KV, 16 * it + 4 * (lr & 3)));
+          Tt[u][it] = mma16<T>(af, bf, Tt[u][it]);
+        }
       }
     }
-    if (rec && tid == 0) rec[(p.layer * p.page + pos) * p.HV + h] = g;
-  }
+    float vin[TPW][4];
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) {
+      const uint2 raw = *reinterpret_cast<const uint2*>(v + j0[u]);
+      split2<T>(raw.x, vin[u][0], vin[u][1]);
+      split2<T>(raw.y, vin[u][2], vin[u][3]);
+    }
+    lds_barrier();  // MID: the replayed rows are consumed
 
-  // ---- the work state: every step (eager), else at the end of a replay window
-  if (p.eager || (pos + 1) % kReplayWindow == 0) {
+    // ---- the step's scalars and store addresses (this slot's stay until END)
+    const float g = sHS[hi].g;
+    const bool ok = hs.ok != 0;
+    const int64_t klog = hs.klog[tid % KV];
+    const int64_t grec = hs.grec;
+    const bool write_back = ok && (p.eager || (pos + 1) % kReplayWindow == 0);
+    char* const orow = static_cast<char*>(p.out) + (static_cast<int64_t>(b) * nhv + h) * kRow;
+    // a work state in one frame: a uniform base plus an opaque 32-bit lane offset
+    const uint64_t ho = hs.head;
+    char* const hb = p.storage + ((static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(ho >> 32)))
+                                   << 32) |
+                                  __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(ho)));
+
+    // ---- one step per d_v tile: row sums of T against k and q (S^T k, S^T q)
+    // for rows j0 + e, then the tile's output, log row and work-state rows
 #pragma unroll
-    for (int it = 0; it < RT; ++it) {
-      T* row = p.head_bytes <= p.frame_bytes ? (head ? const_cast<T*>(head) + (16 * it + lr) * DV : nullptr)
-                                             : state_row<T>(p, w, h, 16 * it + lr, DV);
-      if (!row) continue;
+    for (int u = 0; u < TPW; ++u) {
+      float delta[4], out[4];
+      if (p.eager) {
+        // S <- e^g S; delta = (v - S^T k) beta; S <- S + k delta^T; o = S^T q
 #pragma unroll
-      for (int u = 0; u < TPW; ++u) {
-        float v4[4];
+        for (int e = 0; e < 4; ++e) {
+          float acc = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          v4[e] = p.eager ? Tt[u][it][e] : fmaf(delta[u][e], kv[it], Tt[u][it][e] * decay);
-        *reinterpret_cast<uint2*>(row + j0[u]) =
-            make_uint2(out_pack2<T>(v4[0], v4[1]), out_pack2<T>(v4[2], v4[3]));
+          for (int it = 0; it < RT; ++it) {
+            Tt[u][it][e] *= decay;
+            acc = fmaf(Tt[u][it][e], kv[it], acc);
+          }
+          delta[e] = (vin[u][e] - row16_sum(acc)) * beta;
+          float accq = 0.f;
+#pragma unroll
+          for (int it = 0; it < RT; ++it) {
+            Tt[u][it][e] = fmaf(delta[e], kv[it], Tt[u][it][e]);
+            accq = fmaf(Tt[u][it][e], qv[it], accq);
+          }
+          out[e] = row16_sum(accq);
+        }
+      } else {
+        // delta = (v - e^g S^T k) beta; o = e^g S^T q + delta (k . q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float ak = 0.f, aq = 0.f;
+#pragma unroll
+          for (int it = 0; it < RT; ++it) {
+            ak = fmaf(Tt[u][it][e], kv[it], ak);
+            aq = fmaf(Tt[u][it][e], qv[it], aq);
+          }
+          delta[e] = (vin[u][e] - row16_sum(ak) * decay) * beta;
+          out[e] = row16_sum(aq) * decay + delta[e] * kq;
+        }
+      }
+      if (lr == 0) {
+        uint32_t o = 2 * j0[u];  // opaque 32-bit lane offset from a uniform base
+        asm volatile("" : "+v"(o));
+        *reinterpret_cast<uint2*>(orow + o) = make_uint2(out_pack2<T>(out[0], out[1]), out_pack2<T>(out[2], out[3]));
+        const int64_t vlog = hs.vlog[j0[u] >> 3];
+        if (vlog >= 0)
+          *reinterpret_cast<uint2*>(p.storage + vlog + (o & 15)) =
+              make_uint2(out_pack2<T>(delta[0], delta[1]), out_pack2<T>(delta[2], delta[3]));
+      }
+      // the work state: every step (eager), else at the end of a replay window
+      if (write_back) {
+#pragma unroll
+        for (int it = 0; it < RT; ++it) {
+          uint32_t lo = lr * kRow + 2 * j0[u];
+          asm volatile("" : "+v"(lo));
+          char* row = hb + it * 16 * kRow + lo;
+          if (!one_frame) {  // a head over several frames: a lookup per row
+            T* r = state_row<T>(p, w, h, 16 * it + lr, DV);
+            if (!r) continue;
+            row = reinterpret_cast<char*>(r) + 2 * j0[u];
+          }
+          float v4[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v4[e] = p.eager ? Tt[u][it][e] : fmaf(delta[e], kv[it], Tt[u][it][e] * decay);
+          *reinterpret_cast<uint2*>(row) = make_uint2(out_pack2<T>(v4[0], v4[1]), out_pack2<T>(v4[2], v4[3]));
+        }
       }
     }
+    if (tid < KV && klog >= 0) {
+      int c = 8 * tid;  // opaque, as above
+      asm volatile("" : "+v"(c));
+      const uint4 raw = *reinterpret_cast<const uint4*>(k + c);
+      const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
+      uint32_t pk[4];
+#pragma unroll
+      for (int q2 = 0; q2 < 4; ++q2) {
+        float a, b2;
+        split2<T>(wv[q2], a, b2);
+        pk[q2] = out_pack2<T>(a * rk, b2 * rk);
+      }
+      *reinterpret_cast<uint4*>(p.storage + klog) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    }
+    if (grec >= 0 && tid == 0) *reinterpret_cast<float*>(p.storage + grec) = g;
+    lds_barrier();  // END: the next head is resident
   }
 }
 
@@ -1071,14 +1301,21 @@ extern "C" int gdn_recurrent_logstate(
   p.layer = layer; p.layers = num_layers; p.gran = granularity; p.page = page_size;
   p.fdiv = make_div32(frame_bytes); p.gdiv = make_div32(granularity);
   p.eager = eager; p.out = out; p.scale = scale;
-  const dim3 grid(static_cast<unsigned>(batch * HV));
+  p.group = static_cast<int>(HV / H);
+  // Heads per block: a block's first head waits for the whole lookup chain,
+  // the later ones overlap the previous head's compute; up to 8 while the
+  // grid keeps 1024 blocks (2 rounds of 2 blocks per CU), fewer for small batches.
+  p.hpb = 1;
+  while (p.hpb < kMaxHeadsPerBlock && HV % (2 * p.hpb) == 0 && batch * HV / (2 * p.hpb) >= 1024) p.hpb *= 2;
+  const dim3 grid(static_cast<unsigned>(batch * HV / p.hpb));
   auto s = static_cast<hipStream_t>(stream);
   auto launch = [&](auto dkc, auto dvc) {
     constexpr int DK = decltype(dkc)::value, DV = decltype(dvc)::value;
+    const dim3 block(DecodeShape<DK, DV>::NT);
     if (io_dtype == GDN_BF16)
-      hipLaunchKernelGGL((logstate_decode_kernel<DK, DV, bf16>), grid, dim3(DV * 4 / (DV >= 128 ? 2 : 1)), 0, s, p);
+      hipLaunchKernelGGL((logstate_decode_kernel<DK, DV, bf16>), grid, block, 0, s, p);
     else
-      hipLaunchKernelGGL((logstate_decode_kernel<DK, DV, f16>), grid, dim3(DV * 4 / (DV >= 128 ? 2 : 1)), 0, s, p);
+      hipLaunchKernelGGL((logstate_decode_kernel<DK, DV, f16>), grid, block, 0, s, p);
     return GDN_LAUNCH_CHECK("gdn_recurrent_logstate launch");
   };
   using I128 = std::integral_constant<int, 128>;

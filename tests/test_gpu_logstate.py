@@ -272,11 +272,13 @@ def test_logstate_decode_steps(case):
     _decode_steps(eager, dk, dv, seed=91 + int(eager) + dk + 3 * dv)
 
 
-@pytest.mark.parametrize("B", [64, 128])
+@pytest.mark.parametrize("B", [64, 128, 256])
 def test_logstate_decode_wide_batches(B):
-    """64 and 128 sequences at 16 key / 32 value heads (2048 and 4096 decode
-    blocks over 512 and 1024 slots): 18 steps against the oracle, with a
-    write-back at position 15 and replays of up to 15 logged tokens."""
+    """64, 128 and 256 sequences at 16 key / 32 value heads, where a decode
+    block takes 2, 4 and 8 value heads of its sequence in turn (its loading
+    wave fetching the next head while the current one computes): 18 steps
+    against the oracle, with a write-back at position 15 and replays of up to
+    15 logged tokens."""
     _decode_steps(False, 64, 64, seed=7 + B, B=B, H=16, HV=32, layers=1, layer=0, page=32, gran=16, T=18)
 
 
