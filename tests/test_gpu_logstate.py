@@ -282,13 +282,22 @@ def test_logstate_decode_wide_batches(B):
     _decode_steps(False, 64, 64, seed=7 + B, B=B, H=16, HV=32, layers=1, layer=0, page=32, gran=16, T=18)
 
 
-def _decode_steps(eager, dk, dv, seed, B=3, H=2, HV=4, layers=2, layer=1, page=64, gran=16, T=34):
+@pytest.mark.parametrize("eager,dk,frame_bytes", [(False, 64, 49152), (False, 128, 16384), (True, 128, 16384)])
+def test_logstate_decode_frame_shapes(eager, dk, frame_bytes):
+    """Frames of a size that is not a power of two (49152 bytes: frame
+    arithmetic by division) and frames smaller than a head (a 128 x 128 bf16
+    head over two 16 KiB frames: a frame lookup per state row, for the loads
+    and for the write-backs): LogState decode steps against the oracle."""
+    _decode_steps(eager, dk, dk, seed=301 + dk + frame_bytes // 4096 + int(eager), frame_bytes=frame_bytes, T=20)
+
+
+def _decode_steps(eager, dk, dv, seed, B=3, H=2, HV=4, layers=2, layer=1, page=64, gran=16, T=34, frame_bytes=65536):
     from types import SimpleNamespace
     from logssms_amd.kernel.linear_attention import conv_decode, fused_recurrent_gated_delta_rule_to_logstate
     g = gen(seed)
     W = 4
     conv_dim = 2 * H * dk + HV * dv
-    frame_bytes, head_bytes = 65536, dk * dv * 2
+    head_bytes = dk * dv * 2
     slots = 2 * B
     storage, payload, decay, conv, record, pool = _decode_pool(g, slots, H, HV, dk, dv, layers, page, gran, conv_dim,
                                                                W, frame_bytes, head_bytes)
