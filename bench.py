@@ -644,15 +644,15 @@ def logstate_gpu(dev, steps, warmup, B=256):
                       layer=0, num_layers=1, granularity=LS_GRAN, page_size=LS_PAGE)
     log = ChunkLogIO(slots=log_slots, token_offsets=offsets, decay_frames=ppool.decay_frame_table, gate=gg,
                      page_size=LS_PAGE, decay_record_bytes=ppool.layout.log_decay_bytes, num_key_heads=H)
-    def prefill_step():
-        chunk_gated_delta_rule_to_cache(q, k, v, gg, bb, io, cu, chunk_size=LS_GRAN, log_io=log)
+    def prefill_step():  # as the LogState backend calls it: v' into the log only
+        chunk_gated_delta_rule_to_cache(q, k, v, gg, bb, io, cu, chunk_size=LS_GRAN, log_io=log, return_v_new=False)
 
     pf_ms = _time(prefill_step, max(steps // 2, 5), warmup)
     flops = FLOP_PER_TOKEN_HEAD * T * HV
     out["prefill"] = {
         "config": "BASELINE config 2 lengths (4 x 4096), bf16 frame-table states in and out of work slots, "
                   "checkpoints every 1024 tokens, granularity 32, every token logged (v', key, gate); one step "
-                  "= the chunk kernel (v' written out) + the token-log store",
+                  "= the chunk kernel (v' rows written into the log) + the key / gate log store",
         "ms": pf_ms, "tokens/s": T / (pf_ms * 1e-3), "step_tflops": flops / (pf_ms * 1e-3) / 1e12,
         "frac_mfma": flops / (pf_ms * 1e-3) / PEAK_MFMA_16BIT}
     del ppool, io, log

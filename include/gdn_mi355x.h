@@ -142,13 +142,40 @@ int gdn_chunk_gated_delta_rule(const void* q, const void* k, const void* v, int 
                                void* stream);
 
 /*
+ * gdn_chunk_gated_delta_rule on frame storage with the token log's value rows
+ * written by the chunk kernel itself: replaces the v_new output of the chunked
+ * rule (vendor/fla/chunk_delta_h.py:183-192) followed by the value-row stores
+ * of the log (kernel/linear_attention/state_io.py:83-126), so v' never makes
+ * an HBM round trip.  Arguments as gdn_chunk_gated_delta_rule (the state is
+ * the frame storage, frames required; no strides, no v_new) plus the log
+ * arguments of gdn_store_chunk_log: for every token t with log_slots[t] >= 0
+ * and 0 <= token_offsets[t] < page_size, v'[t, h, :] goes to the value row
+ * (h, position) of that slot's log.  Keys and gates are then stored by
+ * gdn_store_chunk_log with v_new = NULL.  Needs dv % 64 == 0, frames of a
+ * multiple of 128 bytes and io dtype == state dtype; returns status 2
+ * (unsupported, nothing launched) otherwise.
+ */
+int gdn_chunk_gated_delta_rule_logged(const void* q, const void* k, const void* v, int io_dtype, const float* g,
+                                      const float* beta, const void* cu_seqlens, int cu_dtype, int64_t num_seqs,
+                                      int64_t total_tokens, int64_t H, int64_t HV, int64_t dk, int64_t dv,
+                                      void* state, int state_dtype, int64_t layer, const void* read_slots,
+                                      int read_dtype, const void* chunk_write_slots, int chunk_write_dtype,
+                                      const void* final_write_slots, int final_write_dtype, int64_t chunk_size,
+                                      const void* frames, int frames_dtype, int64_t frames_per_slot,
+                                      int64_t frame_bytes, int64_t head_bytes, int64_t num_frames,
+                                      const void* log_slots, int log_dtype, const void* token_offsets,
+                                      int offsets_dtype, int64_t key_heads, int64_t num_layers, int64_t page_size,
+                                      void* out, float scale, void* stream);
+
+/*
  * LogState token log of the chunked prefill: replaces the log stores of
  * kernel/linear_attention/state_io.py:83-126 (_store_chunk_log, called from
  * vendor/fla/chunk_delta_h.py:183-192 when a ChunkLogIO is given), with the
  * log layout of kernel/linear_attention/layout.py:29-80 (log_pointer).
  * For every token t with log_slots[t] >= 0 and 0 <= token_offsets[t] <
  * page_size, and every value head h:
- *   v_new[t, h, :] -> the value row (h, position) of the slot's log;
+ *   v_new[t, h, :] -> the value row (h, position) of the slot's log (skipped
+ *     when v_new is NULL: gdn_chunk_gated_delta_rule_logged wrote them);
  *   key[t, h / (HV / H), :] -> key row (h / (HV / key_heads), position) when
  *     h % (HV / key_heads) == 0;
  *   gate[t, h] (fp32) -> float (layer page_size + position) HV + h of the

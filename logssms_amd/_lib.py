@@ -43,6 +43,9 @@ SIGNATURES = {
     "gdn_chunk_gated_delta_rule": [P, P, P, I32, P, P, P, I32, I64, I64, I64, I64, I64, I64, P, I32, I64, I64,
                                    I64, I64, P, I32, P, I32, P, I32, I64, P, I32, I64, I64, I64, I64, P, P, F32,
                                    P],
+    "gdn_chunk_gated_delta_rule_logged": [P, P, P, I32, P, P, P, I32, I64, I64, I64, I64, I64, I64, P, I32, I64, P,
+                                          I32, P, I32, P, I32, I64, P, I32, I64, I64, I64, I64, P, I32, P, I32, I64,
+                                          I64, I64, P, F32, P],
     "gdn_store_chunk_log": [P, P, I32, I64, I64, I64, P, I32, P, I32, I64, P, P, I64, I64, I64, I64, I64, P, P,
                             I32, I64, I64, I64, I64, I64, P],
     "gdn_conv_windows_logstate": [P, I64, I64, I32, P, P, I32, I64, I64, I64, I32, P, P, I32, I64, I64, I64, I64,

@@ -775,21 +775,31 @@ int set_frame_layout(ChunkParams& p, int64_t dk, int state_dtype, const void* fr
   p.frame_bytes = frame_bytes;
   p.head_bytes = head_bytes;
   p.num_frames = num_frames;
+  p.fdiv = make_div32(frame_bytes);
   return GDN_OK;
 }
 
 }  // namespace gdn
 
-extern "C" int gdn_chunk_gated_delta_rule(const void* q, const void* k, const void* v, int io_dtype, const float* g,
-                                          const float* beta, const void* cu_seqlens, int cu_dtype, int64_t num_seqs,
-                                          int64_t total_tokens, int64_t H, int64_t HV, int64_t dk, int64_t dv,
-                                          void* state, int state_dtype, int64_t slot_stride, int64_t layer_stride,
-                                          int64_t head_stride, int64_t layer, const void* read_slots, int read_dtype,
-                                          const void* chunk_write_slots, int chunk_write_dtype,
-                                          const void* final_write_slots, int final_write_dtype, int64_t chunk_size,
-                                          const void* frames, int frames_dtype, int64_t frames_per_slot,
-                                          int64_t frame_bytes, int64_t head_bytes, int64_t num_frames, void* out,
-                                          void* v_new, float scale, void* stream) {
+namespace gdn {
+namespace {
+// The token log arguments of gdn_chunk_gated_delta_rule_logged.
+struct LogArgs {
+  const void* slots;
+  int slots_dtype;
+  const void* offsets;
+  int offsets_dtype;
+  int64_t key_heads, layers, page;
+};
+
+int chunk_entry(const void* q, const void* k, const void* v, int io_dtype, const float* g, const float* beta,
+                const void* cu_seqlens, int cu_dtype, int64_t num_seqs, int64_t total_tokens, int64_t H, int64_t HV,
+                int64_t dk, int64_t dv, void* state, int state_dtype, int64_t slot_stride, int64_t layer_stride,
+                int64_t head_stride, int64_t layer, const void* read_slots, int read_dtype,
+                const void* chunk_write_slots, int chunk_write_dtype, const void* final_write_slots,
+                int final_write_dtype, int64_t chunk_size, const void* frames, int frames_dtype,
+                int64_t frames_per_slot, int64_t frame_bytes, int64_t head_bytes, int64_t num_frames, void* out,
+                void* v_new, float scale, const LogArgs* log, void* stream) {
   GDN_REQUIRE(num_seqs >= 0 && total_tokens >= 0 && H > 0 && HV > 0 && HV % H == 0 && layer >= 0,
               "gdn_chunk_gated_delta_rule: bad sizes");
   GDN_REQUIRE(chunk_size == 16 || chunk_size == 32 || chunk_size == 64,
@@ -812,6 +822,31 @@ extern "C" int gdn_chunk_gated_delta_rule(const void* q, const void* k, const vo
     const int rc = set_frame_layout(p, dk, state_dtype, frames, frames_dtype, frames_per_slot, frame_bytes, head_bytes,
                                     num_frames);
     if (rc != GDN_OK) return rc;
+  }
+  // the log-slot loads of the kernel read T words in any case: without a log, the gates
+  p.logging = log != nullptr;
+  p.log_slots = log ? log->slots : static_cast<const void*>(g);
+  p.log_is64 = log ? log->slots_dtype == GDN_I64 : 0;
+  p.log_pos = log ? log->offsets : static_cast<const void*>(g);
+  p.log_pos_is64 = log ? log->offsets_dtype == GDN_I64 : 0;
+  p.log_table = log ? frames : static_cast<const void*>(g);
+  p.log_table_is64 = log ? frames_dtype == GDN_I64 : 0;
+  if (log) {
+    GDN_REQUIRE(frames && log->slots && log->offsets && log->key_heads > 0 && H % log->key_heads == 0 &&
+                    HV % log->key_heads == 0 && log->layers > layer && log->page > 0 && log->page % chunk_size == 0,
+                "gdn_chunk_gated_delta_rule_logged: bad token log layout");
+    GDN_REQUIRE(io_dtype == state_dtype, "gdn_chunk_gated_delta_rule_logged: log rows are stored in the io dtype");
+    GDN_REQUIRE(2 * log->page * log->layers * (log->key_heads * dk + HV * dv) <= frames_per_slot * frame_bytes &&
+                    frames_per_slot * frame_bytes < kMaxOffset32,
+                "gdn_chunk_gated_delta_rule_logged: the log exceeds a slot's frames or 4 GiB");
+    p.log_key_heads = log->key_heads;
+    p.log_layers = log->layers;
+    p.log_page = log->page;
+    // a 64-column slice of a value row (128-byte aligned) must not straddle two frames
+    if (dv % 64 != 0 || frame_bytes % 128 != 0) {
+      set_error("gdn_chunk_gated_delta_rule_logged: needs dv %% 64 == 0 and frames of a multiple of 128 bytes");
+      return GDN_ERR_UNSUPPORTED;
+    }
   }
   auto s = static_cast<hipStream_t>(stream);
   const int64_t groups = num_seqs * H;
@@ -837,4 +872,40 @@ extern "C" int gdn_chunk_gated_delta_rule(const void* q, const void* k, const vo
   set_error("gdn_chunk_gated_delta_rule: unsupported head dims dk=%lld dv=%lld (dk in {32,64,128}, dv 32 or "
             "a multiple of 64)", (long long)dk, (long long)dv);
   return GDN_ERR_UNSUPPORTED;
+}
+}  // namespace
+}  // namespace gdn
+
+extern "C" int gdn_chunk_gated_delta_rule(const void* q, const void* k, const void* v, int io_dtype, const float* g,
+                                          const float* beta, const void* cu_seqlens, int cu_dtype, int64_t num_seqs,
+                                          int64_t total_tokens, int64_t H, int64_t HV, int64_t dk, int64_t dv,
+                                          void* state, int state_dtype, int64_t slot_stride, int64_t layer_stride,
+                                          int64_t head_stride, int64_t layer, const void* read_slots, int read_dtype,
+                                          const void* chunk_write_slots, int chunk_write_dtype,
+                                          const void* final_write_slots, int final_write_dtype, int64_t chunk_size,
+                                          const void* frames, int frames_dtype, int64_t frames_per_slot,
+                                          int64_t frame_bytes, int64_t head_bytes, int64_t num_frames, void* out,
+                                          void* v_new, float scale, void* stream) {
+  return gdn::chunk_entry(q, k, v, io_dtype, g, beta, cu_seqlens, cu_dtype, num_seqs, total_tokens, H, HV, dk, dv,
+                          state, state_dtype, slot_stride, layer_stride, head_stride, layer, read_slots, read_dtype,
+                          chunk_write_slots, chunk_write_dtype, final_write_slots, final_write_dtype, chunk_size, frames,
+                          frames_dtype, frames_per_slot, frame_bytes, head_bytes, num_frames, out, v_new, scale,
+                          nullptr, stream);
+}
+
+extern "C" int gdn_chunk_gated_delta_rule_logged(
+    const void* q, const void* k, const void* v, int io_dtype, const float* g, const float* beta,
+    const void* cu_seqlens, int cu_dtype, int64_t num_seqs, int64_t total_tokens, int64_t H, int64_t HV, int64_t dk,
+    int64_t dv, void* state, int state_dtype, int64_t layer, const void* read_slots, int read_dtype,
+    const void* chunk_write_slots, int chunk_write_dtype, const void* final_write_slots, int final_write_dtype,
+    int64_t chunk_size, const void* frames, int frames_dtype, int64_t frames_per_slot, int64_t frame_bytes,
+    int64_t head_bytes, int64_t num_frames, const void* log_slots, int log_dtype, const void* token_offsets,
+    int offsets_dtype, int64_t key_heads, int64_t num_layers, int64_t page_size, void* out, float scale,
+    void* stream) {
+  GDN_REQUIRE(frames, "gdn_chunk_gated_delta_rule_logged: the token log lives in frame storage");
+  const gdn::LogArgs log{log_slots, log_dtype, token_offsets, offsets_dtype, key_heads, num_layers, page_size};
+  return gdn::chunk_entry(q, k, v, io_dtype, g, beta, cu_seqlens, cu_dtype, num_seqs, total_tokens, H, HV, dk, dv,
+                          state, state_dtype, 0, 0, 0, layer, read_slots, read_dtype, chunk_write_slots,
+                          chunk_write_dtype, final_write_slots, final_write_dtype, chunk_size, frames, frames_dtype,
+                          frames_per_slot, frame_bytes, head_bytes, num_frames, out, nullptr, scale, &log, stream);
 }

@@ -232,6 +232,8 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
   __shared__ __align__(16) _Float16 sA[2 * kC * LDA];  // [A11 | 0 ; -L21 | A22]
   __shared__ __align__(16) _Float16 sM[2 * kC * LDA];  // tril_incl(q k^T 2^(G_i - G_j))
   __shared__ __align__(16) float sG[3 * GTS];
+  // EXT: byte offset in the frame storage of each token's logged v' slice (-1: none), 3 chunks
+  __shared__ int64_t sLog[EXT ? 3 * kC : 1];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int lr = lane & 15, lg = lane >> 4;
@@ -425,22 +427,38 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         V[2] = mma(a2, rb1, zero4());
         V[3] = mma(a3, rb1, zero4());
         vb1 = bfrag(V[2], V[3]);
-        if (vng) {
+        if (vng || (EXT && p.logging)) {
           // v'^T = R^T A^T: the same fragments with the operands swapped (a
           // B fragment of R is an A fragment of R^T), so lane (g, c) holds
-          // columns 4g..4g+3 of token 16 i + c and writes them as 8 bytes.
+          // columns 4g..4g+3 of token 16 i + c and writes them as 8 bytes,
+          // to v_new or to the token's log row.
           const f4_t vt[4] = {mma(rb0, a0, zero4()), mma(rb0, a1, zero4()), mma(rb1, a2, zero4()),
                               mma(rb1, a3, zero4())};
-          char* vb = reinterpret_cast<char*>(vng + c * kC * tok_stride);
-          uint32_t ov = static_cast<uint32_t>((lr * tok_stride + 4 * lg) * 2);
-          asm volatile("" : "+v"(ov));
+          if (EXT && p.logging) {
+            const int64_t* lrow = sLog + (c % 3) * kC;
+            char* const st = static_cast<char*>(p.state);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            if (16 * i + lr < nv) {
-              uint2 w;
-              w.x = out_pack2<IOT>(vt[i][0], vt[i][1]);
-              w.y = out_pack2<IOT>(vt[i][2], vt[i][3]);
-              *reinterpret_cast<uint2*>(vb + 16 * i * tok_stride * 2 + ov) = w;
+            for (int i = 0; i < 4; ++i) {
+              const int64_t off = lrow[16 * i + lr];
+              if (off >= 0) {
+                uint2 w;
+                w.x = out_pack2<IOT>(vt[i][0], vt[i][1]);
+                w.y = out_pack2<IOT>(vt[i][2], vt[i][3]);
+                *reinterpret_cast<uint2*>(st + off + (16 * j + 4 * lg) * 2) = w;
+              }
+            }
+          } else {
+            char* vb = reinterpret_cast<char*>(vng + c * kC * tok_stride);
+            uint32_t ov = static_cast<uint32_t>((lr * tok_stride + 4 * lg) * 2);
+            asm volatile("" : "+v"(ov));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              if (16 * i + lr < nv) {
+                uint2 w;
+                w.x = out_pack2<IOT>(vt[i][0], vt[i][1]);
+                w.y = out_pack2<IOT>(vt[i][2], vt[i][3]);
+                *reinterpret_cast<uint2*>(vb + 16 * i * tok_stride * 2 + ov) = w;
+              }
             }
           }
         }
@@ -712,6 +730,43 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       const bool ok = lane < valid_rows(ck);
       gate_table(ck, ok ? pgate : 0.f, ok ? pbeta : 0.f);
     };
+    // EXT, token log: the log slice of the lane's token of chunk ck, in three
+    // steps one chunk apart so that no wait of the conv waves covers them:
+    // prefetch_log loads the token's log slot and position (stage A),
+    // resolve_log turns stage A into its frame-table entry (stage B), and
+    // stage_log (wave 10) writes stage B's byte offset to LDS.  Both waves 10
+    // and 11 issue the loads, with clamped indices, every chunk.
+    int aslot = 0, apos = 0, bentry = 0;
+    bool aok = false, bvalid = false;
+    uint32_t bbyte = 0;
+    auto prefetch_log = [&](int64_t ck) __attribute__((always_inline)) {
+      const bool ok = lane < valid_rows(ck);
+      const int64_t t = len > 0 ? bos + (ok ? ck * kC + lane : 0) : 0;
+      aslot = static_cast<int>(load_index(p.log_slots, t, p.log_is64));
+      apos = static_cast<int>(load_index(p.log_pos, t, p.log_pos_is64));
+      aok = p.logging && ok;
+    };
+    auto resolve_log = [&]() __attribute__((always_inline)) {
+      const bool valid = aok && aslot >= 0 && apos >= 0 && apos < p.log_page;
+      const uint32_t ps = valid ? static_cast<uint32_t>(apos) : 0u;
+      const uint32_t g = static_cast<uint32_t>(p.gran), sh = static_cast<uint32_t>(__builtin_ctz(g));
+      const uint32_t key_size = g * static_cast<uint32_t>(p.log_key_heads) * DK;
+      const uint32_t layer_size = key_size + g * static_cast<uint32_t>(p.HV) * static_cast<uint32_t>(p.DV);
+      const uint32_t elem = ((ps >> sh) * static_cast<uint32_t>(p.log_layers) + static_cast<uint32_t>(p.layer)) *
+                                layer_size +
+                            key_size + (static_cast<uint32_t>(h) * g + (ps & (g - 1))) * static_cast<uint32_t>(p.DV) +
+                            static_cast<uint32_t>(col_base);
+      bbyte = 2u * elem;
+      const int64_t idx = valid ? static_cast<int64_t>(aslot) * p.fps + p.fdiv.div(bbyte) : 0;
+      bentry = static_cast<int>(load_index(p.log_table, idx, p.log_table_is64));
+      bvalid = valid;
+    };
+    auto stage_log = [&](int64_t ck) __attribute__((always_inline)) {
+      if (wave == kGateWave)
+        sLog[(ck % 3) * kC + lane] = bvalid && bentry >= 0 && bentry < p.num_frames
+                                         ? static_cast<int64_t>(bentry) * p.frame_bytes + p.fdiv.mod(bbyte)
+                                         : -1;
+    };
 
     // ---- fused path: V rows are the conv + SiLU of the projections
     // (packed_conv.py:49-133), computed by waves 10-11 before the M barrier and
@@ -907,6 +962,16 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         prefetch_v(1);
       }
       prefetch_g(2);
+      if constexpr (EXT) {  // log rows of chunks 0 and 1 staged, 2 resolved, 3 loaded
+        for (int64_t ck = 0; ck < 2; ++ck) {
+          prefetch_log(ck);
+          resolve_log();
+          stage_log(ck);
+        }
+        prefetch_log(2);
+        resolve_log();
+        prefetch_log(3);
+      }
       lds_barrier();  // P0
       lds_barrier();  // B(0)
       for (int64_t c = 0; c < nchunks; ++c) {
@@ -932,6 +997,11 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         }
         if (wave == kGateWave) stage_g(c + 2);
         prefetch_g(c + 3);
+        if constexpr (EXT) {
+          stage_log(c + 2);   // resolved one chunk ago
+          resolve_log();      // chunk c + 3, loaded one chunk ago
+          prefetch_log(c + 4);
+        }
         lds_barrier();  // B(c+1)
       }
     } else {

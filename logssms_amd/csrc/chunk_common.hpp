@@ -54,6 +54,21 @@ struct ChunkParams {
   int frames_is64;
   int frame_rows;
   int64_t fps, frame_bytes, head_bytes, num_frames;
+  // Token log of v' (frame storage, EXT instantiation): with `logging` set,
+  // the v' row of token t and value head h goes to the value row (h,
+  // position) of the log of slot log_slots[t] at position log_pos[t], when
+  // that slot is >= 0 and 0 <= position < log_page (the log layout of
+  // gdn_store_chunk_log), instead of v_new.  Without it both pointers still
+  // name T readable words (the kernel loads them unconditionally).
+  int logging;
+  const void* log_slots;
+  int log_is64;
+  const void* log_pos;
+  int log_pos_is64;
+  const void* log_table;  // the frame table when logging, else the same T words (plain pools have none)
+  int log_table_is64;
+  int64_t log_key_heads, log_layers, log_page;
+  Div32 fdiv;  // frame_bytes
 };
 
 // Host-side validation of a frame-table state layout; returns GDN_OK or sets

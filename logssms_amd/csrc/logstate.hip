@@ -78,10 +78,12 @@ __global__ __launch_bounds__(kThreads) void chunk_log_kernel(LogParams p) {
   const int64_t slot = load_index(p.slots, t, p.slots_is64);
   const int64_t pos = load_index(p.offsets, t, p.offsets_is64);
   if (slot < 0 || pos < 0 || pos >= p.page) return;
-  const uint16_t* vrow = p.v_new + (t * p.HV + h) * p.V;
-  for (int64_t col = threadIdx.x; col < p.V; col += kThreads) {
-    uint16_t* d = log_element(p, slot, pos, h, col, true);
-    if (d) *d = vrow[col];
+  if (p.v_new) {  // null: the value rows were written by the chunk kernel
+    const uint16_t* vrow = p.v_new + (t * p.HV + h) * p.V;
+    for (int64_t col = threadIdx.x; col < p.V; col += kThreads) {
+      uint16_t* d = log_element(p, slot, pos, h, col, true);
+      if (d) *d = vrow[col];
+    }
   }
   const int64_t group = p.HV / p.KH;  // value heads per logged key head
   if (h % group == 0) {
@@ -113,7 +115,8 @@ __global__ __launch_bounds__(kLogThreads) void chunk_log_vec_kernel(LogParams p)
   if (slot < 0 || pos < 0 || pos >= p.page) return;
   const int64_t vv = p.V / 8, kv = p.K / 8;
   const int64_t group = p.HV / p.KH;  // value heads per logged key head
-  const int64_t nval = p.HV * vv, total = nval + p.KH * kv;
+  const int64_t nval = p.v_new ? p.HV * vv : 0;  // no value rows: written by the chunk kernel
+  const int64_t total = nval + p.KH * kv;
   for (int64_t i = threadIdx.x; i < total; i += kLogThreads) {
     const bool value = i < nval;
     const int64_t j = value ? i : i - nval;
@@ -1165,7 +1168,7 @@ extern "C" int gdn_store_chunk_log(void* storage, const void* frames, int frames
               "gdn_store_chunk_log: decay records of %lld bytes do not hold %lld layers x %lld positions x %lld heads",
               (long long)decay_record_bytes, (long long)num_layers, (long long)page_size, (long long)HV);
   if (T == 0) return GDN_OK;
-  GDN_REQUIRE(storage && frames && log_slots && token_offsets && v_new && key && gate && decay_frames,
+  GDN_REQUIRE(storage && frames && log_slots && token_offsets && key && gate && decay_frames,
               "gdn_store_chunk_log: null input");
   GDN_REQUIRE(T <= 0x7fffffff && HV <= 65535, "gdn_store_chunk_log: grid too large");
   LogParams p{};

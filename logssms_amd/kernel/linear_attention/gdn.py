@@ -56,7 +56,10 @@ def chunk_gated_delta_rule_to_cache(
     compatibility (the kernel derives interval boundaries from
     ``cu_seqlens``).  With ``log_io`` (frame storage only) every logged
     token's v' rows, key rows and gates then go into its log slot
-    (``state_io.py:83-126``, ``gdn_store_chunk_log``).
+    (``state_io.py:83-126``, ``gdn_store_chunk_log``).  With
+    ``return_v_new=False`` as well, the chunk kernel writes the v' rows into
+    the log itself (``gdn_chunk_gated_delta_rule_logged``; v' never makes an
+    HBM round trip) and ``v_new`` is None.
     """
     del chunk_offsets
     assert query.shape[0] == key.shape[0] == value.shape[0] == 1
@@ -92,7 +95,6 @@ def chunk_gated_delta_rule_to_cache(
         assert log_io.gate.numel() == T * HV and log_io.num_key_heads > 0
         assert H % log_io.num_key_heads == 0 and HV % log_io.num_key_heads == 0
         assert storage.dtype == value.dtype, "log rows are stored in the io dtype"
-        return_v_new = True
     assert storage.device == query.device
     if chunk_indices is not None:
         assert state_io.chunk_write_slots.shape == (len(chunk_indices),)
@@ -103,8 +105,27 @@ def chunk_gated_delta_rule_to_cache(
     beta = beta.float().contiguous()
     o = torch.empty_like(value) if out is None else out
     assert o.shape == value.shape and o.dtype == value.dtype and o.is_contiguous()
-    v_new = torch.empty_like(value) if return_v_new else None
-    if T:
+    # v' straight into the log when the caller does not want v_new back
+    direct_log = (log_io is not None and not return_v_new and dv % 64 == 0 and state_io.frame_bytes % 128 == 0)
+    v_new = torch.empty_like(value) if (return_v_new or (log_io is not None and not direct_log)) else None
+    if T and direct_log:
+        fw = state_io.final_write_slots
+        _lib.call(
+            "gdn_chunk_gated_delta_rule_logged",
+            query.data_ptr(), key.data_ptr(), value.data_ptr(), _lib.dtype_code(value.dtype),
+            gate.data_ptr(), beta.data_ptr(), cu_seqlens.data_ptr(), _lib.index_code(cu_seqlens),
+            len(cu_seqlens) - 1, T, H, HV, dk, dv,
+            storage.data_ptr(), _lib.dtype_code(storage.dtype), state_io.layer,
+            state_io.read_slots.data_ptr(), _lib.index_code(state_io.read_slots),
+            state_io.chunk_write_slots.data_ptr(), _lib.index_code(state_io.chunk_write_slots),
+            _lib.ptr(fw), _lib.index_code(fw) if fw is not None else 0, chunk_size,
+            _lib.ptr(frame_args[0]), *frame_args[1:],
+            log_io.slots.data_ptr(), _lib.index_code(log_io.slots),
+            log_io.token_offsets.data_ptr(), _lib.index_code(log_io.token_offsets),
+            log_io.num_key_heads, state_io.num_layers, log_io.page_size,
+            o.data_ptr(), float(dk) ** -0.5, _lib.stream_of(query),
+        )
+    elif T:
         fw = state_io.final_write_slots
         _lib.call(
             "gdn_chunk_gated_delta_rule",
@@ -118,20 +139,20 @@ def chunk_gated_delta_rule_to_cache(
             _lib.ptr(frame_args[0]), *frame_args[1:],
             o.data_ptr(), _lib.ptr(v_new), float(dk) ** -0.5, _lib.stream_of(query),
         )
-        if log_io is not None:
-            log_gate = log_io.gate.float().contiguous()
-            _lib.call(
-                "gdn_store_chunk_log",
-                storage.data_ptr(), frames.data_ptr(), _lib.index_code(frames), frames.shape[1],
-                state_io.frame_bytes, storage.shape[0],
-                log_io.slots.data_ptr(), _lib.index_code(log_io.slots),
-                log_io.token_offsets.data_ptr(), _lib.index_code(log_io.token_offsets), T,
-                v_new.data_ptr(), key.data_ptr(), H, HV, dk, dv, log_io.num_key_heads,
-                log_gate.data_ptr(), log_io.decay_frames.data_ptr(), _lib.index_code(log_io.decay_frames),
-                log_io.decay_record_bytes, state_io.layer, state_io.num_layers, state_io.granularity,
-                log_io.page_size, _lib.stream_of(query),
-            )
-    return o, v_new
+    if T and log_io is not None:
+        log_gate = log_io.gate.float().contiguous()
+        _lib.call(
+            "gdn_store_chunk_log",
+            storage.data_ptr(), frames.data_ptr(), _lib.index_code(frames), frames.shape[1],
+            state_io.frame_bytes, storage.shape[0],
+            log_io.slots.data_ptr(), _lib.index_code(log_io.slots),
+            log_io.token_offsets.data_ptr(), _lib.index_code(log_io.token_offsets), T,
+            _lib.ptr(None if direct_log else v_new), key.data_ptr(), H, HV, dk, dv, log_io.num_key_heads,
+            log_gate.data_ptr(), log_io.decay_frames.data_ptr(), _lib.index_code(log_io.decay_frames),
+            log_io.decay_record_bytes, state_io.layer, state_io.num_layers, state_io.granularity,
+            log_io.page_size, _lib.stream_of(query),
+        )
+    return o, v_new if return_v_new else None
 
 
 def _gates(gate: torch.Tensor, beta: torch.Tensor, A_log: torch.Tensor, dt_bias: torch.Tensor):

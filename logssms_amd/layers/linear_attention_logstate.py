@@ -295,6 +295,7 @@ class GatedDeltaLogStateBackend:
                               decay_frames=pool.decay_frame_table, gate=prepared_gate, page_size=pool.page_size,
                               decay_record_bytes=layout.log_decay_bytes, num_key_heads=layout.num_key_heads),
             out=None if out is None else out.unsqueeze(0),
+            return_v_new=False,  # v' goes to the log only
         )
         return output.squeeze(0)
 

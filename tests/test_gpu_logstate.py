@@ -153,10 +153,12 @@ def test_frame_table_states(case, chunk_size):
     assert torch.equal(host.reshape(-1)[mask], storage.reshape(-1)[mask])
 
 
-def test_chunk_token_log():
+@pytest.mark.parametrize("direct", [False, True])
+def test_chunk_token_log(direct):
     """ChunkLogIO: each logged token's v' rows, key rows and gate land in its
     log slot (state_io.py:83-126); keys and gates bit-exact, v' rows to the
-    output tolerance, every other byte untouched."""
+    output tolerance, every other byte untouched.  direct: no v_new asked
+    for, so the chunk kernel writes the v' rows into the log itself."""
     from logssms_amd.kernel.linear_attention import ChunkLogIO, ChunkStateIO, chunk_gated_delta_rule_to_cache
     g = gen(71)
     H, HV, dk, dv, layers, layer, gran, page = 2, 4, 128, 128, 2, 1, 32, 64
@@ -208,7 +210,7 @@ def test_chunk_token_log():
     print(f"token log: {T} tokens, {slots - state_slots} log slots", flush=True)
     o, _ = chunk_gated_delta_rule_to_cache(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), gg[None].to(DEV),
                                            beta[None].to(DEV), io, torch.tensor(cu, device=DEV), chunk_size=gran,
-                                           log_io=log)
+                                           log_io=log, return_v_new=not direct)
     torch.cuda.synchronize()
     host = dstore.cpu()
     assert_bf16_close(o[0], o_ref[0])
