@@ -437,6 +437,57 @@ __device__ __forceinline__ void wait_all() {
   __builtin_amdgcn_s_waitcnt(0x0070);  // gfx9 encoding: vmcnt 0, expcnt 7 (no wait), lgkmcnt 0
   asm volatile("" ::: "memory");
 }
+// s_waitcnt vmcnt(N) as the builtin (expcnt and lgkmcnt not waited for).
+template <int N> __device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0070 | 0x0f00);
+  asm volatile("" ::: "memory");
+}
+// LDS reads issued as one statement with their own lgkmcnt wait.  A wave
+// that also has direct-to-LDS loads in flight uses these: the compiler orders
+// every LDS read it knows of behind all such loads (s_waitcnt vmcnt(0)),
+// whatever buffer they fill; the caller's own counted wait and barrier make
+// the data it reads resident instead.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)(p)));
+}
+// Four transpose reads (two 16-column operand tiles of 8 tokens).
+__device__ __forceinline__ void tr_read16x4(const uint16_t* a0, const uint16_t* a1, const uint16_t* a2,
+                                            const uint16_t* a3, uint4& x, uint4& y) {
+  uint2 r0, r1, r2, r3;
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %4\n\t"
+      "ds_read_b64_tr_b16 %1, %5\n\t"
+      "ds_read_b64_tr_b16 %2, %6\n\t"
+      "ds_read_b64_tr_b16 %3, %7\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
+      : "v"(lds_addr(a0)), "v"(lds_addr(a1)), "v"(lds_addr(a2)), "v"(lds_addr(a3))
+      : "memory");
+  x = make_uint4(r0.x, r0.y, r1.x, r1.y);
+  y = make_uint4(r2.x, r2.y, r3.x, r3.y);
+}
+__device__ __forceinline__ uint4 tr_read16x2(const uint16_t* a0, const uint16_t* a1) {
+  uint2 r0, r1;
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %2\n\t"
+      "ds_read_b64_tr_b16 %1, %3\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r0), "=&v"(r1)
+      : "v"(lds_addr(a0)), "v"(lds_addr(a1))
+      : "memory");
+  return make_uint4(r0.x, r0.y, r1.x, r1.y);
+}
+// Two 16-byte reads.
+__device__ __forceinline__ void lds_read128x2(const float* a0, const float* a1, float4& x, float4& y) {
+  asm volatile(
+      "ds_read_b128 %0, %2\n\t"
+      "ds_read_b128 %1, %3\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(x), "=&v"(y)
+      : "v"(lds_addr(a0)), "v"(lds_addr(a1))
+      : "memory");
+}
 // Chunk position of logical chunk c in row r of a swizzled row-major array
 // with `chunks` 16-byte chunks per row (a power of two).
 __device__ __forceinline__ int swz_state(int r, int c, int chunks) { return c ^ (r & (chunks - 1)); }
@@ -899,20 +950,6 @@ __device__ __forceinline__ T* slot_row(const RestoreParams& p, int64_t s, int64_
   return reinterpret_cast<T*>(p.storage + fr * p.frame_bytes + p.fdiv.mod(x));
 }
 
-template <class T>
-__device__ __forceinline__ const T* restore_log(const RestoreParams& p, int64_t slot, int64_t layer, int64_t pos,
-                                                int64_t index, int64_t col, bool value, int DK, int DV) {
-  const int64_t key_size = p.gran * p.KH * DK;
-  const int64_t layer_size = key_size + p.gran * p.HV * DV;
-  const uint32_t ps = static_cast<uint32_t>(pos);
-  const int64_t elem = (p.gdiv.div(ps) * p.layers + layer) * layer_size + (value ? key_size : 0) +
-                       (index * p.gran + p.gdiv.mod(ps)) * (value ? DV : DK) + col;
-  const uint32_t byte = static_cast<uint32_t>(2 * elem);
-  const int64_t fr = load_index(p.frames, slot * p.fps + p.fdiv.div(byte), p.frames_is64);
-  if (fr < 0 || fr >= p.num_frames) return nullptr;
-  return reinterpret_cast<const T*>(p.storage + fr * p.frame_bytes + p.fdiv.mod(byte));
-}
-
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -935,27 +972,41 @@ template <> struct RestoreMma<f16> {
   }
 };
 
-constexpr int kRestoreGroup = 64;               // tokens staged per step (two 32-deep products)
-constexpr int kRestoreLd = kRestoreGroup + 8;   // LDS row of one feature over a group, padded
-constexpr int kRestoreSpan = kDecodeThreads;    // tokens whose suffix decays one block scan yields
+constexpr int kRestoreStep = 32;              // tokens staged per step (one 32-deep product per tile)
+constexpr int kRestoreSpan = kDecodeThreads;  // tokens whose suffix decays one block scan yields
+
+// 16 zero bytes: the source of the direct-to-LDS loads for rows past a
+// segment's end or in an unmapped frame.
+__device__ uint4 g_zero_piece;
 
 // grid (tasks x layers x HV), 4 waves: the state of the task's base slot (or
 // zero), then each segment of logged tokens t = b .. e-1 in one step,
 // S <- e^{sum_t g_t} S + sum_t k_t (e^{sum_{j>t} g_j} v'_t)^T with the scaled
 // v' rounded to the state dtype (logstate_construction.cuh:329-393); written
-// to the output slot.  The sum runs on MFMA, 64 tokens per step: the step's
-// keys and scaled v' rows are staged feature-major in LDS (token index
-// contiguous: the k dimension of both operands), and each wave owns the
-// state's columns of DV / 64 (at least one) 16-wide tiles over all DK rows in
-// fp32 accumulators.  The suffix decays of 256 tokens come from one block
-// scan of their gates.
+// to the output slot.  The sum runs on MFMA, 32 tokens per step: the step's
+// key and value rows land token-major in one of two LDS buffers by
+// direct-to-LDS loads (16-byte chunks XOR-swizzled by row), issued one step
+// ahead of the products, with their frame-table entries loaded two steps
+// ahead; both MFMA operands come out of the token-major rows by transpose
+// reads (`ds_read_b64_tr_b16`), the values scaled by their suffix decay on
+// the way.  Each wave owns the state's columns of DV / 64 (at least one)
+// 16-wide tiles over all DK rows in fp32 accumulators.  The suffix decays of
+// 256 tokens come from one block scan of their gates.  Every wait of the
+// step loop covers loads only (the state is stored after the loop).
 template <int DK, int DV, class T>
-__global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(2))) void restore_kernel(RestoreParams p) {
+__global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(3))) void restore_kernel(RestoreParams p) {
   constexpr int RT = DK / 16, CTT = DV / 16, CT = CTT >= 4 ? CTT / 4 : 1;
-  constexpr int KV = DK / 8, VV = DV / 8;  // 16-byte pieces per row
-  constexpr int PIECES = kRestoreGroup * (KV + VV) / kDecodeThreads;
-  static_assert(DK % 16 == 0 && DV % 16 == 0, "tile split");
-  static_assert(kRestoreGroup * (KV + VV) % kDecodeThreads == 0, "piece split");
+  constexpr int CHK = DK / 8, CHV = DV / 8;             // 16-byte chunks per key / value row
+  constexpr int KI = kRestoreStep * 2 * DK / 1024;      // 1 KiB wave loads of a step's key rows
+  constexpr int NI = KI + kRestoreStep * 2 * DV / 1024;  // ... and of all its rows
+  constexpr int NIW = (NI + 3) / 4;                     // per wave
+  // Loads a wave issues per step (lookups and stage): the same in every wave
+  // when NI is a multiple of 4, so a count-based wait is exact; else wait for all.
+  auto wait_steps = [&]() __attribute__((always_inline)) {
+    if constexpr (NI % 4 == 0) wait_vm<2 * NIW>(); else wait_all();
+  };
+  static_assert(DK % 16 == 0 && DV % 16 == 0 && DK <= 512 && DV <= 512, "tile split");
+  static_assert((kRestoreStep * 2 * DK) % 1024 == 0 && (kRestoreStep * 2 * DV) % 1024 == 0, "whole wave loads");
   const uint32_t bid = blockIdx.x, nhv = static_cast<uint32_t>(p.HV), nl = static_cast<uint32_t>(p.layers);
   const int64_t task = bid / (nl * nhv);
   const int64_t layer = (bid / nhv) % nl;
@@ -963,9 +1014,9 @@ __global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(
   const int64_t kh = h / (p.HV / p.KH);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lq = lane >> 4;
   const bool owner = wave * CT < CTT;  // this wave holds column tiles
-  __shared__ uint16_t s_kt[DK * kRestoreLd];
-  __shared__ uint16_t s_vt[DV * kRestoreLd];
-  __shared__ float s_suffix[kRestoreSpan];
+  __shared__ __attribute__((aligned(16))) uint16_t s_k[3][kRestoreStep * DK];
+  __shared__ __attribute__((aligned(16))) uint16_t s_v[3][kRestoreStep * DV];
+  __shared__ __attribute__((aligned(16))) float s_suffix[kRestoreSpan];
   __shared__ float s_part[kDecodeThreads / 64];
   // acc[i][c] is the transposed tile T = S^T: lane l holds dk column
   // i 16 + l % 16 and dv rows (wave CT + c) 16 + 4 (l / 16) .. + 3, i.e. four
@@ -995,36 +1046,107 @@ __global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(
       acc[i][c] = f32x4{a, b2, c2, d};
     }
   }
+  // The piece of wave load k of this lane: token row t of the step, logical
+  // 16-byte chunk c (the XOR swizzle of its LDS position), key or value row.
+  struct Piece { int t, c; bool key; };
+  auto piece_of = [&](int k) __attribute__((always_inline)) -> Piece {
+    const int rg = wave + 4 * k;
+    const bool key = rg < KI;
+    const int r = key ? rg : rg - KI, ch = key ? CHK : CHV;
+    const int t = r * (64 / ch) + lane / ch;  // 64 / ch rows of ch chunks per 1 KiB wave load
+    return Piece{t, swz_rows(t, lane % ch, ch), key};
+  };
+  const void* const zero_piece = &g_zero_piece;
+  const uint32_t key_size = static_cast<uint32_t>(p.gran * p.KH * DK);
+  const uint32_t layer_size = key_size + static_cast<uint32_t>(p.gran * p.HV * DV);
+  // Byte offset of piece k of the step at g0 inside the log slot (a token
+  // past n reads the first token's place).
+  auto piece_byte = [&](int64_t g0, int n, int k) __attribute__((always_inline)) -> uint32_t {
+    const Piece pc = piece_of(k);
+    const uint32_t ps = static_cast<uint32_t>(g0 + (pc.t < n ? pc.t : 0));
+    const uint32_t elem = (p.gdiv.div(ps) * static_cast<uint32_t>(p.layers) + static_cast<uint32_t>(layer)) * layer_size +
+                          (pc.key ? 0u : key_size) +
+                          (static_cast<uint32_t>(pc.key ? kh : h) * static_cast<uint32_t>(p.gran) + p.gdiv.mod(ps)) *
+                              static_cast<uint32_t>(pc.key ? DK : DV) +
+                          8u * static_cast<uint32_t>(pc.c);
+    return 2u * elem;
+  };
+  // Frame-table entries of the step's pieces.
+  auto lookup = [&](int64_t ls, int64_t g0, int n, int32_t (&entry)[NIW]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < NIW; ++k) {
+      if (wave + 4 * k >= NI) break;
+      entry[k] = static_cast<int32_t>(load_index(p.frames, ls * p.fps + p.fdiv.div(piece_byte(g0, n, k)), p.frames_is64));
+    }
+  };
+  // Direct-to-LDS loads of the step's rows into buffer b (zeros past n and
+  // for unmapped frames).
+  auto stage = [&](int b, int64_t g0, int n, const int32_t (&entry)[NIW]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < NIW; ++k) {
+      const int rg = wave + 4 * k;
+      if (rg >= NI) break;
+      // branch-free select, so the entry's wait stays a counted one
+      const bool live = (piece_of(k).t < n) & (entry[k] >= 0) & (entry[k] < p.num_frames);
+      const char* a = p.storage + static_cast<int64_t>(entry[k]) * p.frame_bytes + p.fdiv.mod(piece_byte(g0, n, k));
+      const void* src = live ? static_cast<const void*>(a) : zero_piece;
+      uint16_t* dst = rg < KI ? &s_k[b][rg * 512] : &s_v[b][(rg - KI) * 512];
+      dma16(src, dst);
+    }
+  };
+  const int64_t out = p.output[task];
+  const T* out_head = p.head_bytes <= p.frame_bytes ? slot_row<T>(p, out, layer, h, 0, DV) : nullptr;
   for (int64_t seg = p.offsets[task]; seg < p.offsets[task + 1]; ++seg) {
     const int64_t ls = p.seg_slots[seg];
-    int64_t fr = -1, ri = -1;
-    if (ls >= 0) {
-      fr = load_index(p.decay, 2 * ls, p.decay_is64);
-      ri = load_index(p.decay, 2 * ls + 1, p.decay_is64);
-    }
-    const bool ok = fr >= 0 && fr < p.num_frames && ri >= 0 && (ri + 1) * p.record_bytes <= p.frame_bytes;
     const int64_t begin = p.seg_begin[seg] < 0 ? 0 : p.seg_begin[seg];
     const int64_t end = p.seg_end[seg] < p.page ? p.seg_end[seg] : p.page;
+    int64_t fr = -1, ri = -1;
+    // frame entries of the first span's first two steps, in flight with the decay lookup
+    int32_t ea[NIW], eb[NIW];
+    const int first_n = static_cast<int>(end - begin < kRestoreStep ? end - begin : kRestoreStep);
+    if (ls >= 0 && begin < end) {
+      fr = load_index(p.decay, 2 * ls, p.decay_is64);
+      ri = load_index(p.decay, 2 * ls + 1, p.decay_is64);
+      lookup(ls, begin, first_n, ea);
+      lookup(ls, end - begin > kRestoreStep ? begin + kRestoreStep : begin,
+             end - begin > kRestoreStep ? static_cast<int>(end - begin - kRestoreStep < kRestoreStep
+                                                               ? end - begin - kRestoreStep : kRestoreStep) : 0, eb);
+    }
+    const bool ok = fr >= 0 && fr < p.num_frames && ri >= 0 && (ri + 1) * p.record_bytes <= p.frame_bytes;
     if (!ok || begin >= end) continue;
     const float* rec =
         reinterpret_cast<const float*>(p.storage + fr * p.frame_bytes + ri * p.record_bytes) + layer * p.page * p.HV + h;
-    // gate sum over the segment
-    float part = 0.f;
-    for (int64_t t = begin + tid; t < end; t += kDecodeThreads) part += rec[t * p.HV];
-    part = wave_sum(part);
-    lds_barrier();  // the previous segment's last step is consumed
-    if (lane == 0) s_part[wave] = part;
-    lds_barrier();
+    // gate sum over the segment: a pass of its own when the segment spans
+    // more than one scan, else the scan's total
+    const bool one_span = end - begin <= kRestoreSpan;
     float total = 0.f;
+    if (!one_span) {
+      float part = 0.f;
+      for (int64_t t = begin + tid; t < end; t += kDecodeThreads) part += rec[t * p.HV];
+      part = wave_sum(part);
+      lds_barrier();  // the previous segment's last step is consumed
+      if (lane == 0) s_part[wave] = part;
+      lds_barrier();
 #pragma unroll
-    for (int w = 0; w < kDecodeThreads / 64; ++w) total += s_part[w];
-    const float decay = expf(total);
-#pragma unroll
-    for (int i = 0; i < RT; ++i)
-#pragma unroll
-      for (int c = 0; c < CT; ++c) acc[i][c] *= decay;
+      for (int w = 0; w < kDecodeThreads / 64; ++w) total += s_part[w];
+    }
     float rest = 0.f;  // the gates of the segment's tokens before the span
     for (int64_t sb = begin; sb < end; sb += kRestoreSpan) {
+      const int64_t span_end = sb + kRestoreSpan < end ? sb + kRestoreSpan : end;
+      const int steps = static_cast<int>((span_end - sb + kRestoreStep - 1) / kRestoreStep);
+      // step j of the span: its first position and token count (a step past
+      // the span is a dummy with no tokens at the span start)
+      auto first = [&](int j) __attribute__((always_inline)) {
+        return j < steps ? sb + static_cast<int64_t>(j) * kRestoreStep : sb;
+      };
+      auto count = [&](int j) __attribute__((always_inline)) {
+        const int64_t left = span_end - sb - static_cast<int64_t>(j) * kRestoreStep;
+        return j < steps ? static_cast<int>(left < kRestoreStep ? left : kRestoreStep) : 0;
+      };
+      if (sb != begin) {
+        lookup(ls, first(0), count(0), ea);
+        lookup(ls, first(1), count(1), eb);
+      }
       // suffix decays of the span: one block inclusive scan of its gates
       float x = sb + tid < end ? rec[(sb + tid) * p.HV] : 0.f;
 #pragma unroll
@@ -1032,8 +1154,13 @@ __global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(
         const float y = __shfl_up(x, off, 64);
         if (lane >= off) x += y;
       }
-      lds_barrier();  // s_part and the previous span's suffixes are consumed
+      lds_barrier();  // s_part and the previous span's suffixes and rows are consumed
       if (lane == 63) s_part[wave] = x;
+      // the order of the loop's bodies (lookups, then loads), so that the
+      // loads in flight at the loop head look alike on entry and on the back edge
+      stage(0, first(0), count(0), ea);
+      lookup(ls, first(2), count(2), ea);
+      stage(1, first(1), count(1), eb);
       lds_barrier();
       float before = rest, span = 0.f;
 #pragma unroll
@@ -1041,72 +1168,82 @@ __global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(
         before += w < wave ? s_part[w] : 0.f;
         span += s_part[w];
       }
+      if (one_span) total = span;
+      if (sb == begin) {
+        const float decay = expf(total);
+#pragma unroll
+        for (int i = 0; i < RT; ++i)
+#pragma unroll
+          for (int c = 0; c < CT; ++c) acc[i][c] *= decay;
+      }
       s_suffix[tid] = expf(total - (before + x));
       rest += span;
-      const int64_t span_end = sb + kRestoreSpan < end ? sb + kRestoreSpan : end;
-      for (int64_t g0 = sb; g0 < span_end; g0 += kRestoreGroup) {
-        const int n = static_cast<int>(span_end - g0 < kRestoreGroup ? span_end - g0 : kRestoreGroup);
-        // the step's pieces: piece j of token t (consecutive threads take consecutive tokens)
-        uint4 raw[PIECES];
-        bool live[PIECES];
-#pragma unroll
-        for (int k = 0; k < PIECES; ++k) {
-          const int idx = tid + k * kDecodeThreads, t = idx % kRestoreGroup, piece = idx / kRestoreGroup;
-          const bool value = piece >= KV;
-          const int col = 8 * (value ? piece - KV : piece);
-          const T* e = restore_log<T>(p, ls, layer, g0 + (t < n ? t : 0), value ? h : kh, col, value, DK, DV);
-          live[k] = t < n && e;
-          raw[k] = *reinterpret_cast<const uint4*>(e ? e : safe);
-        }
-        lds_barrier();  // suffixes written; the previous step's operands are consumed
-#pragma unroll
-        for (int k = 0; k < PIECES; ++k) {
-          const int idx = tid + k * kDecodeThreads, t = idx % kRestoreGroup, piece = idx / kRestoreGroup;
-          const bool value = piece >= KV;
-          const int col = 8 * (value ? piece - KV : piece);
-          const uint32_t wv[4] = {live[k] ? raw[k].x : 0u, live[k] ? raw[k].y : 0u, live[k] ? raw[k].z : 0u,
-                                  live[k] ? raw[k].w : 0u};
-          uint16_t* dst = (value ? s_vt : s_kt) + col * kRestoreLd + t;
-          if (value) {
-            const float sfx = s_suffix[g0 - sb + t];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              float a, b;
-              split2<T>(wv[q], a, b);
-              const uint32_t packed = out_pack2<T>(a * sfx, b * sfx);
-              dst[(2 * q) * kRestoreLd] = static_cast<uint16_t>(packed & 0xffffu);
-              dst[(2 * q + 1) * kRestoreLd] = static_cast<uint16_t>(packed >> 16);
-            }
+      wait_steps();  // step 0 resident (step 1 and the lookups of step 2 may be in flight)
+      lds_barrier();      // and the suffixes written
+      // Step j: look up step j + 3 (into nxt), load step j + 2 (entries in
+      // cur) into buffer (j + 2) % 3, multiply step j, then wait for step
+      // j + 1.  Every step issues the same loads, dummies included, so the
+      // count-based wait is exact.
+      auto body = [&](int j, const int32_t (&cur)[NIW], int32_t (&nxt)[NIW]) __attribute__((always_inline)) {
+        lookup(ls, first(j + 3), count(j + 3), nxt);
+        stage((j + 2) % 3, first(j + 2), count(j + 2), cur);
+        if (owner) {
+          const uint16_t* sk = s_k[j % 3];
+          const uint16_t* sv = s_v[j % 3];
+          float4 s0, s1;
+          lds_read128x2(&s_suffix[j * kRestoreStep + 8 * lq], &s_suffix[j * kRestoreStep + 8 * lq + 4], s0, s1);
+          // transpose-read address of the lane: token 8 (l / 16) + 4 hf + (l % 16) / 4,
+          // columns col0 + 4 (l % 4) .. + 3
+          auto tr_addr = [&](const uint16_t* buf, int ch, int hf, int col0) __attribute__((always_inline)) {
+            const int t = 8 * lq + 4 * hf + (lr >> 2), col = col0 + 4 * (lr & 3);
+            return buf + t * ch * 8 + 8 * swz_rows(t, col >> 3, ch) + (col & 7);
+          };
+          uint4 raw[CT];
+          if constexpr (CT == 2) {
+            tr_read16x4(tr_addr(sv, CHV, 0, wave * 32), tr_addr(sv, CHV, 1, wave * 32), tr_addr(sv, CHV, 0, wave * 32 + 16),
+                        tr_addr(sv, CHV, 1, wave * 32 + 16), raw[0], raw[CT - 1]);
           } else {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              dst[(2 * q) * kRestoreLd] = static_cast<uint16_t>(wv[q] & 0xffffu);
-              dst[(2 * q + 1) * kRestoreLd] = static_cast<uint16_t>(wv[q] >> 16);
-            }
+            for (int c = 0; c < CT; ++c)
+              raw[c] = tr_read16x2(tr_addr(sv, CHV, 0, (wave * CT + c) * 16), tr_addr(sv, CHV, 1, (wave * CT + c) * 16));
+          }
+          const float sf[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+          uint4 af[CT];
+#pragma unroll
+          for (int c = 0; c < CT; ++c) {
+            float v[8];
+            split2<T>(raw[c].x, v[0], v[1]);
+            split2<T>(raw[c].y, v[2], v[3]);
+            split2<T>(raw[c].z, v[4], v[5]);
+            split2<T>(raw[c].w, v[6], v[7]);
+            af[c] = make_uint4(out_pack2<T>(v[0] * sf[0], v[1] * sf[1]), out_pack2<T>(v[2] * sf[2], v[3] * sf[3]),
+                               out_pack2<T>(v[4] * sf[4], v[5] * sf[5]), out_pack2<T>(v[6] * sf[6], v[7] * sf[7]));
+          }
+          static_assert(RT % 2 == 0, "key tiles in pairs");
+#pragma unroll
+          for (int i = 0; i < RT; i += 2) {
+            uint4 kf0, kf1;
+            tr_read16x4(tr_addr(sk, CHK, 0, 16 * i), tr_addr(sk, CHK, 1, 16 * i), tr_addr(sk, CHK, 0, 16 * i + 16),
+                        tr_addr(sk, CHK, 1, 16 * i + 16), kf0, kf1);
+#pragma unroll
+            for (int c = 0; c < CT; ++c) acc[i][c] = RestoreMma<T>::run(af[c], kf0, acc[i][c]);  // T += V'^T K
+#pragma unroll
+            for (int c = 0; c < CT; ++c) acc[i + 1][c] = RestoreMma<T>::run(af[c], kf1, acc[i + 1][c]);
           }
         }
-        lds_barrier();
-        if (owner) {
-#pragma unroll
-          for (int ks = 0; ks < kRestoreGroup / 32; ++ks)
-#pragma unroll
-            for (int c = 0; c < CT; ++c) {
-              const uint4 bfrag = *reinterpret_cast<const uint4*>(
-                  s_vt + ((wave * CT + c) * 16 + lr) * kRestoreLd + 32 * ks + 8 * lq);
-#pragma unroll
-              for (int i = 0; i < RT; ++i) {
-                const uint4 kfrag =
-                    *reinterpret_cast<const uint4*>(s_kt + (i * 16 + lr) * kRestoreLd + 32 * ks + 8 * lq);
-                acc[i][c] = RestoreMma<T>::run(bfrag, kfrag, acc[i][c]);  // T += V'^T K
-              }
-            }
-        }
+        wait_steps();  // step j + 1 resident (the loads of this body may be in flight)
+        lds_barrier();      // and step j's buffer consumed
+      };
+      int j = 0;
+      for (; j + 1 < steps; j += 2) {  // both bodies per pass
+        body(j, ea, eb);
+        body(j + 1, eb, ea);
       }
+      if (j < steps) body(j, ea, eb);
+      wait_all();  // the dummies have landed before the buffers are reused
     }
   }
-  const int64_t out = p.output[task];
   if (!owner) return;
-  const T* out_head = p.head_bytes <= p.frame_bytes ? slot_row<T>(p, out, layer, h, 0, DV) : nullptr;
 #pragma unroll
   for (int i = 0; i < RT; ++i) {
     T* row = const_cast<T*>(row_of(out, out_head, 16 * i + lr));

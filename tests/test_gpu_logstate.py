@@ -495,10 +495,11 @@ def test_logstate_backend_prefill_then_decode(eager):
 
 # (H, frame_bytes, head_bytes, granularity): state heads inside a frame and
 # spanning two frames, one and two key heads
-# (H, frame_bytes, head_bytes, granularity, dk, dv)
+# (H, frame_bytes, head_bytes, granularity, dk, dv[, page]); page 576: chains
+# over three 256-token suffix spans, the last one partial
 RESTORE_CASES = [(1, 65536, 32768, 16, 128, 128), (2, 16384, 32768, 32, 128, 128), (2, 65536, 32768, 64, 128, 128),
                  (2, 65536, 8192, 32, 64, 64), (1, 65536, 2048, 16, 32, 32), (2, 65536, 16384, 32, 128, 64),
-                 (2, 16384, 16384, 32, 64, 128)]
+                 (2, 16384, 16384, 32, 64, 128), (2, 65536, 32768, 32, 128, 128, 576)]
 
 
 @pytest.mark.parametrize("case", RESTORE_CASES)
@@ -513,16 +514,17 @@ def test_logstate_store_copy_restore(case):
     segments one of which is empty (tests/kernel/test_logstate_granules.py:24-49
     is the model)."""
     from logssms_amd.kernel.linear_attention.logstate import copy_states, restore_log_state_chains, store_log_states
-    H, frame_bytes, head_bytes, gran, dk, dv = case
+    H, frame_bytes, head_bytes, gran, dk, dv, page = case if len(case) == 7 else case + (64,)
     g = gen(101 + gran + H + dk + dv)
-    HV, layers, page, slots = 4, 2, 64, 7
+    HV, layers, slots = 4, 2, 7
     storage, payload, decay, conv, record, pool = _decode_pool(g, slots, H, HV, dk, dv, layers, page, gran, 16, 4,
                                                                frame_bytes, head_bytes)
     expected = storage.clone()
     dev_u8 = storage.view(torch.uint8).to(DEV)
     pool.storage = dev_u8
     pool.payload_frame_table, pool.decay_frame_table = payload.to(DEV), decay.to(DEV)
-    print(f"store/copy/restore H={H} frame_bytes={frame_bytes} granularity={gran} dk={dk} dv={dv}", flush=True)
+    print(f"store/copy/restore H={H} frame_bytes={frame_bytes} granularity={gran} dk={dk} dv={dv} page={page}",
+          flush=True)
     for slot in (1, 3):
         for layer in range(layers):
             heads = H if layer == 0 else HV  # keys per key head, then one row per value head
