@@ -178,3 +178,34 @@ def test_config1_against_committed_fixture():
                 torch.tensor([-1] * 7 + [1], device=DEV), torch.tensor([0, T], device=DEV))
     assert_bf16_close(o[0, ::EVERY], o_rows)
     assert_state_close(storage[1, 0], state)
+
+
+@pytest.mark.parametrize("scale", [1e3, 1e5])
+def test_large_magnitude_values(scale):
+    """Where the f16 MFMA operands stop representing the values: v scaled so
+    that v, v' and the state stay below f16's 65504 (scale 1e3: the kernel
+    matches the recurrence to the bf16 output bar, relative to the values'
+    size), and scaled past it (1e5: the operands become +-inf and the
+    overflow shows in the outputs and the final state instead of being
+    saturated silently)."""
+    g = gen(31)
+    T, H, d = 128, 2, 128
+    q, k, v, gg, beta = _inputs(g, T, H, H, d, d, torch.bfloat16)
+    v = (v.float() * scale).to(torch.bfloat16)
+    s0 = torch.zeros(H, d, d)
+    storage = torch.zeros(2, 1, H, d, d, device=DEV)
+    o, _ = _run(q.to(DEV), k.to(DEV), v.to(DEV), gg.to(DEV), beta.to(DEV), storage, torch.tensor([-1], device=DEV),
+                torch.full((2,), -1, device=DEV), torch.tensor([0, T], device=DEV), finals=torch.tensor([1], device=DEV))
+    torch.cuda.synchronize()
+    print(f"scale {scale:g}: |v| max {float(v.float().abs().max()):.3e}", flush=True)
+    if scale < 65504 / 8:
+        o_ref, s_ref, _ = ref.naive_recurrence(q.float(), k.float(), v.float(), gg, beta, d ** -0.5, s0)
+        _report("out / scale", o[0].float() / scale, o_ref / scale)
+        _report("state / scale", storage[1, 0] / scale, s_ref / scale)
+        assert float(v.float().abs().max()) > 1e3 and float(s_ref.abs().max()) < 65504
+        assert_bf16_close(o[0].float() / scale, o_ref / scale)
+        assert_state_close(storage[1, 0].cpu() / scale, s_ref / scale)
+    else:
+        assert float(v.float().abs().max()) > 65504
+        assert not torch.isfinite(o).all(), "values beyond f16's range should overflow visibly"
+        assert not torch.isfinite(storage[1, 0]).all()
