@@ -478,6 +478,30 @@ __device__ __forceinline__ uint4 tr_read16x2(const uint16_t* a0, const uint16_t*
       : "memory");
   return make_uint4(r0.x, r0.y, r1.x, r1.y);
 }
+// Direct-to-LDS load of 4 bytes per active lane: lane l lands at lds + 4 l.
+__device__ __forceinline__ void dma4(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)(lds), 4, 0, 0);
+}
+// N (1..4) 4-byte reads.
+template <int N> __device__ __forceinline__ void lds_read32(const int32_t* const (&a)[N], int32_t (&v)[N]) {
+  static_assert(N >= 1 && N <= 4, "1..4 reads");
+  if constexpr (N == 1) {
+    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v[0]) : "v"(lds_addr(a[0])) : "memory");
+  } else if constexpr (N == 2) {
+    asm volatile("ds_read_b32 %0, %2\n\tds_read_b32 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(v[0]), "=&v"(v[1]) : "v"(lds_addr(a[0])), "v"(lds_addr(a[1])) : "memory");
+  } else if constexpr (N == 3) {
+    asm volatile("ds_read_b32 %0, %3\n\tds_read_b32 %1, %4\n\tds_read_b32 %2, %5\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2])
+                 : "v"(lds_addr(a[0])), "v"(lds_addr(a[1])), "v"(lds_addr(a[2])) : "memory");
+  } else {
+    asm volatile(
+        "ds_read_b32 %0, %4\n\tds_read_b32 %1, %5\n\tds_read_b32 %2, %6\n\tds_read_b32 %3, %7\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+        : "v"(lds_addr(a[0])), "v"(lds_addr(a[1])), "v"(lds_addr(a[2])), "v"(lds_addr(a[3])) : "memory");
+  }
+}
 // Two 16-byte reads.
 __device__ __forceinline__ void lds_read128x2(const float* a0, const float* a1, float4& x, float4& y) {
   asm volatile(
@@ -1000,11 +1024,6 @@ __global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(
   constexpr int KI = kRestoreStep * 2 * DK / 1024;      // 1 KiB wave loads of a step's key rows
   constexpr int NI = KI + kRestoreStep * 2 * DV / 1024;  // ... and of all its rows
   constexpr int NIW = (NI + 3) / 4;                     // per wave
-  // Loads a wave issues per step (lookups and stage): the same in every wave
-  // when NI is a multiple of 4, so a count-based wait is exact; else wait for all.
-  auto wait_steps = [&]() __attribute__((always_inline)) {
-    if constexpr (NI % 4 == 0) wait_vm<2 * NIW>(); else wait_all();
-  };
   static_assert(DK % 16 == 0 && DV % 16 == 0 && DK <= 512 && DV <= 512, "tile split");
   static_assert((kRestoreStep * 2 * DK) % 1024 == 0 && (kRestoreStep * 2 * DV) % 1024 == 0, "whole wave loads");
   const uint32_t bid = blockIdx.x, nhv = static_cast<uint32_t>(p.HV), nl = static_cast<uint32_t>(p.layers);
@@ -1017,6 +1036,7 @@ __global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(
   __shared__ __attribute__((aligned(16))) uint16_t s_k[3][kRestoreStep * DK];
   __shared__ __attribute__((aligned(16))) uint16_t s_v[3][kRestoreStep * DV];
   __shared__ __attribute__((aligned(16))) float s_suffix[kRestoreSpan];
+  __shared__ int32_t s_ent[4][4 * kRestoreStep];  // frame entries of a step's 2 S rows (first / last byte), by step % 4
   __shared__ float s_part[kDecodeThreads / 64];
   // acc[i][c] is the transposed tile T = S^T: lane l holds dk column
   // i 16 + l % 16 and dv rows (wave CT + c) 16 + 4 (l / 16) .. + 3, i.e. four
@@ -1059,36 +1079,53 @@ __global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(
   const void* const zero_piece = &g_zero_piece;
   const uint32_t key_size = static_cast<uint32_t>(p.gran * p.KH * DK);
   const uint32_t layer_size = key_size + static_cast<uint32_t>(p.gran * p.HV * DV);
-  // Byte offset of piece k of the step at g0 inside the log slot (a token
-  // past n reads the first token's place).
-  auto piece_byte = [&](int64_t g0, int n, int k) __attribute__((always_inline)) -> uint32_t {
-    const Piece pc = piece_of(k);
-    const uint32_t ps = static_cast<uint32_t>(g0 + (pc.t < n ? pc.t : 0));
+  // Slot-relative byte of row r of the step at g0: rows 0 .. S-1 are the
+  // tokens' key rows, S .. 2S-1 their value rows (a token past n reads the
+  // first token's place).
+  auto row_byte = [&](int64_t g0, int n, int r) __attribute__((always_inline)) -> uint32_t {
+    const bool key = r < kRestoreStep;
+    const int t = key ? r : r - kRestoreStep;
+    const uint32_t ps = static_cast<uint32_t>(g0 + (t < n ? t : 0));
     const uint32_t elem = (p.gdiv.div(ps) * static_cast<uint32_t>(p.layers) + static_cast<uint32_t>(layer)) * layer_size +
-                          (pc.key ? 0u : key_size) +
-                          (static_cast<uint32_t>(pc.key ? kh : h) * static_cast<uint32_t>(p.gran) + p.gdiv.mod(ps)) *
-                              static_cast<uint32_t>(pc.key ? DK : DV) +
-                          8u * static_cast<uint32_t>(pc.c);
+                          (key ? 0u : key_size) +
+                          (static_cast<uint32_t>(key ? kh : h) * static_cast<uint32_t>(p.gran) + p.gdiv.mod(ps)) *
+                              static_cast<uint32_t>(key ? DK : DV);
     return 2u * elem;
   };
-  // Frame-table entries of the step's pieces.
-  auto lookup = [&](int64_t ls, int64_t g0, int n, int32_t (&entry)[NIW]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int k = 0; k < NIW; ++k) {
-      if (wave + 4 * k >= NI) break;
-      entry[k] = static_cast<int32_t>(load_index(p.frames, ls * p.fps + p.fdiv.div(piece_byte(g0, n, k)), p.frames_is64));
+  // Frame-table entries of the step's rows into entry slot `slot`: waves 0
+  // and 1, one 4-byte direct-to-LDS load per lane, entry 2 r + 0 / 1 for the
+  // frames of row r's first / last byte (a row spans at most two frames).
+  const int32_t* const ftab = static_cast<const int32_t*>(p.frames);
+  auto lookup = [&](int64_t ls, int64_t g0, int n, int slot) __attribute__((always_inline)) {
+    if (wave < 2) {
+      const int q = wave * 64 + lane, r = q >> 1;
+      const uint32_t last = 2u * static_cast<uint32_t>(r < kRestoreStep ? DK : DV) - 1u;
+      const uint32_t b = row_byte(g0, n, r) + ((q & 1) ? last : 0u);
+      dma4(ftab + (ls * p.fps + p.fdiv.div(b)) * (p.frames_is64 ? 2 : 1), &s_ent[slot][wave * 64]);
     }
   };
-  // Direct-to-LDS loads of the step's rows into buffer b (zeros past n and
-  // for unmapped frames).
-  auto stage = [&](int b, int64_t g0, int n, const int32_t (&entry)[NIW]) __attribute__((always_inline)) {
+  // Direct-to-LDS loads of the step's rows into buffer b from the entries in
+  // slot `slot` (zeros past n and for unmapped frames).
+  auto stage = [&](int b, int64_t g0, int n, int slot) __attribute__((always_inline)) {
+    const int32_t* ea[NIW];
+    uint32_t pb[NIW];
+#pragma unroll
+    for (int k = 0; k < NIW; ++k) {
+      const Piece pc = piece_of(k);
+      const int r = wave + 4 * k < NI ? (pc.key ? pc.t : kRestoreStep + pc.t) : 0;  // pieces past NI: unused
+      const uint32_t rb = row_byte(g0, n, r);
+      pb[k] = rb + 16u * static_cast<uint32_t>(pc.c);
+      ea[k] = &s_ent[slot][2 * r + (p.fdiv.div(pb[k]) != p.fdiv.div(rb) ? 1 : 0)];
+    }
+    int32_t entry[NIW];
+    lds_read32<NIW>(ea, entry);
 #pragma unroll
     for (int k = 0; k < NIW; ++k) {
       const int rg = wave + 4 * k;
       if (rg >= NI) break;
-      // branch-free select, so the entry's wait stays a counted one
+      // branch-free select
       const bool live = (piece_of(k).t < n) & (entry[k] >= 0) & (entry[k] < p.num_frames);
-      const char* a = p.storage + static_cast<int64_t>(entry[k]) * p.frame_bytes + p.fdiv.mod(piece_byte(g0, n, k));
+      const char* a = p.storage + static_cast<int64_t>(entry[k]) * p.frame_bytes + p.fdiv.mod(pb[k]);
       const void* src = live ? static_cast<const void*>(a) : zero_piece;
       uint16_t* dst = rg < KI ? &s_k[b][rg * 512] : &s_v[b][(rg - KI) * 512];
       dma16(src, dst);
@@ -1096,21 +1133,24 @@ __global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(
   };
   const int64_t out = p.output[task];
   const T* out_head = p.head_bytes <= p.frame_bytes ? slot_row<T>(p, out, layer, h, 0, DV) : nullptr;
+  // Loads a wave has in flight after the last step's rows at the end of a
+  // step: its rows of the next step and, in waves 0-1, one lookup.  The
+  // count is exact when NI is a multiple of 4 (every wave the same pieces).
+  auto wait_step = [&]() __attribute__((always_inline)) {
+    if constexpr (NI % 4 == 0) {
+      if (wave < 2) wait_vm<NIW + 1>(); else wait_vm<NIW>();
+    } else {
+      wait_all();
+    }
+  };
   for (int64_t seg = p.offsets[task]; seg < p.offsets[task + 1]; ++seg) {
     const int64_t ls = p.seg_slots[seg];
     const int64_t begin = p.seg_begin[seg] < 0 ? 0 : p.seg_begin[seg];
     const int64_t end = p.seg_end[seg] < p.page ? p.seg_end[seg] : p.page;
     int64_t fr = -1, ri = -1;
-    // frame entries of the first span's first two steps, in flight with the decay lookup
-    int32_t ea[NIW], eb[NIW];
-    const int first_n = static_cast<int>(end - begin < kRestoreStep ? end - begin : kRestoreStep);
     if (ls >= 0 && begin < end) {
       fr = load_index(p.decay, 2 * ls, p.decay_is64);
       ri = load_index(p.decay, 2 * ls + 1, p.decay_is64);
-      lookup(ls, begin, first_n, ea);
-      lookup(ls, end - begin > kRestoreStep ? begin + kRestoreStep : begin,
-             end - begin > kRestoreStep ? static_cast<int>(end - begin - kRestoreStep < kRestoreStep
-                                                               ? end - begin - kRestoreStep : kRestoreStep) : 0, eb);
     }
     const bool ok = fr >= 0 && fr < p.num_frames && ri >= 0 && (ri + 1) * p.record_bytes <= p.frame_bytes;
     if (!ok || begin >= end) continue;
@@ -1143,10 +1183,9 @@ __global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(
         const int64_t left = span_end - sb - static_cast<int64_t>(j) * kRestoreStep;
         return j < steps ? static_cast<int>(left < kRestoreStep ? left : kRestoreStep) : 0;
       };
-      if (sb != begin) {
-        lookup(ls, first(0), count(0), ea);
-        lookup(ls, first(1), count(1), eb);
-      }
+      lds_barrier();  // s_part, the entry slots and the previous span's suffixes and rows are consumed
+#pragma unroll
+      for (int j = 0; j < 4; ++j) lookup(ls, first(j), count(j), j);
       // suffix decays of the span: one block inclusive scan of its gates
       float x = sb + tid < end ? rec[(sb + tid) * p.HV] : 0.f;
 #pragma unroll
@@ -1154,14 +1193,11 @@ __global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(
         const float y = __shfl_up(x, off, 64);
         if (lane >= off) x += y;
       }
-      lds_barrier();  // s_part and the previous span's suffixes and rows are consumed
       if (lane == 63) s_part[wave] = x;
-      // the order of the loop's bodies (lookups, then loads), so that the
-      // loads in flight at the loop head look alike on entry and on the back edge
-      stage(0, first(0), count(0), ea);
-      lookup(ls, first(2), count(2), ea);
-      stage(1, first(1), count(1), eb);
-      lds_barrier();
+      wait_all();     // the entries of steps 0-3 have landed
+      lds_barrier();  // for every wave
+      stage(0, first(0), count(0), 0);
+      stage(1, first(1), count(1), 1);
       float before = rest, span = 0.f;
 #pragma unroll
       for (int w = 0; w < kDecodeThreads / 64; ++w) {
@@ -1178,15 +1214,15 @@ __global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(
       }
       s_suffix[tid] = expf(total - (before + x));
       rest += span;
-      wait_steps();  // step 0 resident (step 1 and the lookups of step 2 may be in flight)
-      lds_barrier();      // and the suffixes written
-      // Step j: look up step j + 3 (into nxt), load step j + 2 (entries in
-      // cur) into buffer (j + 2) % 3, multiply step j, then wait for step
-      // j + 1.  Every step issues the same loads, dummies included, so the
-      // count-based wait is exact.
-      auto body = [&](int j, const int32_t (&cur)[NIW], int32_t (&nxt)[NIW]) __attribute__((always_inline)) {
-        lookup(ls, first(j + 3), count(j + 3), nxt);
-        stage((j + 2) % 3, first(j + 2), count(j + 2), cur);
+      if constexpr (NI % 4 == 0) wait_vm<NIW>(); else wait_all();  // step 0 resident
+      lds_barrier();  // for every wave, with the suffixes
+      // Step j: look up step j + 4 (entry slot j % 4), load step j + 2 into
+      // buffer (j + 2) % 3 from entry slot (j + 2) % 4, multiply step j, then
+      // wait for step j + 1's rows and step j + 3's entries.  Every step
+      // issues the same loads, dummies included, so the counted wait is exact.
+      for (int j = 0; j < steps; ++j) {
+        lookup(ls, first(j + 4), count(j + 4), j & 3);
+        stage((j + 2) % 3, first(j + 2), count(j + 2), (j + 2) & 3);
         if (owner) {
           const uint16_t* sk = s_k[j % 3];
           const uint16_t* sv = s_v[j % 3];
@@ -1231,15 +1267,9 @@ __global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(
             for (int c = 0; c < CT; ++c) acc[i + 1][c] = RestoreMma<T>::run(af[c], kf1, acc[i + 1][c]);
           }
         }
-        wait_steps();  // step j + 1 resident (the loads of this body may be in flight)
-        lds_barrier();      // and step j's buffer consumed
-      };
-      int j = 0;
-      for (; j + 1 < steps; j += 2) {  // both bodies per pass
-        body(j, ea, eb);
-        body(j + 1, eb, ea);
+        wait_step();
+        lds_barrier();  // step j + 1 and the entries of step j + 3 resident; step j's buffer consumed
       }
-      if (j < steps) body(j, ea, eb);
       wait_all();  // the dummies have landed before the buffers are reused
     }
   }
@@ -1615,6 +1645,10 @@ extern "C" int gdn_logstate_restore(void* storage, const void* payload_frames, i
                          num_frames, decay_frames, decay_dtype, decay_record_bytes, num_layers, HV, key_heads, dk, dv,
                          granularity, page_size, "gdn_logstate_restore");
   if (rc != GDN_OK) return rc;
+  // the kernel looks up a logged row's frames at its first and last byte
+  GDN_REQUIRE(frame_bytes >= 2 * (dk > dv ? dk : dv),
+              "gdn_logstate_restore: frame_bytes %lld smaller than a logged row (%lld bytes)", (long long)frame_bytes,
+              (long long)(2 * (dk > dv ? dk : dv)));
   p.base = base_slots; p.offsets = segment_offsets; p.seg_slots = log_slots; p.seg_begin = log_begins;
   p.seg_end = log_ends; p.output = output_slots;
   return launch_state_kernel<true>(p, num_tasks * num_layers * HV, dk, dv, dtype,
