@@ -357,14 +357,15 @@ __global__ __launch_bounds__(kThreads) void fused_kernel(RecParams p) {
   const int nch = 2 * DK + group * DV;
   const int W = p.kernel_width;
   const int64_t read_slot = load_index(p.read_slots, b * p.read_stride, p.read_is64);
-  // Verify requests the first v-head's state before the conv, so its latency
-  // overlaps the conv's window loads, and each next v-head's state before the
-  // current one's last store (measured: 261 -> 254 us at config 5).  Decode
-  // keeps one state live at a time: the second register set halves its
+  // The first v-head's state is requested before the conv, so its latency
+  // overlaps the conv's window loads (decode 221 -> 218 us at config 3, at an
+  // unchanged 4 waves per SIMD).  Verify also requests each next v-head's
+  // state before the current one's last store (261 -> 254 us at config 5).
+  // Decode keeps one state live at a time: the second register set halves its
   // occupancy, and its in-place update measured slower with it (213 -> 223 us).
   constexpr bool kPrefetch = !kStreamLoads;
   float st[RPT][4];
-  if constexpr (kPrefetch) load_state<DK, DV, ST, kStreamLoads>(p, st, b, kh * group);
+  load_state<DK, DV, ST, kStreamLoads>(p, st, b, kh * group);
   for (int c = threadIdx.x; c < nch; c += kThreads) {
     int64_t ch;
     float* dst;
@@ -453,7 +454,7 @@ __global__ __launch_bounds__(kThreads) void fused_kernel(RecParams p) {
   __syncthreads();
   for (int j = 0; j < group; ++j) {
     const int64_t h = kh * group + j;
-    if constexpr (!kPrefetch) load_state<DK, DV, ST, kStreamLoads>(p, st, b, h);
+    if (!kPrefetch && j > 0) load_state<DK, DV, ST, kStreamLoads>(p, st, b, h);
     run_steps<DK, DV, IOT, ST>(p, s, st, b, h, j, group, 0, steps, true);
     if constexpr (kPrefetch) {
       float next[RPT][4];
