@@ -278,7 +278,9 @@ int gdn_recurrent_logstate(const void* q, const void* k, const void* v, int io_d
  * (the log layout and decay records of gdn_store_chunk_log, key_heads log
  * key heads); the result goes to output_slots[i].  Slot states use the frame
  * layout of gdn_chunk_gated_delta_rule; dtype bf16 or f16.  Outputs must not
- * be read by another task of the same call.
+ * be read by another task of the same call.  frame_bytes must hold one logged
+ * row (2 max(dk, dv) bytes), so that a row spans at most two frames
+ * (GDN_ERR_INVALID otherwise).
  */
 int gdn_logstate_restore(void* storage, const void* payload_frames, int frames_dtype, int64_t frames_per_slot,
                          int64_t frame_bytes, int64_t head_bytes, int64_t num_frames, const void* decay_frames,
