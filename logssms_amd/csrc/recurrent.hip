@@ -358,8 +358,8 @@ __global__ __launch_bounds__(kThreads) void fused_kernel(RecParams p) {
   const int W = p.kernel_width;
   const int64_t read_slot = load_index(p.read_slots, b * p.read_stride, p.read_is64);
   // The first v-head's state is requested before the conv, so its latency
-  // overlaps the conv's window loads (decode 221 -> 218 us at config 3, at an
-  // unchanged 4 waves per SIMD).  Verify also requests each next v-head's
+  // overlaps the conv's window loads (decode at config 3: 218-223 us, within
+  // the box-to-box spread of the later load, at an unchanged 4 waves per SIMD).  Verify also requests each next v-head's
   // state before the current one's last store (261 -> 254 us at config 5).
   // Decode keeps one state live at a time: the second register set halves its
   // occupancy, and its in-place update measured slower with it (213 -> 223 us).
