@@ -496,10 +496,20 @@ def rmw_sweep(dev, steps, warmup, nbytes=2 << 30):
                 runs.append({"block_kib": block_kib, "loads_in_flight": loads, "nontemporal": nt, "ms": ms,
                              "GB/s": 2 * nbytes / (ms * 1e-3) / 1e9})
     best = max(runs, key=lambda r: r["GB/s"])
+    # store-only stream (loads_in_flight 0): the write ceiling verify's per-step stores are read against
+    writes = []
+    for block_kib in (64, 1024):
+        for nt in (0, 1):
+            ms = _time(lambda: _lib.call("gdn_probe_rmw", buf.data_ptr(), nbytes, block_kib << 10, 0, nt, stream),
+                       steps, warmup)
+            writes.append({"block_kib": block_kib, "nontemporal": nt, "ms": ms, "GB/s": nbytes / (ms * 1e-3) / 1e9})
+    best_w = max(writes, key=lambda r: r["GB/s"])
     del buf
     torch.cuda.empty_cache()
     return {"config": "gdn_probe_rmw over 2 GiB in place (1 read : 1 write, 16-byte vectors)", "best": best,
-            "frac_hbm": best["GB/s"] * 1e9 / PEAK_HBM, "runs": runs}
+            "frac_hbm": best["GB/s"] * 1e9 / PEAK_HBM, "runs": runs,
+            "store_only": {"config": "gdn_probe_rmw loads_in_flight 0: 2 GiB of 16-byte stores", "best": best_w,
+                           "frac_hbm": best_w["GB/s"] * 1e9 / PEAK_HBM, "runs": writes}}
 
 
 # ---------------------------------------------------------------- LogState

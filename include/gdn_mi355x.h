@@ -619,7 +619,8 @@ int64_t gdn_prefill_noalloc_scratch_bytes(void);
  * consecutive bytes and each lane keeping `loads_in_flight` (1, 2, 4, 8, 16)
  * 16-byte loads in flight before its stores, optionally non-temporal.  The
  * 1-read:1-write HBM ceiling the decode / verify state updates are read
- * against (bench.py --only rmw).
+ * against (bench.py --only rmw).  loads_in_flight 0: a store-only stream
+ * (buf[i] <- 1.0, four 16-byte stores per lane per pass), the write ceiling.
  */
 int gdn_probe_rmw(void* buf, int64_t bytes, int64_t block_bytes, int loads_in_flight, int nontemporal,
                   void* stream);

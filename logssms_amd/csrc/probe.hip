@@ -2,7 +2,8 @@
 // stream (x <- a x over 16-byte vectors), the access mix of the decode state
 // update (each 64 KiB of state read once and written back once).  Not part of
 // the GDN path; bench.py --only rmw uses it to measure the 1-read:1-write
-// ceiling of the box that the decode / verify fractions are read against.
+// ceiling of the box that the decode / verify fractions are read against, and
+// a store-only stream (the write ceiling for verify's per-step state stores).
 #include "common.hpp"
 
 namespace gdn {
@@ -29,6 +30,24 @@ __global__ __launch_bounds__(256) void rmw_kernel(f4v* buf, int64_t n_vec, int64
       if (i < end) {
         if (NT) __builtin_nontemporal_store(v[u] * a, buf + i);
         else buf[i] = v[u] * a;
+      }
+    }
+  }
+}
+
+// Store-only stream: buf[i] <- (a, a, a, a), 4 stores per lane per pass.
+template <bool NT>
+__global__ __launch_bounds__(256) void store_kernel(f4v* buf, int64_t n_vec, int64_t per_block, float a) {
+  const int64_t begin = static_cast<int64_t>(blockIdx.x) * per_block;
+  const int64_t end = begin + per_block < n_vec ? begin + per_block : n_vec;
+  const f4v v = {a, a, a, a};
+  for (int64_t i0 = begin + threadIdx.x; i0 < end; i0 += 256 * 4) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t i = i0 + 256 * u;
+      if (i < end) {
+        if (NT) __builtin_nontemporal_store(v, buf + i);
+        else buf[i] = v;
       }
     }
   }
@@ -63,13 +82,22 @@ extern "C" int gdn_probe_rmw(void* buf, int64_t bytes, int64_t block_bytes, int 
   const int64_t n = bytes / 16, per = block_bytes / 16;
   auto s = static_cast<hipStream_t>(stream);
   switch (loads_in_flight) {
+    case 0: {
+      const int64_t blocks = (n + per - 1) / per;
+      GDN_REQUIRE(blocks <= 0x7fffffff, "gdn_probe_rmw: grid too large");
+      if (nontemporal)
+        hipLaunchKernelGGL((store_kernel<true>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, v, n, per, 1.0f);
+      else
+        hipLaunchKernelGGL((store_kernel<false>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, v, n, per, 1.0f);
+      return GDN_LAUNCH_CHECK("gdn_probe_rmw launch");
+    }
     case 1: return launch_rmw<1>(v, n, per, nontemporal, s);
     case 2: return launch_rmw<2>(v, n, per, nontemporal, s);
     case 4: return launch_rmw<4>(v, n, per, nontemporal, s);
     case 8: return launch_rmw<8>(v, n, per, nontemporal, s);
     case 16: return launch_rmw<16>(v, n, per, nontemporal, s);
     default:
-      set_error("gdn_probe_rmw: loads_in_flight %d not in {1, 2, 4, 8, 16}", loads_in_flight);
+      set_error("gdn_probe_rmw: loads_in_flight %d not in {0, 1, 2, 4, 8, 16}", loads_in_flight);
       return GDN_ERR_UNSUPPORTED;
   }
 }
