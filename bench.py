@@ -18,6 +18,10 @@ then the chunk kernel) on the same inputs.
 (config 5) and the gated RMS norm of the config 2 output, in GB/s against
 8 TB/s, from the canonical byte formulas.
 
+Every time is the median over the K timed steps, each bracketed by its own
+pair of HIP events inside one synchronized region, after W warm-up steps
+(defaults K = 50, W = 10).
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 """
 
@@ -122,27 +126,40 @@ def _config(layer=0):
     return GatedDeltaConfig(H, HV, D, D, CONV_DIM, W - 1, layer)
 
 
-def _time(fn, steps, warmup, events=None):
-    """Times `steps` calls of fn between synchronize barriers; returns ms/step.
-    `events` (list) collects per-kernel (start, end) pairs recorded inside fn."""
+def _median(values):
+    v = sorted(values)
+    n = len(v)
+    return v[n // 2] if n % 2 else 0.5 * (v[n // 2 - 1] + v[n // 2])
+
+
+def _time(fn, steps, warmup, events=None, stats=None):
+    """`warmup` untimed calls of fn, then `steps` timed calls between
+    synchronize barriers, each call bracketed by its own pair of events on the
+    current stream (one event between consecutive calls).  Returns the median
+    ms per call; `stats` (dict) receives the mean, min and max.  `events`
+    (list) collects per-kernel (start, end) pairs recorded inside fn."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
     if events is not None:
         events.clear()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(steps):
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    marks[0].record()
+    for i in range(steps):
         fn()
-    end.record()
+        marks[i + 1].record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    per_step = [marks[i].elapsed_time(marks[i + 1]) for i in range(steps)]
+    if stats is not None:
+        stats.update(mean_ms=marks[0].elapsed_time(marks[-1]) / steps, min_ms=min(per_step), max_ms=max(per_step))
+    return _median(per_step)
 
 
 def _kernel_ms(events):
+    """Median duration of the kernel launches bracketed by `events`."""
     if not events:
         return None
-    return sum(a.elapsed_time(b) for a, b in events) / len(events)
+    return _median([a.elapsed_time(b) for a, b in events])
 
 
 # ---------------------------------------------------------------- prefill (config 2)
@@ -352,7 +369,7 @@ def decode_gpu(dev, B=256, slots=1024, seed=3, events=None):
         decode_step(mixed, gate, beta, weight, A_log, dt_bias, cfg, conv, state, slot_idx, slot_idx, out=out)
 
     tensors = dict(mixed=mixed, gate=gate, beta=beta, weight=weight, A_log=A_log, dt_bias=dt_bias, conv=conv,
-                   state=state, reads=slot_idx, writes=slot_idx)
+                   state=state, reads=slot_idx, writes=slot_idx, out=out)
     return step, tensors
 
 
@@ -362,7 +379,7 @@ def decode_cpu_leg(t, budget_s):
     recurrence batched over the 256 sequences) on a host copy of the GPU
     run's pools and inputs, all host threads."""
     from oracle import gdn as ref
-    h = {k: v.cpu() for k, v in t.items()}
+    h = {k: v.cpu() for k, v in t.items() if k != "out"}
 
     def run():
         ref.forward_decode_batched(h["mixed"], h["gate"], h["beta"], h["weight"], h["A_log"], h["dt_bias"],
@@ -403,7 +420,7 @@ def verify_gpu(dev, B=64, T=8, slots=1024, seed=5):
                   accepted.data_ptr(), 1, B, T, _lib.stream_of(state))
 
     tensors = dict(mixed=mixed, gate=gate, beta=beta, weight=weight, A_log=A_log, dt_bias=dt_bias, conv=conv,
-                   state=state, live=live, writes=writes)
+                   state=state, live=live, writes=writes, out=out, accepted=accepted)
     return step, commit, tensors
 
 
@@ -413,7 +430,7 @@ def verify_cpu_leg(t, budget_s):
     sequences, every per-step state and window written with index_copy_) on a
     host copy of the GPU run's pools and inputs, all host threads."""
     from oracle import gdn as ref
-    h = {k: v.cpu() for k, v in t.items()}
+    h = {k: v.cpu() for k, v in t.items() if k not in ("out", "accepted")}
 
     def run():
         ref.forward_verify_batched(h["mixed"], h["gate"], h["beta"], h["weight"], h["A_log"], h["dt_bias"],
@@ -479,20 +496,43 @@ def layer_gpu(dev, hidden=2048, seed=7):
     return step, parts
 
 
+def _probe_lib():
+    """The bench-only probe library (``logssms_amd/libgdn_probe.so``, built
+    beside the product library from ``csrc/probe/rmw_probe.hip``)."""
+    import ctypes
+    path = os.path.join(ROOT, "logssms_amd", "libgdn_probe.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: build with `make -C logssms_amd/csrc`")
+    lib = ctypes.CDLL(path)
+    lib.gdn_probe_rmw.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                  ctypes.c_void_p]
+    lib.gdn_probe_rmw.restype = ctypes.c_int
+    lib.gdn_probe_last_error.restype = ctypes.c_char_p
+    return lib
+
+
 def rmw_sweep(dev, steps, warmup, nbytes=2 << 30):
-    """The box's 1-read:1-write HBM ceiling: ``gdn_probe_rmw`` (an in-place
-    x <- 1.0 x stream over 16-byte vectors) over a 2 GiB buffer, the size of
-    config 3's state pool, for block sizes and loads in flight per lane.
-    GB/s counts the bytes read plus the bytes written."""
+    """The box's 1-read:1-write HBM ceiling over a 2 GiB buffer (the size of
+    config 3's state pool), by three access patterns: ``gdn_probe_rmw`` (an
+    in-place x <- 1.0 x stream over 16-byte vectors, for block sizes and loads
+    in flight per lane), torch's in-place ``mul_`` and torch's device
+    ``copy_`` (2 GiB read into another 2 GiB).  GB/s counts the bytes read plus
+    the bytes written."""
     from logssms_amd import _lib
+    probe = _probe_lib()
+
+    def run(*args):
+        rc = probe.gdn_probe_rmw(*args)
+        if rc:
+            raise RuntimeError(f"gdn_probe_rmw failed ({rc}): {probe.gdn_probe_last_error().decode()}")
+
     buf = torch.ones(nbytes // 4, device=dev)
     stream = _lib.stream_of(buf)
     runs = []
     for block_kib in (64, 1024):
         for loads in (1, 4, 16):
             for nt in (0, 1):
-                ms = _time(lambda: _lib.call("gdn_probe_rmw", buf.data_ptr(), nbytes, block_kib << 10, loads, nt,
-                                             stream), steps, warmup)
+                ms = _time(lambda: run(buf.data_ptr(), nbytes, block_kib << 10, loads, nt, stream), steps, warmup)
                 runs.append({"block_kib": block_kib, "loads_in_flight": loads, "nontemporal": nt, "ms": ms,
                              "GB/s": 2 * nbytes / (ms * 1e-3) / 1e9})
     best = max(runs, key=lambda r: r["GB/s"])
@@ -500,14 +540,21 @@ def rmw_sweep(dev, steps, warmup, nbytes=2 << 30):
     writes = []
     for block_kib in (64, 1024):
         for nt in (0, 1):
-            ms = _time(lambda: _lib.call("gdn_probe_rmw", buf.data_ptr(), nbytes, block_kib << 10, 0, nt, stream),
-                       steps, warmup)
+            ms = _time(lambda: run(buf.data_ptr(), nbytes, block_kib << 10, 0, nt, stream), steps, warmup)
             writes.append({"block_kib": block_kib, "nontemporal": nt, "ms": ms, "GB/s": nbytes / (ms * 1e-3) / 1e9})
     best_w = max(writes, key=lambda r: r["GB/s"])
-    del buf
+    # two library access patterns beside the probe
+    ms_mul = _time(lambda: buf.mul_(1.0), steps, warmup)
+    other = torch.empty_like(buf)
+    ms_copy = _time(lambda: other.copy_(buf), steps, warmup)
+    del buf, other
     torch.cuda.empty_cache()
+    torch_legs = {"mul_": {"ms": ms_mul, "GB/s": 2 * nbytes / (ms_mul * 1e-3) / 1e9},
+                  "copy_": {"ms": ms_copy, "GB/s": 2 * nbytes / (ms_copy * 1e-3) / 1e9}}
+    ceiling = max([best["GB/s"]] + [leg["GB/s"] for leg in torch_legs.values()])
     return {"config": "gdn_probe_rmw over 2 GiB in place (1 read : 1 write, 16-byte vectors)", "best": best,
             "frac_hbm": best["GB/s"] * 1e9 / PEAK_HBM, "runs": runs,
+            "torch": torch_legs, "best_GB/s": ceiling,
             "store_only": {"config": "gdn_probe_rmw loads_in_flight 0: 2 GiB of 16-byte stores", "best": best_w,
                            "frac_hbm": best_w["GB/s"] * 1e9 / PEAK_HBM, "runs": writes}}
 
@@ -673,8 +720,8 @@ def logstate_gpu(dev, steps, warmup, B=256):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="time budget of each CPU baseline leg (chunked prefill; naive prefill, decode and "
@@ -711,7 +758,8 @@ def main():
         inp = make_prefill(draw_device=dev)
         events = []
         step, state_pool, out = prefill_gpu(inp, dev, events)
-        ms = _time(step, args.steps, args.warmup, events)
+        step_stats = {}
+        ms = _time(step, args.steps, args.warmup, events, step_stats)
         chunk_ms = _kernel_ms(events)
         step2, _, _ = prefill_gpu(inp, dev, None, fused=False)
         extra["prefill_two_step_ms"] = _time(step2, args.steps, args.warmup)
@@ -727,6 +775,8 @@ def main():
             value=T / (ms * 1e-3),
             unit="tokens/s",
             n_gpus=1, steps=args.steps, warmup=args.warmup, ms_per_step=ms,
+            ms_per_step_stats={"median": ms, **step_stats,
+                               "timing": "one event pair per step inside the synchronized region; median"},
             higher_is_better=True, scaling="weak", vs_baseline=None,
             dtype="bf16 in / fp16 MFMA operands / fp32 state",
             data="synthetic (seeded N(0,1) mixed_qkv, conv w N(0,0.02), zero initial state)",

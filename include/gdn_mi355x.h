@@ -126,9 +126,10 @@ int gdn_prefill_frontend(const void* mixed, int64_t row_stride, int64_t col_stri
  * the slot; logical byte x lies in frame frames[s frames_per_slot + x /
  * frame_bytes] at offset x % frame_bytes.  head_bytes >= dk dv elt, and either
  * divides frame_bytes or is a multiple of it (then frame_bytes must be a
- * multiple of 16 state rows, 16 dv elt).  A frame entry < 0 or >= num_frames reads as zero state
- * and takes no write.  Granularities below 64 and frame tables need
- * dv % 64 == 0.
+ * multiple of 16 state rows, 16 dv elt).  frames has table_rows rows
+ * (slots); a slot >= table_rows, like a frame entry < 0 or >= num_frames,
+ * reads as zero state and takes no write (table_rows is ignored without
+ * frames).  dk in {32, 64, 128}; dv 32 or a multiple of 64.
  */
 int gdn_chunk_gated_delta_rule(const void* q, const void* k, const void* v, int io_dtype, const float* g,
                                const float* beta, const void* cu_seqlens, int cu_dtype, int64_t num_seqs,
@@ -137,9 +138,9 @@ int gdn_chunk_gated_delta_rule(const void* q, const void* k, const void* v, int 
                                int64_t head_stride, int64_t layer, const void* read_slots, int read_dtype,
                                const void* chunk_write_slots, int chunk_write_dtype,
                                const void* final_write_slots, int final_write_dtype, int64_t chunk_size,
-                               const void* frames, int frames_dtype, int64_t frames_per_slot, int64_t frame_bytes,
-                               int64_t head_bytes, int64_t num_frames, void* out, void* v_new, float scale,
-                               void* stream);
+                               const void* frames, int frames_dtype, int64_t table_rows, int64_t frames_per_slot,
+                               int64_t frame_bytes, int64_t head_bytes, int64_t num_frames, void* out, void* v_new,
+                               float scale, void* stream);
 
 /*
  * gdn_chunk_gated_delta_rule on frame storage with the token log's value rows
@@ -151,9 +152,9 @@ int gdn_chunk_gated_delta_rule(const void* q, const void* k, const void* v, int 
  * arguments of gdn_store_chunk_log: for every token t with log_slots[t] >= 0
  * and 0 <= token_offsets[t] < page_size, v'[t, h, :] goes to the value row
  * (h, position) of that slot's log.  Keys and gates are then stored by
- * gdn_store_chunk_log with v_new = NULL.  Needs dv % 64 == 0, frames of a
- * multiple of 128 bytes and io dtype == state dtype; returns status 2
- * (unsupported, nothing launched) otherwise.
+ * gdn_store_chunk_log with v_new = NULL.  Log slots >= table_rows take no
+ * write.  Needs frames of a multiple of 2 min(dv, 64) bytes and io dtype ==
+ * state dtype; returns status 2 (unsupported, nothing launched) otherwise.
  */
 int gdn_chunk_gated_delta_rule_logged(const void* q, const void* k, const void* v, int io_dtype, const float* g,
                                       const float* beta, const void* cu_seqlens, int cu_dtype, int64_t num_seqs,
@@ -161,9 +162,9 @@ int gdn_chunk_gated_delta_rule_logged(const void* q, const void* k, const void* 
                                       void* state, int state_dtype, int64_t layer, const void* read_slots,
                                       int read_dtype, const void* chunk_write_slots, int chunk_write_dtype,
                                       const void* final_write_slots, int final_write_dtype, int64_t chunk_size,
-                                      const void* frames, int frames_dtype, int64_t frames_per_slot,
-                                      int64_t frame_bytes, int64_t head_bytes, int64_t num_frames,
-                                      const void* log_slots, int log_dtype, const void* token_offsets,
+                                      const void* frames, int frames_dtype, int64_t table_rows,
+                                      int64_t frames_per_slot, int64_t frame_bytes, int64_t head_bytes,
+                                      int64_t num_frames, const void* log_slots, int log_dtype, const void* token_offsets,
                                       int offsets_dtype, int64_t key_heads, int64_t num_layers, int64_t page_size,
                                       void* out, float scale, void* stream);
 
@@ -184,11 +185,13 @@ int gdn_chunk_gated_delta_rule_logged(const void* q, const void* k, const void* 
  * (position / granularity), layer, then keys [key_heads, granularity, dk]
  * and values [HV, granularity, dv]; logical byte x lies in frame
  * frames[slot frames_per_slot + x / frame_bytes] at offset x % frame_bytes
- * (storage = num_frames frames).  Frame entries < 0 or >= num_frames take no
- * write.  v_new and key [T, ., d] contiguous in the storage's 16-bit dtype.
+ * (storage = num_frames frames).  frames and decay_frames have table_rows
+ * rows (slots): a slot >= table_rows, like a frame entry < 0 or >=
+ * num_frames, takes no write.  v_new and key [T, ., d] contiguous in the
+ * storage's 16-bit dtype.
  */
-int gdn_store_chunk_log(void* storage, const void* frames, int frames_dtype, int64_t frames_per_slot,
-                        int64_t frame_bytes, int64_t num_frames, const void* log_slots, int slots_dtype,
+int gdn_store_chunk_log(void* storage, const void* frames, int frames_dtype, int64_t table_rows,
+                        int64_t frames_per_slot, int64_t frame_bytes, int64_t num_frames, const void* log_slots, int slots_dtype,
                         const void* token_offsets, int offsets_dtype, int64_t T, const void* v_new, const void* key,
                         int64_t H, int64_t HV, int64_t dk, int64_t dv, int64_t key_heads, const float* gate,
                         const void* decay_frames, int decay_dtype, int64_t decay_record_bytes, int64_t layer,
@@ -203,16 +206,19 @@ int gdn_store_chunk_log(void* storage, const void* frames, int frames_dtype, int
  * W-1]) goes to the snapshot (token_slots[t], token_granules[t]) when that
  * slot is >= 0, and the last row's window also to granule 0 of
  * final_slots[n] (when final_slots is non-NULL and the slot >= 0).
- * Snapshot addressing as in gdn_conv_decode_logstate.  The conv output
- * itself comes from gdn_packed_causal_conv1d (without state I/O).
+ * Snapshot addressing, table rows and input scales as in
+ * gdn_conv_decode_logstate (inputs are scaled as the conv reads them, the
+ * history is not).  The conv output itself comes from
+ * gdn_packed_causal_conv1d (without state I/O).
  */
 int gdn_conv_windows_logstate(const void* x, int64_t x_row_stride, int64_t x_col_stride, int dtype,
                               const void* history, const void* cu_seqlens, int cu_dtype, int64_t num_seqs,
                               int64_t total_tokens, int64_t channels, int kernel_width, void* storage,
-                              const void* conv_frames, int frames_dtype, int64_t num_granules,
+                              const void* conv_frames, int frames_dtype, int64_t table_rows, int64_t num_granules,
                               int64_t frames_per_granule, int64_t frame_bytes, int64_t num_frames, int64_t layer,
                               const void* token_slots, int slots_dtype, const void* token_granules,
-                              int granules_dtype, const void* final_slots, int finals_dtype, void* stream);
+                              int granules_dtype, const void* final_slots, int finals_dtype, int64_t boundary0,
+                              int64_t boundary1, float scale0, float scale1, float scale2, void* stream);
 
 /*
  * LogState conv decode: replaces conv_decode (kernel/linear_attention/
@@ -224,18 +230,22 @@ int gdn_conv_windows_logstate(const void* x, int64_t x_row_stride, int64_t x_col
  * frame_elems of the storage (F = frames_per_granule; with F == 1,
  * conv_frames[slot G + granule] * frame_elems + e; layout.py:104-112).  The
  * shifted window goes to (write_slots[b], write_granules[b]) and to granule 0
- * of work_slots[b].  A negative slot or an unmapped frame reads zeros and
- * takes no write.  Outputs as gdn_conv_decode; bf16 or f16 storage.
+ * of work_slots[b].  conv_frames has table_rows rows (slots): a negative
+ * slot, a slot >= table_rows or an unmapped frame reads zeros and takes no
+ * write.  Input scales as gdn_conv_decode (the scaled, rounded input also
+ * enters the window).  Outputs as gdn_conv_decode; bf16 or f16 storage.
  */
 int gdn_conv_decode_logstate(const void* x, int64_t x_row_stride, int64_t x_col_stride, int dtype,
                              const void* weight, const void* bias, int kernel_width, int64_t batch, int64_t channels,
-                             void* storage, const void* conv_frames, int frames_dtype, int64_t num_granules,
-                             int64_t frames_per_granule, int64_t frame_bytes, int64_t num_frames, int64_t layer,
+                             void* storage, const void* conv_frames, int frames_dtype, int64_t table_rows,
+                             int64_t num_granules, int64_t frames_per_granule, int64_t frame_bytes,
+                             int64_t num_frames, int64_t layer,
                              const void* read_slots, int read_dtype, const void* read_granules,
                              int read_granules_dtype, const void* write_slots, int write_dtype,
                              const void* write_granules, int write_granules_dtype, const void* work_slots,
                              int work_dtype, void* q_out, void* k_out, void* v_out, int64_t key_dim, int split_qkv,
-                             int round_conv, void* stream);
+                             int round_conv, int64_t boundary0, int64_t boundary1, float scale0, float scale1,
+                             float scale2, void* stream);
 
 /*
  * LogState decode step: replaces fused_recurrent_gated_delta_rule_to_logstate
@@ -254,15 +264,16 @@ int gdn_conv_decode_logstate(const void* x, int64_t x_row_stride, int64_t x_col_
  *   normalised k, decay record float (layer page + p) HV + h = g;
  *   the new state goes to w every step (eager) or when (p + 1) % 16 == 0.
  * The log layout and decay records are those of gdn_store_chunk_log with
- * key_heads = H.  out [B, HV, dv] io dtype.
+ * key_heads = H.  Work and log slots >= table_rows (the rows of both frame
+ * tables) are unmapped, as negative ones.  out [B, HV, dv] io dtype.
  */
 int gdn_recurrent_logstate(const void* q, const void* k, const void* v, int io_dtype, const void* gate,
                            int64_t gate_b_stride, int64_t gate_h_stride, int gate_dtype, const void* beta,
                            int64_t beta_b_stride, int64_t beta_h_stride, int beta_dtype, const void* A_log,
                            int a_dtype, const void* dt_bias, int dt_dtype, int64_t batch, int64_t H, int64_t HV,
                            int64_t dk, int64_t dv, void* storage, const void* payload_frames, int frames_dtype,
-                           int64_t frames_per_slot, int64_t frame_bytes, int64_t head_bytes, int64_t num_frames,
-                           const void* decay_frames, int decay_dtype, int64_t decay_record_bytes,
+                           int64_t table_rows, int64_t frames_per_slot, int64_t frame_bytes, int64_t head_bytes,
+                           int64_t num_frames, const void* decay_frames, int decay_dtype, int64_t decay_record_bytes,
                            const void* work_slots, int work_dtype, const void* log_slots, int log_dtype,
                            const void* token_offsets, int offsets_dtype, const void* replay_counts, int counts_dtype,
                            int64_t layer, int64_t num_layers, int64_t granularity, int64_t page_size, int eager,
@@ -280,10 +291,11 @@ int gdn_recurrent_logstate(const void* q, const void* k, const void* v, int io_d
  * layout of gdn_chunk_gated_delta_rule; dtype bf16 or f16.  Outputs must not
  * be read by another task of the same call.  frame_bytes must hold one logged
  * row (2 max(dk, dv) bytes), so that a row spans at most two frames
- * (GDN_ERR_INVALID otherwise).
+ * (GDN_ERR_INVALID otherwise).  Slots >= table_rows (the rows of both frame
+ * tables) read as zero states, contribute no segment and take no write.
  */
-int gdn_logstate_restore(void* storage, const void* payload_frames, int frames_dtype, int64_t frames_per_slot,
-                         int64_t frame_bytes, int64_t head_bytes, int64_t num_frames, const void* decay_frames,
+int gdn_logstate_restore(void* storage, const void* payload_frames, int frames_dtype, int64_t table_rows,
+                         int64_t frames_per_slot, int64_t frame_bytes, int64_t head_bytes, int64_t num_frames, const void* decay_frames,
                          int decay_dtype, int64_t decay_record_bytes, int64_t num_layers, int64_t HV,
                          int64_t key_heads, int64_t dk, int64_t dv, int64_t granularity, int64_t page_size, int dtype,
                          const int32_t* base_slots, const int32_t* segment_offsets, const int32_t* log_slots,
@@ -293,10 +305,11 @@ int gdn_logstate_restore(void* storage, const void* payload_frames, int frames_d
 /*
  * LogState state copy: replaces copy_states (kernel/linear_attention/logstate.py:118-128
  * -> logstate_construction.cu copy): the states of every layer and value
- * head of sources[i] to destinations[i].
+ * head of sources[i] to destinations[i]; pairs with a slot < 0 or >=
+ * table_rows are skipped.
  */
-int gdn_logstate_copy_states(void* storage, const void* payload_frames, int frames_dtype, int64_t frames_per_slot,
-                             int64_t frame_bytes, int64_t head_bytes, int64_t num_frames, int64_t num_layers,
+int gdn_logstate_copy_states(void* storage, const void* payload_frames, int frames_dtype, int64_t table_rows,
+                             int64_t frames_per_slot, int64_t frame_bytes, int64_t head_bytes, int64_t num_frames, int64_t num_layers,
                              int64_t HV, int64_t dk, int64_t dv, int dtype, const int32_t* sources,
                              const int32_t* destinations, int64_t count, void* stream);
 
@@ -561,6 +574,28 @@ int gdn_metadata_pad(const void* const* srcs, void* const* dsts, const int64_t* 
 int gdn_logstate_prefill_writes(const void* log_slots, int slots_dtype, const void* token_offsets, int offsets_dtype,
                                 const int32_t* plan, void* out, int64_t count, int64_t granularity, void* stream);
 
+/*
+ * Decode slots from the engine's prepared batch packet: replaces
+ * gather_linear_slots (kernel/metadata.py:266-320), which the standard
+ * (layers/linear_attention_backend/standard.py:114-117) and LogState
+ * (logstate.py:113-126) backends call when batch.prepared_indices is set.
+ * Request i has row = table_ids[i] and position = cached_lens[i] of the
+ * [state_rows, state_width] state table (row stride state_row_stride).
+ *   work_table == NULL (standard): out int64 [count, 2] = (state_table[row,
+ *     position - 1], or [row, state_width - 1] when position is 0;
+ *     state_table[row, position]).
+ *   work_table != NULL (LogState): out int32 [4, count] = (work_table[row *
+ *     work_row_stride]; state_table[row, position]; out_loc[i] mod page_size,
+ *     floored; 0).
+ * A row outside [0, state_rows) (or [0, work_rows) for the work slot) or a
+ * position outside [0, state_width) gives -1 slots.
+ */
+int gdn_gather_linear_slots(const void* table_ids, int table_ids_dtype, const void* cached_lens, int cached_dtype,
+                            const void* state_table, int state_dtype, int64_t state_rows, int64_t state_width,
+                            int64_t state_row_stride, const void* work_table, int work_dtype, int64_t work_rows,
+                            int64_t work_row_stride, const void* out_loc, int out_loc_dtype, int64_t page_size,
+                            void* out, int64_t count, void* stream);
+
 /* ------------------------------------------------------------------ output norm */
 
 /*
@@ -612,18 +647,6 @@ int gdn_prefill_fused_noalloc(const void* mixed, int64_t row_stride, int io_dtyp
                               float scale, void* stream);
 /* Bytes of gdn_prefill_fused_noalloc's per-GPU staging array. */
 int64_t gdn_prefill_noalloc_scratch_bytes(void);
-
-/*
- * Measurement probe, no counterpart in the reference: buf[i] <- buf[i] * 1.0
- * in place over `bytes` (16-byte vectors), each block owning `block_bytes`
- * consecutive bytes and each lane keeping `loads_in_flight` (1, 2, 4, 8, 16)
- * 16-byte loads in flight before its stores, optionally non-temporal.  The
- * 1-read:1-write HBM ceiling the decode / verify state updates are read
- * against (bench.py --only rmw).  loads_in_flight 0: a store-only stream
- * (buf[i] <- 1.0, four 16-byte stores per lane per pass), the write ceiling.
- */
-int gdn_probe_rmw(void* buf, int64_t bytes, int64_t block_bytes, int loads_in_flight, int nontemporal,
-                  void* stream);
 
 #ifdef __cplusplus
 }

@@ -40,28 +40,29 @@ SIGNATURES = {
     "gdn_rms_norm_gated": [P, I32, I64, I64, P, I32, I64, I64, I64, I64, P, I32, F32, P, P],
     "gdn_conv_snapshots": [P, I64, I32, P, I32, I64, I64, I64, I32, P, I64, I64, I64, P, I32, P, I32, P, I32, I64,
                            P],
-    "gdn_chunk_gated_delta_rule": [P, P, P, I32, P, P, P, I32, I64, I64, I64, I64, I64, I64, P, I32, I64, I64,
-                                   I64, I64, P, I32, P, I32, P, I32, I64, P, I32, I64, I64, I64, I64, P, P, F32,
-                                   P],
+    "gdn_chunk_gated_delta_rule": [P, P, P, I32, P, P, P, I32, I64, I64, I64, I64, I64, I64, P, I32, I64, I64, I64,
+                                   I64, P, I32, P, I32, P, I32, I64, P, I32, I64, I64, I64, I64, I64, P, P, F32, P],
     "gdn_chunk_gated_delta_rule_logged": [P, P, P, I32, P, P, P, I32, I64, I64, I64, I64, I64, I64, P, I32, I64, P,
-                                          I32, P, I32, P, I32, I64, P, I32, I64, I64, I64, I64, P, I32, P, I32, I64,
-                                          I64, I64, P, F32, P],
-    "gdn_store_chunk_log": [P, P, I32, I64, I64, I64, P, I32, P, I32, I64, P, P, I64, I64, I64, I64, I64, P, P,
+                                          I32, P, I32, P, I32, I64, P, I32, I64, I64, I64, I64, I64, P, I32, P, I32,
+                                          I64, I64, I64, P, F32, P],
+    "gdn_store_chunk_log": [P, P, I32, I64, I64, I64, I64, P, I32, P, I32, I64, P, P, I64, I64, I64, I64, I64, P, P,
                             I32, I64, I64, I64, I64, I64, P],
     "gdn_conv_windows_logstate": [P, I64, I64, I32, P, P, I32, I64, I64, I64, I32, P, P, I32, I64, I64, I64, I64,
-                                  I64, P, I32, P, I32, P, I32, P],
+                                  I64, I64, P, I32, P, I32, P, I32, I64, I64, F32, F32, F32, P],
     "gdn_logstate_copy_conv": [P, P, I32, I64, I64, I64, I64, I64, I64, P, I32, P, I32, P, I32, P, I32, I64, P],
     "gdn_logstate_store_conv": [P, P, I32, I64, I64, I64, I64, I64, P, I32, P, I32, I64, I64, I64, P, P],
     "gdn_logstate_store_states": [P, P, I32, I64, I64, I64, I64, I64, P, I32, I64, I64, I64, I64, P, P],
     "gdn_logstate_prefill_writes": [P, I32, P, I32, P, P, I64, I64, P],
-    "gdn_logstate_restore": [P, P, I32, I64, I64, I64, I64, P, I32, I64, I64, I64, I64, I64, I64, I64, I64, I32, P,
-                             P, P, P, P, P, I64, P],
-    "gdn_logstate_copy_states": [P, P, I32, I64, I64, I64, I64, I64, I64, I64, I64, I32, P, P, I64, P],
-    "gdn_conv_decode_logstate": [P, I64, I64, I32, P, P, I32, I64, I64, P, P, I32, I64, I64, I64, I64, I64, P, I32,
-                                 P, I32, P, I32, P, I32, P, I32, P, P, P, I64, I32, I32, P],
+    "gdn_gather_linear_slots": [P, I32, P, I32, P, I32, I64, I64, I64, P, I32, I64, I64, P, I32, I64, P, I64, P],
+    "gdn_logstate_restore": [P, P, I32, I64, I64, I64, I64, I64, P, I32, I64, I64, I64, I64, I64, I64, I64, I64,
+                             I32, P, P, P, P, P, P, I64, P],
+    "gdn_logstate_copy_states": [P, P, I32, I64, I64, I64, I64, I64, I64, I64, I64, I64, I32, P, P, I64, P],
+    "gdn_conv_decode_logstate": [P, I64, I64, I32, P, P, I32, I64, I64, P, P, I32, I64, I64, I64, I64, I64, I64, P,
+                                 I32, P, I32, P, I32, P, I32, P, I32, P, P, P, I64, I32, I32, I64, I64, F32, F32,
+                                 F32, P],
     "gdn_recurrent_logstate": [P, P, P, I32, P, I64, I64, I32, P, I64, I64, I32, P, I32, P, I32, I64, I64, I64, I64,
-                               I64, P, P, I32, I64, I64, I64, I64, P, I32, I64, P, I32, P, I32, P, I32, P, I32, I64,
-                               I64, I64, I64, I32, P, F32, P],
+                               I64, P, P, I32, I64, I64, I64, I64, I64, P, I32, I64, P, I32, P, I32, P, I32, P, I32,
+                               I64, I64, I64, I64, I32, P, F32, P],
     "gdn_conv_decode": [P, I64, I64, I32, P, P, I32, I64, I64, P, I64, I64, I64, P, I64, I32, P, I64, I32, P,
                         P, P, I64, I32, I32, I64, I64, F32, F32, F32, P],
     "gdn_fused_recurrent": [P, P, P, I32, P, I64, I64, I64, I32, P, I64, I64, I64, I32, P, I32, P, I32, I64,
@@ -76,7 +77,6 @@ SIGNATURES = {
     "gdn_prefill_fused_noalloc": [P, I64, I32, P, I32, P, I32, I64, I64, I64, I64, I64, I64, P, I64, I64, P, I64,
                                   I64, I32, P, I64, I64, I32, P, I32, P, I32, P, I32, I64, I64, I64, I64, P, I32,
                                   P, I32, P, I32, P, I32, I64, P, F32, P],
-    "gdn_probe_rmw": [P, I64, I64, I32, I32, P],
     "gdn_commit_accepted": [P, I64, I64, I64, P, I64, I64, I64, P, I32, P, I64, I64, I32, P, I32, I64, I64, P],
 }
 

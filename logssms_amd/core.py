@@ -44,6 +44,35 @@ class LogStateCacheMetadata:
 
 
 @dataclass
+class BatchIndices:
+    """utils/batch.py:9-32: the fields of the engine's prepared batch packet
+    (``Batch.prepared_indices``) that the linear-attention backends read, all
+    int32 device tensors: per request its table row, cached length, previous
+    position (cached length - 1) and replay count; per token its table row
+    (``token_table_ids``, set by the engine after ``make_batch_mapping``)."""
+
+    table_ids: torch.Tensor
+    cached_lens: torch.Tensor
+    previous_positions: torch.Tensor
+    replay_counts: torch.Tensor
+    token_table_ids: torch.Tensor | None = None
+
+    @classmethod
+    def make(cls, batch: "Batch", device, replay_counts=None) -> "BatchIndices":
+        """The packet of ``batch.padded_reqs`` in one host-to-device copy
+        (utils/batch.py:43-121 builds the same per-request vectors)."""
+        reqs = batch.padded_reqs
+        n = len(reqs)
+        counts = list(replay_counts) if replay_counts is not None else [0] * n
+        assert len(counts) == n
+        host = torch.tensor([r.table_idx for r in reqs] + [r.cached_len for r in reqs] +
+                            [r.cached_len - 1 for r in reqs] + counts, dtype=torch.int32)
+        packet = host.to(device)
+        tables, cached, previous, replay = packet.split(n)
+        return cls(tables, cached, previous, replay)
+
+
+@dataclass
 class Batch:
     reqs: list[Request]
     phase: Literal["prefill", "decode", "verify", "mixed"]
@@ -60,6 +89,8 @@ class Batch:
     # / out_loc), read by the LogState metadata
     positions: torch.Tensor | None = None
     out_loc: torch.Tensor | None = None
+    # the engine's prepared batch packet (core.py:132), or None
+    prepared_indices: BatchIndices | None = None
 
     def __post_init__(self):
         if self.padded_reqs is None:
@@ -144,5 +175,5 @@ def get_global_ctx() -> Context:
     return _GLOBAL_CTX
 
 
-__all__ = ["Batch", "Context", "LogStateCacheMetadata", "MarconiCacheMetadata", "Request", "clear_global_ctx",
+__all__ = ["Batch", "BatchIndices", "Context", "LogStateCacheMetadata", "MarconiCacheMetadata", "Request", "clear_global_ctx",
            "get_global_ctx", "set_global_ctx"]

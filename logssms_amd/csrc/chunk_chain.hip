@@ -248,6 +248,10 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
   const int64_t kh = group % p.H;
   const int64_t h = kh * (p.HV / p.H) + member / p.nvs;
   const int64_t col_base = static_cast<int64_t>(member % p.nvs) * 64;
+  // columns of this slice: 64, or 32 for d_v = 32, where chain waves 2-3 run on
+  // zero columns (zero state, zero V) and store nothing
+  const int vwidth = p.DV - col_base < 64 ? static_cast<int>(p.DV - col_base) : 64;
+  const bool live = 16 * wave < vwidth;
 
   const int64_t bos = uniform_index(p.cu, n, p.cu_is64);
   const int64_t len = uniform_index(p.cu, n + 1, p.cu_is64) - bos;
@@ -277,6 +281,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
   auto slice_base = [&](int64_t s) __attribute__((always_inline)) -> char* {
     if (s < 0) return nullptr;
     if (!EXT || !p.frames) return reinterpret_cast<char*>(pool + s * p.slot_stride + head_off);
+    if (s >= p.frame_slots) return nullptr;  // past the frame table: unmapped
     const int64_t logical = (p.layer * p.HV + h) * p.head_bytes;
     const int64_t fr = uniform_index(p.frames, s * p.fps + logical / p.frame_bytes, p.frames_is64);
     if (fr < 0 || fr >= p.num_frames) return nullptr;
@@ -285,6 +290,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
   // Heads spanning several frames (each frame holds whole 16-row tiles):
   // byte address of element (16 ti, col_base) of slot s, or null.
   auto frame_tile = [&](int64_t s, int ti) __attribute__((always_inline)) -> char* {
+    if (s >= p.frame_slots) return nullptr;
     const int64_t logical = (p.layer * p.HV + h) * p.head_bytes + 16 * ti * row_bytes;
     const int64_t fr = uniform_index(p.frames, s * p.fps + logical / p.frame_bytes, p.frames_is64);
     if (fr < 0 || fr >= p.num_frames) return nullptr;
@@ -296,7 +302,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     return slice ? slice + 16 * ti * row_bytes : nullptr;
   };
   auto load_state = [&]() __attribute__((always_inline)) {
-    const int64_t rs = uniform_index(p.read_slots, n, p.read_is64);
+    const int64_t rs = live ? uniform_index(p.read_slots, n, p.read_is64) : -1;
     char* src = EXT && p.frame_rows ? nullptr : slice_base(rs);
     const uint32_t o = state_lane_off();
 #pragma unroll
@@ -309,6 +315,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
   };
   // Stores tile(ti) (rows 16 ti.., this wave's columns) for every ti to slot s >= 0.
   auto store_tiles = [&](int64_t s, auto&& tile) __attribute__((always_inline)) {
+    if (!live) return;
     char* dst = EXT && p.frame_rows ? nullptr : slice_base(s);
     if (!(EXT && p.frame_rows) && !dst) return;
     const uint32_t o = state_lane_off();
@@ -427,7 +434,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         V[2] = mma(a2, rb1, zero4());
         V[3] = mma(a3, rb1, zero4());
         vb1 = bfrag(V[2], V[3]);
-        if (vng || (EXT && p.logging)) {
+        if (live && (vng || (EXT && p.logging))) {
           // v'^T = R^T A^T: the same fragments with the operands swapped (a
           // B fragment of R is an A fragment of R^T), so lane (g, c) holds
           // columns 4g..4g+3 of token 16 i + c and writes them as 8 bytes,
@@ -482,7 +489,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         asm volatile("" : "+v"(o));
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          if (16 * i + lr < nv) {
+          if (live && 16 * i + lr < nv) {
             uint2 w;
             w.x = out_pack2<IOT>(p.scale * Ot[i][0], p.scale * Ot[i][1]);
             w.y = out_pack2<IOT>(p.scale * Ot[i][2], p.scale * Ot[i][3]);
@@ -747,7 +754,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       aok = p.logging && ok;
     };
     auto resolve_log = [&]() __attribute__((always_inline)) {
-      const bool valid = aok && aslot >= 0 && apos >= 0 && apos < p.log_page;
+      const bool valid = aok && aslot >= 0 && aslot < p.log_rows && apos >= 0 && apos < p.log_page;
       const uint32_t ps = valid ? static_cast<uint32_t>(apos) : 0u;
       const uint32_t g = static_cast<uint32_t>(p.gran), sh = static_cast<uint32_t>(__builtin_ctz(g));
       const uint32_t key_size = g * static_cast<uint32_t>(p.log_key_heads) * DK;
@@ -900,13 +907,15 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     // lane, the fv lane mapping), converted to f16 operands.  Rows past the
     // end are clamped loads, zeroed when staged.
     uint4 pv[4];
+    // columns past a 32-wide slice read the slice's last 8 columns (staged as zeros)
+    const int vcol = 8 * fvdb < vwidth ? 8 * fvdb : vwidth - 8;
     auto prefetch_v = [&](int64_t cv) __attribute__((always_inline)) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int64_t t = cv * kC + VT * fvtb + u;
         const int64_t row = len > 0 ? bos + (t < len ? t : len - 1) : 0;  // a row of the sequence
         pv[u] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.v) + (row * p.HV + h) * p.DV +
-                                                col_base + 8 * fvdb);
+                                                col_base + vcol);
       }
     };
     auto stage_v = [&](int64_t cv) __attribute__((always_inline)) {
@@ -915,7 +924,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const uint4 o = to_f16x8<IOT>(pv[u]);
-        const bool ok = VT * fvtb + u < nk;
+        const bool ok = VT * fvtb + u < nk && 8 * fvdb < vwidth;
         *reinterpret_cast<uint4*>(vd + u * LDV) = make_uint4(ok ? o.x : 0u, ok ? o.y : 0u, ok ? o.z : 0u,
                                                              ok ? o.w : 0u);
       }
@@ -1093,7 +1102,7 @@ int launch_dk(const ChunkParams& p, int io, int st, int64_t groups, hipStream_t 
 
 template <bool FUSED>
 int launch_any(const ChunkParams& p, int64_t dk, int io_dtype, int state_dtype, int64_t groups, hipStream_t stream) {
-  if (p.DV % 64 != 0) return GDN_ERR_UNSUPPORTED;
+  if (p.DV % 64 != 0 && (FUSED || p.DV != 32)) return GDN_ERR_UNSUPPORTED;
   if (dk == 128) return launch_dk<128, FUSED>(p, io_dtype, state_dtype, groups, stream);
   if (dk == 64) return launch_dk<64, FUSED>(p, io_dtype, state_dtype, groups, stream);
   if (dk == 32) return launch_dk<32, FUSED>(p, io_dtype, state_dtype, groups, stream);

@@ -1,5 +1,5 @@
-// Parameters shared by the chunked gated-delta-rule kernels (chunk.hip,
-// chunk_chain.hip).
+// Parameters of the chunked gated-delta-rule kernel (chunk_chain.hip) and its
+// entry points (chunk_entry.hip).
 #pragma once
 
 #include "common.hpp"
@@ -53,6 +53,7 @@ struct ChunkParams {
   const void* frames;
   int frames_is64;
   int frame_rows;
+  int64_t frame_slots;  // rows (slots) of the frame table; slots past it read as unmapped
   int64_t fps, frame_bytes, head_bytes, num_frames;
   // Token log of v' (frame storage, EXT instantiation): with `logging` set,
   // the v' row of token t and value head h goes to the value row (h,
@@ -67,6 +68,7 @@ struct ChunkParams {
   int log_pos_is64;
   const void* log_table;  // the frame table when logging, else the same T words (plain pools have none)
   int log_table_is64;
+  int64_t log_rows;  // rows of the log's frame table; log slots past it take no write
   int64_t log_key_heads, log_layers, log_page;
   Div32 fdiv;  // frame_bytes
 };
@@ -74,10 +76,11 @@ struct ChunkParams {
 // Host-side validation of a frame-table state layout; returns GDN_OK or sets
 // the error and returns GDN_ERR_INVALID.  Fills the frame fields of p.
 int set_frame_layout(ChunkParams& p, int64_t dk, int state_dtype, const void* frames, int frames_dtype,
-                     int64_t frames_per_slot, int64_t frame_bytes, int64_t head_bytes, int64_t num_frames);
+                     int64_t frames_per_slot, int64_t frame_bytes, int64_t head_bytes, int64_t num_frames,
+                     int64_t table_rows);
 
-// Register-chain kernel (chunk_chain.hip) for d_k in {32, 64, 128} and d_v a
-// multiple of 64.  Returns GDN_ERR_UNSUPPORTED (without setting an error) for
+// Register-chain kernel (chunk_chain.hip) for d_k in {32, 64, 128} and d_v 32
+// or a multiple of 64 (the fused variant: a multiple of 64).  Returns GDN_ERR_UNSUPPORTED (without setting an error) for
 // shapes or dtypes it does not cover, so the caller can use another kernel.
 int launch_chunk_chain(const ChunkParams& p, int64_t dk, int io_dtype, int state_dtype, int64_t groups,
                        hipStream_t stream);

@@ -40,6 +40,7 @@ struct LogParams {
   char* storage;
   const void* frames;
   int frames_is64;
+  int64_t rows;  // slots in the payload and decay frame tables
   int64_t fps, frame_bytes, num_frames;
   const void* slots;
   int slots_is64;
@@ -77,7 +78,7 @@ __global__ __launch_bounds__(kThreads) void chunk_log_kernel(LogParams p) {
   const int64_t t = blockIdx.x, h = blockIdx.y;
   const int64_t slot = load_index(p.slots, t, p.slots_is64);
   const int64_t pos = load_index(p.offsets, t, p.offsets_is64);
-  if (slot < 0 || pos < 0 || pos >= p.page) return;
+  if (slot < 0 || slot >= p.rows || pos < 0 || pos >= p.page) return;
   if (p.v_new) {  // null: the value rows were written by the chunk kernel
     const uint16_t* vrow = p.v_new + (t * p.HV + h) * p.V;
     for (int64_t col = threadIdx.x; col < p.V; col += kThreads) {
@@ -112,7 +113,7 @@ __global__ __launch_bounds__(kLogThreads) void chunk_log_vec_kernel(LogParams p)
   const int64_t t = blockIdx.x;
   const int64_t slot = load_index(p.slots, t, p.slots_is64);
   const int64_t pos = load_index(p.offsets, t, p.offsets_is64);
-  if (slot < 0 || pos < 0 || pos >= p.page) return;
+  if (slot < 0 || slot >= p.rows || pos < 0 || pos >= p.page) return;
   const int64_t vv = p.V / 8, kv = p.K / 8;
   const int64_t group = p.HV / p.KH;  // value heads per logged key head
   const int64_t nval = p.v_new ? p.HV * vv : 0;  // no value rows: written by the chunk kernel
@@ -142,9 +143,10 @@ constexpr int kDecodeThreads = 256;
 // Element e of the conv snapshot of (slot, granule), or null when unmapped
 // (layout.py:104-112).
 template <class T>
-__device__ __forceinline__ T* conv_element(T* storage, const void* table, int is64, int64_t slot, int64_t granule,
-                                           int64_t e, int64_t granules, int64_t cf, int64_t fe, int64_t num_frames) {
-  if (slot < 0) return nullptr;
+__device__ __forceinline__ T* conv_element(T* storage, const void* table, int is64, int64_t rows, int64_t slot,
+                                           int64_t granule, int64_t e, int64_t granules, int64_t cf, int64_t fe,
+                                           int64_t num_frames) {
+  if (slot < 0 || slot >= rows) return nullptr;
   const int64_t row = slot * granules + granule;
   if (cf == 1) {
     const int64_t fr = load_index(table, row, is64);
@@ -168,6 +170,7 @@ struct ConvFrameParams {
   void* storage;
   const void* table;
   int table_is64;
+  int64_t rows;  // slots of the conv frame table
   int64_t granules, cf, fe, num_frames, layer;
   const void* reads; int reads_is64;
   const void* rgran; int rgran_is64;
@@ -177,6 +180,8 @@ struct ConvFrameParams {
   void* q; void* k; void* v;
   int64_t key_dim;
   int split, round_conv;
+  int64_t end0, end1;  // input scales: s0 below channel end0, s1 below end1, s2 after
+  float s0, s1, s2;
 };
 
 // grid (channel blocks, batch); one thread per channel.
@@ -191,12 +196,16 @@ __global__ __launch_bounds__(kDecodeThreads) void conv_decode_frames_kernel(Conv
   const int64_t rs = load_index(p.reads, b, p.reads_is64), rg = load_index(p.rgran, b, p.rgran_is64);
   float win[8];
   for (int i = 0; i < S; ++i) {
-    const T* src = conv_element(st, p.table, p.table_is64, rs, rg, e0 + i, p.granules, p.cf, p.fe, p.num_frames);
+    const T* src =
+        conv_element(st, p.table, p.table_is64, p.rows, rs, rg, e0 + i, p.granules, p.cf, p.fe, p.num_frames);
     win[i] = src ? to_f32(*src) : 0.f;
   }
   const T* x = static_cast<const T*>(p.x);
   const T* w = static_cast<const T*>(p.weight);
-  const float xv = to_f32(x[b * p.xr + ch * p.xc]);
+  const float sc = ch < p.end0 ? p.s0 : (ch < p.end1 ? p.s1 : p.s2);
+  const float x0 = to_f32(x[b * p.xr + ch * p.xc]);
+  // a scaled input is rounded to the io type, and the window keeps it scaled
+  const float xv = sc != 1.f ? round_to<T>(x0 * sc) : x0;
   float acc = 0.f;
   for (int i = 0; i < S; ++i) acc = fmaf(to_f32(w[ch * p.W + i]), win[i], acc);
   acc = fmaf(to_f32(w[ch * p.W + S]), xv, acc);
@@ -207,8 +216,8 @@ __global__ __launch_bounds__(kDecodeThreads) void conv_decode_frames_kernel(Conv
   const int64_t wk = load_index(p.works, b, p.works_is64);
   for (int i = 0; i < S; ++i) {
     const T val = from_f32<T>(i + 1 < S ? win[i + 1] : xv);
-    T* d0 = conv_element(st, p.table, p.table_is64, ws, wg, e0 + i, p.granules, p.cf, p.fe, p.num_frames);
-    T* d1 = conv_element(st, p.table, p.table_is64, wk, 0, e0 + i, p.granules, p.cf, p.fe, p.num_frames);
+    T* d0 = conv_element(st, p.table, p.table_is64, p.rows, ws, wg, e0 + i, p.granules, p.cf, p.fe, p.num_frames);
+    T* d1 = conv_element(st, p.table, p.table_is64, p.rows, wk, 0, e0 + i, p.granules, p.cf, p.fe, p.num_frames);
     if (d0) *d0 = val;
     if (d1) *d1 = val;
   }
@@ -238,10 +247,13 @@ struct ConvWindowParams {
   int S;
   void* storage;
   const void* table; int table_is64;
+  int64_t rows;  // slots of the conv frame table
   int64_t granules, cf, fe, num_frames, layer;
   const void* slots; int slots_is64;
   const void* gran; int gran_is64;
   const void* finals; int finals_is64;
+  int64_t end0, end1;  // input scales, as ConvFrameParams
+  float s0, s1, s2;
 };
 
 // grid (T, channel blocks)
@@ -260,11 +272,16 @@ __global__ __launch_bounds__(kDecodeThreads) void conv_windows_frames_kernel(Con
   const T* hist = static_cast<const T*>(p.history) + (n * p.C + ch) * p.S;
   T* st = static_cast<T*>(p.storage);
   const int64_t e0 = p.layer * p.C * p.S + ch * p.S;
+  const float sc = ch < p.end0 ? p.s0 : (ch < p.end1 ? p.s1 : p.s2);
   for (int j = 0; j < p.S; ++j) {
     const int64_t pos = t - (p.S - 1) + j;
-    const T v = pos >= begin ? x[pos * p.xr + ch * p.xc] : hist[pos - begin + p.S];
-    T* d0 = conv_element(st, p.table, p.table_is64, slot, granule, e0 + j, p.granules, p.cf, p.fe, p.num_frames);
-    T* d1 = conv_element(st, p.table, p.table_is64, fin, 0, e0 + j, p.granules, p.cf, p.fe, p.num_frames);
+    // inputs are scaled (and rounded) as the conv reads them; the history is not
+    const T v = pos >= begin ? (sc != 1.f ? from_f32<T>(to_f32(x[pos * p.xr + ch * p.xc]) * sc)
+                                          : x[pos * p.xr + ch * p.xc])
+                             : hist[pos - begin + p.S];
+    T* d0 = conv_element(st, p.table, p.table_is64, p.rows, slot, granule, e0 + j, p.granules, p.cf, p.fe,
+                         p.num_frames);
+    T* d1 = conv_element(st, p.table, p.table_is64, p.rows, fin, 0, e0 + j, p.granules, p.cf, p.fe, p.num_frames);
     if (d0) *d0 = v;
     if (d1) *d1 = v;
   }
@@ -279,6 +296,7 @@ struct LogDecodeParams {
   int64_t H, HV;
   char* storage;
   const void* frames; int frames_is64;
+  int64_t rows;  // slots of the payload and decay frame tables
   int64_t fps, frame_bytes, head_bytes, num_frames;
   const void* decay; int decay_is64;
   int64_t record_bytes;
@@ -540,8 +558,10 @@ __global__ __launch_bounds__((DecodeShape<DK, DV>::NT)) __attribute__((amdgpu_wa
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
 
   // ---- the sequence's slots, read by every wave (uniform)
-  const int w = static_cast<int>(load_index(p.work, b, p.work_is64));
-  const int ls = static_cast<int>(load_index(p.logs, b, p.logs_is64));
+  // slots past the frame tables are unmapped, as negative ones
+  const int64_t w_raw = load_index(p.work, b, p.work_is64), ls_raw = load_index(p.logs, b, p.logs_is64);
+  const int w = w_raw < p.rows ? static_cast<int>(w_raw) : -1;
+  const int ls = ls_raw < p.rows ? static_cast<int>(ls_raw) : -1;
   const int pos = static_cast<int>(load_index(p.offsets, b, p.offsets_is64));
   const bool in_page = ls >= 0 && pos >= 0 && pos < p.page;
   int n = p.eager || !in_page ? 0 : static_cast<int>(load_index(p.counts, b, p.counts_is64));
@@ -949,6 +969,7 @@ __global__ __launch_bounds__((DecodeShape<DK, DV>::NT)) __attribute__((amdgpu_wa
 struct RestoreParams {
   char* storage;
   const void* frames; int frames_is64;
+  int64_t rows;  // slots of the payload and decay frame tables
   int64_t fps, frame_bytes, head_bytes, num_frames;
   const void* decay; int decay_is64;
   int64_t record_bytes;
@@ -967,7 +988,7 @@ struct RestoreParams {
 template <class T>
 __device__ __forceinline__ T* slot_row(const RestoreParams& p, int64_t s, int64_t layer, int64_t h, int64_t row,
                                        int DV) {
-  if (s < 0) return nullptr;
+  if (s < 0 || s >= p.rows) return nullptr;
   const uint32_t x = static_cast<uint32_t>((layer * p.HV + h) * p.head_bytes + row * DV * static_cast<int64_t>(sizeof(T)));
   const int64_t fr = load_index(p.frames, s * p.fps + p.fdiv.div(x), p.frames_is64);
   if (fr < 0 || fr >= p.num_frames) return nullptr;
@@ -1148,7 +1169,7 @@ __global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(
     const int64_t begin = p.seg_begin[seg] < 0 ? 0 : p.seg_begin[seg];
     const int64_t end = p.seg_end[seg] < p.page ? p.seg_end[seg] : p.page;
     int64_t fr = -1, ri = -1;
-    if (ls >= 0 && begin < end) {
+    if (ls >= 0 && ls < p.rows && begin < end) {
       fr = load_index(p.decay, 2 * ls, p.decay_is64);
       ri = load_index(p.decay, 2 * ls + 1, p.decay_is64);
     }
@@ -1307,7 +1328,8 @@ __global__ __launch_bounds__(kDecodeThreads) void copy_states_kernel(RestorePara
 }  // namespace
 }  // namespace gdn
 
-extern "C" int gdn_store_chunk_log(void* storage, const void* frames, int frames_dtype, int64_t frames_per_slot,
+extern "C" int gdn_store_chunk_log(void* storage, const void* frames, int frames_dtype, int64_t table_rows,
+                                   int64_t frames_per_slot,
                                    int64_t frame_bytes, int64_t num_frames, const void* log_slots, int slots_dtype,
                                    const void* token_offsets, int offsets_dtype, int64_t T, const void* v_new,
                                    const void* key, int64_t H, int64_t HV, int64_t dk, int64_t dv, int64_t key_heads,
@@ -1323,7 +1345,7 @@ extern "C" int gdn_store_chunk_log(void* storage, const void* frames, int frames
                   page_size % granularity == 0,
               "gdn_store_chunk_log: bad layout (layer %lld of %lld, granularity %lld, page %lld)", (long long)layer,
               (long long)num_layers, (long long)granularity, (long long)page_size);
-  GDN_REQUIRE(frames_per_slot > 0 && frame_bytes > 0 && frame_bytes % 4 == 0 && num_frames > 0,
+  GDN_REQUIRE(frames_per_slot > 0 && frame_bytes > 0 && frame_bytes % 4 == 0 && num_frames > 0 && table_rows >= 0,
               "gdn_store_chunk_log: bad frame table");
   const int64_t log_bytes = 2 * page_size * num_layers * (key_heads * dk + HV * dv);
   GDN_REQUIRE(frames_per_slot * frame_bytes < kMaxOffset32, "gdn_store_chunk_log: a slot's frames exceed 4 GiB");
@@ -1340,7 +1362,7 @@ extern "C" int gdn_store_chunk_log(void* storage, const void* frames, int frames
   GDN_REQUIRE(T <= 0x7fffffff && HV <= 65535, "gdn_store_chunk_log: grid too large");
   LogParams p{};
   p.storage = static_cast<char*>(storage);
-  p.frames = frames; p.frames_is64 = frames_dtype == GDN_I64;
+  p.frames = frames; p.frames_is64 = frames_dtype == GDN_I64; p.rows = table_rows;
   p.fps = frames_per_slot; p.frame_bytes = frame_bytes; p.num_frames = num_frames;
   p.slots = log_slots; p.slots_is64 = slots_dtype == GDN_I64;
   p.offsets = token_offsets; p.offsets_is64 = offsets_dtype == GDN_I64;
@@ -1366,13 +1388,15 @@ extern "C" int gdn_store_chunk_log(void* storage, const void* frames, int frames
 extern "C" int gdn_conv_decode_logstate(const void* x, int64_t x_row_stride, int64_t x_col_stride, int dtype,
                                         const void* weight, const void* bias, int kernel_width, int64_t batch,
                                         int64_t channels, void* storage, const void* conv_frames, int frames_dtype,
-                                        int64_t num_granules, int64_t frames_per_granule, int64_t frame_bytes,
+                                        int64_t table_rows, int64_t num_granules, int64_t frames_per_granule,
+                                        int64_t frame_bytes,
                                         int64_t num_frames, int64_t layer, const void* read_slots, int read_dtype,
                                         const void* read_granules, int read_granules_dtype,
                                         const void* write_slots, int write_dtype, const void* write_granules,
                                         int write_granules_dtype, const void* work_slots, int work_dtype,
                                         void* q_out, void* k_out, void* v_out, int64_t key_dim, int split_qkv,
-                                        int round_conv, void* stream) {
+                                        int round_conv, int64_t boundary0, int64_t boundary1, float scale0,
+                                        float scale1, float scale2, void* stream) {
   using namespace gdn;
   GDN_REQUIRE(batch >= 0 && channels > 0 && layer >= 0, "gdn_conv_decode_logstate: bad sizes");
   if (batch == 0) return GDN_OK;
@@ -1382,8 +1406,10 @@ extern "C" int gdn_conv_decode_logstate(const void* x, int64_t x_row_stride, int
                   work_slots && q_out,
               "gdn_conv_decode_logstate: null input");
   GDN_REQUIRE(!split_qkv || (k_out && v_out && 2 * key_dim < channels), "gdn_conv_decode_logstate: bad split");
-  GDN_REQUIRE(num_granules > 0 && frames_per_granule > 0 && num_frames > 0 && frame_bytes > 0,
+  GDN_REQUIRE(num_granules > 0 && frames_per_granule > 0 && num_frames > 0 && frame_bytes > 0 && table_rows >= 0,
               "gdn_conv_decode_logstate: bad conv frame table");
+  GDN_REQUIRE(0 <= boundary0 && boundary0 <= boundary1 && boundary1 <= channels,
+              "gdn_conv_decode_logstate: bad input scale boundaries");
   const int64_t elt = dtype == GDN_F32 ? 4 : 2;
   GDN_REQUIRE(frame_bytes % elt == 0, "gdn_conv_decode_logstate: frame_bytes %lld not a multiple of the element",
               (long long)frame_bytes);
@@ -1396,7 +1422,9 @@ extern "C" int gdn_conv_decode_logstate(const void* x, int64_t x_row_stride, int
   ConvFrameParams p{};
   p.x = x; p.xr = x_row_stride; p.xc = x_col_stride; p.weight = weight; p.bias = bias; p.W = kernel_width;
   p.C = channels; p.storage = storage; p.table = conv_frames; p.table_is64 = frames_dtype == GDN_I64;
+  p.rows = table_rows;
   p.granules = num_granules; p.cf = frames_per_granule; p.fe = fe; p.num_frames = num_frames; p.layer = layer;
+  p.end0 = boundary0; p.end1 = boundary1; p.s0 = scale0; p.s1 = scale1; p.s2 = scale2;
   p.reads = read_slots; p.reads_is64 = read_dtype == GDN_I64;
   p.rgran = read_granules; p.rgran_is64 = read_granules_dtype == GDN_I64;
   p.writes = write_slots; p.writes_is64 = write_dtype == GDN_I64;
@@ -1421,7 +1449,8 @@ extern "C" int gdn_recurrent_logstate(
     int64_t gate_h_stride, int gate_dtype, const void* beta, int64_t beta_b_stride, int64_t beta_h_stride,
     int beta_dtype, const void* A_log, int a_dtype, const void* dt_bias, int dt_dtype, int64_t batch, int64_t H,
     int64_t HV, int64_t dk, int64_t dv, void* storage, const void* payload_frames, int frames_dtype,
-    int64_t frames_per_slot, int64_t frame_bytes, int64_t head_bytes, int64_t num_frames, const void* decay_frames,
+    int64_t table_rows, int64_t frames_per_slot, int64_t frame_bytes, int64_t head_bytes, int64_t num_frames,
+    const void* decay_frames,
     int decay_dtype, int64_t decay_record_bytes, const void* work_slots, int work_dtype, const void* log_slots,
     int log_dtype, const void* token_offsets, int offsets_dtype, const void* replay_counts, int counts_dtype,
     int64_t layer, int64_t num_layers, int64_t granularity, int64_t page_size, int eager, void* out, float scale,
@@ -1438,7 +1467,7 @@ extern "C" int gdn_recurrent_logstate(
               "gdn_recurrent_logstate: bad layout");
   const int64_t row = dv * 2;
   GDN_REQUIRE(frames_per_slot > 0 && frame_bytes > 0 && num_frames > 0 && frame_bytes % 16 == 0 &&
-                  head_bytes >= dk * row && head_bytes % 16 == 0 && aligned16(storage),
+                  head_bytes >= dk * row && head_bytes % 16 == 0 && aligned16(storage) && table_rows >= 0,
               "gdn_recurrent_logstate: bad frame layout (frame and head bytes must be multiples of 16, the "
               "storage 16-byte aligned)");
   GDN_REQUIRE(head_bytes <= frame_bytes ? frame_bytes % head_bytes == 0
@@ -1461,7 +1490,7 @@ extern "C" int gdn_recurrent_logstate(
   p.A_log = A_log; p.a_dtype = a_dtype; p.dt_bias = dt_bias; p.dt_dtype = dt_dtype;
   p.H = H; p.HV = HV;
   p.storage = static_cast<char*>(storage);
-  p.frames = payload_frames; p.frames_is64 = frames_dtype == GDN_I64;
+  p.frames = payload_frames; p.frames_is64 = frames_dtype == GDN_I64; p.rows = table_rows;
   p.fps = frames_per_slot; p.frame_bytes = frame_bytes; p.head_bytes = head_bytes; p.num_frames = num_frames;
   p.decay = decay_frames; p.decay_is64 = decay_dtype == GDN_I64; p.record_bytes = decay_record_bytes;
   p.work = work_slots; p.work_is64 = work_dtype == GDN_I64;
@@ -1503,11 +1532,13 @@ extern "C" int gdn_recurrent_logstate(
 extern "C" int gdn_conv_windows_logstate(const void* x, int64_t x_row_stride, int64_t x_col_stride, int dtype,
                                          const void* history, const void* cu_seqlens, int cu_dtype, int64_t num_seqs,
                                          int64_t total_tokens, int64_t channels, int kernel_width, void* storage,
-                                         const void* conv_frames, int frames_dtype, int64_t num_granules,
+                                         const void* conv_frames, int frames_dtype, int64_t table_rows,
+                                         int64_t num_granules,
                                          int64_t frames_per_granule, int64_t frame_bytes, int64_t num_frames,
                                          int64_t layer, const void* token_slots, int slots_dtype,
                                          const void* token_granules, int granules_dtype, const void* final_slots,
-                                         int finals_dtype, void* stream) {
+                                         int finals_dtype, int64_t boundary0, int64_t boundary1, float scale0,
+                                         float scale1, float scale2, void* stream) {
   using namespace gdn;
   GDN_REQUIRE(num_seqs >= 1 && total_tokens >= 0 && channels > 0 && layer >= 0,
               "gdn_conv_windows_logstate: bad sizes");
@@ -1516,8 +1547,11 @@ extern "C" int gdn_conv_windows_logstate(const void* x, int64_t x_row_stride, in
               kernel_width);
   GDN_REQUIRE(x && history && cu_seqlens && storage && conv_frames && token_slots && token_granules,
               "gdn_conv_windows_logstate: null input");
-  GDN_REQUIRE(num_granules > 0 && frames_per_granule > 0 && num_frames > 0 && frame_bytes > 0 && frame_bytes % 2 == 0,
+  GDN_REQUIRE(num_granules > 0 && frames_per_granule > 0 && num_frames > 0 && frame_bytes > 0 &&
+                  frame_bytes % 2 == 0 && table_rows >= 0,
               "gdn_conv_windows_logstate: bad conv frame table");
+  GDN_REQUIRE(0 <= boundary0 && boundary0 <= boundary1 && boundary1 <= channels,
+              "gdn_conv_windows_logstate: bad input scale boundaries");
   const int64_t fe = frame_bytes / 2;
   const int64_t span = (layer + 1) * channels * (kernel_width - 1);
   GDN_REQUIRE(frames_per_granule == 1 ? span <= fe : span <= frames_per_granule * fe,
@@ -1529,8 +1563,9 @@ extern "C" int gdn_conv_windows_logstate(const void* x, int64_t x_row_stride, in
   p.x = x; p.xr = x_row_stride; p.xc = x_col_stride; p.history = history;
   p.cu = cu_seqlens; p.cu_is64 = cu_dtype == GDN_I64;
   p.N = num_seqs; p.T = total_tokens; p.C = channels; p.S = kernel_width - 1;
-  p.storage = storage; p.table = conv_frames; p.table_is64 = frames_dtype == GDN_I64;
+  p.storage = storage; p.table = conv_frames; p.table_is64 = frames_dtype == GDN_I64; p.rows = table_rows;
   p.granules = num_granules; p.cf = frames_per_granule; p.fe = fe; p.num_frames = num_frames; p.layer = layer;
+  p.end0 = boundary0; p.end1 = boundary1; p.s0 = scale0; p.s1 = scale1; p.s2 = scale2;
   p.slots = token_slots; p.slots_is64 = slots_dtype == GDN_I64;
   p.gran = token_granules; p.gran_is64 = granules_dtype == GDN_I64;
   p.finals = final_slots; p.finals_is64 = finals_dtype == GDN_I64;
@@ -1552,11 +1587,11 @@ namespace gdn {
 namespace {
 
 int restore_setup(RestoreParams& p, void* storage, const void* payload_frames, int frames_dtype,
-                  int64_t frames_per_slot, int64_t frame_bytes, int64_t head_bytes, int64_t num_frames,
+                  int64_t table_rows, int64_t frames_per_slot, int64_t frame_bytes, int64_t head_bytes, int64_t num_frames,
                   const void* decay_frames, int decay_dtype, int64_t record_bytes, int64_t layers, int64_t HV,
                   int64_t KH, int64_t dk, int64_t dv, int64_t granularity, int64_t page_size, const char* who) {
   GDN_REQUIRE(layers > 0 && HV > 0 && KH > 0 && HV % KH == 0 && granularity > 0 && page_size > 0 &&
-                  page_size % granularity == 0,
+                  page_size % granularity == 0 && table_rows >= 0,
               "%s: bad layout", who);
   const int64_t row = dv * 2;
   GDN_REQUIRE(frames_per_slot > 0 && frame_bytes > 0 && num_frames > 0 && frame_bytes % 16 == 0 &&
@@ -1575,7 +1610,7 @@ int restore_setup(RestoreParams& p, void* storage, const void* payload_frames, i
   GDN_REQUIRE(record_bytes % 4 == 0 && record_bytes >= 4 * layers * page_size * HV && record_bytes <= frame_bytes,
               "%s: bad decay record size", who);
   p.storage = static_cast<char*>(storage);
-  p.frames = payload_frames; p.frames_is64 = frames_dtype == GDN_I64;
+  p.frames = payload_frames; p.frames_is64 = frames_dtype == GDN_I64; p.rows = table_rows;
   p.fps = frames_per_slot; p.frame_bytes = frame_bytes; p.head_bytes = head_bytes; p.num_frames = num_frames;
   p.decay = decay_frames; p.decay_is64 = decay_dtype == GDN_I64; p.record_bytes = record_bytes;
   p.layers = layers; p.HV = HV; p.KH = KH; p.gran = granularity; p.page = page_size;
@@ -1627,7 +1662,7 @@ int launch_state_kernel(const RestoreParams& p, int64_t blocks, int64_t dk, int6
 }  // namespace gdn
 
 extern "C" int gdn_logstate_restore(void* storage, const void* payload_frames, int frames_dtype,
-                                    int64_t frames_per_slot, int64_t frame_bytes, int64_t head_bytes,
+                                    int64_t table_rows, int64_t frames_per_slot, int64_t frame_bytes, int64_t head_bytes,
                                     int64_t num_frames, const void* decay_frames, int decay_dtype,
                                     int64_t decay_record_bytes, int64_t num_layers, int64_t HV, int64_t key_heads,
                                     int64_t dk, int64_t dv, int64_t granularity, int64_t page_size, int dtype,
@@ -1641,7 +1676,7 @@ extern "C" int gdn_logstate_restore(void* storage, const void* payload_frames, i
                   log_begins && log_ends && output_slots,
               "gdn_logstate_restore: null input");
   RestoreParams p{};
-  int rc = restore_setup(p, storage, payload_frames, frames_dtype, frames_per_slot, frame_bytes, head_bytes,
+  int rc = restore_setup(p, storage, payload_frames, frames_dtype, table_rows, frames_per_slot, frame_bytes, head_bytes,
                          num_frames, decay_frames, decay_dtype, decay_record_bytes, num_layers, HV, key_heads, dk, dv,
                          granularity, page_size, "gdn_logstate_restore");
   if (rc != GDN_OK) return rc;
@@ -1656,7 +1691,7 @@ extern "C" int gdn_logstate_restore(void* storage, const void* payload_frames, i
 }
 
 extern "C" int gdn_logstate_copy_states(void* storage, const void* payload_frames, int frames_dtype,
-                                        int64_t frames_per_slot, int64_t frame_bytes, int64_t head_bytes,
+                                        int64_t table_rows, int64_t frames_per_slot, int64_t frame_bytes, int64_t head_bytes,
                                         int64_t num_frames, int64_t num_layers, int64_t HV, int64_t dk, int64_t dv,
                                         int dtype, const int32_t* sources, const int32_t* destinations,
                                         int64_t count, void* stream) {
@@ -1665,7 +1700,7 @@ extern "C" int gdn_logstate_copy_states(void* storage, const void* payload_frame
   if (count == 0) return GDN_OK;
   GDN_REQUIRE(storage && payload_frames && sources && destinations, "gdn_logstate_copy_states: null input");
   GDN_REQUIRE(num_layers > 0 && HV > 0 && frames_per_slot > 0 && frame_bytes > 0 && num_frames > 0 &&
-                  head_bytes >= dk * dv * 2 &&
+                  table_rows >= 0 && head_bytes >= dk * dv * 2 &&
                   (head_bytes <= frame_bytes ? frame_bytes % head_bytes == 0
                                              : head_bytes % frame_bytes == 0 && frame_bytes % (dv * 2) == 0) &&
                   num_layers * HV * head_bytes <= frames_per_slot * frame_bytes &&
@@ -1673,7 +1708,7 @@ extern "C" int gdn_logstate_copy_states(void* storage, const void* payload_frame
               "gdn_logstate_copy_states: bad frame layout");
   RestoreParams p{};
   p.storage = static_cast<char*>(storage);
-  p.frames = payload_frames; p.frames_is64 = frames_dtype == GDN_I64;
+  p.frames = payload_frames; p.frames_is64 = frames_dtype == GDN_I64; p.rows = table_rows;
   p.fps = frames_per_slot; p.frame_bytes = frame_bytes; p.head_bytes = head_bytes; p.num_frames = num_frames;
   p.layers = num_layers; p.HV = HV; p.KH = 1;
   p.fdiv = make_div32(frame_bytes); p.gdiv = make_div32(1);

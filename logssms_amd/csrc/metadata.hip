@@ -188,3 +188,68 @@ extern "C" int gdn_logstate_prefill_writes(const void* log_slots, int slots_dtyp
                      slots_dtype == GDN_I64, count, granularity);
   return GDN_LAUNCH_CHECK("gdn_logstate_prefill_writes");
 }
+
+// Decode slots from the engine's prepared batch packet (kernel/metadata.py:
+// 266-320, gather_linear_slots): per request i, row = table_ids[i] and
+// position = cached_lens[i] of the state table (and, for LogState, the work
+// table and the request's KV location).
+//   standard: out int64 [count, 2] = (state_table[row, position - 1, or the
+//     row's last column when position is 0], state_table[row, position]);
+//   LogState: out int32 [4, count] = (work_table[row, 0],
+//     state_table[row, position], out_loc[i] mod page_size (floored), 0).
+// A row outside the tables or a position outside [0, width) gives -1 slots.
+namespace gdn {
+namespace {
+
+__global__ __launch_bounds__(kThreads) void gather_linear_slots_kernel(
+    const void* tables, int tables_is64, const void* cached, int cached_is64, const void* state, int state_is64,
+    int64_t rows, int64_t state_stride, int64_t width, const void* work, int work_is64, int64_t work_rows,
+    int64_t work_stride, const void* out_loc, int loc_is64, int64_t page_size, void* out, int64_t count) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= count) return;
+  const int64_t row = load_index(tables, i, tables_is64);
+  const int64_t pos = load_index(cached, i, cached_is64);
+  const bool ok = row >= 0 && row < rows && pos >= 0 && pos < width;
+  const int64_t now = ok ? load_index(state, row * state_stride + pos, state_is64) : -1;
+  if (work) {
+    int32_t* o = static_cast<int32_t*>(out);
+    const int64_t loc = load_index(out_loc, i, loc_is64);
+    const int64_t r = loc % page_size;
+    const bool wok = row >= 0 && row < work_rows;
+    o[i] = wok ? static_cast<int32_t>(load_index(work, row * work_stride, work_is64)) : -1;
+    o[count + i] = static_cast<int32_t>(now);
+    o[2 * count + i] = static_cast<int32_t>(r < 0 ? r + page_size : r);
+    o[3 * count + i] = 0;
+  } else {
+    int64_t* o = static_cast<int64_t*>(out);
+    o[2 * i] = ok ? load_index(state, row * state_stride + (pos > 0 ? pos - 1 : width - 1), state_is64) : -1;
+    o[2 * i + 1] = now;
+  }
+}
+
+}  // namespace
+}  // namespace gdn
+
+extern "C" int gdn_gather_linear_slots(const void* table_ids, int table_ids_dtype, const void* cached_lens,
+                                       int cached_dtype, const void* state_table, int state_dtype,
+                                       int64_t state_rows, int64_t state_width, int64_t state_row_stride,
+                                       const void* work_table, int work_dtype, int64_t work_rows,
+                                       int64_t work_row_stride,
+                                       const void* out_loc, int out_loc_dtype, int64_t page_size, void* out,
+                                       int64_t count, void* stream) {
+  using namespace gdn;
+  GDN_REQUIRE(count >= 0 && state_rows > 0 && state_width > 0 && state_row_stride >= state_width,
+              "gdn_gather_linear_slots: bad sizes");
+  if (count == 0) return GDN_OK;
+  GDN_REQUIRE(table_ids && cached_lens && state_table && out, "gdn_gather_linear_slots: null input");
+  GDN_REQUIRE(!work_table || (out_loc && page_size > 0 && work_row_stride > 0),
+              "gdn_gather_linear_slots: LogState slots need the work table, out_loc and the page size");
+  const int64_t blocks = (count + kThreads - 1) / kThreads;
+  GDN_REQUIRE(blocks <= 0x7fffffff, "gdn_gather_linear_slots: too many requests");
+  hipLaunchKernelGGL(gather_linear_slots_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), table_ids, table_ids_dtype == GDN_I64, cached_lens,
+                     cached_dtype == GDN_I64, state_table, state_dtype == GDN_I64, state_rows, state_row_stride,
+                     state_width, work_table, work_dtype == GDN_I64, work_rows, work_row_stride, out_loc,
+                     out_loc_dtype == GDN_I64, page_size, out, count);
+  return GDN_LAUNCH_CHECK("gdn_gather_linear_slots");
+}

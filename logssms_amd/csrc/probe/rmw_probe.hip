@@ -1,12 +1,41 @@
 // Bandwidth probe for the HBM-bound kernels: an in-place read-modify-write
 // stream (x <- a x over 16-byte vectors), the access mix of the decode state
 // update (each 64 KiB of state read once and written back once).  Not part of
-// the GDN path; bench.py --only rmw uses it to measure the 1-read:1-write
-// ceiling of the box that the decode / verify fractions are read against, and
-// a store-only stream (the write ceiling for verify's per-step state stores).
-#include "common.hpp"
+// the GDN path and not in libgdn_mi355x.so: it builds into the bench-only
+// libgdn_probe.so, which bench.py --only rmw uses to measure the
+// 1-read:1-write ceiling of the box that the decode / verify fractions are
+// read against, and a store-only stream (the write ceiling for verify's
+// per-step state stores).
+//
+// int gdn_probe_rmw(void* buf, int64_t bytes, int64_t block_bytes,
+//                   int loads_in_flight, int nontemporal, void* stream):
+// buf[i] <- buf[i] * 1.0 in place over `bytes` (16-byte vectors), each block
+// owning `block_bytes` consecutive bytes and each lane keeping
+// `loads_in_flight` (1, 2, 4, 8, 16) 16-byte loads in flight before its
+// stores, optionally non-temporal; loads_in_flight 0: a store-only stream
+// (buf[i] <- 1.0).  Returns 0, or an error code with gdn_probe_last_error().
+#include <cstdarg>
+
+#include "../common.hpp"
 
 namespace gdn {
+
+// This library's own error store (hidden: the product library has its own).
+static thread_local char g_probe_error[512] = "";
+
+__attribute__((visibility("hidden"))) void set_error(const char* fmt, ...) {
+  va_list args;
+  va_start(args, fmt);
+  vsnprintf(g_probe_error, sizeof(g_probe_error), fmt, args);
+  va_end(args);
+}
+
+__attribute__((visibility("hidden"))) int hip_status(hipError_t err, const char* what) {
+  if (err == hipSuccess) return GDN_OK;
+  set_error("%s: %s", what, hipGetErrorString(err));
+  return GDN_ERR_HIP;
+}
+
 namespace {
 
 typedef float f4v __attribute__((ext_vector_type(4)));
@@ -101,3 +130,5 @@ extern "C" int gdn_probe_rmw(void* buf, int64_t bytes, int64_t block_bytes, int 
       return GDN_ERR_UNSUPPORTED;
   }
 }
+
+extern "C" const char* gdn_probe_last_error(void) { return gdn::g_probe_error; }

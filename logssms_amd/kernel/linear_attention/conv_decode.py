@@ -98,9 +98,8 @@ def _conv_decode_logstate(mixed_qkv, weight, config, bias, split_qkv, round_conv
                           read_granules, write_granules, work_slots, input_boundaries, input_scales):
     """The LogState mode of ``conv_decode`` (``conv_decode.py:320-345``)."""
     assert read_granules is not None and write_granules is not None and work_slots is not None
-    if input_boundaries is not None or tuple(input_scales) != (1.0, 1.0, 1.0):
-        raise NotImplementedError("input scales are not supported with LogState conv pools")
     bs, channels = mixed_qkv.shape
+    scale_args = conv_input_scale_args(channels, input_boundaries, input_scales)
     assert channels == config.conv_dim
     assert read_slots.shape == write_slots.shape == read_granules.shape == write_granules.shape == (bs,)
     assert work_slots.shape == (bs,)
@@ -120,13 +119,14 @@ def _conv_decode_logstate(mixed_qkv, weight, config, bias, split_qkv, round_conv
             "gdn_conv_decode_logstate",
             mixed_qkv.data_ptr(), mixed_qkv.stride(0), mixed_qkv.stride(1), _lib.dtype_code(mixed_qkv.dtype),
             weight.data_ptr(), _lib.ptr(bias), config.state_len + 1, bs, channels,
-            storage.data_ptr(), table.data_ptr(), _lib.index_code(table), table.shape[1], table.shape[2],
-            pool.frame_bytes, num_frames, config.layer_idx,
+            storage.data_ptr(), table.data_ptr(), _lib.index_code(table), table.shape[0], table.shape[1],
+            table.shape[2], pool.frame_bytes, num_frames, config.layer_idx,
             read_slots.data_ptr(), _lib.index_code(read_slots), read_granules.data_ptr(),
             _lib.index_code(read_granules), write_slots.data_ptr(), _lib.index_code(write_slots),
             write_granules.data_ptr(), _lib.index_code(write_granules), work_slots.data_ptr(),
             _lib.index_code(work_slots), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-            config.key_dim if split_qkv else 0, int(split_qkv), int(round_conv), _lib.stream_of(mixed_qkv),
+            config.key_dim if split_qkv else 0, int(split_qkv), int(round_conv), *scale_args,
+            _lib.stream_of(mixed_qkv),
         )
     return (q, k, v) if split_qkv else q
 

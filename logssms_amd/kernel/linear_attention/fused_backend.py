@@ -34,7 +34,7 @@ def _check_pools(conv_state: torch.Tensor, recurrent_state: torch.Tensor | None,
 
 
 def prefill_frontend(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, conv_state, cu_seqlens,
-                     baseline_slots, snapshot_rows=None, snapshot_slots=None):
+                     baseline_slots, snapshot_rows=None, snapshot_slots=None, *, layer=None):
     """Returns ``(q [1,T,H,dk], k, v [1,T,HV,dv], g [1,T,HV] fp32, beta fp32)``
     exactly as ``prepare_gdn(split(packed_causal_conv1d(...)))`` would, with
     the conv history read from ``conv_state[baseline_slots, layer]`` (zeros for
@@ -43,7 +43,8 @@ def prefill_frontend(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config,
     launch, after every history has been read: a window slot may equal a
     baseline slot (a prefill resuming mid-page writes its checkpoint to the
     page it resumed from), and the reference reads all histories before any
-    window is written (``gdn.py:107-112`` gathers them with ``index_select``)."""
+    window is written (``gdn.py:107-112`` gathers them with ``index_select``).
+    ``layer`` (default ``config.layer_idx``) is the conv pool's layer read."""
     T, C = mixed_qkv.shape
     assert C == config.conv_dim == 2 * config.key_dim + config.value_dim
     assert gate.shape == beta.shape == (T, config.num_v_heads)
@@ -66,8 +67,8 @@ def prefill_frontend(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config,
         mixed_qkv.data_ptr(), mixed_qkv.stride(0), mixed_qkv.stride(1), _lib.dtype_code(dt),
         weight.data_ptr(), None, config.state_len + 1, cu_seqlens.data_ptr(), _lib.index_code(cu_seqlens),
         len(cu_seqlens) - 1, T, config.num_k_heads, config.num_v_heads, config.head_k_dim, config.head_v_dim,
-        conv_state.data_ptr(), conv_state.stride(0), conv_state.stride(1), config.layer_idx,
-        baseline_slots.data_ptr(), _lib.index_code(baseline_slots),
+        conv_state.data_ptr(), conv_state.stride(0), conv_state.stride(1),
+        config.layer_idx if layer is None else layer, baseline_slots.data_ptr(), _lib.index_code(baseline_slots),
         gate.data_ptr(), gate.stride(0), gate.stride(1), _lib.dtype_code(gate.dtype),
         beta.data_ptr(), beta.stride(0), beta.stride(1), _lib.dtype_code(beta.dtype),
         A_log.data_ptr(), _lib.dtype_code(A_log.dtype), dt_bias.data_ptr(), _lib.dtype_code(dt_bias.dtype),

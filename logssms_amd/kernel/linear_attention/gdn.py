@@ -76,25 +76,25 @@ def chunk_gated_delta_rule_to_cache(
     if frames is None:
         _check_state_storage(storage, HV, dk, dv)
         strides = (storage.stride(0), storage.stride(1), storage.stride(2))
-        frame_args = (None, 0, 0, 0, 0, 0)
+        frame_args = (None, 0, 0, 0, 0, 0, 0)
     else:
         assert storage.ndim == 2 and storage.is_contiguous()
         assert state_io.frame_bytes > 0 and state_io.head_payload_bytes > 0
         assert storage.shape[1] * storage.element_size() == state_io.frame_bytes
         assert frames.ndim == 2 and frames.is_contiguous() and frames.device == storage.device
-        if dv % 64:
-            raise NotImplementedError("frame-table states need head_v_dim % 64 == 0 on the MI355X backend")
         strides = (0, 0, 0)
-        frame_args = (frames, _lib.index_code(frames), frames.shape[1], state_io.frame_bytes,
+        # slots past the table's rows (and past the decay table's, when logging) are unmapped
+        rows = frames.shape[0] if log_io is None else min(frames.shape[0], log_io.decay_frames.shape[0])
+        frame_args = (frames, _lib.index_code(frames), rows, frames.shape[1], state_io.frame_bytes,
                       state_io.head_payload_bytes, storage.shape[0])
-    if chunk_size != 64 and dv % 64:
-        raise NotImplementedError("chunk_size 16/32 needs head_v_dim % 64 == 0 on the MI355X backend")
     if log_io is not None:
         assert frames is not None, "the token log lives in the LogState frame storage"
         assert log_io.slots.shape == log_io.token_offsets.shape == (T,)
         assert log_io.gate.numel() == T * HV and log_io.num_key_heads > 0
         assert H % log_io.num_key_heads == 0 and HV % log_io.num_key_heads == 0
         assert storage.dtype == value.dtype, "log rows are stored in the io dtype"
+    if dv != 32 and dv % 64:
+        raise NotImplementedError("head_v_dim must be 32 or a multiple of 64 on the MI355X backend")
     assert storage.device == query.device
     if chunk_indices is not None:
         assert state_io.chunk_write_slots.shape == (len(chunk_indices),)
@@ -106,7 +106,7 @@ def chunk_gated_delta_rule_to_cache(
     o = torch.empty_like(value) if out is None else out
     assert o.shape == value.shape and o.dtype == value.dtype and o.is_contiguous()
     # v' straight into the log when the caller does not want v_new back
-    direct_log = (log_io is not None and not return_v_new and dv % 64 == 0 and state_io.frame_bytes % 128 == 0)
+    direct_log = (log_io is not None and not return_v_new and state_io.frame_bytes % (2 * min(dv, 64)) == 0)
     v_new = torch.empty_like(value) if (return_v_new or (log_io is not None and not direct_log)) else None
     if T and direct_log:
         fw = state_io.final_write_slots
@@ -143,7 +143,7 @@ def chunk_gated_delta_rule_to_cache(
         log_gate = log_io.gate.float().contiguous()
         _lib.call(
             "gdn_store_chunk_log",
-            storage.data_ptr(), frames.data_ptr(), _lib.index_code(frames), frames.shape[1],
+            storage.data_ptr(), frames.data_ptr(), _lib.index_code(frames), frame_args[2], frames.shape[1],
             state_io.frame_bytes, storage.shape[0],
             log_io.slots.data_ptr(), _lib.index_code(log_io.slots),
             log_io.token_offsets.data_ptr(), _lib.index_code(log_io.token_offsets), T,
@@ -293,6 +293,8 @@ def fused_recurrent_gated_delta_rule_to_logstate(
     assert seq_len == 1
     assert head_k_dim == layout.head_k_dim and head_v_dim == layout.head_v_dim
     assert num_v_heads == layout.num_value_heads and num_v_heads % num_k_heads == 0
+    # the step's key rows go to the log at the prefill's key-head layout
+    assert getattr(layout, "num_key_heads", num_k_heads) == num_k_heads, "log key heads != query key heads"
     assert replay_counts.shape == work_slots.shape == log_slots.shape == token_offsets.shape == (batch_size,)
     assert pool.frame_bytes % pool.head_payload_bytes == 0 or pool.head_payload_bytes % pool.frame_bytes == 0
     output = torch.empty_like(value) if out is None else out
@@ -314,8 +316,8 @@ def fused_recurrent_gated_delta_rule_to_logstate(
         beta.data_ptr(), beta.stride(0), beta.stride(2), _lib.dtype_code(beta.dtype),
         A_log.data_ptr(), _lib.dtype_code(A_log.dtype), dt_bias.data_ptr(), _lib.dtype_code(dt_bias.dtype),
         batch_size, num_k_heads, num_v_heads, head_k_dim, head_v_dim,
-        storage.data_ptr(), frames.data_ptr(), _lib.index_code(frames), frames.shape[1], pool.frame_bytes,
-        pool.head_payload_bytes, num_frames, decay.data_ptr(), _lib.index_code(decay), layout.log_decay_bytes,
+        storage.data_ptr(), frames.data_ptr(), _lib.index_code(frames), min(frames.shape[0], decay.shape[0]),
+        frames.shape[1], pool.frame_bytes, pool.head_payload_bytes, num_frames, decay.data_ptr(), _lib.index_code(decay), layout.log_decay_bytes,
         slots[0].data_ptr(), _lib.index_code(slots[0]), slots[1].data_ptr(), _lib.index_code(slots[1]),
         slots[2].data_ptr(), _lib.index_code(slots[2]), slots[3].data_ptr(), _lib.index_code(slots[3]),
         layer, layout.num_linear_layers, layout.granularity, pool.page_size, int(enable_eager_state),

@@ -69,7 +69,8 @@ def restore_log_state_chains(pool, chains: Sequence[tuple[int | None, Sequence[t
     decay = pool.decay_frame_table.contiguous()
     _lib.call(
         "gdn_logstate_restore",
-        storage.data_ptr(), frames.data_ptr(), _lib.index_code(frames), frames.shape[1], pool.frame_bytes,
+        storage.data_ptr(), frames.data_ptr(), _lib.index_code(frames), min(frames.shape[0], decay.shape[0]),
+        frames.shape[1], pool.frame_bytes,
         pool.head_payload_bytes, num_frames, decay.data_ptr(), _lib.index_code(decay), layout.log_decay_bytes,
         layout.num_linear_layers, layout.num_value_heads, layout.num_key_heads, layout.head_k_dim,
         layout.head_v_dim, layout.granularity, pool.page_size, _lib.dtype_code(pool.dtype),
@@ -97,7 +98,8 @@ def store_log_states(pool, slots: torch.Tensor, token_offsets: torch.Tensor, key
     decay = pool.decay_frame_table.contiguous()
     _lib.call(
         "gdn_store_chunk_log",
-        storage.data_ptr(), frames.data_ptr(), _lib.index_code(frames), frames.shape[1], pool.frame_bytes,
+        storage.data_ptr(), frames.data_ptr(), _lib.index_code(frames), min(frames.shape[0], decay.shape[0]),
+        frames.shape[1], pool.frame_bytes,
         num_frames, slots.contiguous().data_ptr(), _lib.index_code(slots), token_offsets.contiguous().data_ptr(),
         _lib.index_code(token_offsets), T, residual.data_ptr(), keys.data_ptr(), keys.shape[1], HV,
         layout.head_k_dim, dv, layout.num_key_heads, gates.data_ptr(), decay.data_ptr(), _lib.index_code(decay),
@@ -117,7 +119,8 @@ def copy_states(pool, sources: Sequence[int], destinations: Sequence[int]) -> No
     src, dst = _vectors([list(sources), list(destinations)], storage.device)
     _lib.call(
         "gdn_logstate_copy_states",
-        storage.data_ptr(), frames.data_ptr(), _lib.index_code(frames), frames.shape[1], pool.frame_bytes,
+        storage.data_ptr(), frames.data_ptr(), _lib.index_code(frames), frames.shape[0], frames.shape[1],
+        pool.frame_bytes,
         pool.head_payload_bytes, num_frames, layout.num_linear_layers, layout.num_value_heads, layout.head_k_dim,
         layout.head_v_dim, _lib.dtype_code(pool.dtype), src.data_ptr(), dst.data_ptr(), len(src),
         _lib.stream_of(storage),

@@ -103,13 +103,25 @@ def packed_causal_conv1d(
 
 def _packed_conv_logstate(x, weight, history, cu_seqlens, bias, state_io, input_boundaries, input_scales):
     """LogState mode of ``packed_causal_conv1d`` (``packed_conv.py:160-189``):
-    the conv itself, then the windows through the conv frame table
-    (``gdn_conv_windows_logstate``)."""
-    if input_boundaries is not None or tuple(input_scales) != (1.0, 1.0, 1.0):
-        raise NotImplementedError("input scales are not supported with LogState conv frames")
+    the conv itself, then the windows through the conv frame table."""
+    output = packed_causal_conv1d(x, weight, history, cu_seqlens, None, bias, input_boundaries=input_boundaries,
+                                  input_scales=input_scales)
+    conv_windows_logstate(x, history, cu_seqlens, state_io, weight.shape[-1], input_boundaries, input_scales)
+    return output
+
+
+def conv_windows_logstate(x, history, cu_seqlens, state_io: PackedConvStateIO, kernel_size: int,
+                          input_boundaries=None, input_scales=(1.0, 1.0, 1.0)) -> None:
+    """The state writes of ``packed_causal_conv1d`` with a LogState
+    ``state_io`` (``packed_conv.py:75-133`` with LOGSTATE): the raw window
+    ending at each packed row t (inputs scaled as the conv reads them, rows
+    before a sequence from ``history``) to the conv snapshot
+    (``slots[t]``, ``granules[t]``) when that slot is >= 0, and each sequence's
+    last window to granule 0 of ``final_slots`` (``gdn_conv_windows_logstate``)."""
     total_tokens, channels = x.shape
-    kernel_size = weight.shape[-1]
+    scale_args = conv_input_scale_args(channels, input_boundaries, input_scales)
     table = state_io.frame_table
+    assert history.shape == (len(cu_seqlens) - 1, channels, kernel_size - 1)
     assert state_io.granules is not None and state_io.granules.shape == (total_tokens,)
     assert state_io.slots.shape == (total_tokens,)
     assert state_io.frame_bytes % x.element_size() == 0
@@ -118,9 +130,8 @@ def _packed_conv_logstate(x, weight, history, cu_seqlens, bias, state_io, input_
     assert storage.dtype == x.dtype and storage.device == x.device and storage.is_contiguous()
     if state_io.final_slots is not None:
         assert state_io.final_slots.shape == (len(cu_seqlens) - 1,)
-    output = packed_causal_conv1d(x, weight, history, cu_seqlens, None, bias)
     if total_tokens == 0:
-        return output
+        return
     history = history.to(x.dtype).contiguous()
     slots, granules = state_io.slots.contiguous(), state_io.granules.contiguous()
     final = state_io.final_slots.contiguous() if state_io.final_slots is not None else None
@@ -129,12 +140,11 @@ def _packed_conv_logstate(x, weight, history, cu_seqlens, bias, state_io, input_
         "gdn_conv_windows_logstate",
         x.data_ptr(), x.stride(0), x.stride(1), _lib.dtype_code(x.dtype), history.data_ptr(),
         cu_seqlens.data_ptr(), _lib.index_code(cu_seqlens), len(cu_seqlens) - 1, total_tokens, channels,
-        kernel_size, storage.data_ptr(), table.data_ptr(), _lib.index_code(table), table.shape[1], table.shape[2],
-        state_io.frame_bytes, num_frames, state_io.layer, slots.data_ptr(), _lib.index_code(slots),
+        kernel_size, storage.data_ptr(), table.data_ptr(), _lib.index_code(table), table.shape[0], table.shape[1],
+        table.shape[2], state_io.frame_bytes, num_frames, state_io.layer, slots.data_ptr(), _lib.index_code(slots),
         granules.data_ptr(), _lib.index_code(granules), _lib.ptr(final),
-        _lib.index_code(final) if final is not None else 0, _lib.stream_of(x),
+        _lib.index_code(final) if final is not None else 0, *scale_args, _lib.stream_of(x),
     )
-    return output
 
 
-__all__ = ["PackedConvStateIO", "packed_causal_conv1d"]
+__all__ = ["PackedConvStateIO", "conv_windows_logstate", "packed_causal_conv1d"]

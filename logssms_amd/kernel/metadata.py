@@ -86,16 +86,10 @@ def make_logstate_prefill_writes(logs: torch.Tensor, offsets: torch.Tensor, plan
     offsets ``offsets`` and the int32 host plan ``[conv slot | conv granule |
     log enabled]`` (conv slot -2: the token's own log slot), the
     ``(log write slots, conv token slots, conv token granules)`` of a LogState
-    prefill (``gdn_logstate_prefill_writes`` on the device; host tensors take
-    the same torch expressions)."""
+    prefill (``gdn_logstate_prefill_writes``)."""
     count = logs.numel()
     output = torch.empty((3, count), dtype=logs.dtype, device=logs.device)
-    if not logs.is_cuda:
-        conv, granules, enabled = plan[:3 * count].view(3, count)
-        output[0] = torch.where(enabled != 0, logs, -1)
-        output[1] = torch.where(conv == -2, logs, conv)
-        output[2] = torch.where(conv == -2, offsets // granularity, granules)
-        return output.unbind(0)
+    assert logs.is_cuda and offsets.device == plan.device == logs.device
     assert plan.dtype == torch.int32 and plan.is_contiguous() and plan.numel() >= 3 * count
     logs, offsets = logs.contiguous(), offsets.contiguous()
     _lib.call("gdn_logstate_prefill_writes", logs.data_ptr(), _lib.index_code(logs), offsets.data_ptr(),
@@ -104,4 +98,38 @@ def make_logstate_prefill_writes(logs: torch.Tensor, offsets: torch.Tensor, plan
     return output.unbind(0)
 
 
-__all__ = ["copy_metadata", "make_logstate_prefill_writes", "pad_metadata"]
+def gather_linear_slots(indices, state_table: torch.Tensor, *, work_table: torch.Tensor | None = None,
+                        out_loc: torch.Tensor | None = None, page_size: int = 1) -> torch.Tensor:
+    """metadata.py:266-320: decode slots from the engine's prepared batch
+    packet (``indices.table_ids``, ``indices.cached_lens``) in one launch
+    (``gdn_gather_linear_slots``), with no host copy of the tables.
+
+    Standard pool: int64 ``[count, 2]`` of (read, write) slots,
+    ``state_table[row, cached - 1]`` (the row's last column for cached 0) and
+    ``state_table[row, cached]``.  LogState (``work_table`` given): int32
+    ``[4, count]`` of (work slot, log slot, ``out_loc mod page_size``, 0)."""
+    tables, cached = indices.table_ids, indices.cached_lens
+    count = tables.numel()
+    assert cached.numel() == count and state_table.ndim == 2 and state_table.stride(1) == 1
+    assert tables.is_cuda and cached.device == tables.device == state_table.device
+    logstate = work_table is not None
+    if logstate:
+        assert out_loc is not None and out_loc.numel() >= count and page_size > 0
+        assert work_table.ndim == 2 and work_table.device == state_table.device
+        output = torch.empty((4, count), dtype=torch.int32, device=state_table.device)
+    else:
+        output = torch.empty((count, 2), dtype=torch.int64, device=state_table.device)
+    if count == 0:
+        return output
+    tables, cached = tables.contiguous(), cached.contiguous()
+    loc = out_loc.contiguous() if logstate else None
+    _lib.call("gdn_gather_linear_slots", tables.data_ptr(), _lib.index_code(tables), cached.data_ptr(),
+              _lib.index_code(cached), state_table.data_ptr(), _lib.index_code(state_table), state_table.shape[0],
+              state_table.shape[1], state_table.stride(0), _lib.ptr(work_table),
+              _lib.index_code(work_table) if logstate else 0, work_table.shape[0] if logstate else 0,
+              work_table.stride(0) if logstate else 0, _lib.ptr(loc), _lib.index_code(loc) if logstate else 0,
+              page_size, output.data_ptr(), count, _lib.stream_of(state_table))
+    return output
+
+
+__all__ = ["copy_metadata", "gather_linear_slots", "make_logstate_prefill_writes", "pad_metadata"]

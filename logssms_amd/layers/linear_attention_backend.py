@@ -30,6 +30,7 @@ from ..core import MarconiCacheMetadata, get_global_ctx
 from ..kernel.linear_attention.fused_backend import decode_step, prefill_frontend, prefill_fused, verify_group
 from ..kernel.linear_attention.gdn import chunk_gated_delta_rule_to_cache
 from ..kernel.linear_attention.state_io import ChunkStateIO
+from ..kernel.metadata import gather_linear_slots
 
 
 @dataclass
@@ -116,7 +117,27 @@ def _gather(table: torch.Tensor, rows, cols) -> torch.Tensor:
     return table[r, c].to(torch.int64)
 
 
-class GatedDeltaBackend:
+class MixedForward:
+    """``forward_mixed`` of the reference's ``BaseLinearAttnBackend``
+    (``base.py:20-42``) for the GDN backends here: a mixed batch's prefill
+    part (its first ``prefill_token_capacity`` rows, or the prefill tokens)
+    and decode part (the remaining rows), each through ``forward`` into slices
+    of one output."""
+
+    def forward_mixed(self, batch, token_inputs: dict[str, torch.Tensor], **kwargs) -> torch.Tensor:
+        assert batch.mixed_parts is not None
+        split = batch.prefill_token_capacity or batch.prefill_tokens
+        example = next(iter(token_inputs.values()))
+        config = kwargs["config"]
+        output = torch.empty(len(example), config.num_v_heads, config.head_v_dim, dtype=example.dtype,
+                             device=example.device)
+        for part, begin, end in ((batch.mixed_parts[0], 0, split), (batch.mixed_parts[1], split, len(example))):
+            self.forward(**{name: tensor[begin:end] for name, tensor in token_inputs.items()}, **kwargs,
+                         batch=part, out=output[begin:end])
+        return output
+
+
+class GatedDeltaBackend(MixedForward):
     def __init__(self, ctx=None) -> None:
         self._ctx = ctx
         self.capture: LinearAttnCaptureData | None = None
@@ -133,13 +154,18 @@ class GatedDeltaBackend:
         assert state_table is not None
         metadata = LinearAttnMetadata(phase=batch.phase)
         if batch.is_decode:
-            reqs = batch.padded_reqs
-            t = [r.table_idx for r in reqs]
-            c = np.asarray([r.cached_len for r in reqs], dtype=np.int64)
-            # cached_len - 1 = -1 wraps to the row's last entry, as torch indexing does
-            read = _gather(state_table, t, np.where(c - 1 < 0, c - 1 + state_table.shape[1], c - 1))
-            write = _gather(state_table, t, c)
-            metadata.slots = torch.stack([read, write], 1)
+            packet = batch.prepared_indices
+            if packet is not None and state_table.is_cuda:
+                # standard.py:114-117: the engine's packet, gathered on the device
+                metadata.slots = gather_linear_slots(packet, state_table)
+            else:
+                reqs = batch.padded_reqs
+                t = [r.table_idx for r in reqs]
+                c = np.asarray([r.cached_len for r in reqs], dtype=np.int64)
+                # cached_len - 1 = -1 wraps to the row's last entry, as torch indexing does
+                read = _gather(state_table, t, np.where(c - 1 < 0, c - 1 + state_table.shape[1], c - 1))
+                write = _gather(state_table, t, c)
+                metadata.slots = torch.stack([read, write], 1)
             metadata.read_slots = metadata.slots[:, 0]
             metadata.write_slots = metadata.slots[:, 1]
         elif batch.is_prefill:
@@ -239,21 +265,6 @@ class GatedDeltaBackend:
         self.capture.slots[:bs].copy_(metadata.slots)
 
     # ------------------------------------------------------------ forward
-    def forward_mixed(self, batch, token_inputs: dict[str, torch.Tensor], **kwargs) -> torch.Tensor:
-        """base.py:20-42: a mixed batch's prefill part (its first
-        ``prefill_token_capacity`` rows, or the prefill tokens) and decode part
-        (the remaining rows), each through ``forward`` into slices of one output."""
-        assert batch.mixed_parts is not None
-        split = batch.prefill_token_capacity or batch.prefill_tokens
-        example = next(iter(token_inputs.values()))
-        config = kwargs["config"]
-        output = torch.empty(len(example), config.num_v_heads, config.head_v_dim, dtype=example.dtype,
-                             device=example.device)
-        for part, begin, end in ((batch.mixed_parts[0], 0, split), (batch.mixed_parts[1], split, len(example))):
-            self.forward(**{name: tensor[begin:end] for name, tensor in token_inputs.items()}, **kwargs,
-                         batch=part, out=output[begin:end])
-        return output
-
     def forward(self, mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, batch, out=None):
         """gdn.py:20-49."""
         metadata = batch.linear_attn_metadata
@@ -300,4 +311,4 @@ class GatedDeltaBackend:
         return output
 
 
-__all__ = ["GatedDeltaBackend", "LinearAttnCaptureData", "LinearAttnMetadata", "PackedLinearIndices"]
+__all__ = ["GatedDeltaBackend", "LinearAttnCaptureData", "LinearAttnMetadata", "MixedForward", "PackedLinearIndices"]

@@ -1,57 +1,75 @@
-"""``GatedDeltaLogStateBackend`` -- the LogState variant of the GDN backend,
-drop-in for the reference's
-``python/logssms/layers/linear_attention_backend/{logstate,gdn_logstate}.py``.
+"""``GatedDeltaLogStateBackend``: the Gated DeltaNet backend over a LogState
+cache, drop-in for the reference's
+``python/logssms/layers/linear_attention_backend/{logstate,gdn_logstate}.py``
+(same class, dataclass and method names and fields, same slot plan).
 
-In the LogState cache a request keeps one *work slot* (its running state and
-conv window) and writes per-token *logs* (key, v' residual, gate) into the
-frames of its pages; decode rebuilds the state from the work slot plus the
-tokens logged since its last write-back (at most 16).  The forward passes
-here are the reference's, on this library's kernels:
+In a LogState cache a request owns one *work slot* (its running state and
+conv window) and logs every token (key, v' residual, gate) into the frames of
+the log slot of the page the token lands in; decode rebuilds the state from
+the work slot plus the at most 16 tokens logged since its last write-back.
 
-* prefill (``gdn_logstate.py:85-172``): conv history read through the pool,
-  packed conv with window snapshots to (slot, granule) frames and the final
-  window to the work slot, ``prepare_gdn``, the chunked rule with frame-table
-  states (read from and finally written to the work slot, checkpoints every
-  ``granularity`` tokens) and the token log;
-* decode (``gdn_logstate.py:174-224``): conv decode through the conv frame
-  table, then the replayed recurrence with its log rows.
+Metadata (``prepare_metadata``), from the context's ``state_table`` (the log
+slot of every position), ``work_state_table`` and ``page_table``:
 
-The pool is the process-global ``ctx.linear_state`` (or the context bound at
-construction) and must provide what ``cache/logstate/frame_pool.py``'s pool
-provides: ``storage`` (uint8 frames), ``dtype``, ``frame_bytes``,
-``head_payload_bytes``, ``page_size``, ``payload_frame_table``,
-``decay_frame_table``, ``conv_frame_table``, ``layout`` and ``read_conv``.
-``prepare_metadata`` (``logstate.py:92-272``) builds the metadata from the
-context's ``state_table`` (the log slot of each position), ``work_state_table``
-and ``page_table``, the batch's ``positions`` / ``out_loc`` and its
-``LogStateCacheMetadata`` (replay counts, checkpoint writes and unlogged
-ranges, which the LogState cache manager plans); the pool's ``allocator``
-tells work slots from others.  Speculative verify raises
+* decode: work slot, log slot at the new position, the position's page
+  offset and the replay count per request -- gathered on the device from the
+  engine's prepared packet when the batch carries one (``gdn_gather_linear_
+  slots``), else from the tables with one host upload;
+* prefill: the same per token, the conv history source of each request (the
+  log slot and granule of its previous position, else its work slot), and
+  the write plan -- per token the conv snapshot target and the log write
+  slot, per ``granularity``-token chunk the checkpoint slot.  The plan's host
+  part is built vectorised in numpy (``logstate_prefill_plan``) from the
+  ``LogStateCacheMetadata`` the cache manager fills in (first page offsets,
+  checkpoint writes, unlogged ranges) and finished on the device
+  (``make_logstate_prefill_writes``).
+
+Forward, on this library's kernels:
+
+* prefill (``gdn_logstate.py:85-172``'s results): the conv history is read
+  through the pool (``read_conv``); one front-end pass computes the packed
+  conv + SiLU, the q/k/v split and ``prepare_gdn``
+  (``gdn_prefill_frontend``) where the reference runs two ops; the raw conv
+  windows go to their (slot, granule) snapshots and each request's last one
+  to its work slot; the chunked rule runs at the pool's granularity on
+  frame-table states with the v' rows written into the log by the chunk
+  kernel, and the log store adds keys and gates;
+* decode (``gdn_logstate.py:174-224``): the conv decode through the conv
+  frame table, then the replayed recurrence.
+
+The pool is the process-global ``ctx.linear_state`` (or that of the context
+bound at construction) and provides what the reference's
+``cache/logstate/frame_pool.py`` pool provides: ``storage`` (uint8 frames),
+``dtype``, ``frame_bytes``, ``head_payload_bytes``, ``page_size``,
+``payload_frame_table``, ``decay_frame_table``, ``conv_frame_table``,
+``layout``, ``allocator`` and ``read_conv``.  Speculative verify raises
 ``NotImplementedError``, as in the reference.
 """
 
 from __future__ import annotations
 
 from dataclasses import dataclass
+from typing import NamedTuple
 
+import numpy as np
 import torch
 
 from ..core import LogStateCacheMetadata, get_global_ctx
-from ..kernel.fused import prepare_gdn
-from ..kernel.metadata import copy_metadata, make_logstate_prefill_writes
 from ..kernel.linear_attention.conv_decode import conv_decode
+from ..kernel.linear_attention.fused_backend import prefill_frontend
 from ..kernel.linear_attention.gdn import (
     chunk_gated_delta_rule_to_cache,
     fused_recurrent_gated_delta_rule_to_logstate,
 )
-from ..kernel.linear_attention.packed_conv import PackedConvStateIO, packed_causal_conv1d
+from ..kernel.linear_attention.packed_conv import PackedConvStateIO, conv_windows_logstate
 from ..kernel.linear_attention.state_io import ChunkLogIO, ChunkStateIO
-from .linear_attention_backend import PackedLinearIndices
+from ..kernel.metadata import copy_metadata, gather_linear_slots, make_logstate_prefill_writes
+from .linear_attention_backend import MixedForward, PackedLinearIndices
 
 
 @dataclass
 class LogStateLinearAttnMetadata:
-    """logstate.py:21-35."""
+    """logstate.py:21-35 (field names and meaning are the interface)."""
 
     phase: str
     work_slots: torch.Tensor
@@ -68,10 +86,15 @@ class LogStateLinearAttnMetadata:
     conv_token_granules: torch.Tensor | None = None
 
 
+# the per-request fields a captured decode reads (all int32)
+_DECODE_FIELDS = ("work_slots", "log_slots", "token_offsets", "conv_read_slots", "conv_read_granules",
+                  "replay_counts")
+
+
 @dataclass
 class LogStateLinearAttnCaptureData:
-    """logstate.py:38-61: decode capture buffers, one int32 entry per
-    sequence of the largest captured batch."""
+    """logstate.py:38-61: the decode capture buffers, one int32 entry per
+    request of the largest captured batch."""
 
     work_slots: torch.Tensor
     log_slots: torch.Tensor
@@ -82,18 +105,117 @@ class LogStateLinearAttnCaptureData:
 
     @classmethod
     def make(cls, max_bs: int, device) -> "LogStateLinearAttnCaptureData":
-        return cls(*(torch.zeros(max_bs, dtype=torch.int32, device=device) for _ in range(6)))
+        block = torch.zeros(len(_DECODE_FIELDS), max_bs, dtype=torch.int32, device=device)
+        return cls(*block.unbind(0))
+
+    def view(self, bs: int) -> LogStateLinearAttnMetadata:
+        """Decode metadata reading the first ``bs`` entries of the buffers."""
+        return LogStateLinearAttnMetadata(phase="decode", **{f: getattr(self, f)[:bs] for f in _DECODE_FIELDS})
 
 
-_CAPTURED = ("work_slots", "log_slots", "token_offsets", "conv_read_slots", "conv_read_granules", "replay_counts")
+def logstate_prefill_plan(lengths, cached_lens, first_offsets, checkpoint_writes, checkpoint_ranges,
+                          granularity: int, num_granules: int, work_slot) -> np.ndarray:
+    """The host part of the LogState prefill write plan
+    (``logstate.py:215-272``), one int32 vector ``[conv slot (T) | conv
+    granule (T) | log enabled (T) | chunk write slot (chunks)]`` for T packed
+    tokens and ``sum(ceil(length / granularity))`` chunks.
+
+    Conv slot -2 marks a token whose snapshot goes to its own log slot (at a
+    granule end, ``(first + row + 1) % granularity == 0``, and at its
+    request's last token); tokens inside an unlogged range ``(request, begin,
+    end)`` (positions; ``begin - cached_len`` .. ``end - cached_len`` clipped
+    to the request) are not logged and take no snapshot.  A checkpoint
+    ``(global row, slot)`` whose token is a marked one makes that token's
+    snapshot and its chunk's state write go to ``slot`` (granule 0 when
+    ``work_slot(slot)``, else the last granule); among checkpoints on one
+    token or one chunk the last in sorted ``(row, slot)`` order wins, and the
+    rest are ignored."""
+    g = int(granularity)
+    lens = np.asarray(lengths, dtype=np.int64)
+    n = lens.size
+    tok_start = np.zeros(n + 1, dtype=np.int64)
+    np.cumsum(lens, out=tok_start[1:])
+    chunk_start = np.zeros(n + 1, dtype=np.int64)
+    np.cumsum((lens + g - 1) // g, out=chunk_start[1:])
+    T, chunks = int(tok_start[-1]), int(chunk_start[-1])
+    owner = np.repeat(np.arange(n, dtype=np.int64), lens)
+    row = np.arange(T, dtype=np.int64) - tok_start[owner]
+    first = np.asarray(first_offsets, dtype=np.int64).reshape(n)
+    marked = ((first[owner] + row + 1) % g == 0) | (row + 1 == lens[owner])
+
+    plan = np.empty(3 * T + chunks, dtype=np.int32)
+    conv, gran, logged, chunk = plan[:T], plan[T:2 * T], plan[2 * T:3 * T], plan[3 * T:]
+    conv[:] = np.where(marked, -2, -1)
+    gran[:] = 0
+    logged[:] = 1
+    chunk[:] = -1
+
+    if len(checkpoint_ranges):
+        spans = np.asarray(checkpoint_ranges, dtype=np.int64).reshape(-1, 3)
+        spans = spans[(spans[:, 0] >= 0) & (spans[:, 0] < n)]  # ranges of other batches' requests: none
+        req = spans[:, 0]
+        cached = np.asarray(cached_lens, dtype=np.int64).reshape(n)[req]
+        lo = np.maximum(0, spans[:, 1] - cached)
+        hi = np.minimum(lens[req], spans[:, 2] - cached)
+        keep = lo < hi
+        edges = np.zeros(T + 1, dtype=np.int64)  # +1 at a range's first token, -1 after its last
+        np.add.at(edges, tok_start[req[keep]] + lo[keep], 1)
+        np.add.at(edges, tok_start[req[keep]] + hi[keep], -1)
+        unlogged = np.cumsum(edges[:T]) > 0
+        logged[unlogged] = 0
+        conv[unlogged] = -1
+
+    if len(checkpoint_writes):
+        writes = np.asarray(sorted(checkpoint_writes), dtype=np.int64).reshape(-1, 2)
+        assert (writes[:, 0] >= 0).all(), "checkpoint rows are packed token indices"
+        writes = writes[writes[:, 0] < T]  # rows past the batch are never reached
+        writes = writes[marked[writes[:, 0]]]
+        if len(writes):
+            tok, slot = writes[:, 0], writes[:, 1]
+            kind = np.asarray([0 if work_slot(int(s)) else num_granules - 1 for s in slot], dtype=np.int64)
+            target = chunk_start[owner[tok]] + row[tok] // g
+
+            def last_of(keys):  # index of the last entry of each distinct key (entries in sorted order)
+                _, from_end = np.unique(keys[::-1], return_index=True)
+                return len(keys) - 1 - from_end
+
+            t_last = last_of(tok)
+            conv[tok[t_last]] = slot[t_last]
+            gran[tok[t_last]] = kind[t_last]
+            c_last = last_of(target)
+            chunk[target[c_last]] = slot[c_last]
+    return plan
 
 
-class GatedDeltaLogStateBackend:
+class _Tables(NamedTuple):
+    pool: object
+    state: torch.Tensor  # [rows, positions]: the log slot of every position
+    work: torch.Tensor   # [rows, 1]
+    page: torch.Tensor   # [rows, positions]: KV locations
+
+    @classmethod
+    def of(cls, ctx) -> "_Tables":
+        assert ctx.state_table is not None and ctx.work_state_table is not None and ctx.page_table is not None
+        assert ctx.work_state_table.shape[1] == 1
+        return cls(ctx.linear_state, ctx.state_table, ctx.work_state_table, ctx.page_table)
+
+
+def _upload(values: np.ndarray, device) -> torch.Tensor:
+    """One host-to-device copy of an index vector (pinned, asynchronous)."""
+    host = torch.from_numpy(np.ascontiguousarray(values))
+    device = torch.device(device)
+    if device.type != "cuda":
+        return host.to(device)
+    return host.pin_memory().to(device, non_blocking=True)
+
+
+class GatedDeltaLogStateBackend(MixedForward):
     def __init__(self, ctx=None, *, enable_eager_state: bool = False) -> None:
         self._ctx = ctx
         self.enable_eager_state = enable_eager_state
         self.capture: LogStateLinearAttnCaptureData | None = None
         self.capture_bs: list[int] = []
+        self._sequence_ids: torch.Tensor | None = None  # 0, 1, 2, ... on the pool's device
 
     @property
     def ctx(self):
@@ -101,114 +223,84 @@ class GatedDeltaLogStateBackend:
 
     # ------------------------------------------------------------ metadata
     def prepare_metadata(self, batch) -> None:
-        """logstate.py:92-212 (the table path; the reference's prepared-packet
-        shortcut gathers the same slots)."""
         if batch.cache_metadata is None:
             batch.cache_metadata = LogStateCacheMetadata()
         assert isinstance(batch.cache_metadata, LogStateCacheMetadata)
         if batch.is_verify:
             raise NotImplementedError("LogState speculative verify is not implemented yet.")
-        ctx = self.ctx
-        pool = ctx.linear_state
-        state_table, work_table = ctx.state_table, ctx.work_state_table
-        assert state_table is not None and work_table is not None and ctx.page_table is not None
-        assert work_table.shape[1] == 1
         assert batch.positions is not None and batch.out_loc is not None
-        device = pool.storage.device
-        reqs = batch.padded_reqs if batch.is_decode else batch.reqs
-        table_indices = torch.tensor([r.table_idx for r in reqs], dtype=torch.int64, device=state_table.device)
+        tables = _Tables.of(self.ctx)
         if batch.is_decode:
-            row_table_indices = table_indices
+            batch.linear_attn_metadata = self._decode_metadata(batch, tables)
         else:
-            row_table_indices = torch.tensor([r.table_idx for r in reqs for _ in range(r.extend_len)],
-                                             dtype=torch.int64, device=state_table.device)
-        work_slots = work_table[table_indices, 0]
-        positions = batch.positions
-        assert len(positions) == len(row_table_indices)
-        log_slots = state_table[row_table_indices, positions.long()]
-        token_offsets = batch.out_loc.remainder(pool.page_size).to(torch.int32)
-        if batch.is_decode:
-            counts = batch.cache_metadata.replay_counts
-            if counts is None:
-                counts = [0] * len(reqs)
-            assert len(counts) == len(reqs)
-            replay_counts = torch.tensor(counts, dtype=torch.int32, device=device)
-            conv_read_slots = work_slots
-            conv_read_granules = torch.zeros_like(work_slots)
-        else:
-            replay_counts = torch.empty(0, dtype=torch.int32, device=device)
-            previous = torch.tensor([r.cached_len - 1 for r in reqs], dtype=torch.int64, device=state_table.device)
-            previous_slots = state_table[table_indices, previous.clamp_min(0)]
-            previous_kv = ctx.page_table[table_indices, previous.clamp_min(0)]
-            mapped = (previous >= 0) & (previous_slots >= 0)
-            conv_read_slots = torch.where(mapped, previous_slots, work_slots)
-            conv_read_granules = torch.where(
-                mapped, previous_kv.remainder(pool.page_size) // pool.layout.granularity, 0).to(torch.int32)
-        metadata = LogStateLinearAttnMetadata(
-            phase=batch.phase, work_slots=work_slots, log_slots=log_slots, token_offsets=token_offsets,
-            conv_read_slots=conv_read_slots, conv_read_granules=conv_read_granules, replay_counts=replay_counts)
-        if batch.is_prefill:
-            self._prepare_direct_prefill(batch, metadata, pool)
-        batch.linear_attn_metadata = metadata
+            batch.linear_attn_metadata = self._prefill_metadata(batch, tables)
 
     @staticmethod
-    def _prepare_direct_prefill(batch, metadata, pool) -> None:
-        """logstate.py:214-272: the packed-sequence indices, the chunk
-        checkpoint slots, and per token the log write slot (none inside an
-        unlogged range) and the conv snapshot target: the token's own log
-        slot and granule at each granule end and at the sequence end, or a
-        checkpoint slot (granule 0 of a work slot, else the last granule)."""
-        lengths = [r.extend_len for r in batch.reqs]
-        granularity = pool.layout.granularity
-        device = pool.storage.device
-        metadata.prefill_indices = PackedLinearIndices.from_lengths(lengths, device, granularity)
-        metadata.cu_seqlens = metadata.prefill_indices.cu_seqlens
-        first_offsets = batch.cache_metadata.first_offsets
-        if first_offsets is None:
-            first_offsets = metadata.token_offsets.index_select(0, metadata.cu_seqlens[:-1]).tolist()
-        total = sum(lengths)
-        chunks = len(metadata.prefill_indices.chunk_indices)
-        host = torch.empty(3 * total + chunks, dtype=torch.int32, pin_memory=device.type == "cuda")
-        conv_slots, conv_granules, log_mask = host[:3 * total].view(3, total).numpy()
-        chunk_writes = host[3 * total:].numpy()
-        conv_slots.fill(-1)
-        conv_granules.fill(0)
-        log_mask.fill(1)
-        chunk_writes.fill(-1)
-        checkpoints = iter(sorted(batch.cache_metadata.checkpoint_writes))
-        checkpoint = next(checkpoints, None)
-        ranges: dict[int, list[tuple[int, int]]] = {}
-        for req, begin, end in batch.cache_metadata.checkpoint_ranges:
-            ranges.setdefault(req, []).append((begin, end))
-        token_begin = chunk_begin = 0
-        for i, req in enumerate(batch.reqs):
-            length, first = lengths[i], first_offsets[i]
-            token_end = token_begin + length
-            conv_slots[token_begin + granularity - 1 - first % granularity:token_end:granularity] = -2
-            if length:
-                conv_slots[token_end - 1] = -2
-            for begin, end in ranges.get(i, ()):
-                begin = max(0, begin - req.cached_len)
-                end = min(length, end - req.cached_len)
-                if begin < end:
-                    log_mask[token_begin + begin:token_begin + end] = 0
-                    conv_slots[token_begin + begin:token_begin + end] = -1
-            while checkpoint is not None and checkpoint[0] < token_end:
-                global_row, slot = checkpoint
-                row = global_row - token_begin
-                assert row >= 0
-                if (first + row + 1) % granularity == 0 or row + 1 == length:
-                    conv_slots[global_row] = slot
-                    conv_granules[global_row] = (
-                        0 if pool.allocator.slot(slot).kind == "work" else pool.layout.num_granules - 1)
-                    chunk_writes[chunk_begin + row // granularity] = slot
-                checkpoint = next(checkpoints, None)
-            token_begin += length
-            chunk_begin += (length + granularity - 1) // granularity
-        packet = host.to(device, non_blocking=device.type == "cuda")
-        metadata.chunk_write_slots = packet[3 * total:]
-        metadata.log_write_slots, metadata.conv_token_slots, metadata.conv_token_granules = (
-            make_logstate_prefill_writes(metadata.log_slots, metadata.token_offsets, packet, granularity))
+    def _decode_metadata(batch, t: _Tables) -> LogStateLinearAttnMetadata:
+        reqs = batch.padded_reqs
+        packet = batch.prepared_indices
+        if packet is not None and t.state.is_cuda:
+            work, logs, offsets, granules = gather_linear_slots(
+                packet, t.state, work_table=t.work, out_loc=batch.out_loc, page_size=t.pool.page_size).unbind(0)
+            counts = packet.replay_counts
+        else:
+            replay = batch.cache_metadata.replay_counts
+            replay = [0] * len(reqs) if replay is None else list(replay)
+            assert len(replay) == len(reqs)
+            host = np.asarray([[r.table_idx for r in reqs], replay], dtype=np.int64)
+            rows, counts = _upload(host, t.state.device).unbind(0)
+            work = t.work[rows, 0]
+            assert len(batch.positions) == len(reqs)
+            logs = t.state[rows, batch.positions.long()]
+            offsets = batch.out_loc.remainder(t.pool.page_size).to(torch.int32)
+            granules = torch.zeros_like(work)
+            counts = counts.to(torch.int32)
+        return LogStateLinearAttnMetadata(phase=batch.phase, work_slots=work, log_slots=logs, token_offsets=offsets,
+                                          conv_read_slots=work, conv_read_granules=granules, replay_counts=counts)
+
+    def _prefill_metadata(self, batch, t: _Tables) -> LogStateLinearAttnMetadata:
+        pool = t.pool
+        reqs = batch.reqs
+        lengths = np.asarray([r.extend_len for r in reqs], dtype=np.int64)
+        cached = np.asarray([r.cached_len for r in reqs], dtype=np.int64)
+        packet = batch.prepared_indices
+        if packet is not None and packet.token_table_ids is not None:
+            req_rows, token_rows, previous = packet.table_ids, packet.token_table_ids, packet.previous_positions
+        else:
+            ids = np.asarray([r.table_idx for r in reqs], dtype=np.int64)
+            req_rows, token_rows, previous = _upload(
+                np.concatenate([ids, np.repeat(ids, lengths), cached - 1]), t.state.device).split(
+                    [len(reqs), int(lengths.sum()), len(reqs)])
+        assert len(batch.positions) == len(token_rows)
+        work = t.work[req_rows, 0]
+        logs = t.state[token_rows, batch.positions.long()]
+        offsets = batch.out_loc.remainder(pool.page_size).to(torch.int32)
+        # the conv history: the snapshot at the previous position when it is logged, else the work slot's window
+        before = previous.clamp_min(0)
+        before_slots = t.state[req_rows, before]
+        before_granules = t.page[req_rows, before].remainder(pool.page_size) // pool.layout.granularity
+        logged_before = (previous >= 0) & (before_slots >= 0)
+        conv_read_slots = torch.where(logged_before, before_slots, work)
+        conv_read_granules = torch.where(logged_before, before_granules, 0).to(torch.int32)
+
+        gran = pool.layout.granularity
+        indices = PackedLinearIndices.from_lengths(lengths, pool.storage.device, gran)
+        cm = batch.cache_metadata
+        first = cm.first_offsets
+        if first is None:  # read back from the device (a sync, as in the reference)
+            first = offsets.index_select(0, indices.cu_seqlens[:-1]).tolist()
+        plan = _upload(logstate_prefill_plan(lengths, cached, first, cm.checkpoint_writes, cm.checkpoint_ranges,
+                                             gran, pool.layout.num_granules,
+                                             lambda s: pool.allocator.slot(s).kind == "work"),
+                       pool.storage.device)
+        T = int(lengths.sum())
+        log_writes, conv_slots, conv_granules = make_logstate_prefill_writes(logs, offsets, plan, gran)
+        return LogStateLinearAttnMetadata(
+            phase=batch.phase, work_slots=work, log_slots=logs, token_offsets=offsets,
+            conv_read_slots=conv_read_slots, conv_read_granules=conv_read_granules,
+            replay_counts=torch.empty(0, dtype=torch.int32, device=pool.storage.device),
+            cu_seqlens=indices.cu_seqlens, prefill_indices=indices, chunk_write_slots=plan[3 * T:],
+            log_write_slots=log_writes, conv_token_slots=conv_slots, conv_token_granules=conv_granules)
 
     # ------------------------------------------------------------ decode graphs
     def init_capture_graph(self, max_seq_len: int, bs_list: list[int]) -> None:
@@ -217,104 +309,86 @@ class GatedDeltaLogStateBackend:
         self.capture_bs = sorted(bs_list)
         self.capture = LogStateLinearAttnCaptureData.make(max(bs_list), self.ctx.linear_state.storage.device)
 
+    def _refresh_capture(self, metadata: LogStateLinearAttnMetadata, bs: int) -> LogStateLinearAttnMetadata:
+        """The six decode fields of ``metadata`` into the first ``bs`` capture
+        entries (one launch); returns the metadata that reads them."""
+        assert self.capture is not None and bs in self.capture_bs
+        assert isinstance(metadata, LogStateLinearAttnMetadata)
+        target = self.capture.view(bs)
+        copy_metadata([getattr(metadata, f).to(torch.int32) for f in _DECODE_FIELDS],
+                      [getattr(target, f) for f in _DECODE_FIELDS])
+        return target
+
     def prepare_for_capture(self, batch) -> None:
-        """logstate.py:285-292: the batch's metadata, copied into the capture
-        buffers, which the captured decode then reads."""
-        assert self.capture is not None and batch.size in self.capture_bs
+        """logstate.py:285-292."""
         self.prepare_metadata(batch)
-        batch.linear_attn_metadata = self._copy_to_capture(batch.linear_attn_metadata, batch.size)
+        batch.linear_attn_metadata = self._refresh_capture(batch.linear_attn_metadata, batch.size)
 
     def prepare_for_replay(self, batch) -> None:
-        """logstate.py:294-299: the fresh metadata of ``batch`` into the
-        capture buffers."""
-        bs = batch.padded_size
-        assert self.capture is not None and bs in self.capture_bs
-        self._copy_to_capture(batch.linear_attn_metadata, bs)
-
-    def _copy_to_capture(self, metadata, bs: int) -> "LogStateLinearAttnMetadata":
-        """logstate.py:301-329: one batched copy of the six decode fields."""
-        assert self.capture is not None and isinstance(metadata, LogStateLinearAttnMetadata)
-        copy_metadata(tuple(getattr(metadata, name).to(torch.int32) for name in _CAPTURED),
-                      tuple(getattr(self.capture, name)[:bs] for name in _CAPTURED))
-        return LogStateLinearAttnMetadata(phase="decode",
-                                          **{name: getattr(self.capture, name)[:bs] for name in _CAPTURED})
+        """logstate.py:294-299."""
+        self._refresh_capture(batch.linear_attn_metadata, batch.padded_size)
 
     # ------------------------------------------------------------ forward
     def forward(self, mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, batch, out=None):
         """gdn_logstate.py:19-59."""
         metadata = batch.linear_attn_metadata
-        assert isinstance(metadata, LogStateLinearAttnMetadata)
-        assert metadata.phase == batch.phase
-        if batch.is_prefill:
-            return self._forward_prefill(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, metadata, out)
+        assert isinstance(metadata, LogStateLinearAttnMetadata) and metadata.phase == batch.phase
         if batch.is_verify:
             raise NotImplementedError("LogState speculative verify is not implemented yet.")
-        return self._forward_decode(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, metadata, out)
+        run = self._prefill if batch.is_prefill else self._decode
+        return run(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, metadata, out)
 
-    @staticmethod
-    def _split_qkv(mixed_qkv, config):
-        """gdn_logstate.py:61-83."""
-        query, key, value = torch.split(mixed_qkv, [config.key_dim, config.key_dim, config.value_dim], dim=-1)
-        seq_len = mixed_qkv.shape[1]
-        return (query.reshape(mixed_qkv.shape[0], seq_len, -1, config.head_k_dim),
-                key.reshape(mixed_qkv.shape[0], seq_len, -1, config.head_k_dim),
-                value.reshape(mixed_qkv.shape[0], seq_len, -1, config.head_v_dim))
+    def _sequence_index(self, n: int, device) -> torch.Tensor:
+        """0..n-1 (int32) on ``device``, from a cached vector."""
+        ids = self._sequence_ids
+        if ids is None or ids.numel() < n or ids.device != torch.device(device):
+            ids = self._sequence_ids = torch.arange(max(n, 64), dtype=torch.int32, device=device)
+        return ids[:n]
 
-    def _forward_prefill(self, mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, metadata, out=None):
-        """gdn_logstate.py:85-172."""
+    def _prefill(self, mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, m, out=None):
         pool = self.ctx.linear_state
-        layer = config.layer_idx
-        assert metadata.cu_seqlens is not None and metadata.prefill_indices is not None
-        assert metadata.chunk_write_slots is not None
-        assert metadata.conv_token_slots is not None and metadata.conv_token_granules is not None
-        assert metadata.log_write_slots is not None
-        storage = pool.storage.view(pool.dtype)
-        history = pool.read_conv(metadata.conv_read_slots, metadata.conv_read_granules, layer)
-        mixed = packed_causal_conv1d(
-            mixed_qkv, conv_weight, history, metadata.cu_seqlens, metadata.prefill_indices.conv_chunks,
-            state_io=PackedConvStateIO(storage=storage, slots=metadata.conv_token_slots,
-                                       granules=metadata.conv_token_granules, final_slots=metadata.work_slots,
-                                       frame_table=pool.conv_frame_table, frame_bytes=pool.frame_bytes,
-                                       layer=layer),
-        ).unsqueeze(0)
-        query, key, value = self._split_qkv(mixed, config)
-        query, key, value, prepared_gate, prepared_beta = prepare_gdn(query, key, value, gate.unsqueeze(0),
-                                                                      beta.unsqueeze(0), A_log, dt_bias)
-        layout = pool.layout
-        output, _ = chunk_gated_delta_rule_to_cache(
-            query, key, value, prepared_gate, prepared_beta,
-            ChunkStateIO(storage=storage, read_slots=metadata.work_slots,
-                         chunk_write_slots=metadata.chunk_write_slots, final_write_slots=metadata.work_slots,
-                         payload_frames=pool.payload_frame_table, frame_bytes=pool.frame_bytes,
-                         head_payload_bytes=pool.head_payload_bytes, layer=layer,
-                         num_layers=layout.num_linear_layers, granularity=layout.granularity,
-                         page_size=pool.page_size),
-            metadata.cu_seqlens,
-            chunk_size=layout.granularity,
-            log_io=ChunkLogIO(slots=metadata.log_write_slots, token_offsets=metadata.token_offsets,
-                              decay_frames=pool.decay_frame_table, gate=prepared_gate, page_size=pool.page_size,
-                              decay_record_bytes=layout.log_decay_bytes, num_key_heads=layout.num_key_heads),
-            out=None if out is None else out.unsqueeze(0),
-            return_v_new=False,  # v' goes to the log only
-        )
-        return output.squeeze(0)
+        layout, layer = pool.layout, config.layer_idx
+        assert m.prefill_indices is not None and m.chunk_write_slots is not None
+        assert m.conv_token_slots is not None and m.conv_token_granules is not None and m.log_write_slots is not None
+        frames16 = pool.storage.view(pool.dtype)
+        cu = m.cu_seqlens
+        assert cu is not None
+        history = pool.read_conv(m.conv_read_slots, m.conv_read_granules, layer).contiguous()
+        # conv + SiLU + split + prepare_gdn in one pass, the history read as a pool of one slot per sequence
+        q, k, v, g, b = prefill_frontend(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config,
+                                         history.unsqueeze(1), cu,
+                                         self._sequence_index(history.shape[0], history.device), layer=0)
+        conv_windows_logstate(
+            mixed_qkv, history, cu,
+            PackedConvStateIO(storage=frames16, slots=m.conv_token_slots, granules=m.conv_token_granules,
+                              final_slots=m.work_slots, frame_table=pool.conv_frame_table,
+                              frame_bytes=pool.frame_bytes, layer=layer),
+            conv_weight.shape[-1])
+        states = ChunkStateIO(storage=frames16, read_slots=m.work_slots, chunk_write_slots=m.chunk_write_slots,
+                              final_write_slots=m.work_slots, payload_frames=pool.payload_frame_table,
+                              frame_bytes=pool.frame_bytes, head_payload_bytes=pool.head_payload_bytes, layer=layer,
+                              num_layers=layout.num_linear_layers, granularity=layout.granularity,
+                              page_size=pool.page_size)
+        log = ChunkLogIO(slots=m.log_write_slots, token_offsets=m.token_offsets, decay_frames=pool.decay_frame_table,
+                         gate=g, page_size=pool.page_size, decay_record_bytes=layout.log_decay_bytes,
+                         num_key_heads=layout.num_key_heads)
+        o, _ = chunk_gated_delta_rule_to_cache(q, k, v, g, b, states, cu, chunk_size=layout.granularity,
+                                               log_io=log, out=None if out is None else out.unsqueeze(0),
+                                               return_v_new=False)
+        return o.squeeze(0)
 
-    def _forward_decode(self, mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, metadata, out=None):
-        """gdn_logstate.py:174-224."""
+    def _decode(self, mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, m, out=None):
         pool = self.ctx.linear_state
-        layer = config.layer_idx
-        query, key, value = conv_decode(
-            mixed_qkv, conv_weight, config, split_qkv=True,
-            read_slots=metadata.conv_read_slots, read_granules=metadata.conv_read_granules,
-            write_slots=metadata.log_slots, write_granules=metadata.token_offsets // pool.layout.granularity,
-            work_slots=metadata.work_slots, pool=pool,
-        )
-        output = fused_recurrent_gated_delta_rule_to_logstate(
-            query, key, value, gate.unsqueeze(1), beta.unsqueeze(1), A_log, dt_bias, pool,
-            metadata.work_slots, metadata.log_slots, metadata.token_offsets, layer, metadata.replay_counts,
-            enable_eager_state=self.enable_eager_state, out=None if out is None else out.unsqueeze(1),
-        )
-        return output.squeeze(1)
+        q, k, v = conv_decode(mixed_qkv, conv_weight, config, split_qkv=True, read_slots=m.conv_read_slots,
+                              read_granules=m.conv_read_granules, write_slots=m.log_slots,
+                              write_granules=m.token_offsets // pool.layout.granularity, work_slots=m.work_slots,
+                              pool=pool)
+        o = fused_recurrent_gated_delta_rule_to_logstate(
+            q, k, v, gate.unsqueeze(1), beta.unsqueeze(1), A_log, dt_bias, pool, m.work_slots, m.log_slots,
+            m.token_offsets, config.layer_idx, m.replay_counts, enable_eager_state=self.enable_eager_state,
+            out=None if out is None else out.unsqueeze(1))
+        return o.squeeze(1)
 
 
-__all__ = ["GatedDeltaLogStateBackend", "LogStateLinearAttnCaptureData", "LogStateLinearAttnMetadata"]
+__all__ = ["GatedDeltaLogStateBackend", "LogStateLinearAttnCaptureData", "LogStateLinearAttnMetadata",
+           "logstate_prefill_plan"]

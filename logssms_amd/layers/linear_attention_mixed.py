@@ -14,11 +14,14 @@ to shapes that depend on the bucket only:
 * padded write slots are -1 (the kernels skip them), padded index entries are
   0 (they read the first real row), padded chunk pairs are ``(0, capacity)``
   (a chunk starting past the packed tokens, which the kernels clamp away);
-* decode slot tables become int64.
+* decode slot tables of the standard backend become int64.
 
-All padding of one bucket is one ``gdn_metadata_pad`` launch; no device
-tensor is read on the host.  Only the standard (radix-pool) metadata is
-handled -- the LogState variant is not part of this library.
+Both backends' metadata are handled: the standard (radix / Marconi pool)
+``LinearAttnMetadata`` with 64-token chunks, and the LogState
+``LogStateLinearAttnMetadata`` with chunks of the pool's granularity and its
+per-token log / snapshot tables (``mixed.py:90-121``).  All padding of one
+bucket is one ``gdn_metadata_pad`` launch; no device tensor is read on the
+host.
 """
 
 from __future__ import annotations
@@ -27,12 +30,17 @@ from dataclasses import fields, is_dataclass, replace
 
 import torch
 
+from ..core import get_global_ctx
 from ..kernel.metadata import copy_metadata, pad_metadata
 from .linear_attention_backend import LinearAttnMetadata
+from .linear_attention_logstate import LogStateLinearAttnMetadata
 
-# prefill tables padded to the bucket's chunk capacity, and their fill values
-_CHUNK_TABLE_FILLS = {"chunk_write_slots": -1, "checkpoint_slots": -1, "checkpoint_chunks": 0,
-                      "snapshot_rows": 0, "snapshot_reqs": 0}
+# standard prefill tables padded to the bucket's chunk capacity (at most one
+# checkpoint per chunk), and their fill values: padded index entries read the
+# first real row, padded destinations are -1 (skipped)
+_CHUNK_TABLE_FILLS = {"checkpoint_slots": -1, "checkpoint_chunks": 0, "snapshot_rows": 0, "snapshot_reqs": 0}
+# LogState per-token tables padded to the token capacity
+_LOGSTATE_TOKEN_FILLS = {"log_slots": -1, "token_offsets": 0, "log_write_slots": -1, "conv_token_granules": 0}
 _DECODE_SLOT_TABLES = ("slots", "read_slots", "write_slots")
 
 
@@ -70,7 +78,7 @@ def prepare_mixed_linear_metadata(prefill, decode, prefill_capacity: int):
     are real; ``cu_seqlens`` and request-level arrays keep their actual
     values.  The input metadata objects are left unmodified."""
     pm, dm = prefill.linear_attn_metadata, decode.linear_attn_metadata
-    if not isinstance(pm, LinearAttnMetadata):
+    if not isinstance(pm, (LinearAttnMetadata, LogStateLinearAttnMetadata)):
         raise TypeError("mixed prefill requires prepared linear metadata")
     if type(dm) is not type(pm) or (pm.phase, dm.phase) != ("prefill", "decode"):
         raise ValueError("mixed metadata requires matching prefill/decode backends")
@@ -84,21 +92,30 @@ def prepare_mixed_linear_metadata(prefill, decode, prefill_capacity: int):
         raise ValueError("prepare ordinary actual-length metadata before normalization")
     if pm.chunk_write_slots is None or pm.conv_token_slots is None:
         raise ValueError("mixed prefill requires direct-write metadata")
-    missing = [name for name in _CHUNK_TABLE_FILLS if getattr(pm, name) is None]
+    logstate = isinstance(pm, LogStateLinearAttnMetadata)
+    per_token, per_chunk = (_LOGSTATE_TOKEN_FILLS, {}) if logstate else ({}, _CHUNK_TABLE_FILLS)
+    missing = [name for name in (*per_token, *per_chunk) if getattr(pm, name) is None]
     if missing:
         raise ValueError(f"missing prefill {missing[0]}")
+    # LogState chunks are the pool's checkpoint granularity (mixed.py:90-93)
+    chunk = get_global_ctx().linear_state.layout.granularity if logstate else 64
 
-    chunks = chunk_capacity(len(lengths), prefill_capacity)
+    chunks = chunk_capacity(len(lengths), prefill_capacity, chunk)
     padding = _Padding()
     packed = replace(
         indices,
         chunk_indices=padding.add(indices.chunk_indices, chunks, pair_tail=prefill_capacity),
         conv_chunks=padding.add(indices.conv_chunks, chunk_capacity(len(lengths), prefill_capacity, 64),
                                 pair_tail=prefill_capacity))
-    prefill_tables = {name: padding.add(getattr(pm, name), chunks, fill) for name, fill in _CHUNK_TABLE_FILLS.items()}
-    prefill_tables["conv_token_slots"] = padding.add(pm.conv_token_slots, prefill_capacity, -1)
+    prefill_tables = {"chunk_write_slots": padding.add(pm.chunk_write_slots, chunks, -1),
+                      "conv_token_slots": padding.add(pm.conv_token_slots, prefill_capacity, -1)}
+    prefill_tables.update({name: padding.add(getattr(pm, name), chunks, fill) for name, fill in per_chunk.items()})
+    prefill_tables.update({name: padding.add(getattr(pm, name), prefill_capacity, fill)
+                           for name, fill in per_token.items()})
+    if logstate:
+        prefill_tables["cu_seqlens"] = packed.cu_seqlens
     decode_tables = {name: getattr(dm, name).to(torch.int64) for name in _DECODE_SLOT_TABLES
-                     if getattr(dm, name) is not None}
+                     if isinstance(dm, LinearAttnMetadata) and getattr(dm, name) is not None}
     padding.flush()
     normalized = (replace(pm, prefill_indices=packed, **prefill_tables), replace(dm, **decode_tables))
     prefill.linear_attn_metadata, decode.linear_attn_metadata = normalized

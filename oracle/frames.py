@@ -37,7 +37,7 @@ from __future__ import annotations
 
 import torch
 
-from .gdn import chunk_gated_delta_rule_to_cache, l2norm, softplus_decode
+from .gdn import _scale_inputs, chunk_gated_delta_rule_to_cache, l2norm, softplus_decode
 
 
 def frame_state_index(frames, slots, layer, HV, dk, dv, itemsize, frame_bytes, head_bytes):
@@ -194,13 +194,17 @@ def conv_element_index(conv_frames, slots, granules, layer, C, S, frame_elems):
 
 
 def conv_decode_logstate(x, weight, storage, conv_frames, frame_bytes, layer, read_slots, read_granules,
-                         write_slots, write_granules, work_slots, *, round_conv=False):
+                         write_slots, write_granules, work_slots, *, round_conv=False, input_boundaries=None,
+                         input_scales=(1.0, 1.0, 1.0)):
     """``conv_decode`` with the LogState pool (``conv_decode.py:293-352`` with
     ``pool=``, kernel ``:25-289``): the window is read from (read slot, read
     granule), and the shifted window goes to (write slot, write granule) and to
     granule 0 of the work slot.  ``storage`` ([num_frames, frame elements], the
-    io dtype) is modified in place.  Returns y [B, C]."""
+    io dtype) is modified in place.  The input is scaled per channel range
+    (``conv_decode.py:142``, ``_scale_conv_input``) before the conv and the
+    window.  Returns y [B, C]."""
     B, C = x.shape
+    x = _scale_inputs(x, torch.arange(C)[None, :], input_boundaries or (C, C), input_scales)
     W = weight.shape[-1]
     S = W - 1
     fe = frame_bytes // storage.element_size()

@@ -197,3 +197,86 @@ def commit_speculative(state_table, work_state_table, uid, C, num_sampled, page_
         for p in range(live_pos, min(live_pos + page_size, len(row))):
             row[p] = verify
         work_state_table[uid][cand] = live
+
+
+def logstate_prefill_plan(lengths, cached_lens, first_offsets, checkpoint_writes, checkpoint_ranges, granularity,
+                          num_granules, work_slots):
+    """layers/linear_attention_backend/logstate.py:215-272 -- the host part of
+    the LogState prefill write plan, token by token.
+
+    ``lengths`` / ``cached_lens`` / ``first_offsets`` per request (the page
+    offset of its first new token); ``checkpoint_writes`` = (global token
+    row, slot) pairs; ``checkpoint_ranges`` = (request, begin, end) position
+    ranges whose tokens are not logged; ``work_slots`` = the set of slots of
+    kind "work".  Returns dict of python lists: ``conv_slots`` (per token: -1
+    none, -2 the token's own log slot, else a checkpoint slot),
+    ``conv_granules``, ``log_enabled`` (0 / 1) and ``chunk_writes`` (per
+    ``granularity``-token chunk of each request, -1 or a checkpoint slot).
+
+    Per request: every token at a granule end ((first + row + 1) %
+    granularity == 0) and its last token are marked -2; a token inside an
+    unlogged range (positions relative to cached_len, clipped to the request)
+    gets log_enabled 0 and conv slot -1; then, in sorted order, a checkpoint
+    whose row lies in this request and sits at a granule end or at the
+    request's last token sets the token's conv slot and granule (0 for a work
+    slot, else the last granule) and its chunk's write slot.  Later
+    checkpoints overwrite earlier ones; checkpoints elsewhere are ignored.
+    """
+    total = sum(lengths)
+    conv_slots = [-1] * total
+    conv_granules = [0] * total
+    log_enabled = [1] * total
+    chunk_writes = [-1] * sum((n + granularity - 1) // granularity for n in lengths)
+    pending = sorted(checkpoint_writes)
+    k = 0
+    token_begin = chunk_begin = 0
+    for i, length in enumerate(lengths):
+        first = first_offsets[i]
+        token_end = token_begin + length
+        for row in range(length):
+            if (first + row + 1) % granularity == 0 or row + 1 == length:
+                conv_slots[token_begin + row] = -2
+        for req, begin, end in checkpoint_ranges:
+            if req != i:
+                continue
+            for row in range(max(0, begin - cached_lens[i]), min(length, end - cached_lens[i])):
+                log_enabled[token_begin + row] = 0
+                conv_slots[token_begin + row] = -1
+        while k < len(pending) and pending[k][0] < token_end:
+            global_row, slot = pending[k]
+            row = global_row - token_begin
+            assert row >= 0
+            if (first + row + 1) % granularity == 0 or row + 1 == length:
+                conv_slots[global_row] = slot
+                conv_granules[global_row] = 0 if slot in work_slots else num_granules - 1
+                chunk_writes[chunk_begin + row // granularity] = slot
+            k += 1
+        token_begin = token_end
+        chunk_begin += (length + granularity - 1) // granularity
+    return dict(conv_slots=conv_slots, conv_granules=conv_granules, log_enabled=log_enabled,
+                chunk_writes=chunk_writes)
+
+
+def logstate_prefill_writes(log_slots, token_offsets, plan, granularity):
+    """kernel/metadata.py:150-178 (make_logstate_prefill_writes) -- the device
+    half of the plan: per token, the log write slot (its log slot where
+    logging is enabled, else -1), the conv snapshot slot (its log slot where
+    the plan says -2) and granule (its page offset // granularity there)."""
+    log_writes, conv_slots, conv_granules = [], [], []
+    for t, slot in enumerate(log_slots):
+        conv = plan["conv_slots"][t]
+        log_writes.append(slot if plan["log_enabled"][t] else -1)
+        conv_slots.append(slot if conv == -2 else conv)
+        conv_granules.append(token_offsets[t] // granularity if conv == -2 else plan["conv_granules"][t])
+    return log_writes, conv_slots, conv_granules
+
+
+def logstate_decode_slots(work_table, state_table, reqs, out_loc, page_size):
+    """logstate.py:128-175 (decode branch) and kernel/metadata.py:290-300
+    (gather_linear_slots, LogState) -- per decode request (table_idx,
+    cached_len): the work slot, the log slot at the new position, the page
+    offset of its KV location, and conv read granule 0."""
+    work = [work_table[t][0] for t, _ in reqs]
+    logs = [state_table[t][c] for t, c in reqs]
+    offsets = [loc % page_size for loc in out_loc]
+    return work, logs, offsets, [0] * len(reqs)

@@ -44,7 +44,8 @@ def test_header_declares_expected_entry_points():
             "gdn_conv_decode", "gdn_store_state", "gdn_copy_rows", "gdn_zero_rows",
             "gdn_commit_accepted", "gdn_prefill_qk", "gdn_prefill_fused", "gdn_conv_snapshots",
             "gdn_rms_norm_gated", "gdn_metadata_copy", "gdn_metadata_pad", "gdn_prefill_fused_noalloc",
-            "gdn_prefill_noalloc_scratch_bytes", "gdn_probe_rmw"} <= names
+            "gdn_prefill_noalloc_scratch_bytes", "gdn_gather_linear_slots"} <= names
+    assert "gdn_probe_rmw" not in names  # the bench-only probe lives in libgdn_probe.so
 
 
 def test_ctypes_table_matches_header():
@@ -66,7 +67,7 @@ def test_library_loads_and_exports_every_symbol():
     lib = _lib.lib()
     for name in _declarations():
         assert hasattr(lib, name), name
-    assert lib.gdn_abi_version() == 4
+    assert lib.gdn_abi_version() == 5
     assert lib.gdn_prefill_noalloc_scratch_bytes() == 64 << 20
     assert lib.gdn_last_error() in (b"",) or isinstance(lib.gdn_last_error(), bytes)
 

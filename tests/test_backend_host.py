@@ -318,11 +318,11 @@ def test_marconi_copy_blocks_rejects_aliasing():
 
 
 def test_chunk_entry_rejects_what_it_does_not_cover():
-    """A token log without frame storage is rejected, and frame tables /
-    granularities below 64 with head_v_dim 32 raise NotImplementedError,
-    before anything is launched."""
+    """A token log without frame storage is rejected, and head_v_dim other
+    than 32 or a multiple of 64 raises NotImplementedError (plain pools at
+    any granularity, and frame tables), before anything is launched."""
     from logssms_amd.kernel.linear_attention import ChunkLogIO, ChunkStateIO, chunk_gated_delta_rule_to_cache
-    T, H, dk, dv = 4, 1, 32, 32
+    T, H, dk, dv = 4, 1, 32, 48
     q = torch.zeros(1, T, H, dk, dtype=torch.bfloat16)
     v = torch.zeros(1, T, H, dv, dtype=torch.bfloat16)
     g = torch.zeros(1, T, H)
@@ -341,3 +341,41 @@ def test_chunk_entry_rejects_what_it_does_not_cover():
                           head_payload_bytes=2048)
     with pytest.raises(NotImplementedError):
         chunk_gated_delta_rule_to_cache(q, q, v, g, g, frames, cu)
+
+
+@pytest.mark.parametrize("granularity", [16, 32, 64])
+def test_logstate_prefill_plan_matches_oracle(granularity):
+    """The vectorised LogState prefill plan (layers/linear_attention_logstate.py)
+    against the oracle's token-by-token statement of logstate.py:215-272:
+    random batches with granule-end and off-granule checkpoints (some
+    duplicated, some past the batch), work and log checkpoint slots, and
+    unlogged ranges (some clipped, some of absent requests)."""
+    import numpy as np
+
+    from logssms_amd.layers.linear_attention_logstate import logstate_prefill_plan
+    rng = random.Random(granularity)
+    for trial in range(60):
+        n = rng.randrange(1, 6)
+        lengths = [rng.choice([1, granularity - 1, granularity, granularity + 1, rng.randrange(1, 300)])
+                   for _ in range(n)]
+        cached = [rng.randrange(0, 500) for _ in range(n)]
+        first = [rng.randrange(0, 256) for _ in range(n)]
+        total = sum(lengths)
+        writes = [(rng.randrange(0, total + 5), rng.randrange(0, 40)) for _ in range(rng.randrange(0, 12))]
+        starts = np.concatenate([[0], np.cumsum(lengths)])
+        for i in range(n):  # checkpoints at the marked rows too
+            row = rng.randrange(lengths[i])
+            writes.append((int(starts[i]) + lengths[i] - 1, rng.randrange(0, 40)))
+            writes.append((int(starts[i]) + row, rng.randrange(0, 40)))
+        if writes and rng.random() < 0.5:
+            writes.append(writes[0])
+        ranges = [(rng.randrange(-1, n + 1), cached[0] + rng.randrange(-20, 200), cached[0] + rng.randrange(0, 400))
+                  for _ in range(rng.randrange(0, 4))]
+        work = {s for s in range(40) if s % 3 == 0}
+        got = logstate_prefill_plan(lengths, cached, first, writes, ranges, granularity, 7, lambda s: s in work)
+        want = md.logstate_prefill_plan(lengths, cached, first, writes, ranges, granularity, 7, work)
+        assert got.dtype == np.int32
+        assert got[:total].tolist() == want["conv_slots"], trial
+        assert got[total:2 * total].tolist() == want["conv_granules"], trial
+        assert got[2 * total:3 * total].tolist() == want["log_enabled"], trial
+        assert got[3 * total:].tolist() == want["chunk_writes"], trial

@@ -69,3 +69,67 @@ def test_full_config_prefill_matches_oracle(name, fused):
     assert torch.equal(got_conv, want_conv), "conv pool differs from the oracle"
     print(f"{name} {'fused' if fused else 'two-step'}: output max-abs {out_err:.3e}, "
           f"{len(written)} written states max-abs {state_err:.3e}", flush=True)
+
+
+def test_full_config3_decode_matches_oracle():
+    """Config 3 as ``bench.py`` builds it: 256 sequences, in-place
+    read-modify-write of random-permutation slots of a 1024-slot fp32 pool
+    (2 GiB) and its bf16 conv pool, against the oracle's batched decode on
+    host copies: outputs within 1e-2 + 2e-2 |e|, the 256 written states within
+    1e-3, conv windows bit-exact, the other 768 slots untouched."""
+    step, t = bench.decode_gpu(DEV)
+    conv0, state0 = t["conv"].cpu(), t["state"].cpu()
+    h = {k: v.cpu() for k, v in t.items() if k not in ("conv", "state", "out")}
+    print("config 3 decode: 256 sequences on the GPU", flush=True)
+    step()
+    torch.cuda.synchronize()
+    got_o, got_conv, got_state = t["out"].cpu(), t["conv"].cpu(), t["state"].cpu()
+    conv, state = conv0.clone(), state0.clone()
+    want_o = ref.forward_decode_batched(h["mixed"], h["gate"], h["beta"], h["weight"], h["A_log"], h["dt_bias"],
+                                        conv, state, 0, h["reads"], h["writes"], bench.H, bench.D, bench.HV, bench.D)
+    assert_bf16_close(got_o, want_o.view(got_o.shape))
+    slots = h["writes"].long()
+    err = float((got_state[slots] - state[slots]).abs().max())
+    assert err <= 1e-3, f"written state max-abs error {err:.3e}"
+    assert torch.equal(got_conv, conv), "conv pool differs from the oracle"
+    untouched = torch.ones(state.shape[0], dtype=torch.bool)
+    untouched[slots] = False
+    assert torch.equal(got_state[untouched], state0[untouched])
+    print(f"config 3 decode: output max-abs {float((got_o.float() - want_o.float().view(got_o.shape)).abs().max()):.3e}, "
+          f"states {err:.3e}", flush=True)
+
+
+def test_full_config5_verify_and_commit_match_oracle():
+    """Config 5 as ``bench.py`` builds it: 64 sequences x 8 drafts from random
+    live slots, every per-step state and conv window written to 512 fresh
+    slots, against the oracle's batched verify on host copies (outputs within
+    1e-2 + 2e-2 |e|, the 512 step states within 1e-3, windows bit-exact, other
+    slots untouched); then the commit copies each sequence's accepted step
+    (accepted ~ U{1..8}) into its live slot, bit for bit."""
+    step, commit, t = bench.verify_gpu(DEV)
+    conv0, state0 = t["conv"].cpu(), t["state"].cpu()
+    h = {k: v.cpu() for k, v in t.items() if k not in ("conv", "state", "out")}
+    print("config 5 verify: 64 x 8 drafts on the GPU", flush=True)
+    step()
+    torch.cuda.synchronize()
+    got_o, got_conv, got_state = t["out"].cpu(), t["conv"].cpu(), t["state"].cpu()
+    conv, state = conv0.clone(), state0.clone()
+    want_o = ref.forward_verify_batched(h["mixed"], h["gate"], h["beta"], h["weight"], h["A_log"], h["dt_bias"],
+                                        conv, state, 0, h["live"], h["writes"], bench.H, bench.D, bench.HV, bench.D)
+    assert_bf16_close(got_o, want_o.view(got_o.shape))
+    written = h["writes"].reshape(-1).long()
+    err = float((got_state[written] - state[written]).abs().max())
+    assert err <= 1e-3, f"step state max-abs error {err:.3e}"
+    assert torch.equal(got_conv, conv), "conv pool differs from the oracle"
+    untouched = torch.ones(state.shape[0], dtype=torch.bool)
+    untouched[written] = False
+    assert torch.equal(got_state[untouched], state0[untouched])
+    # commit: live[b] <- step accepted[b] - 1 of sequence b, state and conv window
+    commit()
+    torch.cuda.synchronize()
+    live, acc = h["live"].long(), h["accepted"].long()
+    src = h["writes"].long()[torch.arange(len(live)), acc - 1]
+    assert torch.equal(t["state"].cpu()[live], got_state[src])
+    assert torch.equal(t["conv"].cpu()[live], got_conv[src])
+    print(f"config 5 verify: output max-abs {float((got_o.float() - want_o.float().view(got_o.shape)).abs().max()):.3e}, "
+          f"states {err:.3e}; commit bit-exact", flush=True)

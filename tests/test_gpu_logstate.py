@@ -90,10 +90,10 @@ def test_granularity_checkpoints_plain_pool(chunk_size):
     assert torch.equal(host[2 * N + 3], storage[2 * N + 3])
 
 
-def _frame_setup(g, slots, layers, HV, dk, dv, frame_bytes, head_bytes, spare=7):
-    """A fragmented frame storage: every slot's frames drawn at random from a
-    shuffled pool with spare frames, unused table columns -1."""
-    fps = -(-layers * HV * head_bytes // frame_bytes)
+def _frame_setup(g, slots, layers, HV, dk, dv, frame_bytes, head_bytes, spare=7, min_fps=1):
+    """A fragmented frame storage: every slot's frames (at least min_fps)
+    drawn at random from a shuffled pool with spare frames."""
+    fps = max(min_fps, -(-layers * HV * head_bytes // frame_bytes))
     num_frames = slots * fps + spare
     order = torch.randperm(num_frames, generator=g)[:slots * fps]
     frames = order.reshape(slots, fps).to(torch.int32)
@@ -102,8 +102,11 @@ def _frame_setup(g, slots, layers, HV, dk, dv, frame_bytes, head_bytes, spare=7)
 
 
 # (dk, dv, frame_bytes, head_bytes): two heads per frame; a head over two
-# frames; a padded head (128 x 192 bf16 = 48 KiB in a 64 KiB payload)
-FRAME_CASES = [(128, 128, 65536, 32768), (128, 128, 16384, 32768), (128, 192, 131072, 65536)]
+# frames; a padded head (128 x 192 bf16 = 48 KiB in a 64 KiB payload);
+# d_v = 32 (a 32-column workgroup slice): 32 x 32 heads inside a frame, and
+# 128 x 32 heads over two frames
+FRAME_CASES = [(128, 128, 65536, 32768), (128, 128, 16384, 32768), (128, 192, 131072, 65536), (32, 32, 16384, 2048),
+               (128, 32, 4096, 8192)]
 
 
 @pytest.mark.parametrize("chunk_size", [32, 16, 64])
@@ -153,16 +156,21 @@ def test_frame_table_states(case, chunk_size):
     assert torch.equal(host.reshape(-1)[mask], storage.reshape(-1)[mask])
 
 
+# (dk, dv, frame_bytes, head_bytes)
+LOG_SHAPES = [(128, 128, 65536, 32768), (32, 32, 16384, 2048)]
+
+
+@pytest.mark.parametrize("shape", LOG_SHAPES)
 @pytest.mark.parametrize("direct", [False, True])
-def test_chunk_token_log(direct):
+def test_chunk_token_log(direct, shape):
     """ChunkLogIO: each logged token's v' rows, key rows and gate land in its
     log slot (state_io.py:83-126); keys and gates bit-exact, v' rows to the
     output tolerance, every other byte untouched.  direct: no v_new asked
     for, so the chunk kernel writes the v' rows into the log itself."""
     from logssms_amd.kernel.linear_attention import ChunkLogIO, ChunkStateIO, chunk_gated_delta_rule_to_cache
     g = gen(71)
-    H, HV, dk, dv, layers, layer, gran, page = 2, 4, 128, 128, 2, 1, 32, 64
-    frame_bytes, head_bytes = 65536, 32768
+    dk, dv, frame_bytes, head_bytes = shape
+    H, HV, layers, layer, gran, page = 2, 4, 2, 1, 32, 64
     lengths = [100, 37]
     cu = _cu(lengths)
     T, N = cu[-1], len(lengths)
@@ -181,7 +189,9 @@ def test_chunk_token_log(direct):
             pos.append(t % page)
     log_slot[5] = -1  # one token without a log
     slots = next_slot
-    storage, frames = _frame_setup(g, slots, layers, HV, dk, dv, frame_bytes, head_bytes, spare=2)
+    log_bytes = 2 * page * layers * (H * dk + HV * dv)  # a slot's frames also hold its log
+    storage, frames = _frame_setup(g, slots, layers, HV, dk, dv, frame_bytes, head_bytes, spare=2,
+                                   min_fps=-(-log_bytes // frame_bytes))
     record = 4 * layers * page * HV
     # decay records: 32 to a frame, in extra frames appended to the storage
     n_dec = -(-slots // (frame_bytes // record))

@@ -123,3 +123,58 @@ def test_commit_speculative_remaps_pages():
     # positions 6,7 are on page 1 (last = 7 -> cand 1); position 8 on page 2 (cand 2)
     assert table[0] == [1] * 4 + [101] * 4 + [102] * 4
     assert work[0] == [100, 2, 3, 103, 104]
+
+
+def test_logstate_prefill_plan_known_answer():
+    """layers/linear_attention_backend/logstate.py:215-272 worked by hand on a
+    granularity-4 page: request 0 (6 tokens from page offset 1, nothing
+    cached), request 1 (3 tokens from offset 2 after 5 cached).
+
+    Marks (-2): request 0 at rows whose offset closes a granule ((1 + row + 1)
+    % 4 == 0: row 2) and its last row 5; request 1 at row 1 and its last row
+    2 (global 7, 8).  The unlogged range (1, 5, 7) covers positions 5, 6 =
+    rows 0, 1 of request 1 (global 6, 7): not logged, no snapshot.
+    Checkpoints, sorted: (1, 10) sits at no mark: ignored.  (5, 11) at the
+    last row of request 0: slot 11 (a work slot: granule 0), chunk 5 // 4 = 1.
+    (7, 12) at a granule end inside the unlogged range: the snapshot goes to
+    slot 12 (granule 3 = the last of 4) while the token stays unlogged; its
+    chunk is chunk 0 of request 1 = global chunk 2.  (8, 9) and then (8, 13)
+    at request 1's last row, the same token and chunk: 13 wins.  (20, 14)
+    lies past the batch: never reached."""
+    plan = md.logstate_prefill_plan(
+        [6, 3], [0, 5], [1, 2], [(8, 13), (1, 10), (5, 11), (7, 12), (8, 9), (20, 14)], [(1, 5, 7)],
+        granularity=4, num_granules=4, work_slots={11})
+    assert plan["conv_slots"] == [-1, -1, -2, -1, -1, 11, -1, 12, 13]
+    assert plan["conv_granules"] == [0, 0, 0, 0, 0, 0, 0, 3, 3]
+    assert plan["log_enabled"] == [1, 1, 1, 1, 1, 1, 0, 0, 1]
+    assert plan["chunk_writes"] == [-1, 11, 13]
+
+
+def test_logstate_prefill_plan_unlogged_range_clipping():
+    """A range reaching before the cached prefix and past the request is
+    clipped to the request's own rows; ranges of other requests do nothing."""
+    plan = md.logstate_prefill_plan([5], [10], [2], [], [(0, 4, 12), (3, 0, 100)], granularity=4,
+                                    num_granules=2, work_slots=set())
+    # positions 10..14 are rows 0..4; the range [4, 12) covers rows 0, 1
+    assert plan["log_enabled"] == [0, 0, 1, 1, 1]
+    # marks: (2 + row + 1) % 4 == 0 at row 1 (cleared by the range), last row 4
+    assert plan["conv_slots"] == [-1, -1, -1, -1, -2]
+    assert plan["chunk_writes"] == [-1, -1]
+
+
+def test_logstate_prefill_writes_known_answer():
+    """kernel/metadata.py:150-178: -2 resolves to the token's log slot at
+    granule offset // granularity; disabled tokens get no log write."""
+    plan = {"conv_slots": [-2, -2, 5, -1], "conv_granules": [0, 0, 2, 0], "log_enabled": [1, 0, 1, 1]}
+    writes, conv, granules = md.logstate_prefill_writes([7, 7, 7, 8], [3, 7, 11, 12], plan, 4)
+    assert writes == [7, -1, 7, 8]
+    assert conv == [7, 7, 5, -1]
+    assert granules == [0, 1, 2, 0]
+
+
+def test_logstate_decode_slots_known_answer():
+    """tests/layers/test_logstate_linear_attention_backend.py:74-96: a decode
+    at position 20 of a row whose first page logs to slot 0, work slot 2."""
+    state = [[0] * 64 + [1] * 64, [1] * 128]
+    work = [[2], [3]]
+    assert md.logstate_decode_slots(work, state, [(0, 20)], [20], 64) == ([2], [0], [20], [0])
