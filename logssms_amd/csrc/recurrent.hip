@@ -5,9 +5,15 @@
 // once and written once per launch (decode) or once per step (verify); the
 // arithmetic (two column reductions and a rank-1 update) is ~6 flop/element,
 // far below the CDNA4 balance point, so no MFMA is used.  The state lives in
-// VGPRs for all steps of a launch: thread (rg, cg) owns 4 consecutive columns
-// (one 16-byte global access) of rows rg, rg + RG, rg + 2 RG, ..., so each
-// load instruction of the block covers RG full rows contiguously.
+// VGPRs for all steps of a launch, 4 consecutive columns (one 16-byte access)
+// per row and lane.
+//   * wave_kernel (decode and verify with the conv, gdn_fused_conv_recurrent):
+//     one wave per 32 columns of a v-head, the column sums as in-wave
+//     butterflies, every state load of a (sequence, key head) block issued up
+//     front (see the kernel).
+//   * recurrent_kernel (the standalone recurrence): thread (rg, cg) owns
+//     columns 4 cg.. of rows rg, rg + RG, ..., so each load instruction of the
+//     block covers RG full rows contiguously; column sums through LDS.
 //
 // Both column reductions (S^T k and S^T q) are taken from the decayed state
 // in one pass, using o = e^g S^T q + delta (k.q) with S' = e^g S + k delta^T
@@ -338,35 +344,19 @@ __global__ __launch_bounds__(kThreads) void recurrent_kernel(RecParams p) {
   store_final<DK, DV, ST>(p, st, b, h);
 }
 
-// Fused conv + recurrence: one block per (sequence, key head) owning the q/k
-// channels of that key head and the v channels of its HV/H v-heads, so the
-// conv window of every channel is read and rewritten by exactly one block
-// (in-place decode, read slot == write slot, is race free).
-template <int DK, int DV, class IOT, class ST, bool kStreamLoads>
-__global__ __launch_bounds__(kThreads) void fused_kernel(RecParams p) {
-  extern __shared__ __align__(16) char smem_raw[];
-  constexpr int CG = DV / 4;
-  constexpr int RG = kThreads / CG;
-  constexpr int RPT = DK / RG;
-  const int64_t b = blockIdx.x / p.H;
-  const int64_t kh = blockIdx.x % p.H;
-  const int group = static_cast<int>(p.HV / p.H);
-  const int steps = static_cast<int>(p.T);
-  Smem s = carve<DK, DV>(smem_raw, steps, group);
+// Conv of one key head's group of channels (q and k of key head kh, v of its
+// `group` v-heads) over `steps` tokens, one channel per thread tid, tid +
+// nthreads, ... (conv_decode.py:25-289 per step): raw q, k into s.qn / s.kn,
+// v into s.vv, and each step's shifted window to that step's write slot.  A
+// negative read slot is a zero history.
+template <int DK, int DV, class IOT>
+__device__ __forceinline__ void conv_group(const RecParams& p, Smem& s, int64_t b, int64_t kh, int group, int steps,
+                                           int tid, int nthreads) {
   const int64_t key_dim = p.H * DK;
   const int nch = 2 * DK + group * DV;
   const int W = p.kernel_width;
   const int64_t read_slot = load_index(p.read_slots, b * p.read_stride, p.read_is64);
-  // The first v-head's state is requested before the conv, so its latency
-  // overlaps the conv's window loads (decode at config 3: 218-223 us, within
-  // the box-to-box spread of the later load, at an unchanged 4 waves per SIMD).  Verify also requests each next v-head's
-  // state before the current one's last store (261 -> 254 us at config 5).
-  // Decode keeps one state live at a time: the second register set halves its
-  // occupancy, and its in-place update measured slower with it (213 -> 223 us).
-  constexpr bool kPrefetch = !kStreamLoads;
-  float st[RPT][4];
-  load_state<DK, DV, ST, kStreamLoads>(p, st, b, kh * group);
-  for (int c = threadIdx.x; c < nch; c += kThreads) {
+  for (int c = tid; c < nch; c += nthreads) {
     int64_t ch;
     float* dst;
     int dst_stride;
@@ -386,9 +376,9 @@ __global__ __launch_bounds__(kThreads) void fused_kernel(RecParams p) {
     }
     float win[8];
     float w[9];
-    const IOT* cs = static_cast<const IOT*>(p.conv_state) + read_slot * p.conv_slot_stride +
+    const IOT* cs = static_cast<const IOT*>(p.conv_state) + (read_slot >= 0 ? read_slot : 0) * p.conv_slot_stride +
                     p.layer * p.conv_layer_stride + ch * (W - 1);
-    for (int i = 0; i < W - 1; ++i) win[i] = to_f32(cs[i]);
+    for (int i = 0; i < W - 1; ++i) win[i] = read_slot >= 0 ? to_f32(cs[i]) : 0.f;
     for (int i = 0; i < W; ++i) w[i] = to_f32(static_cast<const IOT*>(p.conv_w)[ch * W + i]);
     const float bias = p.conv_b ? to_f32(static_cast<const IOT*>(p.conv_b)[ch]) : 0.f;
     for (int t = 0; t < steps; ++t) {
@@ -411,12 +401,19 @@ __global__ __launch_bounds__(kThreads) void fused_kernel(RecParams p) {
       }
     }
   }
-  __syncthreads();
+}
+
+// The q / k L2 norms and k.q of each staged token, and the gates of each
+// (token, v-head) (fused_recurrent.py:202-215; gate/beta rows follow the
+// token rows: (row, head) strides).
+template <int DK>
+__device__ __forceinline__ void norm_group(const RecParams& p, Smem& s, int64_t b, int64_t kh, int group, int steps,
+                                           int tid, int nthreads) {
   // gate/beta rows follow the token rows: (row, head) strides
   {
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    for (int t = wave; t < steps; t += kThreads / 64) {
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    for (int t = wave; t < steps; t += nthreads / 64) {
       float sq = 0.f, sk = 0.f;
       for (int i = lane; i < DK; i += 64) {
         const float qv = s.qn[t * DK + i], kv = s.kn[t * DK + i];
@@ -437,7 +434,7 @@ __global__ __launch_bounds__(kThreads) void fused_kernel(RecParams p) {
       kq = wave_sum<64>(kq);
       if (lane == 0) s.kq[t] = kq;
     }
-    for (int i = threadIdx.x; i < steps * group; i += kThreads) {
+    for (int i = tid; i < steps * group; i += nthreads) {
       const int t = i / group, j = i % group;
       const int64_t h = kh * group + j;
       const int64_t flat = b * p.T + t;
@@ -451,25 +448,193 @@ __global__ __launch_bounds__(kThreads) void fused_kernel(RecParams p) {
       s.beta[i] = sigmoid(bv);
     }
   }
-  __syncthreads();
-  for (int j = 0; j < group; ++j) {
-    const int64_t h = kh * group + j;
-    if (!kPrefetch && j > 0) load_state<DK, DV, ST, kStreamLoads>(p, st, b, h);
-    run_steps<DK, DV, IOT, ST>(p, s, st, b, h, j, group, 0, steps, true);
-    if constexpr (kPrefetch) {
-      float next[RPT][4];
-      if (j + 1 < group) load_state<DK, DV, ST, kStreamLoads>(p, next, b, h + 1);
-      store_final<DK, DV, ST>(p, st, b, h);
-      if (j + 1 < group) {
+}
+
+// Three zero elements of any io type: the conv history of a negative read slot.
+__device__ const uint32_t kZeroWindow[4] = {0u, 0u, 0u, 0u};
+
+// Block-uniform index read through the scalar data cache (waited on with the
+// LDS / scalar counter, never behind the block's vector loads).
+__device__ __forceinline__ int64_t scalar_index(const void* p, int64_t i, int is64) {
+  typedef __attribute__((address_space(4))) const int32_t ci32;
+  return static_cast<int64_t>(reinterpret_cast<ci32*>(reinterpret_cast<uintptr_t>(p))[is64 ? 2 * i : i]);
+}
+
+// The bits of one io element (zero-extended 16-bit or 32-bit) and its value.
+// (read through a global address-space pointer, so the load is a global load
+// that the waits count exactly, whatever the pointer's origin)
+template <class T> __device__ __forceinline__ uint32_t raw_bits(const T* p) {
+  typedef __attribute__((address_space(1))) const uint16_t g16;
+  typedef __attribute__((address_space(1))) const uint32_t g32;
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  if constexpr (sizeof(T) == 2) return *reinterpret_cast<g16*>(a);
+  else return *reinterpret_cast<g32*>(a);
+}
+template <class T> __device__ __forceinline__ float f32_from_bits(uint32_t r);
+template <> __device__ __forceinline__ float f32_from_bits<bf16>(uint32_t r) { return __uint_as_float(r << 16); }
+template <> __device__ __forceinline__ float f32_from_bits<f16>(uint32_t r) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r)));
+}
+template <> __device__ __forceinline__ float f32_from_bits<float>(uint32_t r) { return __uint_as_float(r); }
+
+// Decode and verify with one wave per 32 state columns of a v-head (d_v a
+// multiple of 32, d_k in {32, 64, 128}): one block per (sequence, key head)
+// of group * d_v / 32 waves.  Lane (rg = lane / 8, cg = lane % 8) of a wave
+// holds state columns 4 cg .. 4 cg + 3 of its 32 and rows rg RPT .. rg RPT +
+// RPT - 1 (RPT = d_k / 8), moved as RPT 16-byte pieces (each load or store
+// instruction of a wave covers 8 rows of 128 contiguous bytes).  Every wave
+// issues its state loads before the conv phase, so all of the group's states
+// are in flight while the conv runs; a step's column sums (S^T k, S^T q) are
+// butterflies over the wave's 8 row groups (lanes xor 8, 16, 32), with no LDS
+// round trip and no block barrier.  A negative read slot is a zero state, a
+// negative write slot takes no write.
+template <int DK, int DV, class IOT, class ST, bool kStream, bool kEarlyConv>
+__global__ __launch_bounds__(1024) void wave_kernel(RecParams p) {
+  extern __shared__ __align__(16) char smem_raw[];
+  constexpr int WPH = DV / 32;  // waves per v-head
+  constexpr int RPT = DK / 8;   // state rows per lane
+  static_assert(DV % 32 == 0 && RPT % 4 == 0, "d_v % 32 == 0, d_k in {32, 64, 128}");
+  const int group = static_cast<int>(p.HV / p.H);
+  const int steps = static_cast<int>(p.T);
+  const int64_t b = blockIdx.x / p.H;
+  const int64_t kh = blockIdx.x % p.H;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, rg = lane >> 3, cg = lane & 7;
+  const int j = wave / WPH;  // v-head of the group
+  const int64_t h = kh * group + j;
+  const int c0 = (wave % WPH) * 32 + 4 * cg;  // first state column of the lane
+  const int r0 = rg * RPT;                    // first state row of the lane
+  Smem s = carve<DK, DV>(smem_raw, steps, group);
+  ST* const pool = static_cast<ST*>(p.state);
+  const int64_t head_off = p.layer * p.layer_stride + h * p.head_stride + static_cast<int64_t>(r0) * DV + c0;
+  const int64_t rs = scalar_index(p.read_slots, b * p.read_stride, p.read_is64);
+  // kEarlyConv (decode with conv width 4 and at most one channel per thread,
+  // chosen by the host): the conv inputs are requested (as raw bits,
+  // branch-free, idle threads reading a clamped channel) before the state, and
+  // unpacked after it, so the conv waits for them alone (a wave's loads return
+  // in order) while the state arrives.
+  const int nch = 2 * DK + group * DV;
+  constexpr bool early_conv = kEarlyConv;
+  const int c = threadIdx.x < nch ? static_cast<int>(threadIdx.x) : nch - 1;
+  const int64_t key_dim = p.H * DK;
+  const int64_t ch = c < DK ? kh * DK + c
+                            : (c < 2 * DK ? key_dim + kh * DK + (c - DK) : 2 * key_dim + kh * group * DV + (c - 2 * DK));
+  float* const cdst = c < DK ? s.qn + c : (c < 2 * DK ? s.kn + (c - DK) : s.vv + (c - 2 * DK));
+  uint32_t rwin[3] = {0u, 0u, 0u}, rw[4] = {0u, 0u, 0u, 0u}, rx = 0u, rb = 0u;
+  if (early_conv) {
+    // a negative read slot reads its (zero) history from a zero array: no select on loaded data
+    const IOT* ccs = rs >= 0 ? static_cast<const IOT*>(p.conv_state) + rs * p.conv_slot_stride +
+                                   p.layer * p.conv_layer_stride + ch * 3
+                             : reinterpret_cast<const IOT*>(kZeroWindow);
+    const int64_t row = p.row_index ? scalar_index(p.row_index, b, p.row_index_is64) : b;
+    const IOT* wts = static_cast<const IOT*>(p.conv_w) + ch * 4;
 #pragma unroll
-        for (int i = 0; i < RPT; ++i)
+    for (int i = 0; i < 3; ++i) rwin[i] = raw_bits(ccs + i);
 #pragma unroll
-          for (int c = 0; c < 4; ++c) st[i][c] = next[i][c];
-      }
-    } else {
-      store_final<DK, DV, ST>(p, st, b, h);
+    for (int i = 0; i < 4; ++i) rw[i] = raw_bits(wts + i);
+    rx = raw_bits(static_cast<const IOT*>(p.mixed) + row * p.mixed_row_stride + ch * p.mixed_col_stride);
+    rb = raw_bits(p.conv_b ? static_cast<const IOT*>(p.conv_b) + ch : wts);  // no branch: a bias-less read is unused
+  }
+  float st[RPT][4];
+  {
+    const ST* src = pool + (rs >= 0 ? rs : 0) * p.slot_stride + head_off;
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      if constexpr (kStream) Vec4<ST>::load_nt(src + i * DV, st[i]);
+      else Vec4<ST>::load(src + i * DV, st[i]);
     }
-    __syncthreads();
+  }
+  if (early_conv) {  // conv_decode.py:25-289 for one token, as conv_group computes it
+    float win[3], acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) win[i] = f32_from_bits<IOT>(rwin[i]);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) acc = fmaf(f32_from_bits<IOT>(rw[i]), win[i], acc);
+    const float x = f32_from_bits<IOT>(rx);
+    acc = fmaf(f32_from_bits<IOT>(rw[3]), x, acc);
+    acc += p.conv_b ? f32_from_bits<IOT>(rb) : 0.f;
+    if (p.round_conv) acc = round_to<IOT>(acc);
+    if (static_cast<int>(threadIdx.x) < nch) {
+      *cdst = round_to<IOT>(silu(acc));
+      const int64_t ws = load_index(p.write_slots, b * p.write_b, p.write_is64);
+      if (ws >= 0) {
+        IOT* out = static_cast<IOT*>(p.conv_state) + ws * p.conv_slot_stride + p.layer * p.conv_layer_stride + ch * 3;
+        out[0] = from_f32<IOT>(win[1]);
+        out[1] = from_f32<IOT>(win[2]);
+        out[2] = from_f32<IOT>(x);
+      }
+    }
+  } else {
+    conv_group<DK, DV, IOT>(p, s, b, kh, group, steps, threadIdx.x, blockDim.x);
+  }
+  __syncthreads();
+  norm_group<DK>(p, s, b, kh, group, steps, threadIdx.x, blockDim.x);
+  __syncthreads();
+  if (rs < 0) {
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) st[i][c] = 0.f;
+  }
+  auto store_state = [&](int64_t slot) __attribute__((always_inline)) {
+    ST* dst = pool + slot * p.slot_stride + head_off;
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) Vec4<ST>::store(dst + i * DV, st[i]);
+  };
+  for (int t = 0; t < steps; ++t) {
+    const float* kn = s.kn + t * DK + r0;
+    const float* qn = s.qn + t * DK + r0;
+    float pk[4] = {0.f, 0.f, 0.f, 0.f}, pq[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < RPT; i += 4) {
+      const float4 k4 = *reinterpret_cast<const float4*>(kn + i);
+      const float4 q4 = *reinterpret_cast<const float4*>(qn + i);
+      const float kr[4] = {k4.x, k4.y, k4.z, k4.w}, qr[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          pk[c] = fmaf(st[i + u][c], kr[u], pk[c]);
+          pq[c] = fmaf(st[i + u][c], qr[u], pq[c]);
+        }
+    }
+#pragma unroll
+    for (int m = 8; m < 64; m <<= 1)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        pk[c] += __shfl_xor(pk[c], m);
+        pq[c] += __shfl_xor(pq[c], m);
+      }
+    const float d = s.decay[t * group + j], bt = s.beta[t * group + j], kq = s.kq[t];
+    const float4 v4 = *reinterpret_cast<const float4*>(s.vv + (t * group + j) * DV + c0);
+    const float vr[4] = {v4.x, v4.y, v4.z, v4.w};
+    float dl[4], o[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      dl[c] = (vr[c] - d * pk[c]) * bt;
+      o[c] = d * pq[c] + dl[c] * kq;
+    }
+    if (rg == 0) {
+      const int64_t flat = b * p.T + t;
+      const int64_t orow = p.row_index ? load_index(p.row_index, flat, p.row_index_is64) : flat;
+      Vec4<IOT>::store(static_cast<IOT*>(p.out) + (orow * p.HV + h) * DV + c0, o);
+    }
+#pragma unroll
+    for (int i = 0; i < RPT; i += 4) {
+      const float4 k4 = *reinterpret_cast<const float4*>(kn + i);
+      const float kr[4] = {k4.x, k4.y, k4.z, k4.w};
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) st[i + u][c] = fmaf(kr[u], dl[c], d * st[i + u][c]);
+    }
+    if (p.write_t != 0) {  // verify: every step's state to its slot
+      const int64_t slot = load_index(p.write_slots, b * p.write_b + t * p.write_t, p.write_is64);
+      if (slot >= 0) store_state(slot);
+    }
+  }
+  if (p.write_t == 0) {  // decode: the final state
+    const int64_t slot = load_index(p.write_slots, b * p.write_b, p.write_is64);
+    if (slot >= 0) store_state(slot);
   }
 }
 
@@ -641,12 +806,18 @@ extern "C" int gdn_fused_conv_recurrent(const void* mixed, int64_t row_stride, i
       using IOT = decltype(iot);
       using ST = decltype(stt);
       const size_t shm = smem_bytes<DK, DV>(static_cast<int>(steps), static_cast<int>(HV / H));
-      if (steps == 1)  // decode: streaming state loads
-        hipLaunchKernelGGL((fused_kernel<DK, DV, IOT, ST, true>), dim3(static_cast<unsigned>(batch * H)),
-                           dim3(kThreads), shm, static_cast<hipStream_t>(stream), p);
+      const dim3 grid(static_cast<unsigned>(batch * H));
+      auto s = static_cast<hipStream_t>(stream);
+      const unsigned waves = static_cast<unsigned>((HV / H) * (DV / 32));
+      // decode: streaming state loads, and the conv inputs fetched before the state
+      // when the conv has width 4 and at most one channel per thread
+      const bool early = kernel_width == 4 && 2 * DK + (HV / H) * DV <= 64 * static_cast<int64_t>(waves);
+      if (steps == 1 && early)
+        hipLaunchKernelGGL((wave_kernel<DK, DV, IOT, ST, true, true>), grid, dim3(64 * waves), shm, s, p);
+      else if (steps == 1)
+        hipLaunchKernelGGL((wave_kernel<DK, DV, IOT, ST, true, false>), grid, dim3(64 * waves), shm, s, p);
       else
-        hipLaunchKernelGGL((fused_kernel<DK, DV, IOT, ST, false>), dim3(static_cast<unsigned>(batch * H)),
-                           dim3(kThreads), shm, static_cast<hipStream_t>(stream), p);
+        hipLaunchKernelGGL((wave_kernel<DK, DV, IOT, ST, false, false>), grid, dim3(64 * waves), shm, s, p);
       return GDN_LAUNCH_CHECK("gdn_fused_conv_recurrent launch");
     });
   });
