@@ -507,8 +507,40 @@ def _probe_lib():
     lib.gdn_probe_rmw.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
                                   ctypes.c_void_p]
     lib.gdn_probe_rmw.restype = ctypes.c_int
+    lib.gdn_probe_mfma.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    lib.gdn_probe_mfma.restype = ctypes.c_int
     lib.gdn_probe_last_error.restype = ctypes.c_char_p
     return lib
+
+
+def mfma_ceiling(dev, steps=10, warmup=3, iters=4096):
+    """The box's sustained dense-f16 matrix-core rate: ``gdn_probe_mfma``
+    (independent 16x16x32 f16 MFMA chains in every wave, 4 and 8 waves per
+    CU, 4 workgroups per CU), timed like the kernels.  Under this load the
+    engine clock falls below its 2.4 GHz maximum, so the rate lies below the
+    published 2.5 PFLOP/s; the chunk kernel's fraction of it is reported beside
+    the fraction of the published peak."""
+    from logssms_amd import _lib
+    probe = _probe_lib()
+    props = torch.cuda.get_device_properties(dev)
+    blocks = 4 * props.multi_processor_count
+    runs = []
+    for threads in (256, 512):
+        out = torch.empty(blocks * threads, device=dev)
+        stream = _lib.stream_of(out)
+
+        def run():
+            rc = probe.gdn_probe_mfma(out.data_ptr(), blocks, threads, iters, stream)
+            if rc:
+                raise RuntimeError(f"gdn_probe_mfma failed ({rc}): {probe.gdn_probe_last_error().decode()}")
+        ms = _time(run, steps, warmup)
+        flop = blocks * (threads // 64) * iters * 8 * 16384
+        runs.append({"waves_per_cu": 4 * threads // 64, "ms": ms, "TFLOP/s": flop / (ms * 1e-3) / 1e12})
+        del out
+    best = max(runs, key=lambda r: r["TFLOP/s"])
+    return {"config": f"gdn_probe_mfma: {blocks} workgroups, 8 independent v_mfma_f32_16x16x32_f16 chains per wave, "
+                      f"{iters} rounds", "best_TFLOP/s": best["TFLOP/s"],
+            "frac_of_published": best["TFLOP/s"] * 1e12 / PEAK_MFMA_16BIT, "runs": runs}
 
 
 def rmw_sweep(dev, steps, warmup, nbytes=2 << 30):
@@ -727,7 +759,7 @@ def main():
                     help="time budget of each CPU baseline leg (chunked prefill; naive prefill, decode and "
                          "verify get a share of it)")
     ap.add_argument("--only", choices=["all", "prefill", "decode", "verify", "norm", "layer", "logstate", "copy",
-                                       "rmw"],
+                                       "rmw", "mfma"],
                     default="all",
                     help="'copy' times a plain 512 MiB device copy (the calibration kernel for the "
                          "FETCH_SIZE / WRITE_SIZE counter passes); 'rmw' the in-place read-modify-write "
@@ -790,6 +822,10 @@ def main():
                       "algorithmic_flop_per_launch": flops, "algorithmic_bytes_per_launch": chunk_bytes},
         )
         extra["prefill_qk_and_snapshot_ms"] = ms - chunk_ms
+        if args.only == "all":
+            ceil = mfma_ceiling(dev)
+            ceil["chunk_kernel_frac_of_ceiling"] = achieved / (ceil["best_TFLOP/s"] * 1e12)
+            extra["mfma_ceiling"] = ceil
         if not args.no_cpu_baseline:
             chunked, naive = prefill_cpu_legs(inp, 4096, 256, args.cpu_seconds)
             result["cpu_baseline"] = {**chunked, **cpu_info, "kind": "port", "naive_recurrence": naive}
@@ -814,6 +850,9 @@ def main():
 
     if args.only == "rmw":
         print(json.dumps({"rmw": rmw_sweep(dev, max(args.steps, 10), args.warmup)}))
+        return
+    if args.only == "mfma":
+        print(json.dumps({"mfma_ceiling": mfma_ceiling(dev, max(args.steps, 10), args.warmup)}))
         return
     if args.only in ("all", "decode"):
         step, tensors = decode_gpu(dev)

@@ -621,14 +621,14 @@ int gdn_rms_norm_gated(const void* x, int dtype, int64_t rows, int64_t cols, con
  * memory (code under HIP graph capture, serving loops or harnesses that
  * forbid hipMalloc): the fused prefill of gdn_prefill_qk + gdn_prefill_fused
  * + gdn_conv_snapshots in one call, with the staging the first launch hands
- * to the second (f16 q/k operands, head-major g/beta) kept in a 64 MiB
+ * to the second (f16 q/k operands, head-major g/beta) kept in a 256 MiB
  * file-scope device array of the library, one per GPU, instead of
  * caller-allocated buffers.  It allocates nothing.  Inputs, pools, slots and
  * `out` [T, HV, dv] as in those three entry points (snapshot_rows/slots[count]
  * as gdn_conv_snapshots' rows/slots; no final write slots).
  * Returns GDN_ERR_INVALID when the staging, 2 * align256(T * H * dk * 2) +
  * 2 * align256(T * HV * 4) bytes, exceeds gdn_prefill_noalloc_scratch_bytes()
- * (7,943 tokens at Qwen3-Next shape, H = 16, HV = 32, dk = 128), and
+ * (31,775 tokens at Qwen3-Next shape, H = 16, HV = 32, dk = 128), and
  * GDN_ERR_UNSUPPORTED for shapes outside the fused kernel.  Calls on one GPU
  * share the array: calls that overlap on one GPU (unordered streams) race.
  * The device must be current on the calling thread.

@@ -20,7 +20,7 @@
 namespace gdn {
 namespace {
 
-constexpr size_t kScratchBytes = size_t(64) << 20;  // 64 MiB per GPU
+constexpr size_t kScratchBytes = size_t(256) << 20;  // 256 MiB per GPU
 constexpr int kMaxDevices = 64;
 
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];

@@ -7,6 +7,11 @@
 // read against, and a store-only stream (the write ceiling for verify's
 // per-step state stores).
 //
+// It also holds the matrix-core ceiling probe: gdn_probe_mfma runs independent
+// 16x16x32 f16 MFMA chains on every CU, the dense-f16 rate the chunk kernel's
+// MFMA fraction can be read against besides the published peak (under a
+// sustained MFMA load the engine clock drops below its 2.4 GHz maximum).
+//
 // int gdn_probe_rmw(void* buf, int64_t bytes, int64_t block_bytes,
 //                   int loads_in_flight, int nontemporal, void* stream):
 // buf[i] <- buf[i] * 1.0 in place over `bytes` (16-byte vectors), each block
@@ -82,6 +87,31 @@ __global__ __launch_bounds__(256) void store_kernel(f4v* buf, int64_t n_vec, int
   }
 }
 
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+
+// Each wave runs `iters` rounds of 8 independent 16x16x32 f16 MFMAs (fp32
+// accumulators) and writes one value per lane so nothing is dead code.
+__global__ __launch_bounds__(512) void mfma_kernel(float* out, int iters) {
+  const int lane = threadIdx.x & 63;
+  h8v a, b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = static_cast<_Float16>(0.001f * (lane + i));
+    b[i] = static_cast<_Float16>(0.002f * (lane - i));
+  }
+  f4v acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = f4v{0.f, 0.f, 0.f, 0.f};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[i], 0, 0, 0);
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) sum += acc[i][0] + acc[i][1] + acc[i][2] + acc[i][3];
+  out[static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x] = sum;
+}
+
 template <int U>
 int launch_rmw(f4v* buf, int64_t n_vec, int64_t per_block, int nontemporal, hipStream_t s) {
   const int64_t blocks = (n_vec + per_block - 1) / per_block;
@@ -129,6 +159,19 @@ extern "C" int gdn_probe_rmw(void* buf, int64_t bytes, int64_t block_bytes, int 
       set_error("gdn_probe_rmw: loads_in_flight %d not in {0, 1, 2, 4, 8, 16}", loads_in_flight);
       return GDN_ERR_UNSUPPORTED;
   }
+}
+
+// Dense f16 matrix-core probe: `blocks` workgroups of `threads` (64..512,
+// a multiple of 64) threads, each wave 8 x iters MFMAs of 16 x 16 x 32
+// (16384 flop each); out holds blocks * threads floats.
+extern "C" int gdn_probe_mfma(float* out, int64_t blocks, int threads, int iters, void* stream) {
+  using namespace gdn;
+  GDN_REQUIRE(out && blocks > 0 && blocks <= 0x7fffffff && threads >= 64 && threads <= 512 && threads % 64 == 0 &&
+                  iters > 0,
+              "gdn_probe_mfma: bad sizes");
+  hipLaunchKernelGGL(mfma_kernel, dim3(static_cast<unsigned>(blocks)), dim3(threads), 0,
+                     static_cast<hipStream_t>(stream), out, iters);
+  return GDN_LAUNCH_CHECK("gdn_probe_mfma launch");
 }
 
 extern "C" const char* gdn_probe_last_error(void) { return gdn::g_probe_error; }

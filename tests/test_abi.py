@@ -68,7 +68,7 @@ def test_library_loads_and_exports_every_symbol():
     for name in _declarations():
         assert hasattr(lib, name), name
     assert lib.gdn_abi_version() == 5
-    assert lib.gdn_prefill_noalloc_scratch_bytes() == 64 << 20
+    assert lib.gdn_prefill_noalloc_scratch_bytes() == 256 << 20
     assert lib.gdn_last_error() in (b"",) or isinstance(lib.gdn_last_error(), bytes)
 
 

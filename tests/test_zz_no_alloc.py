@@ -13,10 +13,10 @@ from tests.test_gpu_fused_prefill import _cfg, _setup
 pytestmark = pytest.mark.gpu
 
 
-def _run_both(cfg, lengths, seed):
+def _run_both(cfg, lengths, seed, **pool_args):
     from logssms_amd.kernel.linear_attention.fused_backend import prefill_fused, prefill_fused_noalloc
-    pool_a, w, meta = _setup(cfg, lengths, gen(seed))
-    pool_b, _, _ = _setup(cfg, lengths, gen(seed))
+    pool_a, w, meta = _setup(cfg, lengths, gen(seed), **pool_args)
+    pool_b, _, _ = _setup(cfg, lengths, gen(seed), **pool_args)
     assert torch.equal(pool_a.recurrent_state, pool_b.recurrent_state)
     T = sum(lengths)
     args = (w["mixed"], w["gate"], w["beta"], w["weight"].contiguous(), w["A_log"], w["dt_bias"], cfg)
@@ -38,6 +38,18 @@ def test_noalloc_prefill_equals_allocating_entry_point_twice():
     _run_both(cfg, [300, 64, 5, 130], 901)
     print("noalloc call 2 (smaller): lengths [70, 3]", flush=True)
     _run_both(cfg, [70, 3], 902)
+
+
+def test_noalloc_prefill_at_config2_shape():
+    """BASELINE config 2's batch (4 x 4096 tokens, 16 / 32 heads, d = 128) fits
+    the array: bit for bit against the allocating entry point."""
+    from logssms_amd import _lib
+    cfg = _cfg(16, 32, 128, 128, layer=0)
+    lengths = [4096] * 4
+    need = 2 * sum(lengths) * 16 * 128 * 2 + 2 * sum(lengths) * 32 * 4
+    assert need <= _lib.lib().gdn_prefill_noalloc_scratch_bytes()
+    print("noalloc config 2: 4 x 4096 tokens, 16 / 32 heads", flush=True)
+    _run_both(cfg, lengths, 904, slots=160, layers=1)
 
 
 def test_noalloc_prefill_rejects_inputs_beyond_its_scratch():
