@@ -860,7 +860,7 @@ def main():
         nb = decode_bytes(256)
         extra["decode"] = {"config": "BASELINE config 3 (256 seqs, in-place RMW of randperm pool slots)",
                            "ms": ms, "bytes": nb, "GB/s": nb / (ms * 1e-3) / 1e9,
-                           "frac_hbm": nb / (ms * 1e-3) / PEAK_HBM, "traffic": _traffic("fused_kernel_decode_cfg3")}
+                           "frac_hbm": nb / (ms * 1e-3) / PEAK_HBM, "traffic": _traffic("wave_kernel_decode_cfg3")}
         if not args.no_cpu_baseline:
             extra["decode"]["cpu_baseline"] = {**decode_cpu_leg(tensors, args.cpu_seconds / 2), **cpu_info,
                                                "kind": "port"}
@@ -876,7 +876,7 @@ def main():
         cb = 64 * 2 * (S_BYTES + SC_BYTES)
         extra["verify"] = {"config": "BASELINE config 5 (64 seqs x 8 drafts, per-step states to slots)",
                            "ms": ms, "bytes": nb, "GB/s": nb / (ms * 1e-3) / 1e9,
-                           "frac_hbm": nb / (ms * 1e-3) / PEAK_HBM, "traffic": _traffic("fused_kernel_verify_cfg5"),
+                           "frac_hbm": nb / (ms * 1e-3) / PEAK_HBM, "traffic": _traffic("wave_kernel_verify_cfg5"),
                            "commit_ms": cms, "commit_GB/s": cb / (cms * 1e-3) / 1e9,
                            "commit_traffic": _traffic("commit_kernel_cfg5")}
         if not args.no_cpu_baseline:
