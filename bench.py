@@ -4,9 +4,9 @@ Headline (``value``): Qwen3-Next linear-attention layer prefill (BASELINE
 config 2) -- 4 x 4096 packed tokens, 16 qk / 32 v heads, d = 128, bf16
 projections, fp32 state pool, conv width 4.  One step = the backend prefill
 ``prefill_fused``: the q/k pass (conv + SiLU + L2 norm of the q/k channels),
-the chunk-kernel launch whose staging waves compute the v conv + SiLU and the
-gates of each chunk from mixed_qkv, writing the output and the final
-per-sequence states into pool slots, then the conv-window snapshot launch.
+then the chunk-kernel launch whose staging waves compute the v conv + SiLU and
+the gates of each chunk from mixed_qkv, writing the output, the final
+per-sequence states into pool slots and the conv windows into the conv pool.
 ``value`` is prefill tokens/s; ``roofline`` reports the chunk kernel (timed
 alone with events around its launch) against the dense 16-bit MFMA peak from
 the algorithmic flop count (10 C d + 6 d^2 + 2/3 C^2 per token per v-head).
@@ -252,8 +252,8 @@ def make_prefill_pools(inp, dev):
 
 def prefill_gpu(inp, dev, events=None, fused=True, pools=None):
     """One backend prefill step.  fused: ``prefill_fused`` (q/k pass, then the
-    chunk kernel computing the v conv + SiLU and the gates itself, then the
-    conv-snapshot launch); otherwise the two-step path (``prefill_frontend``
+    chunk kernel computing the v conv + SiLU and the gates itself and writing
+    the conv windows); otherwise the two-step path (``prefill_frontend``
     writing q, k, v, g, beta and then the windows, then the chunk kernel).
     `events` collects a (start, end) event pair around each chunk-kernel
     launch; `pools` = (conv_pool, state_pool) to run on, else fresh ones."""
@@ -821,7 +821,7 @@ def main():
                       "kernel": "chunk_chain_kernel<128, bf16, float, fused>", "kernel_ms": chunk_ms,
                       "algorithmic_flop_per_launch": flops, "algorithmic_bytes_per_launch": chunk_bytes},
         )
-        extra["prefill_qk_and_snapshot_ms"] = ms - chunk_ms
+        extra["prefill_outside_chunk_kernel_ms"] = ms - chunk_ms  # the q/k pass and the launch gaps
         if args.only == "all":
             ceil = mfma_ceiling(dev)
             ceil["chunk_kernel_frac_of_ceiling"] = achieved / (ceil["best_TFLOP/s"] * 1e12)

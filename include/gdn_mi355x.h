@@ -356,14 +356,15 @@ int gdn_logstate_store_states(void* storage, const void* payload_frames, int fra
 /*
  * The GDN prefill of one layer (layers/linear_attention_backend/gdn.py:100-150:
  * history gather, packed_causal_conv1d, split, prepare_gdn,
- * chunk_gated_delta_rule_to_cache) as three launches whose results equal
- * gdn_prefill_frontend followed by gdn_chunk_gated_delta_rule bit for bit:
+ * chunk_gated_delta_rule_to_cache) as two launches whose results equal
+ * gdn_prefill_frontend followed by gdn_chunk_gated_delta_rule and
+ * gdn_conv_snapshots bit for bit:
  *   1. gdn_prefill_qk: the q/k channels only -> normalised q, k, plus the
  *      prepared gates g, beta.
  *   2. gdn_prefill_fused: the chunk kernel, with the v conv + SiLU done by its
- *      staging waves from the projections (v never reaches HBM).
- *   3. gdn_conv_snapshots: conv windows into the pool, after 2 has read the
- *      histories (a snapshot may overwrite a baseline slot).
+ *      staging waves from the projections (v never reaches HBM), and the conv
+ *      windows of the snapshot rows written into the pool once the histories
+ *      are read (a snapshot may overwrite a baseline slot).
  * Each returns GDN_ERR_UNSUPPORTED, launching nothing, for shapes outside it:
  * kernel_width 4, bf16/f16 io, dk in {32, 64, 128}, dv % 64 == 0, 16-byte
  * aligned rows and conv pool, fp32 or io-typed state.
@@ -391,16 +392,19 @@ int gdn_prefill_qk(const void* mixed, int64_t row_stride, int io_dtype, const vo
  * gdn_prefill_fused: q, k (f16), g, beta ([HV, T]) from gdn_prefill_qk; mixed, weight,
  * conv_state and baseline_slots as there (the v channels' history, and the
  * initial recurrent state, come from baseline_slots); state pool,
- * chunk/final write slots and out as in gdn_chunk_gated_delta_rule.
+ * chunk/final write slots and out as in gdn_chunk_gated_delta_rule;
+ * snapshot_rows/slots[snapshot_count] as gdn_conv_snapshots' rows/slots
+ * (the windows it would write, written by this launch; count 0: none).
  */
 int gdn_prefill_fused(const void* q, const void* k, const void* mixed, int64_t row_stride, int io_dtype,
                       const void* weight, int kernel_width, const void* cu_seqlens, int cu_dtype, int64_t num_seqs,
-                      int64_t total_tokens, int64_t H, int64_t HV, int64_t dk, int64_t dv, const void* conv_state,
+                      int64_t total_tokens, int64_t H, int64_t HV, int64_t dk, int64_t dv, void* conv_state,
                       int64_t conv_slot_stride, int64_t conv_layer_stride, const float* g, const float* beta,
                       void* state, int state_dtype, int64_t slot_stride, int64_t layer_stride, int64_t head_stride,
                       int64_t layer, const void* baseline_slots, int baseline_dtype, const void* chunk_write_slots,
-                      int chunk_write_dtype, const void* final_write_slots, int final_write_dtype, void* out,
-                      float scale, void* stream);
+                      int chunk_write_dtype, const void* final_write_slots, int final_write_dtype,
+                      const void* snapshot_rows, int rows_dtype, const void* snapshot_slots, int slots_dtype,
+                      int64_t snapshot_count, void* out, float scale, void* stream);
 
 /*
  * gdn_conv_snapshots: for each i < count with slots[i] >= 0, conv_state[slots[i],
@@ -620,11 +624,11 @@ int gdn_rms_norm_gated(const void* x, int dtype, int64_t rows, int64_t cols, con
  * No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, serving loops or harnesses that
  * forbid hipMalloc): the fused prefill of gdn_prefill_qk + gdn_prefill_fused
- * + gdn_conv_snapshots in one call, with the staging the first launch hands
+ * (with its conv windows) in one call, with the staging the first launch hands
  * to the second (f16 q/k operands, head-major g/beta) kept in a 256 MiB
  * file-scope device array of the library, one per GPU, instead of
  * caller-allocated buffers.  It allocates nothing.  Inputs, pools, slots and
- * `out` [T, HV, dv] as in those three entry points (snapshot_rows/slots[count]
+ * `out` [T, HV, dv] as in those two entry points (snapshot_rows/slots[count]
  * as gdn_conv_snapshots' rows/slots; no final write slots).
  * Returns GDN_ERR_INVALID when the staging, 2 * align256(T * H * dk * 2) +
  * 2 * align256(T * HV * 4) bytes, exceeds gdn_prefill_noalloc_scratch_bytes()

@@ -34,7 +34,7 @@ SIGNATURES = {
     "gdn_prefill_qk": [P, I64, I32, P, I32, P, I32, I64, I64, I64, I64, P, I64, I64, I64, P, I32, P, P, I32, I64,
                        P, I64, I64, I32, P, I64, I64, I32, P, I32, P, I32, P, P, P],
     "gdn_prefill_fused": [P, P, P, I64, I32, P, I32, P, I32, I64, I64, I64, I64, I64, I64, P, I64, I64, P, P, P, I32,
-                          I64, I64, I64, I64, P, I32, P, I32, P, I32, P, F32, P],
+                          I64, I64, I64, I64, P, I32, P, I32, P, I32, P, I32, P, I32, I64, P, F32, P],
     "gdn_metadata_copy": [P, P, PI64, PI64, PI64, P, I32, P],
     "gdn_metadata_pad": [P, P, PI64, PI64, PI64, PI64, P, I32, P],
     "gdn_rms_norm_gated": [P, I32, I64, I64, P, I32, I64, I64, I64, I64, P, I32, F32, P, P],

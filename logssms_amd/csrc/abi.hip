@@ -24,4 +24,4 @@ int hip_status(hipError_t err, const char* what) {
 
 extern "C" const char* gdn_last_error(void) { return gdn::g_last_error; }
 
-extern "C" int gdn_abi_version(void) { return 5; }
+extern "C" int gdn_abi_version(void) { return 6; }

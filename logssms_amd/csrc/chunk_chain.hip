@@ -930,6 +930,112 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       }
     };
 
+    // Fused path: the conv windows of this sequence's snapshot rows (the raw
+    // inputs ending at each row, oldest first; before the sequence start, the
+    // history), written by the conv waves in the last chunk's first phase,
+    // while the chain runs that chunk.  Each workgroup writes its own v slice
+    // (whose history only its conv waves read, in the prologue) and a
+    // 1/members share of its key head's q and k channels (whose history the
+    // q/k pass read in the previous launch).  Writes into the baseline slot
+    // come last, after every read of that slot's history.
+    // Its parameters are read after the loop through an opaque kernarg-segment
+    // pointer and an opaque block index: loaded at kernel entry, they would
+    // hold scalar registers through every role's loop (the kernel is at its
+    // scalar register limit).  mixed, rs, vch, bos, len and hist are live in
+    // the conv loop anyway.  The first 256 entries of the snapshot list are
+    // loaded before the loop (lane l: entries l, 64 + l, 128 + l, 192 + l),
+    // so the end waits on no list load.
+    typedef __attribute__((address_space(4))) const ChunkParams kernarg_params;
+    constexpr int kSnapBlocks = 4;
+    int snap_row[kSnapBlocks], snap_slot[kSnapBlocks];
+    auto snapshot_prefetch = [&]() __attribute__((always_inline)) {
+#pragma unroll
+      for (int k = 0; k < kSnapBlocks; ++k) {
+        const int64_t i = 64 * k + lane;
+        snap_row[k] = snap_slot[k] = -1;
+        if (i < f.snap_count) {
+          snap_row[k] = static_cast<int>(load_index(f.snap_rows, i, f.snap_rows_is64));
+          snap_slot[k] = static_cast<int>(load_index(f.snap_slots, i, f.snap_slots_is64));
+        }
+      }
+    };
+    auto snapshot_windows = [&]() __attribute__((always_inline)) {
+      kernarg_params* ka = (kernarg_params*)__builtin_amdgcn_kernarg_segment_ptr();
+      asm volatile("" : "+s"(ka));
+      kernarg_params& q = *ka;
+      const int64_t count = q.front.snap_count;
+      if (count == 0 || !fv_thread) return;
+      uint32_t bid = blockIdx.x;
+      asm volatile("" : "+s"(bid));
+      const int64_t sl8 = bid / 8;
+      const int mem = static_cast<int>(sl8 % q.members);
+      const int64_t grp = (sl8 / q.members) * 8 + (bid % 8);
+      const int64_t khq = grp % q.H;
+      const int64_t cb = static_cast<int64_t>(mem % q.nvs) * 64;
+      const int64_t vw_ = q.DV - cb < 64 ? q.DV - cb : 64;
+      const int64_t share = (DK + q.members - 1) / q.members;
+      const int64_t q0 = mem * share;
+      const int64_t nq = q0 >= DK ? 0 : (DK - q0 < share ? DK - q0 : share);
+      const int64_t nch = 2 * nq + vw_;
+      const int bslot = static_cast<int>(uniform_index(q.read_slots, grp / q.H, q.read_is64));
+      uint16_t* const pool = static_cast<uint16_t*>(q.front.conv_state) + q.layer * q.front.conv_layer_stride;
+      const int64_t sstride = q.front.conv_slot_stride;
+      // Windows of up to 4 matching entries of a lane-indexed (row, slot)
+      // block, taken lowest lane first: rows and slots are broadcast into
+      // vector registers (ds_bpermute), and every load comes before any store
+      // (the history of the baseline slot is read before a window may
+      // overwrite it).  Non-baseline slots go first (pass 0).
+      auto block = [&](int row, int sl, int pass) __attribute__((always_inline)) {
+        const bool mine = sl >= 0 && row >= bos && row < bos + len && ((sl == bslot) == (pass == 1));
+        uint64_t mask = __ballot(mine);
+        while (mask) {
+          int r[4], s[4], m = 0;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int b = mask ? __builtin_ctzll(mask) : 0;
+            r[k] = __shfl(row, b);
+            s[k] = __shfl(sl, b);
+            if (mask) {
+              mask &= mask - 1;
+              m = k + 1;
+            }
+          }
+          for (int64_t u = fst; u < nch; u += 128) {
+            const int64_t ch = u < nq ? khq * DK + q0 + u
+                                      : (u < 2 * nq ? q.front.key_dim + khq * DK + q0 + (u - nq) : vch + (u - 2 * nq));
+            uint16_t w[4][3];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+#pragma unroll
+              for (int j = 0; j < 3; ++j) {
+                const int64_t pos = static_cast<int64_t>(r[k]) - 2 + j;
+                w[k][j] = k >= m ? 0
+                                 : (pos >= bos ? mixed[pos * rs + ch] : (hist ? hist[ch * 3 + (pos - bos + 3)] : 0));
+              }
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+              if (k < m) {
+#pragma unroll
+                for (int j = 0; j < 3; ++j) pool[static_cast<int64_t>(s[k]) * sstride + ch * 3 + j] = w[k][j];
+              }
+          }
+        }
+      };
+      for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+        for (int k = 0; k < kSnapBlocks; ++k) block(snap_row[k], snap_slot[k], pass);
+        for (int64_t i0 = 64 * kSnapBlocks; i0 < count; i0 += 64) {  // entries past the prefetched ones
+          const int64_t i = i0 + lane;
+          int row = -1, sl = -1;
+          if (i < count) {
+            row = static_cast<int>(load_index(q.front.snap_rows, i, q.front.snap_rows_is64));
+            sl = static_cast<int>(load_index(q.front.snap_slots, i, q.front.snap_slots_is64));
+          }
+          block(row, sl, pass);
+        }
+      }
+    };
+
     // Waves 4-5 (inverses), 6-9 (tiles, K/Q staging) and 10-11 (v conv on the
     // fused path or V staging on the two-step path, gates) run separate loops
     // with the same barrier sequence.  Staging and
@@ -981,9 +1087,12 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         resolve_log();
         prefetch_log(3);
       }
+      if constexpr (FUSED) snapshot_prefetch();
       lds_barrier();  // P0
       lds_barrier();  // B(0)
-      for (int64_t c = 0; c < nchunks; ++c) {
+      // fused: the last chunk, with nothing left to convolve or stage, is
+      // peeled off below and writes the conv windows while the chain runs it
+      for (int64_t c = 0; c < (FUSED ? nchunks - 1 : nchunks); ++c) {
         if constexpr (FUSED) {
           conv_v(c + 1);
           // keep the conv in this phase: the scheduler would otherwise sink
@@ -1012,6 +1121,11 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
           prefetch_log(c + 4);
         }
         lds_barrier();  // B(c+1)
+      }
+      if constexpr (FUSED) {
+        snapshot_windows();
+        lds_barrier();  // M(nchunks - 1)
+        lds_barrier();  // B(nchunks)
       }
     } else {
       const int st = tid - 384;       // staging thread index (waves 6-9)
@@ -1126,18 +1240,22 @@ int launch_chunk_chain_fused(const ChunkParams& p, int64_t dk, int io_dtype, int
 extern "C" int gdn_prefill_fused(const void* q, const void* k, const void* mixed, int64_t row_stride, int io_dtype,
                                  const void* weight, int kernel_width, const void* cu_seqlens, int cu_dtype,
                                  int64_t num_seqs, int64_t total_tokens, int64_t H, int64_t HV, int64_t dk,
-                                 int64_t dv, const void* conv_state, int64_t conv_slot_stride,
+                                 int64_t dv, void* conv_state, int64_t conv_slot_stride,
                                  int64_t conv_layer_stride, const float* g, const float* beta, void* state,
                                  int state_dtype,
                                  int64_t slot_stride, int64_t layer_stride, int64_t head_stride, int64_t layer,
                                  const void* baseline_slots, int baseline_dtype, const void* chunk_write_slots,
                                  int chunk_write_dtype, const void* final_write_slots, int final_write_dtype,
-                                 void* out, float scale, void* stream) {
+                                 const void* snapshot_rows, int rows_dtype, const void* snapshot_slots,
+                                 int slots_dtype, int64_t snapshot_count, void* out, float scale, void* stream) {
   using namespace gdn;
   GDN_REQUIRE(num_seqs >= 1 && total_tokens >= 0 && H > 0 && HV > 0 && HV % H == 0, "gdn_prefill_fused: bad sizes");
   GDN_REQUIRE(q && k && mixed && weight && cu_seqlens && conv_state && baseline_slots && g && beta && state &&
                   chunk_write_slots && out,
               "gdn_prefill_fused: null input");
+  GDN_REQUIRE(snapshot_count >= 0 && snapshot_count <= 0x7fffffff &&
+                  (snapshot_count == 0 || (snapshot_rows && snapshot_slots)),
+              "gdn_prefill_fused: bad snapshot list");
   const bool covered = kernel_width == 4 && (io_dtype == GDN_BF16 || io_dtype == GDN_F16) && dv % 64 == 0 &&
                        (dk == 32 || dk == 64 || dk == 128) && row_stride % 8 == 0 && row_stride > 0 &&
                        row_stride < (int64_t(1) << 24) && aligned16(mixed) &&
@@ -1165,5 +1283,8 @@ extern "C" int gdn_prefill_fused(const void* q, const void* k, const void* mixed
   f.mixed = mixed; f.row_stride = row_stride; f.weight = weight;
   f.conv_state = conv_state; f.conv_slot_stride = conv_slot_stride; f.conv_layer_stride = conv_layer_stride;
   f.key_dim = H * dk;
+  f.snap_rows = snapshot_rows; f.snap_rows_is64 = rows_dtype == GDN_I64;
+  f.snap_slots = snapshot_slots; f.snap_slots_is64 = slots_dtype == GDN_I64;
+  f.snap_count = snapshot_count;
   return launch_chunk_chain_fused(p, dk, io_dtype, state_dtype, num_seqs * H, static_cast<hipStream_t>(stream));
 }

@@ -12,9 +12,15 @@ struct FrontIn {
   const void* mixed;  // [T, conv_dim] projections, unit column stride
   int64_t row_stride;
   const void* weight;      // [conv_dim, 4]
-  const void* conv_state;  // [slots, layers, conv_dim, 3] conv history pool
+  void* conv_state;  // [slots, layers, conv_dim, 3] conv history pool (windows written back)
   int64_t conv_slot_stride, conv_layer_stride;
   int64_t key_dim;  // H * d_k: q channels [0, key_dim), k, then v
+  // conv windows: for i < snap_count with snap_slots[i] >= 0, the 3 raw inputs
+  // ending at packed row snap_rows[i] go to conv_state[snap_slots[i], layer]
+  const void* snap_rows;
+  const void* snap_slots;
+  int snap_rows_is64, snap_slots_is64;
+  int64_t snap_count;
 };
 
 struct ChunkParams {

@@ -1,5 +1,6 @@
-// gdn_prefill_fused_noalloc: the three-launch fused prefill (gdn_prefill_qk,
-// gdn_prefill_fused, gdn_conv_snapshots) with its staging -- the f16 q/k
+// gdn_prefill_fused_noalloc: the two-launch fused prefill (gdn_prefill_qk,
+// then gdn_prefill_fused, which also writes the conv windows) with its
+// staging -- the f16 q/k
 // MFMA operands and the head-major prepared gates that pass from the first
 // launch to the second -- in a file-scope device array instead of buffers
 // the caller allocates.  For callers that cannot allocate device memory
@@ -100,11 +101,7 @@ extern "C" int gdn_prefill_fused_noalloc(
   rc = gdn_prefill_fused(q, k, mixed, row_stride, io_dtype, weight, kernel_width, cu_seqlens, cu_dtype, num_seqs,
                          total_tokens, H, HV, dk, dv, conv_state, conv_slot_stride, conv_layer_stride, g, b, state,
                          state_dtype, slot_stride, layer_stride, head_stride, layer, baseline_slots, baseline_dtype,
-                         chunk_write_slots, chunk_write_dtype, nullptr, 0, out, scale, stream);
-  if (rc != GDN_OK) return rc;
-  if (snapshot_count == 0) return GDN_OK;
-  return gdn_conv_snapshots(mixed, row_stride, io_dtype, cu_seqlens, cu_dtype, num_seqs, total_tokens,
-                            2 * H * dk + HV * dv, kernel_width, conv_state, conv_slot_stride, conv_layer_stride, layer,
-                            baseline_slots, baseline_dtype, snapshot_rows, snapshot_rows_dtype, snapshot_slots,
-                            snapshot_slots_dtype, snapshot_count, stream);
+                         chunk_write_slots, chunk_write_dtype, nullptr, 0, snapshot_rows, snapshot_rows_dtype,
+                         snapshot_slots, snapshot_slots_dtype, snapshot_count, out, scale, stream);
+  return rc;
 }

@@ -4,8 +4,8 @@
 smallest number of gfx950 kernels.
 
 * ``prefill_fused`` -- the whole prefill (``gdn.py:100-150``): a q/k pass,
-  the chunk kernel computing the v conv + SiLU and the gates in its staging
-  waves, and a small conv-snapshot launch.
+  then the chunk kernel computing the v conv + SiLU and the gates in its
+  staging waves and writing the conv windows once the histories are read.
 * ``prefill_frontend`` -- conv-history gather + packed conv + split +
   ``prepare_gdn`` in one pass over ``mixed_qkv`` (``gdn.py:100-132``), then
   the window snapshots, for shapes outside the fused kernel.
@@ -118,15 +118,16 @@ def _fused_covered(mixed_qkv, config, conv_state, recurrent_state) -> bool:
 def prefill_fused(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, conv_state, recurrent_state,
                   cu_seqlens, baseline_slots, chunk_write_slots, snapshot_rows, snapshot_slots, out=None,
                   chunk_events=None):
-    """``gdn.py:100-150`` in three launches: the q/k pass writes normalised
+    """``gdn.py:100-150`` in two launches: the q/k pass writes normalised
     q and k (their conv is shared by all the v heads and d_v slices of a key
-    head) and the prepared gates, the chunk kernel's staging waves compute
+    head) and the prepared gates; the chunk kernel's staging waves compute
     the v conv + SiLU of each 64-token chunk from ``mixed_qkv`` (no v round
-    trip through HBM), and the conv windows of ``snapshot_rows`` go to
-    ``conv_state[snapshot_slots]`` last.  Conv history and initial state come
+    trip through HBM), and its side waves write the conv windows of
+    ``snapshot_rows`` to ``conv_state[snapshot_slots]`` once their loops
+    (and every read of the histories) are done.  Conv history and initial state come
     from ``baseline_slots``; chunk-end states go to ``chunk_write_slots``.
     Results equal ``prefill_frontend`` + ``chunk_gated_delta_rule_to_cache``
-    bit for bit.  Returns o [T, HV, dv], or None (nothing launched) when the
+    + ``conv_snapshots`` bit for bit.  Returns o [T, HV, dv], or None (nothing launched) when the
     shapes are outside the fused kernel -- conv width 4, d_k in {32, 64, 128},
     d_v % 64 == 0, 16-byte aligned rows, fp32 or io-typed state -- and the
     two-step path has to be used.  ``chunk_events``: optional (start, end)
@@ -166,10 +167,9 @@ def prefill_fused(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, co
     if chunk_events is not None:
         chunk_events[0].record()
     prefill_chunk_fused(q, k, g, b, mixed_qkv, weight, config, conv_state, recurrent_state, cu_seqlens,
-                        baseline_slots, chunk_write_slots, out)
+                        baseline_slots, chunk_write_slots, out, snapshot_rows, snapshot_slots)
     if chunk_events is not None:
         chunk_events[1].record()
-    conv_snapshots(mixed_qkv, config, conv_state, cu_seqlens, baseline_slots, snapshot_rows, snapshot_slots)
     return out
 
 
@@ -209,10 +209,16 @@ def prefill_fused_noalloc(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, co
 
 
 def prefill_chunk_fused(q, k, g, b, mixed_qkv, weight, config, conv_state, recurrent_state, cu_seqlens,
-                        baseline_slots, chunk_write_slots, out):
+                        baseline_slots, chunk_write_slots, out, snapshot_rows=None, snapshot_slots=None):
     """The chunk-kernel launch of ``prefill_fused`` (q, k, g, beta from the q/k
-    pass, g and beta head-major ``[HV, T]``; v computed from ``mixed_qkv`` inside)."""
+    pass, g and beta head-major ``[HV, T]``; v computed from ``mixed_qkv`` inside).
+    The conv windows of ``snapshot_rows`` go to ``conv_state[snapshot_slots]``
+    in the same launch, after the histories are read (none when omitted)."""
     T = mixed_qkv.shape[0]
+    count = 0 if snapshot_rows is None else snapshot_rows.numel()
+    if count:
+        assert snapshot_slots is not None and snapshot_slots.shape == snapshot_rows.shape
+        assert snapshot_rows.is_contiguous() and snapshot_slots.is_contiguous()
     _lib.call(
         "gdn_prefill_fused",
         q.data_ptr(), k.data_ptr(), mixed_qkv.data_ptr(), mixed_qkv.stride(0), _lib.dtype_code(mixed_qkv.dtype),
@@ -223,6 +229,8 @@ def prefill_chunk_fused(q, k, g, b, mixed_qkv, weight, config, conv_state, recur
         recurrent_state.stride(1), recurrent_state.stride(2), config.layer_idx,
         baseline_slots.data_ptr(), _lib.index_code(baseline_slots),
         chunk_write_slots.data_ptr(), _lib.index_code(chunk_write_slots), None, 0,
+        snapshot_rows.data_ptr() if count else None, _lib.index_code(snapshot_rows) if count else 0,
+        snapshot_slots.data_ptr() if count else None, _lib.index_code(snapshot_slots) if count else 0, count,
         out.data_ptr(), float(config.head_k_dim) ** -0.5, _lib.stream_of(mixed_qkv),
     )
     return out

@@ -67,7 +67,7 @@ def test_library_loads_and_exports_every_symbol():
     lib = _lib.lib()
     for name in _declarations():
         assert hasattr(lib, name), name
-    assert lib.gdn_abi_version() == 5
+    assert lib.gdn_abi_version() == 6
     assert lib.gdn_prefill_noalloc_scratch_bytes() == 256 << 20
     assert lib.gdn_last_error() in (b"",) or isinstance(lib.gdn_last_error(), bytes)
 
@@ -116,7 +116,7 @@ def test_fused_prefill_reports_uncovered_shapes_without_launching():
 
     def fused(width, dk, dv, row_stride=8192):
         return lib.gdn_prefill_fused(d, d, d, row_stride, 1, d, width, d, 1, 1, 64, 16, 32, dk, dv, d, 0, 0, d, d, d,
-                                     0, 0, 0, 0, 0, d, 1, d, 1, None, 1, d, 0.1, None)
+                                     0, 0, 0, 0, 0, d, 1, d, 1, None, 1, None, 0, None, 0, 0, d, 0.1, None)
     assert qk(3, 128) == 2
     assert b"not covered" in lib.gdn_last_error()
     assert qk(4, 256) == 2
