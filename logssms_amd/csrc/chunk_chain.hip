@@ -87,9 +87,13 @@ constexpr int LDV = 80;      // V rows (64 columns)
 // banks once (a stride of 0 mod 4 pairs rows r and r + 8 on one bank).
 constexpr int LDA = kC + 4;
 // Gate table per chunk (floats): G, 2^G, 2^(G_last - G) (0 past the end),
-// beta, then 2^G_last.
-constexpr int GTS = 264;
-constexpr int G_EXP = 64, G_DEC = 128, G_BETA = 192, G_LAST = 256;
+// beta, 2^G_last; then the factors of the off-diagonal 16 x 16 decay tiles:
+// 2^(G_t - G_16b) for token t of 16-token block b (G_RF), and for b = 1..3
+// 2^(G_16b - G_s) for s < 16 b (G_CF + 64 (b - 1) + s).  For t >= 16 b > s
+// their product is 2^(G_t - G_s), so off-diagonal tiles need no exponential;
+// with log-decay gates (<= 0, G non-increasing) both factors are <= 1.
+constexpr int GTS = 520;
+constexpr int G_EXP = 64, G_DEC = 128, G_BETA = 192, G_LAST = 256, G_RF = 264, G_CF = 328;
 
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
@@ -564,6 +568,16 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       }
       return s;
     };
+    // The same for a tile whose rows t lie in 16-token block t / 16 >= 1 and
+    // whose columns lie in earlier blocks (every entry kept): the decay from
+    // the gate table's row and boundary factors.
+    auto masked_off = [&](const float* gt, f4_t s, int t, int s0, bool with_beta) __attribute__((always_inline)) {
+      const f4_t cf = *reinterpret_cast<const f4_t*>(gt + G_CF + 64 * ((t >> 4) - 1) + s0);
+      const float r = with_beta ? gt[G_RF + t] * gt[G_BETA + t] : gt[G_RF + t];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s[e] = r * s[e] * cf[e];
+      return s;
+    };
     auto store_row4 = [&](_Float16* X, int t, int s0, f4_t v) __attribute__((always_inline)) {
       const h4_t w = {to_op(v[0]), to_op(v[1]), to_op(v[2]), to_op(v[3])};
       *reinterpret_cast<h4_t*>(X + t * LDA + s0) = w;
@@ -606,12 +620,22 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       auto lmask_t = [&](f4_t s, int tc, int s0) {  // entries (tc + c, s0 + 4g + e)
         return masked(gt, s, tc + lr, s0 + 4 * lg, true, true);
       };
+      // the off-diagonal 16 x 16 block (rows r0 + 16.., columns r0..), from the
+      // table's row and boundary factors
+      auto lmask_c_off = [&](f4_t s, int t0, int sc) {  // entries (t0 + 4g + e, sc + c)
+        const f4_t rf4 = *reinterpret_cast<const f4_t*>(gt + G_RF + t0 + 4 * lg);
+        const f4_t bt4 = *reinterpret_cast<const f4_t*>(gt + G_BETA + t0 + 4 * lg);
+        const float cf = gt[G_CF + 64 * ((t0 >> 4) - 1) + sc + lr];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[e] = rf4[e] * bt4[e] * s[e] * cf;
+        return s;
+      };
       Tri L;
       L.x[0] = lmask_c(s00, r0, r0);
-      L.x[1] = lmask_c(s10, r0 + 16, r0);
+      L.x[1] = lmask_c_off(s10, r0 + 16, r0);
       L.x[2] = lmask_c(s11, r0 + 16, r0 + 16);
       L.t[0] = lmask_t(s00, r0, r0);
-      L.t[1] = lmask_t(s01, r0 + 16, r0);
+      L.t[1] = masked_off(gt, s01, r0 + 16 + lr, r0 + 4 * lg, true);
       L.t[2] = lmask_t(s11, r0 + 16, r0 + 16);
       // P1 = I - L + L^2 - L^3, then P <- P + P L^4
       const Tri L2 = tri_mul(L, L);
@@ -671,11 +695,12 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       };
       auto mtile = [&](int ti, int tj) {
         const int t = 16 * ti + lr, s0 = 16 * tj + 4 * lg;
-        store_row4(M, t, s0, masked(gt, tile(Q, LDQ, ti, tj), t, s0, false, false));
+        const f4_t x = tile(Q, LDQ, ti, tj);
+        store_row4(M, t, s0, ti > tj ? masked_off(gt, x, t, s0, false) : masked(gt, x, t, s0, false, false));
       };
-      auto ltile = [&](int ti, int tj) {
+      auto ltile = [&](int ti, int tj) {  // ti > tj: -L21
         const int t = 16 * ti + lr, s0 = 16 * tj + 4 * lg;
-        store_row4(A, t, s0, -masked(gt, tile(K, LDK, ti, tj), t, s0, true, true));
+        store_row4(A, t, s0, -masked_off(gt, tile(K, LDK, ti, tj), t, s0, true));
       };
       const int w = sw - 2;  // 0..3 tile waves; -2, -1 the inverse waves (phase B only)
       // waves 6-7 share SIMDs with the v conv waves, 8-9 with the inverse waves;
@@ -720,8 +745,22 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       gt[G_BETA + lane] = bt;
       if (lane == 0) gt[G_LAST] = fast_exp2(Gl);
     };
+    // The off-diagonal decay factors of chunk ck (the other conv wave, from
+    // its own scan of the same gates, so that it balances the gate wave).
+    auto factor_table = [&](int64_t ck, float x) __attribute__((always_inline)) {
+      const float G = wave_prefix_sum(x) * kRcpLn2;
+      float* gt = sG + (ck % 3) * GTS;
+      const float G16 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(G), 16));
+      const float G32 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(G), 32));
+      const float G48 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(G), 48));
+      const float G0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(G), 0));
+      gt[G_RF + lane] = fast_exp2(G - (lane < 16 ? G0 : lane < 32 ? G16 : lane < 48 ? G32 : G48));
+      gt[G_CF + lane] = lane < 16 ? fast_exp2(G16 - G) : 0.f;
+      gt[G_CF + 64 + lane] = lane < 32 ? fast_exp2(G32 - G) : 0.f;
+      gt[G_CF + 128 + lane] = lane < 48 ? fast_exp2(G48 - G) : 0.f;
+    };
 
-    // ---- gates (one wave, after the M barrier), one token per lane; the
+    // ---- gates (the conv waves, after the M barrier), one token per lane; the
     // prepared g and beta (kernel/fused.py:105-117) feed the gate table.
     const FrontIn& f = p.front;
     float pgate = 0.f, pbeta = 0.f;
@@ -735,7 +774,8 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     };
     auto stage_g = [&](int64_t ck) __attribute__((always_inline)) {
       const bool ok = lane < valid_rows(ck);
-      gate_table(ck, ok ? pgate : 0.f, ok ? pbeta : 0.f);
+      if (wave == kGateWave) gate_table(ck, ok ? pgate : 0.f, ok ? pbeta : 0.f);
+      else factor_table(ck, ok ? pgate : 0.f);
     };
     // EXT, token log: the log slice of the lane's token of chunk ck, in three
     // steps one chunk apart so that no wait of the conv waves covers them:
@@ -1060,12 +1100,10 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         lds_barrier();  // B(c+1)
       }
     } else if (sw >= 6) {
-      if (wave == kGateWave) {
-        prefetch_g(0);
-        stage_g(0);
-        prefetch_g(1);
-        stage_g(1);
-      }
+      prefetch_g(0);  // (both conv waves: the gate table on one, its decay factors on the other)
+      stage_g(0);
+      prefetch_g(1);
+      stage_g(1);
       if constexpr (FUSED) {
         prefetch_fv(0);
         conv_v(0);
@@ -1113,7 +1151,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
           stage_v(c + 1);
           prefetch_v(c + 2);
         }
-        if (wave == kGateWave) stage_g(c + 2);
+        stage_g(c + 2);
         prefetch_g(c + 3);
         if constexpr (EXT) {
           stage_log(c + 2);   // resolved one chunk ago
@@ -1132,20 +1170,25 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       const bool kq_thread = st >= 0 && st < KBLK;
       // K/Q block: 16-byte column block fastest (conflict-free 16-byte LDS writes)
       const int ktb = st / DB, kdb = st % DB;
-      const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + ((bos + 4 * ktb) * p.H + kh) * DK + 8 * kdb;
-      const uint16_t* qbase = static_cast<const uint16_t*>(p.q) + ((bos + 4 * ktb) * p.H + kh) * DK + 8 * kdb;
+      // row 0 of the sequence, this thread's column block (threads past KBLK
+      // read block 0: their loads are never staged)
+      const int kcol = kq_thread ? 8 * kdb : 0;
+      const uint16_t* kbase0 = static_cast<const uint16_t*>(p.k) + (bos * p.H + kh) * DK + kcol;
+      const uint16_t* qbase0 = static_cast<const uint16_t*>(p.q) + (bos * p.H + kh) * DK + kcol;
       const int64_t krow = p.H * DK, kstride = kC * krow;
       uint4 pk[4], pq[4];
 
+      // Every thread loads every chunk, rows past the sequence end from its
+      // last row (no branch, so no prefetch register is left maybe-pending):
+      // those rows only meet beta = 0 (R and v' rows zero), strictly earlier
+      // columns in L and M, and outputs that are not stored.
       auto prefetch_kq = [&](int64_t ck) __attribute__((always_inline)) {
-        const int nk = valid_rows(ck);
+        const int64_t r0 = ck * kC + 4 * ktb;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-          pk[u] = pq[u] = make_uint4(0, 0, 0, 0);
-          if (kq_thread && 4 * ktb + u < nk) {
-            pk[u] = *reinterpret_cast<const uint4*>(kbase + ck * kstride + u * krow);
-            pq[u] = *reinterpret_cast<const uint4*>(qbase + ck * kstride + u * krow);
-          }
+          const int64_t r = r0 + u < len ? r0 + u : len - 1;
+          pk[u] = *reinterpret_cast<const uint4*>(kbase0 + r * krow);
+          pq[u] = *reinterpret_cast<const uint4*>(qbase0 + r * krow);
         }
       };
       auto stage_kq = [&](int64_t ck) __attribute__((always_inline)) {
