@@ -800,8 +800,10 @@ def main():
         flops = FLOP_PER_TOKEN_HEAD * T * HV
         achieved = flops / (chunk_ms * 1e-3)
         # HBM traffic of the fused chunk kernel (algorithmic): f16 q, k and the v columns of
-        # mixed_qkv in, prepared fp32 g/beta in, o out, final states out
-        chunk_bytes = T * (2 * H * D + HV * D) * 2 + 2 * T * HV * 4 + T * HV * D * 2 + inp["N"] * S_BYTES
+        # mixed_qkv in, prepared fp32 g/beta in, o out, final states out, and each sequence's
+        # conv window (its last W - 1 q/k input columns in, the whole window out)
+        chunk_bytes = (T * (2 * H * D + HV * D) * 2 + 2 * T * HV * 4 + T * HV * D * 2 + inp["N"] * S_BYTES
+                       + inp["N"] * (SC_BYTES + (W - 1) * 2 * H * D * 2))
         result.update(
             metric="GDN prefill tokens/s (% MFMA peak); decode state-update GB/s (% HBM peak)",
             value=T / (ms * 1e-3),
