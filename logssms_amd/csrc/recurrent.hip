@@ -406,9 +406,10 @@ __device__ __forceinline__ void conv_group(const RecParams& p, Smem& s, int64_t 
 // The q / k L2 norms and k.q of each staged token, and the gates of each
 // (token, v-head) (fused_recurrent.py:202-215; gate/beta rows follow the
 // token rows: (row, head) strides).
+// with_gates false: the caller has written s.decay / s.beta itself.
 template <int DK>
 __device__ __forceinline__ void norm_group(const RecParams& p, Smem& s, int64_t b, int64_t kh, int group, int steps,
-                                           int tid, int nthreads) {
+                                           int tid, int nthreads, bool with_gates = true) {
   // gate/beta rows follow the token rows: (row, head) strides
   {
     const int lane = tid & 63;
@@ -434,7 +435,7 @@ __device__ __forceinline__ void norm_group(const RecParams& p, Smem& s, int64_t 
       kq = wave_sum<64>(kq);
       if (lane == 0) s.kq[t] = kq;
     }
-    for (int i = tid; i < steps * group; i += nthreads) {
+    for (int i = tid; with_gates && i < steps * group; i += nthreads) {
       const int t = i / group, j = i % group;
       const int64_t h = kh * group + j;
       const int64_t flat = b * p.T + t;
@@ -469,6 +470,21 @@ template <class T> __device__ __forceinline__ uint32_t raw_bits(const T* p) {
   const uintptr_t a = reinterpret_cast<uintptr_t>(p);
   if constexpr (sizeof(T) == 2) return *reinterpret_cast<g16*>(a);
   else return *reinterpret_cast<g32*>(a);
+}
+// Element i of a runtime-typed float array (bf16, f16, else fp32) as two
+// 16-bit loads whose address is chosen by arithmetic, not by a branch (an fp32
+// element as its two halves, a 16-bit one read twice), so that the loads issue
+// back to back and their waits are counted; float_of_halves gives the value.
+__device__ __forceinline__ void load_halves(const void* base, int64_t i, int dtype, uint32_t (&r)[2]) {
+  const bool wide = dtype != GDN_BF16 && dtype != GDN_F16;
+  const uint16_t* a = reinterpret_cast<const uint16_t*>(static_cast<const char*>(base) + i * (wide ? 4 : 2));
+  r[0] = raw_bits(a);
+  r[1] = raw_bits(a + (wide ? 1 : 0));
+}
+__device__ __forceinline__ float float_of_halves(const uint32_t (&r)[2], int dtype) {
+  if (dtype == GDN_BF16) return __uint_as_float(r[0] << 16);
+  if (dtype == GDN_F16) return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r[0])));
+  return __uint_as_float(r[0] | (r[1] << 16));
 }
 template <class T> __device__ __forceinline__ float f32_from_bits(uint32_t r);
 template <> __device__ __forceinline__ float f32_from_bits<bf16>(uint32_t r) { return __uint_as_float(r << 16); }
@@ -520,6 +536,9 @@ __global__ __launch_bounds__(1024) void wave_kernel(RecParams p) {
                             : (c < 2 * DK ? key_dim + kh * DK + (c - DK) : 2 * key_dim + kh * group * DV + (c - 2 * DK));
   float* const cdst = c < DK ? s.qn + c : (c < 2 * DK ? s.kn + (c - DK) : s.vv + (c - 2 * DK));
   uint32_t rwin[3] = {0u, 0u, 0u}, rw[4] = {0u, 0u, 0u, 0u}, rx = 0u, rb = 0u;
+  // (early path, one step) the gate inputs of v-head threadIdx.x of the group,
+  // requested with the conv inputs: A_log, dt_bias, gate, beta
+  uint32_t rg4[4][2] = {{0u, 0u}, {0u, 0u}, {0u, 0u}, {0u, 0u}};
   if (early_conv) {
     // a negative read slot reads its (zero) history from a zero array: no select on loaded data
     const IOT* ccs = rs >= 0 ? static_cast<const IOT*>(p.conv_state) + rs * p.conv_slot_stride +
@@ -533,6 +552,11 @@ __global__ __launch_bounds__(1024) void wave_kernel(RecParams p) {
     for (int i = 0; i < 4; ++i) rw[i] = raw_bits(wts + i);
     rx = raw_bits(static_cast<const IOT*>(p.mixed) + row * p.mixed_row_stride + ch * p.mixed_col_stride);
     rb = raw_bits(p.conv_b ? static_cast<const IOT*>(p.conv_b) + ch : wts);  // no branch: a bias-less read is unused
+    const int64_t hg = kh * group + (static_cast<int>(threadIdx.x) < group ? static_cast<int>(threadIdx.x) : 0);
+    load_halves(p.A_log, hg, p.a_dtype, rg4[0]);
+    load_halves(p.dt_bias, hg, p.dt_dtype, rg4[1]);
+    load_halves(p.gate, row * p.gate_t + hg * p.gate_h, p.gate_dtype, rg4[2]);
+    load_halves(p.beta, row * p.beta_t + hg * p.beta_h, p.beta_dtype, rg4[3]);
   }
   float st[RPT][4];
   {
@@ -563,11 +587,18 @@ __global__ __launch_bounds__(1024) void wave_kernel(RecParams p) {
         out[2] = from_f32<IOT>(x);
       }
     }
+    if (static_cast<int>(threadIdx.x) < group) {  // fused_recurrent.py:202-215, as norm_group computes it
+      const float a = float_of_halves(rg4[0], p.a_dtype), bias = float_of_halves(rg4[1], p.dt_dtype);
+      const float gv = float_of_halves(rg4[2], p.gate_dtype), bv = float_of_halves(rg4[3], p.beta_dtype);
+      const float g = -expf(a) * softplus_decode(gv + bias);
+      s.decay[threadIdx.x] = expf(g);
+      s.beta[threadIdx.x] = sigmoid(bv);
+    }
   } else {
     conv_group<DK, DV, IOT>(p, s, b, kh, group, steps, threadIdx.x, blockDim.x);
   }
   __syncthreads();
-  norm_group<DK>(p, s, b, kh, group, steps, threadIdx.x, blockDim.x);
+  norm_group<DK>(p, s, b, kh, group, steps, threadIdx.x, blockDim.x, !early_conv);
   __syncthreads();
   if (rs < 0) {
 #pragma unroll
