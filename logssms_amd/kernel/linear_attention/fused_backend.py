@@ -176,7 +176,7 @@ def prefill_fused(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, co
 def prefill_fused_noalloc(mixed_qkv, gate, beta, conv_weight, A_log, dt_bias, config, conv_state, recurrent_state,
                           cu_seqlens, baseline_slots, chunk_write_slots, snapshot_rows, snapshot_slots, out):
     """``prefill_fused`` through ``gdn_prefill_fused_noalloc``: the same
-    three launches, with the q/k operands and prepared gates staged in the
+    two launches, with the q/k operands and prepared gates staged in the
     library's per-GPU device array, so nothing is allocated (``out`` [T, HV,
     dv] is the caller's).  Raises ``RuntimeError`` when T exceeds what the
     array holds and ``NotImplementedError`` for shapes outside the fused
