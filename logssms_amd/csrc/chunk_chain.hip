@@ -1215,15 +1215,17 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       stage_kq(0);
       prefetch_kq(1);
       stage_kq(1);
-      prefetch_kq(2);
       lds_barrier();  // P0
       tiles(0, false);
       lds_barrier();  // B(0)
+      // The loads of chunk c + 2 go out at the start of the first phase, which
+      // has few other memory operations (the second carries the chain's
+      // stores and the conv waves' row loads), and arrive while the tiles run.
       for (int64_t c = 0; c < nchunks; ++c) {
+        prefetch_kq(c + 2);
         if (c + 1 < nchunks) tiles(c + 1, false);
         lds_barrier();  // M(c)
         stage_kq(c + 2);
-        prefetch_kq(c + 3);
         lds_barrier();  // B(c+1)
       }
     }
