@@ -45,7 +45,8 @@
 // convert exactly within f16's normal range, magnitudes below 2^-14 keep
 // fewer bits (f16 subnormals; at most 2^-25 absolute error) and magnitudes
 // beyond 65504 become +-inf.  The operands are normalised q / k, decays and
-// beta <= 1, the solve's A, v / v' and the state slices.
+// beta <= 1, the solve's A, the residuals R and v', and the state slices; v
+// itself stays in the io type in LDS and enters R exactly.
 //
 // Roofline: MFMA (16-bit).  Algorithmic flops per token per v-head:
 // 10 C d + 6 d^2 + 2/3 C^2 (C = 64, d = 128).
@@ -118,6 +119,20 @@ __device__ __forceinline__ h8_t afrag(const _Float16* base, int ld, int row, int
 __device__ __forceinline__ h8_t kqfrag(const _Float16* base, int ld, int row, int k0, int g) {
   const _Float16* p = base + row * ld + k0 + 4 * (g ^ ((row >> 2) & 3));
   return cat(*reinterpret_cast<const h4_t*>(p), *reinterpret_cast<const h4_t*>(p + 16));
+}
+// Four V values read from the V buffer, which holds them in the io type
+// (exact: no operand conversion on the way in).
+template <class IOT> __device__ __forceinline__ void v_rows(h4_t raw, float (&x)[4]);
+template <> __device__ __forceinline__ void v_rows<f16>(h4_t raw, float (&x)[4]) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) x[e] = static_cast<float>(raw[e]);
+}
+template <> __device__ __forceinline__ void v_rows<bf16>(h4_t raw, float (&x)[4]) {
+  const uint2 w = __builtin_bit_cast(uint2, raw);
+  x[0] = __uint_as_float(w.x << 16);
+  x[1] = __uint_as_float(w.x & 0xffff0000u);
+  x[2] = __uint_as_float(w.y << 16);
+  x[3] = __uint_as_float(w.y & 0xffff0000u);
 }
 // LDS transpose read: the 16 lanes of a group read a 4-row x 16-column block
 // (lane r: row r / 4, columns 4 (r % 4)..+3) and lane r receives column r.
@@ -232,7 +247,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
 
   __shared__ __align__(16) _Float16 sK[3 * kC * LDK];
   __shared__ __align__(16) _Float16 sQ[2 * kC * LDQ];
-  __shared__ __align__(16) _Float16 sV[kC * LDV];
+  __shared__ __align__(16) _Float16 sV[kC * LDV];  // V rows, io-type bits (bf16 or f16)
   __shared__ __align__(16) _Float16 sA[2 * kC * LDA];  // [A11 | 0 ; -L21 | A22]
   __shared__ __align__(16) _Float16 sM[2 * kC * LDA];  // tril_incl(q k^T 2^(G_i - G_j))
   __shared__ __align__(16) float sG[3 * GTS];
@@ -412,9 +427,10 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
           const f4_t e4 = *reinterpret_cast<const f4_t*>(gt + G_EXP + t0);
           const f4_t b4 = *reinterpret_cast<const f4_t*>(gt + G_BETA + t0);
           // V rows t0..t0+3 at column 16j + lr
-          const h4_t v4 = tr_read(sV + (16 * i + 4 * lg + (lr >> 2)) * LDV + 16 * j + 4 * (lr & 3));
+          float v4[4];
+          v_rows<IOT>(tr_read(sV + (16 * i + 4 * lg + (lr >> 2)) * LDV + 16 * j + 4 * (lr & 3)), v4);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) R[i][e] = b4[e] * (static_cast<float>(v4[e]) - e4[e] * P[i][e]);
+          for (int e = 0; e < 4; ++e) R[i][e] = b4[e] * (v4[e] - e4[e] * P[i][e]);
         }
       }
 #pragma unroll
@@ -704,24 +720,69 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       };
       const int w = sw - 2;  // 0..3 tile waves; -2, -1 the inverse waves (phase B only)
       // waves 6-7 share SIMDs with the v conv waves, 8-9 with the inverse waves;
-      // the inverse waves, done early in the second phase, take its two tiles
+      // the inverse waves, done early in the second phase, take its two tiles.
+      // A wave's tiles are formed together: every fragment read first (each
+      // 16-row block once), then the independent products, then the masks,
+      // so the LDS and MFMA latencies of the tiles overlap.
+      auto frags = [&](const _Float16* X, int ldx, int r, h8_t (&f)[KS]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int m = 0; m < KS; ++m) f[m] = kqfrag(X, ldx, 16 * r + lr, 32 * m, lg);
+      };
+      auto dot = [&](const h8_t (&a)[KS], const h8_t (&b)[KS]) __attribute__((always_inline)) {
+        f4_t acc = zero4();
+#pragma unroll
+        for (int m = 0; m < KS; ++m) acc = mma(a[m], b[m], acc);
+        return acc;
+      };
+      auto put_l = [&](int ti, int tj, f4_t x) __attribute__((always_inline)) {
+        const int t = 16 * ti + lr, s0 = 16 * tj + 4 * lg;
+        store_row4(A, t, s0, -masked_off(gt, x, t, s0, true));
+      };
+      auto put_m = [&](int ti, int tj, f4_t x) __attribute__((always_inline)) {
+        const int t = 16 * ti + lr, s0 = 16 * tj + 4 * lg;
+        store_row4(M, t, s0, ti > tj ? masked_off(gt, x, t, s0, false) : masked(gt, x, t, s0, false, false));
+      };
       if (!second) {
         if (w == 0) {
-          ltile(2, 0);
-          ltile(2, 1);
-          mtile(0, 0);
-          mtile(1, 0);
+          h8_t k0[KS], k1[KS], k2[KS], q0[KS], q1[KS];
+          frags(K, LDK, 0, k0);
+          frags(K, LDK, 2, k2);
+          frags(K, LDK, 1, k1);
+          frags(Q, LDQ, 0, q0);
+          frags(Q, LDQ, 1, q1);
+          const f4_t l20 = dot(k0, k2), l21 = dot(k1, k2), m00 = dot(k0, q0), m10 = dot(k0, q1);
+          put_l(2, 0, l20);
+          put_l(2, 1, l21);
+          put_m(0, 0, m00);
+          put_m(1, 0, m10);
         } else if (w == 1) {
-          ltile(3, 0);
-          ltile(3, 1);
-          mtile(1, 1);
-          mtile(2, 0);
+          h8_t k0[KS], k1[KS], k3[KS], q1[KS], q2[KS];
+          frags(K, LDK, 0, k0);
+          frags(K, LDK, 3, k3);
+          frags(K, LDK, 1, k1);
+          frags(Q, LDQ, 1, q1);
+          frags(Q, LDQ, 2, q2);
+          const f4_t l30 = dot(k0, k3), l31 = dot(k1, k3), m11 = dot(k1, q1), m20 = dot(k0, q2);
+          put_l(3, 0, l30);
+          put_l(3, 1, l31);
+          put_m(1, 1, m11);
+          put_m(2, 0, m20);
         } else if (w == 2) {
-          mtile(2, 1);
-          mtile(2, 2);
+          h8_t k1[KS], k2[KS], q2[KS];
+          frags(Q, LDQ, 2, q2);
+          frags(K, LDK, 1, k1);
+          frags(K, LDK, 2, k2);
+          const f4_t m21 = dot(k1, q2), m22 = dot(k2, q2);
+          put_m(2, 1, m21);
+          put_m(2, 2, m22);
         } else {
-          mtile(3, 0);
-          mtile(3, 1);
+          h8_t k0[KS], k1[KS], q3[KS];
+          frags(Q, LDQ, 3, q3);
+          frags(K, LDK, 0, k0);
+          frags(K, LDK, 1, k1);
+          const f4_t m30 = dot(k0, q3), m31 = dot(k1, q3);
+          put_m(3, 0, m30);
+          put_m(3, 1, m31);
         }
       } else {
         if (w == -2) {
@@ -934,7 +995,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         for (int c = 0; c < 8; ++c) y[i][c] *= d[i][c];  // fast_silu
         // rows past the end hold the conv of clamped (real, finite) rows; the
         // chain scales them by beta = 0 there
-        vo[i] = to_f16x8<IOT>(pack8_io<IOT>(y[i]));
+        vo[i] = pack8_io<IOT>(y[i]);
       }
     };
     auto stage_fv = [&]() __attribute__((always_inline)) {
@@ -944,7 +1005,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     };
 
     // Two-step path: waves 10-11 stage the V rows (4 tokens x 8 columns per
-    // lane, the fv lane mapping), converted to f16 operands.  Rows past the
+    // lane, the fv lane mapping) as they are, in the io type.  Rows past the
     // end are clamped loads, zeroed when staged.
     uint4 pv[4];
     // columns past a 32-wide slice read the slice's last 8 columns (staged as zeros)
@@ -963,7 +1024,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       _Float16* vd = sV + (VT * fvtb) * LDV + 8 * fvdb;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const uint4 o = to_f16x8<IOT>(pv[u]);
+        const uint4 o = pv[u];
         const bool ok = VT * fvtb + u < nk && 8 * fvdb < vwidth;
         *reinterpret_cast<uint4*>(vd + u * LDV) = make_uint4(ok ? o.x : 0u, ok ? o.y : 0u, ok ? o.z : 0u,
                                                              ok ? o.w : 0u);
