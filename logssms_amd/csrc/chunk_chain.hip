@@ -938,17 +938,23 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         vraw[i] = *reinterpret_cast<const u4_t*>(cb + off);
       }
     };
-    // conv of chunk cv into registers, stage by stage over all VT x 8 values
-    // so the exp / reciprocal latencies overlap (before M); the rows go into
-    // the single V buffer after M, when the chain has read the previous
-    // chunk's.  Same operation order and rounding as the standalone front end:
-    // y = round(silu(round(sum_tap w x))), the outer rounding being the io pack.
+    // conv of chunk cv into registers, stage by stage over the rows' x 8
+    // values so the exp / reciprocal latencies overlap.  In the loop the
+    // first VT - 1 rows are convolved before M and the last after it (the
+    // conv waves are the first phase's longest and have slack in the second);
+    // all rows go into the single V buffer after M, when the chain has read
+    // the previous chunk's.  Same operation order and rounding as the
+    // standalone front end: y = round(silu(round(sum_tap w x))), the outer
+    // rounding being the io pack.
     uint4 vo[VT];
-    auto conv_v = [&](int64_t cv) __attribute__((always_inline)) {
+    // rows I0 .. I0 + NR - 1 of the lane's VT (row i's window is vraw rows
+    // i .. i + 3, unpacked again per call)
+    auto conv_rows = [&](int64_t cv, auto i0c, auto nrc) __attribute__((always_inline)) {
+      constexpr int I0 = decltype(i0c)::value, NR = decltype(nrc)::value;
       float win[3][8];
 #pragma unroll
-      for (int j = 0; j < 3; ++j) unpack8<IOT>(to_uint4(vraw[j]), win[j]);
-      if (cv == 0 && fvtb == 0) {  // the 3 inputs before the sequence: history ([channel][tap]) or zero
+      for (int j = 0; j < 3; ++j) unpack8<IOT>(to_uint4(vraw[I0 + j]), win[j]);
+      if (I0 == 0 && cv == 0 && fvtb == 0) {  // the 3 inputs before the sequence: history ([channel][tap]) or zero
         float e[3][8];
 #pragma unroll
         for (int j = 0; j < 3; ++j) {
@@ -961,11 +967,11 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
 #pragma unroll
           for (int j = 0; j < 3; ++j) win[j][c] = e[(3 * c + j) / 8][(3 * c + j) % 8];
       }
-      float y[VT][8];
+      float y[NR][8];
 #pragma unroll
-      for (int i = 0; i < VT; ++i) {
+      for (int i = 0; i < NR; ++i) {
         float x[8];
-        unpack8<IOT>(to_uint4(vraw[3 + i]), x);
+        unpack8<IOT>(to_uint4(vraw[3 + I0 + i]), x);
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
           float acc = 0.f;
@@ -980,23 +986,26 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         }
         round8<IOT>(y[i]);
       }
-      float d[VT][8];
+      float d[NR][8];
 #pragma unroll
-      for (int i = 0; i < VT; ++i)
+      for (int i = 0; i < NR; ++i)
 #pragma unroll
         for (int c = 0; c < 8; ++c) d[i][c] = fast_exp2(-1.4426950408889634f * y[i][c]);
 #pragma unroll
-      for (int i = 0; i < VT; ++i)
+      for (int i = 0; i < NR; ++i)
 #pragma unroll
         for (int c = 0; c < 8; ++c) d[i][c] = __builtin_amdgcn_rcpf(1.0f + d[i][c]);
 #pragma unroll
-      for (int i = 0; i < VT; ++i) {
+      for (int i = 0; i < NR; ++i) {
 #pragma unroll
         for (int c = 0; c < 8; ++c) y[i][c] *= d[i][c];  // fast_silu
         // rows past the end hold the conv of clamped (real, finite) rows; the
         // chain scales them by beta = 0 there
-        vo[i] = pack8_io<IOT>(y[i]);
+        vo[I0 + i] = pack8_io<IOT>(y[i]);
       }
+    };
+    auto conv_v = [&](int64_t cv) __attribute__((always_inline)) {
+      conv_rows(cv, std::integral_constant<int, 0>{}, std::integral_constant<int, VT>{});
     };
     auto stage_fv = [&]() __attribute__((always_inline)) {
       _Float16* vd = sV + (VT * fvtb) * LDV + 8 * fvdb;
@@ -1193,13 +1202,15 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       // peeled off below and writes the conv windows while the chain runs it
       for (int64_t c = 0; c < (FUSED ? nchunks - 1 : nchunks); ++c) {
         if constexpr (FUSED) {
-          conv_v(c + 1);
+          conv_rows(c + 1, std::integral_constant<int, 0>{}, std::integral_constant<int, VT - 1>{});
           // keep the conv in this phase: the scheduler would otherwise sink
           // it past the barrier into the busier second phase
 #pragma unroll
-          for (int i = 0; i < VT; ++i) asm volatile("" ::"v"(vo[i].x), "v"(vo[i].y), "v"(vo[i].z), "v"(vo[i].w));
+          for (int i = 0; i < VT - 1; ++i) asm volatile("" ::"v"(vo[i].x), "v"(vo[i].y), "v"(vo[i].z), "v"(vo[i].w));
         }
         lds_barrier();  // M(c)
+        // the last conv row, before the row loads of chunk c + 2 replace vraw
+        if constexpr (FUSED) conv_rows(c + 1, std::integral_constant<int, VT - 1>{}, std::integral_constant<int, 1>{});
         // The row loads for the conv of c + 2 go out first, so they have the
         // whole phase to arrive before that conv (right after the next
         // barrier).  Both waves issue the gate loads, after the row loads:
