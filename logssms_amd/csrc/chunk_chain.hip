@@ -1245,22 +1245,34 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       // row 0 of the sequence, this thread's column block (threads past KBLK
       // read block 0: their loads are never staged)
       const int kcol = kq_thread ? 8 * kdb : 0;
-      const uint16_t* kbase0 = static_cast<const uint16_t*>(p.k) + (bos * p.H + kh) * DK + kcol;
-      const uint16_t* qbase0 = static_cast<const uint16_t*>(p.q) + (bos * p.H + kh) * DK + kcol;
-      const int64_t krow = p.H * DK, kstride = kC * krow;
+      // this key head's row 0 of the sequence (wave-uniform)
+      const uint16_t* kseq = static_cast<const uint16_t*>(p.k) + (bos * p.H + kh) * DK;
+      const uint16_t* qseq = static_cast<const uint16_t*>(p.q) + (bos * p.H + kh) * DK;
+      const int64_t krow = p.H * DK;
+      const uint32_t row_bytes = static_cast<uint32_t>(krow * 2);
+      // the lane's byte offsets inside a chunk: rows 4 ktb + u, its column block
+      uint32_t lane_off[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) lane_off[u] = static_cast<uint32_t>(4 * ktb + u) * row_bytes + 2 * kcol;
       uint4 pk[4], pq[4];
 
-      // Every thread loads every chunk, rows past the sequence end from its
-      // last row (no branch, so no prefetch register is left maybe-pending):
-      // those rows only meet beta = 0 (R and v' rows zero), strictly earlier
-      // columns in L and M, and outputs that are not stored.
+      // Every thread loads every chunk through a buffer resource per chunk
+      // whose range ends at the sequence end: rows past it read as zeros (no
+      // branch, so no prefetch register is left maybe-pending, and no address
+      // arithmetic per load).  Those rows only meet beta = 0 (R and v' rows
+      // zero), strictly earlier columns in L and M, and outputs that are not
+      // stored.
       auto prefetch_kq = [&](int64_t ck) __attribute__((always_inline)) {
-        const int64_t r0 = ck * kC + 4 * ktb;
+        const int64_t left = len - ck * kC;  // rows of the chunk inside the sequence
+        const uint32_t nrec = static_cast<uint32_t>(left <= 0 ? 0 : (left < kC ? left : kC)) * row_bytes;
+        const __amdgpu_buffer_rsrc_t kr =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kseq + ck * kC * krow), 0, nrec, 0x00020000);
+        const __amdgpu_buffer_rsrc_t qr =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(qseq + ck * kC * krow), 0, nrec, 0x00020000);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-          const int64_t r = r0 + u < len ? r0 + u : len - 1;
-          pk[u] = *reinterpret_cast<const uint4*>(kbase0 + r * krow);
-          pq[u] = *reinterpret_cast<const uint4*>(qbase0 + r * krow);
+          pk[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kr, lane_off[u], 0, 0));
+          pq[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(qr, lane_off[u], 0, 0));
         }
       };
       auto stage_kq = [&](int64_t ck) __attribute__((always_inline)) {
