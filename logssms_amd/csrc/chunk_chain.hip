@@ -915,28 +915,29 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       if (bslot >= 0)
         hist = static_cast<const uint16_t*>(f.conv_state) + bslot * f.conv_slot_stride + p.layer * f.conv_layer_stride;
     }
-    // Every row of the window is a clamped row of the sequence, loaded with
-    // no select on the data, so nothing waits for these loads before the next
-    // chunk's conv.  Rows past the end only feed V rows that beta = 0 removes
-    // from the chain; the rows before the start (first chunk) are the conv
-    // history or zero, which conv_v substitutes.
-    // Addressing: a wave-uniform row base plus a 32-bit lane offset.  The
-    // rows a chunk's lanes read lie in [cv kC - 3, cv kC + 63] clamped to the
-    // sequence [0, len), so their offsets from the lowest clamped row are
-    // small and non-negative (row_stride < 2^24 elements keeps them in 32 bits).
+    // The window rows of a chunk, [cv kC - 3, cv kC + 63], come through one
+    // buffer resource per chunk whose range is the sequence's rows from
+    // max(cv kC - 3, 0) to the end: rows before the sequence start (first
+    // chunk: the conv history or zero, which conv_v substitutes) and past
+    // its end read as zeros, with no select on the data, so nothing waits
+    // for these loads before the next chunk's conv.  Rows past the end only
+    // feed V rows that beta = 0 removes from the chain.  A lane's offset is
+    // one add per row (row_stride < 2^24 elements keeps the range's 67 rows
+    // in 32 bits; a negative row wraps far past the range).
+    const uint32_t vrow_bytes = static_cast<uint32_t>(2 * rs);
     auto prefetch_fv = [&](int64_t cv) __attribute__((always_inline)) {
       const int64_t c0 = cv * kC;
-      const int hi = static_cast<int>(len - 1 - c0);            // last row, relative to the chunk start
-      const int lo = c0 >= 3 ? -3 : -static_cast<int>(c0);      // first row the window may reach
-      const int base = lo < hi ? lo : hi;
-      const uint16_t* cb = mixed + (bos + c0 + base) * rs + vch;
+      const int64_t b0 = c0 >= 3 ? c0 - 3 : 0;  // first row of the range
+      const int64_t left = len - b0;
+      const uint32_t nrec = static_cast<uint32_t>(left <= 0 ? 0 : (left < kC + 3 ? left : kC + 3)) * vrow_bytes;
+      const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(mixed + (bos + b0) * rs + vch), 0, nrec, 0x00020000);
+      // window row 0 of the lane (token VT fvtb - 3 of the chunk), from row b0
+      const int first = VT * fvtb - 3 + static_cast<int>(c0 - b0);
+      const uint32_t vbase = static_cast<uint32_t>(first) * vrow_bytes + static_cast<uint32_t>(16 * fvdb);
 #pragma unroll
-      for (int i = 0; i < VNR; ++i) {
-        const int t = VT * fvtb + i - 3;
-        const int r = (t < lo ? lo : t) < hi ? (t < lo ? lo : t) : hi;
-        const uint32_t off = static_cast<uint32_t>((r - base) * static_cast<int>(rs) + 8 * fvdb);
-        vraw[i] = *reinterpret_cast<const u4_t*>(cb + off);
-      }
+      for (int i = 0; i < VNR; ++i)
+        vraw[i] = __builtin_bit_cast(u4_t, __builtin_amdgcn_raw_buffer_load_b128(vr, vbase + i * vrow_bytes, 0, 0));
     };
     // conv of chunk cv into registers, stage by stage over the rows' x 8
     // values so the exp / reciprocal latencies overlap.  In the loop the
