@@ -980,6 +980,7 @@ struct RestoreParams {
   const int32_t* seg_begin; // [segments] first position
   const int32_t* seg_end;   // [segments] end position
   const int32_t* output;    // [tasks]
+  int64_t tasks;
   Div32 fdiv, gdiv;         // frame_bytes, gran
 };
 
@@ -1047,11 +1048,18 @@ __global__ __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(
   constexpr int NIW = (NI + 3) / 4;                     // per wave
   static_assert(DK % 16 == 0 && DV % 16 == 0 && DK <= 512 && DV <= 512, "tile split");
   static_assert((kRestoreStep * 2 * DK) % 1024 == 0 && (kRestoreStep * 2 * DV) % 1024 == 0, "whole wave loads");
-  const uint32_t bid = blockIdx.x, nhv = static_cast<uint32_t>(p.HV), nl = static_cast<uint32_t>(p.layers);
-  const int64_t task = bid / (nl * nhv);
-  const int64_t layer = (bid / nhv) % nl;
-  const int64_t h = bid % nhv;
-  const int64_t kh = h / (p.HV / p.KH);
+  // block -> (task, layer, key head, member v-head): the v-heads of one key
+  // head run on one XCD (block i goes to XCD i mod 8) one after another, so
+  // the key rows the first one fetches are L2 hits for the others
+  const uint32_t bid = blockIdx.x, nl = static_cast<uint32_t>(p.layers), nkh = static_cast<uint32_t>(p.KH);
+  const uint32_t members = static_cast<uint32_t>(p.HV / p.KH);
+  const uint32_t slot = bid / 8;
+  const uint64_t group = static_cast<uint64_t>(slot / members) * 8 + bid % 8;
+  if (group >= static_cast<uint64_t>(p.tasks) * nl * nkh) return;
+  const int64_t task = static_cast<int64_t>(group / (nl * nkh));
+  const int64_t layer = static_cast<int64_t>((group / nkh) % nl);
+  const int64_t kh = static_cast<int64_t>(group % nkh);
+  const int64_t h = kh * members + slot % members;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lq = lane >> 4;
   const bool owner = wave * CT < CTT;  // this wave holds column tiles
   __shared__ __attribute__((aligned(16))) uint16_t s_k[3][kRestoreStep * DK];
@@ -1685,8 +1693,10 @@ extern "C" int gdn_logstate_restore(void* storage, const void* payload_frames, i
               "gdn_logstate_restore: frame_bytes %lld smaller than a logged row (%lld bytes)", (long long)frame_bytes,
               (long long)(2 * (dk > dv ? dk : dv)));
   p.base = base_slots; p.offsets = segment_offsets; p.seg_slots = log_slots; p.seg_begin = log_begins;
-  p.seg_end = log_ends; p.output = output_slots;
-  return launch_state_kernel<true>(p, num_tasks * num_layers * HV, dk, dv, dtype,
+  p.seg_end = log_ends; p.output = output_slots; p.tasks = num_tasks;
+  // (task, layer, key head) groups in runs of 8, each run once per member v-head
+  const int64_t groups = num_tasks * num_layers * key_heads;
+  return launch_state_kernel<true>(p, (groups + 7) / 8 * 8 * (HV / key_heads), dk, dv, dtype,
                                              static_cast<hipStream_t>(stream), "gdn_logstate_restore");
 }
 
