@@ -106,24 +106,28 @@ __global__ __launch_bounds__(kThreads) void chunk_log_kernel(LogParams p) {
 
 // grid (T): one 256-thread block per token moves all its log rows in 16-byte
 // pieces (v' rows of every value head, the logged key rows) and its gates.
-// Needs dk, dv multiples of 8, frames a multiple of 16 bytes and 16-byte
-// aligned sources (checked by the host); a piece never straddles two frames.
+// Index arithmetic is 32-bit (a row has at most 64 pieces; 64-bit divisions
+// per piece had cost a fifth of the kernel).  Needs dk, dv multiples of 8,
+// frames a multiple of 16 bytes and 16-byte aligned sources (checked by the
+// host); a piece never straddles two frames.
 constexpr int kLogThreads = 256;
 __global__ __launch_bounds__(kLogThreads) void chunk_log_vec_kernel(LogParams p) {
   const int64_t t = blockIdx.x;
   const int64_t slot = load_index(p.slots, t, p.slots_is64);
   const int64_t pos = load_index(p.offsets, t, p.offsets_is64);
   if (slot < 0 || slot >= p.rows || pos < 0 || pos >= p.page) return;
-  const int64_t vv = p.V / 8, kv = p.K / 8;
-  const int64_t group = p.HV / p.KH;  // value heads per logged key head
-  const int64_t nval = p.v_new ? p.HV * vv : 0;  // no value rows: written by the chunk kernel
-  const int64_t total = nval + p.KH * kv;
-  for (int64_t i = threadIdx.x; i < total; i += kLogThreads) {
+  const int vv = static_cast<int>(p.V / 8), kv = static_cast<int>(p.K / 8);
+  const int group = static_cast<int>(p.HV / p.KH);   // value heads per logged key head
+  const int kstride = static_cast<int>(p.HV / p.H);  // value heads per key head of the input
+  const int nval = p.v_new ? static_cast<int>(p.HV) * vv : 0;  // no value rows: written by the chunk kernel
+  const int total = nval + static_cast<int>(p.KH) * kv;
+  for (int i = threadIdx.x; i < total; i += kLogThreads) {
     const bool value = i < nval;
-    const int64_t j = value ? i : i - nval;
-    const int64_t row = j / (value ? vv : kv), col = 8 * (j % (value ? vv : kv));
+    const int j = value ? i : i - nval;
+    const int per = value ? vv : kv;
+    const int row = j / per, col = 8 * (j - row * per);
     const uint16_t* src = value ? p.v_new + (t * p.HV + row) * p.V + col
-                                : p.key + (t * p.H + row * group / (p.HV / p.H)) * p.K + col;
+                                : p.key + (t * p.H + row * group / kstride) * p.K + col;
     uint16_t* d = log_element(p, slot, pos, row, col, value);
     if (d) *reinterpret_cast<uint4*>(d) = *reinterpret_cast<const uint4*>(src);
   }
@@ -131,7 +135,7 @@ __global__ __launch_bounds__(kLogThreads) void chunk_log_vec_kernel(LogParams p)
   const int64_t rec = load_index(p.decay, 2 * slot + 1, p.decay_is64);
   if (fr >= 0 && fr < p.num_frames && rec >= 0 && (rec + 1) * p.record_bytes <= p.frame_bytes) {
     float* d = reinterpret_cast<float*>(p.storage + fr * p.frame_bytes + rec * p.record_bytes);
-    for (int64_t h = threadIdx.x; h < p.HV; h += kLogThreads) d[(p.layer * p.page + pos) * p.HV + h] = p.gate[t * p.HV + h];
+    for (int h = threadIdx.x; h < p.HV; h += kLogThreads) d[(p.layer * p.page + pos) * p.HV + h] = p.gate[t * p.HV + h];
   }
 }
 
