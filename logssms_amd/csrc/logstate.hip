@@ -237,6 +237,87 @@ __global__ __launch_bounds__(kDecodeThreads) void conv_decode_frames_kernel(Conv
   }
 }
 
+// The same for 8 consecutive channels per thread with 16-byte accesses
+// (the scalar form moves 2-byte elements and looks its frames up per
+// element): width 4, one frame per snapshot granule, unit input column
+// stride and 16-byte aligned rows (checked by the host).  The 8 channels'
+// windows ([channel][tap], 24 elements) are 48 contiguous bytes of one frame.
+// Same arithmetic, order and rounding per channel as the scalar form.
+template <class T>
+__device__ __forceinline__ uint32_t bits16(T v) {
+  if constexpr (std::is_same<T, bf16>::value) return v.bits;
+  else return __builtin_bit_cast(uint16_t, v);
+}
+template <class T>
+__global__ __launch_bounds__(kDecodeThreads) void conv_decode_frames_vec_kernel(ConvFrameParams p) {
+  const int64_t b = blockIdx.y;
+  const int64_t ch0 = (static_cast<int64_t>(blockIdx.x) * kDecodeThreads + threadIdx.x) * 8;
+  if (ch0 >= p.C) return;
+  T* st = static_cast<T*>(p.storage);
+  const int64_t e0 = p.layer * p.C * 3 + ch0 * 3;
+  const int64_t rs = load_index(p.reads, b, p.reads_is64), rg = load_index(p.rgran, b, p.rgran_is64);
+  const T* src = conv_element(st, p.table, p.table_is64, p.rows, rs, rg, e0, p.granules, 1, p.fe, p.num_frames);
+  float flat[24];  // window of channel c at flat[3 c ..]
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    float f[8];
+    unpack8<T>(src ? reinterpret_cast<const uint4*>(src)[j] : make_uint4(0, 0, 0, 0), f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) flat[8 * j + e] = f[e];
+  }
+  float xv[8], wf[32], bias[8];
+  unpack8<T>(*reinterpret_cast<const uint4*>(static_cast<const T*>(p.x) + b * p.xr + ch0), xv);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float f[8];
+    unpack8<T>(reinterpret_cast<const uint4*>(static_cast<const T*>(p.weight) + ch0 * 4)[j], f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) wf[8 * j + e] = f[e];
+  }
+  if (p.bias) {
+    unpack8<T>(*reinterpret_cast<const uint4*>(static_cast<const T*>(p.bias) + ch0), bias);
+  }
+  uint32_t yb[8], nb[24];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const int64_t ch = ch0 + c;
+    const float sc = ch < p.end0 ? p.s0 : (ch < p.end1 ? p.s1 : p.s2);
+    // a scaled input is rounded to the io type, and the window keeps it scaled
+    const float x = sc != 1.f ? round_to<T>(xv[c] * sc) : xv[c];
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) acc = fmaf(wf[4 * c + i], flat[3 * c + i], acc);
+    acc = fmaf(wf[4 * c + 3], x, acc);
+    if (p.bias) acc += bias[c];
+    if (p.round_conv) acc = round_to<T>(acc);
+    yb[c] = bits16<T>(from_f32<T>(silu(acc)));
+    nb[3 * c] = bits16<T>(from_f32<T>(flat[3 * c + 1]));
+    nb[3 * c + 1] = bits16<T>(from_f32<T>(flat[3 * c + 2]));
+    nb[3 * c + 2] = bits16<T>(from_f32<T>(x));
+  }
+  uint4 nw[3];
+#pragma unroll
+  for (int j = 0; j < 3; ++j)
+    nw[j] = make_uint4(nb[8 * j] | nb[8 * j + 1] << 16, nb[8 * j + 2] | nb[8 * j + 3] << 16,
+                       nb[8 * j + 4] | nb[8 * j + 5] << 16, nb[8 * j + 6] | nb[8 * j + 7] << 16);
+  const int64_t ws = load_index(p.writes, b, p.writes_is64), wg = load_index(p.wgran, b, p.wgran_is64);
+  const int64_t wk = load_index(p.works, b, p.works_is64);
+  T* d0 = conv_element(st, p.table, p.table_is64, p.rows, ws, wg, e0, p.granules, 1, p.fe, p.num_frames);
+  T* d1 = conv_element(st, p.table, p.table_is64, p.rows, wk, 0, e0, p.granules, 1, p.fe, p.num_frames);
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    if (d0) reinterpret_cast<uint4*>(d0)[j] = nw[j];
+    if (d1) reinterpret_cast<uint4*>(d1)[j] = nw[j];
+  }
+  const uint4 y = make_uint4(yb[0] | yb[1] << 16, yb[2] | yb[3] << 16, yb[4] | yb[5] << 16, yb[6] | yb[7] << 16);
+  T* dst;
+  if (!p.split) dst = static_cast<T*>(p.q) + b * p.C + ch0;
+  else if (ch0 < p.key_dim) dst = static_cast<T*>(p.q) + b * p.key_dim + ch0;
+  else if (ch0 < 2 * p.key_dim) dst = static_cast<T*>(p.k) + b * p.key_dim + ch0 - p.key_dim;
+  else dst = static_cast<T*>(p.v) + b * (p.C - 2 * p.key_dim) + ch0 - 2 * p.key_dim;
+  *reinterpret_cast<uint4*>(dst) = y;
+}
+
 // ---- LogState prefill conv windows (packed_conv.py:53-133 with LOGSTATE):
 // the raw window ending at packed row t goes to (token_slots[t],
 // token_granules[t]) when that slot is >= 0, and a sequence's last window to
@@ -1445,10 +1526,23 @@ extern "C" int gdn_conv_decode_logstate(const void* x, int64_t x_row_stride, int
   p.q = q_out; p.k = k_out; p.v = v_out; p.key_dim = key_dim; p.split = split_qkv; p.round_conv = round_conv;
   dim3 grid(static_cast<unsigned>((channels + kDecodeThreads - 1) / kDecodeThreads), static_cast<unsigned>(batch));
   auto s = static_cast<hipStream_t>(stream);
+  // 8 channels per thread, 16-byte accesses (windows 48 contiguous bytes of one frame)
+  const bool vec = kernel_width == 4 && frames_per_granule == 1 && x_col_stride == 1 && channels % 8 == 0 &&
+                   x_row_stride % 8 == 0 && frame_bytes % 16 == 0 && aligned16(x) && aligned16(weight) &&
+                   (bias == nullptr || aligned16(bias)) && aligned16(storage) && aligned16(q_out) &&
+                   (!split_qkv || (key_dim % 8 == 0 && aligned16(k_out) && aligned16(v_out)));
+  const dim3 vgrid(static_cast<unsigned>((channels / 8 + kDecodeThreads - 1) / kDecodeThreads),
+                   static_cast<unsigned>(batch));
   if (dtype == GDN_BF16) {
-    hipLaunchKernelGGL(conv_decode_frames_kernel<bf16>, grid, dim3(kDecodeThreads), 0, s, p);
+    if (vec)
+      hipLaunchKernelGGL(conv_decode_frames_vec_kernel<bf16>, vgrid, dim3(kDecodeThreads), 0, s, p);
+    else
+      hipLaunchKernelGGL(conv_decode_frames_kernel<bf16>, grid, dim3(kDecodeThreads), 0, s, p);
   } else if (dtype == GDN_F16) {
-    hipLaunchKernelGGL(conv_decode_frames_kernel<f16>, grid, dim3(kDecodeThreads), 0, s, p);
+    if (vec)
+      hipLaunchKernelGGL(conv_decode_frames_vec_kernel<f16>, vgrid, dim3(kDecodeThreads), 0, s, p);
+    else
+      hipLaunchKernelGGL(conv_decode_frames_kernel<f16>, grid, dim3(kDecodeThreads), 0, s, p);
   } else {
     set_error("gdn_conv_decode_logstate: unsupported dtype %d (bf16 or f16)", dtype);
     return GDN_ERR_UNSUPPORTED;
