@@ -33,7 +33,8 @@
 //     10-11 the V tiles (staged, or on the fused path computed) and wave 10
 //     the gate table.
 //   * Fused variant (FUSED): the V tiles are the conv + SiLU of the raw
-//     projections, computed by waves 10-11 before the M barrier, and the gate
+//     projections, computed by waves 10-11 (three of each lane's four rows
+//     before the M barrier, the fourth after it), and the gate
 //     table is prepared from the raw gate / beta projections; q and k come
 //     normalised from a separate pass (their conv is shared by every
 //     workgroup of a key head).
