@@ -715,10 +715,6 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
         const f4_t x = tile(Q, LDQ, ti, tj);
         store_row4(M, t, s0, ti > tj ? masked_off(gt, x, t, s0, false) : masked(gt, x, t, s0, false, false));
       };
-      auto ltile = [&](int ti, int tj) {  // ti > tj: -L21
-        const int t = 16 * ti + lr, s0 = 16 * tj + 4 * lg;
-        store_row4(A, t, s0, -masked_off(gt, tile(K, LDK, ti, tj), t, s0, true));
-      };
       const int w = sw - 2;  // 0..3 tile waves; -2, -1 the inverse waves (phase B only)
       // waves 6-7 share SIMDs with the v conv waves, 8-9 with the inverse waves;
       // the inverse waves, done early in the second phase, take its two tiles.
