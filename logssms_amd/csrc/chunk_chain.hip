@@ -201,37 +201,26 @@ template <class ST> __device__ __forceinline__ void store_st(ST* p, float v) { *
 struct Tri {
   f4_t x[3], t[3];
 };
-// Left operand for row tile a of X (= C-layout tiles of X^T in column a),
-// right operand for column tile b of X.
-__device__ __forceinline__ h8_t tri_row(const Tri& X, int a) {
-  return a == 0 ? bfrag(X.t[0], zero4()) : bfrag(X.t[1], X.t[2]);
+// A 16 x 16 block X as C-layout tiles of X (x) and of X^T (t).  Fed to a
+// 16x16x16 MFMA, the 4 halfs a lane holds of a C-layout tile of Y are the
+// A operand Y^T or the B operand Y, so X W comes from (X.t, W.x) and
+// (X W)^T from (W.x, X.t) with no data movement between lanes.
+struct Sq {
+  f4_t x, t;
+};
+__device__ __forceinline__ h4_t hfrag(f4_t a) {
+  h4_t o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = to_op(a[e]);
+  return o;
 }
-__device__ __forceinline__ h8_t tri_col(const Tri& X, int b) {
-  return b == 0 ? bfrag(X.x[0], X.x[1]) : bfrag(zero4(), X.x[2]);
+__device__ __forceinline__ f4_t mma16(h4_t a, h4_t b, f4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
-// Z = X Y for lower-triangular X, Y (both orientations).
-__device__ __forceinline__ Tri tri_mul(const Tri& X, const Tri& Y) {
-  const h8_t r0 = tri_row(X, 0), r1 = tri_row(X, 1), c0 = tri_col(Y, 0), c1 = tri_col(Y, 1);
-  Tri Z;
-  Z.x[0] = mma(r0, c0, zero4());
-  Z.x[1] = mma(r1, c0, zero4());
-  Z.x[2] = mma(r1, c1, zero4());
-  Z.t[0] = mma(c0, r0, zero4());
-  Z.t[1] = mma(c0, r1, zero4());
-  Z.t[2] = mma(c1, r1, zero4());
-  return Z;
-}
-// P + P Y (both orientations).
-__device__ __forceinline__ Tri tri_mul_add(const Tri& P, const Tri& Y) {
-  const h8_t r0 = tri_row(P, 0), r1 = tri_row(P, 1), c0 = tri_col(Y, 0), c1 = tri_col(Y, 1);
-  Tri Z;
-  Z.x[0] = mma(r0, c0, P.x[0]);
-  Z.x[1] = mma(r1, c0, P.x[1]);
-  Z.x[2] = mma(r1, c1, P.x[2]);
-  Z.t[0] = mma(c0, r0, P.t[0]);
-  Z.t[1] = mma(c0, r1, P.t[1]);
-  Z.t[2] = mma(c1, r1, P.t[2]);
-  return Z;
+// X X for a block in both orientations.
+__device__ __forceinline__ Sq sq_square(const Sq& X) {
+  const h4_t xt = hfrag(X.t), xx = hfrag(X.x);
+  return Sq{mma16(xt, xx, zero4()), mma16(xx, xt, zero4())};
 }
 
 // EXT: checkpoint granularities below 64 and frame-table states (a separate
@@ -601,15 +590,21 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
     };
 
     // ---- inverses (waves 4-5): A_bb = (I + L_bb)^-1 for the 32-token half b,
-    // in two parts so that it spans both phases of a chunk:
-    //   first:  L, P = I - L + L^2 - L^3, L^4
-    //   second: P <- P (I + L^4)(I + L^8)(I + L^16), stored into A.
-    Tri invP, invL4;
+    // blocked into 16 x 16 blocks: with L_bb = [D0 0; O D1], A_bb = [A0 0;
+    // -A1 O A0  A1], and each (I + D)^-1 = (I - D)(I + D^2)(I + D^4)(I + D^8)
+    // (D strictly lower triangular, so D^16 = 0).  In two parts, so that it
+    // spans both phases of a chunk:
+    //   first:  L, D^2, D^4, G = (I - D)(I + D^2) for both diagonal blocks
+    //   second: D^8, A_i = G (I + D^4)(I + D^8), -A1 O A0, stored into A.
+    // Block 1 is needed only as A1^T (the store and -A1 O A0 take that form);
+    // block 0 also as A0 (the right factor of O A0).
+    Sq invD4[2], invG[2];
+    f4_t invOt;  // C-layout tile of O^T
     auto inv_first = [&](int64_t nc) __attribute__((always_inline)) {
       const _Float16* K = sK + (nc % 3) * kC * LDK;
       const float* gt = sG + (nc % 3) * GTS;
       const int r0 = 32 * sw;
-      f4_t s00 = zero4(), s11 = zero4(), s10 = zero4(), s01 = zero4();
+      f4_t s00 = zero4(), s11 = zero4(), s01 = zero4();
       h8_t k0[KS], k1[KS];
 #pragma unroll
       for (int m = 0; m < KS; ++m) {
@@ -620,7 +615,6 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       for (int m = 0; m < KS; ++m) {
         s00 = mma(k0[m], k0[m], s00);
         s11 = mma(k1[m], k1[m], s11);
-        s10 = mma(k1[m], k0[m], s10);  // C layout: entry (16 + 4g + e, c)
         s01 = mma(k0[m], k1[m], s01);  // C layout: entry (4g + e, 16 + c) of S^T
       }
       // C-layout tiles of L (row 4g + e, col c) and of L^T (row 4g + e, col c
@@ -637,55 +631,51 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       auto lmask_t = [&](f4_t s, int tc, int s0) {  // entries (tc + c, s0 + 4g + e)
         return masked(gt, s, tc + lr, s0 + 4 * lg, true, true);
       };
-      // the off-diagonal 16 x 16 block (rows r0 + 16.., columns r0..), from the
-      // table's row and boundary factors
-      auto lmask_c_off = [&](f4_t s, int t0, int sc) {  // entries (t0 + 4g + e, sc + c)
-        const f4_t rf4 = *reinterpret_cast<const f4_t*>(gt + G_RF + t0 + 4 * lg);
-        const f4_t bt4 = *reinterpret_cast<const f4_t*>(gt + G_BETA + t0 + 4 * lg);
-        const float cf = gt[G_CF + 64 * ((t0 >> 4) - 1) + sc + lr];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) s[e] = rf4[e] * bt4[e] * s[e] * cf;
-        return s;
-      };
+      // L.x[1], the off-diagonal block itself, is not needed: O enters only
+      // as the left factor of O A0, that is through O^T (L.t[1], from the
+      // table's row and boundary factors)
       Tri L;
       L.x[0] = lmask_c(s00, r0, r0);
-      L.x[1] = lmask_c_off(s10, r0 + 16, r0);
       L.x[2] = lmask_c(s11, r0 + 16, r0 + 16);
       L.t[0] = lmask_t(s00, r0, r0);
       L.t[1] = masked_off(gt, s01, r0 + 16 + lr, r0 + 4 * lg, true);
       L.t[2] = lmask_t(s11, r0 + 16, r0 + 16);
-      // P1 = I - L + L^2 - L^3, then P <- P + P L^4
-      const Tri L2 = tri_mul(L, L);
-      const Tri L3 = tri_mul(L, L2);
-      Tri P;
+      const f4_t id = f4_t{4 * lg == lr ? 1.f : 0.f, 4 * lg + 1 == lr ? 1.f : 0.f, 4 * lg + 2 == lr ? 1.f : 0.f,
+                           4 * lg + 3 == lr ? 1.f : 0.f};
 #pragma unroll
-      for (int q = 0; q < 3; ++q) {
-        P.x[q] = L2.x[q] - L.x[q] - L3.x[q];
-        P.t[q] = L2.t[q] - L.t[q] - L3.t[q];
+      for (int b = 0; b < 2; ++b) {
+        const Sq D{L.x[2 * b], L.t[2 * b]};
+        const Sq D2 = sq_square(D);
+        invD4[b] = sq_square(D2);
+        const Sq F{id - D.x, id - D.t};
+        const h4_t d2x = hfrag(D2.x), ft = hfrag(F.t);
+        invG[b].t = mma16(d2x, ft, F.t);
+        invG[b].x = b == 0 ? mma16(ft, d2x, F.x) : zero4();
       }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float one = (4 * lg + e == lr) ? 1.f : 0.f;
-        P.x[0][e] += one;
-        P.x[2][e] += one;
-        P.t[0][e] += one;
-        P.t[2][e] += one;
-      }
-      invL4 = tri_mul(L2, L2);
-      invP = P;
+      invOt = L.t[1];
     };
     auto inv_second = [&](int64_t nc) __attribute__((always_inline)) {
       _Float16* A = sA + (nc & 1) * kC * LDA;
       const int r0 = 32 * sw;
-      Tri P = tri_mul_add(invP, invL4);
-      const Tri L8 = tri_mul(invL4, invL4);
-      P = tri_mul_add(P, L8);
-      const Tri L16 = tri_mul(L8, L8);
-      P = tri_mul_add(P, L16);
+      Sq Ai[2];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const Sq& D4 = invD4[b];
+        const Sq& G = invG[b];
+        const h4_t d4x = hfrag(D4.x), d4t = hfrag(D4.t), gt4 = hfrag(G.t);
+        const h4_t d8x = hfrag(mma16(d4t, d4x, zero4()));
+        const Sq H{b == 0 ? mma16(gt4, d4x, G.x) : zero4(), mma16(d4x, gt4, G.t)};
+        const h4_t ht = hfrag(H.t);
+        Ai[b].t = mma16(d8x, ht, H.t);
+        Ai[b].x = b == 0 ? mma16(ht, d8x, H.x) : zero4();
+      }
+      // T = O A0, then (-A1 T)^T = -T^T A1^T
+      const f4_t Tx = mma16(hfrag(invOt), hfrag(Ai[0].x), zero4());
+      const f4_t A10t = -mma16(hfrag(Tx), hfrag(Ai[1].t), zero4());
       // row-major A_bb: C-layout tile (a, b) of A^T holds row 16b + c, columns 16a + 4g..+3
-      store_row4(A, r0 + lr, r0 + 4 * lg, P.t[0]);
-      store_row4(A, r0 + 16 + lr, r0 + 4 * lg, P.t[1]);
-      store_row4(A, r0 + 16 + lr, r0 + 16 + 4 * lg, P.t[2]);
+      store_row4(A, r0 + lr, r0 + 4 * lg, Ai[0].t);
+      store_row4(A, r0 + 16 + lr, r0 + 4 * lg, A10t);
+      store_row4(A, r0 + 16 + lr, r0 + 16 + 4 * lg, Ai[1].t);
     };
 
     // ---- row-orientation tiles (waves 6-9): (ti, tj) of Q K^T -> M, and of
