@@ -430,10 +430,24 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       const _Float16* A = sA + (c & 1) * kC * LDA;
       f4_t V[4];
       h8_t vb0, vb1;
+      h8_t mf[6];  // M's fragments for S3a
+      auto read_m = [&]() __attribute__((always_inline)) {
+        const _Float16* M = sM + (c & 1) * kC * LDA;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mf[i] = afrag(M, LDA, 16 * i + lr, 0, lg);
+        mf[4] = afrag(M, LDA, 32 + lr, 32, lg);
+        mf[5] = afrag(M, LDA, 48 + lr, 32, lg);
+      };
       {
         const h8_t a0 = afrag(A, LDA, lr, 0, lg), a1 = afrag(A, LDA, 16 + lr, 0, lg);
         const h8_t l2 = afrag(A, LDA, 32 + lr, 0, lg), l3 = afrag(A, LDA, 48 + lr, 0, lg);  // -L21
         const h8_t a2 = afrag(A, LDA, 32 + lr, 32, lg), a3 = afrag(A, LDA, 48 + lr, 32, lg);
+        if constexpr (!EXT) {
+          // M's fragments are read with A's, so their LDS latency passes under
+          // the solve's dependent steps (the EXT kernel would spill for it)
+          read_m();
+          __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
+        }
         const h8_t rb0 = bfrag(R[0], R[1]);
         V[0] = mma(a0, rb0, zero4());
         V[1] = mma(a1, rb0, zero4());
@@ -482,12 +496,7 @@ __global__ __launch_bounds__(kThreads, 1) void chunk_chain_kernel(ChunkParams p)
       }
       // ---- S3a: o^T += v'^T M^T; a lane holds 4 consecutive output columns of one token
       {
-        const _Float16* M = sM + (c & 1) * kC * LDA;
-        h8_t mf[6];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) mf[i] = afrag(M, LDA, 16 * i + lr, 0, lg);
-        mf[4] = afrag(M, LDA, 32 + lr, 32, lg);
-        mf[5] = afrag(M, LDA, 48 + lr, 32, lg);
+        if constexpr (EXT) read_m();
 #pragma unroll
         for (int i = 0; i < 4; ++i) Ot[i] = mma(vb0, mf[i], Ot[i]);
         Ot[2] = mma(vb1, mf[4], Ot[2]);
