@@ -10,9 +10,10 @@
 //   h <- 2^G_last h + (2^(G_last - G) k)^T v'                     (chunk_delta_h.py:194-224)
 // The solve splits the 64-token chunk into 32-token halves:
 //   v'_top = A11 R_top,  v'_bot = A22 (R_bot - L21 v'_top),  A_ii = (I + L_ii)^-1,
-// and each 32x32 inverse is the product form
-//   (I + L)^-1 = (I - L + L^2 - L^3)(I + L^4)(I + L^8)(I + L^16)
-// (L is nilpotent), evaluated with MFMA products in registers.
+// and each 32x32 inverse is formed from its 16x16 blocks, L = [D0 0; O D1]:
+//   (I + L)^-1 = [A0 0; -A1 O A0  A1],  A_j = (I - D)(I + D^2)(I + D^4)(I + D^8)
+// (D strictly lower triangular, so D^16 = 0), evaluated with 16x16x16 MFMA
+// products in registers.
 //
 // Mapping: one workgroup per (sequence, v-head, 64-column slice of d_v); 12
 // waves, waves i, i + 4 and i + 8 on SIMD i.
@@ -27,7 +28,7 @@
 //     q^T, R, v', o^T += v'^T M^T (stored directly: a lane holds 4 consecutive
 //     output columns of one token), h update, checkpoint stores.
 //   * Side waves prepare chunk c+1 while the chain runs chunk c: waves 4-5
-//     form A11 and A22 (k k^T tiles, masks, product-form inverse, all in
+//     form A11 and A22 (k k^T tiles, masks, blocked inverse, all in
 //     registers) and two masked tiles; waves 6-9 the other masked q k^T tiles
 //     (M) and -L21, and stage / prefetch later chunks (K, Q tiles); waves
 //     10-11 the V tiles (staged, or on the fused path computed) and wave 10
